@@ -1,0 +1,128 @@
+// common.h -- shared host/device definitions for libe4b (gfx950 / MI355X).
+//
+// Packed weight layouts (built on the host by pack.cpp, read by the kernels):
+//
+// q4_0 matrix [rows][cols], nb = cols/32 blocks per row:
+//   nibble plane  rows*nb uint4 (16 B per block)      at offset 0
+//   scale plane   rows*nb f16 (the block's d)          at offset align256(rows*nb*16)
+//   Inside a block the 32 nibbles are re-ordered so that dword k (k = 0..3)
+//   holds elements 8k..8k+7 with element 8k+2i in bits [8*i' ...] such that
+//       (w >> s_i) & 0x000F000F  ==  (n[8k+2i], n[8k+2i+1])  as two u16 halves,
+//   s_0 = 0, s_1 = 8, s_2 = 4, s_3 = 12.  A half holding n (0..15) is the f16
+//   subnormal n * 2^-24, so v_dot2_f32_f16 against the natural f16 pair
+//   (x[2j], x[2j+1]) yields 2^-24 * (n0 x0 + n1 x1) exactly; the -8 offset is
+//   folded as d * (2^24 * acc - 8 * sum(x_block)).
+//
+// Q6_K matrix [rows][cols], cols % 256 == 0; a 32-element "segment" s covers
+// scale groups 2s and 2s+1 (a ggml Q6_K scale group is 16 contiguous elements):
+//   qa plane  rows*nseg uint4  = (g0.w0, g0.w1, g1.w0, g1.w1)
+//   qb plane  rows*nseg uint2  = (g0.w2, g1.w2)
+//   sc plane  rows*ngrp int8   (ggml per-group scale, group order)
+//   d  plane  rows*nsb  f16    (ggml superblock d)
+//   Group words hold the 6-bit values q0..q15 of one group as u16-half pairs:
+//     w0: (q0,q1)@[0:5|16:21] (q2,q3)@[6:11|22:27] low nibbles of (q4,q5)@[12:15|28:31]
+//     w1: (q6,q7)            (q8,q9)              low nibbles of (q10,q11)
+//     w2: (q12,q13)          (q14,q15)            hi bits q4@[12:13] q5@[28:29]
+//                                                  hi bits q10@[14:15] q11@[30:31]
+#pragma once
+#include <stdint.h>
+#include <stddef.h>
+
+#define E4B_ALIGN256(x) ((((size_t)(x)) + 255u) & ~(size_t)255u)
+
+static inline size_t q40_nib_bytes(int64_t rows, int64_t cols) {
+  return (size_t)rows * (size_t)(cols / 32) * 16u;
+}
+static inline size_t q40_packed_bytes(int64_t rows, int64_t cols) {
+  return E4B_ALIGN256(q40_nib_bytes(rows, cols)) + E4B_ALIGN256((size_t)rows * (size_t)(cols / 32) * 2u);
+}
+
+struct Q6Planes {
+  size_t qa, qb, sc, d, total;
+};
+static inline Q6Planes q6k_planes(int64_t rows, int64_t cols) {
+  Q6Planes p;
+  size_t nseg = (size_t)(cols / 32), ngrp = (size_t)(cols / 16), nsb = (size_t)(cols / 256);
+  p.qa = 0;
+  p.qb = E4B_ALIGN256((size_t)rows * nseg * 16u);
+  p.sc = p.qb + E4B_ALIGN256((size_t)rows * nseg * 8u);
+  p.d = p.sc + E4B_ALIGN256((size_t)rows * ngrp);
+  p.total = p.d + E4B_ALIGN256((size_t)rows * nsb * 2u);
+  return p;
+}
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+
+typedef _Float16 e4b_h2 __attribute__((ext_vector_type(2)));
+
+#define DEV __device__ __forceinline__
+
+// acc + a.lo*b.lo + a.hi*b.hi with f16 inputs, f32 accumulate (v_dot2_f32_f16)
+DEV float fdot2u(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(e4b_h2, a), __builtin_bit_cast(e4b_h2, b), c, false);
+}
+
+DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// sum of the 32 f16 values of one q4_0 x block (16 packed pairs)
+DEV float xsum16(const uint32_t* xp) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s = fdot2u(xp[i], 0x3C003C00u, s);
+  return s;
+}
+
+// 2^-24 * sum n_i x_i over one repacked q4_0 block
+DEV float q40_dot(uint4 w, const uint32_t* xp, float acc) {
+  const uint32_t M = 0x000F000Fu;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t v = ws[k];
+    acc = fdot2u(v & M, xp[4 * k + 0], acc);
+    acc = fdot2u((v >> 8) & M, xp[4 * k + 1], acc);
+    acc = fdot2u((v >> 4) & M, xp[4 * k + 2], acc);
+    acc = fdot2u((v >> 12) & M, xp[4 * k + 3], acc);
+  }
+  return acc;
+}
+
+// the 8 (q_2i, q_2i+1) subnormal-f16 pairs of one packed Q6_K group
+DEV void q6_pairs(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t* p) {
+  const uint32_t M6 = 0x003F003Fu, M4 = 0x000F000Fu, MH = 0x00300030u;
+  p[0] = w0 & M6;
+  p[1] = (w0 >> 6) & M6;
+  p[2] = ((w0 >> 12) & M4) | ((w2 >> 8) & MH);
+  p[3] = w1 & M6;
+  p[4] = (w1 >> 6) & M6;
+  p[5] = ((w1 >> 12) & M4) | ((w2 >> 10) & MH);
+  p[6] = w2 & M6;
+  p[7] = (w2 >> 6) & M6;
+}
+
+template <typename T>
+DEV T wave_shfl_xor(T v, int m) {
+  return __shfl_xor(v, m, 64);
+}
+
+DEV float group_sum(float v, int lpr) {
+  for (int off = lpr >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// non-temporal 16 B load for streamed weights (read once per token)
+typedef uint32_t e4b_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t e4b_u32x2 __attribute__((ext_vector_type(2)));
+DEV uint4 ld_nt_u4(const uint4* p) {
+  const e4b_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const e4b_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+DEV uint2 ld_nt_u2(const uint2* p) {
+  const e4b_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const e4b_u32x2*>(p));
+  return make_uint2(v.x, v.y);
+}
+DEV uint16_t ld_nt_u16(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+
+#endif  // __HIPCC__

@@ -1,0 +1,63 @@
+// kernels.h -- device-side views of packed weights and launch helpers shared
+// by the kernel translation units and the engine.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+struct Q40Mat {
+  const uint4* nib;      // [rows][nb] re-ordered nibble blocks
+  const uint16_t* sc;    // [rows][nb] f16 block scales
+  int64_t rows;
+  int nb;                // blocks per row = cols / 32
+};
+
+static inline Q40Mat q40_view(const void* packed, int64_t rows, int64_t cols) {
+  Q40Mat m;
+  m.nib = (const uint4*)packed;
+  m.sc = (const uint16_t*)((const uint8_t*)packed + E4B_ALIGN256(q40_nib_bytes(rows, cols)));
+  m.rows = rows;
+  m.nb = (int)(cols / 32);
+  return m;
+}
+
+struct Q6Mat {
+  const uint4* qa;       // [rows][nseg]
+  const uint2* qb;       // [rows][nseg]
+  const int8_t* sc;      // [rows][ngrp]
+  const uint16_t* d;     // [rows][nsb]
+  int64_t rows;
+  int nseg;              // cols / 32
+};
+
+static inline Q6Mat q6_view(const void* packed, int64_t rows, int64_t cols) {
+  const Q6Planes P = q6k_planes(rows, cols);
+  const uint8_t* b = (const uint8_t*)packed;
+  Q6Mat m;
+  m.qa = (const uint4*)(b + P.qa);
+  m.qb = (const uint2*)(b + P.qb);
+  m.sc = (const int8_t*)(b + P.sc);
+  m.d = (const uint16_t*)(b + P.d);
+  m.rows = rows;
+  m.nseg = (int)(cols / 32);
+  return m;
+}
+
+// Per-device library workspace (argmax partials, counters, x staging).  The
+// counters are zeroed once at allocation and every kernel that uses one
+// returns it to zero, so launches can be captured into a hipGraph.
+struct Workspace {
+  uint8_t* buf;          // general scratch
+  size_t cap;
+  uint32_t* counters;    // E4B_NCOUNTERS zero-initialised u32
+};
+#define E4B_NCOUNTERS 4096
+int e4b_workspace(size_t bytes, Workspace* ws);
+
+// launchers (defined in k_gemv.hip); all asynchronous on `st`
+int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st);
+int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st);
+int launch_q6k_gemv_argmax(const Q6Mat& W, const uint32_t* xh, const uint32_t* xl, float softcap,
+                           float* logits, uint32_t* amax, uint2* part, uint32_t* counter, hipStream_t st);
+int launch_q6k_row(const Q6Mat& W, int64_t row, const uint32_t* row_dev, float mult, float* out, hipStream_t st);
+int launch_argmax(const float* x, int64_t n, uint32_t* amax, uint2* part, uint32_t* counter, hipStream_t st);

@@ -1,0 +1,195 @@
+// lib.hip -- C-ABI plumbing (errors, device memory, workspace) and the
+// kernel-level entry points of libe4b.
+#include <mutex>
+#include <string.h>
+
+#include "../../include/e4b.h"
+#include "kernels.h"
+#include "util.h"
+
+static thread_local char g_last_error[1024] = "";
+
+int e4b_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+extern "C" const char* e4b_version(void) { return "e4b-mi355x 0.1 (gfx950)"; }
+extern "C" const char* e4b_last_error(void) { return g_last_error; }
+
+extern "C" int e4b_device_count(int* n) {
+  if (!n) return e4b_fail(E4B_EINVAL, "e4b_device_count: null");
+  E4B_HIP(hipGetDeviceCount(n));
+  return E4B_OK;
+}
+extern "C" int e4b_set_device(int device) {
+  E4B_HIP(hipSetDevice(device));
+  return E4B_OK;
+}
+extern "C" void* e4b_dev_alloc(size_t bytes) {
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    e4b_fail(E4B_ENOMEM, "hipMalloc(%zu) -> %s", bytes, hipGetErrorString(e));
+    return nullptr;
+  }
+  return p;
+}
+extern "C" int e4b_dev_free(void* p) {
+  if (p) E4B_HIP(hipFree(p));
+  return E4B_OK;
+}
+extern "C" int e4b_memcpy_h2d(void* dst, const void* src, size_t n) {
+  E4B_HIP(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+  return E4B_OK;
+}
+extern "C" int e4b_memcpy_d2h(void* dst, const void* src, size_t n) {
+  E4B_HIP(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+  return E4B_OK;
+}
+extern "C" int e4b_memset_dev(void* dst, int value, size_t n) {
+  E4B_HIP(hipMemset(dst, value, n));
+  return E4B_OK;
+}
+extern "C" int e4b_sync(void) {
+  E4B_HIP(hipDeviceSynchronize());
+  return E4B_OK;
+}
+extern "C" int e4b_stream_sync(void* stream) {
+  E4B_HIP(hipStreamSynchronize((hipStream_t)stream));
+  return E4B_OK;
+}
+
+extern "C" void* e4b_event_create(void) {
+  hipEvent_t e = nullptr;
+  hipError_t rc = hipEventCreate(&e);
+  if (rc != hipSuccess) {
+    e4b_fail(E4B_EHIP, "hipEventCreate -> %s", hipGetErrorString(rc));
+    return nullptr;
+  }
+  return (void*)e;
+}
+extern "C" int e4b_event_record(void* ev, void* stream) {
+  E4B_HIP(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream));
+  return E4B_OK;
+}
+extern "C" int e4b_event_elapsed_ms(void* a, void* b, float* ms) {
+  if (!ms) return e4b_fail(E4B_EINVAL, "e4b_event_elapsed_ms: null");
+  E4B_HIP(hipEventSynchronize((hipEvent_t)b));
+  E4B_HIP(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+  return E4B_OK;
+}
+extern "C" int e4b_event_destroy(void* ev) {
+  if (ev) E4B_HIP(hipEventDestroy((hipEvent_t)ev));
+  return E4B_OK;
+}
+
+// ---- per-device workspace ---------------------------------------------------
+// One grow-only scratch buffer per device plus a zeroed counter array.  Calls
+// that use it on one device must not overlap (one stream at a time).
+namespace {
+struct DevWs {
+  uint8_t* buf = nullptr;
+  size_t cap = 0;
+  uint32_t* counters = nullptr;
+};
+std::mutex g_ws_mu;
+DevWs g_ws[64];
+}  // namespace
+
+int e4b_workspace(size_t bytes, Workspace* out) {
+  int dev = 0;
+  E4B_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return e4b_fail(E4B_EINVAL, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  DevWs& w = g_ws[dev];
+  if (!w.counters) {
+    E4B_HIP(hipMalloc(&w.counters, E4B_NCOUNTERS * sizeof(uint32_t)));
+    E4B_HIP(hipMemset(w.counters, 0, E4B_NCOUNTERS * sizeof(uint32_t)));
+  }
+  if (bytes > w.cap) {
+    if (w.buf) {
+      E4B_HIP(hipDeviceSynchronize());
+      E4B_HIP(hipFree(w.buf));
+      w.buf = nullptr;
+      w.cap = 0;
+    }
+    const size_t cap = E4B_ALIGN256(bytes < (1u << 20) ? (1u << 20) : bytes);
+    E4B_HIP(hipMalloc(&w.buf, cap));
+    w.cap = cap;
+  }
+  out->buf = w.buf;
+  out->cap = w.cap;
+  out->counters = w.counters;
+  return E4B_OK;
+}
+
+// ---- kernel-level entry points -----------------------------------------------
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+extern "C" int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, const void* x, int x_dtype,
+                              float* y, void* stream) {
+  if (!w_packed || !x || !y || rows <= 0 || cols <= 0 || cols % 32)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemv: bad arguments (rows=%lld cols=%lld)", (long long)rows,
+                    (long long)cols);
+  if (!aligned16(w_packed) || !aligned16(x))
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemv: weight and x must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const Q40Mat W = q40_view(w_packed, rows, cols);
+  if (x_dtype == E4B_DT_F16) return launch_q40_gemv(W, (const uint32_t*)x, nullptr, y, st);
+  if (x_dtype == E4B_DT_F32_HL)
+    return launch_q40_gemv(W, (const uint32_t*)x, (const uint32_t*)((const uint16_t*)x + cols), y, st);
+  if (x_dtype != E4B_DT_F32) return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemv: x_dtype %d", x_dtype);
+  Workspace ws;
+  const size_t half = E4B_ALIGN256((size_t)cols * 2);
+  int rc = e4b_workspace(2 * half, &ws);
+  if (rc) return rc;
+  uint16_t* hi = (uint16_t*)ws.buf;
+  uint16_t* lo = (uint16_t*)(ws.buf + half);
+  if ((rc = launch_split_f32((const float*)x, cols, hi, lo, st))) return rc;
+  return launch_q40_gemv(W, (const uint32_t*)hi, (const uint32_t*)lo, y, st);
+}
+
+extern "C" int e4b_split_f32(const float* x, int64_t n, void* hl, void* stream) {
+  if (!x || !hl || n <= 0) return e4b_fail(E4B_EINVAL, "e4b_split_f32: bad arguments");
+  return launch_split_f32(x, n, (uint16_t*)hl, (uint16_t*)hl + n, (hipStream_t)stream);
+}
+
+extern "C" int e4b_k_q6k_gemv_argmax(const void* w_packed, int64_t rows, int64_t cols, const float* x,
+                                     float softcap, float* logits, uint32_t* amax, void* stream) {
+  if (!w_packed || !x || !amax || rows <= 0 || rows > 0xffffffffLL || cols <= 0 || cols % 256)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q6k_gemv_argmax: bad arguments (rows=%lld cols=%lld)", (long long)rows,
+                    (long long)cols);
+  if (!aligned16(w_packed)) return e4b_fail(E4B_EINVAL, "e4b_k_q6k_gemv_argmax: weight must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  Workspace ws;
+  const size_t half = E4B_ALIGN256((size_t)cols * 2);
+  const size_t partb = 2048 * sizeof(uint2);
+  int rc = e4b_workspace(2 * half + partb, &ws);
+  if (rc) return rc;
+  uint16_t* hi = (uint16_t*)ws.buf;
+  uint16_t* lo = (uint16_t*)(ws.buf + half);
+  uint2* part = (uint2*)(ws.buf + 2 * half);
+  if ((rc = launch_split_f32(x, cols, hi, lo, st))) return rc;
+  return launch_q6k_gemv_argmax(q6_view(w_packed, rows, cols), (const uint32_t*)hi, (const uint32_t*)lo, softcap,
+                                logits, amax, part, &ws.counters[0], st);
+}
+
+extern "C" int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row, float mult, float* out,
+                             void* stream) {
+  if (!w_packed || !out || rows <= 0 || cols <= 0 || cols % 256 || row < 0 || row >= rows)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q6k_row: bad arguments (rows=%lld cols=%lld row=%lld)", (long long)rows,
+                    (long long)cols, (long long)row);
+  return launch_q6k_row(q6_view(w_packed, rows, cols), row, nullptr, mult, out, (hipStream_t)stream);
+}
+
+extern "C" int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* stream) {
+  if (!x || !amax || n <= 0 || n > 0xffffffffLL) return e4b_fail(E4B_EINVAL, "e4b_k_argmax: bad arguments");
+  Workspace ws;
+  int rc = e4b_workspace(1024 * sizeof(uint2), &ws);
+  if (rc) return rc;
+  return launch_argmax(x, n, amax, (uint2*)ws.buf, &ws.counters[1], (hipStream_t)stream);
+}

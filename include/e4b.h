@@ -1,0 +1,124 @@
+/*
+ * e4b.h -- C ABI of libe4b.so, the MI355X (gfx950) batch-1 decode library.
+ *
+ * Plain C: pointers, sizes, return codes.  No C++ exceptions cross this ABI.
+ * Return codes: 0 = ok, negative = error (see E4B_E*); e4b_last_error() gives
+ * the message of the last failure on the calling thread.
+ *
+ * Ownership: input buffers are borrowed for the duration of a call; output
+ * buffers are caller-allocated.  Device pointers are HIP device addresses
+ * (from e4b_dev_alloc or any other HIP allocation on the current device).
+ * `stream` arguments are hipStream_t values passed as void*; NULL means the
+ * library's default stream (the HIP null stream).  Kernel-level entry points
+ * are asynchronous on that stream; engine calls that return results are
+ * synchronous.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (paths relative to the Verilean/e4b-webgpu checkout).
+ */
+#ifndef E4B_H
+#define E4B_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define E4B_OK 0
+#define E4B_EINVAL (-1)   /* bad argument / shape                        */
+#define E4B_ENOMEM (-2)   /* device or host allocation failed             */
+#define E4B_EHIP (-3)     /* HIP runtime error                            */
+#define E4B_ESTATE (-4)   /* call out of order (e.g. step before finalize) */
+#define E4B_ENOTENSOR (-5) /* required tensor missing at finalize          */
+#define E4B_ERANGE (-6)   /* position / token / size beyond capacity       */
+
+/* ggml tensor type ids, as src/gguf.js:3 GGML */
+#define E4B_GGML_F32 0
+#define E4B_GGML_F16 1
+#define E4B_GGML_Q4_0 2
+#define E4B_GGML_Q6_K 14
+
+/* activation dtypes for kernel-level entry points */
+#define E4B_DT_F32 0     /* f32[n]                                              */
+#define E4B_DT_F16 1     /* f16[n]                                              */
+#define E4B_DT_F32_HL 2  /* an f32 vector pre-split as f16 hi[n] then f16 lo[n], */
+                         /* x = hi + lo exactly (see e4b_split_f32)              */
+
+/* ---------------------------------------------------------------------------
+ * Library / device plumbing (replaces src/gpu.js:4-50 initDevice, upload,
+ * alloc, readback).
+ * ------------------------------------------------------------------------- */
+const char* e4b_version(void);
+const char* e4b_last_error(void);
+int   e4b_device_count(int* n);
+int   e4b_set_device(int device);
+void* e4b_dev_alloc(size_t bytes);                           /* NULL on failure */
+int   e4b_dev_free(void* p);
+int   e4b_memcpy_h2d(void* dst_dev, const void* src_host, size_t bytes);
+int   e4b_memcpy_d2h(void* dst_host, const void* src_dev, size_t bytes);
+int   e4b_memset_dev(void* dst_dev, int value, size_t bytes);
+int   e4b_sync(void);                                        /* device-wide */
+int   e4b_stream_sync(void* stream);
+
+/* HIP events for timing on a stream (replaces the timestamp-query profiling of
+ * src/engine-a4b.js:707-740) */
+void* e4b_event_create(void);
+int   e4b_event_record(void* event, void* stream);
+int   e4b_event_elapsed_ms(void* start, void* end, float* ms); /* waits for end */
+int   e4b_event_destroy(void* event);
+
+/* f32 -> (hi, lo) f16 split on the device: hi = f16(x), lo = f16(x - hi). */
+int   e4b_split_f32(const float* x, int64_t n, void* hl_out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Seeded synthetic data (portable counter-based splitmix64; identical bytes
+ * from any caller).  Distributions follow BASELINE configs: q4_0 d =
+ * f16(|N(0,sigma)|/8), nibbles U{0..15}; Q6_K d = f16(|N(0,sigma)|), scales
+ * U{-32..31}, quants U{0..63}.
+ * ------------------------------------------------------------------------- */
+uint64_t e4b_synth_u64(uint64_t seed, uint64_t index);
+int e4b_synth_normal_f32(uint64_t seed, int64_t n, float mean, float std, float* out);
+int e4b_synth_uniform_u32(uint64_t seed, int64_t n, uint32_t lo, uint32_t hi_exclusive, uint32_t* out);
+int e4b_synth_q40(uint64_t seed, int64_t rows, int64_t cols, float sigma, void* out_ggml);
+int e4b_synth_q6k(uint64_t seed, int64_t rows, int64_t cols, float sigma, void* out_ggml);
+
+/* ---------------------------------------------------------------------------
+ * Weight formats.  Replaces repackQ40 / repackQ6K / q40cat
+ * (src/engine-a4b.js:29-73, 126-138): raw ggml blocks in, the library's
+ * device layout out.  Packing is a host-to-host transform; the caller uploads
+ * the result (or uses e4b_*_upload which packs and copies in one call).
+ * ------------------------------------------------------------------------- */
+size_t e4b_q40_packed_bytes(int64_t rows, int64_t cols);
+int    e4b_q40_pack(const void* ggml, int64_t rows, int64_t cols, void* packed_host);
+size_t e4b_q6k_packed_bytes(int64_t rows, int64_t cols);
+int    e4b_q6k_pack(const void* ggml, int64_t rows, int64_t cols, void* packed_host);
+
+/* ---------------------------------------------------------------------------
+ * Kernel-level entry points (parity + per-config benches).  All pointers are
+ * device pointers; weights are in the packed layout above.
+ * ------------------------------------------------------------------------- */
+
+/* q4_0 GEMV y[rows] = W[rows x cols] . x  (kernels/q40mv.wgsl:56-89).
+ * x_dtype E4B_DT_F32 (x is f32[cols]) or E4B_DT_F16 (x is f16[cols]).
+ * cols % 32 == 0. */
+int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, const void* x,
+                   int x_dtype, float* y, void* stream);
+
+/* Q6_K GEMV + softcap + argmax (kernels/q6k.wgsl:75-130 MODE 1, then
+ * kernels/argmax2.wgsl:8-48).  logits f32[rows] (may be NULL), amax u32[2] =
+ * {index, f32 bits of the max}; ties -> lowest index; NaN never wins.
+ * cols % 256 == 0.  softcap 0 disables the cap. */
+int e4b_k_q6k_gemv_argmax(const void* w_packed, int64_t rows, int64_t cols, const float* x,
+                          float softcap, float* logits, uint32_t* amax, void* stream);
+
+/* Q6_K row dequant * mult (kernels/q6k.wgsl:37-73 MODE 0): out f32[cols]. */
+int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row, float mult,
+                  float* out, void* stream);
+
+/* argmax over f32[n] (kernels/argmax2.wgsl:8-48): amax u32[2]. */
+int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

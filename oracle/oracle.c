@@ -1,0 +1,725 @@
+/*
+ * oracle.c -- CPU restatement of the reference's batch-1 decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h).  Plain C99 + OpenMP; no GPU code,
+ * no dependency on the product library.  Each function cites the reference
+ * file:line whose semantics it restates.  Sums are carried in double and
+ * rounded where the reference stores f32/f16.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* IEEE binary16 <-> binary32 (textbook; round-to-nearest-even)             */
+/* ------------------------------------------------------------------------ */
+float orc_h2f(uint16_t h) {
+  uint32_t s = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    if (m == 0) {
+      bits = s;
+    } else { /* subnormal: value = m * 2^-24 */
+      float v = (float)m * 5.9604644775390625e-08f;
+      memcpy(&bits, &v, 4);
+      bits |= s;
+    }
+  } else if (e == 31) {
+    bits = s | 0x7f800000u | (m << 13);
+  } else {
+    bits = s | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t orc_f2h(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) /* inf / nan */
+    return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+  if (ax >= 0x477ff000u) /* >= 65520 rounds to inf */
+    return (uint16_t)(sign | 0x7c00u);
+  if (ax < 0x38800000u) { /* below the smallest normal half: subnormal or 0 */
+    /* value / 2^-24, rounded to nearest even integer */
+    float a;
+    memcpy(&a, &ax, 4);
+    double q = (double)a * 16777216.0;
+    double fl = floor(q);
+    double r = q - fl;
+    uint32_t m = (uint32_t)fl;
+    if (r > 0.5 || (r == 0.5 && (m & 1u))) m++;
+    return (uint16_t)(sign | m); /* m == 1024 becomes the smallest normal */
+  }
+  uint32_t e = ((ax >> 23) - 112u) << 10;
+  uint32_t m = (ax >> 13) & 0x3ffu;
+  uint32_t rest = ax & 0x1fffu;
+  uint32_t h = e | m;
+  if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+void orc_h2f_n(const uint16_t* h, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_h2f(h[i]);
+}
+void orc_f2h_n(const float* f, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_f2h(f[i]);
+}
+
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* ------------------------------------------------------------------------ */
+/* q4_0: 18 B = f16 d, qs[16]; element j = (qs[j] & 15) - 8, element j+16 =  */
+/* (qs[j] >> 4) - 8, value * d.  Follows kernels/q40mv.wgsl:22-29 (lo plane */
+/* = elements 0..15, hi plane = 16..31) and scripts/ternarize_a4b.py:80-88. */
+/* ------------------------------------------------------------------------ */
+void orc_q40_dequant(const uint8_t* blocks, int64_t nblocks, float* out) {
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const uint8_t* p = blocks + b * 18;
+    double d = orc_h2f(rd16(p));
+    for (int j = 0; j < 16; ++j) {
+      out[b * 32 + j] = (float)(d * (double)((p[2 + j] & 15) - 8));
+      out[b * 32 + j + 16] = (float)(d * (double)((p[2 + j] >> 4) - 8));
+    }
+  }
+}
+
+/* y[o] = sum_b d(o,b) * sum_i (q-8) x[32b+i]  (kernels/q40mv.wgsl:56-89) */
+static double q40_row_dot(const uint8_t* row, int64_t nb, const float* x) {
+  double acc = 0.0;
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint8_t* p = row + b * 18;
+    const float* xb = x + b * 32;
+    double s = 0.0;
+    for (int j = 0; j < 16; ++j) {
+      s += (double)((p[2 + j] & 15) - 8) * (double)xb[j];
+      s += (double)((p[2 + j] >> 4) - 8) * (double)xb[j + 16];
+    }
+    acc += (double)orc_h2f(rd16(p)) * s;
+  }
+  return acc;
+}
+
+void orc_q40_gemv(const uint8_t* w, int64_t rows, int64_t cols, const float* x, float* y) {
+  const int64_t nb = cols / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t o = 0; o < rows; ++o) y[o] = (float)q40_row_dot(w + o * nb * 18, nb, x);
+}
+
+/* EXPERT=1 indirection: weight base = topk[z] * OUT * rowB (q40mv.wgsl:70-74) */
+void orc_q40_gemv_expert(const uint8_t* w, int expert, int64_t rows, int64_t cols,
+                         const float* x, float* y) {
+  orc_q40_gemv(w + (int64_t)expert * rows * (cols / 32) * 18, rows, cols, x, y);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q6_K: 210 B = ql[128], qh[64], int8 scales[16], f16 d.  Element order is */
+/* ggml dequantize_row_q6_K as restated by kernels/q6k.wgsl:44-71 (MODE 0). */
+/* ------------------------------------------------------------------------ */
+static inline int q6_val(const uint8_t* blk, int e) {
+  /* element e (0..255) of one superblock -> 6-bit value 0..63 */
+  int half = e >> 7, r = e & 127, quad = r >> 5, l = r & 31;
+  const uint8_t* ql = blk + 64 * half;
+  const uint8_t* qh = blk + 128 + 32 * half;
+  int lo = (quad & 1) ? ql[l + 32] : ql[l];
+  lo = (quad >= 2) ? (lo >> 4) : (lo & 15);
+  int hi = (qh[l] >> (2 * quad)) & 3;
+  return lo | (hi << 4);
+}
+static inline int q6_scale_index(int e) {
+  /* sc_h[is + 2*quad], is = l/16, sc_h = scales + 8*half */
+  int half = e >> 7, r = e & 127, quad = r >> 5, l = r & 31;
+  return 8 * half + (l >> 4) + 2 * quad;
+}
+
+void orc_q6k_dequant(const uint8_t* blocks, int64_t nblocks, float mult, float* out) {
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const uint8_t* blk = blocks + b * 210;
+    double d = orc_h2f(rd16(blk + 208));
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    for (int e = 0; e < 256; ++e)
+      out[b * 256 + e] =
+          (float)(d * (double)sc[q6_scale_index(e)] * (double)(q6_val(blk, e) - 32) * (double)mult);
+  }
+}
+
+void orc_q6k_dequant_row(const uint8_t* w, int64_t cols, int64_t row, float mult, float* out) {
+  const int64_t nsb = cols / 256;
+  orc_q6k_dequant(w + row * nsb * 210, nsb, mult, out);
+}
+
+/* MODE 1 lm-head (kernels/q6k.wgsl:75-130): the 255*bacc - 32*gsum refold is */
+/* algebraically sum d*s_j*(q-32)*x, computed here directly; then           */
+/* SOFTCAP*tanh(y/SOFTCAP) when SOFTCAP != 0.                               */
+void orc_q6k_gemv(const uint8_t* w, int64_t rows, int64_t cols, const float* x, float softcap,
+                  float* y) {
+  const int64_t nsb = cols / 256;
+#pragma omp parallel for schedule(static)
+  for (int64_t o = 0; o < rows; ++o) {
+    double acc = 0.0;
+    for (int64_t b = 0; b < nsb; ++b) {
+      const uint8_t* blk = w + (o * nsb + b) * 210;
+      const int8_t* sc = (const int8_t*)(blk + 192);
+      const float* xb = x + b * 256;
+      double g[16] = {0};
+      for (int e = 0; e < 256; ++e) g[q6_scale_index(e)] += (double)(q6_val(blk, e) - 32) * (double)xb[e];
+      double s = 0.0;
+      for (int j = 0; j < 16; ++j) s += (double)sc[j] * g[j];
+      acc += (double)orc_h2f(rd16(blk + 208)) * s;
+    }
+    float v = (float)acc;
+    if (softcap != 0.0f) v = (float)((double)softcap * tanh((double)v / (double)softcap));
+    y[o] = v;
+  }
+}
+
+/* argmax2 (kernels/argmax2.wgsl:8-48): start (bv=-3e38, bi=0), take v when */
+/* v > bv or (v == bv and i < bi): lowest index among maxima; NaN never wins. */
+void orc_argmax(const float* x, int64_t n, uint32_t out[2]) {
+  float bv = -3.0e38f;
+  uint32_t bi = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float v = x[i];
+    if (v > bv || (v == bv && (uint32_t)i < bi)) {
+      bv = v;
+      bi = (uint32_t)i;
+    }
+  }
+  out[0] = bi;
+  memcpy(&out[1], &bv, 4);
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm y = x * (mean x^2 + eps)^-1/2 * w  (kernels/rmsnorm.wgsl:13-51;   */
+/* Gemma weight used directly, NOTES/arch-spec.md:97-118).  w may be NULL.  */
+/* ------------------------------------------------------------------------ */
+static double rms_inv(const float* x, int64_t n, float eps) {
+  double s = 0.0;
+  for (int64_t i = 0; i < n; ++i) s += (double)x[i] * (double)x[i];
+  return 1.0 / sqrt(s / (double)n + (double)eps);
+}
+void orc_rmsnorm(const float* x, const float* w, int64_t n, float eps, float* y) {
+  double inv = rms_inv(x, n, eps);
+  for (int64_t i = 0; i < n; ++i) y[i] = (float)((double)x[i] * inv * (w ? (double)w[i] : 1.0));
+}
+
+/* gelu_pytorch_tanh with the reference's +-20 clamp (kernels/q40gu.wgsl:114) */
+static double gelu_d(double g) {
+  double t = 0.7978845608028654 * (g + 0.044715 * g * g * g);
+  if (t > 20.0) t = 20.0;
+  if (t < -20.0) t = -20.0;
+  return 0.5 * g * (1.0 + tanh(t));
+}
+float orc_gelu_tanh(float g) { return (float)gelu_d(g); }
+
+/* ------------------------------------------------------------------------ */
+/* Router + top-K (kernels/routertop.wgsl:19-71, same epilogue as           */
+/* kernels/top8.wgsl:9-29): scores = x.W_e; softmax; K rounds of a strict  */
+/* '>' scan from bv=-1 (ties -> lowest index), winner set to -2; w_k =     */
+/* p_k/sum, renormalised by sum of the K picks, times pes[idx_k].          */
+/* ------------------------------------------------------------------------ */
+void orc_router_topk(const float* x, const float* W, const float* pes, int H, int E, int K,
+                     uint32_t* idx, float* wts, float* scores) {
+  double* p = (double*)malloc(sizeof(double) * (size_t)E);
+  double mx = -3.0e38;
+  for (int e = 0; e < E; ++e) {
+    double s = 0.0;
+    for (int j = 0; j < H; ++j) s += (double)x[j] * (double)W[(int64_t)e * H + j];
+    float sf = (float)s; /* the reference stores f32 scores */
+    if (scores) scores[e] = sf;
+    p[e] = sf;
+    if (p[e] > mx) mx = p[e];
+  }
+  double sum = 0.0;
+  for (int e = 0; e < E; ++e) {
+    p[e] = exp(p[e] - mx);
+    sum += p[e];
+  }
+  double wk[64], wsum = 0.0;
+  for (int k = 0; k < K; ++k) {
+    int bi = 0;
+    double bv = -1.0;
+    for (int e = 0; e < E; ++e)
+      if (p[e] > bv) {
+        bv = p[e];
+        bi = e;
+      }
+    idx[k] = (uint32_t)bi;
+    wk[k] = bv / sum;
+    wsum += wk[k];
+    p[bi] = -2.0;
+  }
+  for (int k = 0; k < K; ++k) wts[k] = (float)(wk[k] / wsum * (double)pes[idx[k]]);
+  free(p);
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE inverse frequencies THETA^(-2p/HD) for p < angles, rounded once to  */
+/* f32; the angle is th = f32(pos) * inv[p] in f32, as headprep.wgsl:54-64 */
+/* forms fp * pow(THETA, -2p/HD).                                          */
+/* ------------------------------------------------------------------------ */
+void orc_rope_inv_freq(float theta, int head_dim, int angles, float* inv) {
+  for (int p = 0; p < angles; ++p) inv[p] = (float)pow((double)theta, -2.0 * (double)p / (double)head_dim);
+}
+
+/* headprep (kernels/headprep.wgsl:19-87): per head weighted RMS; q/k rotate  */
+/* pairs (p, p+HD/2) for p < angles; k and v (scale-less RMS) stored as f16. */
+static void prep_head(const float* x, int hd, int angles, const float* inv_freq, const float* w,
+                      float eps, uint32_t pos, double* out) {
+  double inv = rms_inv(x, hd, eps);
+  int half = hd / 2;
+  float fp = (float)pos;
+  for (int p = 0; p < half; ++p) {
+    double x0 = (double)x[p] * inv * (double)w[p];
+    double x1 = (double)x[p + half] * inv * (double)w[p + half];
+    if (p < angles) {
+      float th = fp * inv_freq[p];
+      double c = cos((double)th), s = sin((double)th);
+      out[p] = x0 * c - x1 * s;
+      out[p + half] = x0 * s + x1 * c;
+    } else {
+      out[p] = x0;
+      out[p + half] = x1;
+    }
+  }
+}
+
+void orc_headprep(const float* qkv, int qh, int kvh, int hd, int angles, const float* inv_freq,
+                  const float* qw, const float* kw, float eps, uint32_t pos, float* q_out,
+                  uint16_t* k_out, uint16_t* v_out) {
+  double tmp[1024];
+  for (int h = 0; h < qh; ++h) {
+    prep_head(qkv + h * hd, hd, angles, inv_freq, qw, eps, pos, tmp);
+    for (int d = 0; d < hd; ++d) q_out[h * hd + d] = (float)tmp[d];
+  }
+  for (int h = 0; h < kvh; ++h) {
+    prep_head(qkv + (qh + h) * hd, hd, angles, inv_freq, kw, eps, pos, tmp);
+    for (int d = 0; d < hd; ++d) k_out[h * hd + d] = orc_f2h((float)tmp[d]);
+    const float* v = qkv + (qh + kvh + h) * hd;
+    double inv = rms_inv(v, hd, eps);
+    for (int d = 0; d < hd; ++d) v_out[h * hd + d] = orc_f2h((float)((double)v[d] * inv));
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* KV ring slot recovery RecPs(t, m) = m - ((m + RING - t) % RING)           */
+/* (specs/KVRing.tla:45, kernels/attnf32.wgsl:50-52).                       */
+/* ------------------------------------------------------------------------ */
+int64_t orc_kvring_recover(int64_t t, int64_t mw, int64_t ring) {
+  return mw - ((mw + ring - t) % ring);
+}
+
+/* Softmax attention of one q head over a list of (slot) rows; scale 1.0    */
+/* (NOTES/arch-spec.md:383-392).  Dead rows are skipped: their contribution */
+/* is exactly 0 (the reference multiplies 0*v, kernels/attnf32.wgsl:89-90). */
+static void attn_rows(const float* q, const uint16_t* kc, const uint16_t* vc, int kvh, int h_kv,
+                      int hd, const int64_t* slots, int64_t n, uint16_t* out) {
+  double* s = (double*)malloc(sizeof(double) * (size_t)(n > 0 ? n : 1));
+  double m = -3.0e38;
+  for (int64_t i = 0; i < n; ++i) {
+    const uint16_t* k = kc + (slots[i] * kvh + h_kv) * hd;
+    double a = 0.0;
+    for (int d = 0; d < hd; ++d) a += (double)q[d] * (double)orc_h2f(k[d]);
+    s[i] = a;
+    if (a > m) m = a;
+  }
+  double den = 0.0;
+  double acc[1024];
+  for (int d = 0; d < hd; ++d) acc[d] = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    double e = exp(s[i] - m);
+    den += e;
+    const uint16_t* v = vc + (slots[i] * kvh + h_kv) * hd;
+    for (int d = 0; d < hd; ++d) acc[d] += e * (double)orc_h2f(v[d]);
+  }
+  for (int d = 0; d < hd; ++d) out[d] = orc_f2h((float)(acc[d] / den));
+  free(s);
+}
+
+/* attnf32 CACHEMODE 1 decode (kernels/attnf32.wgsl:21-105): qp = maxW = pos, */
+/* len = min(pos+1, RING); slot t dead iff ps > qp or ps + W <= qp.           */
+void orc_attn_ring(const float* q, const uint16_t* kc, const uint16_t* vc, int qh, int kvh,
+                   int hd, int ring, int window, uint32_t pos, uint16_t* out) {
+  int64_t qp = pos, mw = pos;
+  int64_t len = mw + 1 < ring ? mw + 1 : ring;
+  int64_t* slots = (int64_t*)malloc(sizeof(int64_t) * (size_t)len);
+  int64_t n = 0;
+  for (int64_t t = 0; t < len; ++t) {
+    int64_t ps = orc_kvring_recover(t, mw, ring);
+    int dead = ps > qp || ps + window <= qp;
+    if (!dead) slots[n++] = t;
+  }
+  for (int h = 0; h < qh; ++h)
+    attn_rows(q + h * hd, kc, vc, kvh, h / (qh / kvh), hd, slots, n, out + h * hd);
+  free(slots);
+}
+
+/* attnos full-layer decode (kernels/attnos.wgsl:22-98): positions 0..len-1. */
+void orc_attn_linear(const float* q, const uint16_t* kc, const uint16_t* vc, int qh, int kvh,
+                     int hd, uint32_t len, uint16_t* out) {
+  int64_t* slots = (int64_t*)malloc(sizeof(int64_t) * (size_t)(len ? len : 1));
+  for (uint32_t t = 0; t < len; ++t) slots[t] = t;
+  for (int h = 0; h < qh; ++h)
+    attn_rows(q + h * hd, kc, vc, kvh, h / (qh / kvh), hd, slots, len, out + h * hd);
+  free(slots);
+}
+
+/* Split-K phase A (kernels/attsplit.wgsl:16-76): chunk c covers positions  */
+/* [start + c*cs, min(start+(c+1)*cs, len)); start = len - window when the  */
+/* window is active.  Empty chunk -> (m, e) = (-3e38, 0).  part_o is the     */
+/* unnormalised sum e^{s-m_c} v; part_me = (m_c, sum e^{s-m_c}).            */
+void orc_attn_split(const float* q, const uint16_t* kc, const uint16_t* vc, int qh, int kvh,
+                    int hd, uint32_t len, int window, int chunks, int cs, float* part_o,
+                    float* part_me) {
+  int64_t start = (window != 0 && (int64_t)len > window) ? (int64_t)len - window : 0;
+  for (int h = 0; h < qh; ++h) {
+    int hk = h / (qh / kvh);
+    for (int c = 0; c < chunks; ++c) {
+      int64_t pi = (int64_t)h * chunks + c;
+      int64_t lo = start + (int64_t)c * cs;
+      float* po = part_o + pi * hd;
+      for (int d = 0; d < hd; ++d) po[d] = 0.0f;
+      if (lo >= (int64_t)len) {
+        part_me[2 * pi] = -3.0e38f;
+        part_me[2 * pi + 1] = 0.0f;
+        continue;
+      }
+      int64_t hi = lo + cs < (int64_t)len ? lo + cs : (int64_t)len;
+      double m = -3.0e38;
+      double* s = (double*)malloc(sizeof(double) * (size_t)(hi - lo));
+      for (int64_t t = lo; t < hi; ++t) {
+        const uint16_t* k = kc + (t * kvh + hk) * hd;
+        double a = 0.0;
+        for (int d = 0; d < hd; ++d) a += (double)q[h * hd + d] * (double)orc_h2f(k[d]);
+        s[t - lo] = a;
+        if (a > m) m = a;
+      }
+      double e = 0.0, acc[1024];
+      for (int d = 0; d < hd; ++d) acc[d] = 0.0;
+      for (int64_t t = lo; t < hi; ++t) {
+        double p = exp(s[t - lo] - m);
+        e += p;
+        const uint16_t* v = vc + (t * kvh + hk) * hd;
+        for (int d = 0; d < hd; ++d) acc[d] += p * (double)orc_h2f(v[d]);
+      }
+      free(s);
+      for (int d = 0; d < hd; ++d) po[d] = (float)acc[d];
+      part_me[2 * pi] = (float)m;
+      part_me[2 * pi + 1] = (float)e;
+    }
+  }
+}
+
+/* Split-K phase B (kernels/attcomb.wgsl:10-36): M = max m_c over the n live */
+/* chunks, o = sum_{e_c>0} partO_c e^{m_c-M} / sum e_c e^{m_c-M}; the        */
+/* reference then SRQ-packs for the E4B o-proj, this build stores f16.      */
+void orc_attn_combine(const float* part_o, const float* part_me, int qh, int hd, int n_chunks,
+                      int chunks, uint16_t* out) {
+  for (int h = 0; h < qh; ++h) {
+    double M = -3.0e38;
+    for (int c = 0; c < n_chunks; ++c) {
+      double m = part_me[2 * ((int64_t)h * chunks + c)];
+      if (m > M) M = m;
+    }
+    double den = 0.0;
+    for (int c = 0; c < n_chunks; ++c) {
+      const float* me = part_me + 2 * ((int64_t)h * chunks + c);
+      den += (double)me[1] * exp((double)me[0] - M);
+    }
+    for (int d = 0; d < hd; ++d) {
+      double a = 0.0;
+      for (int c = 0; c < n_chunks; ++c) {
+        const float* me = part_me + 2 * ((int64_t)h * chunks + c);
+        if (me[1] > 0.0f) a += (double)part_o[((int64_t)h * chunks + c) * hd + d] * exp((double)me[0] - M);
+      }
+      out[h * hd + d] = orc_f2h((float)(a / den));
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* KVRing.tla (specs/KVRing.tla:29-85) as a direct state walk: the spec's   */
+/* Next relation is deterministic, so TLC's reachable set is one behaviour. */
+/* Returns 0 = both invariants hold, 1 = SoundRec violated, 2 = Complete.  */
+/* ------------------------------------------------------------------------ */
+static int served(int64_t qp, int64_t m, int64_t W, int64_t RING) {
+  int64_t lo = qp + 1 >= W ? qp + 1 - W : 0;
+  for (int64_t p = lo; p <= qp; ++p)
+    if (orc_kvring_recover(p % RING, m, RING) != p) return 0;
+  return 1;
+}
+static int sound_rec(int64_t mw, int64_t RING) {
+  for (int64_t t = 0; t < RING; ++t) {
+    if (t > mw) continue;
+    int64_t r = orc_kvring_recover(t, mw, RING);
+    int64_t best = -1;
+    for (int64_t p = t; p <= mw; p += RING) best = p; /* max of S */
+    if (r != best) return 0;
+  }
+  return 1;
+}
+int orc_kvring_check(int W, int C, int RING, int NCHUNKS, int GEN) {
+  int64_t total = (int64_t)NCHUNKS * C;
+  int64_t mw = C - 1, base = 0;
+  int phase = 0; /* 0 pre, 1 gen, 2 done */
+  for (;;) {
+    if (!sound_rec(mw, RING)) return 1;
+    if (phase == 0) {
+      for (int64_t qp = base; qp <= base + C - 1; ++qp)
+        if (!served(qp, mw, W, RING)) return 2;
+    } else if (phase == 1) {
+      if (!served(mw, mw, W, RING)) return 2;
+    }
+    if (phase == 2) break;
+    if (phase == 0) {
+      if (base + C < total) {
+        mw = base + 2 * (int64_t)C - 1;
+        base = base + C;
+      } else if (GEN > 0) {
+        mw = mw + 1;
+        phase = 1;
+      } else {
+        phase = 2;
+      }
+    } else {
+      if (mw < total + GEN - 1)
+        mw = mw + 1;
+      else
+        phase = 2;
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoE FFN half-layer, A4B engine order (src/engine-a4b.js:438-462):         */
+/* rmsacc3's three scaled outputs (kernels/rmsacc3.wgsl:44-53, without the   */
+/* attention residual), routertop, q40gu EXPERT=2 (kernels/q40gu.wgsl:62-119) */
+/* for the dense branch and the K expert slots, dense q40mv down,            */
+/* q40moedown (kernels/q40moedown.wgsl:42-75) and a4btail                    */
+/* (kernels/a4btail.wgsl:26-71, NEXT=0).                                     */
+/* ------------------------------------------------------------------------ */
+static void geglu_rows(const uint8_t* gu, int64_t ff, int64_t in, const float* x, float* out_f16_as_f32) {
+  float* g = (float*)malloc(sizeof(float) * (size_t)ff * 2);
+  orc_q40_gemv(gu, 2 * ff, in, x, g);
+  for (int64_t i = 0; i < ff; ++i)
+    out_f16_as_f32[i] = orc_h2f(orc_f2h((float)(gelu_d(g[i]) * (double)g[ff + i])));
+  free(g);
+}
+
+void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
+                 float* dense_out, float* moe_out, float* h_out) {
+  const int H = m->hidden, E = m->n_experts, K = m->top_k, FF = m->expert_ffn, FF2 = m->dense_ffn;
+  float *xd = malloc(sizeof(float) * H), *xr = malloc(sizeof(float) * H), *xm = malloc(sizeof(float) * H);
+  double inv = rms_inv(h, H, m->eps);
+  double rs = 1.0 / sqrt((double)H); /* ffn_gate_inp.scale * H^-1/2, src/engine-a4b.js:174-179 */
+  for (int i = 0; i < H; ++i) {
+    double v = (double)h[i] * inv;
+    xd[i] = orc_h2f(orc_f2h((float)(v * (double)m->ffn_norm[i])));
+    xr[i] = (float)(v * (double)((float)((double)m->router_scale[i] * rs)));
+    xm[i] = orc_h2f(orc_f2h((float)(v * (double)m->pre_ffw2[i])));
+  }
+  orc_router_topk(xr, m->router_w, m->pes, H, E, K, topk_idx, topk_w, NULL);
+
+  /* dense branch: gate rows [0,FF2), up rows [FF2,2FF2) */
+  float* gd = malloc(sizeof(float) * FF2);
+  {
+    uint8_t* cat = malloc((size_t)2 * FF2 * (H / 32) * 18);
+    size_t half = (size_t)FF2 * (H / 32) * 18;
+    memcpy(cat, m->dense_gate, half);
+    memcpy(cat + half, m->dense_up, half);
+    geglu_rows(cat, FF2, H, xd, gd);
+    free(cat);
+  }
+  orc_q40_gemv(m->dense_down, H, FF2, gd, dense_out);
+
+  /* expert slots: sum_k w_k * W_down[e_k] . geglu_k */
+  float* ge = malloc(sizeof(float) * FF);
+  float* yk = malloc(sizeof(float) * H);
+  double* acc = calloc((size_t)H, sizeof(double));
+  const int64_t gu_stride = (int64_t)2 * FF * (H / 32) * 18;
+  for (int k = 0; k < K; ++k) {
+    int e = (int)topk_idx[k];
+    geglu_rows(m->exp_gate_up + e * gu_stride, FF, H, xm, ge);
+    orc_q40_gemv_expert(m->exp_down, e, H, FF, ge, yk);
+    for (int i = 0; i < H; ++i) acc[i] += (double)topk_w[k] * (double)yk[i];
+  }
+  for (int i = 0; i < H; ++i) moe_out[i] = (float)acc[i];
+
+  /* a4btail: comb = rms(t1) w1 + rms(m) w2; h = (h + rms(comb) wp) * MUL */
+  double i1 = rms_inv(dense_out, H, m->eps), i2 = rms_inv(moe_out, H, m->eps);
+  float* comb = malloc(sizeof(float) * H);
+  for (int i = 0; i < H; ++i)
+    comb[i] = (float)((double)dense_out[i] * i1 * (double)m->post_ffw1[i] +
+                      (double)moe_out[i] * i2 * (double)m->post_ffw2[i]);
+  double i3 = rms_inv(comb, H, m->eps);
+  for (int i = 0; i < H; ++i)
+    h_out[i] = (float)(((double)h[i] + (double)comb[i] * i3 * (double)m->post_ffw[i]) * (double)m->layer_scale);
+  free(xd); free(xr); free(xm); free(gd); free(ge); free(yk); free(acc); free(comb);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Full E4B-shaped decode step.  Layer order follows the A4B engine's        */
+/* encodeLayer (src/engine-a4b.js:424-463) for the attention/FFN halves and  */
+/* the E4B engine's PLE dataflow (src/engine.js:282-323, kernels/pleprep.wgsl */
+/* :15-46, kernels/plegatemv.wgsl:20-60) with the SRQ int8 steps dropped;    */
+/* the lm-head is the tied Q6_K embedding with softcap, then argmax          */
+/* (src/engine-a4b.js:683-693).                                             */
+/* ------------------------------------------------------------------------ */
+struct orc_state {
+  int layers;
+  uint16_t** kc;
+  uint16_t** vc;
+  float* ple; /* [layers][ple_dim] per-layer inputs of the current token */
+};
+
+static int64_t slots_of(const orc_model* m, int l) {
+  return m->layer_global[l] ? m->max_seq : m->ring;
+}
+
+orc_state* orc_state_new(const orc_model* m) {
+  orc_state* s = calloc(1, sizeof(orc_state));
+  s->layers = m->layers;
+  s->kc = calloc((size_t)m->layers, sizeof(uint16_t*));
+  s->vc = calloc((size_t)m->layers, sizeof(uint16_t*));
+  for (int l = 0; l < m->layers; ++l) {
+    size_t n = (size_t)slots_of(m, l) * m->kv_heads * m->head_dim;
+    s->kc[l] = calloc(n, sizeof(uint16_t));
+    s->vc[l] = calloc(n, sizeof(uint16_t));
+  }
+  s->ple = calloc((size_t)m->layers * (m->ple_dim > 0 ? m->ple_dim : 1), sizeof(float));
+  return s;
+}
+void orc_state_free(orc_state* s) {
+  if (!s) return;
+  for (int l = 0; l < s->layers; ++l) {
+    free(s->kc[l]);
+    free(s->vc[l]);
+  }
+  free(s->kc);
+  free(s->vc);
+  free(s->ple);
+  free(s);
+}
+const uint16_t* orc_state_kcache(const orc_state* s, int layer) { return s->kc[layer]; }
+const uint16_t* orc_state_vcache(const orc_state* s, int layer) { return s->vc[layer]; }
+
+int64_t orc_kv_slot(const orc_model* m, int is_global, uint32_t pos) {
+  return is_global ? (int64_t)pos : (int64_t)(pos % (uint32_t)m->ring);
+}
+
+static void round_f16(float* x, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) x[i] = orc_h2f(orc_f2h(x[i]));
+}
+
+uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t pos, float* logits,
+                  float* hidden_out) {
+  const int H = m->hidden, QH = m->q_heads, KVH = m->kv_heads, HD = m->head_dim;
+  const int FF = m->ffn, PD = m->ple_dim, L = m->layers;
+  const int QKV = (QH + 2 * KVH) * HD;
+  float* h = malloc(sizeof(float) * H);
+  float* x = malloc(sizeof(float) * (FF > QKV ? FF : QKV) * 2);
+  float* qkv = malloc(sizeof(float) * QKV);
+  float* qp = malloc(sizeof(float) * QH * HD);
+  uint16_t* ao = malloc(sizeof(uint16_t) * QH * HD);
+  float* a = malloc(sizeof(float) * QH * HD);
+  float* o = malloc(sizeof(float) * H);
+  float* gu = malloc(sizeof(float) * 2 * FF);
+  float* gg = malloc(sizeof(float) * FF);
+  float* inv_l = malloc(sizeof(float) * HD);
+  float* inv_g = malloc(sizeof(float) * HD);
+  orc_rope_inv_freq(m->theta_local, HD, m->rope_angles, inv_l);
+  orc_rope_inv_freq(m->theta_global, HD, m->rope_angles, inv_g);
+
+  /* embedding row * sqrt(H) (kernels/q6k.wgsl:37-73, MULT = sqrt(hidden)) */
+  orc_q6k_dequant_row(m->tok_embd, H, token, (float)sqrt((double)H), h);
+
+  if (PD > 0) {
+    /* PLE inputs: proj = W_pm h * H^-1/2; per block b:                      */
+    /* (rms(proj_b) * w_pn + row_b(token) * sqrt(PD)) * 2^-1/2             */
+    const int NP = L * PD;
+    float* proj = malloc(sizeof(float) * NP);
+    float* idv = malloc(sizeof(float) * NP);
+    orc_q40_gemv(m->ple_proj, NP, H, h, proj);
+    double sc = 1.0 / sqrt((double)H);
+    for (int i = 0; i < NP; ++i) proj[i] = (float)((double)proj[i] * sc);
+    orc_q6k_dequant_row(m->ple_tab, NP, token, (float)sqrt((double)PD), idv);
+    for (int b = 0; b < L; ++b) {
+      double inv = rms_inv(proj + b * PD, PD, m->eps);
+      for (int i = 0; i < PD; ++i)
+        st->ple[b * PD + i] = (float)(((double)proj[b * PD + i] * inv * (double)m->ple_proj_norm[i] +
+                                       (double)idv[b * PD + i]) * 0.70710678118654752);
+    }
+    free(proj);
+    free(idv);
+  }
+
+  for (int l = 0; l < L; ++l) {
+    const orc_layer* ly = &m->L[l];
+    const int glob = m->layer_global[l];
+    /* attention block */
+    orc_rmsnorm(h, ly->attn_norm, H, m->eps, x);
+    round_f16(x, H);
+    orc_q40_gemv(ly->wq, QH * HD, H, x, qkv);
+    orc_q40_gemv(ly->wk, KVH * HD, H, x, qkv + QH * HD);
+    orc_q40_gemv(ly->wv, KVH * HD, H, x, qkv + (QH + KVH) * HD);
+    int64_t slot = orc_kv_slot(m, glob, pos);
+    orc_headprep(qkv, QH, KVH, HD, m->rope_angles, glob ? inv_g : inv_l, ly->q_norm, ly->k_norm,
+                 m->eps, pos, qp, st->kc[l] + slot * KVH * HD, st->vc[l] + slot * KVH * HD);
+    if (glob)
+      orc_attn_linear(qp, st->kc[l], st->vc[l], QH, KVH, HD, pos + 1, ao);
+    else
+      orc_attn_ring(qp, st->kc[l], st->vc[l], QH, KVH, HD, m->ring, m->window, pos, ao);
+    orc_h2f_n(ao, QH * HD, a);
+    orc_q40_gemv(ly->wo, H, QH * HD, a, o);
+    /* h1 = h + rms(o) w_pa; x = f16(rms(h1) w_ffn) (kernels/rmsacc3.wgsl:36-53) */
+    {
+      double io = rms_inv(o, H, m->eps);
+      for (int i = 0; i < H; ++i) h[i] = (float)((double)h[i] + (double)o[i] * io * (double)ly->post_attn_norm[i]);
+    }
+    orc_rmsnorm(h, ly->ffn_norm, H, m->eps, x);
+    round_f16(x, H);
+    /* gate/up + GeGLU -> f16 (kernels/q40gu.wgsl:62-119) */
+    orc_q40_gemv(ly->wgate, FF, H, x, gu);
+    orc_q40_gemv(ly->wup, FF, H, x, gu + FF);
+    for (int i = 0; i < FF; ++i) gg[i] = orc_h2f(orc_f2h((float)(gelu_d(gu[i]) * (double)gu[FF + i])));
+    orc_q40_gemv(ly->wdown, H, FF, gg, o);
+    {
+      double io = rms_inv(o, H, m->eps);
+      for (int i = 0; i < H; ++i) h[i] = (float)((double)h[i] + (double)o[i] * io * (double)ly->post_ffw_norm[i]);
+    }
+    if (PD > 0) {
+      /* PLE block: g = f16(gelu(W_gate f16(h)) * ple_l); p = W_proj g;       */
+      /* h = (h + rms(p) w_post) * layer_scale                                */
+      for (int i = 0; i < H; ++i) x[i] = orc_h2f(orc_f2h(h[i]));
+      float* pg = gu;
+      orc_q40_gemv(ly->inp_gate, PD, H, x, pg);
+      for (int i = 0; i < PD; ++i)
+        gg[i] = orc_h2f(orc_f2h((float)(gelu_d(pg[i]) * (double)st->ple[l * PD + i])));
+      orc_q40_gemv(ly->proj, H, PD, gg, o);
+      double io = rms_inv(o, H, m->eps);
+      for (int i = 0; i < H; ++i)
+        h[i] = (float)(((double)h[i] + (double)o[i] * io * (double)ly->post_norm[i]) * (double)ly->layer_scale);
+    } else {
+      for (int i = 0; i < H; ++i) h[i] = (float)((double)h[i] * (double)ly->layer_scale);
+    }
+  }
+  if (hidden_out) memcpy(hidden_out, h, sizeof(float) * H);
+
+  /* final norm (f32) -> Q6_K lm-head + softcap -> argmax */
+  orc_rmsnorm(h, m->out_norm, H, m->eps, x);
+  float* lg = logits ? logits : malloc(sizeof(float) * (size_t)m->vocab);
+  orc_q6k_gemv(m->tok_embd, m->vocab, H, x, m->softcap, lg);
+  uint32_t am[2];
+  orc_argmax(lg, m->vocab, am);
+  if (!logits) free(lg);
+  free(h); free(x); free(qkv); free(qp); free(ao); free(a); free(o); free(gu); free(gg);
+  free(inv_l); free(inv_g);
+  return am[0];
+}

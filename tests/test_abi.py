@@ -1,0 +1,126 @@
+"""C-ABI surface and host-side code of libe4b.so (no GPU needed).
+
+* every function declared in include/e4b.h is exported by the library and
+  bound in e4b._lib;
+* the seeded generator reproduces the published splitmix64 sequence;
+* the packed q4_0 / Q6_K device layouts, decoded here in numpy exactly as
+  the kernels decode them, reproduce the oracle's ggml dequantisation.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from e4b import _lib, formats
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    txt = open(os.path.join(ROOT, "include", "e4b.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(e4b_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    decl = declared_functions()
+    assert len(decl) >= 20
+    bound = set(_lib.exported_symbols())
+    for name in decl:
+        assert hasattr(_lib.lib, name), f"{name} declared in e4b.h but not exported"
+        assert name in bound, f"{name} declared in e4b.h but not bound in e4b._lib"
+
+
+def test_version_and_error_channel():
+    assert b"gfx950" in _lib.lib.e4b_version()
+    rc = _lib.lib.e4b_q40_pack(None, 1, 33, None)
+    assert rc == _lib.E4B_EINVAL
+    assert "e4b_q40_pack" in _lib.last_error()
+
+
+def test_splitmix64_known_answers():
+    # splitmix64 seeded with 0: 0xe220a8397b1dcdaf, 0x6e789e6aa1b965f4, 0x06c45d188009454f
+    assert formats.synth_u64(0, 0) == 0xE220A8397B1DCDAF
+    assert formats.synth_u64(0, 1) == 0x6E789E6AA1B965F4
+    assert formats.synth_u64(0, 2) == 0x06C45D188009454F
+
+
+def test_synth_distributions():
+    x = formats.synth_normal(1, 200000)
+    assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1.0) < 0.01
+    u = formats.synth_uniform_u32(2, 100000, 0, 262144)
+    assert u.min() >= 0 and u.max() < 262144
+    w = formats.synth_q40(3, 64, 2048, 0.02)
+    d = w.reshape(-1, 18)[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+    assert np.all(d >= 0) and abs(d.mean() / (0.02 / 8 * np.sqrt(2 / np.pi)) - 1) < 0.05
+    q6 = formats.synth_q6k(4, 32, 2048, 1e-3).reshape(-1, 210)
+    sc = q6[:, 192:208].view(np.int8)
+    assert sc.min() == -32 and sc.max() == 31
+
+
+def unpack_q40(packed, rows, cols):
+    """numpy decode of the packed q4_0 layout, mirroring q40_dot in common.h"""
+    nb = cols // 32
+    nib = packed[: rows * nb * 16].view(np.uint32).reshape(rows, nb, 4)
+    off = (rows * nb * 16 + 255) // 256 * 256
+    sc = packed[off: off + rows * nb * 2].view(np.float16).astype(np.float64).reshape(rows, nb)
+    out = np.zeros((rows, nb, 32))
+    for k in range(4):
+        w = nib[:, :, k]
+        for i, s in enumerate((0, 8, 4, 12)):
+            out[:, :, 8 * k + 2 * i] = (w >> s) & 15
+            out[:, :, 8 * k + 2 * i + 1] = (w >> (s + 16)) & 15
+    return ((out - 8) * sc[:, :, None]).reshape(rows, cols)
+
+
+def unpack_q6k(packed, rows, cols):
+    """numpy decode of the packed Q6_K layout, mirroring q6_pairs in common.h"""
+    nseg, ngrp, nsb = cols // 32, cols // 16, cols // 256
+    a256 = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    o_qb = a256(rows * nseg * 16)
+    o_sc = o_qb + a256(rows * nseg * 8)
+    o_d = o_sc + a256(rows * ngrp)
+    qa = packed[: rows * nseg * 16].view(np.uint32).reshape(rows, nseg, 4)
+    qb = packed[o_qb: o_qb + rows * nseg * 8].view(np.uint32).reshape(rows, nseg, 2)
+    sc = packed[o_sc: o_sc + rows * ngrp].view(np.int8).astype(np.float64).reshape(rows, ngrp)
+    d = packed[o_d: o_d + rows * nsb * 2].view(np.float16).astype(np.float64).reshape(rows, nsb)
+    out = np.zeros((rows, nseg, 32))
+    M6, M4, MH = 0x3F003F, 0xF000F, 0x300030
+    for g in range(2):
+        w0, w1, w2 = qa[:, :, 2 * g], qa[:, :, 2 * g + 1], qb[:, :, g]
+        pairs = [w0 & M6, (w0 >> 6) & M6, ((w0 >> 12) & M4) | ((w2 >> 8) & MH), w1 & M6, (w1 >> 6) & M6,
+                 ((w1 >> 12) & M4) | ((w2 >> 10) & MH), w2 & M6, (w2 >> 6) & M6]
+        for i, p in enumerate(pairs):
+            out[:, :, 16 * g + 2 * i] = p & 0x3F
+            out[:, :, 16 * g + 2 * i + 1] = (p >> 16) & 0x3F
+    out = out.reshape(rows, ngrp, 16) - 32
+    dd = np.repeat(d, 16, axis=1)
+    return (out * sc[:, :, None] * dd[:, :, None]).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols", [(5, 32), (7, 2048), (3, 704)])
+def test_q40_pack_roundtrip(rows, cols):
+    w = formats.synth_q40(7, rows, cols)
+    packed = formats.q40_pack(w, rows, cols)
+    assert packed.nbytes == _lib.lib.e4b_q40_packed_bytes(rows, cols)
+    np.testing.assert_array_equal(unpack_q40(packed, rows, cols), orc.q40_dequant(w).reshape(rows, cols))
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 256), (5, 2048), (2, 2816 // 256 * 256)])
+def test_q6k_pack_roundtrip(rows, cols):
+    w = formats.synth_q6k(8, rows, cols)
+    packed = formats.q6k_pack(w, rows, cols)
+    assert packed.nbytes == _lib.lib.e4b_q6k_packed_bytes(rows, cols)
+    got = unpack_q6k(packed, rows, cols)
+    want = np.stack([orc.q6k_row(w, cols, r) for r in range(rows)])
+    np.testing.assert_allclose(got, want, rtol=1e-7, atol=0)
+
+
+def test_tensor_bytes_matches_gguf_js():
+    assert formats.tensor_bytes(_lib.GGML_Q4_0, [2048, 16384]) == 16384 * 64 * 18
+    assert formats.tensor_bytes(_lib.GGML_Q6_K, [2048, 262144]) == 262144 * 8 * 210
+    assert formats.tensor_bytes(_lib.GGML_F32, [7]) == 28
+    with pytest.raises(ValueError):
+        formats.tensor_bytes(_lib.GGML_Q4_0, [33])
