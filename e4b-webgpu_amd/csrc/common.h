@@ -112,6 +112,98 @@ DEV float group_sum(float v, int lpr) {
   return v;
 }
 
+// ---- cross-lane exchange (wave64) -------------------------------------------
+// swapx32(a, b): lanes [32,64) of a <-> lanes [0,32) of b (v_permlane32_swap);
+// swapx16(a, b): odd 16-lane rows of a <-> even rows of b (v_permlane16_swap).
+// After either, a + b on every lane is "my own value of the half I keep plus
+// my partner's value of the same half", i.e. one transposed-butterfly step.
+DEV void swapx32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+DEV void swapx16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+// value of lane (l ^ m) for m in {1, 2, 4, 8}
+template <int M>
+DEV float lane_xor(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "lane_xor: 1, 2, 4 or 8");
+  const int iv = __float_as_int(v);
+  if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, true));
+  if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, true));
+  if constexpr (M == 4) return __int_as_float(__builtin_amdgcn_ds_swizzle(iv, 0x101F));
+  if constexpr (M == 8) return __int_as_float(__builtin_amdgcn_ds_swizzle(iv, 0x201F));
+  return v;
+}
+
+// One transposed step with lane-distance M on the pair (lo, hi): lanes whose
+// bit M is clear keep the `lo` row, the others keep `hi`; the result is the
+// kept row's partial summed over the lane pair.
+template <int M>
+DEV float tstep(float lo, float hi) {
+  if constexpr (M == 32) {
+    swapx32(lo, hi);
+    return lo + hi;
+  } else if constexpr (M == 16) {
+    swapx16(lo, hi);
+    return lo + hi;
+  } else {
+    const float plo = lane_xor<M>(lo), phi = lane_xor<M>(hi);
+    const bool up = (threadIdx.x & M) != 0;
+    return up ? hi + phi : lo + plo;
+  }
+}
+template <int M>
+DEV float xsum_step(float s) {
+  if constexpr (M == 32) {
+    float t = s;
+    swapx32(s, t);
+    return s + t;
+  } else if constexpr (M == 16) {
+    float t = s;
+    swapx16(s, t);
+    return s + t;
+  } else {
+    return s + lane_xor<M>(s);
+  }
+}
+
+template <int LPR, int R, int N>
+struct RowReduce {
+  // N partials remain, next step distance M = LPR * N / (2 R)
+  static DEV float run(float* v) {
+    constexpr int M = LPR * N / (2 * R);
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) v[i] = tstep<M>(v[i], v[N / 2 + i]);
+    return RowReduce<LPR, R, N / 2>::run(v);
+  }
+};
+template <int LPR, int R>
+struct RowReduce<LPR, R, 1> {
+  template <int M>
+  static DEV float tail(float s) {
+    if constexpr (M == 0) {
+      return s;
+    } else {
+      return tail<M / 2>(xsum_step<M>(s));
+    }
+  }
+  static DEV float run(float* v) { return tail<LPR / (2 * R)>(v[0]); }
+};
+
+// Transposed butterfly inside LPR-lane groups: lane l of a group holds
+// partials v[0..R) of R rows; on return it holds the group total of row
+// l / (LPR/R).  R-1 exchanges + log2(LPR/R) reduction steps instead of
+// R*log2(LPR) shuffles.  R <= LPR, powers of two.
+template <int LPR, int R>
+DEV float reduce_rows(float (&v)[R]) {
+  static_assert(R <= LPR && (R & (R - 1)) == 0 && (LPR & (LPR - 1)) == 0, "powers of two, R <= LPR");
+  return RowReduce<LPR, R, R>::run(v);
+}
+
 // non-temporal 16 B load for streamed weights (read once per token)
 typedef uint32_t e4b_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t e4b_u32x2 __attribute__((ext_vector_type(2)));

@@ -54,10 +54,29 @@ struct Workspace {
 #define E4B_NCOUNTERS 4096
 int e4b_workspace(size_t bytes, Workspace* ws);
 
+// q4_0 GEMV epilogues
+enum GemvEpi {
+  EPI_F32 = 0,       // y[ks * rows + row] = dot                       (partials when KS > 1)
+  EPI_GEGLU = 1,     // rows [0,FF) gate, [FF,2FF) up: yh[i] = f16(gelu(g_i) * u_i)
+  EPI_GELU_MUL = 2,  // yh[row] = f16(gelu(dot) * mul[row])
+};
+struct GemvOut {
+  float* y;          // EPI_F32 output (KS slices of `rows` each)
+  uint16_t* yh;      // f16 output of EPI_GEGLU / EPI_GELU_MUL
+  const float* mul;  // EPI_GELU_MUL multiplier
+  int64_t ff;        // EPI_GEGLU: rows per half
+};
+
 // launchers (defined in k_gemv.hip); all asynchronous on `st`
+// ks > 1 splits the columns into ks equal slices (cols/32 divisible by ks)
+// and writes ks partial vectors (EPI_F32 only).
+int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi, const GemvOut& o, int ks,
+               hipStream_t st);
 int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st);
 int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st);
+// part: one (index, value) partial per block (<= 2048); amax may be NULL to
+// leave the fold to the caller (k_amax_final semantics)
 int launch_q6k_gemv_argmax(const Q6Mat& W, const uint32_t* xh, const uint32_t* xl, float softcap,
-                           float* logits, uint32_t* amax, uint2* part, uint32_t* counter, hipStream_t st);
+                           float* logits, uint32_t* amax, uint2* part, hipStream_t st);
 int launch_q6k_row(const Q6Mat& W, int64_t row, const uint32_t* row_dev, float mult, float* out, hipStream_t st);
-int launch_argmax(const float* x, int64_t n, uint32_t* amax, uint2* part, uint32_t* counter, hipStream_t st);
+int launch_argmax(const float* x, int64_t n, uint32_t* amax, uint2* part, hipStream_t st);

@@ -175,7 +175,7 @@ extern "C" int e4b_k_q6k_gemv_argmax(const void* w_packed, int64_t rows, int64_t
   uint2* part = (uint2*)(ws.buf + 2 * half);
   if ((rc = launch_split_f32(x, cols, hi, lo, st))) return rc;
   return launch_q6k_gemv_argmax(q6_view(w_packed, rows, cols), (const uint32_t*)hi, (const uint32_t*)lo, softcap,
-                                logits, amax, part, &ws.counters[0], st);
+                                logits, amax, part, st);
 }
 
 extern "C" int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row, float mult, float* out,
@@ -191,5 +191,5 @@ extern "C" int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* str
   Workspace ws;
   int rc = e4b_workspace(1024 * sizeof(uint2), &ws);
   if (rc) return rc;
-  return launch_argmax(x, n, amax, (uint2*)ws.buf, &ws.counters[1], (hipStream_t)stream);
+  return launch_argmax(x, n, amax, (uint2*)ws.buf, (hipStream_t)stream);
 }
