@@ -1,0 +1,608 @@
+// engine.hip -- the batch-1 decode engine behind the e4b_* context ABI.
+//
+// Host orchestration of one token (the A4B engine's encodeForward /
+// encodeLayer order, src/engine-a4b.js:424-463, 683-693, with the E4B per-layer
+// embedding dataflow of src/engine.js:282-323), captured once into a hipGraph
+// and replayed per token.  Every kernel reads the position / token from the
+// device-side params block, and the last kernel feeds the argmax back as the
+// next input token, so GPU-fed decode needs no host work between tokens.
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/e4b.h"
+#include "kernels.h"
+#include "step.h"
+#include "util.h"
+
+namespace {
+
+enum LayerPart {
+  P_ATTN_NORM, P_Q, P_K, P_V, P_Q_NORM, P_K_NORM, P_O, P_POST_ATTN, P_FFN_NORM, P_GATE, P_UP, P_DOWN,
+  P_POST_FFW, P_INP_GATE, P_PROJ, P_POST_NORM, P_SCALE, P_COUNT
+};
+const char* kPartNames[P_COUNT] = {
+    "attn_norm", "attn_q", "attn_k", "attn_v", "attn_q_norm", "attn_k_norm", "attn_output", "post_attention_norm",
+    "ffn_norm", "ffn_gate", "ffn_up", "ffn_down", "post_ffw_norm", "inp_gate", "proj", "post_norm",
+    "layer_output_scale"};
+
+struct Layer {
+  bool global = false;
+  uint8_t* qkv = nullptr;  // packed q4_0 [(QH + 2 KVH) HD][H]: q rows, k rows, v rows
+  uint8_t* o = nullptr;    // [H][QH HD]
+  uint8_t* gu = nullptr;   // [2 FF][H]: gate rows, then up rows
+  uint8_t* down = nullptr; // [H][FF]
+  uint8_t* pg = nullptr;   // PLE gate [PD][H]
+  uint8_t* pp = nullptr;   // PLE proj [H][PD]
+  float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr, *ffn_norm = nullptr,
+        *post_ffw = nullptr, *post_norm = nullptr;
+  float scale = 1.0f;
+  uint16_t *kc = nullptr, *vc = nullptr;
+  int slots = 0;
+  uint32_t have = 0;
+};
+
+}  // namespace
+
+struct e4b_ctx {
+  e4b_config cfg;
+  std::vector<uint8_t> lglobal;
+  hipStream_t st = nullptr;
+  std::vector<void*> allocs;
+  // weights
+  uint8_t* embd = nullptr;      // packed Q6_K [V][H] (embedding + tied lm-head)
+  float* out_norm = nullptr;
+  uint8_t* ple_tab = nullptr;   // ggml Q6_K blocks [V][L PD]
+  uint8_t* ple_proj = nullptr;  // packed q4_0 [L PD][H]
+  float* ple_norm = nullptr;    // [PD]
+  std::vector<Layer> L;
+  float* inv_local = nullptr;
+  float* inv_global = nullptr;
+  // state / activations
+  uint32_t *params = nullptr, *prompt = nullptr, *tok_ring = nullptr, *amax = nullptr, *status = nullptr;
+  float *h = nullptr, *proj = nullptr, *ple = nullptr, *qkv = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  float *o = nullptr, *dn = nullptr, *pp = nullptr, *logits = nullptr;
+  uint16_t *h_hl = nullptr, *xn = nullptr, *attn = nullptr, *xf = nullptr, *gg = nullptr, *xg = nullptr,
+           *gp = nullptr, *xo_hl = nullptr;
+  uint2* amax_part = nullptr;
+  int nch = 16, ks_down = 1, ring_cap = 0, max_prompt = 0, amax_parts = 0;
+  int64_t qkv_rows = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool finalized = false;
+};
+
+namespace {
+
+int dalloc(e4b_ctx* c, void** p, size_t bytes) {
+  hipError_t e = hipMalloc(p, bytes ? bytes : 16);
+  if (e != hipSuccess) return e4b_fail(E4B_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  c->allocs.push_back(*p);
+  return E4B_OK;
+}
+template <typename T>
+int dalloc_t(e4b_ctx* c, T** p, size_t count) {
+  return dalloc(c, reinterpret_cast<void**>(p), count * sizeof(T));
+}
+
+// pack `rows` q4_0 rows and place them at row offset `row_off` of a packed
+// matrix with `total_rows` rows (row-concatenation of same-width linears, the
+// q40cat of src/engine-a4b.js:126-138)
+int upload_q40_rows(uint8_t* dst, int64_t total_rows, int64_t cols, int64_t row_off, const void* ggml,
+                    int64_t rows) {
+  std::vector<uint8_t> tmp(e4b_q40_packed_bytes(rows, cols));
+  int rc = e4b_q40_pack(ggml, rows, cols, tmp.data());
+  if (rc) return rc;
+  const size_t nb = (size_t)(cols / 32);
+  const size_t nib_bytes = (size_t)rows * nb * 16, sc_bytes = (size_t)rows * nb * 2;
+  const size_t dst_sc = E4B_ALIGN256((size_t)total_rows * nb * 16);
+  E4B_HIP(hipMemcpy(dst + (size_t)row_off * nb * 16, tmp.data(), nib_bytes, hipMemcpyHostToDevice));
+  E4B_HIP(hipMemcpy(dst + dst_sc + (size_t)row_off * nb * 2, tmp.data() + E4B_ALIGN256(nib_bytes), sc_bytes,
+                    hipMemcpyHostToDevice));
+  return E4B_OK;
+}
+
+int upload_f32(e4b_ctx* c, float** dst, const void* bytes, int64_t n) {
+  if (!*dst) {
+    int rc = dalloc_t(c, dst, (size_t)n);
+    if (rc) return rc;
+  }
+  E4B_HIP(hipMemcpy(*dst, bytes, (size_t)n * 4, hipMemcpyHostToDevice));
+  return E4B_OK;
+}
+
+int64_t nelems(const int64_t* dims, int nd) {
+  int64_t n = 1;
+  for (int i = 0; i < nd; ++i) n *= dims[i];
+  return n;
+}
+
+int expect(const char* name, int type, int want_type, const int64_t* dims, int nd, int64_t cols, int64_t rows) {
+  if (type != want_type) return e4b_fail(E4B_EINVAL, "%s: ggml type %d, expected %d", name, type, want_type);
+  const int64_t d0 = nd > 0 ? dims[0] : 1, d1 = nd > 1 ? dims[1] : 1;
+  if (d0 != cols || d1 != rows || nd > 2)
+    return e4b_fail(E4B_EINVAL, "%s: dims [%lld, %lld], expected [%lld, %lld]", name, (long long)d0, (long long)d1,
+                    (long long)cols, (long long)rows);
+  return E4B_OK;
+}
+
+int record_step(e4b_ctx* c);
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+extern "C" e4b_ctx* e4b_create(const e4b_config* cfg) {
+  if (!cfg) {
+    e4b_fail(E4B_EINVAL, "e4b_create: null config");
+    return nullptr;
+  }
+  const e4b_config& k = *cfg;
+  if (k.hidden <= 0 || k.hidden % 256 || k.hidden > 4096 || k.layers <= 0 || k.head_dim != 256 || k.kv_heads <= 0 ||
+      k.q_heads != 4 * k.kv_heads || k.ffn <= 0 || k.ffn % 32 || k.vocab <= 0 ||
+      (k.ple_dim != 0 && k.ple_dim != 256) || k.window <= 0 || k.ring < k.window || k.max_seq <= 0 ||
+      k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || k.attn_chunks < 0 || k.max_prompt < 0) {
+    e4b_fail(E4B_EINVAL,
+             "e4b_create: unsupported config (hidden %d multiple of 256 and <= 4096, head_dim 256, q_heads = 4 * "
+             "kv_heads, ple_dim 0 or 256, ring >= window)",
+             k.hidden);
+    return nullptr;
+  }
+  e4b_ctx* c = new e4b_ctx();
+  c->cfg = k;
+  c->lglobal.resize(k.layers);
+  for (int i = 0; i < k.layers; ++i) c->lglobal[i] = k.layer_global ? (k.layer_global[i] != 0) : (i % 5 == 4);
+  c->cfg.layer_global = nullptr;
+  c->L.resize(k.layers);
+  for (int i = 0; i < k.layers; ++i) c->L[i].global = c->lglobal[i] != 0;
+  c->qkv_rows = (int64_t)(k.q_heads + 2 * k.kv_heads) * k.head_dim;
+  hipError_t e = hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    e4b_fail(E4B_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+    delete c;
+    return nullptr;
+  }
+  return c;
+}
+
+extern "C" int e4b_set_tensor(e4b_ctx* c, const char* name, int type, const int64_t* dims, int nd,
+                              const void* bytes, size_t nbytes) {
+  if (!c || !name || !bytes || (nd > 0 && !dims)) return e4b_fail(E4B_EINVAL, "e4b_set_tensor: null argument");
+  if (c->finalized) return e4b_fail(E4B_ESTATE, "e4b_set_tensor(%s) after e4b_finalize", name);
+  const e4b_config& k = c->cfg;
+  const int64_t H = k.hidden, V = k.vocab, PD = k.ple_dim, LPD = (int64_t)k.layers * k.ple_dim;
+  const int64_t n = nelems(dims, nd);
+  int rc;
+  auto check_bytes = [&](size_t want) -> int {
+    if (nbytes != want)
+      return e4b_fail(E4B_EINVAL, "%s: %zu bytes, expected %zu", name, nbytes, want);
+    return E4B_OK;
+  };
+  const std::string nm(name);
+  if (nm == "token_embd.weight") {
+    if ((rc = expect(name, type, E4B_GGML_Q6_K, dims, nd, H, V)) || (rc = check_bytes((size_t)(V * H / 256) * 210)))
+      return rc;
+    const size_t pb = e4b_q6k_packed_bytes(V, H);
+    if (!c->embd && (rc = dalloc(c, (void**)&c->embd, pb))) return rc;
+    std::vector<uint8_t> tmp(pb);
+    if ((rc = e4b_q6k_pack(bytes, V, H, tmp.data()))) return rc;
+    E4B_HIP(hipMemcpy(c->embd, tmp.data(), pb, hipMemcpyHostToDevice));
+    return E4B_OK;
+  }
+  if (nm == "output_norm.weight") {
+    if ((rc = expect(name, type, E4B_GGML_F32, dims, nd, H, 1)) || (rc = check_bytes((size_t)H * 4))) return rc;
+    return upload_f32(c, &c->out_norm, bytes, H);
+  }
+  if (nm == "per_layer_token_embd.weight") {
+    if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
+    if ((rc = expect(name, type, E4B_GGML_Q6_K, dims, nd, LPD, V)) || (rc = check_bytes((size_t)(V * LPD / 256) * 210)))
+      return rc;
+    if (!c->ple_tab && (rc = dalloc(c, (void**)&c->ple_tab, nbytes))) return rc;
+    E4B_HIP(hipMemcpy(c->ple_tab, bytes, nbytes, hipMemcpyHostToDevice));
+    return E4B_OK;
+  }
+  if (nm == "per_layer_model_proj.weight") {
+    if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
+    if ((rc = expect(name, type, E4B_GGML_Q4_0, dims, nd, H, LPD)) || (rc = check_bytes((size_t)(LPD * H / 32) * 18)))
+      return rc;
+    if (!c->ple_proj && (rc = dalloc(c, (void**)&c->ple_proj, e4b_q40_packed_bytes(LPD, H)))) return rc;
+    return upload_q40_rows(c->ple_proj, LPD, H, 0, bytes, LPD);
+  }
+  if (nm == "per_layer_proj_norm.weight") {
+    if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
+    if ((rc = expect(name, type, E4B_GGML_F32, dims, nd, PD, 1)) || (rc = check_bytes((size_t)PD * 4))) return rc;
+    return upload_f32(c, &c->ple_norm, bytes, PD);
+  }
+  // blk.N.part.weight
+  int li = -1, used = 0;
+  char part[64] = {0};
+  if (sscanf(name, "blk.%d.%63[a-z_0-9].weight%n", &li, part, &used) != 2 || (size_t)used != nm.size() || li < 0 ||
+      li >= k.layers)
+    return e4b_fail(E4B_EINVAL, "e4b_set_tensor: unknown tensor '%s'", name);
+  int pi = -1;
+  for (int i = 0; i < P_COUNT; ++i)
+    if (strcmp(part, kPartNames[i]) == 0) pi = i;
+  if (pi < 0) return e4b_fail(E4B_EINVAL, "e4b_set_tensor: unknown tensor '%s'", name);
+  Layer& ly = c->L[li];
+  const int64_t QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn;
+  auto q40 = [&](uint8_t** dst, int64_t total_rows, int64_t cols, int64_t row_off, int64_t rows) -> int {
+    int r2;
+    if ((r2 = expect(name, type, E4B_GGML_Q4_0, dims, nd, cols, rows)) ||
+        (r2 = check_bytes((size_t)(rows * cols / 32) * 18)))
+      return r2;
+    if (!*dst && (r2 = dalloc(c, (void**)dst, e4b_q40_packed_bytes(total_rows, cols)))) return r2;
+    return upload_q40_rows(*dst, total_rows, cols, row_off, bytes, rows);
+  };
+  auto f32v = [&](float** dst, int64_t len) -> int {
+    int r2;
+    if ((r2 = expect(name, type, E4B_GGML_F32, dims, nd, len, 1)) || (r2 = check_bytes((size_t)len * 4))) return r2;
+    return upload_f32(c, dst, bytes, len);
+  };
+  switch (pi) {
+    case P_ATTN_NORM: rc = f32v(&ly.attn_norm, H); break;
+    case P_Q: rc = q40(&ly.qkv, c->qkv_rows, H, 0, QH * HD); break;
+    case P_K: rc = q40(&ly.qkv, c->qkv_rows, H, QH * HD, KVH * HD); break;
+    case P_V: rc = q40(&ly.qkv, c->qkv_rows, H, (QH + KVH) * HD, KVH * HD); break;
+    case P_Q_NORM: rc = f32v(&ly.q_norm, HD); break;
+    case P_K_NORM: rc = f32v(&ly.k_norm, HD); break;
+    case P_O: rc = q40(&ly.o, H, QH * HD, 0, H); break;
+    case P_POST_ATTN: rc = f32v(&ly.post_attn, H); break;
+    case P_FFN_NORM: rc = f32v(&ly.ffn_norm, H); break;
+    case P_GATE: rc = q40(&ly.gu, 2 * FF, H, 0, FF); break;
+    case P_UP: rc = q40(&ly.gu, 2 * FF, H, FF, FF); break;
+    case P_DOWN: rc = q40(&ly.down, H, FF, 0, H); break;
+    case P_POST_FFW: rc = f32v(&ly.post_ffw, H); break;
+    case P_INP_GATE:
+      if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
+      rc = q40(&ly.pg, PD, H, 0, PD);
+      break;
+    case P_PROJ:
+      if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
+      rc = q40(&ly.pp, H, PD, 0, H);
+      break;
+    case P_POST_NORM: rc = f32v(&ly.post_norm, H); break;
+    case P_SCALE:
+      if (type != E4B_GGML_F32 || n != 1 || nbytes != 4) return e4b_fail(E4B_EINVAL, "%s: expected one f32", name);
+      memcpy(&ly.scale, bytes, 4);
+      rc = E4B_OK;
+      break;
+    default: rc = e4b_fail(E4B_EINVAL, "unhandled part %d", pi);
+  }
+  if (rc == E4B_OK) ly.have |= 1u << pi;
+  return rc;
+}
+
+extern "C" int e4b_finalize(e4b_ctx* c) {
+  if (!c) return e4b_fail(E4B_EINVAL, "e4b_finalize: null");
+  if (c->finalized) return E4B_OK;
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
+  if (!c->embd) return e4b_fail(E4B_ENOTENSOR, "missing token_embd.weight");
+  if (!c->out_norm) return e4b_fail(E4B_ENOTENSOR, "missing output_norm.weight");
+  if (PD && (!c->ple_tab || !c->ple_proj || !c->ple_norm))
+    return e4b_fail(E4B_ENOTENSOR, "missing per_layer_token_embd / per_layer_model_proj / per_layer_proj_norm");
+  uint32_t need = 0;
+  for (int i = 0; i < P_COUNT; ++i) need |= 1u << i;
+  need &= ~(1u << P_SCALE);
+  if (!PD) need &= ~((1u << P_INP_GATE) | (1u << P_PROJ) | (1u << P_POST_NORM));
+  for (int l = 0; l < k.layers; ++l) {
+    const uint32_t miss = need & ~c->L[l].have;
+    if (miss)
+      for (int i = 0; i < P_COUNT; ++i)
+        if (miss & (1u << i)) return e4b_fail(E4B_ENOTENSOR, "missing blk.%d.%s.weight", l, kPartNames[i]);
+  }
+  int rc;
+  // RoPE inverse frequencies THETA^(-2p/HD), rounded once to f32
+  {
+    std::vector<float> il(HD / 2), ig(HD / 2);
+    for (int p = 0; p < HD / 2; ++p) {
+      il[p] = (float)pow((double)k.theta_local, -2.0 * p / (double)HD);
+      ig[p] = (float)pow((double)k.theta_global, -2.0 * p / (double)HD);
+    }
+    if ((rc = upload_f32(c, &c->inv_local, il.data(), HD / 2)) || (rc = upload_f32(c, &c->inv_global, ig.data(), HD / 2)))
+      return rc;
+  }
+  // split-K chunking: every chunk covers at most attn_max_positions(nch)/nch positions
+  c->nch = k.attn_chunks > 0 ? k.attn_chunks : 16;
+  while (attn_max_positions(c->nch) < k.max_seq) c->nch *= 2;
+  // down projection: one column slice per 2048 columns, partials summed by the consumer
+  const int nb_down = FF / 32;
+  c->ks_down = (nb_down % 64 == 0) ? nb_down / 64 : 1;
+  c->ring_cap = k.max_seq;
+  c->max_prompt = k.max_prompt > 0 ? k.max_prompt : k.max_seq;
+  c->amax_parts = q6k_gemv_grid(k.vocab);
+  // caches
+  for (int l = 0; l < k.layers; ++l) {
+    Layer& ly = c->L[l];
+    ly.slots = ly.global ? k.max_seq : k.ring;
+    const size_t n = (size_t)KVH * ly.slots * HD;
+    if ((rc = dalloc_t(c, &ly.kc, n)) || (rc = dalloc_t(c, &ly.vc, n))) return rc;
+  }
+  // activations
+  const int NP = PD ? k.layers * PD : 1;
+  if ((rc = dalloc_t(c, &c->params, 16)) || (rc = dalloc_t(c, &c->prompt, (size_t)c->max_prompt)) ||
+      (rc = dalloc_t(c, &c->tok_ring, (size_t)c->ring_cap)) || (rc = dalloc_t(c, &c->amax, 4)) ||
+      (rc = dalloc_t(c, &c->status, 4)) || (rc = dalloc_t(c, &c->h, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->h_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->proj, (size_t)NP)) ||
+      (rc = dalloc_t(c, &c->ple, (size_t)NP)) || (rc = dalloc_t(c, &c->xn, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) ||
+      (rc = dalloc_t(c, &c->part_o, (size_t)QH * c->nch * HD)) ||
+      (rc = dalloc_t(c, &c->part_ml, (size_t)QH * c->nch * 2)) || (rc = dalloc_t(c, &c->attn, (size_t)QH * HD)) ||
+      (rc = dalloc_t(c, &c->o, (size_t)H)) || (rc = dalloc_t(c, &c->xf, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)c->ks_down * H)) ||
+      (rc = dalloc_t(c, &c->xg, (size_t)H)) || (rc = dalloc_t(c, &c->gp, (size_t)(PD ? PD : 1))) ||
+      (rc = dalloc_t(c, &c->pp, (size_t)H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
+      (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)))
+    return rc;
+  c->finalized = true;
+  if ((rc = e4b_reset(c))) return rc;
+  // capture one token
+  E4B_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+  rc = record_step(c);
+  hipGraph_t g = nullptr;
+  hipError_t ce = hipStreamEndCapture(c->st, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    c->finalized = false;
+    return rc;
+  }
+  if (ce != hipSuccess) {
+    c->finalized = false;
+    return e4b_fail(E4B_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(ce));
+  }
+  c->graph = g;
+  E4B_HIP(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
+  return E4B_OK;
+}
+
+namespace {
+
+int record_step(e4b_ctx* c) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
+  const int Lc = k.layers;
+  hipStream_t st = c->st;
+  int rc;
+  const Q6Mat E = q6_view(c->embd, k.vocab, H);
+  if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, st))) return rc;
+  if (PD) {
+    GemvOut po = {c->proj, nullptr, nullptr, 0};
+    if ((rc = launch_q40(q40_view(c->ple_proj, (int64_t)Lc * PD, H), (const uint32_t*)c->h_hl,
+                         (const uint32_t*)(c->h_hl + H), EPI_F32, po, 1, st)))
+      return rc;
+    if ((rc = launch_ple_prep(c->proj, c->ple_tab, c->ple_norm, c->params, c->prompt, Lc, k.vocab,
+                              1.0f / sqrtf((float)H), c->ple, c->h, c->L[0].attn_norm, c->xn, H, k.eps, st)))
+      return rc;
+  } else {
+    if ((rc = launch_tail(c->h, nullptr, nullptr, 1.0f, c->L[0].attn_norm, c->xn, nullptr, H, k.eps, st))) return rc;
+  }
+  for (int l = 0; l < Lc; ++l) {
+    const Layer& ly = c->L[l];
+    GemvOut oq = {c->qkv, nullptr, nullptr, 0};
+    if ((rc = launch_q40(q40_view(ly.qkv, c->qkv_rows, H), (const uint32_t*)c->xn, nullptr, EPI_F32, oq, 1, st)))
+      return rc;
+    AttnLaunch a;
+    a.qkv = c->qkv;
+    a.qw = ly.q_norm;
+    a.kw = ly.k_norm;
+    a.inv_freq = ly.global ? c->inv_global : c->inv_local;
+    a.kc = ly.kc;
+    a.vc = ly.vc;
+    a.params = c->params;
+    a.part_o = c->part_o;
+    a.part_ml = c->part_ml;
+    a.out = c->attn;
+    a.qh = QH;
+    a.kvh = KVH;
+    a.hd = HD;
+    a.angles = k.rope_angles;
+    a.slots = ly.slots;
+    a.window = ly.global ? 0 : k.window;
+    a.nch = c->nch;
+    a.eps = k.eps;
+    if ((rc = launch_attn(a, st))) return rc;
+    GemvOut oo = {c->o, nullptr, nullptr, 0};
+    if ((rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * HD), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st)))
+      return rc;
+    if ((rc = launch_post_attn(c->h, c->o, ly.post_attn, ly.ffn_norm, c->xf, H, k.eps, st))) return rc;
+    GemvOut og = {nullptr, c->gg, nullptr, FF};
+    if ((rc = launch_q40(q40_view(ly.gu, 2 * (int64_t)FF, H), (const uint32_t*)c->xf, nullptr, EPI_GEGLU, og, 1, st)))
+      return rc;
+    GemvOut od = {c->dn, nullptr, nullptr, 0};
+    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, c->ks_down, st)))
+      return rc;
+    if ((rc = launch_post_ffn(c->h, c->dn, c->ks_down, ly.post_ffw, c->xg, H, k.eps, st))) return rc;
+    const bool last = (l + 1 == Lc);
+    const float* w_next = last ? c->out_norm : c->L[l + 1].attn_norm;
+    uint16_t* xn = last ? nullptr : c->xn;
+    uint16_t* xo = last ? c->xo_hl : nullptr;
+    if (PD) {
+      GemvOut ogp = {nullptr, c->gp, c->ple + (int64_t)l * PD, 0};
+      if ((rc = launch_q40(q40_view(ly.pg, PD, H), (const uint32_t*)c->xg, nullptr, EPI_GELU_MUL, ogp, 1, st)))
+        return rc;
+      GemvOut opp = {c->pp, nullptr, nullptr, 0};
+      if ((rc = launch_q40(q40_view(ly.pp, H, PD), (const uint32_t*)c->gp, nullptr, EPI_F32, opp, 1, st))) return rc;
+      if ((rc = launch_tail(c->h, c->pp, ly.post_norm, ly.scale, w_next, xn, xo, H, k.eps, st))) return rc;
+    } else {
+      if ((rc = launch_tail(c->h, nullptr, nullptr, ly.scale, w_next, xn, xo, H, k.eps, st))) return rc;
+    }
+  }
+  if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
+                                   c->logits, nullptr, c->amax_part, st)))
+    return rc;
+  return launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st);
+}
+
+int ready(e4b_ctx* c, const char* fn) {
+  if (!c) return e4b_fail(E4B_EINVAL, "%s: null context", fn);
+  if (!c->finalized) return e4b_fail(E4B_ESTATE, "%s before e4b_finalize", fn);
+  return E4B_OK;
+}
+
+int check_status(e4b_ctx* c) {
+  uint32_t s = 0;
+  E4B_HIP(hipMemcpyAsync(&s, c->status, 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  if (s) {
+    uint32_t z = 0;
+    E4B_HIP(hipMemcpy(c->status, &z, 4, hipMemcpyHostToDevice));
+    return e4b_fail(E4B_ERANGE, "token id out of range [0, %d)", c->cfg.vocab);
+  }
+  return E4B_OK;
+}
+
+int put_params(e4b_ctx* c, const uint32_t* v, int first, int count) {
+  E4B_HIP(hipMemcpyAsync(c->params + first, v, (size_t)count * 4, hipMemcpyHostToDevice, c->st));
+  return E4B_OK;
+}
+
+}  // namespace
+
+extern "C" int e4b_step(e4b_ctx* c, uint32_t token, uint32_t pos, float* logits, uint32_t* argmax_out) {
+  int rc = ready(c, "e4b_step");
+  if (rc) return rc;
+  if (token >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_step: token %u >= vocab %d", token, c->cfg.vocab);
+  if (pos >= (uint32_t)c->cfg.max_seq) return e4b_fail(E4B_ERANGE, "e4b_step: pos %u >= max_seq %d", pos, c->cfg.max_seq);
+  const uint32_t p[4] = {pos, token, 0u, 0u};
+  if ((rc = put_params(c, p, 0, 4))) return rc;
+  E4B_HIP(hipGraphLaunch(c->exec, c->st));
+  uint32_t am[2] = {0, 0};
+  E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
+  if (logits) E4B_HIP(hipMemcpyAsync(logits, c->logits, (size_t)c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->st));
+  if ((rc = check_status(c))) return rc;
+  if (argmax_out) *argmax_out = am[0];
+  return E4B_OK;
+}
+
+extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
+  int rc = ready(c, "e4b_prefill");
+  if (rc) return rc;
+  if (!ids || n == 0) return e4b_fail(E4B_EINVAL, "e4b_prefill: empty prompt");
+  if (n > (uint32_t)c->max_prompt || n > (uint32_t)c->cfg.max_seq)
+    return e4b_fail(E4B_ERANGE, "e4b_prefill: %u tokens exceeds the prompt capacity %d", n, c->max_prompt);
+  for (uint32_t i = 0; i < n; ++i)
+    if (ids[i] >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_prefill: ids[%u] = %u >= vocab", i, ids[i]);
+  E4B_HIP(hipMemcpyAsync(c->prompt, ids, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
+  const uint32_t p[4] = {0u, 0u, 0u, n};
+  if ((rc = put_params(c, p, 0, 4))) return rc;
+  for (uint32_t i = 0; i < n; ++i) E4B_HIP(hipGraphLaunch(c->exec, c->st));
+  uint32_t am[2] = {0, 0};
+  E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
+  if ((rc = check_status(c))) return rc;
+  if (argmax_out) *argmax_out = am[0];
+  return E4B_OK;
+}
+
+static int decode_launch(e4b_ctx* c, uint32_t start_pos, uint32_t count) {
+  if ((uint64_t)start_pos + count > (uint64_t)c->cfg.max_seq)
+    return e4b_fail(E4B_ERANGE, "decode: positions [%u, %u) exceed max_seq %d", start_pos, start_pos + count,
+                    c->cfg.max_seq);
+  if (count > (uint32_t)c->ring_cap) return e4b_fail(E4B_ERANGE, "decode: %u tokens exceed the token ring", count);
+  const uint32_t p0 = start_pos, z[2] = {0u, 0u};
+  int rc;
+  if ((rc = put_params(c, &p0, 0, 1)) || (rc = put_params(c, z, 2, 2))) return rc;
+  for (uint32_t i = 0; i < count; ++i) E4B_HIP(hipGraphLaunch(c->exec, c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_decode(e4b_ctx* c, uint32_t start_pos, uint32_t count, uint32_t* tokens_out) {
+  int rc = ready(c, "e4b_decode");
+  if (rc) return rc;
+  if (count == 0) return E4B_OK;
+  if (!tokens_out) return e4b_fail(E4B_EINVAL, "e4b_decode: null tokens_out");
+  if ((rc = decode_launch(c, start_pos, count))) return rc;
+  E4B_HIP(hipMemcpyAsync(tokens_out, c->tok_ring, (size_t)count * 4, hipMemcpyDeviceToHost, c->st));
+  return check_status(c);
+}
+
+extern "C" int e4b_time_decode(e4b_ctx* c, uint32_t start_pos, uint32_t count, float* ms_out) {
+  int rc = ready(c, "e4b_time_decode");
+  if (rc) return rc;
+  if (!ms_out) return e4b_fail(E4B_EINVAL, "e4b_time_decode: null ms_out");
+  hipEvent_t a, b;
+  E4B_HIP(hipEventCreate(&a));
+  E4B_HIP(hipEventCreate(&b));
+  E4B_HIP(hipEventRecord(a, c->st));
+  rc = decode_launch(c, start_pos, count);
+  if (rc == E4B_OK) {
+    E4B_HIP(hipEventRecord(b, c->st));
+    E4B_HIP(hipEventSynchronize(b));
+    E4B_HIP(hipEventElapsedTime(ms_out, a, b));
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return rc ? rc : check_status(c);
+}
+
+extern "C" int e4b_argmax(e4b_ctx* c, uint32_t* token_out) {
+  int rc = ready(c, "e4b_argmax");
+  if (rc) return rc;
+  if (!token_out) return e4b_fail(E4B_EINVAL, "e4b_argmax: null");
+  uint32_t am[2];
+  E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  *token_out = am[0];
+  return E4B_OK;
+}
+
+extern "C" int e4b_read_hidden(e4b_ctx* c, float* out) {
+  int rc = ready(c, "e4b_read_hidden");
+  if (rc) return rc;
+  E4B_HIP(hipMemcpyAsync(out, c->h, (size_t)c->cfg.hidden * 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_read_logits(e4b_ctx* c, float* out) {
+  int rc = ready(c, "e4b_read_logits");
+  if (rc) return rc;
+  E4B_HIP(hipMemcpyAsync(out, c->logits, (size_t)c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_kv_slots(e4b_ctx* c, int layer) {
+  int rc = ready(c, "e4b_kv_slots");
+  if (rc) return rc;
+  if (layer < 0 || layer >= c->cfg.layers) return e4b_fail(E4B_EINVAL, "layer %d", layer);
+  return c->L[layer].slots;
+}
+
+extern "C" int e4b_read_kv(e4b_ctx* c, int layer, uint16_t* k_out, uint16_t* v_out) {
+  int rc = ready(c, "e4b_read_kv");
+  if (rc) return rc;
+  if (layer < 0 || layer >= c->cfg.layers) return e4b_fail(E4B_EINVAL, "layer %d", layer);
+  const Layer& ly = c->L[layer];
+  const size_t n = (size_t)c->cfg.kv_heads * ly.slots * c->cfg.head_dim * 2;
+  if (k_out) E4B_HIP(hipMemcpyAsync(k_out, ly.kc, n, hipMemcpyDeviceToHost, c->st));
+  if (v_out) E4B_HIP(hipMemcpyAsync(v_out, ly.vc, n, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_reset(e4b_ctx* c) {
+  int rc = ready(c, "e4b_reset");
+  if (rc) return rc;
+  for (const Layer& ly : c->L) {
+    const size_t n = (size_t)c->cfg.kv_heads * ly.slots * c->cfg.head_dim * 2;
+    E4B_HIP(hipMemsetAsync(ly.kc, 0, n, c->st));
+    E4B_HIP(hipMemsetAsync(ly.vc, 0, n, c->st));
+  }
+  E4B_HIP(hipMemsetAsync(c->params, 0, 16 * 4, c->st));
+  E4B_HIP(hipMemsetAsync(c->status, 0, 4 * 4, c->st));
+  E4B_HIP(hipMemsetAsync(c->amax, 0, 4 * 4, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" void e4b_destroy(e4b_ctx* c) {
+  if (!c) return;
+  if (c->st) (void)hipStreamSynchronize(c->st);
+  if (c->exec) (void)hipGraphExecDestroy(c->exec);
+  if (c->graph) (void)hipGraphDestroy(c->graph);
+  for (void* p : c->allocs) (void)hipFree(p);
+  if (c->st) (void)hipStreamDestroy(c->st);
+  delete c;
+}

@@ -19,6 +19,7 @@
 namespace {
 
 constexpr float kTwo24 = 16777216.0f;
+constexpr int kQ6Rows = 8;  // lm-head rows per wave tile
 
 DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
   const uint4* v = reinterpret_cast<const uint4*>(x) + (size_t)jb * 4;
@@ -464,12 +465,17 @@ int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipS
   return E4B_OK;
 }
 
+int q6k_gemv_grid(int64_t rows) {
+  const int64_t ntiles = (rows + kQ6Rows - 1) / kQ6Rows;
+  const int64_t wgs = (ntiles + 3) / 4;
+  return (int)(wgs < 2048 ? wgs : 2048);
+}
+
 int launch_q6k_gemv_argmax(const Q6Mat& W, const uint32_t* xh, const uint32_t* xl, float softcap, float* logits,
                            uint32_t* amax, uint2* part, hipStream_t st) {
-  constexpr int R = 8;
+  constexpr int R = kQ6Rows;
   const int64_t ntiles = (W.rows + R - 1) / R;
-  int64_t wgs = (ntiles + 3) / 4;
-  if (wgs > 2048) wgs = 2048;
+  const int64_t wgs = q6k_gemv_grid(W.rows);
   if (W.nseg <= 64)
     hipLaunchKernelGGL((k_q6k_gemv_argmax<1, R>), dim3((unsigned)wgs), dim3(256), 0, st, W, xh, xl, softcap, logits,
                        part, ntiles);

@@ -1,0 +1,39 @@
+// step.h -- launchers of the decode-step kernels in k_step.hip.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "kernels.h"
+
+struct AttnLaunch {
+  const float* qkv;        // raw q | k | v (f32) of the current token
+  const float* qw;         // q head-norm weight [hd]
+  const float* kw;         // k head-norm weight [hd]
+  const float* inv_freq;   // RoPE inverse frequencies [angles]
+  uint16_t* kc;            // [kvh][slots][hd] f16 key cache
+  uint16_t* vc;            // [kvh][slots][hd] f16 value cache
+  const uint32_t* params;  // params[0] = position of the current token
+  float* part_o;           // [qh][nch][hd] split-K partial outputs
+  float* part_ml;          // [qh][nch][2]  (chunk max, chunk sum)
+  uint16_t* out;           // [qh][hd] f16 attention output
+  int qh, kvh, hd, angles;
+  int slots;               // ring slots (sliding) or capacity (global)
+  int window;              // sliding window; 0 = global layer (linear cache)
+  int nch;                 // split-K chunks
+  float eps;
+};
+
+int launch_attn(const AttnLaunch& a, hipStream_t st);
+int attn_max_positions(int nch);
+int launch_post_attn(float* h, const float* o, const float* w_pa, const float* w_ffn, uint16_t* xf, int H, float eps,
+                     hipStream_t st);
+int launch_post_ffn(float* h, const float* dn, int ks, const float* w_pf, uint16_t* xg, int H, float eps,
+                    hipStream_t st);
+int launch_tail(float* h, const float* p, const float* w_post, float scale, const float* w_next, uint16_t* xn,
+                uint16_t* xo_hl, int H, float eps, hipStream_t st);
+int launch_embed(const Q6Mat& E, const uint32_t* params, const uint32_t* prompt, float mult, float* h, uint16_t* h_hl,
+                 uint32_t* status, hipStream_t st);
+int launch_ple_prep(const float* proj, const uint8_t* table, const float* w_pn, const uint32_t* params,
+                    const uint32_t* prompt, int L, int vocab, float proj_scale, float* ple, const float* h,
+                    const float* w_attn0, uint16_t* xn, int H, float eps, hipStream_t st);
+int launch_feedback(const uint2* part, int nparts, uint32_t* amax, uint32_t* params, uint32_t* tok_ring, int ring_cap,
+                    hipStream_t st);

@@ -80,7 +80,32 @@ SIGNATURES = [
     ("e4b_k_q6k_gemv_argmax", _i32, [_vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_row", _i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),
     ("e4b_k_argmax", _i32, [_vp, _i64, _vp, _vp]),
+    ("e4b_create", _vp, [_vp]),
+    ("e4b_set_tensor", _i32, [_vp, C.c_char_p, _i32, _P(_i64), _i32, _vp, _sz]),
+    ("e4b_finalize", _i32, [_vp]),
+    ("e4b_step", _i32, [_vp, _u32, _u32, _vp, _vp]),
+    ("e4b_prefill", _i32, [_vp, _vp, _u32, _vp]),
+    ("e4b_decode", _i32, [_vp, _u32, _u32, _vp]),
+    ("e4b_argmax", _i32, [_vp, _vp]),
+    ("e4b_read_hidden", _i32, [_vp, _vp]),
+    ("e4b_read_logits", _i32, [_vp, _vp]),
+    ("e4b_read_kv", _i32, [_vp, _i32, _vp, _vp]),
+    ("e4b_kv_slots", _i32, [_vp, _i32]),
+    ("e4b_reset", _i32, [_vp]),
+    ("e4b_destroy", None, [_vp]),
+    ("e4b_time_decode", _i32, [_vp, _u32, _u32, _P(_f32)]),
 ]
+
+
+class ConfigC(C.Structure):
+    """struct e4b_config (include/e4b.h)."""
+
+    _fields_ = [
+        ("hidden", _i32), ("layers", _i32), ("q_heads", _i32), ("kv_heads", _i32), ("head_dim", _i32),
+        ("ffn", _i32), ("ple_dim", _i32), ("vocab", _i32), ("window", _i32), ("ring", _i32), ("max_seq", _i32),
+        ("rope_angles", _i32), ("theta_local", _f32), ("theta_global", _f32), ("eps", _f32), ("softcap", _f32),
+        ("layer_global", _vp), ("attn_chunks", _i32), ("max_prompt", _i32),
+    ]
 
 for _name, _res, _args in SIGNATURES:
     _fn = getattr(lib, _name)

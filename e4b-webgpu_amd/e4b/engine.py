@@ -1,0 +1,192 @@
+"""Engine: the host surface of the reference's decode engine over libe4b.
+
+Mirrors the object returned by loadEngineA4B (src/engine-a4b.js:854-856):
+``step(token, pos)``, ``argmax_fast()``, ``decode_chunk(start_pos, count)``,
+``generate_fast(ids, max_new, eos)``, ``prefill(ids)``, ``read_hidden()``.
+The compute runs in libe4b.so (HIP, gfx950); this module only moves tensors
+and calls the C ABI.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import ConfigC, check, lib
+from .gguf import open_gguf
+from .model import E4BConfig, Tensor
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# GGUF metadata keys of the E4B-shaped model (gemma3n-style prefix)
+_KV = {
+    "hidden": "embedding_length", "layers": "block_count", "q_heads": "attention.head_count",
+    "kv_heads": "attention.head_count_kv", "head_dim": "attention.key_length", "ffn": "feed_forward_length",
+    "ple_dim": "embedding_length_per_layer_input", "vocab": "vocab_size", "window": "attention.sliding_window",
+    "rope_angles": "rope.dimension_count_half", "theta_local": "rope.freq_base_swa", "theta_global": "rope.freq_base",
+    "eps": "attention.layer_norm_rms_epsilon", "softcap": "final_logit_softcapping",
+}
+ARCH = "e4b"
+
+
+def config_to_kv(cfg: E4BConfig) -> dict:
+    kv = {"general.architecture": ARCH}
+    for f, k in _KV.items():
+        kv[f"{ARCH}.{k}"] = getattr(cfg, f)
+    kv[f"{ARCH}.attention.sliding_window_pattern"] = [not bool(g) for g in cfg.layer_global]
+    return kv
+
+
+def config_from_kv(kv: dict, **overrides) -> E4BConfig:
+    arch = kv.get("general.architecture", ARCH)
+    args = {}
+    for f, k in _KV.items():
+        key = f"{arch}.{k}"
+        if key in kv:
+            args[f] = kv[key]
+    pat = kv.get(f"{arch}.attention.sliding_window_pattern")
+    if pat is not None:
+        args["layer_global"] = [0 if s else 1 for s in pat]
+    args.update(overrides)
+    for f in ("theta_local", "theta_global", "eps", "softcap"):
+        if f in args:
+            args[f] = float(args[f])
+    return E4BConfig(**args)
+
+
+class Engine:
+    def __init__(self, cfg: E4BConfig, tensors=None):
+        self.cfg = cfg
+        c = ConfigC()
+        for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
+                  "max_seq", "rope_angles", "attn_chunks", "max_prompt"):
+            setattr(c, f, int(getattr(cfg, f)))
+        for f in ("theta_local", "theta_global", "eps", "softcap"):
+            setattr(c, f, float(getattr(cfg, f)))
+        self._lg = np.ascontiguousarray(np.asarray(cfg.layer_global, np.uint8))
+        c.layer_global = _p(self._lg)
+        ctx = lib.e4b_create(C.byref(c))
+        if not ctx:
+            check(-1, "e4b_create")
+        self.ctx = C.c_void_p(ctx)
+        if tensors is not None:
+            for t in (tensors.values() if isinstance(tensors, dict) else tensors):
+                self.set_tensor(t.name, t.ggml_type, t.dims, t.data)
+            self.finalize()
+
+    # ---- loading (src/gguf.js fetch -> upload) ------------------------------
+    def set_tensor(self, name: str, ggml_type: int, dims, data) -> None:
+        data = np.ascontiguousarray(data)
+        d = (C.c_int64 * len(dims))(*[int(x) for x in dims])
+        check(lib.e4b_set_tensor(self.ctx, name.encode(), int(ggml_type), d, len(dims), _p(data), data.nbytes),
+              f"e4b_set_tensor({name})")
+
+    def finalize(self) -> None:
+        check(lib.e4b_finalize(self.ctx), "e4b_finalize")
+
+    @classmethod
+    def from_gguf(cls, path: str, **overrides) -> "Engine":
+        g = open_gguf(path)
+        cfg = config_from_kv(g.kv, **overrides)
+        eng = cls(cfg)
+        for name in g.tensors:
+            t = g.fetch(name)
+            eng.set_tensor(name, t["type"], t["dims"], t["buf"])
+        eng.finalize()
+        return eng
+
+    # ---- the token loop -----------------------------------------------------
+    def step(self, token: int, pos: int, want_logits: bool = False):
+        """One decode step (src/engine-a4b.js:695-705); returns the argmax
+        token, plus the logits when asked."""
+        am = C.c_uint32(0)
+        lg = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        check(lib.e4b_step(self.ctx, int(token), int(pos), _p(lg), C.byref(am)), "e4b_step")
+        return (int(am.value), lg) if want_logits else int(am.value)
+
+    def argmax_fast(self) -> int:
+        am = C.c_uint32(0)
+        check(lib.e4b_argmax(self.ctx, C.byref(am)), "e4b_argmax")
+        return int(am.value)
+
+    def prefill(self, ids) -> int:
+        ids = np.ascontiguousarray(np.asarray(ids, np.uint32))
+        am = C.c_uint32(0)
+        check(lib.e4b_prefill(self.ctx, _p(ids), ids.size, C.byref(am)), "e4b_prefill")
+        return int(am.value)
+
+    def decode_chunk(self, start_pos: int, count: int) -> np.ndarray:
+        """GPU-fed greedy decode (src/engine-a4b.js:786-824): `count` tokens,
+        each fed with the previous argmax, starting at start_pos."""
+        out = np.empty(count, np.uint32)
+        check(lib.e4b_decode(self.ctx, int(start_pos), int(count), _p(out)), "e4b_decode")
+        return out
+
+    def generate_fast(self, ids, max_new: int, eos=(106, 1)) -> list:
+        """src/engine-a4b.js:826-848: prompt, then GPU-fed chunks of <= 8 with
+        an EOS check after each chunk readback."""
+        eos = set(eos)
+        g0 = self.prefill(ids)
+        out = [g0]
+        if g0 in eos:
+            return out
+        pos, done = len(ids), 1
+        while done < max_new:
+            n = min(8, max_new - done)
+            toks = self.decode_chunk(pos, n)
+            pos += n
+            stop = False
+            for t in toks.tolist():
+                out.append(int(t))
+                if t in eos:
+                    stop = True
+                    break
+            done += n
+            if stop:
+                break
+        return out[:max_new]
+
+    def time_decode(self, start_pos: int, count: int) -> float:
+        ms = C.c_float(0)
+        check(lib.e4b_time_decode(self.ctx, int(start_pos), int(count), C.byref(ms)), "e4b_time_decode")
+        return float(ms.value)
+
+    # ---- inspection -----------------------------------------------------------
+    def read_hidden(self) -> np.ndarray:
+        out = np.empty(self.cfg.hidden, np.float32)
+        check(lib.e4b_read_hidden(self.ctx, _p(out)), "e4b_read_hidden")
+        return out
+
+    def read_logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.vocab, np.float32)
+        check(lib.e4b_read_logits(self.ctx, _p(out)), "e4b_read_logits")
+        return out
+
+    def kv_slots(self, layer: int) -> int:
+        return check(lib.e4b_kv_slots(self.ctx, layer), "e4b_kv_slots")
+
+    def read_kv(self, layer: int):
+        """(k, v) caches of a layer as uint16 (f16 bits) [kv_heads][slots][head_dim]."""
+        slots = self.kv_slots(layer)
+        shape = (self.cfg.kv_heads, slots, self.cfg.head_dim)
+        k = np.empty(shape, np.uint16)
+        v = np.empty(shape, np.uint16)
+        check(lib.e4b_read_kv(self.ctx, layer, _p(k), _p(v)), "e4b_read_kv")
+        return k, v
+
+    def reset(self) -> None:
+        check(lib.e4b_reset(self.ctx), "e4b_reset")
+
+    def close(self) -> None:
+        if getattr(self, "ctx", None):
+            lib.e4b_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

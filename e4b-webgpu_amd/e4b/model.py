@@ -1,0 +1,145 @@
+"""E4B-shaped model description and seeded random-init tensors.
+
+The BASELINE "E4B-shaped q4_0" model combines Gemma-3n-E4B shapes (35 layers,
+hidden 2048, GeGLU FFN 16384, 4 sliding : 1 global, per-layer embeddings of
+256) with the A4B engine's formats (q4_0 linears, Q6_K tied embedding /
+lm-head, f16 KV ring).  Tensor names follow the GGUF naming of that family;
+dims are ggml order (ne0 = row length).
+"""
+from __future__ import annotations
+
+import dataclasses
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from ._lib import GGML_F32, GGML_Q4_0, GGML_Q6_K
+from . import formats
+
+
+@dataclass
+class E4BConfig:
+    hidden: int = 2048
+    layers: int = 35
+    q_heads: int = 8
+    kv_heads: int = 2
+    head_dim: int = 256
+    ffn: int = 16384
+    ple_dim: int = 256
+    vocab: int = 262144
+    window: int = 512
+    ring: int = 1024
+    max_seq: int = 4096
+    rope_angles: int = 128
+    theta_local: float = 1e4
+    theta_global: float = 1e6
+    eps: float = 1e-6
+    softcap: float = 30.0
+    layer_global: list = field(default_factory=list)
+    attn_chunks: int = 0
+    max_prompt: int = 0
+
+    def __post_init__(self):
+        if not self.layer_global:
+            self.layer_global = [1 if i % 5 == 4 else 0 for i in range(self.layers)]
+
+    def as_dict(self) -> dict:
+        return dataclasses.asdict(self)
+
+    def bytes_per_token(self, pos: int) -> int:
+        """Algorithmic HBM bytes of one decode step at position `pos`: every
+        weight read once (q4_0 18 B / 32, Q6_K 210 B / 256), the K/V rows the
+        attention reads, the PLE table row and the logits written."""
+        H, F, PD, L = self.hidden, self.ffn, self.ple_dim, self.layers
+        qkv = (self.q_heads + 2 * self.kv_heads) * self.head_dim
+        q40 = lambda r, c: r * c // 32 * 18  # noqa: E731
+        per_layer = q40(qkv, H) + q40(H, self.q_heads * self.head_dim) + q40(2 * F, H) + q40(H, F)
+        if PD:
+            per_layer += q40(PD, H) + q40(H, PD)
+        kv_row = 2 * self.kv_heads * self.head_dim * 2  # K and V, f16
+        kv = 0
+        for g in self.layer_global:
+            live = pos + 1 if g else min(pos + 1, self.window)
+            kv += live * kv_row
+        head = self.vocab * H // 256 * 210 + self.vocab * 4
+        ple = (q40(L * PD, H) + L * PD // 256 * 210) if PD else 0
+        emb = H // 256 * 210
+        return L * per_layer + kv + head + ple + emb
+
+
+def tiny_config(**kw) -> E4BConfig:
+    """Small model with the same code path (hidden 256, 5 layers, 1 global)."""
+    base = dict(hidden=256, layers=5, q_heads=8, kv_heads=2, head_dim=256, ffn=512, ple_dim=256, vocab=1000,
+                window=8, ring=16, max_seq=64, rope_angles=128)
+    base.update(kw)
+    return E4BConfig(**base)
+
+
+@dataclass
+class Tensor:
+    name: str
+    ggml_type: int
+    dims: tuple  # ggml order
+    data: np.ndarray  # uint8 block bytes (quantized) or float32
+
+
+def synth_tensors(cfg: E4BConfig, seed: int = 0, lin_sigma: float = 0.02, emb_sigma: float = 1e-3):
+    """Random-init tensors of the E4B-shaped model (BASELINE config c4):
+    q4_0 linears with d = f16(|N(0, lin_sigma)|/8), Q6_K embedding / PLE table
+    with d = f16(|N(0, emb_sigma)|), norm weights 1, layer scalars 1."""
+    H, F, PD, L, V = cfg.hidden, cfg.ffn, cfg.ple_dim, cfg.layers, cfg.vocab
+    QH, KVH, HD = cfg.q_heads, cfg.kv_heads, cfg.head_dim
+    out = {}
+    counter = [0]
+
+    def sub():
+        counter[0] += 1
+        return (seed * 1000003 + counter[0]) & 0xFFFFFFFFFFFFFFFF
+
+    def q40(name, rows, cols):
+        out[name] = Tensor(name, GGML_Q4_0, (cols, rows), formats.synth_q40(sub(), rows, cols, lin_sigma))
+
+    def q6k(name, rows, cols):
+        out[name] = Tensor(name, GGML_Q6_K, (cols, rows), formats.synth_q6k(sub(), rows, cols, emb_sigma))
+
+    def ones(name, n):
+        sub()
+        out[name] = Tensor(name, GGML_F32, (n,), np.ones(n, np.float32))
+
+    q6k("token_embd.weight", V, H)
+    ones("output_norm.weight", H)
+    if PD:
+        q6k("per_layer_token_embd.weight", V, L * PD)
+        q40("per_layer_model_proj.weight", L * PD, H)
+        ones("per_layer_proj_norm.weight", PD)
+    for i in range(L):
+        p = f"blk.{i}."
+        ones(p + "attn_norm.weight", H)
+        q40(p + "attn_q.weight", QH * HD, H)
+        q40(p + "attn_k.weight", KVH * HD, H)
+        q40(p + "attn_v.weight", KVH * HD, H)
+        ones(p + "attn_q_norm.weight", HD)
+        ones(p + "attn_k_norm.weight", HD)
+        q40(p + "attn_output.weight", H, QH * HD)
+        ones(p + "post_attention_norm.weight", H)
+        ones(p + "ffn_norm.weight", H)
+        q40(p + "ffn_gate.weight", F, H)
+        q40(p + "ffn_up.weight", F, H)
+        q40(p + "ffn_down.weight", H, F)
+        ones(p + "post_ffw_norm.weight", H)
+        if PD:
+            q40(p + "inp_gate.weight", PD, H)
+            q40(p + "proj.weight", H, PD)
+            ones(p + "post_norm.weight", H)
+        out[p + "layer_output_scale.weight"] = Tensor(p + "layer_output_scale.weight", GGML_F32, (1,),
+                                                      np.ones(1, np.float32))
+    return out
+
+
+def norm_weights_random(tensors: dict, seed: int = 1, lo: float = 0.5, hi: float = 1.5) -> dict:
+    """Replace the f32 norm vectors by U(lo, hi) so that tests see every weight."""
+    rng = np.random.default_rng(seed)
+    for t in tensors.values():
+        if t.ggml_type == GGML_F32 and t.data.size > 1:
+            t.data = rng.uniform(lo, hi, t.data.size).astype(np.float32)
+    return tensors

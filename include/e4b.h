@@ -118,6 +118,71 @@ int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row,
 /* argmax over f32[n] (kernels/argmax2.wgsl:8-48): amax u32[2]. */
 int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Engine: the per-token batch-1 decode step of an E4B-shaped decoder
+ * (35 layers, 4 sliding : 1 global, GeGLU FFN, per-layer embeddings, q4_0
+ * linears, Q6_K tied embedding / lm-head, f16 KV ring).  Replaces the engine
+ * object of loadEngineA4B (src/engine-a4b.js:75, returned at :854-856): load
+ * (openGGUF fetch + upload, src/gguf.js:74-81), step (:695-705), the GPU-fed
+ * decodeChunk / generateFast loop (:786-848), argmaxFast (:781-784) and
+ * readHidden (:850-852).  One context = one HIP stream; not reentrant.
+ * ------------------------------------------------------------------------- */
+typedef struct e4b_ctx e4b_ctx;
+
+typedef struct e4b_config {
+  int32_t hidden;         /* 2048 */
+  int32_t layers;         /* 35 */
+  int32_t q_heads;        /* 8 */
+  int32_t kv_heads;       /* 2 (head_dim 256, 4 q heads per kv head) */
+  int32_t head_dim;       /* 256 */
+  int32_t ffn;            /* 16384 */
+  int32_t ple_dim;        /* 256, or 0 = no per-layer embeddings */
+  int32_t vocab;          /* 262144 */
+  int32_t window;         /* sliding window, 512 */
+  int32_t ring;           /* sliding-layer ring slots (>= window), 1024 */
+  int32_t max_seq;        /* global-layer cache capacity (positions) */
+  int32_t rope_angles;    /* rotated pairs per head, 128 */
+  float theta_local;      /* 1e4 */
+  float theta_global;     /* 1e6 */
+  float eps;              /* 1e-6 */
+  float softcap;          /* 30 (0 = none) */
+  const uint8_t* layer_global; /* [layers] 1 = global; NULL = (i % 5 == 4) */
+  int32_t attn_chunks;    /* split-K chunks per layer, 0 = default */
+  int32_t max_prompt;     /* prompt buffer capacity, 0 = max_seq */
+} e4b_config;
+
+/* tensor names follow the GGUF naming of the E4B family:
+ *   token_embd.weight (Q6_K [vocab][hidden], tied lm-head), output_norm.weight,
+ *   per_layer_token_embd.weight (Q6_K [vocab][layers*ple_dim]),
+ *   per_layer_model_proj.weight (q4_0 [layers*ple_dim][hidden]),
+ *   per_layer_proj_norm.weight, and per layer blk.N.{attn_norm, attn_q, attn_k,
+ *   attn_v, attn_q_norm, attn_k_norm, attn_output, post_attention_norm,
+ *   ffn_norm, ffn_gate, ffn_up, ffn_down, post_ffw_norm, inp_gate, proj,
+ *   post_norm, layer_output_scale}.weight.  dims are ggml order (ne0 = row
+ *   length).  Linear weights must be q4_0, norms f32. */
+e4b_ctx* e4b_create(const e4b_config* cfg);   /* NULL on error (e4b_last_error) */
+int  e4b_set_tensor(e4b_ctx* ctx, const char* name, int ggml_type, const int64_t* dims, int nd,
+                    const void* bytes, size_t nbytes);
+int  e4b_finalize(e4b_ctx* ctx);              /* allocates KV/activations, captures the step graph */
+/* one token at `pos` (positions must be fed in order from 0); logits may be
+ * NULL; argmax_out may be NULL */
+int  e4b_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, float* logits_or_null, uint32_t* argmax_out);
+/* token-by-token prefill of ids[0..n) from position 0; argmax_out = greedy
+ * continuation of the last prompt token */
+int  e4b_prefill(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* argmax_out);
+/* GPU-fed greedy decode of `count` tokens starting at start_pos, fed with the
+ * previous step's argmax; tokens_out[count] */
+int  e4b_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, uint32_t* tokens_out);
+int  e4b_argmax(e4b_ctx* ctx, uint32_t* token_out);     /* argmaxFast: last step's argmax */
+int  e4b_read_hidden(e4b_ctx* ctx, float* out);         /* hidden state after the last layer */
+int  e4b_read_logits(e4b_ctx* ctx, float* out);         /* last step's logits [vocab] */
+int  e4b_read_kv(e4b_ctx* ctx, int layer, uint16_t* k_out, uint16_t* v_out); /* [kvh][slots][hd] f16 */
+int  e4b_kv_slots(e4b_ctx* ctx, int layer);             /* slots of that layer's cache */
+int  e4b_reset(e4b_ctx* ctx);                           /* zero KV caches and state */
+void e4b_destroy(e4b_ctx* ctx);
+/* timing: run `count` GPU-fed steps and return the elapsed device ms */
+int  e4b_time_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, float* ms_out);
+
 #ifdef __cplusplus
 }
 #endif

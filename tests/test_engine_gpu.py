@@ -1,0 +1,156 @@
+"""End-to-end parity of the decode engine (libe4b, HIP) with the CPU oracle.
+
+Tolerances (stated, as the north star asks):
+  * greedy tokens: bit-exact, except at a near-tie where the oracle's top-2
+    logit margin is below 2e-3 of its logit range (reported, then the oracle's
+    choice is fed to both sides so the comparison continues in lock-step);
+  * logits: max |gpu - oracle| <= 1e-3 * max |oracle|;
+  * hidden state: max |gpu - oracle| <= 1e-3 * max |oracle|;
+  * KV caches: the set of written ring slots is identical (bit-exact slot
+    indices); values: max error <= 1e-2 * max |value| and mean error <=
+    1e-3 * mean |value|.  Later layers' K/V inherit the upstream hidden-state
+    differences (f16 rounding points of f32 results that differ in the last
+    bits, amplified by scale-1.0 attention), so single entries drift more
+    than the hidden state itself.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from e4b.engine import Engine
+from e4b.model import E4BConfig, norm_weights_random, synth_tensors, tiny_config
+from tests.util import top2_margin
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+TIE_TOL = 2e-3
+KV_MAX_TOL = 1e-2
+KV_MEAN_TOL = 1e-3
+
+
+def build(cfg: E4BConfig, seed: int):
+    tensors = norm_weights_random(synth_tensors(cfg, seed), seed + 1)
+    eng = Engine(cfg, tensors)
+    om = orc.OracleModel(cfg.as_dict(), {n: t.data for n, t in tensors.items()})
+    return eng, om
+
+
+def lockstep(eng, om, prompt, n_decode, check_logits_every=0):
+    """Prefill + GPU-fed decode on the engine; the oracle replays the same token
+    stream.  Returns (tokens, near_ties)."""
+    cfg = eng.cfg
+    g0 = eng.prefill(prompt)
+    for i, t in enumerate(prompt):
+        o_tok, o_lg, _ = om.step(int(t), i, want_logits=(i == len(prompt) - 1))
+    ties = []
+    tok = g0
+    if tok != o_tok:
+        assert top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max(), f"prefill argmax {tok} vs oracle {o_tok}"
+        ties.append(len(prompt) - 1)
+    gpu_tokens = eng.decode_chunk(len(prompt), n_decode)
+    fed = [tok] + gpu_tokens.tolist()
+    for i in range(n_decode):
+        pos = len(prompt) + i
+        o_tok, o_lg, _ = om.step(int(fed[i]), pos, want_logits=True)
+        if o_tok != fed[i + 1]:
+            margin = top2_margin(o_lg)
+            assert margin < TIE_TOL * np.abs(o_lg).max(), (
+                f"decode step {i} (pos {pos}): gpu {fed[i + 1]} vs oracle {o_tok}, margin {margin:.3e}")
+            ties.append(pos)
+            return fed, ties, None  # the two streams diverge at a genuine near-tie
+    return fed, ties, o_lg
+
+
+def test_tiny_engine_tokens_logits_kv():
+    cfg = tiny_config()
+    eng, om = build(cfg, 11)
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab, 12)
+    toks, ties, _ = lockstep(eng, om, prompt, 40)
+    print(f"tiny: {len(toks)} tokens, near-ties at {ties}")
+    assert len(ties) == 0
+    pos = 12 + 40  # next position
+    # one more host-fed step with logits and hidden
+    lg_tok, lg = eng.step(toks[-1], pos, want_logits=True)
+    o_tok, o_lg, o_h = om.step(int(toks[-1]), pos, want_logits=True, want_hidden=True)
+    err = float(np.max(np.abs(lg - o_lg)) / np.max(np.abs(o_lg)))
+    herr = float(np.max(np.abs(eng.read_hidden() - o_h)) / np.max(np.abs(o_h)))
+    print(f"tiny logits err {err:.2e} hidden err {herr:.2e}")
+    assert err < LOGIT_TOL and herr < LOGIT_TOL
+    assert lg_tok == o_tok or top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max()
+    # KV caches: same written slots, values within tolerance
+    for layer in range(cfg.layers):
+        k, v = eng.read_kv(layer)  # [kvh][slots][hd]
+        slots = k.shape[1]
+        ok = om.kcache(layer, slots * cfg.kv_heads * cfg.head_dim).reshape(slots, cfg.kv_heads, cfg.head_dim)
+        ov = om.vcache(layer, slots * cfg.kv_heads * cfg.head_dim).reshape(slots, cfg.kv_heads, cfg.head_dim)
+        ok, ov = ok.transpose(1, 0, 2), ov.transpose(1, 0, 2)
+        written_g = np.any(k != 0, axis=(0, 2))
+        written_o = np.any(ok != 0, axis=(0, 2))
+        assert np.array_equal(written_g, written_o), f"layer {layer}: written slots differ"
+        for a, b in ((k, ok), (v, ov)):
+            fa = a.view(np.float16).astype(np.float64)
+            fb = b.view(np.float16).astype(np.float64)
+            d = np.abs(fa - fb)
+            print(f"layer {layer} cache max err {d.max() / np.abs(fb).max():.2e} mean err "
+                  f"{d.mean() / max(np.abs(fb).mean(), 1e-30):.2e}")
+            assert d.max() <= KV_MAX_TOL * np.abs(fb).max(), f"layer {layer} cache values (max)"
+            assert d.mean() <= KV_MEAN_TOL * np.abs(fb).mean(), f"layer {layer} cache values (mean)"
+        expect_written = (pos + 1) if cfg.layer_global[layer] else min(pos + 1, slots)
+        assert int(written_g.sum()) == expect_written
+
+
+def test_tiny_engine_step_api_and_reset():
+    cfg = tiny_config(layers=5)
+    eng, om = build(cfg, 5)
+    ids = [3, 17, 999, 0, 42]
+    a = [eng.step(t, i) for i, t in enumerate(ids)]
+    b = [om.step(t, i)[0] for i, t in enumerate(ids)]
+    assert a == b
+    eng.reset()
+    assert eng.prefill(ids) == b[-1]
+    assert eng.argmax_fast() == b[-1]
+    with pytest.raises(Exception):
+        eng.step(cfg.vocab, 0)  # token out of range
+    with pytest.raises(Exception):
+        eng.step(1, cfg.max_seq)  # position beyond the cache
+
+
+def test_generate_fast_matches_step_loop():
+    cfg = tiny_config()
+    eng, _ = build(cfg, 21)
+    prompt = [5, 6, 7, 8]
+    gen = eng.generate_fast(prompt, 20, eos=())
+    eng.reset()
+    toks = [eng.step(t, i) for i, t in enumerate(prompt)]
+    cur = toks[-1]
+    ref = [cur]
+    for i in range(19):
+        cur = eng.step(cur, len(prompt) + i)
+        ref.append(cur)
+    assert gen == ref
+
+
+def test_c4_width_five_layers():
+    cfg = E4BConfig(layers=5, max_seq=256, layer_global=[0, 0, 0, 0, 1])
+    eng, om = build(cfg, 3)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, 6)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 6)
+    print(f"c4-width 5 layers: near-ties {ties}")
+    assert len(ties) == 0
+    err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
+    print(f"c4-width logits err {err:.2e}")
+    assert err < LOGIT_TOL
+
+
+@pytest.mark.slow
+def test_c4_full_model_lockstep():
+    cfg = E4BConfig(max_seq=1024)  # BASELINE config c4 shapes (35 layers)
+    eng, om = build(cfg, 0)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, 8)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 16)
+    print(f"c4 full: tokens {toks[:8]}..., near-ties {ties}")
+    assert len(ties) == 0
+    err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
+    print(f"c4 full logits err {err:.2e}")
+    assert err < LOGIT_TOL
