@@ -130,22 +130,115 @@ def bench_c1(steps: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
+def _time_geglu(cfg, steps: int) -> dict:
+    """Dominant kernel of the c4 step: the fused gate/up GeGLU GEMV
+    ([2*ffn][hidden] q4_0, x f16 -> f16[ffn]).  Timed with HIP events over
+    `steps` launches that rotate over one copy per layer (as in the step, so
+    no launch is served from the 256 MB MALL)."""
+    from e4b import formats
+    from e4b.device import DeviceBuffer, Event
+    from e4b.kernels import Q40Matrix
+
+    rows, cols = 2 * cfg.ffn, cfg.hidden
+    w = formats.synth_q40(123, rows, cols, 0.02)
+    packed = formats.q40_pack(w, rows, cols)
+    mats = []
+    for _ in range(cfg.layers):
+        m = Q40Matrix.__new__(Q40Matrix)
+        m.rows, m.cols = rows, cols
+        m.buf = DeviceBuffer.from_array(packed)
+        mats.append(m)
+    x = DeviceBuffer.from_array(formats.synth_normal(5, cols).astype(np.float16))
+    out = DeviceBuffer(cfg.ffn * 2)
+    for i in range(2 * cfg.layers):
+        mats[i % len(mats)].geglu_dev(x, out)
+    e0, e1 = Event(), Event()
+    e0.record()
+    for i in range(steps):
+        mats[i % len(mats)].geglu_dev(x, out)
+    e1.record()
+    us = e0.elapsed_ms(e1) * 1e3 / steps
+    algo = rows * cols // 32 * 18 + cols * 2 + cfg.ffn * 2
+    return {"us": us, "algo": algo, "gbs": algo / (us * 1e-6) / 1e9}
+
+
+def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict:
+    from e4b import formats
+    from e4b._lib import FLAG_NO_GRAPH
+    from e4b.engine import Engine
+    from e4b.model import E4BConfig, synth_tensors
+
+    prompt_len = 512
+    cfg = E4BConfig(max_seq=max(1024, prompt_len + warmup + steps + 8), flags=FLAG_NO_GRAPH if no_graph else 0)
+    t0 = time.perf_counter()
+    tensors = synth_tensors(cfg, seed=0)
+    t_synth = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    eng = Engine(cfg, tensors)
+    t_load = time.perf_counter() - t0
+    prompt = formats.synth_uniform_u32(7, prompt_len, 0, cfg.vocab)
+    t0 = time.perf_counter()
+    eng.prefill(prompt)
+    t_prefill = time.perf_counter() - t0
+    eng.time_decode(prompt_len, warmup)
+    ms = eng.time_decode(prompt_len + warmup, steps)
+    ms_tok = ms / steps
+    positions = range(prompt_len + warmup, prompt_len + warmup + steps)
+    bytes_tok = sum(cfg.bytes_per_token(p) for p in positions) / steps
+    step_gbs = bytes_tok / (ms_tok * 1e-3) / 1e9
+    dom = _time_geglu(cfg, max(steps, 4 * cfg.layers))
+    out = {
+        "metric": METRIC, "value": round(1e3 / ms_tok, 2), "unit": "tokens/s", "ms_per_step": ms_tok,
+        "dtype": "q4_0/q6_K weights, f16 activations and KV, f32 accumulate",
+        "config": {"workload": "c4: E4B-shaped random-init decoder, 35 layers, hidden 2048, ffn 16384, "
+                               "8q/2kv x 256, 4 sliding(512):1 global, PLE 256, vocab 262144, q4_0 + Q6_K",
+                   "prompt_tokens": prompt_len, "decode_tokens_timed": steps, "decode_positions":
+                   [prompt_len + warmup, prompt_len + warmup + steps],
+                   "bytes_per_token": int(bytes_tok), "step_hbm_gbs": round(step_gbs, 1),
+                   "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "prefill_tokens_per_s": round(prompt_len / t_prefill, 1),
+                   "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
+        "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_q40 (gate/up GeGLU epilogue) 32768x2048",
+                     "algorithmic_bytes_per_launch": dom["algo"], "avg_launch_us": round(dom["us"], 3)},
+    }
+    eng.close()
+    if cpu:
+        import oracle as orc
+        om = orc.OracleModel(cfg.as_dict(), {n: t.data for n, t in tensors.items()})
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 15.0:
+            om.step(int(prompt[n]), n)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        out["cpu_baseline"] = {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": _cpu_cores(),
+                               "kind": "port", "sample": f"{n} oracle decode steps of the same model (~15 s)"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c1", choices=["c0", "c1"])
+    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c4"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="c4: launch the step kernels directly instead of replaying the hipGraph (for profilers)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
               "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
-    fn = {"c0": bench_c0, "c1": bench_c1}[a.workload]
-    steps = a.steps if a.steps is not None else 200
-    warmup = a.warmup if a.warmup is not None else 20
-    res = fn(steps, warmup, not a.no_cpu)
+    fn = {"c0": bench_c0, "c1": bench_c1, "c4": bench_c4}[a.workload]
+    steps = a.steps if a.steps is not None else (240 if a.workload == "c4" else 200)
+    warmup = a.warmup if a.warmup is not None else (16 if a.workload == "c4" else 20)
+    if a.workload == "c4":
+        res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph)
+    else:
+        res = fn(steps, warmup, not a.no_cpu)
     line = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(res["ms_per_step"], 6), "higher_is_better": True,

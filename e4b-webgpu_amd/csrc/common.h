@@ -204,6 +204,44 @@ DEV float reduce_rows(float (&v)[R]) {
   return RowReduce<LPR, R, R>::run(v);
 }
 
+// ---- block-level helpers (256 threads = 4 waves) --------------------------------
+DEV float wave_sum(float v) {
+  v = xsum_step<32>(v);
+  v = xsum_step<16>(v);
+  v = xsum_step<8>(v);
+  v = xsum_step<4>(v);
+  v = xsum_step<2>(v);
+  return xsum_step<1>(v);
+}
+DEV float wave_max(float v) {
+  float t = v;
+  swapx32(v, t);
+  v = fmaxf(v, t);
+  t = v;
+  swapx16(v, t);
+  v = fmaxf(v, t);
+  v = fmaxf(v, lane_xor<8>(v));
+  v = fmaxf(v, lane_xor<4>(v));
+  v = fmaxf(v, lane_xor<2>(v));
+  return fmaxf(v, lane_xor<1>(v));
+}
+// sum over a 256-thread block; every thread gets the total.  `red` = 4 floats of LDS.
+DEV float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+// RMSNorm scale (mean(x^2) + eps)^-1/2 from a sum of squares
+DEV float rms_inv(float ss, int n, float eps) { return 1.0f / sqrtf(ss / (float)n + eps); }
+// gelu_pytorch_tanh with the tanh argument clamped to +-20 (kernels/q40gu.wgsl:114)
+DEV float gelu_tanh(float g) {
+  float t = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+  t = fminf(fmaxf(t, -20.f), 20.f);
+  return 0.5f * g * (1.f + tanhf(t));
+}
+
 // non-temporal 16 B load for streamed weights (read once per token)
 typedef uint32_t e4b_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t e4b_u32x2 __attribute__((ext_vector_type(2)));

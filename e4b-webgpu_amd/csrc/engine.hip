@@ -63,12 +63,14 @@ struct e4b_ctx {
   float* inv_global = nullptr;
   // state / activations
   uint32_t *params = nullptr, *prompt = nullptr, *tok_ring = nullptr, *amax = nullptr, *status = nullptr;
-  float *h = nullptr, *proj = nullptr, *ple = nullptr, *qkv = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  float *h = nullptr, *hb = nullptr, *h_final = nullptr, *proj = nullptr, *ple = nullptr, *qkv = nullptr,
+        *part_o = nullptr, *part_ml = nullptr;
+  uint32_t* attn_cnt = nullptr;  // [kv_heads] attention combine counters
   float *o = nullptr, *dn = nullptr, *pp = nullptr, *logits = nullptr;
   uint16_t *h_hl = nullptr, *xn = nullptr, *attn = nullptr, *xf = nullptr, *gg = nullptr, *xg = nullptr,
            *gp = nullptr, *xo_hl = nullptr;
   uint2* amax_part = nullptr;
-  int nch = 16, ks_down = 1, ring_cap = 0, max_prompt = 0, amax_parts = 0;
+  int nch = 0, chunk = 64, ring_cap = 0, max_prompt = 0, amax_parts = 0;
   int64_t qkv_rows = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -140,12 +142,12 @@ extern "C" e4b_ctx* e4b_create(const e4b_config* cfg) {
     return nullptr;
   }
   const e4b_config& k = *cfg;
-  if (k.hidden <= 0 || k.hidden % 256 || k.hidden > 4096 || k.layers <= 0 || k.head_dim != 256 || k.kv_heads <= 0 ||
+  if (!q40_prologue_supported(k.hidden) || k.layers <= 0 || k.head_dim != 256 || k.kv_heads <= 0 ||
       k.q_heads != 4 * k.kv_heads || k.ffn <= 0 || k.ffn % 32 || k.vocab <= 0 ||
       (k.ple_dim != 0 && k.ple_dim != 256) || k.window <= 0 || k.ring < k.window || k.max_seq <= 0 ||
-      k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || k.attn_chunks < 0 || k.max_prompt < 0) {
+      k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || (k.attn_chunk != 0 && k.attn_chunk != 32 && k.attn_chunk != 64) || k.max_prompt < 0) {
     e4b_fail(E4B_EINVAL,
-             "e4b_create: unsupported config (hidden %d multiple of 256 and <= 4096, head_dim 256, q_heads = 4 * "
+             "e4b_create: unsupported config (hidden %d not 256, 512, 1024 or 2048, or: head_dim 256, q_heads = 4 * "
              "kv_heads, ple_dim 0 or 256, ring >= window)",
              k.hidden);
     return nullptr;
@@ -297,19 +299,17 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   // RoPE inverse frequencies THETA^(-2p/HD), rounded once to f32
   {
     std::vector<float> il(HD / 2), ig(HD / 2);
-    for (int p = 0; p < HD / 2; ++p) {
-      il[p] = (float)pow((double)k.theta_local, -2.0 * p / (double)HD);
-      ig[p] = (float)pow((double)k.theta_global, -2.0 * p / (double)HD);
-    }
+    rope_inv_freq(k.theta_local, HD, HD / 2, il.data());
+    rope_inv_freq(k.theta_global, HD, HD / 2, ig.data());
     if ((rc = upload_f32(c, &c->inv_local, il.data(), HD / 2)) || (rc = upload_f32(c, &c->inv_global, ig.data(), HD / 2)))
       return rc;
   }
-  // split-K chunking: every chunk covers at most attn_max_positions(nch)/nch positions
-  c->nch = k.attn_chunks > 0 ? k.attn_chunks : 16;
-  while (attn_max_positions(c->nch) < k.max_seq) c->nch *= 2;
-  // down projection: one column slice per 2048 columns, partials summed by the consumer
-  const int nb_down = FF / 32;
-  c->ks_down = (nb_down % 64 == 0) ? nb_down / 64 : 1;
+  // split-K attention: chunks of `chunk` positions; partials sized for the
+  // layer with the most live positions
+  c->chunk = k.attn_chunk ? k.attn_chunk : 64;
+  c->nch = attn_chunks(k.max_seq > k.window ? k.max_seq : k.window, c->chunk);
+  if (c->nch > kAttnMaxChunks)
+    return e4b_fail(E4B_EINVAL, "max_seq %d needs %d attention chunks (max %d)", k.max_seq, c->nch, kAttnMaxChunks);
   c->ring_cap = k.max_seq;
   c->max_prompt = k.max_prompt > 0 ? k.max_prompt : k.max_seq;
   c->amax_parts = q6k_gemv_grid(k.vocab);
@@ -325,19 +325,21 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   if ((rc = dalloc_t(c, &c->params, 16)) || (rc = dalloc_t(c, &c->prompt, (size_t)c->max_prompt)) ||
       (rc = dalloc_t(c, &c->tok_ring, (size_t)c->ring_cap)) || (rc = dalloc_t(c, &c->amax, 4)) ||
       (rc = dalloc_t(c, &c->status, 4)) || (rc = dalloc_t(c, &c->h, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->hb, (size_t)H)) || (rc = dalloc_t(c, &c->attn_cnt, (size_t)KVH)) ||
       (rc = dalloc_t(c, &c->h_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->proj, (size_t)NP)) ||
       (rc = dalloc_t(c, &c->ple, (size_t)NP)) || (rc = dalloc_t(c, &c->xn, (size_t)H)) ||
       (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) ||
       (rc = dalloc_t(c, &c->part_o, (size_t)QH * c->nch * HD)) ||
       (rc = dalloc_t(c, &c->part_ml, (size_t)QH * c->nch * 2)) || (rc = dalloc_t(c, &c->attn, (size_t)QH * HD)) ||
       (rc = dalloc_t(c, &c->o, (size_t)H)) || (rc = dalloc_t(c, &c->xf, (size_t)H)) ||
-      (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)c->ks_down * H)) ||
+      (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)H)) ||
       (rc = dalloc_t(c, &c->xg, (size_t)H)) || (rc = dalloc_t(c, &c->gp, (size_t)(PD ? PD : 1))) ||
       (rc = dalloc_t(c, &c->pp, (size_t)H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)))
     return rc;
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
+  if (k.flags & E4B_FLAG_NO_GRAPH) return E4B_OK;
   // capture one token
   E4B_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
   rc = record_step(c);
@@ -366,6 +368,27 @@ int record_step(e4b_ctx* c) {
   hipStream_t st = c->st;
   int rc;
   const Q6Mat E = q6_view(c->embd, k.vocab, H);
+  // the hidden state ping-pongs between two buffers: a fused prologue reads
+  // `hcur` in every block while block (0,0) writes the updated state to `hnext`
+  float* hcur = c->h;
+  float* hnext = c->hb;
+  auto swap_h = [&]() {
+    float* t = hcur;
+    hcur = hnext;
+    hnext = t;
+  };
+  auto pro = [&](float* hout, const float* a, const float* w1, const float* w2, float scale) {
+    ProArgs p;
+    p.hin = hcur;
+    p.hout = hout;
+    p.a = a;
+    p.w1 = w1;
+    p.w2 = w2;
+    p.scale = scale;
+    p.H = H;
+    p.eps = k.eps;
+    return p;
+  };
   if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, st))) return rc;
   if (PD) {
     GemvOut po = {c->proj, nullptr, nullptr, 0};
@@ -375,14 +398,29 @@ int record_step(e4b_ctx* c) {
     if ((rc = launch_ple_prep(c->proj, c->ple_tab, c->ple_norm, c->params, c->prompt, Lc, k.vocab,
                               1.0f / sqrtf((float)H), c->ple, c->h, c->L[0].attn_norm, c->xn, H, k.eps, st)))
       return rc;
-  } else {
-    if ((rc = launch_tail(c->h, nullptr, nullptr, 1.0f, c->L[0].attn_norm, c->xn, nullptr, H, k.eps, st))) return rc;
   }
   for (int l = 0; l < Lc; ++l) {
     const Layer& ly = c->L[l];
+    // 1. qkv GEMV; its prologue finishes the previous layer (last residual,
+    //    layer scalar) and applies this layer's input norm
     GemvOut oq = {c->qkv, nullptr, nullptr, 0};
-    if ((rc = launch_q40(q40_view(ly.qkv, c->qkv_rows, H), (const uint32_t*)c->xn, nullptr, EPI_F32, oq, 1, st)))
-      return rc;
+    const Q40Mat Wqkv = q40_view(ly.qkv, c->qkv_rows, H);
+    if (l == 0) {
+      if (PD) {
+        rc = launch_q40(Wqkv, (const uint32_t*)c->xn, nullptr, EPI_F32, oq, 1, st);
+      } else {
+        const ProArgs p = pro(nullptr, nullptr, nullptr, ly.attn_norm, 1.0f);
+        rc = launch_q40(Wqkv, nullptr, nullptr, EPI_F32, oq, 1, st, &p);
+      }
+    } else {
+      const Layer& pv = c->L[l - 1];
+      const ProArgs p = PD ? pro(hnext, c->pp, pv.post_norm, ly.attn_norm, pv.scale)
+                           : pro(hnext, c->dn, pv.post_ffw, ly.attn_norm, pv.scale);
+      rc = launch_q40(Wqkv, nullptr, nullptr, EPI_F32, oq, 1, st, &p);
+      swap_h();
+    }
+    if (rc) return rc;
+    // 2. attention (head prep, KV write, split-K, combine)
     AttnLaunch a;
     a.qkv = c->qkv;
     a.qw = ly.q_norm;
@@ -391,8 +429,10 @@ int record_step(e4b_ctx* c) {
     a.kc = ly.kc;
     a.vc = ly.vc;
     a.params = c->params;
+    a.pos = 0;
     a.part_o = c->part_o;
     a.part_ml = c->part_ml;
+    a.counter = c->attn_cnt;
     a.out = c->attn;
     a.qh = QH;
     a.kvh = KVH;
@@ -400,35 +440,44 @@ int record_step(e4b_ctx* c) {
     a.angles = k.rope_angles;
     a.slots = ly.slots;
     a.window = ly.global ? 0 : k.window;
-    a.nch = c->nch;
+    a.chunk = c->chunk;
     a.eps = k.eps;
     if ((rc = launch_attn(a, st))) return rc;
+    // 3. o projection
     GemvOut oo = {c->o, nullptr, nullptr, 0};
     if ((rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * HD), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st)))
       return rc;
-    if ((rc = launch_post_attn(c->h, c->o, ly.post_attn, ly.ffn_norm, c->xf, H, k.eps, st))) return rc;
-    GemvOut og = {nullptr, c->gg, nullptr, FF};
-    if ((rc = launch_q40(q40_view(ly.gu, 2 * (int64_t)FF, H), (const uint32_t*)c->xf, nullptr, EPI_GEGLU, og, 1, st)))
-      return rc;
-    GemvOut od = {c->dn, nullptr, nullptr, 0};
-    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, c->ks_down, st)))
-      return rc;
-    if ((rc = launch_post_ffn(c->h, c->dn, c->ks_down, ly.post_ffw, c->xg, H, k.eps, st))) return rc;
-    const bool last = (l + 1 == Lc);
-    const float* w_next = last ? c->out_norm : c->L[l + 1].attn_norm;
-    uint16_t* xn = last ? nullptr : c->xn;
-    uint16_t* xo = last ? c->xo_hl : nullptr;
-    if (PD) {
-      GemvOut ogp = {nullptr, c->gp, c->ple + (int64_t)l * PD, 0};
-      if ((rc = launch_q40(q40_view(ly.pg, PD, H), (const uint32_t*)c->xg, nullptr, EPI_GELU_MUL, ogp, 1, st)))
+    // 4. gate/up + GeGLU; prologue: post-attention residual + FFN input norm
+    {
+      const ProArgs p = pro(hnext, c->o, ly.post_attn, ly.ffn_norm, 1.0f);
+      GemvOut og = {nullptr, c->gg, nullptr, FF};
+      if ((rc = launch_q40(q40_view(ly.gu, 2 * (int64_t)FF, H), nullptr, nullptr, EPI_GEGLU, og, 1, st, &p)))
         return rc;
+      swap_h();
+    }
+    // 5. down projection
+    GemvOut od = {c->dn, nullptr, nullptr, 0};
+    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, 1, st)))
+      return rc;
+    if (PD) {
+      // 6. PLE gate + GELU x per-layer input; prologue: post-FFN residual
+      const ProArgs p = pro(hnext, c->dn, ly.post_ffw, nullptr, 1.0f);
+      GemvOut ogp = {nullptr, c->gp, c->ple + (int64_t)l * PD, 0};
+      if ((rc = launch_q40(q40_view(ly.pg, PD, H), nullptr, nullptr, EPI_GELU_MUL, ogp, 1, st, &p))) return rc;
+      swap_h();
+      // 7. PLE projection
       GemvOut opp = {c->pp, nullptr, nullptr, 0};
       if ((rc = launch_q40(q40_view(ly.pp, H, PD), (const uint32_t*)c->gp, nullptr, EPI_F32, opp, 1, st))) return rc;
-      if ((rc = launch_tail(c->h, c->pp, ly.post_norm, ly.scale, w_next, xn, xo, H, k.eps, st))) return rc;
-    } else {
-      if ((rc = launch_tail(c->h, nullptr, nullptr, ly.scale, w_next, xn, xo, H, k.eps, st))) return rc;
     }
   }
+  // last residual + final norm (f32, hi/lo split) -> lm-head -> argmax/feedback
+  const Layer& last = c->L[Lc - 1];
+  if (PD)
+    rc = launch_tail(hcur, c->pp, last.post_norm, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
+  else
+    rc = launch_tail(hcur, c->dn, last.post_ffw, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
+  if (rc) return rc;
+  c->h_final = hcur;
   if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
                                    c->logits, nullptr, c->amax_part, st)))
     return rc;
@@ -453,6 +502,15 @@ int check_status(e4b_ctx* c) {
   return E4B_OK;
 }
 
+// one token: replay the captured graph, or launch the kernels directly
+int launch_token(e4b_ctx* c) {
+  if (c->exec) {
+    E4B_HIP(hipGraphLaunch(c->exec, c->st));
+    return E4B_OK;
+  }
+  return record_step(c);
+}
+
 int put_params(e4b_ctx* c, const uint32_t* v, int first, int count) {
   E4B_HIP(hipMemcpyAsync(c->params + first, v, (size_t)count * 4, hipMemcpyHostToDevice, c->st));
   return E4B_OK;
@@ -466,8 +524,7 @@ extern "C" int e4b_step(e4b_ctx* c, uint32_t token, uint32_t pos, float* logits,
   if (token >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_step: token %u >= vocab %d", token, c->cfg.vocab);
   if (pos >= (uint32_t)c->cfg.max_seq) return e4b_fail(E4B_ERANGE, "e4b_step: pos %u >= max_seq %d", pos, c->cfg.max_seq);
   const uint32_t p[4] = {pos, token, 0u, 0u};
-  if ((rc = put_params(c, p, 0, 4))) return rc;
-  E4B_HIP(hipGraphLaunch(c->exec, c->st));
+  if ((rc = put_params(c, p, 0, 4)) || (rc = launch_token(c))) return rc;
   uint32_t am[2] = {0, 0};
   E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
   if (logits) E4B_HIP(hipMemcpyAsync(logits, c->logits, (size_t)c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->st));
@@ -487,7 +544,8 @@ extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t
   E4B_HIP(hipMemcpyAsync(c->prompt, ids, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
   const uint32_t p[4] = {0u, 0u, 0u, n};
   if ((rc = put_params(c, p, 0, 4))) return rc;
-  for (uint32_t i = 0; i < n; ++i) E4B_HIP(hipGraphLaunch(c->exec, c->st));
+  for (uint32_t i = 0; i < n; ++i)
+    if ((rc = launch_token(c))) return rc;
   uint32_t am[2] = {0, 0};
   E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
   if ((rc = check_status(c))) return rc;
@@ -503,7 +561,8 @@ static int decode_launch(e4b_ctx* c, uint32_t start_pos, uint32_t count) {
   const uint32_t p0 = start_pos, z[2] = {0u, 0u};
   int rc;
   if ((rc = put_params(c, &p0, 0, 1)) || (rc = put_params(c, z, 2, 2))) return rc;
-  for (uint32_t i = 0; i < count; ++i) E4B_HIP(hipGraphLaunch(c->exec, c->st));
+  for (uint32_t i = 0; i < count; ++i)
+    if ((rc = launch_token(c))) return rc;
   return E4B_OK;
 }
 
@@ -550,7 +609,8 @@ extern "C" int e4b_argmax(e4b_ctx* c, uint32_t* token_out) {
 extern "C" int e4b_read_hidden(e4b_ctx* c, float* out) {
   int rc = ready(c, "e4b_read_hidden");
   if (rc) return rc;
-  E4B_HIP(hipMemcpyAsync(out, c->h, (size_t)c->cfg.hidden * 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipMemcpyAsync(out, c->h_final ? c->h_final : c->h, (size_t)c->cfg.hidden * 4, hipMemcpyDeviceToHost,
+                         c->st));
   E4B_HIP(hipStreamSynchronize(c->st));
   return E4B_OK;
 }
@@ -591,6 +651,7 @@ extern "C" int e4b_reset(e4b_ctx* c) {
     E4B_HIP(hipMemsetAsync(ly.vc, 0, n, c->st));
   }
   E4B_HIP(hipMemsetAsync(c->params, 0, 16 * 4, c->st));
+  E4B_HIP(hipMemsetAsync(c->attn_cnt, 0, (size_t)c->cfg.kv_heads * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->status, 0, 4 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->amax, 0, 4 * 4, c->st));
   E4B_HIP(hipStreamSynchronize(c->st));

@@ -205,3 +205,10 @@ extern "C" int e4b_synth_q6k(uint64_t seed, int64_t rows, int64_t cols, float si
   }
   return E4B_OK;
 }
+
+// ---------------------------------------------------------------------------
+// RoPE table (the inverse-frequency uniform of kernels/headprep.wgsl)
+// ---------------------------------------------------------------------------
+void rope_inv_freq(float theta, int head_dim, int angles, float* out) {
+  for (int p = 0; p < angles; ++p) out[p] = (float)pow((double)theta, -2.0 * (double)p / (double)head_dim);
+}

@@ -1,0 +1,328 @@
+// k_attn.hip -- decode attention for one layer in one launch: head prep (q/k
+// weighted head-RMS + NeoX-half RoPE, v scale-less RMS; kernels/headprep.wgsl
+// :19-87), the K/V cache write of the new position, split-K online-softmax
+// partials over the live positions (kernels/attsplit.wgsl:16-76) and the
+// log-sum-exp combine (kernels/attcomb.wgsl:10-36), done by the last block
+// of each KV group to finish.
+//
+// Split-K: the live positions are cut into chunks of CS (32 or 64)
+// positions, one block per (KV group, chunk); the grid is sized for the most
+// live positions a layer can have and blocks past the live chunks exit.
+//
+// Cache layout [kv_head][slot][256] f16.  Sliding layers keep a ring of
+// `slots` entries: position p lives in slot p % slots, and the live window is
+// (pos - W, pos]; since slots >= W every live position still owns its slot,
+// which is the SoundRec/Complete property of specs/KVRing.tla for decode.
+// Iterating positions (instead of the reference's slot scan with position
+// recovery, kernels/attnf32.wgsl:30-53) visits exactly the live slots.
+#include "../../include/e4b.h"
+#include "kernels.h"
+#include "step.h"
+#include "util.h"
+
+namespace {
+
+constexpr int HD = 256;
+constexpr int GQA = 4;
+
+struct AttnArgs {
+  const float* qkv;
+  const float* qw;
+  const float* kw;
+  const float* inv_freq;
+  uint16_t* kc;
+  uint16_t* vc;
+  const uint32_t* params;
+  uint32_t pos;
+  float* part_o;
+  float* part_ml;
+  uint32_t* counter;  // [kvh] arrivals, returned to 0 by the combining block
+  uint16_t* out;
+  int qh, kvh, angles, slots, window;
+  float eps;
+};
+
+// weighted head RMS over 256 dims held 4 per lane, then NeoX-half RoPE:
+// dims p < 128 (lanes 0..31) pair with p + 128 (lanes 32..63).
+DEV void prep_head(float (&x)[4], const float* w, const float* inv_freq, int angles, float eps, float fpos,
+                   bool rotate) {
+  const int lane = threadIdx.x & 63;
+  const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+  const float inv = rms_inv(ss, HD, eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = x[i] * inv * (w ? w[4 * lane + i] : 1.f);
+  if (!rotate) return;
+  const bool hi = lane >= 32;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float a = x[i], b = x[i];
+    swapx32(a, b);  // lo lanes: b = partner (dim p + 128); hi lanes: a = partner (dim p)
+    const float partner = hi ? a : b;
+    const int p = 4 * (lane & 31) + i;
+    if (p < angles) {
+      const float th = fpos * inv_freq[p];
+      float sn, cs;
+      sincosf(th, &sn, &cs);
+      x[i] = hi ? (partner * sn + x[i] * cs) : (x[i] * cs - partner * sn);
+    }
+  }
+}
+
+DEV void unpack16(const uint4& a, const uint4& b, float* f) {
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f[2 * i] = h2f((uint16_t)(w[i] & 0xffff));
+    f[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+  }
+}
+
+// One block per (KV group g, chunk c of CS positions).  Every K and V row of
+// the chunk is requested before the head prep starts, so the whole chunk is
+// one memory round trip: K as 16 lanes x 32 B per position (4 positions per
+// wave-step), V as 8 B per lane (wave w takes positions w, w+4, ...).
+template <int CS>
+__global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
+  constexpr int KS = CS / 16;  // score steps
+  constexpr int VS = CS / 4;   // P.V positions per wave
+  __shared__ float qs[GQA][HD];
+  __shared__ __align__(16) uint16_t knew[HD];
+  __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ float sc[GQA][CS];
+  __shared__ float po[4][GQA][HD];
+  __shared__ float mlx[GQA][2];
+  __shared__ int is_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = blockIdx.x, c = blockIdx.y;
+  // 32-bit position arithmetic throughout (positions < 2^31): a 64-bit
+  // modulo is a long software sequence on this ISA
+  const int pos = (int)(A.params ? A.params[0] : A.pos);
+  const int lo = (A.window > 0 && pos + 1 > A.window) ? pos + 1 - A.window : 0;
+  const int n = pos + 1 - lo;
+  const int nch = (n + CS - 1) / CS;  // live chunks; the rest of the grid idles
+  if (c >= nch) return;
+  const int c_lo = lo + c * CS;
+  const int m = min(CS, n - c * CS);
+  const float fpos = (float)pos;
+  uint16_t* kc = A.kc + (int64_t)g * A.slots * HD;
+  uint16_t* vc = A.vc + (int64_t)g * A.slots * HD;
+  // slot of position c_lo + j: one modulo per block; j < m <= window <= slots
+  // so the ring index wraps at most once inside a chunk
+  const int s_lo = A.window > 0 ? c_lo % A.slots : c_lo;
+  auto slot_at = [&](int j) -> int64_t {
+    const int s = s_lo + j;
+    return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
+  };
+  const int sub = lane >> 4, dl = lane & 15;
+
+  // 0. request the chunk's K and V rows (index clamped into the chunk; the
+  //    row of `pos` is not written yet and is replaced from LDS below)
+  uint4 kr[KS][2];
+  uint2 vr[VS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int j = min(16 * s + 4 * wave + sub, m - 1);
+    const uint4* p = reinterpret_cast<const uint4*>(kc + slot_at(j) * HD + 16 * dl);
+    kr[s][0] = p[0];
+    kr[s][1] = p[1];
+  }
+#pragma unroll
+  for (int i = 0; i < VS; ++i) {
+    const int j = min(4 * i + wave, m - 1);
+    vr[i] = *reinterpret_cast<const uint2*>(vc + slot_at(j) * HD + 4 * lane);
+  }
+
+  // 1. head prep: wave j preps q head 4g+j; waves 0/1 also prep the group's
+  //    new k/v (f16-rounded, as stored); the chunk owning `pos` writes them
+  {
+    float x[4];
+    const float* src = A.qkv + (int64_t)(g * GQA + wave) * HD + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = src[i];
+    prep_head(x, A.qw, A.inv_freq, A.angles, A.eps, fpos, true);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = x[i];
+  }
+  const bool owner = pos < c_lo + m;  // the last live chunk holds pos, at j = m - 1
+  if (wave < 2) {
+    float x[4];
+    const float* src = A.qkv + (int64_t)(A.qh + (wave == 0 ? 0 : A.kvh) + g) * HD + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = src[i];
+    prep_head(x, wave == 0 ? A.kw : nullptr, A.inv_freq, A.angles, A.eps, fpos, wave == 0);
+    const uint2 pk = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
+                                (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
+    *reinterpret_cast<uint2*>((wave == 0 ? knew : vnew) + 4 * lane) = pk;
+    if (owner) *reinterpret_cast<uint2*>((wave == 0 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
+  }
+  __syncthreads();
+
+  // 2. scores: 16 lanes per position (16 dims each), 4 positions per wave-step
+  {
+    float q[GQA][16];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q[h][i] = qs[h][16 * dl + i];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int j = 16 * s + 4 * wave + sub;
+      uint4 ka = kr[s][0], kb = kr[s][1];
+      if (c_lo + j == pos) {
+        const uint4* kn = reinterpret_cast<const uint4*>(knew + 16 * dl);
+        ka = kn[0];
+        kb = kn[1];
+      }
+      float kf[16];
+      unpack16(ka, kb, kf);
+      float t[GQA];
+#pragma unroll
+      for (int h = 0; h < GQA; ++h) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a = fmaf(q[h][i], kf[i], a);
+        t[h] = a;
+      }
+      const float v = reduce_rows<16, GQA>(t);  // lane dl holds head dl/4
+      if ((dl & 3) == 0 && j < m) sc[dl >> 2][j] = v;
+    }
+  }
+  __syncthreads();
+
+  // 3. chunk softmax statistics: wave h owns head h, lane j position j
+  {
+    float mx = -3.0e38f;
+    for (int j = lane; j < m; j += 64) mx = fmaxf(mx, sc[wave][j]);
+    mx = wave_max(mx);
+    float sum = 0.f;
+    for (int j = lane; j < m; j += 64) {
+      const float e = __expf(sc[wave][j] - mx);
+      sc[wave][j] = e;
+      sum += e;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      mlx[wave][0] = mx;
+      mlx[wave][1] = sum;
+    }
+  }
+  __syncthreads();
+
+  // 4. P.V: wave w takes positions j = w, w+4, ...; lane covers dims 4l..4l+3
+  {
+    float acc[GQA][4];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[h][i] = 0.f;
+    const uint2 vn = *reinterpret_cast<const uint2*>(vnew + 4 * lane);
+#pragma unroll
+    for (int i = 0; i < VS; ++i) {
+      const int j = 4 * i + wave;
+      if (j < m) {
+        const uint2 vv = (c_lo + j == pos) ? vn : vr[i];
+        const float vf[4] = {h2f((uint16_t)(vv.x & 0xffff)), h2f((uint16_t)(vv.x >> 16)),
+                             h2f((uint16_t)(vv.y & 0xffff)), h2f((uint16_t)(vv.y >> 16))};
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+          const float pj = sc[h][j];
+#pragma unroll
+          for (int d = 0; d < 4; ++d) acc[h][d] = fmaf(pj, vf[d], acc[h][d]);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) po[wave][h][4 * lane + d] = acc[h][d];
+  }
+  __syncthreads();
+
+  // 5. this chunk's partials ([head][chunk][dim], [head][chunk][max, sum])
+  const int gch = gridDim.y;  // partial stride: chunks allocated per head
+  for (int i = threadIdx.x; i < GQA * HD; i += 256) {
+    const int h = i / HD, d = i % HD;
+    A.part_o[((int64_t)(g * GQA + h) * gch + c) * HD + d] = (po[0][h][d] + po[1][h][d]) + (po[2][h][d] + po[3][h][d]);
+  }
+  if (threadIdx.x < GQA) {
+    const int64_t pi = ((int64_t)(g * GQA + threadIdx.x) * gch + c) * 2;
+    A.part_ml[pi] = mlx[threadIdx.x][0];
+    A.part_ml[pi + 1] = mlx[threadIdx.x][1];
+  }
+
+  // 6. the last live chunk of this KV group to finish combines its four heads
+  //    (log-sum-exp merge, kernels/attcomb.wgsl:10-36)
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&A.counter[g], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (prev == (uint32_t)nch - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();  // acquire: every chunk's partials are visible (plain loads below)
+  __shared__ float mls[GQA][2 * kAttnMaxChunks];
+#pragma unroll
+  for (int h = 0; h < GQA; ++h)
+    for (int r = threadIdx.x; r < 2 * nch; r += 256) mls[h][r] = A.part_ml[((int64_t)(g * GQA + h) * gch) * 2 + r];
+  __syncthreads();
+  const int d = threadIdx.x;
+#pragma unroll
+  for (int hh = 0; hh < GQA; ++hh) {
+    float M = -3.0e38f;
+    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, mls[hh][2 * cc]);
+    const float* po_h = A.part_o + (int64_t)(g * GQA + hh) * gch * HD + d;
+    float den = 0.f, acc = 0.f;
+#pragma unroll 8
+    for (int cc = 0; cc < nch; ++cc) {
+      const float f = __expf(mls[hh][2 * cc] - M);
+      den = fmaf(mls[hh][2 * cc + 1], f, den);
+      acc = fmaf(po_h[(int64_t)cc * HD], f, acc);
+    }
+    A.out[(g * GQA + hh) * HD + d] = f2h(acc / den);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&A.counter[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+int attn_chunks(int max_positions, int chunk) { return (max_positions + chunk - 1) / chunk; }
+
+int launch_attn(const AttnLaunch& a, hipStream_t st) {
+  if (a.hd != HD || a.qh != GQA * a.kvh)
+    return e4b_fail(E4B_EINVAL, "attention kernel supports head_dim 256 and 4 q heads per kv head (got %d, %d/%d)", a.hd,
+                    a.qh, a.kvh);
+  if (a.chunk != 32 && a.chunk != 64) return e4b_fail(E4B_EINVAL, "attention: chunk %d is not 32 or 64", a.chunk);
+  const int span = a.window > 0 ? a.window : a.slots;  // most live positions
+  if (a.window > a.slots) return e4b_fail(E4B_EINVAL, "attention: window %d exceeds %d ring slots", a.window, a.slots);
+  const int nch = attn_chunks(span, a.chunk);
+  if (nch > kAttnMaxChunks)
+    return e4b_fail(E4B_EINVAL, "attention: %d positions need %d chunks of %d (max %d)", span, nch, a.chunk,
+                    kAttnMaxChunks);
+  if (!a.counter) return e4b_fail(E4B_EINVAL, "attention: null counter");
+  AttnArgs A;
+  A.qkv = a.qkv;
+  A.qw = a.qw;
+  A.kw = a.kw;
+  A.inv_freq = a.inv_freq;
+  A.kc = a.kc;
+  A.vc = a.vc;
+  A.params = a.params;
+  A.pos = a.pos;
+  A.part_o = a.part_o;
+  A.part_ml = a.part_ml;
+  A.counter = a.counter;
+  A.out = a.out;
+  A.qh = a.qh;
+  A.kvh = a.kvh;
+  A.angles = a.angles;
+  A.slots = a.slots;
+  A.window = a.window;
+  A.eps = a.eps;
+  if (a.chunk == 64)
+    hipLaunchKernelGGL(k_attn<64>, dim3(a.kvh, nch), dim3(256), 0, st, A);
+  else
+    hipLaunchKernelGGL(k_attn<32>, dim3(a.kvh, nch), dim3(256), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}

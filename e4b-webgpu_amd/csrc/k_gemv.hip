@@ -1,17 +1,9 @@
-// k_gemv.hip -- q4_0 and Q6_K dequant-GEMV kernels for gfx950 (wave64).
+// k_gemv.hip -- Q6_K dequant-GEMV (lm-head + softcap + argmax), Q6_K row
+// dequant, argmax and the f32 -> hi/lo f16 split for gfx950 (wave64).  The
+// q4_0 GEMV lives in q40_kernel.h.
 //
-// Design (HBM-bound, batch 1):
-//  * every lane streams 16 B weight blocks with non-temporal dwordx4 loads;
-//    all of a lane's loads for one pass are issued before any math, so each
-//    lane keeps R*BPL loads in flight;
-//  * dequant happens in registers: a repacked nibble pair is an f16
-//    subnormal pair and one v_dot2_f32_f16 multiplies it with the natural
-//    (x[2j], x[2j+1]) f16 pair, accumulating in f32 (layout in common.h);
-//  * a wave is split into 64/LPR lane groups, one row per group, so short
-//    rows (e.g. 22 or 8 blocks) do not idle most of the wave;
-//  * the per-row partials are reduced with a butterfly inside the group.
-// f32 activations are carried as an exact hi/lo f16 split (x = hi + lo), so
-// the f32 path is as accurate as an f32 dot product.
+// f32 activations are carried as an exact hi/lo f16 split (x = hi + lo), so a
+// v_dot2_f32_f16 product over both halves is as accurate as an f32 dot.
 #include "../../include/e4b.h"
 #include "kernels.h"
 #include "util.h"
@@ -30,113 +22,6 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
     xp[4 * i + 1] = t.y;
     xp[4 * i + 2] = t.z;
     xp[4 * i + 3] = t.w;
-  }
-}
-
-DEV float gelu_tanh(float g) {
-  float t = 0.7978845608028654f * (g + 0.044715f * g * g * g);
-  t = fminf(fmaxf(t, -20.f), 20.f);
-  return 0.5f * g * (1.f + tanhf(t));
-}
-
-// Persistent q4_0 GEMV.  A wave splits into 64/LPR lane groups; a group owns
-// R rows ("slots") of a tile and each lane covers blocks jb = l + LPR*k of
-// them; the activation slice of those blocks stays in registers for the
-// whole kernel while the wave strides over tiles.  blockIdx.y selects one of
-// KS column slices (partial outputs).
-template <int LPR, int BPL, int R, bool XLO, int EPI>
-__global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restrict__ xh,
-                                             const uint32_t* __restrict__ xl, GemvOut o, int64_t ntiles,
-                                             int nbk) {
-  constexpr int G = 64 / LPR, SPAN = LPR / R;
-  static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane / LPR, l = lane - g * LPR;
-  const int kslice = blockIdx.y, jb0 = kslice * nbk;
-  const int nb = W.nb;
-
-  uint32_t xp[BPL][16];
-  uint32_t xq[BPL][XLO ? 16 : 1];
-  float xs8[BPL];
-#pragma unroll
-  for (int k = 0; k < BPL; ++k) {
-    const int jb = l + LPR * k;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) xp[k][i] = 0u;
-    if constexpr (XLO) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xq[k][i] = 0u;
-    }
-    xs8[k] = 0.f;
-    if (jb < nbk) {
-      load_x16(xh, jb0 + jb, xp[k]);
-      float xs = xsum16(xp[k]);
-      if constexpr (XLO) {
-        load_x16(xl, jb0 + jb, xq[k]);
-        xs += xsum16(xq[k]);
-      }
-      xs8[k] = -8.f * xs;
-    }
-  }
-
-  const int64_t units = (EPI == EPI_GEGLU) ? 2 * o.ff : W.rows;
-  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 4) {
-    const int64_t slot0 = tile * (G * R) + (int64_t)g * R;
-    int64_t rowof[R];
-    bool ok[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if constexpr (EPI == EPI_GEGLU) {
-        const int64_t u = slot0 / 2 + r / 2;
-        rowof[r] = (r & 1) ? o.ff + u : u;
-        ok[r] = u < o.ff;
-      } else {
-        rowof[r] = slot0 + r;
-        ok[r] = slot0 + r < units;
-      }
-    }
-    // loads always issue (row and block clamped into range); slots past the
-    // end are computed on duplicate data and never stored, and blocks past
-    // the slice end meet zeroed activations
-    uint4 wq[R][BPL];
-    uint16_t ws[R][BPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t row = ok[r] ? rowof[r] : (W.rows - 1);
-      const uint4* nrow = W.nib + row * nb + jb0;
-      const uint16_t* srow = W.sc + row * nb + jb0;
-#pragma unroll
-      for (int k = 0; k < BPL; ++k) {
-        const int jb = min(l + LPR * k, nbk - 1);
-        wq[r][k] = ld_nt_u4(nrow + jb);
-        ws[r][k] = ld_nt_u16(srow + jb);
-      }
-    }
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      acc[r] = 0.f;
-#pragma unroll
-      for (int k = 0; k < BPL; ++k) {
-        float a = q40_dot(wq[r][k], xp[k], 0.f);
-        if constexpr (XLO) a = q40_dot(wq[r][k], xq[k], a);
-        acc[r] = fmaf(h2f(ws[r][k]), fmaf(a, kTwo24, xs8[k]), acc[r]);
-      }
-    }
-    float v = reduce_rows<LPR, R>(acc);
-    const int r = l / SPAN;  // this lane now holds slot r of the tile
-    if constexpr (EPI == EPI_GEGLU) {
-      const float up = __shfl_xor(v, SPAN, 64);
-      const int64_t u = slot0 / 2 + r / 2;
-      if ((l % (2 * SPAN)) == 0 && u < o.ff) o.yh[u] = f2h(gelu_tanh(v) * up);
-    } else {
-      const int64_t row = slot0 + r;
-      if ((l % SPAN) == 0 && row < W.rows) {
-        if constexpr (EPI == EPI_F32) o.y[(int64_t)kslice * W.rows + row] = v;
-        if constexpr (EPI == EPI_GELU_MUL) o.yh[row] = f2h(gelu_tanh(v) * o.mul[row]);
-      }
-    }
   }
 }
 
@@ -343,121 +228,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int
   amax_block(bv, bi, part);
 }
 
-// ---- q4_0 launch configuration ---------------------------------------------
-struct Q40Cfg {
-  int lpr, bpl, r;
-};
-
-static Q40Cfg pick_q40(int nbk, int64_t units, int epi) {
-  Q40Cfg best = {64, 1, 1};
-  double best_util = -1.0;
-  const int lprs[4] = {64, 32, 16, 8};
-  for (int i = 0; i < 4; ++i) {
-    const int lpr = lprs[i];
-    int bpl = (nbk + lpr - 1) / lpr;
-    if (bpl > 8) continue;
-    if (bpl == 5) bpl = 6;
-    if (bpl == 7) bpl = 8;
-    const double util = (double)nbk / (double)(lpr * bpl);
-    if (util > best_util + 1e-9) {
-      best_util = util;
-      best = {lpr, bpl, 1};
-    }
-  }
-  // rows per group: ~8 weight loads in flight per lane, but keep >= 512 workgroups
-  const int G = 64 / best.lpr;
-  int r = best.bpl == 1 ? 8 : best.bpl == 2 ? 4 : best.bpl <= 4 ? 2 : 1;
-  if (r > best.lpr) r = best.lpr;
-  const int rmin = (epi == EPI_GEGLU) ? 2 : 1;
-  while (r > rmin && (units + 4 * G * r - 1) / (4 * G * r) < 512) r >>= 1;
-  if (r < rmin) r = rmin;
-  best.r = r;
-  return best;
-}
-
-template <int LPR, int BPL, int R, bool XLO, int EPI>
-static void launch_t(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, const GemvOut& o, int64_t units,
-                     int ks, int nbk, hipStream_t st) {
-  constexpr int G = 64 / LPR;
-  const int64_t ntiles = (units + G * R - 1) / (G * R);
-  int64_t wgs = (ntiles + 3) / 4;
-  if (wgs > 2048) wgs = 2048;
-  hipLaunchKernelGGL((k_q40<LPR, BPL, R, XLO, EPI>), dim3((unsigned)wgs, (unsigned)ks), dim3(256), 0, st, W, xh, xl, o,
-                     ntiles, nbk);
-}
-
-template <int LPR, int BPL, bool XLO, int EPI>
-static bool launch_r(int r, const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, const GemvOut& o, int64_t units,
-                     int ks, int nbk, hipStream_t st) {
-  switch (r) {
-    case 1:
-      if constexpr (EPI != EPI_GEGLU) {
-        launch_t<LPR, BPL, 1, XLO, EPI>(W, xh, xl, o, units, ks, nbk, st);
-        return true;
-      }
-      return false;
-    case 2: launch_t<LPR, BPL, 2, XLO, EPI>(W, xh, xl, o, units, ks, nbk, st); return true;
-    case 4: launch_t<LPR, BPL, 4, XLO, EPI>(W, xh, xl, o, units, ks, nbk, st); return true;
-    case 8: launch_t<LPR, BPL, 8, XLO, EPI>(W, xh, xl, o, units, ks, nbk, st); return true;
-  }
-  return false;
-}
-
-template <int LPR, bool XLO, int EPI>
-static bool launch_b(const Q40Cfg& c, const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, const GemvOut& o,
-                     int64_t units, int ks, int nbk, hipStream_t st) {
-  switch (c.bpl) {
-    case 1: return launch_r<LPR, 1, XLO, EPI>(c.r, W, xh, xl, o, units, ks, nbk, st);
-    case 2: return launch_r<LPR, 2, XLO, EPI>(c.r, W, xh, xl, o, units, ks, nbk, st);
-    case 3: return launch_r<LPR, 3, XLO, EPI>(c.r, W, xh, xl, o, units, ks, nbk, st);
-    case 4: return launch_r<LPR, 4, XLO, EPI>(c.r, W, xh, xl, o, units, ks, nbk, st);
-    case 6: return launch_r<LPR, 6, XLO, EPI>(c.r, W, xh, xl, o, units, ks, nbk, st);
-    case 8: return launch_r<LPR, 8, XLO, EPI>(c.r, W, xh, xl, o, units, ks, nbk, st);
-  }
-  return false;
-}
-
-template <bool XLO, int EPI>
-static bool launch_l(const Q40Cfg& c, const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, const GemvOut& o,
-                     int64_t units, int ks, int nbk, hipStream_t st) {
-  switch (c.lpr) {
-    case 64: return launch_b<64, XLO, EPI>(c, W, xh, xl, o, units, ks, nbk, st);
-    case 32: return launch_b<32, XLO, EPI>(c, W, xh, xl, o, units, ks, nbk, st);
-    case 16: return launch_b<16, XLO, EPI>(c, W, xh, xl, o, units, ks, nbk, st);
-    case 8: return launch_b<8, XLO, EPI>(c, W, xh, xl, o, units, ks, nbk, st);
-  }
-  return false;
-}
-
 }  // namespace
-
-int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi, const GemvOut& o, int ks,
-               hipStream_t st) {
-  if (ks < 1 || W.nb % ks) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per row not divisible by ks=%d", W.nb, ks);
-  if (ks > 1 && epi != EPI_F32) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: column split needs the f32 epilogue");
-  const int nbk = W.nb / ks;
-  if (nbk > 64 * 8)
-    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per slice exceeds the 512-block (16384-column) maximum", nbk);
-  const int64_t units = (epi == EPI_GEGLU) ? 2 * o.ff : W.rows;
-  const Q40Cfg c = pick_q40(nbk, units, epi);
-  bool ok = false;
-  switch (epi) {
-    case EPI_F32:
-      ok = xl ? launch_l<true, EPI_F32>(c, W, xh, xl, o, units, ks, nbk, st)
-              : launch_l<false, EPI_F32>(c, W, xh, xl, o, units, ks, nbk, st);
-      break;
-    case EPI_GEGLU: ok = !xl && launch_l<false, EPI_GEGLU>(c, W, xh, xl, o, units, ks, nbk, st); break;
-    case EPI_GELU_MUL: ok = !xl && launch_l<false, EPI_GELU_MUL>(c, W, xh, xl, o, units, ks, nbk, st); break;
-  }
-  if (!ok) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: no kernel for epi=%d lpr=%d bpl=%d r=%d", epi, c.lpr, c.bpl, c.r);
-  E4B_HIP(hipGetLastError());
-  return E4B_OK;
-}
-
-int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st) {
-  GemvOut o = {y, nullptr, nullptr, 0};
-  return launch_q40(W, xh, xl, EPI_F32, o, 1, st);
-}
 
 int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st) {
   hipLaunchKernelGGL(k_split_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, hi, lo);

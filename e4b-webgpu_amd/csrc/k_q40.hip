@@ -1,0 +1,56 @@
+// k_q40.hip -- q4_0 GEMV entry point: validates the request, picks the lane
+// split / rows per group / column split, and hands over to the translation
+// unit that instantiates the matching kernel variant (k_q40_*.hip).
+#include "../../include/e4b.h"
+#include "q40_kernel.h"
+#include "util.h"
+
+bool q40_prologue_supported(int H) { return H == 256 || H == 512 || H == 1024 || H == 2048; }
+
+int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi, const GemvOut& o, int ks,
+               hipStream_t st, const ProArgs* pro) {
+  if (epi != EPI_F32 && epi != EPI_GEGLU && epi != EPI_GELU_MUL)
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: unknown epilogue %d", epi);
+  if (ks < 1 || W.nb % ks) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per row not divisible by ks=%d", W.nb, ks);
+  if (ks > 1 && epi != EPI_F32) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: column split needs the f32 epilogue");
+  if (xl && epi != EPI_F32) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: hi/lo input needs the f32 epilogue");
+  if (epi == EPI_GEGLU && (o.ff < 1 || 2 * o.ff != W.rows))
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: GeGLU needs 2*ff rows (rows=%lld ff=%lld)", (long long)W.rows,
+                    (long long)o.ff);
+  const int nbk = W.nb / ks;
+  if (nbk < 1) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: empty row");
+  if (pro && (xl || ks != 1 || pro->H != W.nb * 32 || !q40_prologue_supported(pro->H) || !pro->hin ||
+              (pro->a && !pro->w1)))
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: prologue needs f16 input of a full 256/512/1024/2048 row (H=%d, cols=%d)",
+                    pro ? pro->H : 0, W.nb * 32);
+  q40k::Launch L;
+  L.W = W;
+  L.xh = xh;
+  L.xl = xl;
+  L.o = o;
+  L.units = (epi == EPI_GEGLU) ? 2 * o.ff : W.rows;
+  L.ks = ks;
+  L.nbk = nbk;
+  L.pa = pro ? *pro : ProArgs{};
+  L.st = st;
+  const q40k::Cfg c = q40k::pick(nbk, L.units, epi, pro != nullptr);
+  if (c.bpl > 8 || c.lpr * c.bpl * c.kw < nbk)
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per slice exceeds the 2048-block (65536-column) maximum", nbk);
+  bool ok;
+  if (pro)
+    ok = q40k::dispatch_pro(c, L, epi);
+  else if (c.kw == 4)
+    ok = q40k::dispatch_kw4(c, L, epi);
+  else if (epi != EPI_F32)
+    ok = q40k::dispatch_glu(c, L, epi);
+  else
+    ok = xl ? q40k::dispatch_f32_hl(c, L) : q40k::dispatch_f32(c, L);
+  if (!ok) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: no kernel for epi=%d lpr=%d bpl=%d r=%d kw=%d", epi, c.lpr, c.bpl, c.r, c.kw);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st) {
+  GemvOut o = {y, nullptr, nullptr, 0};
+  return launch_q40(W, xh, xl, EPI_F32, o, 1, st, nullptr);
+}

@@ -1,0 +1,9 @@
+// k_q40_pro.hip -- q4_0 GEMV variants with the fused residual/norm prologue.
+#include "q40_kernel.h"
+
+bool q40k::dispatch_pro(const Cfg& c, const Launch& L, int epi) {
+  if (epi == EPI_F32) return launch_pro<EPI_F32>(c, L);
+  if (epi == EPI_GEGLU) return launch_pro<EPI_GEGLU>(c, L);
+  if (epi == EPI_GELU_MUL) return launch_pro<EPI_GELU_MUL>(c, L);
+  return false;
+}

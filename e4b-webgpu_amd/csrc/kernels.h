@@ -67,11 +67,28 @@ struct GemvOut {
   int64_t ff;        // EPI_GEGLU: rows per half
 };
 
-// launchers (defined in k_gemv.hip); all asynchronous on `st`
+// Optional fused input prologue of a q4_0 GEMV (q40_kernel.h):
+// h = (hin + rms(a) * w1) * scale (a may be null: h = hin * scale),
+// x = w2 ? f16(rms(h) * w2) : f16(h); block (0,0) stores h to hout.
+// H = cols must be 256, 512, 1024 or 2048.
+struct ProArgs {
+  const float* hin;
+  float* hout;       // may be null
+  const float* a;    // may be null
+  const float* w1;
+  const float* w2;   // may be null
+  float scale;
+  int H;
+  float eps;
+};
+bool q40_prologue_supported(int H);
+
+// launchers (q4_0 in k_q40.hip, the rest in k_gemv.hip); all asynchronous on `st`
 // ks > 1 splits the columns into ks equal slices (cols/32 divisible by ks)
-// and writes ks partial vectors (EPI_F32 only).
+// and writes ks partial vectors (EPI_F32 only).  pro != null replaces the
+// f16 input xh by the fused prologue (cols must equal pro->H).
 int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi, const GemvOut& o, int ks,
-               hipStream_t st);
+               hipStream_t st, const ProArgs* pro = nullptr);
 int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st);
 int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st);
 // part: one (index, value) partial per block (<= 2048); amax may be NULL to

@@ -5,6 +5,7 @@
 
 #include "../../include/e4b.h"
 #include "kernels.h"
+#include "step.h"
 #include "util.h"
 
 static thread_local char g_last_error[1024] = "";
@@ -153,6 +154,18 @@ extern "C" int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, 
   return launch_q40_gemv(W, (const uint32_t*)hi, (const uint32_t*)lo, y, st);
 }
 
+extern "C" int e4b_k_q40_gemv_geglu(const void* w_packed, int64_t ff, int64_t cols, const void* x, void* out,
+                                    void* stream) {
+  if (!w_packed || !x || !out || ff <= 0 || cols <= 0 || cols % 32)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemv_geglu: bad arguments (ff=%lld cols=%lld)", (long long)ff,
+                    (long long)cols);
+  if (!aligned16(w_packed) || !aligned16(x))
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemv_geglu: weight and x must be 16-byte aligned");
+  GemvOut o = {nullptr, (uint16_t*)out, nullptr, ff};
+  return launch_q40(q40_view(w_packed, 2 * ff, cols), (const uint32_t*)x, nullptr, EPI_GEGLU, o, 1,
+                    (hipStream_t)stream);
+}
+
 extern "C" int e4b_split_f32(const float* x, int64_t n, void* hl, void* stream) {
   if (!x || !hl || n <= 0) return e4b_fail(E4B_EINVAL, "e4b_split_f32: bad arguments");
   return launch_split_f32(x, n, (uint16_t*)hl, (uint16_t*)hl + n, (hipStream_t)stream);
@@ -192,4 +205,54 @@ extern "C" int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* str
   int rc = e4b_workspace(1024 * sizeof(uint2), &ws);
   if (rc) return rc;
   return launch_argmax(x, n, amax, (uint2*)ws.buf, (hipStream_t)stream);
+}
+
+extern "C" int e4b_rope_inv_freq(float theta, int head_dim, int angles, float* out) {
+  if (!out || head_dim <= 0 || head_dim % 2 || angles < 0 || angles > head_dim / 2 || !(theta > 0.f))
+    return e4b_fail(E4B_EINVAL, "e4b_rope_inv_freq: bad arguments (theta=%g head_dim=%d angles=%d)", (double)theta,
+                    head_dim, angles);
+  rope_inv_freq(theta, head_dim, angles, out);
+  return E4B_OK;
+}
+
+extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const float* k_norm, const float* inv_freq,
+                                 int rope_angles, void* k_cache, void* v_cache, int q_heads, int kv_heads,
+                                 int head_dim, int slots, int window, uint32_t pos, float eps, int chunk,
+                                 void* out_f16, void* stream) {
+  if (!qkv || !q_norm || !k_norm || (rope_angles > 0 && !inv_freq) || !k_cache || !v_cache || !out_f16 ||
+      q_heads <= 0 || kv_heads <= 0 || slots <= 0 || window < 0 || rope_angles < 0 || rope_angles > head_dim / 2)
+    return e4b_fail(E4B_EINVAL, "e4b_k_attn_decode: bad arguments");
+  if (window == 0 && pos >= (uint32_t)slots)
+    return e4b_fail(E4B_ERANGE, "e4b_k_attn_decode: position %u beyond the %d-position global cache", pos, slots);
+  if (kv_heads > E4B_NCOUNTERS) return e4b_fail(E4B_EINVAL, "e4b_k_attn_decode: %d kv heads", kv_heads);
+  if (chunk == 0) chunk = 64;
+  const int span = window > 0 ? window : slots;
+  const int nch = attn_chunks(span, chunk > 0 ? chunk : 64);
+  Workspace ws;
+  const size_t ob = E4B_ALIGN256((size_t)q_heads * nch * head_dim * sizeof(float));
+  const size_t mb = (size_t)q_heads * nch * 2 * sizeof(float);
+  int rc = e4b_workspace(ob + mb, &ws);
+  if (rc) return rc;
+  AttnLaunch a;
+  a.qkv = qkv;
+  a.qw = q_norm;
+  a.kw = k_norm;
+  a.inv_freq = inv_freq;
+  a.kc = (uint16_t*)k_cache;
+  a.vc = (uint16_t*)v_cache;
+  a.params = nullptr;
+  a.pos = pos;
+  a.part_o = (float*)ws.buf;
+  a.part_ml = (float*)(ws.buf + ob);
+  a.counter = ws.counters;
+  a.out = (uint16_t*)out_f16;
+  a.qh = q_heads;
+  a.kvh = kv_heads;
+  a.hd = head_dim;
+  a.angles = rope_angles;
+  a.slots = slots;
+  a.window = window;
+  a.chunk = chunk;
+  a.eps = eps;
+  return launch_attn(a, (hipStream_t)stream);
 }

@@ -1,4 +1,4 @@
-// step.h -- launchers of the decode-step kernels in k_step.hip.
+// step.h -- launchers of the decode-step kernels in k_attn.hip / k_step.hip.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -11,24 +11,24 @@ struct AttnLaunch {
   const float* inv_freq;   // RoPE inverse frequencies [angles]
   uint16_t* kc;            // [kvh][slots][hd] f16 key cache
   uint16_t* vc;            // [kvh][slots][hd] f16 value cache
-  const uint32_t* params;  // params[0] = position of the current token
-  float* part_o;           // [qh][nch][hd] split-K partial outputs
-  float* part_ml;          // [qh][nch][2]  (chunk max, chunk sum)
+  const uint32_t* params;  // params[0] = position of the current token (device), or
+  uint32_t pos;            //   this position when params is null
+  float* part_o;           // [qh][attn_chunks(span, chunk)][hd] split-K partial outputs
+  float* part_ml;          // [qh][attn_chunks(span, chunk)][2]  (chunk max, chunk sum)
+  uint32_t* counter;       // [kvh] zero-initialised arrival counters
   uint16_t* out;           // [qh][hd] f16 attention output
   int qh, kvh, hd, angles;
   int slots;               // ring slots (sliding) or capacity (global)
   int window;              // sliding window; 0 = global layer (linear cache)
-  int nch;                 // split-K chunks
+  int chunk;               // positions per split-K chunk: 32 or 64
   float eps;
 };
 
 int launch_attn(const AttnLaunch& a, hipStream_t st);
-int attn_max_positions(int nch);
-int launch_post_attn(float* h, const float* o, const float* w_pa, const float* w_ffn, uint16_t* xf, int H, float eps,
-                     hipStream_t st);
-int launch_post_ffn(float* h, const float* dn, int ks, const float* w_pf, uint16_t* xg, int H, float eps,
-                    hipStream_t st);
-int launch_tail(float* h, const float* p, const float* w_post, float scale, const float* w_next, uint16_t* xn,
+constexpr int kAttnMaxChunks = 512;
+// split-K chunks a layer of `max_positions` live positions needs
+int attn_chunks(int max_positions, int chunk);
+int launch_tail(float* h, const float* p, const float* w_post, float scale, const float* w_out,
                 uint16_t* xo_hl, int H, float eps, hipStream_t st);
 int launch_embed(const Q6Mat& E, const uint32_t* params, const uint32_t* prompt, float mult, float* h, uint16_t* h_hl,
                  uint32_t* status, hipStream_t st);

@@ -7,6 +7,10 @@
 // `code`, so call sites read `return e4b_fail(E4B_EINVAL, "...")`.
 int e4b_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// RoPE inverse frequencies theta^(-2p/head_dim) for p < angles, rounded once
+// to f32 from a double pow (host.cpp)
+void rope_inv_freq(float theta, int head_dim, int angles, float* out);
+
 #ifdef __HIPCC__
 #include <hip/hip_runtime.h>
 #define E4B_HIP(call)                                                                      \

@@ -77,9 +77,13 @@ SIGNATURES = [
     ("e4b_q6k_packed_bytes", _sz, [_i64, _i64]),
     ("e4b_q6k_pack", _i32, [_vp, _i64, _i64, _vp]),
     ("e4b_k_q40_gemv", _i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
+    ("e4b_k_q40_gemv_geglu", _i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     ("e4b_k_q6k_gemv_argmax", _i32, [_vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_row", _i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),
     ("e4b_k_argmax", _i32, [_vp, _i64, _vp, _vp]),
+    ("e4b_rope_inv_freq", _i32, [_f32, _i32, _i32, _vp]),
+    ("e4b_k_attn_decode", _i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _u32, _f32,
+                                 _i32, _vp, _vp]),
     ("e4b_create", _vp, [_vp]),
     ("e4b_set_tensor", _i32, [_vp, C.c_char_p, _i32, _P(_i64), _i32, _vp, _sz]),
     ("e4b_finalize", _i32, [_vp]),
@@ -104,8 +108,11 @@ class ConfigC(C.Structure):
         ("hidden", _i32), ("layers", _i32), ("q_heads", _i32), ("kv_heads", _i32), ("head_dim", _i32),
         ("ffn", _i32), ("ple_dim", _i32), ("vocab", _i32), ("window", _i32), ("ring", _i32), ("max_seq", _i32),
         ("rope_angles", _i32), ("theta_local", _f32), ("theta_global", _f32), ("eps", _f32), ("softcap", _f32),
-        ("layer_global", _vp), ("attn_chunks", _i32), ("max_prompt", _i32),
+        ("layer_global", _vp), ("attn_chunk", _i32), ("max_prompt", _i32), ("flags", _u32),
     ]
+
+
+FLAG_NO_GRAPH = 1
 
 for _name, _res, _args in SIGNATURES:
     _fn = getattr(lib, _name)

@@ -62,7 +62,7 @@ class Engine:
         self.cfg = cfg
         c = ConfigC()
         for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
-                  "max_seq", "rope_angles", "attn_chunks", "max_prompt"):
+                  "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags"):
             setattr(c, f, int(getattr(cfg, f)))
         for f in ("theta_local", "theta_global", "eps", "softcap"):
             setattr(c, f, float(getattr(cfg, f)))

@@ -31,6 +31,17 @@ class Q40Matrix:
         check(lib.e4b_k_q40_gemv(_vp(self.buf), self.rows, self.cols, _vp(x), x_dtype, _vp(y), _vp(stream)),
               "e4b_k_q40_gemv")
 
+    def geglu_dev(self, x: DeviceBuffer, out: DeviceBuffer, stream=None) -> None:
+        """rows = [gate (ff) ; up (ff)]: out f16[ff] = gelu(gate . x) * (up . x)"""
+        check(lib.e4b_k_q40_gemv_geglu(_vp(self.buf), self.rows // 2, self.cols, _vp(x), _vp(out), _vp(stream)),
+              "e4b_k_q40_gemv_geglu")
+
+    def geglu(self, x: np.ndarray) -> np.ndarray:
+        xd = DeviceBuffer.from_array(x.astype(np.float16))
+        out = DeviceBuffer(self.rows // 2 * 2)
+        self.geglu_dev(xd, out)
+        return out.download(np.float16, self.rows // 2)
+
     def gemv(self, x: np.ndarray) -> np.ndarray:
         """Host convenience: x is float32 or float16 [cols] -> float32 [rows]."""
         dt = DT_F16 if x.dtype == np.float16 else DT_F32
@@ -72,3 +83,56 @@ def argmax(x: np.ndarray):
     check(lib.e4b_k_argmax(_vp(xd), x.size, _vp(am), None), "e4b_k_argmax")
     a = am.download(np.uint32, 2)
     return int(a[0]), float(a[1:2].view(np.float32)[0])
+
+
+def rope_inv_freq(theta: float, head_dim: int, angles: int) -> np.ndarray:
+    """f32 RoPE inverse frequencies theta^(-2p/head_dim), p < angles."""
+    out = np.zeros(max(angles, 1), np.float32)
+    check(lib.e4b_rope_inv_freq(C.c_float(theta), head_dim, angles, out.ctypes.data_as(C.c_void_p)),
+          "e4b_rope_inv_freq")
+    return out[:angles]
+
+
+class AttnLayer:
+    """One layer's decode attention with its f16 KV cache resident on the device.
+
+    Cache layout [kv_heads][slots][head_dim]; window > 0 is a sliding ring
+    (position p in slot p % slots), window == 0 a global cache (slot p).
+    """
+
+    def __init__(self, q_heads: int, kv_heads: int, head_dim: int, slots: int, window: int,
+                 theta: float, rope_angles: int, q_norm: np.ndarray, k_norm: np.ndarray, eps: float = 1e-6,
+                 chunk: int = 0):
+        self.qh, self.kvh, self.hd, self.slots, self.window = q_heads, kv_heads, head_dim, slots, window
+        self.angles, self.eps, self.chunk = rope_angles, eps, chunk
+        self.inv_freq = DeviceBuffer.from_array(rope_inv_freq(theta, head_dim, rope_angles)
+                                                if rope_angles else np.zeros(1, np.float32))
+        self.qw = DeviceBuffer.from_array(np.asarray(q_norm, np.float32))
+        self.kw = DeviceBuffer.from_array(np.asarray(k_norm, np.float32))
+        n = kv_heads * slots * head_dim
+        self.kc = DeviceBuffer(n * 2)
+        self.vc = DeviceBuffer(n * 2)
+        self.out = DeviceBuffer(q_heads * head_dim * 2)
+        self.qkv = DeviceBuffer((q_heads + 2 * kv_heads) * head_dim * 4)
+
+    def load_cache(self, k: np.ndarray, v: np.ndarray) -> None:
+        """k, v: f16 [kv_heads][slots][head_dim]"""
+        self.kc.upload(np.ascontiguousarray(k, np.float16))
+        self.vc.upload(np.ascontiguousarray(v, np.float16))
+
+    def read_cache(self):
+        shape = (self.kvh, self.slots, self.hd)
+        n = self.kvh * self.slots * self.hd
+        return (self.kc.download(np.float16, n).reshape(shape), self.vc.download(np.float16, n).reshape(shape))
+
+    def step_dev(self, pos: int, stream=None) -> None:
+        check(lib.e4b_k_attn_decode(_vp(self.qkv), _vp(self.qw), _vp(self.kw), _vp(self.inv_freq), self.angles,
+                                    _vp(self.kc), _vp(self.vc), self.qh, self.kvh, self.hd, self.slots, self.window,
+                                    pos, C.c_float(self.eps), self.chunk, _vp(self.out), _vp(stream)),
+              "e4b_k_attn_decode")
+
+    def step(self, qkv: np.ndarray, pos: int) -> np.ndarray:
+        """qkv f32 [(qh + 2 kvh) * hd] raw projections -> f16 [qh * hd]"""
+        self.qkv.upload(np.ascontiguousarray(qkv, np.float32))
+        self.step_dev(pos)
+        return self.out.download(np.float16, self.qh * self.hd)

@@ -36,8 +36,9 @@ class E4BConfig:
     eps: float = 1e-6
     softcap: float = 30.0
     layer_global: list = field(default_factory=list)
-    attn_chunks: int = 0
+    attn_chunk: int = 0
     max_prompt: int = 0
+    flags: int = 0
 
     def __post_init__(self):
         if not self.layer_global:

@@ -104,6 +104,12 @@ int    e4b_q6k_pack(const void* ggml, int64_t rows, int64_t cols, void* packed_h
 int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, const void* x,
                    int x_dtype, float* y, void* stream);
 
+/* Fused gate/up q4_0 GEMV + GeGLU (kernels/q40gu.wgsl:62-119, dense role):
+ * w_packed is [2*ff][cols] with gate rows [0,ff) then up rows [ff,2ff); x f16;
+ * out f16[ff] = f16(gelu_tanh(gate) * up), tanh argument clamped to +-20. */
+int e4b_k_q40_gemv_geglu(const void* w_packed, int64_t ff, int64_t cols, const void* x_f16,
+                         void* out_f16, void* stream);
+
 /* Q6_K GEMV + softcap + argmax (kernels/q6k.wgsl:75-130 MODE 1, then
  * kernels/argmax2.wgsl:8-48).  logits f32[rows] (may be NULL), amax u32[2] =
  * {index, f32 bits of the max}; ties -> lowest index; NaN never wins.
@@ -117,6 +123,29 @@ int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row,
 
 /* argmax over f32[n] (kernels/argmax2.wgsl:8-48): amax u32[2]. */
 int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* stream);
+
+/* RoPE inverse frequencies out[p] = f32(theta^(-2p/head_dim)), p < angles
+ * (host; the table headprep uses, kernels/headprep.wgsl:19-87). */
+int e4b_rope_inv_freq(float theta, int head_dim, int angles, float* out_host);
+
+/* One layer's decode attention for the token at `pos` (kernels/headprep.wgsl
+ * :19-87, kernels/attsplit.wgsl:16-76 + kernels/attcomb.wgsl:10-36; one launch).
+ *   qkv       f32[(q_heads + 2 kv_heads) * 256]: raw q heads, then k, then v
+ *   q_norm, k_norm  f32[256] head-RMS weights (v gets a scale-less RMS)
+ *   inv_freq  f32[rope_angles] (e4b_rope_inv_freq), NeoX pairs (p, p + 128)
+ *   k_cache, v_cache  f16 [kv_heads][slots][256]; position p lives in slot
+ *             p % slots when window > 0 (sliding ring, slots >= window), in
+ *             slot p when window == 0 (global, pos < slots).  The new k/v is
+ *             written to the slot of `pos`; live positions are
+ *             (pos - window, pos] (sliding) or [0, pos] (global).
+ *   chunk     positions per split-K chunk: 32 or 64 (0 = 64)
+ *   out_f16   [q_heads][256] attention output, f16.
+ * head_dim must be 256 and q_heads = 4 * kv_heads.  Uses the per-device
+ * workspace: calls on one device must be ordered (one stream). */
+int e4b_k_attn_decode(const float* qkv, const float* q_norm, const float* k_norm,
+                      const float* inv_freq, int rope_angles, void* k_cache, void* v_cache,
+                      int q_heads, int kv_heads, int head_dim, int slots, int window,
+                      uint32_t pos, float eps, int chunk, void* out_f16, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Engine: the per-token batch-1 decode step of an E4B-shaped decoder
@@ -147,9 +176,14 @@ typedef struct e4b_config {
   float eps;              /* 1e-6 */
   float softcap;          /* 30 (0 = none) */
   const uint8_t* layer_global; /* [layers] 1 = global; NULL = (i % 5 == 4) */
-  int32_t attn_chunks;    /* split-K chunks per layer, 0 = default */
+  int32_t attn_chunk;     /* positions per split-K attention chunk: 32 or 64, 0 = 64 */
   int32_t max_prompt;     /* prompt buffer capacity, 0 = max_seq */
+  uint32_t flags;         /* E4B_FLAG_* */
 } e4b_config;
+
+/* launch the step's kernels directly each token instead of replaying the
+ * captured hipGraph (same kernels; for profilers that do not follow graphs) */
+#define E4B_FLAG_NO_GRAPH 1u
 
 /* tensor names follow the GGUF naming of the E4B family:
  *   token_embd.weight (Q6_K [vocab][hidden], tied lm-head), output_norm.weight,

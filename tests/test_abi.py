@@ -124,3 +124,9 @@ def test_tensor_bytes_matches_gguf_js():
     assert formats.tensor_bytes(_lib.GGML_F32, [7]) == 28
     with pytest.raises(ValueError):
         formats.tensor_bytes(_lib.GGML_Q4_0, [33])
+
+
+def test_rope_table_matches_oracle():
+    from e4b.kernels import rope_inv_freq
+    for theta in (1e4, 1e6):
+        np.testing.assert_array_equal(rope_inv_freq(theta, 256, 128), orc.rope_inv_freq(theta, 256, 128))
