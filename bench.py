@@ -131,10 +131,12 @@ def bench_c1(steps: int, warmup: int, cpu: bool) -> dict:
 
 
 def _time_geglu(cfg, steps: int) -> dict:
-    """Dominant kernel of the c4 step: the fused gate/up GeGLU GEMV
-    ([2*ffn][hidden] q4_0, x f16 -> f16[ffn]).  Timed with HIP events over
-    `steps` launches that rotate over one copy per layer (as in the step, so
-    no launch is served from the 256 MB MALL)."""
+    """Dominant kernel of the c4 step: the FFN input GEMV exactly as the step
+    launches it -- fused residual + RMSNorm prologue, gate/up q4_0 GEMV
+    ([2*ffn][hidden]) and GeGLU epilogue to f16[ffn]
+    (e4b_k_q40_geglu_prenorm).  Timed with HIP events on the launch stream
+    over `steps` launches that rotate over one weight copy per layer (as in
+    the step, so no launch is served from the 256 MB MALL)."""
     from e4b import formats
     from e4b.device import DeviceBuffer, Event
     from e4b.kernels import Q40Matrix
@@ -148,17 +150,26 @@ def _time_geglu(cfg, steps: int) -> dict:
         m.rows, m.cols = rows, cols
         m.buf = DeviceBuffer.from_array(packed)
         mats.append(m)
-    x = DeviceBuffer.from_array(formats.synth_normal(5, cols).astype(np.float16))
+    h_in = DeviceBuffer.from_array(formats.synth_normal(5, cols))
+    resid = DeviceBuffer.from_array(formats.synth_normal(6, cols))
+    w_res = DeviceBuffer.from_array(np.ones(cols, np.float32))
+    w_in = DeviceBuffer.from_array(np.ones(cols, np.float32))
+    h_out = DeviceBuffer(cols * 4)
     out = DeviceBuffer(cfg.ffn * 2)
+
+    def launch(i):
+        mats[i % len(mats)].geglu_prenorm_dev(h_in, resid, w_res, w_in, 1.0, cfg.eps, h_out, out)
+
     for i in range(2 * cfg.layers):
-        mats[i % len(mats)].geglu_dev(x, out)
+        launch(i)
     e0, e1 = Event(), Event()
     e0.record()
     for i in range(steps):
-        mats[i % len(mats)].geglu_dev(x, out)
+        launch(i)
     e1.record()
     us = e0.elapsed_ms(e1) * 1e3 / steps
-    algo = rows * cols // 32 * 18 + cols * 2 + cfg.ffn * 2
+    # weights + 4 f32 prologue vectors in + h out (f32) + f16 GeGLU out
+    algo = rows * cols // 32 * 18 + 4 * cols * 4 + cols * 4 + cfg.ffn * 2
     return {"us": us, "algo": algo, "gbs": algo / (us * 1e-6) / 1e9}
 
 
@@ -200,7 +211,7 @@ def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict
                    "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_q40 (gate/up GeGLU epilogue) 32768x2048",
+                     "kernel": "k_q40 gate/up 32768x2048, residual+norm prologue, GeGLU epilogue",
                      "algorithmic_bytes_per_launch": dom["algo"], "avg_launch_us": round(dom["us"], 3)},
     }
     eng.close()
@@ -225,6 +236,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c4"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (the byte scale for rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--no-graph", action="store_true",
                     help="c4: launch the step kernels directly instead of replaying the hipGraph (for profilers)")
     a = ap.parse_args()
@@ -239,6 +252,13 @@ def main() -> int:
         res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph)
     else:
         res = fn(steps, warmup, not a.no_cpu)
+    if a.copy_probe:
+        from e4b._lib import check, lib
+        from e4b.device import DeviceBuffer, sync
+        n = 256 << 20
+        src, dst = DeviceBuffer(n), DeviceBuffer(n)
+        check(lib.e4b_memcpy_d2d(dst.ptr, src.ptr, n, None), "copy probe")
+        sync()
     line = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(res["ms_per_step"], 6), "higher_is_better": True,

@@ -74,6 +74,23 @@ DEV float xsum16(const uint32_t* xp) {
   return s;
 }
 
+// Two-accumulator form of q40_dot: the pairs at bits 0-3 of each half go to
+// a0 (value n * 2^-24), the pairs at bits 4-7 are used in place (value
+// 16 n * 2^-24) and go to a1, so a word costs 4 masks and 1 shift instead of
+// 4 masks and 3 shifts.  2^-24 sum n_i x_i = a0 + a1 / 16.
+DEV void q40_dot2(uint4 w, const uint32_t* xp, float& a0, float& a1) {
+  const uint32_t M = 0x000F000Fu, M4 = 0x00F000F0u;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t v = ws[k], v8 = ws[k] >> 8;
+    a0 = fdot2u(v & M, xp[4 * k + 0], a0);
+    a1 = fdot2u(v & M4, xp[4 * k + 2], a1);
+    a0 = fdot2u(v8 & M, xp[4 * k + 1], a0);
+    a1 = fdot2u(v8 & M4, xp[4 * k + 3], a1);
+  }
+}
+
 // 2^-24 * sum n_i x_i over one repacked q4_0 block
 DEV float q40_dot(uint4 w, const uint32_t* xp, float acc) {
   const uint32_t M = 0x000F000Fu;
@@ -232,6 +249,13 @@ DEV float block_sum(float v, float* red) {
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   return (red[0] + red[1]) + (red[2] + red[3]);
+}
+DEV float block_max(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 // RMSNorm scale (mean(x^2) + eps)^-1/2 from a sum of squares
 DEV float rms_inv(float ss, int n, float eps) { return 1.0f / sqrtf(ss / (float)n + eps); }

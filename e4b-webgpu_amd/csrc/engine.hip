@@ -65,7 +65,7 @@ struct e4b_ctx {
   uint32_t *params = nullptr, *prompt = nullptr, *tok_ring = nullptr, *amax = nullptr, *status = nullptr;
   float *h = nullptr, *hb = nullptr, *h_final = nullptr, *proj = nullptr, *ple = nullptr, *qkv = nullptr,
         *part_o = nullptr, *part_ml = nullptr;
-  uint32_t* attn_cnt = nullptr;  // [kv_heads] attention combine counters
+  float2* rope = nullptr;        // [2][head_dim/2] (cos, sin) at the current position: local, global
   float *o = nullptr, *dn = nullptr, *pp = nullptr, *logits = nullptr;
   uint16_t *h_hl = nullptr, *xn = nullptr, *attn = nullptr, *xf = nullptr, *gg = nullptr, *xg = nullptr,
            *gp = nullptr, *xo_hl = nullptr;
@@ -325,7 +325,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   if ((rc = dalloc_t(c, &c->params, 16)) || (rc = dalloc_t(c, &c->prompt, (size_t)c->max_prompt)) ||
       (rc = dalloc_t(c, &c->tok_ring, (size_t)c->ring_cap)) || (rc = dalloc_t(c, &c->amax, 4)) ||
       (rc = dalloc_t(c, &c->status, 4)) || (rc = dalloc_t(c, &c->h, (size_t)H)) ||
-      (rc = dalloc_t(c, &c->hb, (size_t)H)) || (rc = dalloc_t(c, &c->attn_cnt, (size_t)KVH)) ||
+      (rc = dalloc_t(c, &c->hb, (size_t)H)) || (rc = dalloc_t(c, &c->rope, (size_t)HD)) ||
       (rc = dalloc_t(c, &c->h_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->proj, (size_t)NP)) ||
       (rc = dalloc_t(c, &c->ple, (size_t)NP)) || (rc = dalloc_t(c, &c->xn, (size_t)H)) ||
       (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) ||
@@ -389,7 +389,9 @@ int record_step(e4b_ctx* c) {
     p.eps = k.eps;
     return p;
   };
-  if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, st))) return rc;
+  if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, c->inv_local,
+                         c->inv_global, HD / 2, c->rope, st)))
+    return rc;
   if (PD) {
     GemvOut po = {c->proj, nullptr, nullptr, 0};
     if ((rc = launch_q40(q40_view(c->ple_proj, (int64_t)Lc * PD, H), (const uint32_t*)c->h_hl,
@@ -432,7 +434,7 @@ int record_step(e4b_ctx* c) {
     a.pos = 0;
     a.part_o = c->part_o;
     a.part_ml = c->part_ml;
-    a.counter = c->attn_cnt;
+    a.rope = c->rope + (ly.global ? HD / 2 : 0);
     a.out = c->attn;
     a.qh = QH;
     a.kvh = KVH;
@@ -651,7 +653,6 @@ extern "C" int e4b_reset(e4b_ctx* c) {
     E4B_HIP(hipMemsetAsync(ly.vc, 0, n, c->st));
   }
   E4B_HIP(hipMemsetAsync(c->params, 0, 16 * 4, c->st));
-  E4B_HIP(hipMemsetAsync(c->attn_cnt, 0, (size_t)c->cfg.kv_heads * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->status, 0, 4 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->amax, 0, 4 * 4, c->st));
   E4B_HIP(hipStreamSynchronize(c->st));

@@ -1,13 +1,19 @@
-// k_attn.hip -- decode attention for one layer in one launch: head prep (q/k
-// weighted head-RMS + NeoX-half RoPE, v scale-less RMS; kernels/headprep.wgsl
-// :19-87), the K/V cache write of the new position, split-K online-softmax
-// partials over the live positions (kernels/attsplit.wgsl:16-76) and the
-// log-sum-exp combine (kernels/attcomb.wgsl:10-36), done by the last block
-// of each KV group to finish.
+// k_attn.hip -- decode attention for one layer: head prep (q/k weighted
+// head-RMS + NeoX-half RoPE, v scale-less RMS; kernels/headprep.wgsl:19-87)
+// with the K/V cache write of the new position, split-K softmax partials over
+// the live positions (kernels/attsplit.wgsl:16-76) in one launch, and the
+// log-sum-exp combine (kernels/attcomb.wgsl:10-36) in a second.
+//
+// The combine is its own launch on purpose: on this part a kernel boundary
+// (~2.5 us) is the cheapest grid-wide ordering.  A last-block combine needs
+// an agent-scope release/acquire pair per block (L2 write-back and
+// invalidate across the 8 XCDs), which measured 5-9 us for 16-36 blocks.
 //
 // Split-K: the live positions are cut into chunks of CS (32 or 64)
-// positions, one block per (KV group, chunk); the grid is sized for the most
-// live positions a layer can have and blocks past the live chunks exit.
+// positions, one 512-thread block per (KV group, chunk); the grid is sized
+// for the most live positions a layer can have and blocks past the live
+// chunks exit.  Every K and V row of a chunk is requested before the head
+// prep starts, so the chunk costs one memory round trip.
 //
 // Cache layout [kv_head][slot][256] f16.  Sliding layers keep a ring of
 // `slots` entries: position p lives in slot p % slots, and the live window is
@@ -30,13 +36,13 @@ struct AttnArgs {
   const float* qw;
   const float* kw;
   const float* inv_freq;
+  const float2* rope;  // per-step (cos, sin) table, or null to evaluate sincosf here
   uint16_t* kc;
   uint16_t* vc;
   const uint32_t* params;
   uint32_t pos;
   float* part_o;
   float* part_ml;
-  uint32_t* counter;  // [kvh] arrivals, returned to 0 by the combining block
   uint16_t* out;
   int qh, kvh, angles, slots, window;
   float eps;
@@ -44,8 +50,8 @@ struct AttnArgs {
 
 // weighted head RMS over 256 dims held 4 per lane, then NeoX-half RoPE:
 // dims p < 128 (lanes 0..31) pair with p + 128 (lanes 32..63).
-DEV void prep_head(float (&x)[4], const float* w, const float* inv_freq, int angles, float eps, float fpos,
-                   bool rotate) {
+DEV void prep_head(float (&x)[4], const float* w, const float* inv_freq, const float2* rope, int angles, float eps,
+                   float fpos, bool rotate) {
   const int lane = threadIdx.x & 63;
   const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
   const float inv = rms_inv(ss, HD, eps);
@@ -60,9 +66,13 @@ DEV void prep_head(float (&x)[4], const float* w, const float* inv_freq, int ang
     const float partner = hi ? a : b;
     const int p = 4 * (lane & 31) + i;
     if (p < angles) {
-      const float th = fpos * inv_freq[p];
       float sn, cs;
-      sincosf(th, &sn, &cs);
+      if (rope) {
+        cs = rope[p].x;
+        sn = rope[p].y;
+      } else {
+        sincosf(fpos * inv_freq[p], &sn, &cs);
+      }
       x[i] = hi ? (partner * sn + x[i] * cs) : (x[i] * cs - partner * sn);
     }
   }
@@ -77,21 +87,20 @@ DEV void unpack16(const uint4& a, const uint4& b, float* f) {
   }
 }
 
-// One block per (KV group g, chunk c of CS positions).  Every K and V row of
-// the chunk is requested before the head prep starts, so the whole chunk is
-// one memory round trip: K as 16 lanes x 32 B per position (4 positions per
-// wave-step), V as 8 B per lane (wave w takes positions w, w+4, ...).
+// One block of 8 waves per (KV group g, chunk c of CS positions).
+// K is read as 16 lanes x 32 B per position (4 positions per wave, 32 per
+// block step); V as 8 B per lane (wave w takes positions w, w+8, ...).
 template <int CS>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
-  constexpr int KS = CS / 16;  // score steps
-  constexpr int VS = CS / 4;   // P.V positions per wave
+__global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
+  constexpr int NW = 8;
+  constexpr int KS = CS / 32;  // score steps
+  constexpr int VS = CS / 8;   // P.V positions per wave
   __shared__ float qs[GQA][HD];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ float sc[GQA][CS];
-  __shared__ float po[4][GQA][HD];
+  __shared__ float po[NW][GQA][HD];
   __shared__ float mlx[GQA][2];
-  __shared__ int is_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = blockIdx.x, c = blockIdx.y;
   // 32-bit position arithmetic throughout (positions < 2^31): a 64-bit
@@ -121,43 +130,40 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   uint2 vr[VS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    const int j = min(16 * s + 4 * wave + sub, m - 1);
+    const int j = min(32 * s + 4 * wave + sub, m - 1);
     const uint4* p = reinterpret_cast<const uint4*>(kc + slot_at(j) * HD + 16 * dl);
     kr[s][0] = p[0];
     kr[s][1] = p[1];
   }
 #pragma unroll
   for (int i = 0; i < VS; ++i) {
-    const int j = min(4 * i + wave, m - 1);
+    const int j = min(NW * i + wave, m - 1);
     vr[i] = *reinterpret_cast<const uint2*>(vc + slot_at(j) * HD + 4 * lane);
   }
 
-  // 1. head prep: wave j preps q head 4g+j; waves 0/1 also prep the group's
-  //    new k/v (f16-rounded, as stored); the chunk owning `pos` writes them
-  {
-    float x[4];
-    const float* src = A.qkv + (int64_t)(g * GQA + wave) * HD + 4 * lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = src[i];
-    prep_head(x, A.qw, A.inv_freq, A.angles, A.eps, fpos, true);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = x[i];
-  }
+  // 1. head prep: waves 0-3 prep q heads 4g..4g+3, wave 4 the new k, wave 5
+  //    the new v (f16-rounded, as stored); the chunk owning `pos` stores them
   const bool owner = pos < c_lo + m;  // the last live chunk holds pos, at j = m - 1
-  if (wave < 2) {
+  if (wave < 6) {
+    const int row = wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g;
+    const float* src = A.qkv + (int64_t)row * HD + 4 * lane;
     float x[4];
-    const float* src = A.qkv + (int64_t)(A.qh + (wave == 0 ? 0 : A.kvh) + g) * HD + 4 * lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = src[i];
-    prep_head(x, wave == 0 ? A.kw : nullptr, A.inv_freq, A.angles, A.eps, fpos, wave == 0);
-    const uint2 pk = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
-                                (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
-    *reinterpret_cast<uint2*>((wave == 0 ? knew : vnew) + 4 * lane) = pk;
-    if (owner) *reinterpret_cast<uint2*>((wave == 0 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
+    prep_head(x, wave < 4 ? A.qw : wave == 4 ? A.kw : nullptr, A.inv_freq, A.rope, A.angles, A.eps, fpos, wave < 5);
+    if (wave < 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = x[i];
+    } else {
+      const uint2 pk = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
+                                  (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
+      *reinterpret_cast<uint2*>((wave == 4 ? knew : vnew) + 4 * lane) = pk;
+      if (owner) *reinterpret_cast<uint2*>((wave == 4 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
+    }
   }
   __syncthreads();
 
-  // 2. scores: 16 lanes per position (16 dims each), 4 positions per wave-step
+  // 2. scores: 16 lanes per position (16 dims each)
   {
     float q[GQA][16];
 #pragma unroll
@@ -166,7 +172,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
       for (int i = 0; i < 16; ++i) q[h][i] = qs[h][16 * dl + i];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const int j = 16 * s + 4 * wave + sub;
+      const int j = 32 * s + 4 * wave + sub;
       uint4 ka = kr[s][0], kb = kr[s][1];
       if (c_lo + j == pos) {
         const uint4* kn = reinterpret_cast<const uint4*>(knew + 16 * dl);
@@ -189,8 +195,8 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   }
   __syncthreads();
 
-  // 3. chunk softmax statistics: wave h owns head h, lane j position j
-  {
+  // 3. chunk softmax statistics: wave h < 4 owns head h, lane j position j
+  if (wave < GQA) {
     float mx = -3.0e38f;
     for (int j = lane; j < m; j += 64) mx = fmaxf(mx, sc[wave][j]);
     mx = wave_max(mx);
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   }
   __syncthreads();
 
-  // 4. P.V: wave w takes positions j = w, w+4, ...; lane covers dims 4l..4l+3
+  // 4. P.V: wave w takes positions j = w, w+8, ...; lane covers dims 4l..4l+3
   {
     float acc[GQA][4];
 #pragma unroll
@@ -218,7 +224,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
     const uint2 vn = *reinterpret_cast<const uint2*>(vnew + 4 * lane);
 #pragma unroll
     for (int i = 0; i < VS; ++i) {
-      const int j = 4 * i + wave;
+      const int j = NW * i + wave;
       if (j < m) {
         const uint2 vv = (c_lo + j == pos) ? vn : vr[i];
         const float vf[4] = {h2f((uint16_t)(vv.x & 0xffff)), h2f((uint16_t)(vv.x >> 16)),
@@ -240,48 +246,51 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
 
   // 5. this chunk's partials ([head][chunk][dim], [head][chunk][max, sum])
   const int gch = gridDim.y;  // partial stride: chunks allocated per head
-  for (int i = threadIdx.x; i < GQA * HD; i += 256) {
+  for (int i = threadIdx.x; i < GQA * HD; i += NW * 64) {
     const int h = i / HD, d = i % HD;
-    A.part_o[((int64_t)(g * GQA + h) * gch + c) * HD + d] = (po[0][h][d] + po[1][h][d]) + (po[2][h][d] + po[3][h][d]);
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += po[w][h][d];
+    A.part_o[((int64_t)(g * GQA + h) * gch + c) * HD + d] = v;
   }
   if (threadIdx.x < GQA) {
     const int64_t pi = ((int64_t)(g * GQA + threadIdx.x) * gch + c) * 2;
     A.part_ml[pi] = mlx[threadIdx.x][0];
     A.part_ml[pi + 1] = mlx[threadIdx.x][1];
   }
+}
 
-  // 6. the last live chunk of this KV group to finish combines its four heads
-  //    (log-sum-exp merge, kernels/attcomb.wgsl:10-36)
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&A.counter[g], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (uint32_t)nch - 1);
+// log-sum-exp merge of the live chunks (kernels/attcomb.wgsl:10-36): one block
+// per q head, thread d = output dim d.
+template <int CS>
+__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
+                                                      const float* __restrict__ part_ml, const uint32_t* params,
+                                                      uint32_t pos_imm, int window, int gch,
+                                                      uint16_t* __restrict__ out) {
+  __shared__ float wt[kAttnMaxChunks];
+  __shared__ float red[4];
+  const int h = blockIdx.x, d = threadIdx.x;
+  const int pos = (int)(params ? params[0] : pos_imm);
+  const int lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+  const int nch = (pos + 1 - lo + CS - 1) / CS;
+  const float* ml = part_ml + (int64_t)h * gch * 2;
+  // chunk weights exp(m_c - M) and the denominator sum_c l_c exp(m_c - M)
+  float M = -3.0e38f;
+  for (int cc = threadIdx.x; cc < nch; cc += 256) M = fmaxf(M, ml[2 * cc]);
+  M = block_max(M, red);
+  float den = 0.f;
+  for (int cc = threadIdx.x; cc < nch; cc += 256) {
+    const float f = __expf(ml[2 * cc] - M);
+    wt[cc] = f;
+    den = fmaf(ml[2 * cc + 1], f, den);
   }
+  den = block_sum(den, red);
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();  // acquire: every chunk's partials are visible (plain loads below)
-  __shared__ float mls[GQA][2 * kAttnMaxChunks];
-#pragma unroll
-  for (int h = 0; h < GQA; ++h)
-    for (int r = threadIdx.x; r < 2 * nch; r += 256) mls[h][r] = A.part_ml[((int64_t)(g * GQA + h) * gch) * 2 + r];
-  __syncthreads();
-  const int d = threadIdx.x;
-#pragma unroll
-  for (int hh = 0; hh < GQA; ++hh) {
-    float M = -3.0e38f;
-    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, mls[hh][2 * cc]);
-    const float* po_h = A.part_o + (int64_t)(g * GQA + hh) * gch * HD + d;
-    float den = 0.f, acc = 0.f;
+  const float* po = part_o + (int64_t)h * gch * HD + d;
+  float acc = 0.f;
 #pragma unroll 8
-    for (int cc = 0; cc < nch; ++cc) {
-      const float f = __expf(mls[hh][2 * cc] - M);
-      den = fmaf(mls[hh][2 * cc + 1], f, den);
-      acc = fmaf(po_h[(int64_t)cc * HD], f, acc);
-    }
-    A.out[(g * GQA + hh) * HD + d] = f2h(acc / den);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(&A.counter[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int cc = 0; cc < nch; ++cc) acc = fmaf(po[(int64_t)cc * HD], wt[cc], acc);
+  out[h * HD + d] = f2h(acc / den);
 }
 
 }  // namespace
@@ -299,19 +308,18 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   if (nch > kAttnMaxChunks)
     return e4b_fail(E4B_EINVAL, "attention: %d positions need %d chunks of %d (max %d)", span, nch, a.chunk,
                     kAttnMaxChunks);
-  if (!a.counter) return e4b_fail(E4B_EINVAL, "attention: null counter");
   AttnArgs A;
   A.qkv = a.qkv;
   A.qw = a.qw;
   A.kw = a.kw;
   A.inv_freq = a.inv_freq;
+  A.rope = a.rope;
   A.kc = a.kc;
   A.vc = a.vc;
   A.params = a.params;
   A.pos = a.pos;
   A.part_o = a.part_o;
   A.part_ml = a.part_ml;
-  A.counter = a.counter;
   A.out = a.out;
   A.qh = a.qh;
   A.kvh = a.kvh;
@@ -319,10 +327,15 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.slots = a.slots;
   A.window = a.window;
   A.eps = a.eps;
-  if (a.chunk == 64)
-    hipLaunchKernelGGL(k_attn<64>, dim3(a.kvh, nch), dim3(256), 0, st, A);
-  else
-    hipLaunchKernelGGL(k_attn<32>, dim3(a.kvh, nch), dim3(256), 0, st, A);
+  if (a.chunk == 64) {
+    hipLaunchKernelGGL(k_attn_split<64>, dim3(a.kvh, nch), dim3(512), 0, st, A);
+    hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+                       a.window, nch, a.out);
+  } else {
+    hipLaunchKernelGGL(k_attn_split<32>, dim3(a.kvh, nch), dim3(512), 0, st, A);
+    hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+                       a.window, nch, a.out);
+  }
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

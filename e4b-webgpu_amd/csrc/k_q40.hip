@@ -31,6 +31,7 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
   L.units = (epi == EPI_GEGLU) ? 2 * o.ff : W.rows;
   L.ks = ks;
   L.nbk = nbk;
+  L.max_wgs = 2048;
   L.pa = pro ? *pro : ProArgs{};
   L.st = st;
   const q40k::Cfg c = q40k::pick(nbk, L.units, epi, pro != nullptr);

@@ -58,12 +58,23 @@ __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float
 // token embedding: h = E[token] * sqrt(H) from the packed Q6_K lm-head planes
 // (kernels/q6k.wgsl:37-73 with the TOKSRC feedback folded in), plus the exact
 // hi/lo split of h for the PLE model projection.  The token is prompt[pos]
-// while pos < params[3], else params[1] (GPU-fed greedy decode).
+// while pos < params[3], else params[1] (GPU-fed greedy decode).  Block 0 also
+// evaluates the step's RoPE table (cos, sin)(pos * inv_freq[p]) for local and
+// global layers, the same expression the attention kernel would evaluate.
 __global__ __launch_bounds__(256) void k_embed(Q6Mat E, const uint32_t* __restrict__ params,
                                                const uint32_t* __restrict__ prompt, float mult,
                                                float* __restrict__ h, uint16_t* __restrict__ h_hl,
-                                               uint32_t* __restrict__ status) {
+                                               uint32_t* __restrict__ status, const float* __restrict__ inv_local,
+                                               const float* __restrict__ inv_global, int half,
+                                               float2* __restrict__ rope) {
   const uint32_t pos = params[0];
+  if (blockIdx.x == 0)
+    for (int t = threadIdx.x; t < 2 * half; t += 256) {
+      const float f = t < half ? inv_local[t] : inv_global[t - half];
+      float sn, cs;
+      sincosf((float)pos * f, &sn, &cs);
+      rope[t] = make_float2(cs, sn);
+    }
   uint32_t tok = pos < params[3] ? prompt[pos] : params[1];
   if (tok >= (uint32_t)E.rows) {
     if (threadIdx.x == 0 && blockIdx.x == 0) status[0] = 1u;  // reported by the host as E4B_ERANGE
@@ -207,8 +218,10 @@ int launch_tail(float* h, const float* p, const float* w_post, float scale, cons
   return E4B_OK;
 }
 int launch_embed(const Q6Mat& E, const uint32_t* params, const uint32_t* prompt, float mult, float* h, uint16_t* h_hl,
-                 uint32_t* status, hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3((E.nseg + 255) / 256), dim3(256), 0, st, E, params, prompt, mult, h, h_hl, status);
+                 uint32_t* status, const float* inv_local, const float* inv_global, int half, float2* rope,
+                 hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3((E.nseg + 255) / 256), dim3(256), 0, st, E, params, prompt, mult, h, h_hl, status,
+                     inv_local, inv_global, half, rope);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

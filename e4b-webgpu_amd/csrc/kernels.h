@@ -43,15 +43,11 @@ static inline Q6Mat q6_view(const void* packed, int64_t rows, int64_t cols) {
   return m;
 }
 
-// Per-device library workspace (argmax partials, counters, x staging).  The
-// counters are zeroed once at allocation and every kernel that uses one
-// returns it to zero, so launches can be captured into a hipGraph.
+// Per-device library workspace (argmax and attention partials, x staging).
 struct Workspace {
   uint8_t* buf;          // general scratch
   size_t cap;
-  uint32_t* counters;    // E4B_NCOUNTERS zero-initialised u32
 };
-#define E4B_NCOUNTERS 4096
 int e4b_workspace(size_t bytes, Workspace* ws);
 
 // q4_0 GEMV epilogues

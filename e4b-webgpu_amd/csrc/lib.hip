@@ -89,13 +89,12 @@ extern "C" int e4b_event_destroy(void* ev) {
 }
 
 // ---- per-device workspace ---------------------------------------------------
-// One grow-only scratch buffer per device plus a zeroed counter array.  Calls
-// that use it on one device must not overlap (one stream at a time).
+// One grow-only scratch buffer per device.  Calls that use it on one device
+// must not overlap (one stream at a time).
 namespace {
 struct DevWs {
   uint8_t* buf = nullptr;
   size_t cap = 0;
-  uint32_t* counters = nullptr;
 };
 std::mutex g_ws_mu;
 DevWs g_ws[64];
@@ -107,10 +106,6 @@ int e4b_workspace(size_t bytes, Workspace* out) {
   if (dev < 0 || dev >= 64) return e4b_fail(E4B_EINVAL, "device %d out of range", dev);
   std::lock_guard<std::mutex> lk(g_ws_mu);
   DevWs& w = g_ws[dev];
-  if (!w.counters) {
-    E4B_HIP(hipMalloc(&w.counters, E4B_NCOUNTERS * sizeof(uint32_t)));
-    E4B_HIP(hipMemset(w.counters, 0, E4B_NCOUNTERS * sizeof(uint32_t)));
-  }
   if (bytes > w.cap) {
     if (w.buf) {
       E4B_HIP(hipDeviceSynchronize());
@@ -124,7 +119,6 @@ int e4b_workspace(size_t bytes, Workspace* out) {
   }
   out->buf = w.buf;
   out->cap = w.cap;
-  out->counters = w.counters;
   return E4B_OK;
 }
 
@@ -164,6 +158,31 @@ extern "C" int e4b_k_q40_gemv_geglu(const void* w_packed, int64_t ff, int64_t co
   GemvOut o = {nullptr, (uint16_t*)out, nullptr, ff};
   return launch_q40(q40_view(w_packed, 2 * ff, cols), (const uint32_t*)x, nullptr, EPI_GEGLU, o, 1,
                     (hipStream_t)stream);
+}
+
+extern "C" int e4b_k_q40_geglu_prenorm(const void* w_packed, int64_t ff, int64_t cols, const float* h_in,
+                                       const float* resid, const float* w_resid, const float* w_in, float scale,
+                                       float eps, float* h_out, void* out_f16, void* stream) {
+  if (!w_packed || !h_in || !w_in || !out_f16 || (resid && !w_resid) || ff <= 0 || !q40_prologue_supported((int)cols))
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_geglu_prenorm: bad arguments (ff=%lld cols=%lld; cols 256/512/1024/2048)",
+                    (long long)ff, (long long)cols);
+  if (!aligned16(w_packed)) return e4b_fail(E4B_EINVAL, "e4b_k_q40_geglu_prenorm: weight must be 16-byte aligned");
+  GemvOut o = {nullptr, (uint16_t*)out_f16, nullptr, ff};
+  ProArgs p;
+  p.hin = h_in;
+  p.hout = h_out;
+  p.a = resid;
+  p.w1 = w_resid;
+  p.w2 = w_in;
+  p.scale = scale;
+  p.H = (int)cols;
+  p.eps = eps;
+  return launch_q40(q40_view(w_packed, 2 * ff, cols), nullptr, nullptr, EPI_GEGLU, o, 1, (hipStream_t)stream, &p);
+}
+
+extern "C" int e4b_memcpy_d2d(void* dst, const void* src, size_t n, void* stream) {
+  E4B_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return E4B_OK;
 }
 
 extern "C" int e4b_split_f32(const float* x, int64_t n, void* hl, void* stream) {
@@ -224,7 +243,6 @@ extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const fl
     return e4b_fail(E4B_EINVAL, "e4b_k_attn_decode: bad arguments");
   if (window == 0 && pos >= (uint32_t)slots)
     return e4b_fail(E4B_ERANGE, "e4b_k_attn_decode: position %u beyond the %d-position global cache", pos, slots);
-  if (kv_heads > E4B_NCOUNTERS) return e4b_fail(E4B_EINVAL, "e4b_k_attn_decode: %d kv heads", kv_heads);
   if (chunk == 0) chunk = 64;
   const int span = window > 0 ? window : slots;
   const int nch = attn_chunks(span, chunk > 0 ? chunk : 64);
@@ -238,13 +256,13 @@ extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const fl
   a.qw = q_norm;
   a.kw = k_norm;
   a.inv_freq = inv_freq;
+  a.rope = nullptr;
   a.kc = (uint16_t*)k_cache;
   a.vc = (uint16_t*)v_cache;
   a.params = nullptr;
   a.pos = pos;
   a.part_o = (float*)ws.buf;
   a.part_ml = (float*)(ws.buf + ob);
-  a.counter = ws.counters;
   a.out = (uint16_t*)out_f16;
   a.qh = q_heads;
   a.kvh = kv_heads;

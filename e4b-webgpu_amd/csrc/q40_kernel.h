@@ -107,12 +107,14 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
   ProRegs<PROK> pr;
   if constexpr (PROK > 0) pro_issue<PROK>(pa, pr);
 
-  uint4 wq[R][BPL];
-  uint16_t ws[R][BPL];
-  // loads always issue (row and block clamped into range); slots past the
-  // end are computed on duplicate data and never stored, and blocks past the
-  // range end meet zeroed activations
-  auto load_tile = [&](int64_t tile) {
+  // two register buffers of weight tiles: the loads of tile t + 2*tstep are
+  // issued as soon as tile t is consumed, so a wave always has one tile in
+  // flight while it computes the other.  Loads always issue (row and block
+  // clamped into range); slots past the end are computed on duplicate data
+  // and never stored, and blocks past the range end meet zeroed activations.
+  uint4 wq0[R][BPL], wq1[R][BPL];
+  uint16_t ws0[R][BPL], ws1[R][BPL];
+  auto load_tile = [&](int64_t tile, uint4 (&wq)[R][BPL], uint16_t (&ws)[R][BPL]) {
     const int64_t slot0 = tile * SLOTS + (int64_t)g * R;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -136,7 +138,8 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
 
   const int64_t tile0 = (KW == 1) ? (int64_t)blockIdx.x * 4 + wave : (int64_t)blockIdx.x;
   const int64_t tstep = (int64_t)gridDim.x * WPT;
-  if (tile0 < ntiles) load_tile(tile0);
+  if (tile0 < ntiles) load_tile(tile0, wq0, ws0);
+  if (tile0 + tstep < ntiles) load_tile(tile0 + tstep, wq1, ws1);
 
   uint32_t xp[BPL][16];
   uint32_t xq[BPL][XLO ? 16 : 1];
@@ -175,8 +178,8 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
     }
   }
 
-  for (int64_t tile = tile0; tile < ntiles; tile += tstep) {
-    if (tile != tile0) load_tile(tile);
+  // dot products, reduction and epilogue of one tile
+  auto finish_tile = [&](int64_t tile, const uint4 (&wq)[R][BPL], const uint16_t (&ws)[R][BPL]) {
     const int64_t slot0 = tile * SLOTS + (int64_t)g * R;
     float acc[R];
 #pragma unroll
@@ -184,9 +187,10 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
       acc[r] = 0.f;
 #pragma unroll
       for (int k = 0; k < BPL; ++k) {
-        float a = q40_dot(wq[r][k], xp[k], 0.f);
-        if constexpr (XLO) a = q40_dot(wq[r][k], xq[k], a);
-        acc[r] = fmaf(h2f(ws[r][k]), fmaf(a, kTwo24, xs8[k]), acc[r]);
+        float a0 = 0.f, a1 = 0.f;
+        q40_dot2(wq[r][k], xp[k], a0, a1);
+        if constexpr (XLO) q40_dot2(wq[r][k], xq[k], a0, a1);
+        acc[r] = fmaf(h2f(ws[r][k]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[k])), acc[r]);
       }
     }
     float v = reduce_rows<LPR, R>(acc);
@@ -200,7 +204,7 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
         v = (part[sl] + part[SLOTS + sl]) + (part[2 * SLOTS + sl] + part[3 * SLOTS + sl]);
       }
       __syncthreads();
-      if (wave != 0) continue;
+      if (wave != 0) return;
     }
     if constexpr (EPI == EPI_GEGLU) {
       const float up = __shfl_xor(v, SPAN, 64);
@@ -212,6 +216,17 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
         if constexpr (EPI == EPI_F32) o.y[(int64_t)kslice * W.rows + row] = v;
         if constexpr (EPI == EPI_GELU_MUL) o.yh[row] = f2h(gelu_tanh(v) * o.mul[row]);
       }
+    }
+  };
+
+  // the loop body handles two tiles so that each register buffer keeps a
+  // compile-time name (a runtime buffer index would spill to scratch)
+  for (int64_t tile = tile0; tile < ntiles; tile += 2 * tstep) {
+    finish_tile(tile, wq0, ws0);
+    if (tile + 2 * tstep < ntiles) load_tile(tile + 2 * tstep, wq0, ws0);
+    if (tile + tstep < ntiles) {
+      finish_tile(tile + tstep, wq1, ws1);
+      if (tile + 3 * tstep < ntiles) load_tile(tile + 3 * tstep, wq1, ws1);
     }
   }
 }
@@ -244,19 +259,22 @@ inline void pick_lanes(int nbw, int* lpr_out, int* bpl_out, bool lpr64_only) {
   *bpl_out = bpl_best;
 }
 
-// rows per lane group give ~8 weight loads in flight per lane while keeping
-// >= 512 workgroups when the matrix allows; rows of >= 8192 columns split
+// rows per lane group give ~8-16 weight loads in flight per lane while
+// keeping enough workgroups to cover the chip; rows of >= 8192 columns split
 // their columns over the four waves of a workgroup (KW = 4)
 inline Cfg pick(int nbk, int64_t units, int epi, bool pro) {
   Cfg c;
   c.kw = (!pro && nbk >= 256 && nbk % 4 == 0) ? 4 : 1;
   pick_lanes(nbk / c.kw, &c.lpr, &c.bpl, c.kw == 4);
   const int G = 64 / c.lpr;
-  int r = c.bpl == 1 ? 8 : c.bpl == 2 ? 4 : c.bpl <= 4 ? 2 : 1;
+  int r = c.bpl == 1 ? 8 : c.bpl == 2 ? (c.kw == 4 ? 8 : 4) : c.bpl <= 4 ? 2 : 1;
   if (r > c.lpr) r = c.lpr;
   const int rmin = (epi == EPI_GEGLU) ? 2 : 1;
   const int per_wg = (c.kw == 1 ? 4 : 1) * G;
-  while (r > rmin && (units + per_wg * r - 1) / (per_wg * r) < 512) r >>= 1;
+  // measured on MI355X at the E4B shapes: 256 workgroups (128 with the fused
+  // prologue, which every workgroup repeats) keep enough loads in flight
+  const int64_t min_wgs = pro ? 128 : 256;
+  while (r > rmin && (units + per_wg * r - 1) / (per_wg * r) < min_wgs) r >>= 1;
   if (r < rmin) r = rmin;
   c.r = r;
   return c;
@@ -270,6 +288,7 @@ struct Launch {
   GemvOut o;
   int64_t units;
   int ks, nbk;
+  int max_wgs;  // grid cap; waves stride over the remaining tiles
   ProArgs pa;
   hipStream_t st;
 };
@@ -279,7 +298,7 @@ void launch(const Launch& L) {
   constexpr int G = 64 / LPR;
   const int64_t ntiles = (L.units + G * R - 1) / (G * R);
   int64_t wgs = KW == 1 ? (ntiles + 3) / 4 : ntiles;
-  if (wgs > 2048) wgs = 2048;
+  if (wgs > L.max_wgs) wgs = L.max_wgs;
   hipLaunchKernelGGL((k_q40<LPR, BPL, R, KW, XLO, EPI, PROK>), dim3((unsigned)wgs, (unsigned)L.ks), dim3(256), 0,
                      L.st, L.W, L.xh, L.xl, L.o, ntiles, L.nbk, L.pa);
 }

@@ -9,13 +9,13 @@ struct AttnLaunch {
   const float* qw;         // q head-norm weight [hd]
   const float* kw;         // k head-norm weight [hd]
   const float* inv_freq;   // RoPE inverse frequencies [angles]
+  const float2* rope;      // (cos, sin) of pos * inv_freq[p] for this step, or null
   uint16_t* kc;            // [kvh][slots][hd] f16 key cache
   uint16_t* vc;            // [kvh][slots][hd] f16 value cache
   const uint32_t* params;  // params[0] = position of the current token (device), or
   uint32_t pos;            //   this position when params is null
   float* part_o;           // [qh][attn_chunks(span, chunk)][hd] split-K partial outputs
   float* part_ml;          // [qh][attn_chunks(span, chunk)][2]  (chunk max, chunk sum)
-  uint32_t* counter;       // [kvh] zero-initialised arrival counters
   uint16_t* out;           // [qh][hd] f16 attention output
   int qh, kvh, hd, angles;
   int slots;               // ring slots (sliding) or capacity (global)
@@ -30,8 +30,11 @@ constexpr int kAttnMaxChunks = 512;
 int attn_chunks(int max_positions, int chunk);
 int launch_tail(float* h, const float* p, const float* w_post, float scale, const float* w_out,
                 uint16_t* xo_hl, int H, float eps, hipStream_t st);
+// also fills rope[2 * half] = (cos, sin)(pos * inv_{local,global}[p]) for the
+// attention kernels of this step
 int launch_embed(const Q6Mat& E, const uint32_t* params, const uint32_t* prompt, float mult, float* h, uint16_t* h_hl,
-                 uint32_t* status, hipStream_t st);
+                 uint32_t* status, const float* inv_local, const float* inv_global, int half, float2* rope,
+                 hipStream_t st);
 int launch_ple_prep(const float* proj, const uint8_t* table, const float* w_pn, const uint32_t* params,
                     const uint32_t* prompt, int L, int vocab, float proj_scale, float* ple, const float* h,
                     const float* w_attn0, uint16_t* xn, int H, float eps, hipStream_t st);

@@ -60,6 +60,7 @@ SIGNATURES = [
     ("e4b_memcpy_h2d", _i32, [_vp, _vp, _sz]),
     ("e4b_memcpy_d2h", _i32, [_vp, _vp, _sz]),
     ("e4b_memset_dev", _i32, [_vp, _i32, _sz]),
+    ("e4b_memcpy_d2d", _i32, [_vp, _vp, _sz, _vp]),
     ("e4b_sync", _i32, []),
     ("e4b_stream_sync", _i32, [_vp]),
     ("e4b_event_create", _vp, []),
@@ -78,6 +79,7 @@ SIGNATURES = [
     ("e4b_q6k_pack", _i32, [_vp, _i64, _i64, _vp]),
     ("e4b_k_q40_gemv", _i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
     ("e4b_k_q40_gemv_geglu", _i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    ("e4b_k_q40_geglu_prenorm", _i32, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _f32, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_gemv_argmax", _i32, [_vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_row", _i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),
     ("e4b_k_argmax", _i32, [_vp, _i64, _vp, _vp]),

@@ -36,6 +36,22 @@ class Q40Matrix:
         check(lib.e4b_k_q40_gemv_geglu(_vp(self.buf), self.rows // 2, self.cols, _vp(x), _vp(out), _vp(stream)),
               "e4b_k_q40_gemv_geglu")
 
+    def geglu_prenorm_dev(self, h_in: DeviceBuffer, resid, w_resid, w_in: DeviceBuffer, scale: float, eps: float,
+                          h_out, out: DeviceBuffer, stream=None) -> None:
+        """h = (h_in + rms(resid) * w_resid) * scale; x = f16(rms(h) * w_in); out = GeGLU(x)"""
+        check(lib.e4b_k_q40_geglu_prenorm(_vp(self.buf), self.rows // 2, self.cols, _vp(h_in), _vp(resid),
+                                          _vp(w_resid), _vp(w_in), C.c_float(scale), C.c_float(eps), _vp(h_out),
+                                          _vp(out), _vp(stream)), "e4b_k_q40_geglu_prenorm")
+
+    def geglu_prenorm(self, h_in, resid, w_resid, w_in, scale: float = 1.0, eps: float = 1e-6):
+        """Host convenience: returns (h f32[cols], out f16[ff])."""
+        dev = lambda a: None if a is None else DeviceBuffer.from_array(np.asarray(a, np.float32))  # noqa: E731
+        hi, rd, wr, wi = dev(h_in), dev(resid), dev(w_resid), dev(w_in)
+        ho = DeviceBuffer(self.cols * 4)
+        out = DeviceBuffer(self.rows // 2 * 2)
+        self.geglu_prenorm_dev(hi, rd, wr, wi, scale, eps, ho, out)
+        return ho.download(np.float32, self.cols), out.download(np.float16, self.rows // 2)
+
     def geglu(self, x: np.ndarray) -> np.ndarray:
         xd = DeviceBuffer.from_array(x.astype(np.float16))
         out = DeviceBuffer(self.rows // 2 * 2)

@@ -57,6 +57,7 @@ int   e4b_dev_free(void* p);
 int   e4b_memcpy_h2d(void* dst_dev, const void* src_host, size_t bytes);
 int   e4b_memcpy_d2h(void* dst_host, const void* src_dev, size_t bytes);
 int   e4b_memset_dev(void* dst_dev, int value, size_t bytes);
+int   e4b_memcpy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
 int   e4b_sync(void);                                        /* device-wide */
 int   e4b_stream_sync(void* stream);
 
@@ -109,6 +110,17 @@ int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, const void*
  * out f16[ff] = f16(gelu_tanh(gate) * up), tanh argument clamped to +-20. */
 int e4b_k_q40_gemv_geglu(const void* w_packed, int64_t ff, int64_t cols, const void* x_f16,
                          void* out_f16, void* stream);
+
+/* The FFN input GEMV as the decode step runs it: a fused residual + RMSNorm
+ * prologue, then gate/up + GeGLU (kernels/rmsacc3.wgsl:36-53 folded into
+ * kernels/q40gu.wgsl:62-119):
+ *   h = (h_in + rms(resid) * w_resid) * scale      (resid may be NULL: h = h_in * scale)
+ *   x = f16(rms(h) * w_in);  out f16[ff] = f16(gelu_tanh(W_gate x) * (W_up x))
+ * h_out (may be NULL) receives h.  cols (the hidden size) must be 256, 512,
+ * 1024 or 2048; rms(v) = v * (mean(v^2) + eps)^-1/2. */
+int e4b_k_q40_geglu_prenorm(const void* w_packed, int64_t ff, int64_t cols, const float* h_in,
+                            const float* resid, const float* w_resid, const float* w_in, float scale,
+                            float eps, float* h_out, void* out_f16, void* stream);
 
 /* Q6_K GEMV + softcap + argmax (kernels/q6k.wgsl:75-130 MODE 1, then
  * kernels/argmax2.wgsl:8-48).  logits f32[rows] (may be NULL), amax u32[2] =

@@ -126,3 +126,61 @@ def test_argmax_ties_nan_and_empty_like():
     assert argmax(x) == (0, float(np.float32(-3.0e38)))
     x = formats.synth_normal(10, 1000)
     assert argmax(x)[0] == orc.argmax(x)[0]
+
+
+# --------------------------------------------------------------------------
+# gate/up + GeGLU (kernels/q40gu.wgsl), plain and with the fused residual +
+# RMSNorm prologue the decode step uses (kernels/rmsacc3.wgsl folded in).
+# Output f16: within GEGLU_TOL of |want| plus 1e-4 of max|want| (one f16
+# rounding of the product, GEMV error ~1e-6).
+# --------------------------------------------------------------------------
+GEGLU_TOL = 1.5e-3
+
+
+def _geglu_want(w, ff, cols, x16):
+    g = orc.q40_gemv(w, 2 * ff, cols, x16.astype(np.float32)).astype(np.float64)
+    gate, up = g[:ff], g[ff:]
+    gl = np.array([orc.gelu_tanh(float(v)) for v in gate])
+    return gl * up
+
+
+def _check_geglu(got, want, name):
+    got = got.astype(np.float64)
+    scale = np.abs(want).max()
+    err = np.abs(got - want) - (GEGLU_TOL * np.abs(want) + 1e-4 * scale)
+    print(f"{name}: max excess {err.max():.3e} (scale {scale:.3f})")
+    assert err.max() <= 0
+
+
+@pytest.mark.parametrize("ff,cols", [(16384, 2048), (704, 2816), (1000, 256)])
+def test_q40_geglu(ff, cols):
+    w = formats.synth_q40(ff + cols, 2 * ff, cols, 0.02)
+    x = formats.synth_normal(7, cols).astype(np.float16)
+    got = Q40Matrix(w, 2 * ff, cols).geglu(x)
+    _check_geglu(got, _geglu_want(w, ff, cols, x), f"geglu {ff}x{cols}")
+
+
+@pytest.mark.parametrize("ff,cols,with_resid", [(16384, 2048, True), (512, 256, True), (512, 1024, False)])
+def test_q40_geglu_prenorm(ff, cols, with_resid):
+    rng = np.random.default_rng(ff + cols)
+    w = formats.synth_q40(3 * ff + cols, 2 * ff, cols, 0.02)
+    h_in = rng.standard_normal(cols).astype(np.float32)
+    resid = (3.0 * rng.standard_normal(cols)).astype(np.float32) if with_resid else None
+    w_resid = (1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    w_in = (1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    scale = 0.75
+    h_got, got = Q40Matrix(w, 2 * ff, cols).geglu_prenorm(h_in, resid, w_resid if with_resid else None, w_in, scale)
+    h_want = h_in.astype(np.float64)
+    if with_resid:
+        h_want = h_want + orc.rmsnorm(resid, w_resid).astype(np.float64)
+    h_want = h_want * scale
+    np.testing.assert_allclose(h_got, h_want, rtol=2e-6, atol=2e-6 * np.abs(h_want).max())
+    x16 = orc.rmsnorm(h_want.astype(np.float32), w_in).astype(np.float16)
+    _check_geglu(got, _geglu_want(w, ff, cols, x16), f"geglu prenorm {ff}x{cols}")
+
+
+def test_q40_geglu_prenorm_rejects_unsupported_hidden():
+    from e4b._lib import E4BError
+    w = formats.synth_q40(1, 2 * 64, 2816, 0.02)
+    with pytest.raises(E4BError):
+        Q40Matrix(w, 128, 2816).geglu_prenorm(np.zeros(2816, np.float32), None, None, np.ones(2816, np.float32))
