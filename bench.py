@@ -1,11 +1,13 @@
 """Benchmark of the batch-1 decode path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c0] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c1|c0] [--no-cpu]
 
 Prints ONE JSON line (rank 0).  Workloads:
   c0  one q4_0 GEMV 16384x2048 (x f32), weights rotated over >512 MB so the
       256 MB MALL cannot serve them; a step = one GEMV.
   c1  Q6_K lm-head 262144x2048 + softcap + argmax; a step = one launch.
+  c3  A4B-style MoE half-layer (hidden 2816, 128 experts top-8); a step =
+      one layer (4 launches), weights rotated over 3 copies.
   c4  the E4B-shaped decode loop; a step = one greedy decode token.
 `roofline` is measured live with HIP events on the launch stream; the CPU
 baseline times the oracle (the C restatement, OpenMP) on a bounded sample.
@@ -130,6 +132,67 @@ def bench_c1(steps: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
+def bench_c3(steps: int, warmup: int, cpu: bool) -> dict:
+    """One A4B-style MoE FFN half-layer (router + top-8, dense and 8 expert
+    GeGLU FFNs, slot-combined down, tail).  Three independent copies of the
+    layer's weights (about 1 GB) are rotated so the 256 MB MALL cannot serve
+    the next launch."""
+    from e4b import formats
+    from e4b.device import Event
+    from e4b.kernels import MoeLayer
+
+    H, E, FF, FF2 = 2816, 128, 704, 2112
+    q = lambda rows, cols, s: formats.synth_q40(s, rows, cols, 0.02)  # noqa: E731
+    ones = np.ones(H, np.float32)
+    layers = []
+    for c in range(3):
+        t = {"ffn_norm": ones, "router_scale": ones, "pre_ffw2": ones, "post_ffw1": ones, "post_ffw2": ones,
+             "post_ffw": ones, "router_w": formats.synth_normal(10 + c, E * H, 0.0, 0.02).reshape(E, H),
+             "pes": np.ones(E, np.float32), "dense_gate": q(FF2, H, 100 * c + 1), "dense_up": q(FF2, H, 100 * c + 2),
+             "dense_down": q(H, FF2, 100 * c + 3), "exp_gate_up": q(E * 2 * FF, H, 100 * c + 4),
+             "exp_down": q(E * H, FF, 100 * c + 5)}
+        L = MoeLayer(H, E, FF, FF2, t)
+        L.h.upload(formats.synth_normal(500 + c, H))
+        layers.append(L)
+        if c == 0:
+            t0 = t
+    blk = lambda rows, cols: rows * cols // 32 * 18  # noqa: E731
+    algo = (E * H * 4 + 8 * (blk(2 * FF, H) + blk(H, FF)) + blk(2 * FF2, H) + blk(H, FF2)
+            + 9 * H * 4 + E * 4)
+    for i in range(warmup):
+        layers[i % 3].forward_dev()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for i in range(steps):
+        layers[i % 3].forward_dev()
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    gbs = algo / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "MoE decode layer GB/s (config c3)", "value": round(gbs, 2), "unit": "GB/s", "ms_per_step": ms,
+        "dtype": "q4_0 x f16 (f32 accumulate), f32 router",
+        "config": {"workload": "c3: A4B-style MoE half-layer, hidden 2816, 128 experts top-8, expert ffn 704, "
+                               "dense ffn 2112", "algorithmic_bytes_per_layer": algo},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_moe_router + k_moe_gu + k_moe_down + k_moe_tail (one layer)",
+                     "algorithmic_bytes_per_launch": algo},
+    }
+    if cpu:
+        import oracle as orc
+        m = dict(t0, hidden=H, n_experts=E, top_k=8, expert_ffn=FF, dense_ffn=FF2)
+        h = formats.synth_normal(500, H)
+        t1 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t1 < 10.0:
+            orc.moe_ffn(m, h)
+            n += 1
+        dt = (time.perf_counter() - t1) / n
+        out["cpu_baseline"] = {"value": round(algo / dt / 1e9, 3), "unit": "GB/s", "cores": _cpu_cores(),
+                               "kind": "port", "sample": f"{n} oracle MoE layers (~10 s)"}
+    return out
+
+
 def _time_geglu(cfg, steps: int) -> dict:
     """Dominant kernel of the c4 step: the FFN input GEMV exactly as the step
     launches it -- fused residual + RMSNorm prologue, gate/up q4_0 GEMV
@@ -234,7 +297,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c4"])
+    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c4"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device-to-device copy (the byte scale for rocprof FETCH/WRITE_SIZE)")
@@ -245,7 +308,7 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
               "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
-    fn = {"c0": bench_c0, "c1": bench_c1, "c4": bench_c4}[a.workload]
+    fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c4": bench_c4}[a.workload]
     steps = a.steps if a.steps is not None else (240 if a.workload == "c4" else 200)
     warmup = a.warmup if a.warmup is not None else (16 if a.workload == "c4" else 20)
     if a.workload == "c4":

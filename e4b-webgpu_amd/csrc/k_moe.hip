@@ -1,0 +1,411 @@
+// k_moe.hip -- the MoE FFN half-layer of the A4B-style decode step
+// (src/engine-a4b.js:438-462): router + top-8, dense and expert gate/up
+// GeGLU, dense down and slot-combined expert down, and the fused tail, in
+// four launches that read only the 8 active experts' weight rows.
+//
+//   k_moe_router  h -> rms -> router scores (one wave per expert), plus the
+//                 f16 inputs of the dense (ffn_norm) and expert (pre_ffw2)
+//                 branches                       (kernels/rmsacc3.wgsl:36-53,
+//                                                 kernels/routertop.wgsl:19-35)
+//   k_moe_gu      top-8 selection, redone by every wave from the 128 scores
+//                 (no cross-block handshake), then gate/up + GeGLU for the
+//                 dense branch and the 8 expert slots
+//                                                (kernels/routertop.wgsl:48-71,
+//                                                 kernels/q40gu.wgsl:62-119)
+//   k_moe_down    dense down rows and, per output row, the 8 expert rows
+//                 weighted by the router weights  (kernels/q40moedown.wgsl:42-75)
+//   k_moe_tail    comb = rms(dense) w1 + rms(moe) w2; h = (h + rms(comb) wp) * s
+//                                                (kernels/a4btail.wgsl:26-71)
+//
+// The selection is made on the f32 scores with a strict '>' scan in index
+// order (ties -> lowest index), the order the reference's softmax scan gives
+// since exp is monotonic; weights are p_k / sum(p) renormalised over the
+// picks and scaled by the per-expert scale, in the reference's f32 order.
+#include "../../include/e4b.h"
+#include "kernels.h"
+#include "moe.h"
+#include "util.h"
+
+namespace {
+
+constexpr float kTwo24 = 16777216.0f;
+constexpr int K = kMoeTopK;
+
+DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
+  const uint4* v = reinterpret_cast<const uint4*>(x) + (size_t)jb * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 t = v[i];
+    xp[4 * i + 0] = t.x;
+    xp[4 * i + 1] = t.y;
+    xp[4 * i + 2] = t.z;
+    xp[4 * i + 3] = t.w;
+  }
+}
+
+// ---- router ---------------------------------------------------------------
+// grid ceil(E/4) x 256: wave w of block b scores expert 4b + w; every block
+// computes the rms of h itself; block 0 also writes the two f16 GEMV inputs.
+__global__ __launch_bounds__(256) void k_moe_router(MoeArgs A) {
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int H = A.H, H4 = H / 4;
+  const float4* h4 = reinterpret_cast<const float4*>(A.h);
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H4; i += 256) {
+    const float4 v = h4[i];
+    ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+  }
+  const float inv = rms_inv(block_sum(ss, red), H, A.eps);
+  const int e = blockIdx.x * 4 + wave;
+  if (e < A.E) {
+    const float4* rs4 = reinterpret_cast<const float4*>(A.router_scale);
+    const float4* w4 = reinterpret_cast<const float4*>(A.router_w + (int64_t)e * H);
+    float acc = 0.f;
+    for (int i = lane; i < H4; i += 64) {
+      const float4 v = h4[i], s = rs4[i], w = w4[i];
+      acc = fmaf(v.x * inv * (s.x * A.router_mult), w.x, acc);
+      acc = fmaf(v.y * inv * (s.y * A.router_mult), w.y, acc);
+      acc = fmaf(v.z * inv * (s.z * A.router_mult), w.z, acc);
+      acc = fmaf(v.w * inv * (s.w * A.router_mult), w.w, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) A.scores[e] = acc;
+  }
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < H; i += 256) {
+      const float v = A.h[i] * inv;
+      A.xd[i] = f2h(v * A.ffn_norm[i]);
+      A.xm[i] = f2h(v * A.pre_ffw2[i]);
+    }
+}
+
+// ---- top-8 in one wave ----------------------------------------------------
+// lane l holds the scores of experts l + 64 j (j < 4, E <= 256); every lane
+// returns the same 8 picks and weights.  Selection on the scores equals the
+// reference's selection on p = exp(s - max) unless some of the top-8 p
+// underflow to 0 (scores more than ~87 below the maximum).
+struct TopK {
+  int idx[K];
+  float w[K];
+};
+
+DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__ pes, int E) {
+  const int lane = threadIdx.x & 63;
+  float s[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    s[j] = e < E ? scores[e] : -3.0e38f;
+  }
+  const float M = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  float psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (lane + 64 * j < E) psum += expf(s[j] - M);
+  const float S = wave_sum(psum);
+  TopK t;
+  float wsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    // lane candidate: strict '>' in index order keeps the lowest index
+    float bv = -3.0e38f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (s[j] > bv) {
+        bv = s[j];
+        bi = lane + 64 * j;
+      }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    t.idx[k] = bi;
+    t.w[k] = expf(bv - M) / S;  // p_k / sum p, as the reference stores it
+    wsum += t.w[k];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + 64 * j == bi) s[j] = -3.4e38f;  // below any live score, above nothing picked
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) t.w[k] = t.w[k] / wsum * pes[t.idx[k]];
+  return t;
+}
+
+__global__ __launch_bounds__(64) void k_moe_topk(MoeArgs A) {
+  const TopK t = select_topk(A.scores, A.pes, A.E);
+  const int lane = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (lane == k) {
+      A.topk_idx[k] = (uint32_t)t.idx[k];
+      A.topk_w[k] = t.w[k];
+    }
+}
+
+// ---- gate/up + GeGLU, dense branch and 8 expert slots ------------------------
+// 32 lanes per unit (a gate row and its up row), 3 blocks per lane (88-block
+// rows of the 2816-wide input), 2 units per wave tile.  Units [0, FF2) are
+// dense, then slot k covers [FF2 + k FF, FF2 + (k+1) FF).
+constexpr int GU_LPR = 32, GU_BPL = 3;
+
+__global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane / GU_LPR, l = lane % GU_LPR;
+  const TopK t = select_topk(A.scores, A.pes, A.E);
+  if (blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (lane == k) {
+        A.topk_idx[k] = (uint32_t)t.idx[k];
+        A.topk_w[k] = t.w[k];
+      }
+  }
+  const int nb = A.H / 32;
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 4) {
+    const int u = (int)(2 * tile) + g;  // this group's unit
+    const bool dense = 2 * tile < A.FF2;  // wave-uniform: FF2 and FF are even
+    int slot = 0, j = u;
+    const Q40Mat& W = dense ? A.dense_gu : A.exp_gu;
+    int64_t row_g, row_u;
+    if (dense) {
+      row_g = u;
+      row_u = A.FF2 + u;
+    } else {
+      slot = (u - A.FF2) / A.FF;
+      j = (u - A.FF2) - slot * A.FF;
+      int e = t.idx[0];
+#pragma unroll
+      for (int k = 1; k < K; ++k)
+        if (slot == k) e = t.idx[k];
+      row_g = (int64_t)e * 2 * A.FF + j;
+      row_u = row_g + A.FF;
+    }
+    uint4 wq[2][GU_BPL];
+    uint16_t ws[2][GU_BPL];
+#pragma unroll
+    for (int b = 0; b < GU_BPL; ++b) {
+      const int jb = min(l + GU_LPR * b, nb - 1);
+      wq[0][b] = ld_nt_u4(W.nib + row_g * nb + jb);
+      ws[0][b] = ld_nt_u16(W.sc + row_g * nb + jb);
+      wq[1][b] = ld_nt_u4(W.nib + row_u * nb + jb);
+      ws[1][b] = ld_nt_u16(W.sc + row_u * nb + jb);
+    }
+    const uint32_t* x = reinterpret_cast<const uint32_t*>(dense ? A.xd : A.xm);
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < GU_BPL; ++b) {
+      const int jb = l + GU_LPR * b;
+      uint32_t xp[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xp[i] = 0u;
+      if (jb < nb) load_x16(x, jb, xp);
+      const float xs8 = -8.f * xsum16(xp);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        float a0 = 0.f, a1 = 0.f;
+        q40_dot2(wq[r][b], xp, a0, a1);
+        acc[r] = fmaf(h2f(ws[r][b]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8)), acc[r]);
+      }
+    }
+    const float v = reduce_rows<GU_LPR, 2>(acc);  // lanes 0..15 gate, 16..31 up
+    const float up = __shfl_xor(v, GU_LPR / 2, 64);
+    if (l == 0) {
+      const uint16_t y = f2h(gelu_tanh(v) * up);
+      if (dense)
+        A.g_dense[u] = y;
+      else
+        A.g_slots[(int64_t)slot * A.FF + j] = y;
+    }
+  }
+}
+
+// ---- down projections -------------------------------------------------------
+// Blocks [0, nbd) run the dense down rows (32 lanes x 3 blocks per row of
+// FF2/32 blocks, 2 rows per group, 4 per wave tile); the rest run the expert
+// rows: for output row o the 8 lane groups are the 8 slots (8 lanes x 3
+// blocks of the FF/32 = 22-block rows), 4 output rows per wave tile, and the
+// slot results are combined with the router weights across the groups.
+constexpr int DD_LPR = 32, DD_BPL = 3, DD_R = 2;
+constexpr int DE_LPR = 8, DE_BPL = 3, DE_R = 4;
+
+__global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if ((int)blockIdx.x < nbd) {
+    const int g = lane / DD_LPR, l = lane % DD_LPR;
+    const int nb = A.FF2 / 32;
+    const Q40Mat& W = A.dense_down;
+    const uint32_t* x = reinterpret_cast<const uint32_t*>(A.g_dense);
+    uint32_t xp[DD_BPL][16];
+    float xs8[DD_BPL];
+#pragma unroll
+    for (int b = 0; b < DD_BPL; ++b) {
+      const int jb = l + DD_LPR * b;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xp[b][i] = 0u;
+      if (jb < nb) load_x16(x, jb, xp[b]);
+      xs8[b] = -8.f * xsum16(xp[b]);
+    }
+    const int64_t ntiles = (A.H + 2 * DD_R - 1) / (2 * DD_R);
+    for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)nbd * 4) {
+      const int64_t r0 = tile * 2 * DD_R + g * DD_R;
+      uint4 wq[DD_R][DD_BPL];
+      uint16_t ws[DD_R][DD_BPL];
+#pragma unroll
+      for (int r = 0; r < DD_R; ++r) {
+        const int64_t row = min(r0 + r, (int64_t)A.H - 1);
+#pragma unroll
+        for (int b = 0; b < DD_BPL; ++b) {
+          const int jb = min(l + DD_LPR * b, nb - 1);
+          wq[r][b] = ld_nt_u4(W.nib + row * nb + jb);
+          ws[r][b] = ld_nt_u16(W.sc + row * nb + jb);
+        }
+      }
+      float acc[DD_R];
+#pragma unroll
+      for (int r = 0; r < DD_R; ++r) {
+        acc[r] = 0.f;
+#pragma unroll
+        for (int b = 0; b < DD_BPL; ++b) {
+          float a0 = 0.f, a1 = 0.f;
+          q40_dot2(wq[r][b], xp[b], a0, a1);
+          acc[r] = fmaf(h2f(ws[r][b]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
+        }
+      }
+      const float v = reduce_rows<DD_LPR, DD_R>(acc);
+      const int64_t row = r0 + l / (DD_LPR / DD_R);
+      if ((l % (DD_LPR / DD_R)) == 0 && row < A.H) A.dense_out[row] = v;
+    }
+    return;
+  }
+  // expert rows
+  const int g = lane / DE_LPR, l = lane % DE_LPR;  // g = slot
+  const int nb = A.FF / 32;
+  const Q40Mat& W = A.exp_down;
+  const int e = (int)A.topk_idx[g];
+  const float wk = A.topk_w[g];
+  const uint32_t* x = reinterpret_cast<const uint32_t*>(A.g_slots + (int64_t)g * A.FF);
+  uint32_t xp[DE_BPL][16];
+  float xs8[DE_BPL];
+#pragma unroll
+  for (int b = 0; b < DE_BPL; ++b) {
+    const int jb = l + DE_LPR * b;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xp[b][i] = 0u;
+    if (jb < nb) load_x16(x, jb, xp[b]);
+    xs8[b] = -8.f * xsum16(xp[b]);
+  }
+  const int nbe = gridDim.x - nbd;
+  const int64_t ntiles = (A.H + DE_R - 1) / DE_R;
+  for (int64_t tile = (int64_t)(blockIdx.x - nbd) * 4 + wave; tile < ntiles; tile += (int64_t)nbe * 4) {
+    const int64_t o0 = tile * DE_R;
+    uint4 wq[DE_R][DE_BPL];
+    uint16_t ws[DE_R][DE_BPL];
+#pragma unroll
+    for (int r = 0; r < DE_R; ++r) {
+      const int64_t row = (int64_t)e * A.H + min(o0 + r, (int64_t)A.H - 1);
+#pragma unroll
+      for (int b = 0; b < DE_BPL; ++b) {
+        const int jb = min(l + DE_LPR * b, nb - 1);
+        wq[r][b] = ld_nt_u4(W.nib + row * nb + jb);
+        ws[r][b] = ld_nt_u16(W.sc + row * nb + jb);
+      }
+    }
+    float acc[DE_R];
+#pragma unroll
+    for (int r = 0; r < DE_R; ++r) {
+      acc[r] = 0.f;
+#pragma unroll
+      for (int b = 0; b < DE_BPL; ++b) {
+        float a0 = 0.f, a1 = 0.f;
+        q40_dot2(wq[r][b], xp[b], a0, a1);
+        acc[r] = fmaf(h2f(ws[r][b]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
+      }
+    }
+    // lane l of slot g holds y_g of row o0 + l / 2; weight it and sum the slots
+    float v = reduce_rows<DE_LPR, DE_R>(acc) * wk;
+    v = xsum_step<8>(v);
+    v = xsum_step<16>(v);
+    v = xsum_step<32>(v);
+    const int64_t row = o0 + l / (DE_LPR / DE_R);
+    if (g == 0 && (l % (DE_LPR / DE_R)) == 0 && row < A.H) A.moe_out[row] = v;
+  }
+}
+
+// ---- tail ----------------------------------------------------------------------
+constexpr int kTailPer = 16;  // elements per thread, H <= 4096
+
+__global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
+  __shared__ float red[4];
+  const int H = A.H;
+  float d[kTailPer], m[kTailPer];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kTailPer; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    d[k] = i < H ? A.dense_out[i] : 0.f;
+    m[k] = i < H ? A.moe_out[i] : 0.f;
+    s1 = fmaf(d[k], d[k], s1);
+    s2 = fmaf(m[k], m[k], s2);
+  }
+  const float i1 = rms_inv(block_sum(s1, red), H, A.eps);
+  const float i2 = rms_inv(block_sum(s2, red), H, A.eps);
+  float s3 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kTailPer; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    d[k] = i < H ? d[k] * i1 * A.post_ffw1[i] + m[k] * i2 * A.post_ffw2[i] : 0.f;  // comb
+    s3 = fmaf(d[k], d[k], s3);
+  }
+  const float i3 = rms_inv(block_sum(s3, red), H, A.eps);
+#pragma unroll
+  for (int k = 0; k < kTailPer; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < H) A.h_out[i] = (A.h[i] + d[k] * i3 * A.post_ffw[i]) * A.layer_scale;
+  }
+}
+
+}  // namespace
+
+int launch_moe_router(const MoeArgs& A, hipStream_t st) {
+  hipLaunchKernelGGL(k_moe_router, dim3((A.E + 3) / 4), dim3(256), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
+  if (A.H % 256 || A.H > 4096 || A.H / 32 > GU_LPR * GU_BPL || A.FF % 32 || A.FF2 % 32 || A.FF % 2 ||
+      A.FF2 / 32 > DD_LPR * DD_BPL || A.FF / 32 > DE_LPR * DE_BPL || A.E < K || A.E > 256)
+    return e4b_fail(E4B_EINVAL,
+                    "MoE layer: unsupported shape (H=%d multiple of 256 <= 3072, FF2=%d <= 3072, FF=%d <= 768, "
+                    "8 <= E=%d <= 256)",
+                    A.H, A.FF2, A.FF, A.E);
+  int rc = launch_moe_router(A, st);
+  if (rc) return rc;
+  const int64_t gu_tiles = (A.FF2 + (int64_t)K * A.FF) / 2;
+  const int64_t gu_wgs = (gu_tiles + 3) / 4;
+  hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)(gu_wgs < 2048 ? gu_wgs : 2048)), dim3(256), 0, st, A, gu_tiles);
+  const int dd_tiles = (A.H + 2 * DD_R - 1) / (2 * DD_R), de_tiles = (A.H + DE_R - 1) / DE_R;
+  const int nbd = (dd_tiles + 3) / 4, nbe = (de_tiles + 3) / 4;
+  hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A, nbd);
+  hipLaunchKernelGGL(k_moe_tail, dim3(1), dim3(256), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_moe_topk(const MoeArgs& A, hipStream_t st) {
+  if (A.H % 4 || A.E < K || A.E > 256) return e4b_fail(E4B_EINVAL, "router: H=%d E=%d", A.H, A.E);
+  int rc = launch_moe_router(A, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_moe_topk, dim3(1), dim3(64), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}

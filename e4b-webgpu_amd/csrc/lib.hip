@@ -5,6 +5,7 @@
 
 #include "../../include/e4b.h"
 #include "kernels.h"
+#include "moe.h"
 #include "step.h"
 #include "util.h"
 
@@ -273,4 +274,88 @@ extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const fl
   a.chunk = chunk;
   a.eps = eps;
   return launch_attn(a, (hipStream_t)stream);
+}
+
+// ---- MoE half-layer ----------------------------------------------------------
+static int moe_setup(const e4b_moe_weights* w, const float* h, MoeArgs* A, Workspace* ws) {
+  if (!w || !h || !w->ffn_norm || !w->router_scale || !w->pre_ffw2 || !w->router_w || !w->pes || !w->dense_gate_up ||
+      !w->exp_gate_up || !w->dense_down || !w->exp_down || !w->post_ffw1 || !w->post_ffw2 || !w->post_ffw)
+    return e4b_fail(E4B_EINVAL, "MoE layer: null pointer argument");
+  const int H = w->hidden, E = w->n_experts, FF = w->expert_ffn, FF2 = w->dense_ffn;
+  if (H <= 0 || H % 256 || E < kMoeTopK || E > 256 || FF <= 0 || FF % 32 || FF2 <= 0 || FF2 % 32)
+    return e4b_fail(E4B_EINVAL, "MoE layer: bad shape (hidden %d, experts %d, expert_ffn %d, dense_ffn %d)", H, E, FF,
+                    FF2);
+  if (!aligned16(w->dense_gate_up) || !aligned16(w->exp_gate_up) || !aligned16(w->dense_down) ||
+      !aligned16(w->exp_down) || !aligned16(h) || !aligned16(w->router_w) || !aligned16(w->router_scale))
+    return e4b_fail(E4B_EINVAL, "MoE layer: weights and h must be 16-byte aligned");
+  // scratch: scores, xd, xm, topk, g_dense, g_slots, dense_out, moe_out
+  size_t off[8], cur = 0;
+  const size_t sz[8] = {(size_t)E * 4, (size_t)H * 2, (size_t)H * 2, 64, (size_t)FF2 * 2,
+                        (size_t)kMoeTopK * FF * 2, (size_t)H * 4, (size_t)H * 4};
+  for (int i = 0; i < 8; ++i) {
+    off[i] = cur;
+    cur += E4B_ALIGN256(sz[i]);
+  }
+  int rc = e4b_workspace(cur, ws);
+  if (rc) return rc;
+  MoeArgs& a = *A;
+  a = MoeArgs{};
+  a.h = h;
+  a.ffn_norm = w->ffn_norm;
+  a.router_scale = w->router_scale;
+  a.router_mult = 1.0f / sqrtf((float)H);
+  a.pre_ffw2 = w->pre_ffw2;
+  a.router_w = w->router_w;
+  a.pes = w->pes;
+  a.dense_gu = q40_view(w->dense_gate_up, 2 * (int64_t)FF2, H);
+  a.exp_gu = q40_view(w->exp_gate_up, (int64_t)E * 2 * FF, H);
+  a.dense_down = q40_view(w->dense_down, H, FF2);
+  a.exp_down = q40_view(w->exp_down, (int64_t)E * H, FF);
+  a.post_ffw1 = w->post_ffw1;
+  a.post_ffw2 = w->post_ffw2;
+  a.post_ffw = w->post_ffw;
+  a.layer_scale = w->layer_scale;
+  a.eps = w->eps;
+  a.H = H;
+  a.E = E;
+  a.FF = FF;
+  a.FF2 = FF2;
+  uint8_t* b = ws->buf;
+  a.scores = (float*)(b + off[0]);
+  a.xd = (uint16_t*)(b + off[1]);
+  a.xm = (uint16_t*)(b + off[2]);
+  a.topk_idx = (uint32_t*)(b + off[3]);
+  a.topk_w = (float*)(b + off[3] + 32);
+  a.g_dense = (uint16_t*)(b + off[4]);
+  a.g_slots = (uint16_t*)(b + off[5]);
+  a.dense_out = (float*)(b + off[6]);
+  a.moe_out = (float*)(b + off[7]);
+  return E4B_OK;
+}
+
+extern "C" int e4b_k_router_top8(const e4b_moe_weights* w, const float* h, uint32_t* topk_idx, float* topk_w,
+                                 void* stream) {
+  if (!topk_idx || !topk_w) return e4b_fail(E4B_EINVAL, "e4b_k_router_top8: null output");
+  MoeArgs a;
+  Workspace ws;
+  int rc = moe_setup(w, h, &a, &ws);
+  if (rc) return rc;
+  a.topk_idx = topk_idx;
+  a.topk_w = topk_w;
+  return launch_moe_topk(a, (hipStream_t)stream);
+}
+
+extern "C" int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* h_out, uint32_t* topk_idx,
+                               float* topk_w, float* dense_out, float* moe_out, void* stream) {
+  if (!h_out) return e4b_fail(E4B_EINVAL, "e4b_k_moe_layer: null h_out");
+  MoeArgs a;
+  Workspace ws;
+  int rc = moe_setup(w, h, &a, &ws);
+  if (rc) return rc;
+  a.h_out = h_out;
+  if (topk_idx) a.topk_idx = topk_idx;
+  if (topk_w) a.topk_w = topk_w;
+  if (dense_out) a.dense_out = dense_out;
+  if (moe_out) a.moe_out = moe_out;
+  return launch_moe_ffn(a, (hipStream_t)stream);
 }

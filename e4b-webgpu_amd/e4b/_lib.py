@@ -84,6 +84,8 @@ SIGNATURES = [
     ("e4b_k_q6k_row", _i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),
     ("e4b_k_argmax", _i32, [_vp, _i64, _vp, _vp]),
     ("e4b_rope_inv_freq", _i32, [_f32, _i32, _i32, _vp]),
+    ("e4b_k_router_top8", _i32, [_vp, _vp, _vp, _vp, _vp]),
+    ("e4b_k_moe_layer", _i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     ("e4b_k_attn_decode", _i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _u32, _f32,
                                  _i32, _vp, _vp]),
     ("e4b_create", _vp, [_vp]),
@@ -115,6 +117,18 @@ class ConfigC(C.Structure):
 
 
 FLAG_NO_GRAPH = 1
+
+
+class MoeWeightsC(C.Structure):
+    """struct e4b_moe_weights (include/e4b.h); every pointer is a device pointer."""
+
+    _fields_ = [
+        ("hidden", _i32), ("n_experts", _i32), ("expert_ffn", _i32), ("dense_ffn", _i32),
+        ("eps", _f32), ("layer_scale", _f32),
+        ("ffn_norm", _vp), ("router_scale", _vp), ("pre_ffw2", _vp), ("router_w", _vp), ("pes", _vp),
+        ("dense_gate_up", _vp), ("exp_gate_up", _vp), ("dense_down", _vp), ("exp_down", _vp),
+        ("post_ffw1", _vp), ("post_ffw2", _vp), ("post_ffw", _vp),
+    ]
 
 for _name, _res, _args in SIGNATURES:
     _fn = getattr(lib, _name)

@@ -152,3 +152,56 @@ class AttnLayer:
         self.qkv.upload(np.ascontiguousarray(qkv, np.float32))
         self.step_dev(pos)
         return self.out.download(np.float16, self.qh * self.hd)
+
+
+class MoeLayer:
+    """An A4B-style MoE FFN half-layer resident on the device.
+
+    Weights in raw ggml q4_0 blocks (numpy uint8) and f32 vectors:
+    dense_gate/dense_up [FF2][H], dense_down [H][FF2], exp_gate_up
+    [E][2 FF][H] (gate rows then up rows per expert), exp_down [E][H][FF],
+    router_w [E][H], router_scale / norms [H], pes [E].
+    """
+
+    def __init__(self, H: int, E: int, FF: int, FF2: int, t: dict, eps: float = 1e-6, layer_scale: float = 1.0):
+        from ._lib import MoeWeightsC
+        self.H, self.E, self.FF, self.FF2 = H, E, FF, FF2
+        f = lambda a: DeviceBuffer.from_array(np.ascontiguousarray(a, np.float32))  # noqa: E731
+        self._keep = {}
+        for n in ("ffn_norm", "router_scale", "pre_ffw2", "router_w", "pes", "post_ffw1", "post_ffw2", "post_ffw"):
+            self._keep[n] = f(t[n])
+        dense_gu = np.concatenate([np.asarray(t["dense_gate"], np.uint8).reshape(-1),
+                                   np.asarray(t["dense_up"], np.uint8).reshape(-1)])
+        self._keep["dense_gate_up"] = DeviceBuffer.from_array(q40_pack(dense_gu, 2 * FF2, H))
+        self._keep["exp_gate_up"] = DeviceBuffer.from_array(q40_pack(t["exp_gate_up"], E * 2 * FF, H))
+        self._keep["dense_down"] = DeviceBuffer.from_array(q40_pack(t["dense_down"], H, FF2))
+        self._keep["exp_down"] = DeviceBuffer.from_array(q40_pack(t["exp_down"], E * H, FF))
+        w = MoeWeightsC()
+        w.hidden, w.n_experts, w.expert_ffn, w.dense_ffn = H, E, FF, FF2
+        w.eps, w.layer_scale = eps, layer_scale
+        for n, b in self._keep.items():
+            setattr(w, n, b.ptr)
+        self.w = w
+        self.h = DeviceBuffer(H * 4)
+        self.h_out = DeviceBuffer(H * 4)
+        self.idx = DeviceBuffer(64)
+        self.wts = DeviceBuffer(64)
+        self.dense = DeviceBuffer(H * 4)
+        self.moe = DeviceBuffer(H * 4)
+
+    def forward_dev(self, stream=None) -> None:
+        check(lib.e4b_k_moe_layer(C.byref(self.w), _vp(self.h), _vp(self.h_out), _vp(self.idx), _vp(self.wts),
+                                  _vp(self.dense), _vp(self.moe), _vp(stream)), "e4b_k_moe_layer")
+
+    def forward(self, h: np.ndarray) -> dict:
+        self.h.upload(np.ascontiguousarray(h, np.float32))
+        self.forward_dev()
+        return {"h_out": self.h_out.download(np.float32, self.H), "topk_idx": self.idx.download(np.uint32, 8),
+                "topk_w": self.wts.download(np.float32, 8), "dense_out": self.dense.download(np.float32, self.H),
+                "moe_out": self.moe.download(np.float32, self.H)}
+
+    def router_top8(self, h: np.ndarray):
+        self.h.upload(np.ascontiguousarray(h, np.float32))
+        check(lib.e4b_k_router_top8(C.byref(self.w), _vp(self.h), _vp(self.idx), _vp(self.wts), None),
+              "e4b_k_router_top8")
+        return self.idx.download(np.uint32, 8), self.wts.download(np.float32, 8)

@@ -159,6 +159,51 @@ int e4b_k_attn_decode(const float* qkv, const float* q_norm, const float* k_norm
                       int q_heads, int kv_heads, int head_dim, int slots, int window,
                       uint32_t pos, float eps, int chunk, void* out_f16, void* stream);
 
+/* MoE FFN half-layer of an A4B-style decoder (src/engine-a4b.js:438-462):
+ * all pointers are device pointers; the q4_0 matrices are in the packed
+ * layout (e4b_q40_pack of the ggml rows).  Expert e's gate rows are
+ * [2 ff e, 2 ff e + ff) and its up rows [2 ff e + ff, 2 ff (e+1)) of
+ * exp_gate_up; its down rows are [hidden e, hidden (e+1)) of exp_down. */
+typedef struct e4b_moe_weights {
+  int32_t hidden;             /* 2816 (multiple of 256, <= 3072) */
+  int32_t n_experts;          /* 128 (8..256) */
+  int32_t expert_ffn;         /* 704 (multiple of 32, <= 768) */
+  int32_t dense_ffn;          /* 2112 (multiple of 32, <= 3072) */
+  float eps;                  /* 1e-6 */
+  float layer_scale;          /* layer output scalar */
+  const float* ffn_norm;      /* [hidden] dense-branch input norm */
+  const float* router_scale;  /* [hidden] ffn_gate_inp.scale (raw; the kernel applies hidden^-1/2) */
+  const float* pre_ffw2;      /* [hidden] expert-branch input norm */
+  const float* router_w;      /* [n_experts][hidden] f32 */
+  const float* pes;           /* [n_experts] per-expert output scale */
+  const void* dense_gate_up;  /* q4_0 [2 dense_ffn][hidden]: gate rows then up rows */
+  const void* exp_gate_up;    /* q4_0 [n_experts 2 expert_ffn][hidden] */
+  const void* dense_down;     /* q4_0 [hidden][dense_ffn] */
+  const void* exp_down;       /* q4_0 [n_experts hidden][expert_ffn] */
+  const float* post_ffw1;     /* [hidden] dense-branch post norm */
+  const float* post_ffw2;     /* [hidden] expert-branch post norm */
+  const float* post_ffw;      /* [hidden] combined post norm */
+} e4b_moe_weights;
+
+/* Router + top-8 (kernels/routertop.wgsl:19-71): x = rms(h) * router_scale *
+ * hidden^-1/2, scores = router_w . x, softmax, top-8 by a strict '>' scan
+ * (ties -> lowest index), w_k = p_k / sum_top(p) * pes[idx_k].
+ * topk_idx u32[8], topk_w f32[8] (device). */
+int e4b_k_router_top8(const e4b_moe_weights* w, const float* h, uint32_t* topk_idx, float* topk_w,
+                      void* stream);
+
+/* The whole half-layer (rmsacc3 outputs -> routertop -> q40gu dense + 8 expert
+ * slots -> dense down + q40moedown -> a4btail, kernels/rmsacc3.wgsl:36-53,
+ * kernels/q40gu.wgsl:62-119, kernels/q40moedown.wgsl:42-75,
+ * kernels/a4btail.wgsl:26-71):
+ *   dense = W_down,d . f16(gelu(G x_d) * (U x_d)),  x_d = f16(rms(h) ffn_norm)
+ *   moe   = sum_k w_k W_down,e_k . f16(gelu(G_e_k x_m) * (U_e_k x_m)),  x_m = f16(rms(h) pre_ffw2)
+ *   comb  = rms(dense) post_ffw1 + rms(moe) post_ffw2
+ *   h_out = (h + rms(comb) post_ffw) * layer_scale
+ * Every output pointer except h_out may be NULL. */
+int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* h_out, uint32_t* topk_idx,
+                    float* topk_w, float* dense_out, float* moe_out, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Engine: the per-token batch-1 decode step of an E4B-shaped decoder
  * (35 layers, 4 sliding : 1 global, GeGLU FFN, per-layer embeddings, q4_0

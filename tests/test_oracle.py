@@ -448,3 +448,74 @@ def test_kvring_recover_closed_form():
                     continue
                 r = orc.kvring_recover(t, mw, ring)
                 assert r % ring == t and r <= mw and r + ring > mw
+
+
+# --------------------------------------------------------------------------
+# MoE half-layer (orc_moe_ffn): independent numpy restatement of the A4B
+# order (src/engine-a4b.js:438-462) from pinned primitives (q4_0 dequant,
+# gelu_tanh, f16 rounding) on a small shape.
+# --------------------------------------------------------------------------
+
+
+def _moe_case(seed, H=256, E=16, FF=64, FF2=96):
+    rng = np.random.default_rng(seed)
+    q = lambda rows, cols, s: formats.synth_q40(s, rows, cols, 0.02)  # noqa: E731
+    m = {"hidden": H, "n_experts": E, "top_k": 8, "expert_ffn": FF, "dense_ffn": FF2, "eps": 1e-6,
+         "layer_scale": 0.8,
+         "ffn_norm": 1 + 0.1 * rng.standard_normal(H), "router_scale": 1 + 0.1 * rng.standard_normal(H),
+         "pre_ffw2": 1 + 0.1 * rng.standard_normal(H), "router_w": 0.02 * rng.standard_normal((E, H)) * 40,
+         "pes": 1 + 0.2 * rng.standard_normal(E),
+         "dense_gate": q(FF2, H, seed + 1), "dense_up": q(FF2, H, seed + 2), "dense_down": q(H, FF2, seed + 3),
+         "exp_gate_up": q(E * 2 * FF, H, seed + 4), "exp_down": q(E * H, FF, seed + 5),
+         "post_ffw1": 1 + 0.1 * rng.standard_normal(H), "post_ffw2": 1 + 0.1 * rng.standard_normal(H),
+         "post_ffw": 1 + 0.1 * rng.standard_normal(H)}
+    for k, v in m.items():
+        if isinstance(v, np.ndarray) and v.dtype == np.float64:
+            m[k] = v.astype(np.float32)
+    h = (2.0 * rng.standard_normal(H)).astype(np.float32)
+    return m, h
+
+
+def _moe_numpy(m, h):
+    H, E, FF, FF2 = m["hidden"], m["n_experts"], m["expert_ffn"], m["dense_ffn"]
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float64)  # noqa: E731
+    deq = lambda w, rows, cols: orc.q40_dequant(w).reshape(rows, cols).astype(np.float64)  # noqa: E731
+    gelu = np.vectorize(lambda g: orc.gelu_tanh(float(g)))
+    hd = h.astype(np.float64)
+    rinv = 1.0 / np.sqrt(np.mean(hd * hd) + 1e-6)
+    xd = f16(hd * rinv * m["ffn_norm"])
+    xm = f16(hd * rinv * m["pre_ffw2"])
+    rs = (m["router_scale"].astype(np.float64) / np.sqrt(H)).astype(np.float32).astype(np.float64)
+    xr = (hd * rinv * rs).astype(np.float32).astype(np.float64)
+    s = (m["router_w"].astype(np.float64) @ xr).astype(np.float32).astype(np.float64)
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    idx = np.argsort(-p, kind="stable")[:8]
+    w = p[idx] / p[idx].sum() * m["pes"][idx]
+    Wg = deq(np.concatenate([m["dense_gate"], m["dense_up"]]), 2 * FF2, H)
+    g = Wg @ xd
+    gd = f16(gelu(g[:FF2]) * g[FF2:])
+    dense = (deq(m["dense_down"], H, FF2) @ gd).astype(np.float32).astype(np.float64)
+    Wgu = deq(m["exp_gate_up"], E * 2 * FF, H).reshape(E, 2 * FF, H)
+    Wdn = deq(m["exp_down"], E * H, FF).reshape(E, H, FF)
+    moe = np.zeros(H)
+    for k in range(8):
+        e = idx[k]
+        gk = Wgu[e] @ xm
+        ge = f16(gelu(gk[:FF]) * gk[FF:])
+        moe += float(np.float32(w[k])) * (Wdn[e] @ ge).astype(np.float32)
+    r = lambda v: v / np.sqrt(np.mean(v * v) + 1e-6)  # noqa: E731
+    comb = r(dense) * m["post_ffw1"] + r(moe) * m["post_ffw2"]
+    hout = (hd + r(comb) * m["post_ffw"]) * m["layer_scale"]
+    return idx, w, dense, moe, hout
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_moe_ffn_matches_numpy_restatement(seed):
+    m, h = _moe_case(seed)
+    idx, w, dense, moe, hout = orc.moe_ffn(m, h)
+    ridx, rw, rdense, rmoe, rhout = _moe_numpy(m, h)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=1e-6)
+    for got, want in ((dense, rdense), (moe, rmoe), (hout, rhout)):
+        np.testing.assert_allclose(got, want, rtol=0, atol=1e-5 * np.abs(want).max())
