@@ -154,3 +154,19 @@ def test_c4_full_model_lockstep():
     err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
     print(f"c4 full logits err {err:.2e}")
     assert err < LOGIT_TOL
+
+
+@pytest.mark.slow
+def test_c4_greedy_256_steps():
+    # the GPU-fed greedy sequence at the E4B shape equals
+    # the oracle's over 256 decode steps (near-ties reported, none expected)
+    cfg = E4BConfig(max_seq=1024)
+    eng, om = build(cfg, 3)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 16)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 256)
+    print(f"c4 256 steps: {len(toks) - 1} decoded, distinct tokens {len(set(toks))}, near-ties {ties}")
+    if o_lg is None:  # lockstep already asserted that the divergence is a near-tie
+        return
+    err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
+    print(f"c4 256 steps: final logits err {err:.2e}")
+    assert err < LOGIT_TOL

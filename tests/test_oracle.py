@@ -519,3 +519,66 @@ def test_moe_ffn_matches_numpy_restatement(seed):
     np.testing.assert_allclose(w, rw, rtol=1e-6)
     for got, want in ((dense, rdense), (moe, rmoe), (hout, rhout)):
         np.testing.assert_allclose(got, want, rtol=0, atol=1e-5 * np.abs(want).max())
+
+
+# --------------------------------------------------------------------------
+# Full step (orc_step): a special case that reduces to a closed form.  With
+# every per-layer matrix zero, attention, FFN and the PLE branch add exact
+# zeros (rms of a zero vector is 0), so the hidden state is the embedding row
+# times the product of the layer scalars, and the logits are
+# softcap(E . rms(h) * w_out) with the tied Q6_K embedding E.
+# --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("token,pos", [(17, 0), (999, 5)])
+def test_step_zero_layers_closed_form(token, pos):
+    from e4b.model import norm_weights_random, synth_tensors, tiny_config
+    cfg = tiny_config()
+    t = norm_weights_random(synth_tensors(cfg, 5), 6)
+    for name, ten in t.items():
+        if name.startswith("blk.") and ten.data.dtype == np.uint8:
+            ten.data = np.zeros_like(ten.data)
+        if name.endswith("layer_output_scale.weight"):
+            ten.data = np.full_like(ten.data, 0.75)
+    om = orc.OracleModel(cfg.as_dict(), {n: x.data for n, x in t.items()})
+    for p in range(pos):
+        om.step(3, p)
+    tok, lg, hid = om.step(token, pos, want_logits=True, want_hidden=True)
+    H = cfg.hidden
+    emb = orc.q6k_row(t["token_embd.weight"].data, H, token, math.sqrt(H)).astype(np.float64)
+    np.testing.assert_allclose(hid, emb * 0.75 ** cfg.layers, rtol=1e-6, atol=1e-9)
+    x = emb / np.sqrt(np.mean(emb * emb) + cfg.eps) * t["output_norm.weight"].data
+    E = np.stack([orc.q6k_row(t["token_embd.weight"].data, H, r) for r in range(cfg.vocab)]).astype(np.float64)
+    want = 30.0 * np.tanh((E @ x.astype(np.float32).astype(np.float64)) / 30.0)
+    np.testing.assert_allclose(lg, want, rtol=2e-5, atol=2e-5 * np.abs(want).max())
+    assert tok == int(np.argmax(want)) or np.sort(want)[-1] - np.sort(want)[-2] < 1e-5
+
+
+def test_moe_zero_router_picks_first_eight_uniformly():
+    # zero router rows -> equal scores -> ties resolve to experts 0..7 with
+    # weight p/sum_top(p) = 1/8, times the per-expert scale
+    m, h = _moe_case(7)
+    m["router_w"] = np.zeros_like(m["router_w"])
+    idx, w, _, _, _ = orc.moe_ffn(m, h)
+    np.testing.assert_array_equal(idx, np.arange(8))
+    np.testing.assert_allclose(w, m["pes"][:8] / 8.0, rtol=1e-6)
+
+
+def test_moe_identical_experts_reduce_to_one_expert():
+    # every expert identical and pes = 1: the routed mixture equals one
+    # expert's output whatever the routing (the weights sum to 1)
+    m, h = _moe_case(8)
+    E, FF, H = m["n_experts"], m["expert_ffn"], m["hidden"]
+    gu1 = np.asarray(m["exp_gate_up"]).reshape(E, -1)[0]
+    dn1 = np.asarray(m["exp_down"]).reshape(E, -1)[0]
+    m["exp_gate_up"] = np.tile(gu1, E)
+    m["exp_down"] = np.tile(dn1, E)
+    m["pes"] = np.ones(E, np.float32)
+    _, w, _, moe, _ = orc.moe_ffn(m, h)
+    np.testing.assert_allclose(w.sum(), 1.0, rtol=1e-6)
+    hd = h.astype(np.float64)
+    xm = (hd / np.sqrt(np.mean(hd * hd) + 1e-6) * m["pre_ffw2"]).astype(np.float32).astype(np.float16)
+    g = orc.q40_gemv(gu1, 2 * FF, H, xm.astype(np.float32)).astype(np.float64)
+    ge = np.array([orc.gelu_tanh(float(a)) for a in g[:FF]]) * g[FF:]
+    one = orc.q40_gemv(dn1, H, FF, ge.astype(np.float16).astype(np.float32)).astype(np.float64)
+    np.testing.assert_allclose(moe, one, rtol=0, atol=2e-6 * np.abs(one).max())
