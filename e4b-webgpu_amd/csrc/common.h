@@ -242,19 +242,29 @@ DEV float wave_max(float v) {
   v = fmaxf(v, lane_xor<2>(v));
   return fmaxf(v, lane_xor<1>(v));
 }
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load of the wave (a workgroup-scope fence over all
+// address spaces), which would stall a kernel on its whole in-flight weight
+// stream; barriers that only publish LDS data use this one.
+DEV void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // sum over a 256-thread block; every thread gets the total.  `red` = 4 floats of LDS.
 DEV float block_sum(float v, float* red) {
   v = wave_sum(v);
-  __syncthreads();
+  lds_sync();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_sync();
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 DEV float block_max(float v, float* red) {
   v = wave_max(v);
-  __syncthreads();
+  lds_sync();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_sync();
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 // RMSNorm scale (mean(x^2) + eps)^-1/2 from a sum of squares
@@ -278,5 +288,16 @@ DEV uint2 ld_nt_u2(const uint2* p) {
   return make_uint2(v.x, v.y);
 }
 DEV uint16_t ld_nt_u16(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+DEV uint32_t ld_nt_u32(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
+// f16 block scale e (= row * nb + block) of a q4_0 scale plane, loaded as the
+// aligned 32-bit pair that holds it (the plane is padded to 256 bytes, so the
+// pair is always inside it).  A 16-bit load would let the compiler pack two
+// scales into one register right after the loads, which forces a wait on
+// every load issued before them; the half is selected when it is used.
+DEV uint32_t ld_scale_pair(const uint16_t* sc, int64_t e) {
+  return ld_nt_u32(reinterpret_cast<const uint32_t*>(sc) + (e >> 1));
+}
+DEV float scale_of(uint32_t pair, uint32_t odd) { return h2f((uint16_t)(pair >> (odd * 16))); }
 
 #endif  // __HIPCC__

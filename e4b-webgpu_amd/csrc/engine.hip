@@ -107,6 +107,24 @@ int upload_q40_rows(uint8_t* dst, int64_t total_rows, int64_t cols, int64_t row_
   return E4B_OK;
 }
 
+// q4_0 matrix stored block-transposed: block j of row r at index j * rows + r
+// in both planes, so a kernel that walks one block column over all rows
+// streams contiguous memory (the fused PLE branch's projection)
+int upload_q40_block_t(uint8_t* dst, int64_t rows, int64_t cols, const void* ggml) {
+  std::vector<uint8_t> tmp(e4b_q40_packed_bytes(rows, cols)), out(tmp.size());
+  int rc = e4b_q40_pack(ggml, rows, cols, tmp.data());
+  if (rc) return rc;
+  const int64_t nb = cols / 32;
+  const size_t sc_off = E4B_ALIGN256((size_t)rows * nb * 16);
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t j = 0; j < nb; ++j) {
+      memcpy(&out[(size_t)(j * rows + r) * 16], &tmp[(size_t)(r * nb + j) * 16], 16);
+      memcpy(&out[sc_off + (size_t)(j * rows + r) * 2], &tmp[sc_off + (size_t)(r * nb + j) * 2], 2);
+    }
+  E4B_HIP(hipMemcpy(dst, out.data(), out.size(), hipMemcpyHostToDevice));
+  return E4B_OK;
+}
+
 int upload_f32(e4b_ctx* c, float** dst, const void* bytes, int64_t n) {
   if (!*dst) {
     int rc = dalloc_t(c, dst, (size_t)n);
@@ -260,9 +278,12 @@ extern "C" int e4b_set_tensor(e4b_ctx* c, const char* name, int type, const int6
       if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
       rc = q40(&ly.pg, PD, H, 0, PD);
       break;
-    case P_PROJ:
+    case P_PROJ:  // stored block-transposed for the fused PLE branch
       if (!PD) return e4b_fail(E4B_EINVAL, "%s given but ple_dim is 0", name);
-      rc = q40(&ly.pp, H, PD, 0, H);
+      if ((rc = expect(name, type, E4B_GGML_Q4_0, dims, nd, PD, H)) || (rc = check_bytes((size_t)(H * PD / 32) * 18)))
+        return rc;
+      if (!ly.pp && (rc = dalloc(c, (void**)&ly.pp, e4b_q40_packed_bytes(H, PD)))) return rc;
+      rc = upload_q40_block_t(ly.pp, H, PD, bytes);
       break;
     case P_POST_NORM: rc = f32v(&ly.post_norm, H); break;
     case P_SCALE:
@@ -334,7 +355,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->o, (size_t)H)) || (rc = dalloc_t(c, &c->xf, (size_t)H)) ||
       (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)H)) ||
       (rc = dalloc_t(c, &c->xg, (size_t)H)) || (rc = dalloc_t(c, &c->gp, (size_t)(PD ? PD : 1))) ||
-      (rc = dalloc_t(c, &c->pp, (size_t)H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
+      (rc = dalloc_t(c, &c->pp, (size_t)(PD ? PD / 32 : 1) * H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)))
     return rc;
   c->finalized = true;
@@ -378,7 +399,7 @@ int record_step(e4b_ctx* c) {
     hnext = t;
   };
   auto pro = [&](float* hout, const float* a, const float* w1, const float* w2, float scale) {
-    ProArgs p;
+    ProArgs p{};
     p.hin = hcur;
     p.hout = hout;
     p.a = a;
@@ -416,25 +437,28 @@ int record_step(e4b_ctx* c) {
       }
     } else {
       const Layer& pv = c->L[l - 1];
-      const ProArgs p = PD ? pro(hnext, c->pp, pv.post_norm, ly.attn_norm, pv.scale)
-                           : pro(hnext, c->dn, pv.post_ffw, ly.attn_norm, pv.scale);
+      ProArgs p = PD ? pro(hnext, c->pp, pv.post_norm, ly.attn_norm, pv.scale)
+                     : pro(hnext, c->dn, pv.post_ffw, ly.attn_norm, pv.scale);
+      if (PD) p.na = PD / 32;  // the PLE branch leaves PD/32 partial projections
       rc = launch_q40(Wqkv, nullptr, nullptr, EPI_F32, oq, 1, st, &p);
       swap_h();
     }
     if (rc) return rc;
-    // 2. attention (head prep, KV write, split-K, combine)
+    // 2. attention (head prep, KV write, split-K); the combine is the o
+    //    projection's prologue when the projection has 2048 columns
+    const bool fuse_combine = QH * HD == kProAttnH;
     AttnLaunch a;
     a.qkv = c->qkv;
     a.qw = ly.q_norm;
     a.kw = ly.k_norm;
     a.inv_freq = ly.global ? c->inv_global : c->inv_local;
+    a.rope = c->rope + (ly.global ? HD / 2 : 0);
     a.kc = ly.kc;
     a.vc = ly.vc;
     a.params = c->params;
     a.pos = 0;
     a.part_o = c->part_o;
     a.part_ml = c->part_ml;
-    a.rope = c->rope + (ly.global ? HD / 2 : 0);
     a.out = c->attn;
     a.qh = QH;
     a.kvh = KVH;
@@ -443,12 +467,25 @@ int record_step(e4b_ctx* c) {
     a.slots = ly.slots;
     a.window = ly.global ? 0 : k.window;
     a.chunk = c->chunk;
+    a.combine = !fuse_combine;
     a.eps = k.eps;
     if ((rc = launch_attn(a, st))) return rc;
     // 3. o projection
     GemvOut oo = {c->o, nullptr, nullptr, 0};
-    if ((rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * HD), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st)))
-      return rc;
+    const Q40Mat Wo = q40_view(ly.o, H, (int64_t)QH * HD);
+    if (fuse_combine) {
+      ProArgs pa{};
+      pa.part_o = c->part_o;
+      pa.part_ml = c->part_ml;
+      pa.params = c->params;
+      pa.window = a.window;
+      pa.chunk_shift = c->chunk == 64 ? 6 : 5;
+      pa.gch = attn_chunks(a.window > 0 ? a.window : a.slots, c->chunk);
+      rc = launch_q40(Wo, nullptr, nullptr, EPI_F32, oo, 1, st, &pa);
+    } else {
+      rc = launch_q40(Wo, (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st);
+    }
+    if (rc) return rc;
     // 4. gate/up + GeGLU; prologue: post-attention residual + FFN input norm
     {
       const ProArgs p = pro(hnext, c->o, ly.post_attn, ly.ffn_norm, 1.0f);
@@ -462,22 +499,28 @@ int record_step(e4b_ctx* c) {
     if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, 1, st)))
       return rc;
     if (PD) {
-      // 6. PLE gate + GELU x per-layer input; prologue: post-FFN residual
+      // 6. PLE branch in one launch: post-FFN residual prologue, gate x GELU x
+      //    per-layer input, projection partials (summed by the next consumer)
       const ProArgs p = pro(hnext, c->dn, ly.post_ffw, nullptr, 1.0f);
-      GemvOut ogp = {nullptr, c->gp, c->ple + (int64_t)l * PD, 0};
-      if ((rc = launch_q40(q40_view(ly.pg, PD, H), nullptr, nullptr, EPI_GELU_MUL, ogp, 1, st, &p))) return rc;
+      const size_t nbp = (size_t)H * (PD / 32);
+      PleLaunch pl;
+      pl.gate = q40_view(ly.pg, PD, H);
+      pl.proj_nib = (const uint4*)ly.pp;
+      pl.proj_sc = (const uint16_t*)(ly.pp + E4B_ALIGN256(nbp * 16));
+      pl.ple = c->ple + (int64_t)l * PD;
+      pl.part = c->pp;
+      pl.H = H;
+      pl.PD = PD;
+      if ((rc = launch_ple(pl, p, st))) return rc;
       swap_h();
-      // 7. PLE projection
-      GemvOut opp = {c->pp, nullptr, nullptr, 0};
-      if ((rc = launch_q40(q40_view(ly.pp, H, PD), (const uint32_t*)c->gp, nullptr, EPI_F32, opp, 1, st))) return rc;
     }
   }
   // last residual + final norm (f32, hi/lo split) -> lm-head -> argmax/feedback
   const Layer& last = c->L[Lc - 1];
   if (PD)
-    rc = launch_tail(hcur, c->pp, last.post_norm, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
+    rc = launch_tail(hcur, c->pp, PD / 32, last.post_norm, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
   else
-    rc = launch_tail(hcur, c->dn, last.post_ffw, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
+    rc = launch_tail(hcur, c->dn, 1, last.post_ffw, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
   if (rc) return rc;
   c->h_final = hcur;
   if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,

@@ -329,12 +329,14 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.eps = a.eps;
   if (a.chunk == 64) {
     hipLaunchKernelGGL(k_attn_split<64>, dim3(a.kvh, nch), dim3(512), 0, st, A);
-    hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
-                       a.window, nch, a.out);
+    if (a.combine)
+      hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+                         a.window, nch, a.out);
   } else {
     hipLaunchKernelGGL(k_attn_split<32>, dim3(a.kvh, nch), dim3(512), 0, st, A);
-    hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
-                       a.window, nch, a.out);
+    if (a.combine)
+      hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+                         a.window, nch, a.out);
   }
   E4B_HIP(hipGetLastError());
   return E4B_OK;

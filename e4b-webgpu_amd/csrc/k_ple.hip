@@ -1,0 +1,125 @@
+// k_ple.hip -- the per-layer-embedding branch of one layer in one launch
+// (src/engine.js:282-323: gate GEMV, gelu * per-layer input, projection
+// GEMV; kernels/plegatemv.wgsl:20-60 for the gate).
+//
+// The projection's input has PD = 256 elements = 8 q4_0 blocks, so the
+// branch splits into 8 workgroups by projection block: workgroup w computes
+// gate rows [32w, 32w+32) (after the fused post-FFN residual prologue, which
+// every workgroup repeats), keeps the 32 gated values in LDS, and multiplies
+// them with block w of every projection row.  It writes the partial
+// projection part[w][0..H); the consumer (the next layer's qkv prologue or
+// the step tail) adds the 8 partials in a fixed order.  The projection
+// weights are stored block-transposed ([block][row]) so that a workgroup's
+// block-w column is one contiguous stream.
+#include "../../include/e4b.h"
+#include "q40_kernel.h"
+#include "step.h"
+#include "util.h"
+
+namespace {
+
+constexpr float kTwo24 = 16777216.0f;
+
+// PROK = H / 256: lanes per gate row LPR = H / 32 = 8 PROK, G = 8 / PROK
+// groups per wave, R = PROK rows per group, 8 gate rows per wave.
+template <int PROK>
+__global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
+  constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK;
+  static_assert(G * R == 8, "8 gate rows per wave");
+  __shared__ __align__(16) uint16_t xs[H];
+  __shared__ float red[4];
+  __shared__ __align__(16) uint16_t gs[32];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane / LPR, l = lane - g * LPR;
+  const int w = blockIdx.x;
+
+  q40k::ProRegs<PROK> pr;
+  q40k::pro_issue<PROK>(pa, pr);
+  // gate rows of this lane group, block l
+  const int row0 = 32 * w + 8 * wave + g * R;
+  uint4 wq[R];
+  uint16_t wsc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    wq[r] = ld_nt_u4(A.gate.nib + (int64_t)(row0 + r) * A.gate.nb + l);
+    wsc[r] = ld_nt_u16(A.gate.sc + (int64_t)(row0 + r) * A.gate.nb + l);
+  }
+  // projection rows o = threadIdx.x + 256 i, block w (block-transposed planes)
+  uint4 pq[PROK];
+  uint16_t psc[PROK];
+#pragma unroll
+  for (int i = 0; i < PROK; ++i) {
+    const int64_t o = threadIdx.x + 256 * i;
+    pq[i] = ld_nt_u4(A.proj_nib + (int64_t)w * H + o);
+    psc[i] = ld_nt_u16(A.proj_sc + (int64_t)w * H + o);
+  }
+  q40k::pro_finish<PROK>(pa, pr, xs, red);
+
+  // gate: 32 columns of x per lane (block l), R rows per group
+  {
+    uint32_t xp[16];
+    const uint4* v = reinterpret_cast<const uint4*>(xs) + (size_t)l * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 t = v[i];
+      xp[4 * i + 0] = t.x;
+      xp[4 * i + 1] = t.y;
+      xp[4 * i + 2] = t.z;
+      xp[4 * i + 3] = t.w;
+    }
+    const float xs8 = -8.f * xsum16(xp);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float a0 = 0.f, a1 = 0.f;
+      q40_dot2(wq[r], xp, a0, a1);
+      acc[r] = h2f(wsc[r]) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8));
+    }
+    const float vrow = reduce_rows<LPR, R>(acc);
+    const int r = l / (LPR / R);
+    if ((l % (LPR / R)) == 0) {
+      const int row = row0 + r;
+      gs[row - 32 * w] = f2h(gelu_tanh(vrow) * A.ple[row]);
+    }
+  }
+  __syncthreads();
+
+  // projection partial: part[w][o] = d_{o,w} * sum_j (n_j - 8) g_j
+  {
+    uint32_t gp[16];
+    const uint4* v = reinterpret_cast<const uint4*>(gs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 t = v[i];
+      gp[4 * i + 0] = t.x;
+      gp[4 * i + 1] = t.y;
+      gp[4 * i + 2] = t.z;
+      gp[4 * i + 3] = t.w;
+    }
+    const float gs8 = -8.f * xsum16(gp);
+#pragma unroll
+    for (int i = 0; i < PROK; ++i) {
+      float a0 = 0.f, a1 = 0.f;
+      q40_dot2(pq[i], gp, a0, a1);
+      A.part[(int64_t)w * H + threadIdx.x + 256 * i] =
+          h2f(psc[i]) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, gs8));
+    }
+  }
+}
+
+}  // namespace
+
+int launch_ple(const PleLaunch& A, const ProArgs& pa, hipStream_t st) {
+  if (A.PD != 256 || A.gate.rows != A.PD || A.gate.nb * 32 != A.H || pa.H != A.H || !q40_prologue_supported(A.H))
+    return e4b_fail(E4B_EINVAL, "PLE branch: needs ple_dim 256 and hidden 256/512/1024/2048 (got %d, %d)", A.PD, A.H);
+  const dim3 grid(A.PD / 32);
+  switch (A.H) {
+    case 256: hipLaunchKernelGGL(k_ple<1>, grid, dim3(256), 0, st, A, pa); break;
+    case 512: hipLaunchKernelGGL(k_ple<2>, grid, dim3(256), 0, st, A, pa); break;
+    case 1024: hipLaunchKernelGGL(k_ple<4>, grid, dim3(256), 0, st, A, pa); break;
+    case 2048: hipLaunchKernelGGL(k_ple<8>, grid, dim3(256), 0, st, A, pa); break;
+  }
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}

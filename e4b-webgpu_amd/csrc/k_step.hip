@@ -14,10 +14,12 @@ namespace {
 
 constexpr int kMaxPer = 16;  // elements per thread in the one-block kernels (H <= 4096)
 
-// Last residual of the step and the final norm: p = the PLE projection (or
-// the down projection when there is no PLE); h = (h + rms(p) * w_post) * scale; xo = rms(h) * w_out stored as an exact
+// Last residual of the step and the final norm: p = the sum of `np` partial
+// PLE projections (or the down projection when there is no PLE);
+// h = (h + rms(p) * w_post) * scale; xo = rms(h) * w_out stored as an exact
 // f16 hi/lo split for the lm-head (kernels/a4btail.wgsl:26-71 with the
 // reference's f32 final norm, src/engine-a4b.js:688).
+template <int NP>
 __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float* __restrict__ p,
                                               const float* __restrict__ w_post, float scale,
                                               const float* __restrict__ w_out, uint16_t* __restrict__ xo_hl, int H,
@@ -29,7 +31,12 @@ __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float
 #pragma unroll
   for (int k = 0; k < kMaxPer; ++k) {
     const int i = threadIdx.x + 256 * k;
-    const float v = i < H ? p[i] : 0.f;
+    float pp[NP];
+#pragma unroll
+    for (int s = 0; s < NP; ++s) pp[s] = i < H ? p[(int64_t)s * H + i] : 0.f;
+    float v = pp[0];
+#pragma unroll
+    for (int s = 1; s < NP; ++s) v += pp[s];
     pv[k] = v;
     ss = fmaf(v, v, ss);
   }
@@ -211,9 +218,13 @@ __global__ __launch_bounds__(256) void k_feedback(const uint2* __restrict__ part
 }  // namespace
 
 // ---- launchers --------------------------------------------------------------
-int launch_tail(float* h, const float* p, const float* w_post, float scale, const float* w_out,
+int launch_tail(float* h, const float* p, int np, const float* w_post, float scale, const float* w_out,
                 uint16_t* xo_hl, int H, float eps, hipStream_t st) {
-  hipLaunchKernelGGL(k_tail, dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+  if (np != 1 && np != kMaxPartials) return e4b_fail(E4B_EINVAL, "tail: %d partial vectors (1 or %d)", np, kMaxPartials);
+  if (np == 1)
+    hipLaunchKernelGGL(k_tail<1>, dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+  else
+    hipLaunchKernelGGL(k_tail<kMaxPartials>, dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

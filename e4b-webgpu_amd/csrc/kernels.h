@@ -63,10 +63,16 @@ struct GemvOut {
   int64_t ff;        // EPI_GEGLU: rows per half
 };
 
-// Optional fused input prologue of a q4_0 GEMV (q40_kernel.h):
-// h = (hin + rms(a) * w1) * scale (a may be null: h = hin * scale),
-// x = w2 ? f16(rms(h) * w2) : f16(h); block (0,0) stores h to hout.
-// H = cols must be 256, 512, 1024 or 2048.
+// Optional fused input prologue of a q4_0 GEMV (q40_kernel.h), one of:
+//  * residual + norm: h = (hin + rms(a) * w1) * scale (a may be null: h =
+//    hin * scale), x = w2 ? f16(rms(h) * w2) : f16(h); block (0,0) stores h
+//    to hout; a is the sum of `na` partial vectors a[s*H + i] (s < na <= 8).
+//    H = cols must be 256, 512, 1024 or 2048.
+//  * attention combine (part_o != null): x = the log-sum-exp merge of the
+//    split-K partials of the live chunks of the current position, f16, for
+//    an o projection of 2048 columns (8 heads of 256).
+constexpr int kMaxPartials = 8;
+constexpr int kProAttnH = 2048;  // columns of an o projection with the attention prologue (8 heads of 256)
 struct ProArgs {
   const float* hin;
   float* hout;       // may be null
@@ -76,6 +82,14 @@ struct ProArgs {
   float scale;
   int H;
   float eps;
+  int na;            // partial vectors summed into a (0 -> 1)
+  // attention combine
+  const float* part_o;     // [heads][gch][256]
+  const float* part_ml;    // [heads][gch][2]
+  const uint32_t* params;  // params[0] = position
+  int window;              // 0 = global layer
+  int chunk_shift;         // log2 of the positions per chunk
+  int gch;                 // chunks allocated per head
 };
 bool q40_prologue_supported(int H);
 

@@ -169,7 +169,7 @@ extern "C" int e4b_k_q40_geglu_prenorm(const void* w_packed, int64_t ff, int64_t
                     (long long)ff, (long long)cols);
   if (!aligned16(w_packed)) return e4b_fail(E4B_EINVAL, "e4b_k_q40_geglu_prenorm: weight must be 16-byte aligned");
   GemvOut o = {nullptr, (uint16_t*)out_f16, nullptr, ff};
-  ProArgs p;
+  ProArgs p{};
   p.hin = h_in;
   p.hout = h_out;
   p.a = resid;
@@ -272,6 +272,7 @@ extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const fl
   a.slots = slots;
   a.window = window;
   a.chunk = chunk;
+  a.combine = true;
   a.eps = eps;
   return launch_attn(a, (hipStream_t)stream);
 }

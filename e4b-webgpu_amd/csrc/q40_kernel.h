@@ -33,200 +33,306 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
   }
 }
 
-// registers of the prologue's inputs (element i = threadIdx.x + 256 k)
-template <int PROK>
+// registers of the prologue's inputs: H = 256 PROK elements over TPB
+// threads, element i = threadIdx.x + TPB k
+template <int PROK, int TPB = 256>
 struct ProRegs {
-  float h[PROK > 0 ? PROK : 1], a[PROK > 0 ? PROK : 1], w1[PROK > 0 ? PROK : 1], w2[PROK > 0 ? PROK : 1];
+  static constexpr int N = PROK > 0 ? (256 * PROK + TPB - 1) / TPB : 1;
+  float h[N], a[N], w1[N], w2[N];
 };
 
-template <int PROK>
-DEV void pro_issue(const ProArgs& p, ProRegs<PROK>& r) {
+// sum over a block of NW waves; every thread gets the total (red: NW floats of LDS)
+template <int NW>
+DEV float block_sum_n(float v, float* red) {
+  v = wave_sum(v);
+  lds_sync();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  lds_sync();
+  float t = 0.f;
 #pragma unroll
-  for (int k = 0; k < PROK; ++k) {
-    const int i = threadIdx.x + 256 * k;
+  for (int w = 0; w < NW; ++w) t += red[w];
+  return t;
+}
+
+// NA partial vectors a[s*H + i] (s < NA) are summed into a, in order; all
+// loads are issued before any is consumed
+template <int PROK, int NA = 1, int TPB = 256>
+DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB>& r) {
+  constexpr int N = ProRegs<PROK, TPB>::N;
+  // absent vectors read hin instead (always valid) and are masked after the
+  // load, so every load issues without a branch
+  const bool has_a = p.a != nullptr, has_w2 = p.w2 != nullptr;
+  const float* a = has_a ? p.a : p.hin;
+  const float* w1 = has_a ? p.w1 : p.hin;
+  const float* w2 = has_w2 ? p.w2 : p.hin;
+  const int64_t sstride = has_a ? p.H : 0;
+  float av[NA][N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int i = threadIdx.x + TPB * k;
     r.h[k] = p.hin[i];
-    r.a[k] = p.a ? p.a[i] : 0.f;
-    r.w1[k] = p.a ? p.w1[i] : 0.f;
-    r.w2[k] = p.w2 ? p.w2[i] : 1.f;
+#pragma unroll
+    for (int s = 0; s < NA; ++s) av[s][k] = a[s * sstride + i];
+    r.w1[k] = w1[i];
+    r.w2[k] = w2[i];
   }
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    float sum = av[0][k];
+#pragma unroll
+    for (int s = 1; s < NA; ++s) sum += av[s][k];
+    r.a[k] = has_a ? sum : 0.f;
+    r.w1[k] = has_a ? r.w1[k] : 0.f;
+    r.w2[k] = has_w2 ? r.w2[k] : 1.f;
+  }
+}
+
+// attention-combine prologue of the o projection: x[h*256 + d] = f16 of the
+// log-sum-exp merge of the live split-K chunks of head h (kernels/attcomb.wgsl
+// :10-36), thread d = output dim d.  attn_issue requests, before the weight
+// tile and without waiting for the position, the (max, sum) pairs of every
+// allocated chunk (wave v: heads 2v, 2v+1, one lane per chunk) and the
+// partial outputs of the first 8 chunks of all 8 heads; attn_finish reduces
+// the pairs to normalised chunk weights e^(m_c - M) / sum_c l_c e^(m_c - M)
+// in LDS and accumulates.  Chunks past the eighth are read in a second pass.
+constexpr int kProAttn = -1;
+constexpr int kProAttnMaxCh = 64;  // chunks per head the prologue supports (one lane each)
+constexpr int kProAttnNH = kProAttnH / 256;
+static_assert(kProAttnNH == 8, "two heads per wave");
+struct AttnRegs {
+  uint32_t pos;
+  float m[2], l[2];
+  float v[kProAttnNH][8];
+};
+
+DEV void attn_issue(const ProArgs& p, AttnRegs& r) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  r.pos = p.params[0];
+  const int c = min(lane, p.gch - 1);
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const float* ml = p.part_ml + (int64_t)(2 * wv + hh) * p.gch * 2;
+    r.m[hh] = ml[2 * c];
+    r.l[hh] = ml[2 * c + 1];
+  }
+#pragma unroll
+  for (int h = 0; h < kProAttnNH; ++h)
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      r.v[h][u] = p.part_o[((int64_t)h * p.gch + min(u, p.gch - 1)) * 256 + threadIdx.x];
+}
+
+DEV void attn_finish(const ProArgs& p, AttnRegs& r, uint16_t* xs, float* wts) {
+  const int pos = (int)r.pos;
+  const int lo = (p.window > 0 && pos + 1 > p.window) ? pos + 1 - p.window : 0;
+  const int nch = (pos + 1 - lo + (1 << p.chunk_shift) - 1) >> p.chunk_shift;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const bool live = lane < nch;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const float m = live ? r.m[hh] : -3.0e38f;
+    const float M = wave_max(m);
+    const float f = live ? __expf(m - M) : 0.f;
+    const float den = wave_sum(live ? r.l[hh] * f : 0.f);
+    wts[(2 * wv + hh) * kProAttnMaxCh + lane] = f / den;
+  }
+  lds_sync();
+  float acc[kProAttnNH];
+#pragma unroll
+  for (int h = 0; h < kProAttnNH; ++h) {
+    acc[h] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u < nch) acc[h] = fmaf(r.v[h][u], wts[h * kProAttnMaxCh + u], acc[h]);
+  }
+  for (int c0 = 8; c0 < nch; c0 += 8) {
+#pragma unroll
+    for (int h = 0; h < kProAttnNH; ++h)
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        r.v[h][u] = p.part_o[((int64_t)h * p.gch + min(c0 + u, nch - 1)) * 256 + threadIdx.x];
+#pragma unroll
+    for (int h = 0; h < kProAttnNH; ++h)
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < nch) acc[h] = fmaf(r.v[h][u], wts[h * kProAttnMaxCh + c0 + u], acc[h]);
+  }
+#pragma unroll
+  for (int h = 0; h < kProAttnNH; ++h) xs[h * 256 + threadIdx.x] = f2h(acc[h]);
+  lds_sync();
 }
 
 // h = (hin + rms(a) * w1) * scale; x = w2 ? f16(rms(h) * w2) : f16(h)
 // (kernels/rmsacc3.wgsl:36-53, kernels/a4btail.wgsl:54-71,
 // kernels/rmsacc.wgsl:10-26 folded into the consumer GEMV)
-template <int PROK>
-DEV void pro_finish(const ProArgs& p, ProRegs<PROK>& r, uint16_t* xs, float* red) {
+template <int PROK, int TPB = 256>
+DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB>& r, uint16_t* xs, float* red) {
+  constexpr int N = ProRegs<PROK, TPB>::N;
+  static_assert(256 * PROK % TPB == 0, "whole elements per thread");
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < PROK; ++k) ss = fmaf(r.a[k], r.a[k], ss);
-  const float inv1 = p.a ? rms_inv(block_sum(ss, red), p.H, p.eps) : 0.f;
+  for (int k = 0; k < N; ++k) ss = fmaf(r.a[k], r.a[k], ss);
+  // both reductions run unconditionally: no branch between the weight loads
+  // and their use, so the compiler's wait counts stay exact
+  const float s1 = block_sum_n<TPB / 64>(ss, red);
+  const float inv1 = p.a ? rms_inv(s1, p.H, p.eps) : 0.f;
   float s2 = 0.f;
 #pragma unroll
-  for (int k = 0; k < PROK; ++k) {
+  for (int k = 0; k < N; ++k) {
     r.h[k] = (r.h[k] + r.a[k] * inv1 * r.w1[k]) * p.scale;
     s2 = fmaf(r.h[k], r.h[k], s2);
   }
-  const float inv2 = p.w2 ? rms_inv(block_sum(s2, red), p.H, p.eps) : 1.f;
+  const float s2t = block_sum_n<TPB / 64>(s2, red);
+  const float inv2 = p.w2 ? rms_inv(s2t, p.H, p.eps) : 1.f;
   const bool writer = p.hout && blockIdx.x == 0 && blockIdx.y == 0;
 #pragma unroll
-  for (int k = 0; k < PROK; ++k) {
-    const int i = threadIdx.x + 256 * k;
+  for (int k = 0; k < N; ++k) {
+    const int i = threadIdx.x + TPB * k;
     xs[i] = f2h(p.w2 ? r.h[k] * inv2 * r.w2[k] : r.h[k]);
     if (writer) p.hout[i] = r.h[k];
   }
-  __syncthreads();
+  lds_sync();
 }
 
 // A wave splits into G = 64/LPR lane groups; with KW = 1 a group owns R rows
-// ("slots") of a wave tile, with KW = 4 the four waves share the tile's rows
-// and each covers a quarter of the columns.  Lane l of a group covers blocks
-// jb = l + LPR*k (k < BPL) of its column range; its activation slice stays in
-// registers while the wave strides over tiles.  blockIdx.y selects one of KS
-// column slices (partial outputs, EPI_F32 only).
-template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK>
-__global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restrict__ xh,
-                                             const uint32_t* __restrict__ xl, GemvOut o, int64_t ntiles,
-                                             int nbk, ProArgs pa) {
+// ("slots") of the wave's tile, with KW = 4 the four waves share the tile's
+// rows and each covers a quarter of the columns.  Lane l of a group covers
+// blocks jb = l + LPR*k (k < BPL) of its column range.  blockIdx.y selects
+// one of KS column slices (partial outputs, EPI_F32 only).
+//
+// One tile per wave (the grid covers the matrix): all of the tile's loads are
+// issued up front, with no branch between them and their first use, so the
+// compiler's wait counts stay exact and a fused prologue computes while the
+// weight stream is in flight.
+template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __restrict__ xh,
+                                                  const uint32_t* __restrict__ xl, GemvOut o, int64_t ntiles,
+                                                  int nbk, ProArgs pa) {
   constexpr int G = 64 / LPR, SPAN = LPR / R, SLOTS = G * R;
-  constexpr int WPT = (KW == 1) ? 4 : 1;  // wave tiles per workgroup step
+  constexpr int TPB = 64 * NWV;
   static_assert(KW == 1 || KW == 4, "KW is 1 or 4");
+  static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  __shared__ __align__(16) uint16_t xs_lds[PROK ? 256 * PROK : 8];
-  __shared__ float red[4];
+  static_assert(PROK >= 0 || (PROK == kProAttn && EPI == EPI_F32 && KW == 1), "attention prologue: f32 o projection");
+  static_assert(R * BPL <= 64, "scale parity bits");
+  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK == kProAttn ? kProAttnH : 8];
+  __shared__ float red[NWV];
   __shared__ float part[KW == 4 ? 4 * SLOTS : 1];
+  __shared__ float mls[PROK == kProAttn ? (kProAttnH / 256) * kProAttnMaxCh : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
   const int kslice = blockIdx.y;
-  const int nbw = nbk / KW;                               // blocks per wave
+  const int nbw = nbk / KW;  // blocks per wave
   const int jb0 = kslice * nbk + (KW == 4 ? wave * nbw : 0);
   const int nb = W.nb;
   const int64_t units = (EPI == EPI_GEGLU) ? 2 * o.ff : W.rows;
+  const int64_t tile_id = (KW == 1) ? (int64_t)blockIdx.x * NWV + wave : (int64_t)blockIdx.x;
+  const bool live = tile_id < ntiles;                 // the last workgroup may hold idle waves
+  const int64_t tile = live ? tile_id : ntiles - 1;   // their loads repeat the last tile
+  const int64_t slot0 = tile * SLOTS + (int64_t)g * R;
 
-  ProRegs<PROK> pr;
-  if constexpr (PROK > 0) pro_issue<PROK>(pa, pr);
+  ProRegs<PROK, TPB> pr;
+  if constexpr (PROK > 0) pro_issue<PROK, NA, TPB>(pa, pr);
+  AttnRegs ar;
+  if constexpr (PROK == kProAttn) attn_issue(pa, ar);
 
-  // two register buffers of weight tiles: the loads of tile t + 2*tstep are
-  // issued as soon as tile t is consumed, so a wave always has one tile in
-  // flight while it computes the other.  Loads always issue (row and block
-  // clamped into range); slots past the end are computed on duplicate data
-  // and never stored, and blocks past the range end meet zeroed activations.
-  uint4 wq0[R][BPL], wq1[R][BPL];
-  uint16_t ws0[R][BPL], ws1[R][BPL];
-  auto load_tile = [&](int64_t tile, uint4 (&wq)[R][BPL], uint16_t (&ws)[R][BPL]) {
-    const int64_t slot0 = tile * SLOTS + (int64_t)g * R;
+  // weight tile: rows and blocks clamped into range (slots past the end are
+  // computed on duplicate data and never stored; blocks past the range end
+  // meet zeroed activations); scales as aligned pairs (ld_scale_pair)
+  uint4 wq[R][BPL];
+  uint32_t ws[R][BPL];
+  uint64_t odd = 0;  // bit r*BPL+k: the scale is the odd half of its pair
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      int64_t row;
-      if constexpr (EPI == EPI_GEGLU) {
-        const int64_t u = min(slot0 / 2 + r / 2, o.ff - 1);
-        row = (r & 1) ? o.ff + u : u;
-      } else {
-        row = min(slot0 + r, units - 1);
-      }
-      const uint4* nrow = W.nib + row * nb + jb0;
-      const uint16_t* srow = W.sc + row * nb + jb0;
-#pragma unroll
-      for (int k = 0; k < BPL; ++k) {
-        const int jb = min(l + LPR * k, nbw - 1);
-        wq[r][k] = ld_nt_u4(nrow + jb);
-        ws[r][k] = ld_nt_u16(srow + jb);
-      }
+  for (int r = 0; r < R; ++r) {
+    int64_t row;
+    if constexpr (EPI == EPI_GEGLU) {
+      const int64_t u = min(slot0 / 2 + r / 2, o.ff - 1);
+      row = (r & 1) ? o.ff + u : u;
+    } else {
+      row = min(slot0 + r, units - 1);
     }
-  };
-
-  const int64_t tile0 = (KW == 1) ? (int64_t)blockIdx.x * 4 + wave : (int64_t)blockIdx.x;
-  const int64_t tstep = (int64_t)gridDim.x * WPT;
-  if (tile0 < ntiles) load_tile(tile0, wq0, ws0);
-  if (tile0 + tstep < ntiles) load_tile(tile0 + tstep, wq1, ws1);
+#pragma unroll
+    for (int k = 0; k < BPL; ++k) {
+      const int jb = min(l + LPR * k, nbw - 1);
+      const int64_t e = row * nb + jb0 + jb;
+      wq[r][k] = ld_nt_u4(W.nib + e);
+      ws[r][k] = ld_scale_pair(W.sc, e);
+      odd |= (uint64_t)(e & 1) << (r * BPL + k);
+    }
+  }
+  // keep the scheduler from hoisting prologue math (and its waits) above
+  // the weight loads: every load of the tile is in flight before any wait
+  __builtin_amdgcn_sched_barrier(0);
 
   uint32_t xp[BPL][16];
   uint32_t xq[BPL][XLO ? 16 : 1];
   float xs8[BPL];
-  if constexpr (PROK > 0) pro_finish<PROK>(pa, pr, xs_lds, red);
+  if constexpr (PROK > 0) pro_finish<PROK, TPB>(pa, pr, xs_lds, red);
+  if constexpr (PROK == kProAttn) attn_finish(pa, ar, xs_lds, mls);
 #pragma unroll
   for (int k = 0; k < BPL; ++k) {
     const int jb = l + LPR * k;
+    const bool in = jb < nbw;
+    const int jc = in ? jb : 0;
+    if constexpr (PROK != 0) {
+      const uint4* v = reinterpret_cast<const uint4*>(xs_lds) + (size_t)(jb0 + jc) * 4;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) xp[k][i] = 0u;
-    if constexpr (XLO) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xq[k][i] = 0u;
-    }
-    xs8[k] = 0.f;
-    if (jb < nbw) {
-      if constexpr (PROK > 0) {
-        const uint4* v = reinterpret_cast<const uint4*>(xs_lds) + (size_t)(jb0 + jb) * 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint4 t = v[i];
-          xp[k][4 * i + 0] = t.x;
-          xp[k][4 * i + 1] = t.y;
-          xp[k][4 * i + 2] = t.z;
-          xp[k][4 * i + 3] = t.w;
-        }
-      } else {
-        load_x16(xh, jb0 + jb, xp[k]);
+      for (int i = 0; i < 4; ++i) {
+        const uint4 t = v[i];
+        xp[k][4 * i + 0] = t.x;
+        xp[k][4 * i + 1] = t.y;
+        xp[k][4 * i + 2] = t.z;
+        xp[k][4 * i + 3] = t.w;
       }
-      float xs = xsum16(xp[k]);
-      if constexpr (XLO) {
-        load_x16(xl, jb0 + jb, xq[k]);
-        xs += xsum16(xq[k]);
-      }
-      xs8[k] = -8.f * xs;
+    } else {
+      load_x16(xh, jb0 + jc, xp[k]);
     }
+    if constexpr (XLO) load_x16(xl, jb0 + jc, xq[k]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      xp[k][i] = in ? xp[k][i] : 0u;
+      if constexpr (XLO) xq[k][i] = in ? xq[k][i] : 0u;
+    }
+    float xs = xsum16(xp[k]);
+    if constexpr (XLO) xs += xsum16(xq[k]);
+    xs8[k] = -8.f * xs;
   }
 
-  // dot products, reduction and epilogue of one tile
-  auto finish_tile = [&](int64_t tile, const uint4 (&wq)[R][BPL], const uint16_t (&ws)[R][BPL]) {
-    const int64_t slot0 = tile * SLOTS + (int64_t)g * R;
-    float acc[R];
+  float acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      acc[r] = 0.f;
+  for (int r = 0; r < R; ++r) {
+    acc[r] = 0.f;
 #pragma unroll
-      for (int k = 0; k < BPL; ++k) {
-        float a0 = 0.f, a1 = 0.f;
-        q40_dot2(wq[r][k], xp[k], a0, a1);
-        if constexpr (XLO) q40_dot2(wq[r][k], xq[k], a0, a1);
-        acc[r] = fmaf(h2f(ws[r][k]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[k])), acc[r]);
-      }
+    for (int k = 0; k < BPL; ++k) {
+      float a0 = 0.f, a1 = 0.f;
+      q40_dot2(wq[r][k], xp[k], a0, a1);
+      if constexpr (XLO) q40_dot2(wq[r][k], xq[k], a0, a1);
+      const float d = scale_of(ws[r][k], (uint32_t)(odd >> (r * BPL + k)) & 1u);
+      acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[k])), acc[r]);
     }
-    float v = reduce_rows<LPR, R>(acc);
-    const int r = l / SPAN;  // this lane now holds slot r of the group
-    if constexpr (KW == 4) {
-      // fold the four column quarters through LDS; wave 0 finishes
-      if ((l % SPAN) == 0) part[wave * SLOTS + g * R + r] = v;
-      __syncthreads();
-      if (wave == 0) {
-        const int sl = g * R + r;
-        v = (part[sl] + part[SLOTS + sl]) + (part[2 * SLOTS + sl] + part[3 * SLOTS + sl]);
-      }
-      __syncthreads();
-      if (wave != 0) return;
-    }
-    if constexpr (EPI == EPI_GEGLU) {
-      const float up = __shfl_xor(v, SPAN, 64);
-      const int64_t u = slot0 / 2 + r / 2;
-      if ((l % (2 * SPAN)) == 0 && u < o.ff) o.yh[u] = f2h(gelu_tanh(v) * up);
-    } else {
-      const int64_t row = slot0 + r;
-      if ((l % SPAN) == 0 && row < W.rows) {
-        if constexpr (EPI == EPI_F32) o.y[(int64_t)kslice * W.rows + row] = v;
-        if constexpr (EPI == EPI_GELU_MUL) o.yh[row] = f2h(gelu_tanh(v) * o.mul[row]);
-      }
-    }
-  };
-
-  // the loop body handles two tiles so that each register buffer keeps a
-  // compile-time name (a runtime buffer index would spill to scratch)
-  for (int64_t tile = tile0; tile < ntiles; tile += 2 * tstep) {
-    finish_tile(tile, wq0, ws0);
-    if (tile + 2 * tstep < ntiles) load_tile(tile + 2 * tstep, wq0, ws0);
-    if (tile + tstep < ntiles) {
-      finish_tile(tile + tstep, wq1, ws1);
-      if (tile + 3 * tstep < ntiles) load_tile(tile + 3 * tstep, wq1, ws1);
+  }
+  float v = reduce_rows<LPR, R>(acc);
+  const int r = l / SPAN;  // this lane now holds slot r of the group
+  if constexpr (KW == 4) {
+    // fold the four column quarters through LDS; wave 0 finishes
+    if ((l % SPAN) == 0) part[wave * SLOTS + g * R + r] = v;
+    lds_sync();
+    if (wave != 0) return;
+    const int sl = g * R + r;
+    v = (part[sl] + part[SLOTS + sl]) + (part[2 * SLOTS + sl] + part[3 * SLOTS + sl]);
+  }
+  if (!live) return;
+  if constexpr (EPI == EPI_GEGLU) {
+    const float up = __shfl_xor(v, SPAN, 64);
+    const int64_t u = slot0 / 2 + r / 2;
+    if ((l % (2 * SPAN)) == 0 && u < o.ff) o.yh[u] = f2h(gelu_tanh(v) * up);
+  } else {
+    const int64_t row = slot0 + r;
+    if ((l % SPAN) == 0 && row < W.rows) {
+      if constexpr (EPI == EPI_F32) o.y[(int64_t)kslice * W.rows + row] = v;
+      if constexpr (EPI == EPI_GELU_MUL) o.yh[row] = f2h(gelu_tanh(v) * o.mul[row]);
     }
   }
 }
@@ -234,6 +340,7 @@ __global__ __launch_bounds__(256) void k_q40(Q40Mat W, const uint32_t* __restric
 // ---- launch configuration -----------------------------------------------------
 struct Cfg {
   int lpr, bpl, r, kw;
+  int nwv = 4;  // waves per workgroup
 };
 
 // lanes per row and blocks per lane that maximise lane utilisation for nbw
@@ -288,33 +395,32 @@ struct Launch {
   GemvOut o;
   int64_t units;
   int ks, nbk;
-  int max_wgs;  // grid cap; waves stride over the remaining tiles
   ProArgs pa;
   hipStream_t st;
 };
 
-template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK>
+template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4>
 void launch(const Launch& L) {
   constexpr int G = 64 / LPR;
   const int64_t ntiles = (L.units + G * R - 1) / (G * R);
-  int64_t wgs = KW == 1 ? (ntiles + 3) / 4 : ntiles;
-  if (wgs > L.max_wgs) wgs = L.max_wgs;
-  hipLaunchKernelGGL((k_q40<LPR, BPL, R, KW, XLO, EPI, PROK>), dim3((unsigned)wgs, (unsigned)L.ks), dim3(256), 0,
+  const int64_t wgs = KW == 1 ? (ntiles + NWV - 1) / NWV : ntiles;  // one tile per wave
+  hipLaunchKernelGGL((k_q40<LPR, BPL, R, KW, XLO, EPI, PROK, NA, NWV>), dim3((unsigned)wgs, (unsigned)L.ks),
+                     dim3(64 * NWV), 0,
                      L.st, L.W, L.xh, L.xl, L.o, ntiles, L.nbk, L.pa);
 }
 
-template <int LPR, int BPL, int KW, bool XLO, int EPI, int PROK>
+template <int LPR, int BPL, int KW, bool XLO, int EPI, int PROK, int NA = 1>
 bool launch_r(const Cfg& c, const Launch& L) {
   switch (c.r) {
     case 1:
       if constexpr (EPI != EPI_GEGLU) {
-        launch<LPR, BPL, 1, KW, XLO, EPI, PROK>(L);
+        launch<LPR, BPL, 1, KW, XLO, EPI, PROK, NA>(L);
         return true;
       }
       return false;
-    case 2: launch<LPR, BPL, 2, KW, XLO, EPI, PROK>(L); return true;
-    case 4: launch<LPR, BPL, 4, KW, XLO, EPI, PROK>(L); return true;
-    case 8: launch<LPR, BPL, 8, KW, XLO, EPI, PROK>(L); return true;
+    case 2: launch<LPR, BPL, 2, KW, XLO, EPI, PROK, NA>(L); return true;
+    case 4: launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA>(L); return true;
+    case 8: launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA>(L); return true;
   }
   return false;
 }
@@ -344,15 +450,30 @@ bool launch_plain(const Cfg& c, const Launch& L) {
   return false;
 }
 
-// fused prologue: H = 256 PROK, one block per lane (LPR = H / 32)
-template <int EPI>
+// attention-combine prologue: 2048 columns, one block per lane
+inline bool launch_pro_attn(const Cfg& c, const Launch& L) {
+  if (c.bpl != 1 || c.lpr != 64) return false;
+  return launch_r<64, 1, 1, false, EPI_F32, kProAttn>(c, L);
+}
+
+// fused prologue: H = 256 PROK, one block per lane (LPR = H / 32); NA
+// partial vectors in the residual input
+template <int EPI, int NA = 1>
 bool launch_pro(const Cfg& c, const Launch& L) {
   if (c.bpl != 1) return false;
+  if constexpr (EPI == EPI_GEGLU && NA == 1) {
+    if (c.nwv == 16) {
+      if (c.lpr != 64 || c.r != 8) return false;
+      launch<64, 1, 8, 1, false, EPI_GEGLU, 8, 1, 16>(L);
+      return true;
+    }
+  }
+  if (c.nwv != 4) return false;
   switch (c.lpr) {
-    case 8: return launch_r<8, 1, 1, false, EPI, 1>(c, L);
-    case 16: return launch_r<16, 1, 1, false, EPI, 2>(c, L);
-    case 32: return launch_r<32, 1, 1, false, EPI, 4>(c, L);
-    case 64: return launch_r<64, 1, 1, false, EPI, 8>(c, L);
+    case 8: return launch_r<8, 1, 1, false, EPI, 1, NA>(c, L);
+    case 16: return launch_r<16, 1, 1, false, EPI, 2, NA>(c, L);
+    case 32: return launch_r<32, 1, 1, false, EPI, 4, NA>(c, L);
+    case 64: return launch_r<64, 1, 1, false, EPI, 8, NA>(c, L);
   }
   return false;
 }

@@ -21,6 +21,7 @@ struct AttnLaunch {
   int slots;               // ring slots (sliding) or capacity (global)
   int window;              // sliding window; 0 = global layer (linear cache)
   int chunk;               // positions per split-K chunk: 32 or 64
+  bool combine;            // also launch the combine (false: the o projection's prologue merges)
   float eps;
 };
 
@@ -28,7 +29,18 @@ int launch_attn(const AttnLaunch& a, hipStream_t st);
 constexpr int kAttnMaxChunks = 512;
 // split-K chunks a layer of `max_positions` live positions needs
 int attn_chunks(int max_positions, int chunk);
-int launch_tail(float* h, const float* p, const float* w_post, float scale, const float* w_out,
+// the PLE branch of one layer (k_ple.hip)
+struct PleLaunch {
+  Q40Mat gate;              // [PD][H]
+  const uint4* proj_nib;    // projection [H][PD] stored block-transposed: [PD/32][H] nibble blocks
+  const uint16_t* proj_sc;  // [PD/32][H] block scales
+  const float* ple;         // [PD] this layer's per-layer input
+  float* part;              // [PD/32][H] partial projections (summed by the consumer)
+  int H, PD;
+};
+int launch_ple(const PleLaunch& a, const ProArgs& pa, hipStream_t st);
+// p = sum of np partial vectors (stride H)
+int launch_tail(float* h, const float* p, int np, const float* w_post, float scale, const float* w_out,
                 uint16_t* xo_hl, int H, float eps, hipStream_t st);
 // also fills rope[2 * half] = (cos, sin)(pos * inv_{local,global}[p]) for the
 // attention kernels of this step
