@@ -50,13 +50,16 @@ struct AttnArgs {
 
 // weighted head RMS over 256 dims held 4 per lane, then NeoX-half RoPE:
 // dims p < 128 (lanes 0..31) pair with p + 128 (lanes 32..63).
-DEV void prep_head(float (&x)[4], const float* w, const float* inv_freq, const float2* rope, int angles, float eps,
-                   float fpos, bool rotate) {
+// head prep on inputs that were loaded up front: x (4 dims per lane), the
+// norm weights w (use_w) and, when `have_cs`, the (cos, sin) of this lane's
+// 4 rotary dims; otherwise the angles are evaluated with sincosf
+DEV void prep_head_regs(float (&x)[4], const float (&w)[4], bool use_w, const float2 (&cs)[4], bool have_cs,
+                        const float* inv_freq, int angles, float eps, float fpos, bool rotate) {
   const int lane = threadIdx.x & 63;
   const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
   const float inv = rms_inv(ss, HD, eps);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = x[i] * inv * (w ? w[4 * lane + i] : 1.f);
+  for (int i = 0; i < 4; ++i) x[i] = x[i] * inv * (use_w ? w[i] : 1.f);
   if (!rotate) return;
   const bool hi = lane >= 32;
 #pragma unroll
@@ -66,14 +69,14 @@ DEV void prep_head(float (&x)[4], const float* w, const float* inv_freq, const f
     const float partner = hi ? a : b;
     const int p = 4 * (lane & 31) + i;
     if (p < angles) {
-      float sn, cs;
-      if (rope) {
-        cs = rope[p].x;
-        sn = rope[p].y;
+      float sn, c;
+      if (have_cs) {
+        c = cs[i].x;
+        sn = cs[i].y;
       } else {
-        sincosf(fpos * inv_freq[p], &sn, &cs);
+        sincosf(fpos * inv_freq[p], &sn, &c);
       }
-      x[i] = hi ? (partner * sn + x[i] * cs) : (x[i] * cs - partner * sn);
+      x[i] = hi ? (partner * sn + x[i] * c) : (x[i] * c - partner * sn);
     }
   }
 }
@@ -124,8 +127,18 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   };
   const int sub = lane >> 4, dl = lane & 15;
 
-  // 0. request the chunk's K and V rows (index clamped into the chunk; the
-  //    row of `pos` is not written yet and is replaced from LDS below)
+  // 0. request everything the block reads before any math: the head-prep
+  //    inputs (this wave's q/k/v row, its norm weights, the RoPE (cos, sin)
+  //    of its lane's dims; waves 6-7 repeat wave 5's row and drop it), then
+  //    the chunk's K and V rows (index clamped into the chunk; the row of
+  //    `pos` is not written yet and is replaced from LDS below)
+  const int prow = wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g;
+  const float4 xin = *reinterpret_cast<const float4*>(A.qkv + (int64_t)prow * HD + 4 * lane);
+  const float4 win = *reinterpret_cast<const float4*>((wave < 4 ? A.qw : A.kw) + 4 * lane);
+  const bool have_cs = A.rope != nullptr;
+  const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);  // any readable 1 KB
+  const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
+  const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
   uint4 kr[KS][2];
   uint2 vr[VS];
 #pragma unroll
@@ -140,17 +153,17 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
     const int j = min(NW * i + wave, m - 1);
     vr[i] = *reinterpret_cast<const uint2*>(vc + slot_at(j) * HD + 4 * lane);
   }
+  __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first wait
 
   // 1. head prep: waves 0-3 prep q heads 4g..4g+3, wave 4 the new k, wave 5
   //    the new v (f16-rounded, as stored); the chunk owning `pos` stores them
   const bool owner = pos < c_lo + m;  // the last live chunk holds pos, at j = m - 1
   if (wave < 6) {
-    const int row = wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g;
-    const float* src = A.qkv + (int64_t)row * HD + 4 * lane;
-    float x[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = src[i];
-    prep_head(x, wave < 4 ? A.qw : wave == 4 ? A.kw : nullptr, A.inv_freq, A.rope, A.angles, A.eps, fpos, wave < 5);
+    float x[4] = {xin.x, xin.y, xin.z, xin.w};
+    const float w[4] = {win.x, win.y, win.z, win.w};
+    const float2 cs[4] = {make_float2(rc0.x, rc0.y), make_float2(rc0.z, rc0.w), make_float2(rc1.x, rc1.y),
+                          make_float2(rc1.z, rc1.w)};
+    prep_head_regs(x, w, wave < 5, cs, have_cs, A.inv_freq, A.angles, A.eps, fpos, wave < 5);
     if (wave < 4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = x[i];
@@ -161,7 +174,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       if (owner) *reinterpret_cast<uint2*>((wave == 4 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
     }
   }
-  __syncthreads();
+  lds_sync();
 
   // 2. scores: 16 lanes per position (16 dims each)
   {
@@ -193,7 +206,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       if ((dl & 3) == 0 && j < m) sc[dl >> 2][j] = v;
     }
   }
-  __syncthreads();
+  lds_sync();
 
   // 3. chunk softmax statistics: wave h < 4 owns head h, lane j position j
   if (wave < GQA) {
@@ -212,7 +225,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       mlx[wave][1] = sum;
     }
   }
-  __syncthreads();
+  lds_sync();
 
   // 4. P.V: wave w takes positions j = w, w+8, ...; lane covers dims 4l..4l+3
   {
@@ -242,7 +255,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) po[wave][h][4 * lane + d] = acc[h][d];
   }
-  __syncthreads();
+  lds_sync();
 
   // 5. this chunk's partials ([head][chunk][dim], [head][chunk][max, sum])
   const int gch = gridDim.y;  // partial stride: chunks allocated per head
@@ -285,7 +298,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     den = fmaf(ml[2 * cc + 1], f, den);
   }
   den = block_sum(den, red);
-  __syncthreads();
+  lds_sync();
   const float* po = part_o + (int64_t)h * gch * HD + d;
   float acc = 0.f;
 #pragma unroll 8

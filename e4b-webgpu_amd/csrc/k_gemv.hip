@@ -68,7 +68,7 @@ DEV void amax_block(float bv, uint32_t bi, uint2* part) {
     sv[wave] = bv;
     si[wave] = bi;
   }
-  __syncthreads();
+  lds_sync();
   if (threadIdx.x == 0) {
     float v = sv[0];
     uint32_t i = si[0];
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void k_amax_final(const uint2* __restrict__ pa
     sv[wave] = v;
     si[wave] = i;
   }
-  __syncthreads();
+  lds_sync();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) amax_take(sv[0], si[0], sv[w], si[w]);
     amax[0] = si[0];
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t
   constexpr int SPAN = 64 / R;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nseg = W.nseg, nsb = nseg / 8, ngrp = nseg * 2;
+  const int nseg = W.nseg, nsb = nseg / 8;
   uint32_t xph[BPL][16], xpl[BPL][16];
   float gs[BPL][2];
 #pragma unroll
@@ -141,11 +141,13 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t
     const int64_t row0 = tile * R;
     const uint4* qa = W.qa + row0 * nseg;
     const uint2* qb = W.qb + row0 * nseg;
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(W.sc + row0 * ngrp);
-    const uint16_t* dd = W.d + row0 * nsb;
+    const uint16_t* sc16 = reinterpret_cast<const uint16_t*>(W.sc);  // int8 scale pairs, one per segment
     uint4 a[R][BPL];
     uint2 b[R][BPL];
-    uint16_t s2[R][BPL], dh[R][BPL];
+    // 16-bit scale pairs and f16 d loaded as aligned 32-bit pairs (see
+    // ld_scale_pair): no early wait on the rows' other loads
+    uint32_t s2[R][BPL], dh[R][BPL];
+    uint32_t sodd = 0, dodd = 0;
     const int rlast = (int)min((int64_t)R - 1, W.rows - 1 - row0);  // clamp the tail tile
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -153,12 +155,17 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t
       for (int k = 0; k < BPL; ++k) {
         const int s = min(lane + 64 * k, nseg - 1);  // x is zero past the row end
         const uint32_t o = (uint32_t)(min(r, rlast) * nseg + s);
+        const int64_t es = row0 * nseg + o;
+        const int64_t ed = (row0 + min(r, rlast)) * nsb + (s >> 3);
         a[r][k] = ld_nt_u4(qa + o);
         b[r][k] = ld_nt_u2(qb + o);
-        s2[r][k] = ld_nt_u16(sc + o);
-        dh[r][k] = dd[(uint32_t)(min(r, rlast) * nsb) + (s >> 3)];
+        s2[r][k] = ld_scale_pair(sc16, es);
+        dh[r][k] = ld_scale_pair(W.d, ed);
+        sodd |= (uint32_t)(es & 1) << (r * BPL + k);
+        dodd |= (uint32_t)(ed & 1) << (r * BPL + k);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -180,9 +187,10 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t
           a1 = fdot2u(p[i], xph[k][8 + i], a1);
           a1 = fdot2u(p[i], xpl[k][8 + i], a1);
         }
-        const float s0 = (float)(int8_t)(s2[r][k] & 0xff), s1 = (float)(int8_t)(s2[r][k] >> 8);
+        const uint32_t sp = s2[r][k] >> (((sodd >> (r * BPL + k)) & 1) * 16);
+        const float s0 = (float)(int8_t)(sp & 0xff), s1 = (float)(int8_t)((sp >> 8) & 0xff);
         const float t = s0 * fmaf(a0, kTwo24, gs[k][0]) + s1 * fmaf(a1, kTwo24, gs[k][1]);
-        acc[r] = fmaf(h2f(dh[r][k]), t, acc[r]);
+        acc[r] = fmaf(scale_of(dh[r][k], (dodd >> (r * BPL + k)) & 1), t, acc[r]);
       }
     }
     float v = reduce_rows<64, R>(acc);

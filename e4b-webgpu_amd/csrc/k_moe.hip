@@ -159,71 +159,87 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / GU_LPR, l = lane % GU_LPR;
-  const TopK t = select_topk(A.scores, A.pes, A.E);
-  if (blockIdx.x == 0 && wave == 0) {
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (lane == k) {
-        A.topk_idx[k] = (uint32_t)t.idx[k];
-        A.topk_w[k] = t.w[k];
-      }
-  }
   const int nb = A.H / 32;
-  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 4) {
-    const int u = (int)(2 * tile) + g;  // this group's unit
-    const bool dense = 2 * tile < A.FF2;  // wave-uniform: FF2 and FF are even
-    int slot = 0, j = u;
-    const Q40Mat& W = dense ? A.dense_gu : A.exp_gu;
-    int64_t row_g, row_u;
-    if (dense) {
-      row_g = u;
-      row_u = A.FF2 + u;
-    } else {
+  // one tile (2 units) per wave; idle waves of the last workgroup repeat the
+  // last tile and store nothing
+  const int64_t tile_id = (int64_t)blockIdx.x * 4 + wave;
+  const bool live = tile_id < ntiles;
+  const int64_t tile = live ? tile_id : ntiles - 1;
+  const int u = (int)(2 * tile) + g;    // this group's unit
+  const bool dense = 2 * tile < A.FF2;  // wave-uniform: FF2 and FF are even
+
+  // 1. the input slice of this lane's blocks (independent of the routing)
+  const uint32_t* x = reinterpret_cast<const uint32_t*>(dense ? A.xd : A.xm);
+  uint32_t xp[GU_BPL][16];
+#pragma unroll
+  for (int b = 0; b < GU_BPL; ++b) load_x16(x, min(l + GU_LPR * b, nb - 1), xp[b]);
+
+  // 2. weight rows: dense units are known now; expert units after the top-8
+  //    selection, which every expert wave redoes from the 128 scores (wave 0
+  //    of block 0 also stores it for the down kernel)
+  uint4 wq[2][GU_BPL];
+  uint32_t ws[2][GU_BPL], odd = 0;  // aligned scale pairs (ld_scale_pair)
+  auto load_rows = [&](const Q40Mat& W, int64_t row_g, int64_t row_u) {
+#pragma unroll
+    for (int b = 0; b < GU_BPL; ++b) {
+      const int jb = min(l + GU_LPR * b, nb - 1);
+      const int64_t eg = row_g * nb + jb, eu = row_u * nb + jb;
+      wq[0][b] = ld_nt_u4(W.nib + eg);
+      ws[0][b] = ld_scale_pair(W.sc, eg);
+      wq[1][b] = ld_nt_u4(W.nib + eu);
+      ws[1][b] = ld_scale_pair(W.sc, eu);
+      odd |= (uint32_t)(eg & 1) << b;
+      odd |= (uint32_t)(eu & 1) << (GU_BPL + b);
+    }
+  };
+  int slot = 0, j = u;
+  if (dense) load_rows(A.dense_gu, u, A.FF2 + u);
+  if (!dense || (blockIdx.x == 0 && wave == 0)) {
+    const TopK t = select_topk(A.scores, A.pes, A.E);
+    if (blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if (lane == k) {
+          A.topk_idx[k] = (uint32_t)t.idx[k];
+          A.topk_w[k] = t.w[k];
+        }
+    }
+    if (!dense) {
       slot = (u - A.FF2) / A.FF;
       j = (u - A.FF2) - slot * A.FF;
       int e = t.idx[0];
 #pragma unroll
       for (int k = 1; k < K; ++k)
         if (slot == k) e = t.idx[k];
-      row_g = (int64_t)e * 2 * A.FF + j;
-      row_u = row_g + A.FF;
+      const int64_t row_g = (int64_t)e * 2 * A.FF + j;
+      load_rows(A.exp_gu, row_g, row_g + A.FF);
     }
-    uint4 wq[2][GU_BPL];
-    uint16_t ws[2][GU_BPL];
+  }
+
+  // 3. dot products, GeGLU
+  float acc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int b = 0; b < GU_BPL; ++b) {
-      const int jb = min(l + GU_LPR * b, nb - 1);
-      wq[0][b] = ld_nt_u4(W.nib + row_g * nb + jb);
-      ws[0][b] = ld_nt_u16(W.sc + row_g * nb + jb);
-      wq[1][b] = ld_nt_u4(W.nib + row_u * nb + jb);
-      ws[1][b] = ld_nt_u16(W.sc + row_u * nb + jb);
+  for (int b = 0; b < GU_BPL; ++b) {
+    const bool in = l + GU_LPR * b < nb;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xp[b][i] = in ? xp[b][i] : 0u;
+    const float xs8 = -8.f * xsum16(xp[b]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float a0 = 0.f, a1 = 0.f;
+      q40_dot2(wq[r][b], xp[b], a0, a1);
+      const float d = scale_of(ws[r][b], (odd >> (r * GU_BPL + b)) & 1);
+      acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8)), acc[r]);
     }
-    const uint32_t* x = reinterpret_cast<const uint32_t*>(dense ? A.xd : A.xm);
-    float acc[2] = {0.f, 0.f};
-#pragma unroll
-    for (int b = 0; b < GU_BPL; ++b) {
-      const int jb = l + GU_LPR * b;
-      uint32_t xp[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xp[i] = 0u;
-      if (jb < nb) load_x16(x, jb, xp);
-      const float xs8 = -8.f * xsum16(xp);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        float a0 = 0.f, a1 = 0.f;
-        q40_dot2(wq[r][b], xp, a0, a1);
-        acc[r] = fmaf(h2f(ws[r][b]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8)), acc[r]);
-      }
-    }
-    const float v = reduce_rows<GU_LPR, 2>(acc);  // lanes 0..15 gate, 16..31 up
-    const float up = __shfl_xor(v, GU_LPR / 2, 64);
-    if (l == 0) {
-      const uint16_t y = f2h(gelu_tanh(v) * up);
-      if (dense)
-        A.g_dense[u] = y;
-      else
-        A.g_slots[(int64_t)slot * A.FF + j] = y;
-    }
+  }
+  const float v = reduce_rows<GU_LPR, 2>(acc);  // lanes 0..15 gate, 16..31 up
+  const float up = __shfl_xor(v, GU_LPR / 2, 64);
+  if (live && l == 0) {
+    const uint16_t y = f2h(gelu_tanh(v) * up);
+    if (dense)
+      A.g_dense[u] = y;
+    else
+      A.g_slots[(int64_t)slot * A.FF + j] = y;
   }
 }
 
@@ -258,17 +274,20 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
     for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)nbd * 4) {
       const int64_t r0 = tile * 2 * DD_R + g * DD_R;
       uint4 wq[DD_R][DD_BPL];
-      uint16_t ws[DD_R][DD_BPL];
+      uint32_t ws[DD_R][DD_BPL], odd = 0;
 #pragma unroll
       for (int r = 0; r < DD_R; ++r) {
         const int64_t row = min(r0 + r, (int64_t)A.H - 1);
 #pragma unroll
         for (int b = 0; b < DD_BPL; ++b) {
           const int jb = min(l + DD_LPR * b, nb - 1);
-          wq[r][b] = ld_nt_u4(W.nib + row * nb + jb);
-          ws[r][b] = ld_nt_u16(W.sc + row * nb + jb);
+          const int64_t e = row * nb + jb;
+          wq[r][b] = ld_nt_u4(W.nib + e);
+          ws[r][b] = ld_scale_pair(W.sc, e);
+          odd |= (uint32_t)(e & 1) << (r * DD_BPL + b);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
       float acc[DD_R];
 #pragma unroll
       for (int r = 0; r < DD_R; ++r) {
@@ -277,7 +296,8 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
         for (int b = 0; b < DD_BPL; ++b) {
           float a0 = 0.f, a1 = 0.f;
           q40_dot2(wq[r][b], xp[b], a0, a1);
-          acc[r] = fmaf(h2f(ws[r][b]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
+          const float d = scale_of(ws[r][b], (odd >> (r * DD_BPL + b)) & 1);
+          acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
         }
       }
       const float v = reduce_rows<DD_LPR, DD_R>(acc);
@@ -308,17 +328,20 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
   for (int64_t tile = (int64_t)(blockIdx.x - nbd) * 4 + wave; tile < ntiles; tile += (int64_t)nbe * 4) {
     const int64_t o0 = tile * DE_R;
     uint4 wq[DE_R][DE_BPL];
-    uint16_t ws[DE_R][DE_BPL];
+    uint32_t ws[DE_R][DE_BPL], odd = 0;
 #pragma unroll
     for (int r = 0; r < DE_R; ++r) {
       const int64_t row = (int64_t)e * A.H + min(o0 + r, (int64_t)A.H - 1);
 #pragma unroll
       for (int b = 0; b < DE_BPL; ++b) {
         const int jb = min(l + DE_LPR * b, nb - 1);
-        wq[r][b] = ld_nt_u4(W.nib + row * nb + jb);
-        ws[r][b] = ld_nt_u16(W.sc + row * nb + jb);
+        const int64_t ei = row * nb + jb;
+        wq[r][b] = ld_nt_u4(W.nib + ei);
+        ws[r][b] = ld_scale_pair(W.sc, ei);
+        odd |= (uint32_t)(ei & 1) << (r * DE_BPL + b);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
     float acc[DE_R];
 #pragma unroll
     for (int r = 0; r < DE_R; ++r) {
@@ -327,7 +350,8 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
       for (int b = 0; b < DE_BPL; ++b) {
         float a0 = 0.f, a1 = 0.f;
         q40_dot2(wq[r][b], xp[b], a0, a1);
-        acc[r] = fmaf(h2f(ws[r][b]), fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
+        const float d = scale_of(ws[r][b], (odd >> (r * DE_BPL + b)) & 1);
+        acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
       }
     }
     // lane l of slot g holds y_g of row o0 + l / 2; weight it and sum the slots
@@ -391,8 +415,8 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
   int rc = launch_moe_router(A, st);
   if (rc) return rc;
   const int64_t gu_tiles = (A.FF2 + (int64_t)K * A.FF) / 2;
-  const int64_t gu_wgs = (gu_tiles + 3) / 4;
-  hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)(gu_wgs < 2048 ? gu_wgs : 2048)), dim3(256), 0, st, A, gu_tiles);
+  const int64_t gu_wgs = (gu_tiles + 3) / 4;  // one tile per wave
+  hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)gu_wgs), dim3(256), 0, st, A, gu_tiles);
   const int dd_tiles = (A.H + 2 * DD_R - 1) / (2 * DD_R), de_tiles = (A.H + DE_R - 1) / DE_R;
   const int nbd = (dd_tiles + 3) / 4, nbe = (de_tiles + 3) / 4;
   hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A, nbd);

@@ -39,21 +39,25 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   // gate rows of this lane group, block l
   const int row0 = 32 * w + 8 * wave + g * R;
   uint4 wq[R];
-  uint16_t wsc[R];
+  uint32_t wsc[R], wodd = 0;  // aligned scale pairs (ld_scale_pair) and their half
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    wq[r] = ld_nt_u4(A.gate.nib + (int64_t)(row0 + r) * A.gate.nb + l);
-    wsc[r] = ld_nt_u16(A.gate.sc + (int64_t)(row0 + r) * A.gate.nb + l);
+    const int64_t e = (int64_t)(row0 + r) * A.gate.nb + l;
+    wq[r] = ld_nt_u4(A.gate.nib + e);
+    wsc[r] = ld_scale_pair(A.gate.sc, e);
+    wodd |= (uint32_t)(e & 1) << r;
   }
   // projection rows o = threadIdx.x + 256 i, block w (block-transposed planes)
   uint4 pq[PROK];
-  uint16_t psc[PROK];
+  uint32_t psc[PROK], podd = 0;
 #pragma unroll
   for (int i = 0; i < PROK; ++i) {
-    const int64_t o = threadIdx.x + 256 * i;
-    pq[i] = ld_nt_u4(A.proj_nib + (int64_t)w * H + o);
-    psc[i] = ld_nt_u16(A.proj_sc + (int64_t)w * H + o);
+    const int64_t e = (int64_t)w * H + threadIdx.x + 256 * i;
+    pq[i] = ld_nt_u4(A.proj_nib + e);
+    psc[i] = ld_scale_pair(A.proj_sc, e);
+    podd |= (uint32_t)(e & 1) << i;
   }
+  __builtin_amdgcn_sched_barrier(0);  // every weight load in flight before the prologue waits
   q40k::pro_finish<PROK>(pa, pr, xs, red);
 
   // gate: 32 columns of x per lane (block l), R rows per group
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
     for (int r = 0; r < R; ++r) {
       float a0 = 0.f, a1 = 0.f;
       q40_dot2(wq[r], xp, a0, a1);
-      acc[r] = h2f(wsc[r]) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8));
+      acc[r] = scale_of(wsc[r], (wodd >> r) & 1) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8));
     }
     const float vrow = reduce_rows<LPR, R>(acc);
     const int r = l / (LPR / R);
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
       gs[row - 32 * w] = f2h(gelu_tanh(vrow) * A.ple[row]);
     }
   }
-  __syncthreads();
+  lds_sync();
 
   // projection partial: part[w][o] = d_{o,w} * sum_j (n_j - 8) g_j
   {
@@ -103,7 +107,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
       float a0 = 0.f, a1 = 0.f;
       q40_dot2(pq[i], gp, a0, a1);
       A.part[(int64_t)w * H + threadIdx.x + 256 * i] =
-          h2f(psc[i]) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, gs8));
+          scale_of(psc[i], (podd >> i) & 1) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, gs8));
     }
   }
 }

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void k_feedback(const uint2* __restrict__ part
     sv[threadIdx.x >> 6] = v;
     si[threadIdx.x >> 6] = i;
   }
-  __syncthreads();
+  lds_sync();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w)
       if (sv[w] > sv[0] || (sv[w] == sv[0] && si[w] < si[0])) {
