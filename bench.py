@@ -30,6 +30,11 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 METRIC = "batch-1 decode tokens/s (E4B-shape q4_0) + achieved HBM GB/s % of peak"
 MALL_BYTES = 256 << 20
+# HBM bytes per launch of the dominant c4 kernel from two rocprofv3 counter
+# runs (FETCH_SIZE, WRITE_SIZE per dispatch, each scaled by the same counter
+# on a 256 MiB copy kernel: x2.000 and x1.000); commands and raw values in
+# profiles/geglu_dominant_traffic.md.  Re-measure when the kernel changes.
+GEGLU_TRAFFIC_BYTES = int(18616.5 * 1024 * 2.0 + 40.0 * 1024 * 1.0)
 
 
 def _cpu_cores() -> int:
@@ -273,7 +278,7 @@ def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict
                    "prefill_tokens_per_s": round(prompt_len / t_prefill, 1),
                    "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEGLU_TRAFFIC_BYTES,
                      "kernel": "k_q40 gate/up 32768x2048, residual+norm prologue, GeGLU epilogue",
                      "algorithmic_bytes_per_launch": dom["algo"], "avg_launch_us": round(dom["us"], 3)},
     }
@@ -299,6 +304,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c4"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device-to-device copy (the byte scale for rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--no-graph", action="store_true",
@@ -311,7 +318,14 @@ def main() -> int:
     fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c4": bench_c4}[a.workload]
     steps = a.steps if a.steps is not None else (240 if a.workload == "c4" else 200)
     warmup = a.warmup if a.warmup is not None else (16 if a.workload == "c4" else 20)
-    if a.workload == "c4":
+    if a.workload == "c4" and a.kernel_only:
+        from e4b.model import E4BConfig
+        dom = _time_geglu(E4BConfig(), steps)
+        print(json.dumps({"kernel": "k_q40 gate/up 32768x2048, residual+norm prologue, GeGLU epilogue",
+                          "launches": steps, "avg_launch_us": round(dom["us"], 3),
+                          "algorithmic_bytes_per_launch": dom["algo"], "gbs": round(dom["gbs"], 1)}))
+        res = None
+    elif a.workload == "c4":
         res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph)
     else:
         res = fn(steps, warmup, not a.no_cpu)
@@ -322,6 +336,8 @@ def main() -> int:
         src, dst = DeviceBuffer(n), DeviceBuffer(n)
         check(lib.e4b_memcpy_d2d(dst.ptr, src.ptr, n, None), "copy probe")
         sync()
+    if res is None:
+        return 0
     line = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(res["ms_per_step"], 6), "higher_is_better": True,
