@@ -300,4 +300,15 @@ DEV uint32_t ld_scale_pair(const uint16_t* sc, int64_t e) {
 }
 DEV float scale_of(uint32_t pair, uint32_t odd) { return h2f((uint16_t)(pair >> (odd * 16))); }
 
+// The same loads at a 32-bit offset from a uniform base: the compiler keeps
+// the base in scalar registers and spends one VGPR per address instead of
+// two, which keeps the whole tile's loads in flight without register reuse
+// (callers check that the plane is below 4 GiB).
+DEV uint4 ld_nt_u4_off(const uint4* base, uint32_t block) {
+  return ld_nt_u4(reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + block * 16u));
+}
+DEV uint32_t ld_scale_pair_off(const uint16_t* sc, uint32_t e) {
+  return ld_nt_u32(reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sc) + (e >> 1) * 4u));
+}
+
 #endif  // __HIPCC__

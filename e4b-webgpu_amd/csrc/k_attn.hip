@@ -13,7 +13,10 @@
 // positions, one 512-thread block per (KV group, chunk); the grid is sized
 // for the most live positions a layer can have and blocks past the live
 // chunks exit.  Every K and V row of a chunk is requested before the head
-// prep starts, so the chunk costs one memory round trip.
+// prep starts, so the chunk costs one memory round trip.  Inside the block
+// the split goes one level further: wave w owns positions w, w+8, ... of
+// the chunk and keeps its own softmax statistics, so scores, exponentials
+// and P.V never leave the wave; one LDS merge per block folds the 8 waves.
 //
 // Cache layout [kv_head][slot][256] f16.  Sliding layers keep a ring of
 // `slots` entries: position p lives in slot p % slots, and the live window is
@@ -90,20 +93,34 @@ DEV void unpack16(const uint4& a, const uint4& b, float* f) {
   }
 }
 
-// One block of 8 waves per (KV group g, chunk c of CS positions).
-// K is read as 16 lanes x 32 B per position (4 positions per wave, 32 per
-// block step); V as 8 B per lane (wave w takes positions w, w+8, ...).
+DEV float xmax16(float v) {
+  float t = v;
+  swapx16(v, t);
+  return fmaxf(v, t);
+}
+DEV float xmax32(float v) {
+  float t = v;
+  swapx32(v, t);
+  return fmaxf(v, t);
+}
+
+// One block of 8 waves per (KV group g, chunk c of CS positions); wave w owns
+// the chunk's positions j = w + 8k (k < CS/8).  K is read as 16 lanes per
+// position, lane dl holding dims 8dl..8dl+7 and 128+8dl..128+8dl+7 (two
+// 256-byte contiguous halves per row), 4 positions per pass (lane group
+// `sub` takes k = 4s + sub); V as 16 B per lane, lanes 0-31 one position and
+// lanes 32-63 the next (dims 8(l%32)..8(l%32)+7).
 template <int CS>
 __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   constexpr int NW = 8;
-  constexpr int KS = CS / 32;  // score steps
-  constexpr int VS = CS / 8;   // P.V positions per wave
+  constexpr int KP = CS / 32;  // score passes per wave (4 positions each)
+  constexpr int VS = CS / 8;   // positions per wave
+  constexpr int VQ = VS / 2;   // V loads per lane (two positions per load)
   __shared__ float qs[GQA][HD];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
-  __shared__ float sc[GQA][CS];
-  __shared__ float po[NW][GQA][HD];
-  __shared__ float mlx[GQA][2];
+  __shared__ __align__(16) float po[NW][GQA][HD];
+  __shared__ float wml[NW][GQA][2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = blockIdx.x, c = blockIdx.y;
   // 32-bit position arithmetic throughout (positions < 2^31): a 64-bit
@@ -126,11 +143,12 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
     return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
   };
   const int sub = lane >> 4, dl = lane & 15;
+  const int hi = lane >> 5, l32 = lane & 31;
 
   // 0. request everything the block reads before any math: the head-prep
   //    inputs (this wave's q/k/v row, its norm weights, the RoPE (cos, sin)
   //    of its lane's dims; waves 6-7 repeat wave 5's row and drop it), then
-  //    the chunk's K and V rows (index clamped into the chunk; the row of
+  //    the wave's K and V rows (index clamped into the chunk; the row of
   //    `pos` is not written yet and is replaced from LDS below)
   const int prow = wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g;
   const float4 xin = *reinterpret_cast<const float4*>(A.qkv + (int64_t)prow * HD + 4 * lane);
@@ -139,19 +157,19 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);  // any readable 1 KB
   const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
   const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
-  uint4 kr[KS][2];
-  uint2 vr[VS];
+  uint4 kr[KP][2];
+  uint4 vr[VQ];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const int j = min(32 * s + 4 * wave + sub, m - 1);
-    const uint4* p = reinterpret_cast<const uint4*>(kc + slot_at(j) * HD + 16 * dl);
-    kr[s][0] = p[0];
-    kr[s][1] = p[1];
+  for (int s = 0; s < KP; ++s) {
+    const int j = min(wave + NW * (4 * s + sub), m - 1);
+    const uint16_t* row = kc + slot_at(j) * HD;
+    kr[s][0] = *reinterpret_cast<const uint4*>(row + 8 * dl);
+    kr[s][1] = *reinterpret_cast<const uint4*>(row + 128 + 8 * dl);
   }
 #pragma unroll
-  for (int i = 0; i < VS; ++i) {
-    const int j = min(NW * i + wave, m - 1);
-    vr[i] = *reinterpret_cast<const uint2*>(vc + slot_at(j) * HD + 4 * lane);
+  for (int q = 0; q < VQ; ++q) {
+    const int j = min(wave + NW * (2 * q + hi), m - 1);
+    vr[q] = *reinterpret_cast<const uint4*>(vc + slot_at(j) * HD + 8 * l32);
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first wait
 
@@ -176,21 +194,26 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   }
   lds_sync();
 
-  // 2. scores: 16 lanes per position (16 dims each)
+  // 2. scores of the wave's positions: 16 lanes per position (16 dims each);
+  //    after the reduction lane (sub, dl) holds head dl/4 of position
+  //    k = 4s + sub
+  float sc[KP];
   {
     float q[GQA][16];
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) q[h][i] = qs[h][16 * dl + i];
+      for (int i = 0; i < 8; ++i) {
+        q[h][i] = qs[h][8 * dl + i];
+        q[h][8 + i] = qs[h][128 + 8 * dl + i];
+      }
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int j = 32 * s + 4 * wave + sub;
+    for (int s = 0; s < KP; ++s) {
+      const int j = wave + NW * (4 * s + sub);
       uint4 ka = kr[s][0], kb = kr[s][1];
       if (c_lo + j == pos) {
-        const uint4* kn = reinterpret_cast<const uint4*>(knew + 16 * dl);
-        ka = kn[0];
-        kb = kn[1];
+        ka = *reinterpret_cast<const uint4*>(knew + 8 * dl);
+        kb = *reinterpret_cast<const uint4*>(knew + 128 + 8 * dl);
       }
       float kf[16];
       unpack16(ka, kb, kf);
@@ -202,74 +225,104 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
         for (int i = 0; i < 16; ++i) a = fmaf(q[h][i], kf[i], a);
         t[h] = a;
       }
-      const float v = reduce_rows<16, GQA>(t);  // lane dl holds head dl/4
-      if ((dl & 3) == 0 && j < m) sc[dl >> 2][j] = v;
+      sc[s] = j < m ? reduce_rows<16, GQA>(t) : -3.0e38f;
     }
   }
-  lds_sync();
 
-  // 3. chunk softmax statistics: wave h < 4 owns head h, lane j position j
-  if (wave < GQA) {
-    float mx = -3.0e38f;
-    for (int j = lane; j < m; j += 64) mx = fmaxf(mx, sc[wave][j]);
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int j = lane; j < m; j += 64) {
-      const float e = __expf(sc[wave][j] - mx);
-      sc[wave][j] = e;
-      sum += e;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      mlx[wave][0] = mx;
-      mlx[wave][1] = sum;
-    }
+  // 3. the wave's softmax statistics per head (lanes with equal dl/4 share
+  //    a head): max and sum over the passes and the four lane groups
+  float mx = sc[0];
+#pragma unroll
+  for (int s = 1; s < KP; ++s) mx = fmaxf(mx, sc[s]);
+  mx = xmax32(xmax16(mx));
+  float e[KP], ls = 0.f;
+#pragma unroll
+  for (int s = 0; s < KP; ++s) {
+    e[s] = sc[s] > -1.0e38f ? __expf(sc[s] - mx) : 0.f;
+    ls += e[s];
   }
-  lds_sync();
+  ls = xsum_step<32>(xsum_step<16>(ls));
 
-  // 4. P.V: wave w takes positions j = w, w+8, ...; lane covers dims 4l..4l+3
+  // 4. P.V over the wave's positions: lane covers dims 8(l%32)..8(l%32)+7 of
+  //    position i = 2q + (l >= 32); the weight of position k = 4s + sub,
+  //    head h sits in lane 16 sub + 4h of e[s]
   {
-    float acc[GQA][4];
+    float acc[GQA][8];
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[h][i] = 0.f;
-    const uint2 vn = *reinterpret_cast<const uint2*>(vnew + 4 * lane);
+      for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
+    const uint4 vn = *reinterpret_cast<const uint4*>(vnew + 8 * l32);
 #pragma unroll
-    for (int i = 0; i < VS; ++i) {
-      const int j = NW * i + wave;
-      if (j < m) {
-        const uint2 vv = (c_lo + j == pos) ? vn : vr[i];
-        const float vf[4] = {h2f((uint16_t)(vv.x & 0xffff)), h2f((uint16_t)(vv.x >> 16)),
-                             h2f((uint16_t)(vv.y & 0xffff)), h2f((uint16_t)(vv.y >> 16))};
+    for (int q = 0; q < VQ; ++q) {
+      const int i0 = 2 * q, i1 = 2 * q + 1;
+      const int j = wave + NW * (2 * q + hi);
+      // a position past m reads a clamped, possibly stale row: zero it, so
+      // its zero weight cannot meet a non-finite value
+      const uint4 vv = (c_lo + j == pos) ? vn : (j < m ? vr[q] : make_uint4(0u, 0u, 0u, 0u));
+      float vf[8];
+      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-        for (int h = 0; h < GQA; ++h) {
-          const float pj = sc[h][j];
+      for (int t = 0; t < 4; ++t) {
+        vf[2 * t] = h2f((uint16_t)(w4[t] & 0xffff));
+        vf[2 * t + 1] = h2f((uint16_t)(w4[t] >> 16));
+      }
 #pragma unroll
-          for (int d = 0; d < 4; ++d) acc[h][d] = fmaf(pj, vf[d], acc[h][d]);
-        }
+      for (int h = 0; h < GQA; ++h) {
+        // zero for positions past m (e = 0 there), so no branch
+        const float p0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i0 >> 2]), 16 * (i0 & 3) + 4 * h));
+        const float p1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i1 >> 2]), 16 * (i1 & 3) + 4 * h));
+        const float pf = hi ? p1 : p0;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[h][d] = fmaf(pf, vf[d], acc[h][d]);
       }
     }
+    // fold the two lane halves: lanes < 32 keep heads 0, 1, lanes >= 32
+    // heads 2, 3 (each summed over both halves)
+    float r[2][8];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) r[hh][d] = tstep<32>(acc[hh][d], acc[hh + 2][d]);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float4* dst = reinterpret_cast<float4*>(&po[wave][hh + 2 * hi][8 * l32]);
+      dst[0] = make_float4(r[hh][0], r[hh][1], r[hh][2], r[hh][3]);
+      dst[1] = make_float4(r[hh][4], r[hh][5], r[hh][6], r[hh][7]);
+    }
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) po[wave][h][4 * lane + d] = acc[h][d];
+      if (lane == 4 * h) {
+        wml[wave][h][0] = mx;
+        wml[wave][h][1] = ls;
+      }
   }
   lds_sync();
 
-  // 5. this chunk's partials ([head][chunk][dim], [head][chunk][max, sum])
-  const int gch = gridDim.y;  // partial stride: chunks allocated per head
-  for (int i = threadIdx.x; i < GQA * HD; i += NW * 64) {
-    const int h = i / HD, d = i % HD;
-    float v = 0.f;
+  // 5. fold the 8 waves (log-sum-exp) into this chunk's partials
+  //    ([head][chunk][dim], [head][chunk][max, sum]); thread t: head t/128,
+  //    dims 2(t%128), 2(t%128)+1
+  {
+    const int gch = gridDim.y;  // partial stride: chunks allocated per head
+    const int h = threadIdx.x >> 7, d = 2 * (threadIdx.x & 127);
+    float M = wml[0][h][0];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) v += po[w][h][d];
-    A.part_o[((int64_t)(g * GQA + h) * gch + c) * HD + d] = v;
-  }
-  if (threadIdx.x < GQA) {
-    const int64_t pi = ((int64_t)(g * GQA + threadIdx.x) * gch + c) * 2;
-    A.part_ml[pi] = mlx[threadIdx.x][0];
-    A.part_ml[pi + 1] = mlx[threadIdx.x][1];
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, wml[w][h][0]);
+    float v0 = 0.f, v1 = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = __expf(wml[w][h][0] - M);  // 0 for a wave without positions
+      const float2 pv = *reinterpret_cast<const float2*>(&po[w][h][d]);
+      v0 = fmaf(pv.x, f, v0);
+      v1 = fmaf(pv.y, f, v1);
+      L = fmaf(wml[w][h][1], f, L);
+    }
+    const int64_t base = (int64_t)(g * GQA + h) * gch + c;
+    *reinterpret_cast<float2*>(A.part_o + base * HD + d) = make_float2(v0, v1);
+    if (d == 0) {
+      A.part_ml[base * 2] = M;
+      A.part_ml[base * 2 + 1] = L;
+    }
   }
 }
 

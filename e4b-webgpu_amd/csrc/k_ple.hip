@@ -42,9 +42,9 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   uint32_t wsc[R], wodd = 0;  // aligned scale pairs (ld_scale_pair) and their half
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t e = (int64_t)(row0 + r) * A.gate.nb + l;
-    wq[r] = ld_nt_u4(A.gate.nib + e);
-    wsc[r] = ld_scale_pair(A.gate.sc, e);
+    const uint32_t e = (uint32_t)(row0 + r) * (uint32_t)A.gate.nb + l;
+    wq[r] = ld_nt_u4_off(A.gate.nib, e);
+    wsc[r] = ld_scale_pair_off(A.gate.sc, e);
     wodd |= (uint32_t)(e & 1) << r;
   }
   // projection rows o = threadIdx.x + 256 i, block w (block-transposed planes)
@@ -52,12 +52,15 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   uint32_t psc[PROK], podd = 0;
 #pragma unroll
   for (int i = 0; i < PROK; ++i) {
-    const int64_t e = (int64_t)w * H + threadIdx.x + 256 * i;
-    pq[i] = ld_nt_u4(A.proj_nib + e);
-    psc[i] = ld_scale_pair(A.proj_sc, e);
+    const uint32_t e = (uint32_t)(w * H) + threadIdx.x + 256 * i;
+    pq[i] = ld_nt_u4_off(A.proj_nib, e);
+    psc[i] = ld_scale_pair_off(A.proj_sc, e);
     podd |= (uint32_t)(e & 1) << i;
   }
-  __builtin_amdgcn_sched_barrier(0);  // every weight load in flight before the prologue waits
+  // the per-layer input of the gate row this lane finishes (lanes that finish
+  // no row load a valid neighbour and drop it)
+  const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
+  __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
   q40k::pro_finish<PROK>(pa, pr, xs, red);
 
   // gate: 32 columns of x per lane (block l), R rows per group
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
     const int r = l / (LPR / R);
     if ((l % (LPR / R)) == 0) {
       const int row = row0 + r;
-      gs[row - 32 * w] = f2h(gelu_tanh(vrow) * A.ple[row]);
+      gs[row - 32 * w] = f2h(gelu_tanh(vrow) * ple_v);
     }
   }
   lds_sync();

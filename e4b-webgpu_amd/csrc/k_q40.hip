@@ -17,6 +17,9 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
   if (epi == EPI_GEGLU && (o.ff < 1 || 2 * o.ff != W.rows))
     return e4b_fail(E4B_EINVAL, "q4_0 GEMV: GeGLU needs 2*ff rows (rows=%lld ff=%lld)", (long long)W.rows,
                     (long long)o.ff);
+  if ((uint64_t)W.rows * (uint64_t)W.nb * 16u > 0xffffffffull)
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: a %lld x %d-block matrix exceeds the 4 GiB plane limit", (long long)W.rows,
+                    W.nb);
   const int nbk = W.nb / ks;
   if (nbk < 1) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: empty row");
   if (pro && pro->part_o) {

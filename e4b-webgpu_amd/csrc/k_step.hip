@@ -19,42 +19,51 @@ constexpr int kMaxPer = 16;  // elements per thread in the one-block kernels (H 
 // h = (h + rms(p) * w_post) * scale; xo = rms(h) * w_out stored as an exact
 // f16 hi/lo split for the lm-head (kernels/a4btail.wgsl:26-71 with the
 // reference's f32 final norm, src/engine-a4b.js:688).
-template <int NP>
+template <int NP, int PER>
 __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float* __restrict__ p,
                                               const float* __restrict__ w_post, float scale,
                                               const float* __restrict__ w_out, uint16_t* __restrict__ xo_hl, int H,
                                               float eps) {
   __shared__ float red[4];
-  float hv[kMaxPer];
-  float pv[kMaxPer];
+  float hv[PER];
+  float pv[PER];
+  float wp[PER], wo[PER];
+  // every input is requested before the first reduction waits
+  float pp[PER][NP];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = min((int)threadIdx.x + 256 * k, H - 1);
+#pragma unroll
+    for (int s = 0; s < NP; ++s) pp[k][s] = p[(int64_t)s * H + i];
+    hv[k] = h[i];
+    wp[k] = w_post[i];
+    wo[k] = w_out[i];
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMaxPer; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    float pp[NP];
+  for (int k = 0; k < PER; ++k) {
+    const bool in = (int)threadIdx.x + 256 * k < H;
+    float v = pp[k][0];
 #pragma unroll
-    for (int s = 0; s < NP; ++s) pp[s] = i < H ? p[(int64_t)s * H + i] : 0.f;
-    float v = pp[0];
-#pragma unroll
-    for (int s = 1; s < NP; ++s) v += pp[s];
-    pv[k] = v;
-    ss = fmaf(v, v, ss);
+    for (int s = 1; s < NP; ++s) v += pp[k][s];
+    pv[k] = in ? v : 0.f;
+    ss = fmaf(pv[k], pv[k], ss);
   }
   const float inv = rms_inv(block_sum(ss, red), H, eps);
   float s2 = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMaxPer; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    hv[k] = i < H ? (h[i] + pv[k] * inv * w_post[i]) * scale : 0.f;
+  for (int k = 0; k < PER; ++k) {
+    const bool in = (int)threadIdx.x + 256 * k < H;
+    hv[k] = in ? (hv[k] + pv[k] * inv * wp[k]) * scale : 0.f;
     s2 = fmaf(hv[k], hv[k], s2);
   }
   const float inv2 = rms_inv(block_sum(s2, red), H, eps);
 #pragma unroll
-  for (int k = 0; k < kMaxPer; ++k) {
+  for (int k = 0; k < PER; ++k) {
     const int i = threadIdx.x + 256 * k;
     if (i < H) {
       h[i] = hv[k];
-      const float y = hv[k] * inv2 * w_out[i];
+      const float y = hv[k] * inv2 * wo[k];
       const _Float16 hi = (_Float16)y;
       xo_hl[i] = __builtin_bit_cast(uint16_t, hi);
       xo_hl[H + i] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)hi));
@@ -156,14 +165,17 @@ __global__ __launch_bounds__(256) void k_ple_prep(const float* __restrict__ proj
     }
     return;
   }
+  // the projection value and norm weight load while the token chain
+  // (position -> token -> table row) resolves; the reduction waits last
+  const float pv = proj[b * 256 + t] * proj_scale;
+  const float wn = w_pn[t];
   const uint32_t pos = params[0];
   uint32_t tok = pos < params[3] ? prompt[pos] : params[1];
   if (tok >= (uint32_t)vocab) tok = 0;
-  const float pv = proj[b * 256 + t] * proj_scale;
-  const float inv = rms_inv(block_sum(pv * pv, red), 256, eps);
   const uint8_t* blk = table + ((int64_t)tok * L + b) * 210;
   const float idv = q6k_elem(blk, t) * 16.0f;  // sqrt(PD), PD = 256
-  ple[b * 256 + t] = (pv * inv * w_pn[t] + idv) * 0.70710678118654752f;
+  const float inv = rms_inv(block_sum(pv * pv, red), 256, eps);
+  ple[b * 256 + t] = (pv * inv * wn + idv) * 0.70710678118654752f;
 }
 
 // argmax fold of the lm-head partials + GPU-side greedy feedback: the token
@@ -218,13 +230,30 @@ __global__ __launch_bounds__(256) void k_feedback(const uint2* __restrict__ part
 }  // namespace
 
 // ---- launchers --------------------------------------------------------------
+template <int NP>
+static void launch_tail_np(float* h, const float* p, const float* w_post, float scale, const float* w_out,
+                           uint16_t* xo_hl, int H, float eps, hipStream_t st) {
+  // elements per thread: the smallest power of two covering H over 256 threads
+  if (H <= 256)
+    hipLaunchKernelGGL((k_tail<NP, 1>), dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+  else if (H <= 512)
+    hipLaunchKernelGGL((k_tail<NP, 2>), dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+  else if (H <= 1024)
+    hipLaunchKernelGGL((k_tail<NP, 4>), dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+  else if (H <= 2048)
+    hipLaunchKernelGGL((k_tail<NP, 8>), dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+  else
+    hipLaunchKernelGGL((k_tail<NP, kMaxPer>), dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+}
+
 int launch_tail(float* h, const float* p, int np, const float* w_post, float scale, const float* w_out,
                 uint16_t* xo_hl, int H, float eps, hipStream_t st) {
   if (np != 1 && np != kMaxPartials) return e4b_fail(E4B_EINVAL, "tail: %d partial vectors (1 or %d)", np, kMaxPartials);
+  if (H < 1 || H > 256 * kMaxPer) return e4b_fail(E4B_EINVAL, "tail: hidden %d outside 1..%d", H, 256 * kMaxPer);
   if (np == 1)
-    hipLaunchKernelGGL(k_tail<1>, dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+    launch_tail_np<1>(h, p, w_post, scale, w_out, xo_hl, H, eps, st);
   else
-    hipLaunchKernelGGL(k_tail<kMaxPartials>, dim3(1), dim3(256), 0, st, h, p, w_post, scale, w_out, xo_hl, H, eps);
+    launch_tail_np<kMaxPartials>(h, p, w_post, scale, w_out, xo_hl, H, eps, st);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -34,12 +34,37 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
 }
 
 // registers of the prologue's inputs: H = 256 PROK elements over TPB
-// threads, element i = threadIdx.x + TPB k
-template <int PROK, int TPB = 256>
+// threads, thread t owning the N contiguous elements [N t, N t + N) so that
+// each vector costs N/4 16-byte loads per thread (a wave can have at most 63
+// loads outstanding; dword loads of 11 vectors would exceed that); NA
+// partial vectors of a
+template <int PROK, int TPB = 256, int NA = 1>
 struct ProRegs {
-  static constexpr int N = PROK > 0 ? (256 * PROK + TPB - 1) / TPB : 1;
-  float h[N], a[N], w1[N], w2[N];
+  static constexpr int N = PROK > 0 ? 256 * PROK / TPB : 1;
+  static_assert(PROK <= 0 || (256 * PROK % TPB == 0 && (N == 1 || N == 2 || N % 4 == 0)), "elements per thread");
+  float h[N], a[NA][N], w1[N], w2[N];
 };
+
+// N contiguous floats at p (aligned to min(N, 4) floats) with the widest loads
+template <int N>
+DEV void ld_floats(const float* p, float (&v)[N]) {
+  if constexpr (N == 1) {
+    v[0] = p[0];
+  } else if constexpr (N == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+  } else {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const float4 t = reinterpret_cast<const float4*>(p)[q];
+      v[4 * q] = t.x;
+      v[4 * q + 1] = t.y;
+      v[4 * q + 2] = t.z;
+      v[4 * q + 3] = t.w;
+    }
+  }
+}
 
 // sum over a block of NW waves; every thread gets the total (red: NW floats of LDS)
 template <int NW>
@@ -54,11 +79,12 @@ DEV float block_sum_n(float v, float* red) {
   return t;
 }
 
-// NA partial vectors a[s*H + i] (s < NA) are summed into a, in order; all
-// loads are issued before any is consumed
+// NA partial vectors a[s*H + i] (s < NA) are summed into a, in order, by
+// pro_finish; pro_issue only issues the loads, so nothing between them and
+// the weight loads waits for memory
 template <int PROK, int NA = 1, int TPB = 256>
-DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB>& r) {
-  constexpr int N = ProRegs<PROK, TPB>::N;
+DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB, NA>& r) {
+  constexpr int N = ProRegs<PROK, TPB, NA>::N;
   // absent vectors read hin instead (always valid) and are masked after the
   // load, so every load issues without a branch
   const bool has_a = p.a != nullptr, has_w2 = p.w2 != nullptr;
@@ -66,25 +92,12 @@ DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB>& r) {
   const float* w1 = has_a ? p.w1 : p.hin;
   const float* w2 = has_w2 ? p.w2 : p.hin;
   const int64_t sstride = has_a ? p.H : 0;
-  float av[NA][N];
+  const int i0 = threadIdx.x * N;
+  ld_floats<N>(p.hin + i0, r.h);
 #pragma unroll
-  for (int k = 0; k < N; ++k) {
-    const int i = threadIdx.x + TPB * k;
-    r.h[k] = p.hin[i];
-#pragma unroll
-    for (int s = 0; s < NA; ++s) av[s][k] = a[s * sstride + i];
-    r.w1[k] = w1[i];
-    r.w2[k] = w2[i];
-  }
-#pragma unroll
-  for (int k = 0; k < N; ++k) {
-    float sum = av[0][k];
-#pragma unroll
-    for (int s = 1; s < NA; ++s) sum += av[s][k];
-    r.a[k] = has_a ? sum : 0.f;
-    r.w1[k] = has_a ? r.w1[k] : 0.f;
-    r.w2[k] = has_w2 ? r.w2[k] : 1.f;
-  }
+  for (int s = 0; s < NA; ++s) ld_floats<N>(a + s * sstride + i0, r.a[s]);
+  ld_floats<N>(w1 + i0, r.w1);
+  ld_floats<N>(w2 + i0, r.w2);
 }
 
 // attention-combine prologue of the o projection: x[h*256 + d] = f16 of the
@@ -92,20 +105,26 @@ DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB>& r) {
 // :10-36), thread d = output dim d.  attn_issue requests, before the weight
 // tile and without waiting for the position, the (max, sum) pairs of every
 // allocated chunk (wave v: heads 2v, 2v+1, one lane per chunk) and the
-// partial outputs of the first 8 chunks of all 8 heads; attn_finish reduces
+// partial outputs of the first U chunks of all 8 heads; attn_finish reduces
 // the pairs to normalised chunk weights e^(m_c - M) / sum_c l_c e^(m_c - M)
-// in LDS and accumulates.  Chunks past the eighth are read in a second pass.
+// in LDS and accumulates.  Chunks past the first U are read 8 at a time in
+// further passes (U = kProAttnFirst).
 constexpr int kProAttn = -1;
+constexpr int kProAttnFirst = 8;
 constexpr int kProAttnMaxCh = 64;  // chunks per head the prologue supports (one lane each)
 constexpr int kProAttnNH = kProAttnH / 256;
 static_assert(kProAttnNH == 8, "two heads per wave");
+// thread t merges head t/32, dims 8 (t % 32) .. 8 (t % 32) + 7 (two 16-byte
+// loads per chunk)
+template <int U>
 struct AttnRegs {
   uint32_t pos;
   float m[2], l[2];
-  float v[kProAttnNH][8];
+  float v[U][8];
 };
 
-DEV void attn_issue(const ProArgs& p, AttnRegs& r) {
+template <int U>
+DEV void attn_issue(const ProArgs& p, AttnRegs<U>& r) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   r.pos = p.params[0];
   const int c = min(lane, p.gch - 1);
@@ -115,14 +134,13 @@ DEV void attn_issue(const ProArgs& p, AttnRegs& r) {
     r.m[hh] = ml[2 * c];
     r.l[hh] = ml[2 * c + 1];
   }
+  const int h = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 8;
 #pragma unroll
-  for (int h = 0; h < kProAttnNH; ++h)
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      r.v[h][u] = p.part_o[((int64_t)h * p.gch + min(u, p.gch - 1)) * 256 + threadIdx.x];
+  for (int u = 0; u < U; ++u) ld_floats<8>(p.part_o + ((int64_t)h * p.gch + min(u, p.gch - 1)) * 256 + d0, r.v[u]);
 }
 
-DEV void attn_finish(const ProArgs& p, AttnRegs& r, uint16_t* xs, float* wts) {
+template <int U>
+DEV void attn_finish(const ProArgs& p, AttnRegs<U>& r, uint16_t* xs, float* wts) {
   const int pos = (int)r.pos;
   const int lo = (p.window > 0 && pos + 1 > p.window) ? pos + 1 - p.window : 0;
   const int nch = (pos + 1 - lo + (1 << p.chunk_shift) - 1) >> p.chunk_shift;
@@ -137,41 +155,60 @@ DEV void attn_finish(const ProArgs& p, AttnRegs& r, uint16_t* xs, float* wts) {
     wts[(2 * wv + hh) * kProAttnMaxCh + lane] = f / den;
   }
   lds_sync();
-  float acc[kProAttnNH];
+  const int h = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 8;
+  const float* wh = wts + h * kProAttnMaxCh;
+  float acc[8];
 #pragma unroll
-  for (int h = 0; h < kProAttnNH; ++h) {
-    acc[h] = 0.f;
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (u < nch) acc[h] = fmaf(r.v[h][u], wts[h * kProAttnMaxCh + u], acc[h]);
+  for (int u = 0; u < U; ++u) {
+    if (u < nch) {  // chunks past the live ones may hold stale or unwritten values
+      const float wu = wh[u];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(r.v[u][j], wu, acc[j]);
+    }
   }
-  for (int c0 = 8; c0 < nch; c0 += 8) {
+  for (int c0 = U; c0 < nch; c0 += U) {
 #pragma unroll
-    for (int h = 0; h < kProAttnNH; ++h)
+    for (int u = 0; u < U; ++u)
+      ld_floats<8>(p.part_o + ((int64_t)h * p.gch + min(c0 + u, nch - 1)) * 256 + d0, r.v[u]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        r.v[h][u] = p.part_o[((int64_t)h * p.gch + min(c0 + u, nch - 1)) * 256 + threadIdx.x];
+    for (int u = 0; u < U; ++u) {
+      if (c0 + u < nch) {
+        const float wu = wh[c0 + u];
 #pragma unroll
-    for (int h = 0; h < kProAttnNH; ++h)
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (c0 + u < nch) acc[h] = fmaf(r.v[h][u], wts[h * kProAttnMaxCh + c0 + u], acc[h]);
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(r.v[u][j], wu, acc[j]);
+      }
+    }
   }
+  uint32_t pk[4];
 #pragma unroll
-  for (int h = 0; h < kProAttnNH; ++h) xs[h * 256 + threadIdx.x] = f2h(acc[h]);
+  for (int j = 0; j < 4; ++j) pk[j] = (uint32_t)f2h(acc[2 * j]) | ((uint32_t)f2h(acc[2 * j + 1]) << 16);
+  *reinterpret_cast<uint4*>(xs + h * 256 + d0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
   lds_sync();
 }
 
 // h = (hin + rms(a) * w1) * scale; x = w2 ? f16(rms(h) * w2) : f16(h)
 // (kernels/rmsacc3.wgsl:36-53, kernels/a4btail.wgsl:54-71,
 // kernels/rmsacc.wgsl:10-26 folded into the consumer GEMV)
-template <int PROK, int TPB = 256>
-DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB>& r, uint16_t* xs, float* red) {
-  constexpr int N = ProRegs<PROK, TPB>::N;
+template <int PROK, int TPB = 256, int NA = 1>
+DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, float* red) {
+  constexpr int N = ProRegs<PROK, TPB, NA>::N;
   static_assert(256 * PROK % TPB == 0, "whole elements per thread");
+  const bool has_a = p.a != nullptr, has_w2 = p.w2 != nullptr;
+  float av[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    float sum = r.a[0][k];
+#pragma unroll
+    for (int s = 1; s < NA; ++s) sum += r.a[s][k];
+    av[k] = has_a ? sum : 0.f;
+    r.w1[k] = has_a ? r.w1[k] : 0.f;
+    r.w2[k] = has_w2 ? r.w2[k] : 1.f;
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < N; ++k) ss = fmaf(r.a[k], r.a[k], ss);
+  for (int k = 0; k < N; ++k) ss = fmaf(av[k], av[k], ss);
   // both reductions run unconditionally: no branch between the weight loads
   // and their use, so the compiler's wait counts stay exact
   const float s1 = block_sum_n<TPB / 64>(ss, red);
@@ -179,17 +216,17 @@ DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB>& r, uint16_t* xs, float
   float s2 = 0.f;
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    r.h[k] = (r.h[k] + r.a[k] * inv1 * r.w1[k]) * p.scale;
+    r.h[k] = (r.h[k] + av[k] * inv1 * r.w1[k]) * p.scale;
     s2 = fmaf(r.h[k], r.h[k], s2);
   }
   const float s2t = block_sum_n<TPB / 64>(s2, red);
   const float inv2 = p.w2 ? rms_inv(s2t, p.H, p.eps) : 1.f;
   const bool writer = p.hout && blockIdx.x == 0 && blockIdx.y == 0;
+  const int i0 = threadIdx.x * N;
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    const int i = threadIdx.x + TPB * k;
-    xs[i] = f2h(p.w2 ? r.h[k] * inv2 * r.w2[k] : r.h[k]);
-    if (writer) p.hout[i] = r.h[k];
+    xs[i0 + k] = f2h(p.w2 ? r.h[k] * inv2 * r.w2[k] : r.h[k]);
+    if (writer) p.hout[i0 + k] = r.h[k];
   }
   lds_sync();
 }
@@ -214,12 +251,13 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  static_assert(PROK >= 0 || (PROK == kProAttn && EPI == EPI_F32 && KW == 1), "attention prologue: f32 o projection");
+  static_assert(PROK >= kProAttn, "prologue kind");
+  static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1), "attention prologue: f32 o projection");
   static_assert(R * BPL <= 64, "scale parity bits");
-  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK == kProAttn ? kProAttnH : 8];
+  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK < 0 ? kProAttnH : 8];
   __shared__ float red[NWV];
   __shared__ float part[KW == 4 ? 4 * SLOTS : 1];
-  __shared__ float mls[PROK == kProAttn ? (kProAttnH / 256) * kProAttnMaxCh : 1];
+  __shared__ float mls[PROK < 0 ? (kProAttnH / 256) * kProAttnMaxCh : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
@@ -233,10 +271,10 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   const int64_t tile = live ? tile_id : ntiles - 1;   // their loads repeat the last tile
   const int64_t slot0 = tile * SLOTS + (int64_t)g * R;
 
-  ProRegs<PROK, TPB> pr;
+  ProRegs<PROK, TPB, NA> pr;
   if constexpr (PROK > 0) pro_issue<PROK, NA, TPB>(pa, pr);
-  AttnRegs ar;
-  if constexpr (PROK == kProAttn) attn_issue(pa, ar);
+  AttnRegs<kProAttnFirst> ar;
+  if constexpr (PROK < 0) attn_issue(pa, ar);
 
   // weight tile: rows and blocks clamped into range (slots past the end are
   // computed on duplicate data and never stored; blocks past the range end
@@ -256,9 +294,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
 #pragma unroll
     for (int k = 0; k < BPL; ++k) {
       const int jb = min(l + LPR * k, nbw - 1);
-      const int64_t e = row * nb + jb0 + jb;
-      wq[r][k] = ld_nt_u4(W.nib + e);
-      ws[r][k] = ld_scale_pair(W.sc, e);
+      const uint32_t e = (uint32_t)row * (uint32_t)nb + (uint32_t)(jb0 + jb);  // planes < 4 GiB (host check)
+      wq[r][k] = ld_nt_u4_off(W.nib, e);
+      ws[r][k] = ld_scale_pair_off(W.sc, e);
       odd |= (uint64_t)(e & 1) << (r * BPL + k);
     }
   }
@@ -269,8 +307,8 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   uint32_t xp[BPL][16];
   uint32_t xq[BPL][XLO ? 16 : 1];
   float xs8[BPL];
-  if constexpr (PROK > 0) pro_finish<PROK, TPB>(pa, pr, xs_lds, red);
-  if constexpr (PROK == kProAttn) attn_finish(pa, ar, xs_lds, mls);
+  if constexpr (PROK > 0) pro_finish<PROK, TPB, NA>(pa, pr, xs_lds, red);
+  if constexpr (PROK < 0) attn_finish(pa, ar, xs_lds, mls);
 #pragma unroll
   for (int k = 0; k < BPL; ++k) {
     const int jb = l + LPR * k;
@@ -450,7 +488,10 @@ bool launch_plain(const Cfg& c, const Launch& L) {
   return false;
 }
 
-// attention-combine prologue: 2048 columns, one block per lane
+// attention-combine prologue: 2048 columns, one block per lane.  (Reading 16
+// chunks up front for layers that allocate more than 8 measured slower than
+// a second pass: the loads cannot be trimmed to the live chunks without
+// waiting for the position first.)
 inline bool launch_pro_attn(const Cfg& c, const Launch& L) {
   if (c.bpl != 1 || c.lpr != 64) return false;
   return launch_r<64, 1, 1, false, EPI_F32, kProAttn>(c, L);
