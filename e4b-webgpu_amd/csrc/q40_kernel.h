@@ -300,6 +300,10 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
       odd |= (uint64_t)(e & 1) << (r * BPL + k);
     }
   }
+  // the epilogue multiplier of the row this lane finishes (lanes that finish
+  // no row read a valid neighbour), requested with the tile
+  float mulv = 0.f;
+  if constexpr (EPI == EPI_GELU_MUL) mulv = o.mul[min(slot0 + l / SPAN, units - 1)];
   // keep the scheduler from hoisting prologue math (and its waits) above
   // the weight loads: every load of the tile is in flight before any wait
   __builtin_amdgcn_sched_barrier(0);
@@ -370,7 +374,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
     const int64_t row = slot0 + r;
     if ((l % SPAN) == 0 && row < W.rows) {
       if constexpr (EPI == EPI_F32) o.y[(int64_t)kslice * W.rows + row] = v;
-      if constexpr (EPI == EPI_GELU_MUL) o.yh[row] = f2h(gelu_tanh(v) * o.mul[row]);
+      if constexpr (EPI == EPI_GELU_MUL) o.yh[row] = f2h(gelu_tanh(v) * mulv);
     }
   }
 }
@@ -412,13 +416,18 @@ inline Cfg pick(int nbk, int64_t units, int epi, bool pro) {
   c.kw = (!pro && nbk >= 256 && nbk % 4 == 0) ? 4 : 1;
   pick_lanes(nbk / c.kw, &c.lpr, &c.bpl, c.kw == 4);
   const int G = 64 / c.lpr;
-  int r = c.bpl == 1 ? 8 : c.bpl == 2 ? (c.kw == 4 ? 8 : 4) : c.bpl <= 4 ? 2 : 1;
+  int r = c.bpl == 1 ? 8 : c.bpl == 2 ? 4 : c.bpl <= 4 ? 2 : 1;
+  // the fused-prologue GeGLU reads the prologue's four vectors once per
+  // workgroup: 16 rows per wave halve that on-chip traffic (measured
+  // fastest at the E4B shape, 512 workgroups)
+  if (pro && epi == EPI_GEGLU && c.lpr == 64 && c.bpl == 1 && c.kw == 1 && units >= 16 * 4 * 256) r = 16;
   if (r > c.lpr) r = c.lpr;
   const int rmin = (epi == EPI_GEGLU) ? 2 : 1;
   const int per_wg = (c.kw == 1 ? 4 : 1) * G;
   // measured on MI355X at the E4B shapes: 256 workgroups (128 with the fused
-  // prologue, which every workgroup repeats) keep enough loads in flight
-  const int64_t min_wgs = pro ? 128 : 256;
+  // prologue, which every workgroup repeats; 512 for the column-split down
+  // projection) keep enough loads in flight
+  const int64_t min_wgs = pro ? 128 : c.kw == 4 ? 512 : 256;
   while (r > rmin && (units + per_wg * r - 1) / (per_wg * r) < min_wgs) r >>= 1;
   if (r < rmin) r = rmin;
   c.r = r;
@@ -459,6 +468,12 @@ bool launch_r(const Cfg& c, const Launch& L) {
     case 2: launch<LPR, BPL, 2, KW, XLO, EPI, PROK, NA>(L); return true;
     case 4: launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA>(L); return true;
     case 8: launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA>(L); return true;
+    case 16:
+      if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0) {
+        launch<LPR, BPL, 16, KW, XLO, EPI, PROK, NA>(L);
+        return true;
+      }
+      return false;
   }
   return false;
 }
@@ -501,15 +516,7 @@ inline bool launch_pro_attn(const Cfg& c, const Launch& L) {
 // partial vectors in the residual input
 template <int EPI, int NA = 1>
 bool launch_pro(const Cfg& c, const Launch& L) {
-  if (c.bpl != 1) return false;
-  if constexpr (EPI == EPI_GEGLU && NA == 1) {
-    if (c.nwv == 16) {
-      if (c.lpr != 64 || c.r != 8) return false;
-      launch<64, 1, 8, 1, false, EPI_GEGLU, 8, 1, 16>(L);
-      return true;
-    }
-  }
-  if (c.nwv != 4) return false;
+  if (c.bpl != 1 || c.nwv != 4) return false;
   switch (c.lpr) {
     case 8: return launch_r<8, 1, 1, false, EPI, 1, NA>(c, L);
     case 16: return launch_r<16, 1, 1, false, EPI, 2, NA>(c, L);
