@@ -3,14 +3,17 @@
 // GEMV; kernels/plegatemv.wgsl:20-60 for the gate).
 //
 // The projection's input has PD = 256 elements = 8 q4_0 blocks, so the
-// branch splits into 8 workgroups by projection block: workgroup w computes
-// gate rows [32w, 32w+32) (after the fused post-FFN residual prologue, which
-// every workgroup repeats), keeps the 32 gated values in LDS, and multiplies
-// them with block w of every projection row.  It writes the partial
-// projection part[w][0..H); the consumer (the next layer's qkv prologue or
-// the step tail) adds the 8 partials in a fixed order.  The projection
-// weights are stored block-transposed ([block][row]) so that a workgroup's
-// block-w column is one contiguous stream.
+// branch splits by projection block: workgroup (w, q) computes gate rows
+// [32w, 32w+32) (after the fused post-FFN residual prologue, which every
+// workgroup repeats), keeps the 32 gated values in LDS, and multiplies them
+// with block w of the projection rows in quarter q.  Workgroups (w, *) write
+// the partial projection part[w][0..H); the consumer (the next layer's qkv
+// prologue or the step tail) adds the 8 partials in a fixed order.  Up to
+// four row slices q put the branch on 32 CUs instead of 8 (each CU's share of
+// the weight and vector traffic is what bounds this small launch); the gate
+// rows are recomputed per slice.  The projection weights are stored
+// block-transposed ([block][row]) so that a block-w column is one contiguous
+// stream.
 #include "../../include/e4b.h"
 #include "q40_kernel.h"
 #include "step.h"
@@ -21,11 +24,13 @@ namespace {
 constexpr float kTwo24 = 16777216.0f;
 
 // PROK = H / 256: lanes per gate row LPR = H / 32 = 8 PROK, G = 8 / PROK
-// groups per wave, R = PROK rows per group, 8 gate rows per wave.
-template <int PROK>
+// groups per wave, R = PROK rows per group, 8 gate rows per wave; Q row
+// quarters (blockIdx.y), PR = PROK / Q projection rows per thread.
+template <int PROK, int Q>
 __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
-  constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK;
+  constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK, PR = PROK / Q;
   static_assert(G * R == 8, "8 gate rows per wave");
+  static_assert(PR * Q == PROK, "whole projection rows per thread");
   __shared__ __align__(16) uint16_t xs[H];
   __shared__ float red[4];
   __shared__ __align__(16) uint16_t gs[32];
@@ -35,7 +40,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   const int w = blockIdx.x;
 
   q40k::ProRegs<PROK> pr;
-  q40k::pro_issue<PROK>(pa, pr);
+  q40k::pro_issue<PROK, 1, 256, false>(pa, pr);
   // gate rows of this lane group, block l
   const int row0 = 32 * w + 8 * wave + g * R;
   uint4 wq[R];
@@ -47,12 +52,13 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
     wsc[r] = ld_scale_pair_off(A.gate.sc, e);
     wodd |= (uint32_t)(e & 1) << r;
   }
-  // projection rows o = threadIdx.x + 256 i, block w (block-transposed planes)
-  uint4 pq[PROK];
-  uint32_t psc[PROK], podd = 0;
+  // projection rows o = H/Q q + threadIdx.x + 256 i, block w (block-transposed planes)
+  const int o0 = (H / Q) * blockIdx.y;
+  uint4 pq[PR];
+  uint32_t psc[PR], podd = 0;
 #pragma unroll
-  for (int i = 0; i < PROK; ++i) {
-    const uint32_t e = (uint32_t)(w * H) + threadIdx.x + 256 * i;
+  for (int i = 0; i < PR; ++i) {
+    const uint32_t e = (uint32_t)(w * H + o0) + threadIdx.x + 256 * i;
     pq[i] = ld_nt_u4_off(A.proj_nib, e);
     psc[i] = ld_scale_pair_off(A.proj_sc, e);
     podd |= (uint32_t)(e & 1) << i;
@@ -61,7 +67,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   // no row load a valid neighbour and drop it)
   const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
-  q40k::pro_finish<PROK>(pa, pr, xs, red);
+  q40k::pro_finish<PROK, 256, 1, false>(pa, pr, xs, red);
 
   // gate: 32 columns of x per lane (block l), R rows per group
   {
@@ -106,10 +112,10 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
     }
     const float gs8 = -8.f * xsum16(gp);
 #pragma unroll
-    for (int i = 0; i < PROK; ++i) {
+    for (int i = 0; i < PR; ++i) {
       float a0 = 0.f, a1 = 0.f;
       q40_dot2(pq[i], gp, a0, a1);
-      A.part[(int64_t)w * H + threadIdx.x + 256 * i] =
+      A.part[(int64_t)w * H + o0 + threadIdx.x + 256 * i] =
           scale_of(psc[i], (podd >> i) & 1) * fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, gs8));
     }
   }
@@ -120,12 +126,11 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
 int launch_ple(const PleLaunch& A, const ProArgs& pa, hipStream_t st) {
   if (A.PD != 256 || A.gate.rows != A.PD || A.gate.nb * 32 != A.H || pa.H != A.H || !q40_prologue_supported(A.H))
     return e4b_fail(E4B_EINVAL, "PLE branch: needs ple_dim 256 and hidden 256/512/1024/2048 (got %d, %d)", A.PD, A.H);
-  const dim3 grid(A.PD / 32);
   switch (A.H) {
-    case 256: hipLaunchKernelGGL(k_ple<1>, grid, dim3(256), 0, st, A, pa); break;
-    case 512: hipLaunchKernelGGL(k_ple<2>, grid, dim3(256), 0, st, A, pa); break;
-    case 1024: hipLaunchKernelGGL(k_ple<4>, grid, dim3(256), 0, st, A, pa); break;
-    case 2048: hipLaunchKernelGGL(k_ple<8>, grid, dim3(256), 0, st, A, pa); break;
+    case 256: hipLaunchKernelGGL((k_ple<1, 1>), dim3(A.PD / 32, 1), dim3(256), 0, st, A, pa); break;
+    case 512: hipLaunchKernelGGL((k_ple<2, 2>), dim3(A.PD / 32, 2), dim3(256), 0, st, A, pa); break;
+    case 1024: hipLaunchKernelGGL((k_ple<4, 4>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
+    case 2048: hipLaunchKernelGGL((k_ple<8, 4>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
   }
   E4B_HIP(hipGetLastError());
   return E4B_OK;

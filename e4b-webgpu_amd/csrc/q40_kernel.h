@@ -82,7 +82,8 @@ DEV float block_sum_n(float v, float* red) {
 // NA partial vectors a[s*H + i] (s < NA) are summed into a, in order, by
 // pro_finish; pro_issue only issues the loads, so nothing between them and
 // the weight loads waits for memory
-template <int PROK, int NA = 1, int TPB = 256>
+// NORM2 = false: the prologue ends at h (x = f16(h), w2 unused and not read)
+template <int PROK, int NA = 1, int TPB = 256, bool NORM2 = true>
 DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB, NA>& r) {
   constexpr int N = ProRegs<PROK, TPB, NA>::N;
   // absent vectors read hin instead (always valid) and are masked after the
@@ -97,7 +98,7 @@ DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB, NA>& r) {
 #pragma unroll
   for (int s = 0; s < NA; ++s) ld_floats<N>(a + s * sstride + i0, r.a[s]);
   ld_floats<N>(w1 + i0, r.w1);
-  ld_floats<N>(w2 + i0, r.w2);
+  if constexpr (NORM2) ld_floats<N>(w2 + i0, r.w2);
 }
 
 // attention-combine prologue of the o projection: x[h*256 + d] = f16 of the
@@ -191,7 +192,7 @@ DEV void attn_finish(const ProArgs& p, AttnRegs<U>& r, uint16_t* xs, float* wts)
 // h = (hin + rms(a) * w1) * scale; x = w2 ? f16(rms(h) * w2) : f16(h)
 // (kernels/rmsacc3.wgsl:36-53, kernels/a4btail.wgsl:54-71,
 // kernels/rmsacc.wgsl:10-26 folded into the consumer GEMV)
-template <int PROK, int TPB = 256, int NA = 1>
+template <int PROK, int TPB = 256, int NA = 1, bool NORM2 = true>
 DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, float* red) {
   constexpr int N = ProRegs<PROK, TPB, NA>::N;
   static_assert(256 * PROK % TPB == 0, "whole elements per thread");
@@ -204,7 +205,7 @@ DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, f
     for (int s = 1; s < NA; ++s) sum += r.a[s][k];
     av[k] = has_a ? sum : 0.f;
     r.w1[k] = has_a ? r.w1[k] : 0.f;
-    r.w2[k] = has_w2 ? r.w2[k] : 1.f;
+    r.w2[k] = (NORM2 && has_w2) ? r.w2[k] : 1.f;
   }
   float ss = 0.f;
 #pragma unroll
@@ -219,13 +220,13 @@ DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, f
     r.h[k] = (r.h[k] + av[k] * inv1 * r.w1[k]) * p.scale;
     s2 = fmaf(r.h[k], r.h[k], s2);
   }
-  const float s2t = block_sum_n<TPB / 64>(s2, red);
-  const float inv2 = p.w2 ? rms_inv(s2t, p.H, p.eps) : 1.f;
+  float inv2 = 1.f;
+  if constexpr (NORM2) inv2 = p.w2 ? rms_inv(block_sum_n<TPB / 64>(s2, red), p.H, p.eps) : 1.f;
   const bool writer = p.hout && blockIdx.x == 0 && blockIdx.y == 0;
   const int i0 = threadIdx.x * N;
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    xs[i0 + k] = f2h(p.w2 ? r.h[k] * inv2 * r.w2[k] : r.h[k]);
+    xs[i0 + k] = f2h((NORM2 && p.w2) ? r.h[k] * inv2 * r.w2[k] : r.h[k]);
     if (writer) p.hout[i0 + k] = r.h[k];
   }
   lds_sync();
