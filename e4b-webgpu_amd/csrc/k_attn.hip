@@ -104,25 +104,32 @@ DEV float xmax32(float v) {
   return fmaxf(v, t);
 }
 
-// One block of 8 waves per (KV group g, chunk c of CS positions); wave w owns
-// the chunk's positions j = w + 8k (k < CS/8).  K is read as 16 lanes per
-// position, lane dl holding dims 8dl..8dl+7 and 128+8dl..128+8dl+7 (two
-// 256-byte contiguous halves per row), 4 positions per pass (lane group
-// `sub` takes k = 4s + sub); V as 16 B per lane, lanes 0-31 one position and
-// lanes 32-63 the next (dims 8(l%32)..8(l%32)+7).
-template <int CS>
+// One block of 8 waves per (KV group g, chunk c of CS positions, V slice z);
+// wave w owns the chunk's positions j = w + 8k (k < CS/8).  K is read as 16
+// lanes per position, lane dl holding dims 8dl..8dl+7 and 128+8dl..128+8dl+7
+// (two 256-byte contiguous halves per row), 4 positions per pass (lane group
+// `sub` takes k = 4s + sub).  With NS = 2 the block handles V dims
+// [128z, 128z+128) only: both slices compute the same scores, and each reads
+// half of V, which spreads a chunk's memory traffic over two CUs.  V is read
+// as 16 B per lane, 8 dims each, 64/LV positions per load (LV = lanes per
+// position).
+template <int CS, int NS>
 __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   constexpr int NW = 8;
-  constexpr int KP = CS / 32;  // score passes per wave (4 positions each)
-  constexpr int VS = CS / 8;   // positions per wave
-  constexpr int VQ = VS / 2;   // V loads per lane (two positions per load)
+  constexpr int KP = CS / 32;      // score passes per wave (4 positions each)
+  constexpr int VS = CS / 8;       // positions per wave
+  constexpr int VD = HD / NS;      // V dims per block
+  constexpr int LV = VD / 8;       // lanes per V row
+  constexpr int PPL = 64 / LV;     // positions per V load
+  constexpr int VQ = VS / PPL;     // V loads per lane
+  static_assert(NS == 1 || NS == 2, "one or two V slices");
   __shared__ float qs[GQA][HD];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
-  __shared__ __align__(16) float po[NW][GQA][HD];
+  __shared__ __align__(16) float po[NW][GQA][VD];
   __shared__ float wml[NW][GQA][2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = blockIdx.x, c = blockIdx.y;
+  const int g = blockIdx.x, c = blockIdx.y, zs = NS == 1 ? 0 : (int)blockIdx.z;
   // 32-bit position arithmetic throughout (positions < 2^31): a 64-bit
   // modulo is a long software sequence on this ISA
   const int pos = (int)(A.params ? A.params[0] : A.pos);
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
     return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
   };
   const int sub = lane >> 4, dl = lane & 15;
-  const int hi = lane >> 5, l32 = lane & 31;
+  const int vsub = lane / LV, vl = lane % LV, vd0 = VD * zs + 8 * vl;
 
   // 0. request everything the block reads before any math: the head-prep
   //    inputs (this wave's q/k/v row, its norm weights, the RoPE (cos, sin)
@@ -168,8 +175,8 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   }
 #pragma unroll
   for (int q = 0; q < VQ; ++q) {
-    const int j = min(wave + NW * (2 * q + hi), m - 1);
-    vr[q] = *reinterpret_cast<const uint4*>(vc + slot_at(j) * HD + 8 * l32);
+    const int j = min(wave + NW * (PPL * q + vsub), m - 1);
+    vr[q] = *reinterpret_cast<const uint4*>(vc + slot_at(j) * HD + vd0);
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first wait
 
@@ -189,7 +196,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       const uint2 pk = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
                                   (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
       *reinterpret_cast<uint2*>((wave == 4 ? knew : vnew) + 4 * lane) = pk;
-      if (owner) *reinterpret_cast<uint2*>((wave == 4 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
+      if (owner && zs == 0) *reinterpret_cast<uint2*>((wave == 4 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
     }
   }
   lds_sync();
@@ -243,20 +250,20 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   }
   ls = xsum_step<32>(xsum_step<16>(ls));
 
-  // 4. P.V over the wave's positions: lane covers dims 8(l%32)..8(l%32)+7 of
-  //    position i = 2q + (l >= 32); the weight of position k = 4s + sub,
-  //    head h sits in lane 16 sub + 4h of e[s]
+  // 4. P.V over the wave's positions: lane covers dims vd0..vd0+7 of
+  //    position i = PPL q + vsub; the weight of position k = 4s + sub, head h
+  //    sits in lane 16 sub + 4h of e[s]
   {
     float acc[GQA][8];
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-    const uint4 vn = *reinterpret_cast<const uint4*>(vnew + 8 * l32);
+    const uint4 vn = *reinterpret_cast<const uint4*>(vnew + vd0);
 #pragma unroll
     for (int q = 0; q < VQ; ++q) {
-      const int i0 = 2 * q, i1 = 2 * q + 1;
-      const int j = wave + NW * (2 * q + hi);
+      const int i = PPL * q + vsub;
+      const int j = wave + NW * i;
       // a position past m reads a clamped, possibly stale row: zero it, so
       // its zero weight cannot meet a non-finite value
       const uint4 vv = (c_lo + j == pos) ? vn : (j < m ? vr[q] : make_uint4(0u, 0u, 0u, 0u));
@@ -270,25 +277,41 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
 #pragma unroll
       for (int h = 0; h < GQA; ++h) {
         // zero for positions past m (e = 0 there), so no branch
-        const float p0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i0 >> 2]), 16 * (i0 & 3) + 4 * h));
-        const float p1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i1 >> 2]), 16 * (i1 & 3) + 4 * h));
-        const float pf = hi ? p1 : p0;
+        float pf;
+        if constexpr (PPL == 2) {
+          const int i0 = 2 * q, i1 = 2 * q + 1;
+          const float p0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i0 >> 2]), 16 * (i0 & 3) + 4 * h));
+          const float p1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i1 >> 2]), 16 * (i1 & 3) + 4 * h));
+          pf = vsub ? p1 : p0;
+        } else {
+          // PPL = 4: position 4q + vsub lives in pass q, lane group vsub
+          pf = __shfl(e[q], 16 * vsub + 4 * h, 64);
+        }
 #pragma unroll
         for (int d = 0; d < 8; ++d) acc[h][d] = fmaf(pf, vf[d], acc[h][d]);
       }
     }
-    // fold the two lane halves: lanes < 32 keep heads 0, 1, lanes >= 32
-    // heads 2, 3 (each summed over both halves)
+    // fold the position groups: lanes < 32 keep heads 0, 1, lanes >= 32
+    // heads 2, 3; with four groups, bit 16 then picks one of the two
     float r[2][8];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int d = 0; d < 8; ++d) r[hh][d] = tstep<32>(acc[hh][d], acc[hh + 2][d]);
+    if constexpr (PPL == 2) {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      float4* dst = reinterpret_cast<float4*>(&po[wave][hh + 2 * hi][8 * l32]);
-      dst[0] = make_float4(r[hh][0], r[hh][1], r[hh][2], r[hh][3]);
-      dst[1] = make_float4(r[hh][4], r[hh][5], r[hh][6], r[hh][7]);
+      for (int hh = 0; hh < 2; ++hh) {
+        float4* dst = reinterpret_cast<float4*>(&po[wave][hh + 2 * (lane >> 5)][8 * vl]);
+        dst[0] = make_float4(r[hh][0], r[hh][1], r[hh][2], r[hh][3]);
+        dst[1] = make_float4(r[hh][4], r[hh][5], r[hh][6], r[hh][7]);
+      }
+    } else {
+      float t[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) t[d] = tstep<16>(r[0][d], r[1][d]);
+      float4* dst = reinterpret_cast<float4*>(&po[wave][2 * (lane >> 5) + ((lane >> 4) & 1)][8 * vl]);
+      dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+      dst[1] = make_float4(t[4], t[5], t[6], t[7]);
     }
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
@@ -300,26 +323,30 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   lds_sync();
 
   // 5. fold the 8 waves (log-sum-exp) into this chunk's partials
-  //    ([head][chunk][dim], [head][chunk][max, sum]); thread t: head t/128,
-  //    dims 2(t%128), 2(t%128)+1
+  //    ([head][chunk][dim], [head][chunk][max, sum]); GQA x VD outputs, one
+  //    or two (adjacent dims) per thread
   {
+    constexpr int OPT = GQA * VD / (NW * 64);  // outputs per thread
     const int gch = gridDim.y;  // partial stride: chunks allocated per head
-    const int h = threadIdx.x >> 7, d = 2 * (threadIdx.x & 127);
+    const int h = threadIdx.x / (VD / OPT), d = OPT * (threadIdx.x % (VD / OPT));
     float M = wml[0][h][0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) M = fmaxf(M, wml[w][h][0]);
-    float v0 = 0.f, v1 = 0.f, L = 0.f;
+    float v[OPT], L = 0.f;
+#pragma unroll
+    for (int u = 0; u < OPT; ++u) v[u] = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float f = __expf(wml[w][h][0] - M);  // 0 for a wave without positions
-      const float2 pv = *reinterpret_cast<const float2*>(&po[w][h][d]);
-      v0 = fmaf(pv.x, f, v0);
-      v1 = fmaf(pv.y, f, v1);
+#pragma unroll
+      for (int u = 0; u < OPT; ++u) v[u] = fmaf(po[w][h][d + u], f, v[u]);
       L = fmaf(wml[w][h][1], f, L);
     }
     const int64_t base = (int64_t)(g * GQA + h) * gch + c;
-    *reinterpret_cast<float2*>(A.part_o + base * HD + d) = make_float2(v0, v1);
-    if (d == 0) {
+    float* dst = A.part_o + base * HD + VD * zs + d;
+    if constexpr (OPT == 2) *reinterpret_cast<float2*>(dst) = make_float2(v[0], v[1]);
+    else dst[0] = v[0];
+    if (d == 0 && zs == 0) {
       A.part_ml[base * 2] = M;
       A.part_ml[base * 2 + 1] = L;
     }
@@ -394,12 +421,12 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.window = a.window;
   A.eps = a.eps;
   if (a.chunk == 64) {
-    hipLaunchKernelGGL(k_attn_split<64>, dim3(a.kvh, nch), dim3(512), 0, st, A);
+    hipLaunchKernelGGL((k_attn_split<64, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
     if (a.combine)
       hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
                          a.window, nch, a.out);
   } else {
-    hipLaunchKernelGGL(k_attn_split<32>, dim3(a.kvh, nch), dim3(512), 0, st, A);
+    hipLaunchKernelGGL((k_attn_split<32, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
     if (a.combine)
       hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
                          a.window, nch, a.out);
