@@ -353,7 +353,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->part_o, (size_t)QH * c->nch * HD)) ||
       (rc = dalloc_t(c, &c->part_ml, (size_t)QH * c->nch * 2)) || (rc = dalloc_t(c, &c->attn, (size_t)QH * HD)) ||
       (rc = dalloc_t(c, &c->o, (size_t)H)) || (rc = dalloc_t(c, &c->xf, (size_t)H)) ||
-      (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->xg, (size_t)H)) || (rc = dalloc_t(c, &c->gp, (size_t)(PD ? PD : 1))) ||
       (rc = dalloc_t(c, &c->pp, (size_t)(PD ? PD / 32 : 1) * H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)))
@@ -494,14 +494,18 @@ int record_step(e4b_ctx* c) {
         return rc;
       swap_h();
     }
-    // 5. down projection
+    // 5. down projection; with the PLE branch as its consumer the columns
+    //    are split in two slices (dn[0..H) + dn[H..2H)), which halves the
+    //    GeGLU-vector reads per workgroup; the PLE prologue adds the slices
     GemvOut od = {c->dn, nullptr, nullptr, 0};
-    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, 1, st)))
+    const int dks = (PD && (FF / 32) % 8 == 0) ? 2 : 1;
+    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, dks, st)))
       return rc;
     if (PD) {
       // 6. PLE branch in one launch: post-FFN residual prologue, gate x GELU x
       //    per-layer input, projection partials (summed by the next consumer)
-      const ProArgs p = pro(hnext, c->dn, ly.post_ffw, nullptr, 1.0f);
+      ProArgs p = pro(hnext, c->dn, ly.post_ffw, nullptr, 1.0f);
+      p.na = dks;
       const size_t nbp = (size_t)H * (PD / 32);
       PleLaunch pl;
       pl.gate = q40_view(ly.pg, PD, H);

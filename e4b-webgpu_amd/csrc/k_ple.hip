@@ -26,7 +26,7 @@ constexpr float kTwo24 = 16777216.0f;
 // PROK = H / 256: lanes per gate row LPR = H / 32 = 8 PROK, G = 8 / PROK
 // groups per wave, R = PROK rows per group, 8 gate rows per wave; Q row
 // quarters (blockIdx.y), PR = PROK / Q projection rows per thread.
-template <int PROK, int Q>
+template <int PROK, int Q, int NA>
 __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK, PR = PROK / Q;
   static_assert(G * R == 8, "8 gate rows per wave");
@@ -39,8 +39,8 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   const int g = lane / LPR, l = lane - g * LPR;
   const int w = blockIdx.x;
 
-  q40k::ProRegs<PROK> pr;
-  q40k::pro_issue<PROK, 1, 256, false>(pa, pr);
+  q40k::ProRegs<PROK, 256, NA> pr;
+  q40k::pro_issue<PROK, NA, 256, false>(pa, pr);
   // gate rows of this lane group, block l
   const int row0 = 32 * w + 8 * wave + g * R;
   uint4 wq[R];
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   // no row load a valid neighbour and drop it)
   const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
-  q40k::pro_finish<PROK, 256, 1, false>(pa, pr, xs, red);
+  q40k::pro_finish<PROK, 256, NA, false>(pa, pr, xs, red);
 
   // gate: 32 columns of x per lane (block l), R rows per group
   {
@@ -123,15 +123,25 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
 
 }  // namespace
 
+template <int NA>
+static void launch_ple_na(const PleLaunch& A, const ProArgs& pa, hipStream_t st) {
+  switch (A.H) {
+    case 256: hipLaunchKernelGGL((k_ple<1, 1, NA>), dim3(A.PD / 32, 1), dim3(256), 0, st, A, pa); break;
+    case 512: hipLaunchKernelGGL((k_ple<2, 2, NA>), dim3(A.PD / 32, 2), dim3(256), 0, st, A, pa); break;
+    case 1024: hipLaunchKernelGGL((k_ple<4, 4, NA>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
+    case 2048: hipLaunchKernelGGL((k_ple<8, 4, NA>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
+  }
+}
+
 int launch_ple(const PleLaunch& A, const ProArgs& pa, hipStream_t st) {
   if (A.PD != 256 || A.gate.rows != A.PD || A.gate.nb * 32 != A.H || pa.H != A.H || !q40_prologue_supported(A.H))
     return e4b_fail(E4B_EINVAL, "PLE branch: needs ple_dim 256 and hidden 256/512/1024/2048 (got %d, %d)", A.PD, A.H);
-  switch (A.H) {
-    case 256: hipLaunchKernelGGL((k_ple<1, 1>), dim3(A.PD / 32, 1), dim3(256), 0, st, A, pa); break;
-    case 512: hipLaunchKernelGGL((k_ple<2, 2>), dim3(A.PD / 32, 2), dim3(256), 0, st, A, pa); break;
-    case 1024: hipLaunchKernelGGL((k_ple<4, 4>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
-    case 2048: hipLaunchKernelGGL((k_ple<8, 4>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
-  }
+  if (!pa.a || !pa.w1 || (pa.na > 2))
+    return e4b_fail(E4B_EINVAL, "PLE branch: the residual prologue needs a (1 or 2 column slices) and w1");
+  if (pa.na == 2)
+    launch_ple_na<2>(A, pa, st);
+  else
+    launch_ple_na<1>(A, pa, st);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }
