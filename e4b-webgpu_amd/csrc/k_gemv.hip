@@ -103,16 +103,28 @@ __global__ __launch_bounds__(256) void k_amax_final(const uint2* __restrict__ pa
 // Q6_K GEMV + softcap + argmax.  Lane <-> 32-element segment (s = lane +
 // 64k); a wave owns R rows per tile and strides over tiles; after the
 // transposed reduction lane l holds row l/(64/R), so the softcap and the
-// argmax update run once per R rows.
+// argmax update run once per R rows.  The workgroup reads x (hi and lo) from
+// memory once, into LDS: with one read per wave the x traffic of the grid
+// would be 4x its size again.
 template <int BPL, int R>
 __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t* __restrict__ xh,
                                                          const uint32_t* __restrict__ xl, float softcap,
                                                          float* __restrict__ logits, uint2* part,
                                                          int64_t ntiles) {
   constexpr int SPAN = 64 / R;
+  constexpr int XW = BPL * 64 * 16;  // 32-bit words of x (hi or lo) the block can hold
+  __shared__ __align__(16) uint32_t xs[2][XW];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nseg = W.nseg, nsb = nseg / 8;
+  {
+    const int nw = nseg * 16;  // words of x
+    for (int i = 4 * (int)threadIdx.x; i < nw; i += 4 * 256) {
+      *reinterpret_cast<uint4*>(&xs[0][i]) = *reinterpret_cast<const uint4*>(xh + i);
+      *reinterpret_cast<uint4*>(&xs[1][i]) = *reinterpret_cast<const uint4*>(xl + i);
+    }
+    lds_sync();
+  }
   uint32_t xph[BPL][16], xpl[BPL][16];
   float gs[BPL][2];
 #pragma unroll
@@ -122,8 +134,8 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t
 #pragma unroll
     for (int i = 0; i < 16; ++i) xph[k][i] = xpl[k][i] = 0u;  // lanes past the row end contribute 0
     if (s < nseg) {
-      load_x16(xh, s, xph[k]);
-      load_x16(xl, s, xpl[k]);
+      load_x16(xs[0], s, xph[k]);
+      load_x16(xs[1], s, xpl[k]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         gs[k][0] = fdot2u(xph[k][i], 0x3C003C00u, gs[k][0]);

@@ -42,7 +42,7 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
   L.nbk = nbk;
   L.pa = pro ? *pro : ProArgs{};
   L.st = st;
-  const q40k::Cfg c = q40k::pick(nbk, L.units, epi, pro != nullptr, ks);
+  const q40k::Cfg c = q40k::pick(nbk, L.units, epi, pro != nullptr, ks, pro && pro->part_o);
   if (c.bpl > 8 || c.lpr * c.bpl * c.kw < nbk)
     return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per slice exceeds the 2048-block (65536-column) maximum", nbk);
   bool ok;

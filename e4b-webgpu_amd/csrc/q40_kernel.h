@@ -412,7 +412,7 @@ inline void pick_lanes(int nbw, int* lpr_out, int* bpl_out, bool lpr64_only) {
 // rows per lane group give ~8-16 weight loads in flight per lane while
 // keeping enough workgroups to cover the chip; rows of >= 8192 columns split
 // their columns over the four waves of a workgroup (KW = 4)
-inline Cfg pick(int nbk, int64_t units, int epi, bool pro, int ks = 1) {
+inline Cfg pick(int nbk, int64_t units, int epi, bool pro, int ks = 1, bool attn = false) {
   Cfg c;
   c.kw = (!pro && nbk >= 256 && nbk % 4 == 0) ? 4 : 1;
   pick_lanes(nbk / c.kw, &c.lpr, &c.bpl, c.kw == 4);
@@ -426,9 +426,10 @@ inline Cfg pick(int nbk, int64_t units, int epi, bool pro, int ks = 1) {
   const int rmin = (epi == EPI_GEGLU) ? 2 : 1;
   const int per_wg = (c.kw == 1 ? 4 : 1) * G;
   // measured on MI355X at the E4B shapes: 256 workgroups (128 with the fused
-  // prologue, which every workgroup repeats; 512 for the column-split down
-  // projection) keep enough loads in flight
-  const int64_t min_wgs = pro ? 128 : c.kw == 4 ? 512 : 256;
+  // norm prologue, which every workgroup repeats; 256 with the attention
+  // prologue, whose per-workgroup partial reads favour short tiles; 512 for
+  // the column-split down projection) keep enough loads in flight
+  const int64_t min_wgs = attn ? 256 : pro ? 128 : c.kw == 4 ? 512 : 256;
   while (r > rmin && ks * ((units + per_wg * r - 1) / (per_wg * r)) < min_wgs) r >>= 1;
   if (r < rmin) r = rmin;
   c.r = r;
