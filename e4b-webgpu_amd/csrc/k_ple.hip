@@ -9,9 +9,9 @@
 // with block w of the projection rows in quarter q.  Workgroups (w, *) write
 // the partial projection part[w][0..H); the consumer (the next layer's qkv
 // prologue or the step tail) adds the 8 partials in a fixed order.  Up to
-// four row slices q put the branch on 32 CUs instead of 8 (each CU's share of
-// the weight and vector traffic is what bounds this small launch); the gate
-// rows are recomputed per slice.  The projection weights are stored
+// eight row slices q put the branch on 64 CUs instead of 8 (each CU's share
+// of the weight and vector traffic is what bounds this small launch); the
+// gate rows are recomputed per slice.  The projection weights are stored
 // block-transposed ([block][row]) so that a block-w column is one contiguous
 // stream.
 #include "../../include/e4b.h"
@@ -129,7 +129,7 @@ static void launch_ple_na(const PleLaunch& A, const ProArgs& pa, hipStream_t st)
     case 256: hipLaunchKernelGGL((k_ple<1, 1, NA>), dim3(A.PD / 32, 1), dim3(256), 0, st, A, pa); break;
     case 512: hipLaunchKernelGGL((k_ple<2, 2, NA>), dim3(A.PD / 32, 2), dim3(256), 0, st, A, pa); break;
     case 1024: hipLaunchKernelGGL((k_ple<4, 4, NA>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
-    case 2048: hipLaunchKernelGGL((k_ple<8, 4, NA>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
+    case 2048: hipLaunchKernelGGL((k_ple<8, 8, NA>), dim3(A.PD / 32, 8), dim3(256), 0, st, A, pa); break;
   }
 }
 
