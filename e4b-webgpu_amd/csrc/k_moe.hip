@@ -44,102 +44,144 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
 }
 
 // ---- router ---------------------------------------------------------------
-// grid ceil(E/4) x 256: wave w of block b scores expert 4b + w; every block
-// computes the rms of h itself; block 0 also writes the two f16 GEMV inputs.
-__global__ __launch_bounds__(256) void k_moe_router(MoeArgs A) {
-  __shared__ float red[4];
+// grid ceil(E/2) x 128: wave w of block b scores expert 2b + w.  Every block
+// computes the rms of h itself and stages x_r = h * inv * scale * mult in LDS
+// once; each wave then streams only its expert's row.  Block b also writes
+// its slice of the two f16 GEMV inputs.
+constexpr int kRouterMaxH4 = 768;  // H <= 3072
+
+__global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
+  __shared__ __align__(16) float4 xr[kRouterMaxH4];
+  __shared__ float red[2];
+  constexpr int PT = kRouterMaxH4 / 128;  // float4 per thread
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int H = A.H, H4 = H / 4;
   const float4* h4 = reinterpret_cast<const float4*>(A.h);
+  const float4* rs4 = reinterpret_cast<const float4*>(A.router_scale);
+  const int e = min((int)blockIdx.x * 2 + wave, A.E - 1);
+  const float4* w4 = reinterpret_cast<const float4*>(A.router_w + (int64_t)e * H);
+  // every load up front: h and the scale (thread-strided), the expert row
+  float4 hv[PT], sv[PT], wv[kRouterMaxH4 / 64];
+#pragma unroll
+  for (int k = 0; k < PT; ++k) {
+    const int i = min((int)threadIdx.x + 128 * k, H4 - 1);
+    hv[k] = h4[i];
+    sv[k] = rs4[i];
+  }
+#pragma unroll
+  for (int k = 0; k < kRouterMaxH4 / 64; ++k) wv[k] = w4[min(lane + 64 * k, H4 - 1)];
   float ss = 0.f;
-  for (int i = threadIdx.x; i < H4; i += 256) {
-    const float4 v = h4[i];
-    ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+#pragma unroll
+  for (int k = 0; k < PT; ++k)
+    if ((int)threadIdx.x + 128 * k < H4)
+      ss = fmaf(hv[k].x, hv[k].x, fmaf(hv[k].y, hv[k].y, fmaf(hv[k].z, hv[k].z, fmaf(hv[k].w, hv[k].w, ss))));
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  lds_sync();
+  const float inv = rms_inv(red[0] + red[1], H, A.eps);
+#pragma unroll
+  for (int k = 0; k < PT; ++k) {
+    const int i = (int)threadIdx.x + 128 * k;
+    if (i < H4)
+      xr[i] = make_float4(hv[k].x * inv * (sv[k].x * A.router_mult), hv[k].y * inv * (sv[k].y * A.router_mult),
+                          hv[k].z * inv * (sv[k].z * A.router_mult), hv[k].w * inv * (sv[k].w * A.router_mult));
   }
-  const float inv = rms_inv(block_sum(ss, red), H, A.eps);
-  const int e = blockIdx.x * 4 + wave;
-  if (e < A.E) {
-    const float4* rs4 = reinterpret_cast<const float4*>(A.router_scale);
-    const float4* w4 = reinterpret_cast<const float4*>(A.router_w + (int64_t)e * H);
-    float acc = 0.f;
-    for (int i = lane; i < H4; i += 64) {
-      const float4 v = h4[i], s = rs4[i], w = w4[i];
-      acc = fmaf(v.x * inv * (s.x * A.router_mult), w.x, acc);
-      acc = fmaf(v.y * inv * (s.y * A.router_mult), w.y, acc);
-      acc = fmaf(v.z * inv * (s.z * A.router_mult), w.z, acc);
-      acc = fmaf(v.w * inv * (s.w * A.router_mult), w.w, acc);
+  lds_sync();
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < kRouterMaxH4 / 64; ++k) {
+    const int i = lane + 64 * k;
+    if (i < H4) {
+      const float4 x = xr[i], w = wv[k];
+      acc = fmaf(x.x, w.x, fmaf(x.y, w.y, fmaf(x.z, w.z, fmaf(x.w, w.w, acc))));
     }
-    acc = wave_sum(acc);
-    if (lane == 0) A.scores[e] = acc;
   }
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < H; i += 256) {
-      const float v = A.h[i] * inv;
-      A.xd[i] = f2h(v * A.ffn_norm[i]);
-      A.xm[i] = f2h(v * A.pre_ffw2[i]);
-    }
+  acc = wave_sum(acc);
+  if (lane == 0 && (int)blockIdx.x * 2 + wave < A.E) A.scores[e] = acc;
+  // this block's slice of the f16 branch inputs
+  const int per = (H + gridDim.x - 1) / gridDim.x;
+  for (int i = blockIdx.x * per + threadIdx.x; i < min(H, (int)(blockIdx.x + 1) * per); i += 128) {
+    const float v = A.h[i] * inv;
+    A.xd[i] = f2h(v * A.ffn_norm[i]);
+    A.xm[i] = f2h(v * A.pre_ffw2[i]);
+  }
 }
 
 // ---- top-8 in one wave ----------------------------------------------------
 // lane l holds the scores of experts l + 64 j (j < 4, E <= 256); every lane
-// returns the same 8 picks and weights.  Selection on the scores equals the
-// reference's selection on p = exp(s - max) unless some of the top-8 p
-// underflow to 0 (scores more than ~87 below the maximum).
+// returns the same 8 picks (and, with WEIGHTS, their weights).  Selection on
+// the scores equals the reference's selection on p = exp(s - max) unless some
+// of the top-8 p underflow to 0 (scores more than ~87 below the maximum).
+// Branch-free: compare-and-select only, so a wave runs it in a few hundred
+// instructions.
 struct TopK {
   int idx[K];
   float w[K];
 };
 
+DEV void amax_pick(float& bv, int& bi, float& bp, float ov, int oi, float op) {
+  const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
+  bv = take ? ov : bv;
+  bi = take ? oi : bi;
+  bp = take ? op : bp;
+}
+
+template <bool WEIGHTS>
 DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__ pes, int E) {
   const int lane = threadIdx.x & 63;
-  float s[4];
+  float s[4], pe[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    s[j] = e < E ? scores[e] : -3.0e38f;
+    const int e = min(lane + 64 * j, E - 1);
+    s[j] = scores[e];
+    pe[j] = WEIGHTS ? pes[e] : 0.f;
   }
-  const float M = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-  float psum = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (lane + 64 * j < E) psum += expf(s[j] - M);
-  const float S = wave_sum(psum);
+  for (int j = 0; j < 4; ++j) s[j] = lane + 64 * j < E ? s[j] : -3.0e38f;
+  float M = 0.f, S = 1.f;
+  if constexpr (WEIGHTS) {
+    M = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) psum += lane + 64 * j < E ? expf(s[j] - M) : 0.f;
+    S = wave_sum(psum);
+  }
   TopK t;
   float wsum = 0.f;
+  float pk[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     // lane candidate: strict '>' in index order keeps the lowest index
-    float bv = -3.0e38f;
-    int bi = 0x7fffffff;
+    float bv = s[0], bp = pe[0];
+    int bi = lane;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (s[j] > bv) {
-        bv = s[j];
-        bi = lane + 64 * j;
-      }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
+    for (int j = 1; j < 4; ++j) {
+      const bool take = s[j] > bv;
+      bv = take ? s[j] : bv;
+      bp = take ? pe[j] : bp;
+      bi = take ? lane + 64 * j : bi;
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+      amax_pick(bv, bi, bp, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64), __shfl_xor(bp, off, 64));
     t.idx[k] = bi;
-    t.w[k] = expf(bv - M) / S;  // p_k / sum p, as the reference stores it
-    wsum += t.w[k];
+    pk[k] = bp;
+    if constexpr (WEIGHTS) {
+      t.w[k] = expf(bv - M) / S;  // p_k / sum p, as the reference stores it
+      wsum += t.w[k];
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (lane + 64 * j == bi) s[j] = -3.4e38f;  // below any live score, above nothing picked
+    for (int j = 0; j < 4; ++j) s[j] = lane + 64 * j == bi ? -3.4e38f : s[j];  // below any live score
   }
+  if constexpr (WEIGHTS) {
 #pragma unroll
-  for (int k = 0; k < K; ++k) t.w[k] = t.w[k] / wsum * pes[t.idx[k]];
+    for (int k = 0; k < K; ++k) t.w[k] = t.w[k] / wsum * pk[k];
+  }
   return t;
 }
 
 __global__ __launch_bounds__(64) void k_moe_topk(MoeArgs A) {
-  const TopK t = select_topk(A.scores, A.pes, A.E);
+  const TopK t = select_topk<true>(A.scores, A.pes, A.E);
   const int lane = threadIdx.x;
 #pragma unroll
   for (int k = 0; k < K; ++k)
@@ -152,10 +194,14 @@ __global__ __launch_bounds__(64) void k_moe_topk(MoeArgs A) {
 // ---- gate/up + GeGLU, dense branch and 8 expert slots ------------------------
 // 32 lanes per unit (a gate row and its up row), 3 blocks per lane (88-block
 // rows of the 2816-wide input), 2 units per wave tile.  Units [0, FF2) are
-// dense, then slot k covers [FF2 + k FF, FF2 + (k+1) FF).
+// dense, then slot k covers [FF2 + k FF, FF2 + (k+1) FF).  The block stages
+// both f16 inputs in LDS once (a block can hold dense and expert waves):
+// read per wave, the input would cost more on-chip traffic than the weights.
 constexpr int GU_LPR = 32, GU_BPL = 3;
+constexpr int kMoeMaxH = GU_LPR * GU_BPL * 32;  // 3072
 
 __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
+  __shared__ __align__(16) uint16_t xs[2][kMoeMaxH];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / GU_LPR, l = lane % GU_LPR;
@@ -168,11 +214,13 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   const int u = (int)(2 * tile) + g;    // this group's unit
   const bool dense = 2 * tile < A.FF2;  // wave-uniform: FF2 and FF are even
 
-  // 1. the input slice of this lane's blocks (independent of the routing)
-  const uint32_t* x = reinterpret_cast<const uint32_t*>(dense ? A.xd : A.xm);
-  uint32_t xp[GU_BPL][16];
-#pragma unroll
-  for (int b = 0; b < GU_BPL; ++b) load_x16(x, min(l + GU_LPR * b, nb - 1), xp[b]);
+  // 1. both inputs (independent of the routing), two 16-byte pieces per
+  //    thread and input at most (H <= 3072)
+  // (named registers: an array here is kept in scratch memory by the compiler)
+  const int nv = A.H / 8;
+  const int i0 = min((int)threadIdx.x, nv - 1), i1 = min((int)threadIdx.x + 256, nv - 1);
+  const uint4 xd0 = reinterpret_cast<const uint4*>(A.xd)[i0], xd1 = reinterpret_cast<const uint4*>(A.xd)[i1];
+  const uint4 xm0 = reinterpret_cast<const uint4*>(A.xm)[i0], xm1 = reinterpret_cast<const uint4*>(A.xm)[i1];
 
   // 2. weight rows: dense units are known now; expert units after the top-8
   //    selection, which every expert wave redoes from the 128 scores (wave 0
@@ -194,17 +242,19 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   };
   int slot = 0, j = u;
   if (dense) load_rows(A.dense_gu, u, A.FF2 + u);
-  if (!dense || (blockIdx.x == 0 && wave == 0)) {
-    const TopK t = select_topk(A.scores, A.pes, A.E);
-    if (blockIdx.x == 0 && wave == 0) {
+  if (blockIdx.x == 0 && wave == 0) {
+    // one wave stores the picks and weights for the down kernel
+    const TopK t = select_topk<true>(A.scores, A.pes, A.E);
 #pragma unroll
-      for (int k = 0; k < K; ++k)
-        if (lane == k) {
-          A.topk_idx[k] = (uint32_t)t.idx[k];
-          A.topk_w[k] = t.w[k];
-        }
-    }
-    if (!dense) {
+    for (int k = 0; k < K; ++k)
+      if (lane == k) {
+        A.topk_idx[k] = (uint32_t)t.idx[k];
+        A.topk_w[k] = t.w[k];
+      }
+  }
+  if (!dense) {
+    const TopK t = select_topk<false>(A.scores, A.pes, A.E);
+    {
       slot = (u - A.FF2) / A.FF;
       j = (u - A.FF2) - slot * A.FF;
       int e = t.idx[0];
@@ -216,7 +266,22 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     }
   }
 
-  // 3. dot products, GeGLU
+  // 3. stage the inputs, then this lane's blocks from LDS
+  if ((int)threadIdx.x < nv) {
+    reinterpret_cast<uint4*>(xs[0])[threadIdx.x] = xd0;
+    reinterpret_cast<uint4*>(xs[1])[threadIdx.x] = xm0;
+  }
+  if ((int)threadIdx.x + 256 < nv) {
+    reinterpret_cast<uint4*>(xs[0])[threadIdx.x + 256] = xd1;
+    reinterpret_cast<uint4*>(xs[1])[threadIdx.x + 256] = xm1;
+  }
+  lds_sync();
+  const uint32_t* x = reinterpret_cast<const uint32_t*>(xs[dense ? 0 : 1]);
+  uint32_t xp[GU_BPL][16];
+#pragma unroll
+  for (int b = 0; b < GU_BPL; ++b) load_x16(x, min(l + GU_LPR * b, nb - 1), xp[b]);
+
+  // 4. dot products, GeGLU
   float acc[2] = {0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < GU_BPL; ++b) {
@@ -248,62 +313,83 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
 // FF2/32 blocks, 2 rows per group, 4 per wave tile); the rest run the expert
 // rows: for output row o the 8 lane groups are the 8 slots (8 lanes x 3
 // blocks of the FF/32 = 22-block rows), 4 output rows per wave tile, and the
-// slot results are combined with the router weights across the groups.
+// slot results are combined with the router weights across the groups.  One
+// tile per wave; the block's f16 input (the dense GeGLU output, or the 8
+// slots' outputs) is staged in LDS once.
 constexpr int DD_LPR = 32, DD_BPL = 3, DD_R = 2;
 constexpr int DE_LPR = 8, DE_BPL = 3, DE_R = 4;
+constexpr int kMoeMaxX = K * DE_LPR * DE_BPL * 32;  // 6144 >= FF2 and 8 FF
 
 __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
+  __shared__ __align__(16) uint16_t xs[kMoeMaxX];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if ((int)blockIdx.x < nbd) {
+  const bool dense_blk = (int)blockIdx.x < nbd;  // block-uniform
+  // the block's input: FF2 (dense) or 8 FF (experts) f16 values, three
+  // 16-byte pieces per thread at most
+  const int nx = (dense_blk ? A.FF2 : K * A.FF) / 8;
+  const uint4* xsrc = reinterpret_cast<const uint4*>(dense_blk ? A.g_dense : A.g_slots);
+  // (named registers: an array here is kept in scratch memory by the compiler)
+  const uint4 xv0 = xsrc[min((int)threadIdx.x, nx - 1)];
+  const uint4 xv1 = xsrc[min((int)threadIdx.x + 256, nx - 1)];
+  const uint4 xv2 = xsrc[min((int)threadIdx.x + 512, nx - 1)];
+  auto stage_x = [&]() {
+    uint4* d = reinterpret_cast<uint4*>(xs);
+    if ((int)threadIdx.x < nx) d[threadIdx.x] = xv0;
+    if ((int)threadIdx.x + 256 < nx) d[threadIdx.x + 256] = xv1;
+    if ((int)threadIdx.x + 512 < nx) d[threadIdx.x + 512] = xv2;
+    lds_sync();
+  };
+
+  if (dense_blk) {
     const int g = lane / DD_LPR, l = lane % DD_LPR;
     const int nb = A.FF2 / 32;
     const Q40Mat& W = A.dense_down;
-    const uint32_t* x = reinterpret_cast<const uint32_t*>(A.g_dense);
+    const int64_t ntiles = (A.H + 2 * DD_R - 1) / (2 * DD_R);
+    const int64_t tile = min((int64_t)blockIdx.x * 4 + wave, ntiles - 1);
+    const int64_t r0 = tile * 2 * DD_R + g * DD_R;
+    uint4 wq[DD_R][DD_BPL];
+    uint32_t ws[DD_R][DD_BPL], odd = 0;
+#pragma unroll
+    for (int r = 0; r < DD_R; ++r) {
+      const int64_t row = min(r0 + r, (int64_t)A.H - 1);
+#pragma unroll
+      for (int b = 0; b < DD_BPL; ++b) {
+        const int jb = min(l + DD_LPR * b, nb - 1);
+        const int64_t e = row * nb + jb;
+        wq[r][b] = ld_nt_u4(W.nib + e);
+        ws[r][b] = ld_scale_pair(W.sc, e);
+        odd |= (uint32_t)(e & 1) << (r * DD_BPL + b);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    stage_x();
+    const uint32_t* x = reinterpret_cast<const uint32_t*>(xs);
     uint32_t xp[DD_BPL][16];
     float xs8[DD_BPL];
 #pragma unroll
     for (int b = 0; b < DD_BPL; ++b) {
       const int jb = l + DD_LPR * b;
+      load_x16(x, min(jb, nb - 1), xp[b]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) xp[b][i] = 0u;
-      if (jb < nb) load_x16(x, jb, xp[b]);
+      for (int i = 0; i < 16; ++i) xp[b][i] = jb < nb ? xp[b][i] : 0u;
       xs8[b] = -8.f * xsum16(xp[b]);
     }
-    const int64_t ntiles = (A.H + 2 * DD_R - 1) / (2 * DD_R);
-    for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)nbd * 4) {
-      const int64_t r0 = tile * 2 * DD_R + g * DD_R;
-      uint4 wq[DD_R][DD_BPL];
-      uint32_t ws[DD_R][DD_BPL], odd = 0;
+    float acc[DD_R];
 #pragma unroll
-      for (int r = 0; r < DD_R; ++r) {
-        const int64_t row = min(r0 + r, (int64_t)A.H - 1);
+    for (int r = 0; r < DD_R; ++r) {
+      acc[r] = 0.f;
 #pragma unroll
-        for (int b = 0; b < DD_BPL; ++b) {
-          const int jb = min(l + DD_LPR * b, nb - 1);
-          const int64_t e = row * nb + jb;
-          wq[r][b] = ld_nt_u4(W.nib + e);
-          ws[r][b] = ld_scale_pair(W.sc, e);
-          odd |= (uint32_t)(e & 1) << (r * DD_BPL + b);
-        }
+      for (int b = 0; b < DD_BPL; ++b) {
+        float a0 = 0.f, a1 = 0.f;
+        q40_dot2(wq[r][b], xp[b], a0, a1);
+        const float d = scale_of(ws[r][b], (odd >> (r * DD_BPL + b)) & 1);
+        acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      float acc[DD_R];
-#pragma unroll
-      for (int r = 0; r < DD_R; ++r) {
-        acc[r] = 0.f;
-#pragma unroll
-        for (int b = 0; b < DD_BPL; ++b) {
-          float a0 = 0.f, a1 = 0.f;
-          q40_dot2(wq[r][b], xp[b], a0, a1);
-          const float d = scale_of(ws[r][b], (odd >> (r * DD_BPL + b)) & 1);
-          acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
-        }
-      }
-      const float v = reduce_rows<DD_LPR, DD_R>(acc);
-      const int64_t row = r0 + l / (DD_LPR / DD_R);
-      if ((l % (DD_LPR / DD_R)) == 0 && row < A.H) A.dense_out[row] = v;
     }
+    const float v = reduce_rows<DD_LPR, DD_R>(acc);
+    const int64_t row = r0 + l / (DD_LPR / DD_R);
+    if ((l % (DD_LPR / DD_R)) == 0 && row < A.H && (int64_t)blockIdx.x * 4 + wave < ntiles) A.dense_out[row] = v;
     return;
   }
   // expert rows
@@ -312,71 +398,81 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
   const Q40Mat& W = A.exp_down;
   const int e = (int)A.topk_idx[g];
   const float wk = A.topk_w[g];
-  const uint32_t* x = reinterpret_cast<const uint32_t*>(A.g_slots + (int64_t)g * A.FF);
+  const int64_t ntiles = (A.H + DE_R - 1) / DE_R;
+  const int64_t tile_id = (int64_t)(blockIdx.x - nbd) * 4 + wave;
+  const int64_t o0 = min(tile_id, ntiles - 1) * DE_R;
+  uint4 wq[DE_R][DE_BPL];
+  uint32_t ws[DE_R][DE_BPL], odd = 0;
+#pragma unroll
+  for (int r = 0; r < DE_R; ++r) {
+    const int64_t row = (int64_t)e * A.H + min(o0 + r, (int64_t)A.H - 1);
+#pragma unroll
+    for (int b = 0; b < DE_BPL; ++b) {
+      const int jb = min(l + DE_LPR * b, nb - 1);
+      const int64_t ei = row * nb + jb;
+      wq[r][b] = ld_nt_u4(W.nib + ei);
+      ws[r][b] = ld_scale_pair(W.sc, ei);
+      odd |= (uint32_t)(ei & 1) << (r * DE_BPL + b);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x();
+  const uint32_t* x = reinterpret_cast<const uint32_t*>(xs + (int64_t)g * A.FF);
   uint32_t xp[DE_BPL][16];
   float xs8[DE_BPL];
 #pragma unroll
   for (int b = 0; b < DE_BPL; ++b) {
     const int jb = l + DE_LPR * b;
+    load_x16(x, min(jb, nb - 1), xp[b]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) xp[b][i] = 0u;
-    if (jb < nb) load_x16(x, jb, xp[b]);
+    for (int i = 0; i < 16; ++i) xp[b][i] = jb < nb ? xp[b][i] : 0u;
     xs8[b] = -8.f * xsum16(xp[b]);
   }
-  const int nbe = gridDim.x - nbd;
-  const int64_t ntiles = (A.H + DE_R - 1) / DE_R;
-  for (int64_t tile = (int64_t)(blockIdx.x - nbd) * 4 + wave; tile < ntiles; tile += (int64_t)nbe * 4) {
-    const int64_t o0 = tile * DE_R;
-    uint4 wq[DE_R][DE_BPL];
-    uint32_t ws[DE_R][DE_BPL], odd = 0;
+  float acc[DE_R];
 #pragma unroll
-    for (int r = 0; r < DE_R; ++r) {
-      const int64_t row = (int64_t)e * A.H + min(o0 + r, (int64_t)A.H - 1);
+  for (int r = 0; r < DE_R; ++r) {
+    acc[r] = 0.f;
 #pragma unroll
-      for (int b = 0; b < DE_BPL; ++b) {
-        const int jb = min(l + DE_LPR * b, nb - 1);
-        const int64_t ei = row * nb + jb;
-        wq[r][b] = ld_nt_u4(W.nib + ei);
-        ws[r][b] = ld_scale_pair(W.sc, ei);
-        odd |= (uint32_t)(ei & 1) << (r * DE_BPL + b);
-      }
+    for (int b = 0; b < DE_BPL; ++b) {
+      float a0 = 0.f, a1 = 0.f;
+      q40_dot2(wq[r][b], xp[b], a0, a1);
+      const float d = scale_of(ws[r][b], (odd >> (r * DE_BPL + b)) & 1);
+      acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    float acc[DE_R];
-#pragma unroll
-    for (int r = 0; r < DE_R; ++r) {
-      acc[r] = 0.f;
-#pragma unroll
-      for (int b = 0; b < DE_BPL; ++b) {
-        float a0 = 0.f, a1 = 0.f;
-        q40_dot2(wq[r][b], xp[b], a0, a1);
-        const float d = scale_of(ws[r][b], (odd >> (r * DE_BPL + b)) & 1);
-        acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
-      }
-    }
-    // lane l of slot g holds y_g of row o0 + l / 2; weight it and sum the slots
-    float v = reduce_rows<DE_LPR, DE_R>(acc) * wk;
-    v = xsum_step<8>(v);
-    v = xsum_step<16>(v);
-    v = xsum_step<32>(v);
-    const int64_t row = o0 + l / (DE_LPR / DE_R);
-    if (g == 0 && (l % (DE_LPR / DE_R)) == 0 && row < A.H) A.moe_out[row] = v;
   }
+  // lane l of slot g holds y_g of row o0 + l / 2; weight it and sum the slots
+  float v = reduce_rows<DE_LPR, DE_R>(acc) * wk;
+  v = xsum_step<8>(v);
+  v = xsum_step<16>(v);
+  v = xsum_step<32>(v);
+  const int64_t row = o0 + l / (DE_LPR / DE_R);
+  if (g == 0 && (l % (DE_LPR / DE_R)) == 0 && row < A.H && tile_id < ntiles) A.moe_out[row] = v;
 }
 
 // ---- tail ----------------------------------------------------------------------
-constexpr int kTailPer = 16;  // elements per thread, H <= 4096
+constexpr int kTailPer = 12;  // elements per thread, H <= 3072
 
 __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
   __shared__ float red[4];
   const int H = A.H;
-  float d[kTailPer], m[kTailPer];
+  // every input requested before the first reduction waits
+  float d[kTailPer], m[kTailPer], w1[kTailPer], w2[kTailPer], hv[kTailPer], wp[kTailPer];
+#pragma unroll
+  for (int k = 0; k < kTailPer; ++k) {
+    const int i = min((int)threadIdx.x + 256 * k, H - 1);
+    d[k] = A.dense_out[i];
+    m[k] = A.moe_out[i];
+    w1[k] = A.post_ffw1[i];
+    w2[k] = A.post_ffw2[i];
+    hv[k] = A.h[i];
+    wp[k] = A.post_ffw[i];
+  }
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int k = 0; k < kTailPer; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    d[k] = i < H ? A.dense_out[i] : 0.f;
-    m[k] = i < H ? A.moe_out[i] : 0.f;
+    const bool in = (int)threadIdx.x + 256 * k < H;
+    d[k] = in ? d[k] : 0.f;
+    m[k] = in ? m[k] : 0.f;
     s1 = fmaf(d[k], d[k], s1);
     s2 = fmaf(m[k], m[k], s2);
   }
@@ -385,29 +481,30 @@ __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
   float s3 = 0.f;
 #pragma unroll
   for (int k = 0; k < kTailPer; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    d[k] = i < H ? d[k] * i1 * A.post_ffw1[i] + m[k] * i2 * A.post_ffw2[i] : 0.f;  // comb
+    d[k] = d[k] * i1 * w1[k] + m[k] * i2 * w2[k];  // comb (0 past H)
     s3 = fmaf(d[k], d[k], s3);
   }
   const float i3 = rms_inv(block_sum(s3, red), H, A.eps);
 #pragma unroll
   for (int k = 0; k < kTailPer; ++k) {
     const int i = threadIdx.x + 256 * k;
-    if (i < H) A.h_out[i] = (A.h[i] + d[k] * i3 * A.post_ffw[i]) * A.layer_scale;
+    if (i < H) A.h_out[i] = (hv[k] + d[k] * i3 * wp[k]) * A.layer_scale;
   }
 }
 
 }  // namespace
 
 int launch_moe_router(const MoeArgs& A, hipStream_t st) {
-  hipLaunchKernelGGL(k_moe_router, dim3((A.E + 3) / 4), dim3(256), 0, st, A);
+  if (A.H % 4 || A.H / 4 > kRouterMaxH4) return e4b_fail(E4B_EINVAL, "router: H=%d (multiple of 4, <= 3072)", A.H);
+  hipLaunchKernelGGL(k_moe_router, dim3((A.E + 1) / 2), dim3(128), 0, st, A);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }
 
 int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
-  if (A.H % 256 || A.H > 4096 || A.H / 32 > GU_LPR * GU_BPL || A.FF % 32 || A.FF2 % 32 || A.FF % 2 ||
-      A.FF2 / 32 > DD_LPR * DD_BPL || A.FF / 32 > DE_LPR * DE_BPL || A.E < K || A.E > 256)
+  if (A.H % 256 || A.H > kMoeMaxH || A.H > 256 * kTailPer || A.FF % 32 || A.FF2 % 32 || A.FF % 2 ||
+      A.FF2 / 32 > DD_LPR * DD_BPL || A.FF / 32 > DE_LPR * DE_BPL || A.FF2 > kMoeMaxX || K * A.FF > kMoeMaxX ||
+      A.FF2 > 3 * 256 * 8 || K * A.FF > 3 * 256 * 8 || A.E < K || A.E > 256)
     return e4b_fail(E4B_EINVAL,
                     "MoE layer: unsupported shape (H=%d multiple of 256 <= 3072, FF2=%d <= 3072, FF=%d <= 768, "
                     "8 <= E=%d <= 256)",
