@@ -97,6 +97,9 @@ bool q40_prologue_supported(int H);
 // ks > 1 splits the columns into ks equal slices (cols/32 divisible by ks)
 // and writes ks partial vectors (EPI_F32 only).  pro != null replaces the
 // f16 input xh by the fused prologue (cols must equal pro->H).
+// batched q4_0 GEMM on the matrix cores (k_gemm.hip): Y f32 [M][rows], or
+// with Yh the GeGLU over [gate; up] rows to f16 [M][ff]
+int launch_q40_gemm(const Q40Mat& W, const uint16_t* X, int M, float* Y, uint16_t* Yh, int64_t ff, hipStream_t st);
 int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi, const GemvOut& o, int ks,
                hipStream_t st, const ProArgs* pro = nullptr);
 int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st);

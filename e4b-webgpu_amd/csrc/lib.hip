@@ -161,6 +161,27 @@ extern "C" int e4b_k_q40_gemv_geglu(const void* w_packed, int64_t ff, int64_t co
                     (hipStream_t)stream);
 }
 
+extern "C" int e4b_k_q40_gemm(const void* w_packed, int64_t rows, int64_t cols, const void* x, int m, float* y,
+                              void* stream) {
+  if (!w_packed || !x || !y || rows <= 0 || cols <= 0 || cols % 32 || m <= 0)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemm: bad arguments (rows=%lld cols=%lld m=%d)", (long long)rows,
+                    (long long)cols, m);
+  if (!aligned16(w_packed) || !aligned16(x))
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemm: weight and x must be 16-byte aligned");
+  return launch_q40_gemm(q40_view(w_packed, rows, cols), (const uint16_t*)x, m, y, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int e4b_k_q40_gemm_geglu(const void* w_packed, int64_t ff, int64_t cols, const void* x, int m, void* out,
+                                    void* stream) {
+  if (!w_packed || !x || !out || ff <= 0 || cols <= 0 || cols % 32 || m <= 0)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemm_geglu: bad arguments (ff=%lld cols=%lld m=%d)", (long long)ff,
+                    (long long)cols, m);
+  if (!aligned16(w_packed) || !aligned16(x))
+    return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemm_geglu: weight and x must be 16-byte aligned");
+  return launch_q40_gemm(q40_view(w_packed, 2 * ff, cols), (const uint16_t*)x, m, nullptr, (uint16_t*)out, ff,
+                         (hipStream_t)stream);
+}
+
 extern "C" int e4b_k_q40_geglu_prenorm(const void* w_packed, int64_t ff, int64_t cols, const float* h_in,
                                        const float* resid, const float* w_resid, const float* w_in, float scale,
                                        float eps, float* h_out, void* out_f16, void* stream) {

@@ -79,6 +79,8 @@ SIGNATURES = [
     ("e4b_q6k_pack", _i32, [_vp, _i64, _i64, _vp]),
     ("e4b_k_q40_gemv", _i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
     ("e4b_k_q40_gemv_geglu", _i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    ("e4b_k_q40_gemm", _i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
+    ("e4b_k_q40_gemm_geglu", _i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
     ("e4b_k_q40_geglu_prenorm", _i32, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _f32, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_gemv_argmax", _i32, [_vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_row", _i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),

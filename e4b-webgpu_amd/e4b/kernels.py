@@ -36,6 +36,34 @@ class Q40Matrix:
         check(lib.e4b_k_q40_gemv_geglu(_vp(self.buf), self.rows // 2, self.cols, _vp(x), _vp(out), _vp(stream)),
               "e4b_k_q40_gemv_geglu")
 
+    def gemm_dev(self, x: DeviceBuffer, m: int, y: DeviceBuffer, stream=None) -> None:
+        """x f16[m][cols] -> y f32[m][rows] on the matrix cores"""
+        check(lib.e4b_k_q40_gemm(_vp(self.buf), self.rows, self.cols, _vp(x), m, _vp(y), _vp(stream)),
+              "e4b_k_q40_gemm")
+
+    def gemm_geglu_dev(self, x: DeviceBuffer, m: int, out: DeviceBuffer, stream=None) -> None:
+        """rows = [gate (ff) ; up (ff)]: x f16[m][cols] -> out f16[m][ff]"""
+        check(lib.e4b_k_q40_gemm_geglu(_vp(self.buf), self.rows // 2, self.cols, _vp(x), m, _vp(out), _vp(stream)),
+              "e4b_k_q40_gemm_geglu")
+
+    def gemm(self, x: np.ndarray) -> np.ndarray:
+        """Host convenience: x f16 [m][cols] -> f32 [m][rows]."""
+        x = np.ascontiguousarray(x, np.float16)
+        m = x.shape[0]
+        xd = DeviceBuffer.from_array(x)
+        yd = DeviceBuffer(m * self.rows * 4)
+        self.gemm_dev(xd, m, yd)
+        return yd.download(np.float32, m * self.rows).reshape(m, self.rows)
+
+    def gemm_geglu(self, x: np.ndarray) -> np.ndarray:
+        """Host convenience: x f16 [m][cols] -> f16 [m][rows / 2]."""
+        x = np.ascontiguousarray(x, np.float16)
+        m, ff = x.shape[0], self.rows // 2
+        xd = DeviceBuffer.from_array(x)
+        od = DeviceBuffer(m * ff * 2)
+        self.gemm_geglu_dev(xd, m, od)
+        return od.download(np.float16, m * ff).reshape(m, ff)
+
     def geglu_prenorm_dev(self, h_in: DeviceBuffer, resid, w_resid, w_in: DeviceBuffer, scale: float, eps: float,
                           h_out, out: DeviceBuffer, stream=None) -> None:
         """h = (h_in + rms(resid) * w_resid) * scale; x = f16(rms(h) * w_in); out = GeGLU(x)"""

@@ -111,6 +111,20 @@ int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, const void*
 int e4b_k_q40_gemv_geglu(const void* w_packed, int64_t ff, int64_t cols, const void* x_f16,
                          void* out_f16, void* stream);
 
+/* Batched q4_0 GEMM on the matrix cores, the prefill counterpart of the
+ * GEMV (replaces the multi-column GEMVs of the reference's prefill,
+ * kernels/q40mm.wgsl and kernels/q40sg.wgsl driven by
+ * src/engine-a4b.js:465-585): x is f16[m][cols] row-major (m tokens),
+ * y is f32[m][rows] row-major, y[t][r] = W[r] . x[t].  cols % 32 == 0. */
+int e4b_k_q40_gemm(const void* w_packed, int64_t rows, int64_t cols, const void* x_f16, int m, float* y,
+                   void* stream);
+
+/* Batched gate/up + GeGLU: w_packed is [2*ff][cols] (gate rows then up
+ * rows), x f16[m][cols], out f16[m][ff] = f16(gelu_tanh(gate) * up)
+ * (kernels/q40gu.wgsl:62-119 per token). */
+int e4b_k_q40_gemm_geglu(const void* w_packed, int64_t ff, int64_t cols, const void* x_f16, int m, void* out_f16,
+                         void* stream);
+
 /* The FFN input GEMV as the decode step runs it: a fused residual + RMSNorm
  * prologue, then gate/up + GeGLU (kernels/rmsacc3.wgsl:36-53 folded into
  * kernels/q40gu.wgsl:62-119):
