@@ -36,7 +36,8 @@ struct Layer {
   uint8_t* gu = nullptr;   // [2 FF][H]: gate rows, then up rows
   uint8_t* down = nullptr; // [H][FF]
   uint8_t* pg = nullptr;   // PLE gate [PD][H]
-  uint8_t* pp = nullptr;   // PLE proj [H][PD]
+  uint8_t* pp = nullptr;   // PLE proj [H][PD], block-transposed (decode PLE branch)
+  uint8_t* pp_rm = nullptr; // the same matrix row-major (prefill GEMM)
   float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr, *ffn_norm = nullptr,
         *post_ffw = nullptr, *post_norm = nullptr;
   float scale = 1.0f;
@@ -75,6 +76,13 @@ struct e4b_ctx {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool finalized = false;
+  // batched prefill: chunks of up to pf_cap tokens
+  int pf_cap = 0;
+  uint32_t* pf_ids = nullptr;  // [cap]
+  float *pf_h = nullptr, *pf_proj = nullptr, *pf_ple = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
+        *pf_y = nullptr;       // [cap][H], [2][cap][L PD], [cap][L PD], [cap][QKV], [cap][QH HD], [kPfKs][cap][H]
+  uint16_t *pf_xhl = nullptr, *pf_xn = nullptr, *pf_attn = nullptr, *pf_gg = nullptr,
+           *pf_gp = nullptr;   // [2][cap][H], [cap][H], [cap][QH HD], [cap][FF], [cap][PD]
 };
 
 namespace {
@@ -150,6 +158,11 @@ int expect(const char* name, int type, int want_type, const int64_t* dims, int n
 }
 
 int record_step(e4b_ctx* c);
+
+// batched prefill: tokens per chunk at most, and split-K slices of the
+// o and down projection GEMMs (their consumers sum the slices)
+constexpr int kPfMaxChunk = 512;
+constexpr int kPfKs = 4;
 
 }  // namespace
 
@@ -283,7 +296,9 @@ extern "C" int e4b_set_tensor(e4b_ctx* c, const char* name, int type, const int6
       if ((rc = expect(name, type, E4B_GGML_Q4_0, dims, nd, PD, H)) || (rc = check_bytes((size_t)(H * PD / 32) * 18)))
         return rc;
       if (!ly.pp && (rc = dalloc(c, (void**)&ly.pp, e4b_q40_packed_bytes(H, PD)))) return rc;
-      rc = upload_q40_block_t(ly.pp, H, PD, bytes);
+      if (!ly.pp_rm && (rc = dalloc(c, (void**)&ly.pp_rm, e4b_q40_packed_bytes(H, PD)))) return rc;
+      if ((rc = upload_q40_block_t(ly.pp, H, PD, bytes))) return rc;
+      rc = upload_q40_rows(ly.pp_rm, H, PD, 0, bytes, H);
       break;
     case P_POST_NORM: rc = f32v(&ly.post_norm, H); break;
     case P_SCALE:
@@ -358,6 +373,26 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->pp, (size_t)(PD ? PD / 32 : 1) * H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)))
     return rc;
+  // batched prefill buffers: a chunk of M tokens must leave every key its
+  // queries need in the sliding rings (ring >= window + M - 1, the Complete
+  // condition of specs/KVRing.tla with C = M)
+  {
+    bool any_sliding = false;
+    for (int l = 0; l < k.layers; ++l) any_sliding |= !c->L[l].global;
+    int cap = kPfMaxChunk;
+    if (cap > c->max_prompt) cap = c->max_prompt;
+    if (cap > k.max_seq) cap = k.max_seq;
+    if (any_sliding && cap > k.ring - k.window + 1) cap = k.ring - k.window + 1;
+    c->pf_cap = cap;
+    const size_t M = (size_t)cap, NPs = (size_t)NP;
+    if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
+        (rc = dalloc_t(c, &c->pf_proj, 2 * M * NPs)) || (rc = dalloc_t(c, &c->pf_ple, M * NPs)) ||
+        (rc = dalloc_t(c, &c->pf_qkv, M * (size_t)c->qkv_rows)) || (rc = dalloc_t(c, &c->pf_q, M * QH * HD)) ||
+        (rc = dalloc_t(c, &c->pf_y, (size_t)kPfKs * M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
+        (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * HD)) ||
+        (rc = dalloc_t(c, &c->pf_gg, M * FF)) || (rc = dalloc_t(c, &c->pf_gp, M * (size_t)(PD ? PD : 1))))
+      return rc;
+  }
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
   if (k.flags & E4B_FLAG_NO_GRAPH) return E4B_OK;
@@ -533,6 +568,138 @@ int record_step(e4b_ctx* c) {
   return launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st);
 }
 
+// One prefill chunk: tokens pf_ids[0..M) at positions p0 .. p0 + M - 1,
+// every layer as batched GEMMs on the matrix cores plus per-token kernels
+// (src/engine-a4b.js:465-563 encodeLayerPre / prefill, with the E4B layer
+// recipe of record_step).  Leaves the K/V rows of the chunk in the caches and,
+// in pf_xhl, the final-norm input of every token as an exact f16 hi/lo split.
+int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
+  const int Lc = k.layers;
+  const int64_t NP = (int64_t)Lc * PD;
+  const int64_t MH = (int64_t)M * H;
+  hipStream_t st = c->st;
+  int rc;
+  auto gemm = [&](const Q40Mat& W, const uint16_t* X, int ldx, int epi, float* Y, uint16_t* Yh, int64_t ff,
+                  const float* mul, int64_t mul_ld, int ks) {
+    GemmArgs g{};
+    g.W = W;
+    g.X = X;
+    g.M = M;
+    g.ldx = ldx;
+    g.epi = epi;
+    g.Y = Y;
+    g.Yh = Yh;
+    g.ff = ff;
+    g.mul = mul;
+    g.mul_ld = mul_ld;
+    g.ks = ks;
+    return launch_q40_gemm(g, st);
+  };
+  const Q6Mat E = q6_view(c->embd, k.vocab, H);
+  if ((rc = launch_embed_rows(E, c->pf_ids, M, sqrtf((float)H), c->pf_h, c->pf_xhl, st))) return rc;
+  if (PD) {
+    // PLE model projection of the f32 embedding as two f16 GEMMs (hi, lo)
+    const Q40Mat Wpm = q40_view(c->ple_proj, NP, H);
+    const int64_t slice = (int64_t)M * NP;
+    if ((rc = gemm(Wpm, c->pf_xhl, H, GEMM_F32, c->pf_proj, nullptr, 0, nullptr, 0, 1)) ||
+        (rc = gemm(Wpm, c->pf_xhl + MH, H, GEMM_F32, c->pf_proj + slice, nullptr, 0, nullptr, 0, 1)) ||
+        (rc = launch_ple_prep_rows(c->pf_proj, slice, c->ple_tab, c->ple_norm, c->pf_ids, M, Lc,
+                                   1.0f / sqrtf((float)H), c->pf_ple, k.eps, st)))
+      return rc;
+  }
+  // layer 0 input norm
+  if ((rc = launch_resnorm_rows(M, c->pf_h, nullptr, 0, 0, nullptr, 1.0f, c->L[0].attn_norm, c->pf_xn, nullptr, H,
+                                k.eps, st)))
+    return rc;
+  const int ks_o = q40_gemm_kslices(QH * HD / 32, kPfKs), ks_d = q40_gemm_kslices(FF / 32, kPfKs);
+  for (int l = 0; l < Lc; ++l) {
+    const Layer& ly = c->L[l];
+    // attention block
+    if ((rc = gemm(q40_view(ly.qkv, c->qkv_rows, H), c->pf_xn, H, GEMM_F32, c->pf_qkv, nullptr, 0, nullptr, 0, 1)))
+      return rc;
+    if ((rc = launch_headprep_rows(c->pf_qkv, 1, 0, ly.q_norm, ly.k_norm, ly.global ? c->inv_global : c->inv_local,
+                                   k.rope_angles, ly.kc, ly.vc, ly.slots, !ly.global, p0, M, c->pf_q, QH, KVH, k.eps,
+                                   st)))
+      return rc;
+    PrefillAttnArgs pa;
+    pa.q = c->pf_q;
+    pa.kc = ly.kc;
+    pa.vc = ly.vc;
+    pa.out = c->pf_attn;
+    pa.M = M;
+    pa.qh = QH;
+    pa.kvh = KVH;
+    pa.slots = ly.slots;
+    pa.window = ly.global ? 0 : k.window;
+    pa.p0 = p0;
+    if ((rc = launch_attn_prefill(pa, st))) return rc;
+    if ((rc = gemm(q40_view(ly.o, H, (int64_t)QH * HD), c->pf_attn, QH * HD, GEMM_F32, c->pf_y, nullptr, 0, nullptr,
+                   0, ks_o)))
+      return rc;
+    // post-attention residual + FFN norm; gate/up + GeGLU; down
+    if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_o, MH, ly.post_attn, 1.0f, ly.ffn_norm, c->pf_xn, nullptr,
+                                  H, k.eps, st)) ||
+        (rc = gemm(q40_view(ly.gu, 2 * (int64_t)FF, H), c->pf_xn, H, GEMM_GLU, nullptr, c->pf_gg, FF, nullptr, 0, 1)) ||
+        (rc = gemm(q40_view(ly.down, H, FF), c->pf_gg, FF, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, ks_d)))
+      return rc;
+    // the last residual of the layer is followed by the next layer's input
+    // norm, or after the last layer by the final norm (as an exact hi/lo
+    // split for the lm-head)
+    const bool lastl = l + 1 == Lc;
+    const float* w_next = lastl ? c->out_norm : c->L[l + 1].attn_norm;
+    uint16_t* x_next = lastl ? c->pf_xhl : c->pf_xn;
+    uint16_t* xlo_next = lastl ? c->pf_xhl + MH : nullptr;
+    if (PD) {
+      // post-FFN residual (x = f16(h)); PLE gate * GELU * per-layer input;
+      // projection; post-PLE residual and layer scalar
+      if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_d, MH, ly.post_ffw, 1.0f, nullptr, c->pf_xn, nullptr, H,
+                                    k.eps, st)) ||
+          (rc = gemm(q40_view(ly.pg, PD, H), c->pf_xn, H, GEMM_GELU_MUL, nullptr, c->pf_gp, 0, c->pf_ple + (int64_t)l * PD,
+                     NP, 1)) ||
+          (rc = gemm(q40_view(ly.pp_rm, H, PD), c->pf_gp, PD, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, 1)) ||
+          (rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, 1, 0, ly.post_norm, ly.scale, w_next, x_next, xlo_next, H,
+                                    k.eps, st)))
+        return rc;
+    } else {
+      if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_d, MH, ly.post_ffw, ly.scale, w_next, x_next, xlo_next, H,
+                                    k.eps, st)))
+        return rc;
+    }
+  }
+  return E4B_OK;
+}
+
+int put_params(e4b_ctx* c, const uint32_t* v, int first, int count);
+
+// batched prefill of ids[0..n) from position 0 in chunks of pf_cap tokens;
+// then the lm-head + argmax of the last token, fed back as the next decode
+// input exactly as the step's feedback does (params[0] = n, params[1] = token)
+int prefill_batched(e4b_ctx* c, const uint32_t* ids, uint32_t n) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden;
+  int rc;
+  int M = 0;
+  for (uint32_t off = 0; off < n; off += (uint32_t)M) {
+    M = (int)((n - off) < (uint32_t)c->pf_cap ? (n - off) : (uint32_t)c->pf_cap);
+    E4B_HIP(hipMemcpyAsync(c->pf_ids, ids + off, (size_t)M * 4, hipMemcpyHostToDevice, c->st));
+    if ((rc = prefill_chunk(c, off, M))) return rc;
+  }
+  const int64_t MH = (int64_t)M * H, last = (int64_t)(M - 1) * H;
+  const Q6Mat E = q6_view(c->embd, k.vocab, H);
+  if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)(c->pf_xhl + last), (const uint32_t*)(c->pf_xhl + MH + last),
+                                   k.softcap, c->logits, nullptr, c->amax_part, c->st)))
+    return rc;
+  const uint32_t p[4] = {n - 1, 0u, 0u, 0u};
+  if ((rc = put_params(c, p, 0, 4))) return rc;
+  if ((rc = launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, c->st)))
+    return rc;
+  float* hdst = c->h_final ? c->h_final : c->h;
+  E4B_HIP(hipMemcpyAsync(hdst, c->pf_h + last, (size_t)H * 4, hipMemcpyDeviceToDevice, c->st));
+  return E4B_OK;
+}
+
 int ready(e4b_ctx* c, const char* fn) {
   if (!c) return e4b_fail(E4B_EINVAL, "%s: null context", fn);
   if (!c->finalized) return e4b_fail(E4B_ESTATE, "%s before e4b_finalize", fn);
@@ -590,11 +757,15 @@ extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t
     return e4b_fail(E4B_ERANGE, "e4b_prefill: %u tokens exceeds the prompt capacity %d", n, c->max_prompt);
   for (uint32_t i = 0; i < n; ++i)
     if (ids[i] >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_prefill: ids[%u] = %u >= vocab", i, ids[i]);
-  E4B_HIP(hipMemcpyAsync(c->prompt, ids, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
-  const uint32_t p[4] = {0u, 0u, 0u, n};
-  if ((rc = put_params(c, p, 0, 4))) return rc;
-  for (uint32_t i = 0; i < n; ++i)
-    if ((rc = launch_token(c))) return rc;
+  if (c->cfg.flags & E4B_FLAG_STEP_PREFILL) {
+    E4B_HIP(hipMemcpyAsync(c->prompt, ids, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
+    const uint32_t p[4] = {0u, 0u, 0u, n};
+    if ((rc = put_params(c, p, 0, 4))) return rc;
+    for (uint32_t i = 0; i < n; ++i)
+      if ((rc = launch_token(c))) return rc;
+  } else if ((rc = prefill_batched(c, ids, n))) {
+    return rc;
+  }
   uint32_t am[2] = {0, 0};
   E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
   if ((rc = check_status(c))) return rc;

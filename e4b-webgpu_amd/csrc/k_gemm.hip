@@ -4,8 +4,9 @@
 // kernels/q40sg.wgsl; here it is an MFMA GEMM).
 //
 //   Y[m][n] = sum_k X[m][k] W[n][k],  W q4_0 [N][K] (repacked planes),
-//   X f16 [M][K] row-major, Y f32 [M][N] (or, with the GeGLU epilogue over
-//   W = [gate; up], f16 [M][FF] = gelu(gate) * up).
+//   X f16 [M][K] row-major (row stride ldx), Y f32 [M][N]; epilogues: split-K
+//   partial slices (Y + z M N, summed by the consumer), the GeGLU over
+//   W = [gate; up] to f16 [M][FF] = gelu(gate) * up, or f16 gelu(y) * mul.
 //
 // v_mfma_f32_32x32x16_f16 with A = a 32-token x 16-k slice of X and B = the
 // 16-k x 32-row slice of W^T: lane l holds A[l % 32][8 (l / 32) + t] (t < 8),
@@ -20,7 +21,11 @@
 //
 // Workgroup: 4 waves x 32 rows (x2 for GeGLU: gate and up tiles), T token
 // tiles of 32 per wave; the X slice of KB blocks for the workgroup's 32 T
-// tokens is staged in LDS and shared by the 4 waves.
+// tokens is staged in LDS and shared by the 4 waves.  blockIdx.z selects a
+// split-K slice.  Row tiles are blockIdx.x, so the workgroups that share a
+// weight tile (same x, different token tiles) sit a multiple of 8 apart in
+// dispatch order when the row-tile count is a multiple of 8: the same XCD and
+// its L2.
 #include "../../include/e4b.h"
 #include "kernels.h"
 #include "util.h"
@@ -47,23 +52,25 @@ DEV h8 nib_word_f16(uint32_t w) {
   return r;
 }
 
-template <int T, bool GLU>
-__global__ __launch_bounds__(256) void k_q40_gemm(Q40Mat W, const uint16_t* __restrict__ X, int M, int K,
-                                                   float* __restrict__ Y, uint16_t* __restrict__ Yh, int64_t ff) {
-  constexpr int NT = GLU ? 2 : 1;          // weight tiles per wave (gate, up)
-  constexpr int TOK = 32 * T;              // tokens per workgroup
+template <int T, int EPI>
+__global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
+  constexpr int NT = EPI == GEMM_GLU ? 2 : 1;  // weight tiles per wave (gate, up)
+  constexpr int TOK = 32 * T;                  // tokens per workgroup
   __shared__ __align__(16) uint4 xs[TOK][KB * 4];  // KB blocks x 64 B per token
+  const Q40Mat& W = a.W;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
   const int nb = K / 32;
-  const int64_t rows = W.rows;
-  const int64_t units = GLU ? ff : rows;   // output columns
+  const int M = a.M;
+  const int64_t units = EPI == GEMM_GLU ? a.ff : W.rows;  // output columns
   const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * 32;  // first output column of this wave
   const int tok0 = blockIdx.y * TOK;
+  const int kz = blockIdx.z;
+  const int kbeg = kz * nbs, kend = min(nb, kbeg + nbs);  // this slice's blocks
   // this lane's weight rows (clamped: tiles past the end compute duplicates, never stored)
   int64_t wrow[NT];
   wrow[0] = min(n0 + l32, units - 1);
-  if constexpr (GLU) wrow[1] = ff + wrow[0];
+  if constexpr (EPI == GEMM_GLU) wrow[1] = a.ff + wrow[0];
   f16v acc[NT][T];
 #pragma unroll
   for (int u = 0; u < NT; ++u)
@@ -72,16 +79,8 @@ __global__ __launch_bounds__(256) void k_q40_gemm(Q40Mat W, const uint16_t* __re
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[u][t][r] = 0.f;
 
-  for (int kb0 = 0; kb0 < nb; kb0 += KB) {
-    // stage X[tok0 .. tok0+TOK)[32 kb0 .. 32 (kb0+KB)) (zeros past M or K)
-    for (int i = threadIdx.x; i < TOK * KB * 4; i += 256) {
-      const int m = i / (KB * 4), q = i % (KB * 4);
-      const int kq = kb0 * 32 + q * 8;  // first k of this 16-byte piece
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (tok0 + m < M && kq < K) v = *reinterpret_cast<const uint4*>(X + (int64_t)(tok0 + m) * K + kq);
-      xs[m][q] = v;
-    }
-    // this lane's weight words and scales for the stage
+  for (int kb0 = kbeg; kb0 < kend; kb0 += KB) {
+    // this lane's weight words and scales for the stage, requested first
     uint32_t wv[NT][KB][2];
     float dsc[NT][KB];
 #pragma unroll
@@ -93,8 +92,16 @@ __global__ __launch_bounds__(256) void k_q40_gemm(Q40Mat W, const uint16_t* __re
         const uint4 w4 = ld_nt_u4_off(W.nib, e);
         wv[u][b][0] = hi ? w4.y : w4.x;  // step 0: word (l / 32)
         wv[u][b][1] = hi ? w4.w : w4.z;  // step 1: word 2 + (l / 32)
-        dsc[u][b] = kb0 + b < nb ? scale_of(ld_scale_pair_off(W.sc, e), e & 1) : 0.f;
+        dsc[u][b] = kb0 + b < kend ? scale_of(ld_scale_pair_off(W.sc, e), e & 1) : 0.f;
       }
+    // stage X[tok0 .. tok0+TOK)[32 kb0 .. 32 (kb0+KB)) (zeros past M or the slice)
+    for (int i = threadIdx.x; i < TOK * KB * 4; i += 256) {
+      const int m = i / (KB * 4), q = i % (KB * 4);
+      const int kq = kb0 * 32 + q * 8;  // first k of this 16-byte piece
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (tok0 + m < M && kq < kend * 32) v = *reinterpret_cast<const uint4*>(a.X + (int64_t)(tok0 + m) * a.ldx + kq);
+      xs[m][q] = v;
+    }
     lds_sync();
 #pragma unroll
     for (int b = 0; b < KB; ++b) {
@@ -130,32 +137,93 @@ __global__ __launch_bounds__(256) void k_q40_gemm(Q40Mat W, const uint16_t* __re
     for (int r = 0; r < 16; ++r) {
       const int m = tok0 + 32 * t + 8 * (r / 4) + 4 * hi + (r % 4);
       if (m < M) {
-        if constexpr (GLU)
-          Yh[(int64_t)m * ff + n] = f2h(gelu_tanh(acc[0][t][r]) * acc[1][t][r]);
+        if constexpr (EPI == GEMM_GLU)
+          a.Yh[(int64_t)m * a.ff + n] = f2h(gelu_tanh(acc[0][t][r]) * acc[1][t][r]);
+        else if constexpr (EPI == GEMM_GELU_MUL)
+          a.Yh[(int64_t)m * W.rows + n] = f2h(gelu_tanh(acc[0][t][r]) * a.mul[(int64_t)m * a.mul_ld + n]);
         else
-          Y[(int64_t)m * rows + n] = acc[0][t][r];
+          a.Y[((int64_t)kz * M + m) * W.rows + n] = acc[0][t][r];
       }
     }
 }
 
+template <int EPI>
+void launch_t(int T, const GemmArgs& a, dim3 grid, int K, int nbs, hipStream_t st) {
+  if (T == 4)
+    hipLaunchKernelGGL((k_q40_gemm<4, EPI>), grid, dim3(256), 0, st, a, K, nbs);
+  else if (T == 2)
+    hipLaunchKernelGGL((k_q40_gemm<2, EPI>), grid, dim3(256), 0, st, a, K, nbs);
+  else
+    hipLaunchKernelGGL((k_q40_gemm<1, EPI>), grid, dim3(256), 0, st, a, K, nbs);
+}
+
 }  // namespace
 
-int launch_q40_gemm(const Q40Mat& W, const uint16_t* X, int M, float* Y, uint16_t* Yh, int64_t ff, hipStream_t st) {
+int q40_gemm_kslices(int nb, int want) {
+  for (int ks = want < 1 ? 1 : want; ks > 1; --ks) {
+    const int nbs = ((nb + ks - 1) / ks + KB - 1) / KB * KB;
+    if ((nb + nbs - 1) / nbs == ks) return ks;
+  }
+  return 1;
+}
+
+int launch_q40_gemm(const GemmArgs& a, hipStream_t st) {
+  const Q40Mat& W = a.W;
   const int K = W.nb * 32;
-  if (M < 1 || K < 32) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: empty operand (M=%d K=%d)", M, K);
+  if (a.M < 1 || K < 32) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: empty operand (M=%d K=%d)", a.M, K);
   if ((uint64_t)W.rows * (uint64_t)W.nb * 16u > 0xffffffffull)
     return e4b_fail(E4B_EINVAL, "q4_0 GEMM: a %lld x %d-block matrix exceeds the 4 GiB plane limit",
                     (long long)W.rows, W.nb);
-  const bool glu = Yh != nullptr;
-  if (glu && (ff < 1 || 2 * ff != W.rows)) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: GeGLU needs 2*ff rows");
-  if (!glu && !Y) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: null output");
-  constexpr int T = 4;
-  const int64_t units = glu ? ff : W.rows;
-  const dim3 grid((unsigned)((units + 127) / 128), (unsigned)((M + 32 * T - 1) / (32 * T)));
-  if (glu)
-    hipLaunchKernelGGL((k_q40_gemm<T, true>), grid, dim3(256), 0, st, W, X, M, K, Y, Yh, ff);
+  if (a.ldx < K || a.ldx % 8) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: x row stride %d (>= %d, multiple of 8)", a.ldx, K);
+  const int ks = a.ks > 0 ? a.ks : 1;
+  if (ks > 1 && a.epi != GEMM_F32) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: split-K needs the f32 epilogue");
+  if (ks > W.nb) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: %d K slices for %d blocks", ks, W.nb);
+  int64_t units = W.rows;
+  switch (a.epi) {
+    case GEMM_F32:
+      if (!a.Y) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: null output");
+      break;
+    case GEMM_GLU:
+      if (!a.Yh || a.ff < 1 || 2 * a.ff != W.rows) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: GeGLU needs 2*ff rows");
+      units = a.ff;
+      break;
+    case GEMM_GELU_MUL:
+      if (!a.Yh || !a.mul) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: GELU-multiply needs yh and mul");
+      break;
+    default: return e4b_fail(E4B_EINVAL, "q4_0 GEMM: epilogue %d", a.epi);
+  }
+  // blocks per split-K slice, a multiple of the LDS stage; the consumer sums
+  // exactly `ks` slices, so every slice must hold blocks
+  const int nbs = ((W.nb + ks - 1) / ks + KB - 1) / KB * KB;
+  const int kslices = (W.nb + nbs - 1) / nbs;
+  if (kslices != ks)
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMM: %d blocks do not split into %d slices (use q40_gemm_kslices)", W.nb, ks);
+  // the widest token tile (4 x 32 tokens per wave: the weight-word
+  // conversion is shared by 4 MFMA pairs) that still gives >= 256 workgroups
+  const int64_t rt = (units + 127) / 128;
+  int T = 4;
+  while (T > 1 && rt * ((a.M + 32 * T - 1) / (32 * T)) * kslices < 256) T >>= 1;
+  const dim3 grid((unsigned)rt, (unsigned)((a.M + 32 * T - 1) / (32 * T)), (unsigned)kslices);
+  if (a.epi == GEMM_GLU)
+    launch_t<GEMM_GLU>(T, a, grid, K, nbs, st);
+  else if (a.epi == GEMM_GELU_MUL)
+    launch_t<GEMM_GELU_MUL>(T, a, grid, K, nbs, st);
   else
-    hipLaunchKernelGGL((k_q40_gemm<T, false>), grid, dim3(256), 0, st, W, X, M, K, Y, Yh, ff);
+    launch_t<GEMM_F32>(T, a, grid, K, nbs, st);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
+}
+
+int launch_q40_gemm(const Q40Mat& W, const uint16_t* X, int M, float* Y, uint16_t* Yh, int64_t ff, hipStream_t st) {
+  GemmArgs a{};
+  a.W = W;
+  a.X = X;
+  a.M = M;
+  a.ldx = W.nb * 32;
+  a.epi = Yh ? GEMM_GLU : GEMM_F32;
+  a.Y = Y;
+  a.Yh = Yh;
+  a.ff = ff;
+  a.ks = 1;
+  return launch_q40_gemm(a, st);
 }

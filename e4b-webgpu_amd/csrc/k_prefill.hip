@@ -1,0 +1,421 @@
+// k_prefill.hip -- the per-token kernels of the batched prefill: M prompt
+// tokens per launch, the same per-token arithmetic as the decode step
+// (src/engine-a4b.js:465-585 encodeLayerPre: "per-token math identical to
+// encodeLayer").  The GEMMs between them are k_gemm.hip.
+//
+//   k_embed_rows      token rows of the Q6_K table * sqrt(H), plus the exact
+//                     f16 hi/lo split for the PLE model projection
+//                     (kernels/q6k.wgsl:37-73 per token)
+//   k_ple_prep_rows   per-layer inputs of every token (kernels/pleprep.wgsl:15-46)
+//   k_resnorm_rows    residual + RMSNorm, one workgroup per token
+//                     (kernels/rmsacc3.wgsl:36-53, kernels/a4btail.wgsl:26-71)
+//   k_headprep_rows   q/k head-RMS + RoPE, v RMS, K/V cache write at the
+//                     token's slot (kernels/headprep.wgsl:19-87 per token)
+//   k_attn_prefill    causal softmax attention of the chunk's queries over
+//                     the cache (kernels/attnf32.wgsl:21-105 /
+//                     kernels/attnos.wgsl:22-98 per query) on the matrix
+//                     cores
+#include "../../include/e4b.h"
+#include "attn_prep.h"
+#include "kernels.h"
+#include "step.h"
+#include "util.h"
+
+namespace {
+
+constexpr int kMaxPer = 16;  // elements per thread of the row kernels (H <= 4096)
+
+// h[m] = E[ids[m]] * mult (f32) and its split hi = f16(h), lo = f16(h - hi)
+// into xhl[0][m] / xhl[1][m]; the expression order is k_embed's
+__global__ __launch_bounds__(256) void k_embed_rows(Q6Mat E, const uint32_t* __restrict__ ids, int M, float mult,
+                                                    float* __restrict__ h, uint16_t* __restrict__ xhl) {
+  const int m = blockIdx.y;
+  const int H = E.nseg * 32;
+  const uint32_t tok = ids[m];  // range-checked by the host
+  for (int s = blockIdx.x * 256 + threadIdx.x; s < E.nseg; s += gridDim.x * 256) {
+    const uint4 a = E.qa[(int64_t)tok * E.nseg + s];
+    const uint2 b = E.qb[(int64_t)tok * E.nseg + s];
+    const float d = h2f(E.d[(int64_t)tok * (E.nseg / 8) + (s >> 3)]);
+    const int8_t* scg = E.sc + (int64_t)tok * (E.nseg * 2) + 2 * s;
+    uint32_t pr[8];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      q6_pairs(gi ? a.z : a.x, gi ? a.w : a.y, gi ? b.y : b.x, pr);
+      const float ds = d * (float)scg[gi];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int e = 32 * s + 16 * gi + 2 * i + u;
+          const float v = ds * (float)((int)((pr[i] >> (16 * u)) & 0x3f) - 32) * mult;
+          const int64_t o = (int64_t)m * H + e;
+          h[o] = v;
+          const _Float16 hi = (_Float16)v;
+          xhl[o] = __builtin_bit_cast(uint16_t, hi);
+          xhl[(int64_t)M * H + o] = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)hi));
+        }
+      }
+    }
+  }
+}
+
+// ggml Q6_K element e (0..255) of one superblock (kernels/q6k.wgsl:44-71 order)
+DEV float q6k_elem(const uint8_t* blk, int e) {
+  const int half = e >> 7, r = e & 127, quad = r >> 5, l = r & 31;
+  const uint8_t* ql = blk + 64 * half;
+  const uint8_t* qh = blk + 128 + 32 * half;
+  int q = (quad & 1) ? ql[l + 32] : ql[l];
+  q = (quad >= 2) ? (q >> 4) : (q & 15);
+  q |= ((qh[l] >> (2 * quad)) & 3) << 4;
+  const int is = 8 * half + (l >> 4) + 2 * quad;
+  const float d = h2f((uint16_t)(blk[208] | (blk[209] << 8)));
+  return d * (float)(int8_t)blk[192 + is] * (float)(q - 32);
+}
+
+// block (b, m): ple[m][b] = (rms(proj_m,b * H^-1/2) * w_pn + table_row_b(ids[m])
+// * sqrt(PD)) * 2^-1/2, PD = 256; proj holds two partial products (the hi
+// and lo halves of the input) that are summed first
+__global__ __launch_bounds__(256) void k_ple_prep_rows(const float* __restrict__ proj, int64_t slice,
+                                                       const uint8_t* __restrict__ table,
+                                                       const float* __restrict__ w_pn,
+                                                       const uint32_t* __restrict__ ids, int L, float proj_scale,
+                                                       float* __restrict__ ple, float eps) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const int64_t o = (int64_t)m * L * 256 + b * 256 + t;
+  const float pv = (proj[o] + proj[slice + o]) * proj_scale;
+  const float wn = w_pn[t];
+  const uint8_t* blk = table + ((int64_t)ids[m] * L + b) * 210;
+  const float idv = q6k_elem(blk, t) * 16.0f;  // sqrt(PD), PD = 256
+  const float inv = rms_inv(block_sum(pv * pv, red), 256, eps);
+  ple[o] = (pv * inv * wn + idv) * 0.70710678118654752f;
+}
+
+// one workgroup per token m:
+//   h = (h + rms(a) * w1) * scale, a = sum of na partial slices (a may be null)
+//   w2 != null: x = f16(rms(h) * w2), else x = f16(h); with xlo the value is
+//   stored as the exact split x = f16(y), xlo = f16(y - x) (the lm-head input)
+template <int PER>
+__global__ __launch_bounds__(256) void k_resnorm_rows(float* __restrict__ h, const float* __restrict__ a, int na,
+                                                      int64_t slice, const float* __restrict__ w1, float scale,
+                                                      const float* __restrict__ w2, uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ xlo, int H, float eps) {
+  __shared__ float red[4];
+  const int m = blockIdx.x;
+  float* hm = h + (int64_t)m * H;
+  float hv[PER], av[PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    hv[k] = i < H ? hm[i] : 0.f;
+    float s = 0.f;
+    if (a && i < H) {
+      s = a[(int64_t)m * H + i];
+      for (int z = 1; z < na; ++z) s += a[z * slice + (int64_t)m * H + i];
+    }
+    av[k] = s;
+    ss = fmaf(s, s, ss);
+  }
+  if (a) {
+    const float inv1 = rms_inv(block_sum(ss, red), H, eps);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      hv[k] = i < H ? hv[k] + av[k] * inv1 * w1[i] : 0.f;
+    }
+  }
+  float s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    hv[k] *= scale;
+    s2 = fmaf(hv[k], hv[k], s2);
+  }
+  const float inv2 = w2 ? rms_inv(block_sum(s2, red), H, eps) : 1.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < H) {
+      hm[i] = hv[k];
+      const float y = w2 ? hv[k] * inv2 * w2[i] : hv[k];
+      const _Float16 yh = (_Float16)y;
+      x[(int64_t)m * H + i] = __builtin_bit_cast(uint16_t, yh);
+      if (xlo) xlo[(int64_t)m * H + i] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)yh));
+    }
+  }
+}
+
+// one wave per (head row hh, token m): the qkv row is the sum of ks partial
+// slices; q heads -> q[m][hh] (f32), k heads -> key cache, v heads -> value
+// cache, at the slot of position p0 + m (ring slot for a sliding layer)
+__global__ __launch_bounds__(64) void k_headprep_rows(const float* __restrict__ qkv, int ks, int64_t slice,
+                                                      const float* __restrict__ qw, const float* __restrict__ kw,
+                                                      const float* __restrict__ inv_freq, int angles, uint16_t* kc,
+                                                      uint16_t* vc, int slots, int ring, uint32_t p0,
+                                                      float* __restrict__ q, int qh, int kvh, float eps) {
+  const int hh = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const int rows = (qh + 2 * kvh) * 256;
+  const float* src = qkv + (int64_t)m * rows + hh * 256 + 4 * lane;
+  float4 v = *reinterpret_cast<const float4*>(src);
+  for (int z = 1; z < ks; ++z) {
+    const float4 t = *reinterpret_cast<const float4*>(src + z * slice);
+    v.x += t.x;
+    v.y += t.y;
+    v.z += t.z;
+    v.w += t.w;
+  }
+  float x[4] = {v.x, v.y, v.z, v.w};
+  const bool isq = hh < qh, isk = !isq && hh < qh + kvh;
+  const float* wsrc = isq ? qw : kw;
+  const float4 wv = *reinterpret_cast<const float4*>(wsrc + 4 * lane);
+  const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+  const float2 cs[4] = {};
+  const uint32_t pos = p0 + (uint32_t)m;
+  prep_head_regs(x, w, isq || isk, cs, false, inv_freq, angles, eps, (float)pos, isq || isk);
+  if (isq) {
+    *reinterpret_cast<float4*>(q + ((int64_t)m * qh + hh) * 256 + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
+    return;
+  }
+  const int g = isk ? hh - qh : hh - qh - kvh;
+  const int64_t slot = ring ? (int64_t)(pos % (uint32_t)slots) : (int64_t)pos;
+  uint16_t* dst = (isk ? kc : vc) + ((int64_t)g * slots + slot) * 256 + 4 * lane;
+  *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
+                                             (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
+}
+
+// ---- causal attention of a prefill chunk on the matrix cores ----------------
+//
+// Workgroup (KV group g, tile of 16 queries); wave w = q head 4g + w, so the
+// four heads of a group share each K/V tile staged in LDS.  Key tiles of 32
+// positions walk the union of the tile's windows; per query the live keys
+// are (qp - W, qp] (sliding) or [0, qp] (global), scale 1.0.
+//
+// v_mfma_f32_16x16x32_f16 (lane l: A[l % 16][8 (l / 16) + t], B[8 (l / 16) +
+// t][l % 16], D[4 (l / 16) + r][l % 16]):
+//   S^T (16 keys x 16 queries) = K . Q^T over 8 steps of 32 dims; Q (f32) is
+//   an exact-sum f16 pair hi + lo, K is f16, so two MFMAs give q.k to ~2^-22.
+//   After the online-softmax update each lane holds P^T for its query
+//   (column l % 16) and 8 keys: 4 (l / 16) + r of sub-tile 0 and 16 + 4 (l /
+//   16) + r of sub-tile 1 -- exactly a B operand of a 32-key MFMA when the A
+//   operand (V^T, 16 dims x 32 keys, read from a transposed V tile in LDS)
+//   uses the same key order.  O^T (dims x queries) accumulates P_hi and
+//   P_lo (P = P_hi + P_lo) against V in f32, so every product is as exact
+//   as the decode kernel's f32 arithmetic.
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kKT = 32;            // keys per tile
+constexpr int kKsStride = 256 + 8; // halfs per K row in LDS
+constexpr int kVtStride = kKT + 8; // halfs per transposed V row in LDS
+
+DEV void split8(const float (&v)[8], h8v& hi, h8v& lo) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const _Float16 a = (_Float16)v[t];
+    hi[t] = a;
+    lo[t] = (_Float16)(v[t] - (float)a);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
+  __shared__ __align__(16) uint16_t ks[kKT * kKsStride];
+  __shared__ __align__(16) uint16_t vt[256 * kVtStride];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = blockIdx.x, q0 = blockIdx.y * 16;
+  const int head = 4 * g + wave;
+  const int j = lane & 15, qq = lane >> 4;
+  const int M = A.M;
+  const int qi = q0 + j;                      // this lane's query (column)
+  const int qp = (int)A.p0 + min(qi, M - 1);  // its position
+  const int P0 = (int)A.p0 + q0, P1 = (int)A.p0 + min(q0 + 16, M) - 1;
+  const int W = A.window;
+  const int klo = W > 0 ? max(0, P0 - W + 1) : 0;
+  const uint16_t* kc = A.kc + (int64_t)g * A.slots * 256;
+  const uint16_t* vc = A.vc + (int64_t)g * A.slots * 256;
+
+  // Q^T as the B operand: step s covers dims 32 s + 8 qq .. + 8
+  h8v qh_[8], ql_[8];
+  {
+    const float* qrow = A.q + ((int64_t)min(qi, M - 1) * A.qh + head) * 256;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * s + 8 * qq);
+      const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * s + 8 * qq + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      split8(v, qh_[s], ql_[s]);
+    }
+  }
+  f4v o[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) o[dt] = f4v{0.f, 0.f, 0.f, 0.f};
+  float mrun = -3.0e38f, lrun = 0.f;
+
+  for (int kb = klo; kb <= P1; kb += kKT) {
+    // stage keys kb .. kb + 31 (rows past P1 repeat row P1; they are masked)
+    lds_sync();
+    {
+      const int t = threadIdx.x;
+      // K: 8 threads per row, 64 bytes each
+      const int kr = t >> 3, part = t & 7;
+      const int kp = min(kb + kr, P1);
+      const int64_t sk = W > 0 ? (int64_t)(kp % A.slots) : (int64_t)kp;
+      const uint4* srck = reinterpret_cast<const uint4*>(kc + sk * 256 + 32 * part);
+      uint4* dstk = reinterpret_cast<uint4*>(ks + kr * kKsStride + 32 * part);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dstk[i] = srck[i];
+      // V: thread (key pair kp2, dim chunk dc) transposes 2 keys x 16 dims
+      const int kp2 = t >> 4, dc = t & 15;
+      const int pa = min(kb + 2 * kp2, P1), pb = min(kb + 2 * kp2 + 1, P1);
+      const int64_t sa = W > 0 ? (int64_t)(pa % A.slots) : (int64_t)pa;
+      const int64_t sb = W > 0 ? (int64_t)(pb % A.slots) : (int64_t)pb;
+      const uint4* va = reinterpret_cast<const uint4*>(vc + sa * 256 + 16 * dc);
+      const uint4* vb = reinterpret_cast<const uint4*>(vc + sb * 256 + 16 * dc);
+      const uint4 a0 = va[0], a1 = va[1], b0 = vb[0], b1 = vb[1];
+      const uint32_t aw[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t lo2 = (aw[i] & 0xffffu) | (bw[i] << 16);
+        const uint32_t hi2 = (aw[i] >> 16) | (bw[i] & 0xffff0000u);
+        *reinterpret_cast<uint32_t*>(vt + (16 * dc + 2 * i) * kVtStride + 2 * kp2) = lo2;
+        *reinterpret_cast<uint32_t*>(vt + (16 * dc + 2 * i + 1) * kVtStride + 2 * kp2) = hi2;
+      }
+    }
+    lds_sync();
+    // S^T for the two 16-key sub-tiles
+    f4v sc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f4v d = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = ks + (16 * kt + j) * kKsStride + 8 * qq;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const h8v ka = __builtin_bit_cast(h8v, *reinterpret_cast<const uint4*>(krow + 32 * s));
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh_[s], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql_[s], d, 0, 0, 0);
+      }
+      sc[kt] = d;
+    }
+    // mask, online softmax (per query column; its 32 scores sit in the four
+    // lanes j, j + 16, j + 32, j + 48)
+    float p[8];
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kp = kb + 16 * kt + 4 * qq + r;
+        const bool live = qi < M && kp <= qp && kp <= P1 && (W == 0 || kp > qp - W);
+        p[4 * kt + r] = live ? sc[kt][r] : -3.0e38f;
+        mx = fmaxf(mx, p[4 * kt + r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(mrun, mx);
+    const float alpha = __expf(mrun - mnew);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = p[i] > -1.0e38f ? __expf(p[i] - mnew) : 0.f;
+      ps += p[i];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    lrun = lrun * alpha + ps;
+    mrun = mnew;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
+    h8v phi, plo;
+    split8(p, phi, plo);
+    // O^T += V^T P^T: A = V^T rows 16 dt + j, keys 4 qq .. +3 and 16 + 4 qq .. +3
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const uint16_t* vrow = vt + (16 * dt + j) * kVtStride;
+      const uint2 va = *reinterpret_cast<const uint2*>(vrow + 4 * qq);
+      const uint2 vb = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * qq);
+      const h8v vv = __builtin_bit_cast(h8v, make_uint4(va.x, va.y, vb.x, vb.y));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, phi, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, plo, o[dt], 0, 0, 0);
+    }
+  }
+  if (qi >= M) return;
+  const float inv = 1.f / lrun;
+  uint16_t* dst = A.out + ((int64_t)qi * A.qh + head) * 256 + 4 * qq;
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) {
+    const uint32_t lo2 = (uint32_t)f2h(o[dt][0] * inv) | ((uint32_t)f2h(o[dt][1] * inv) << 16);
+    const uint32_t hi2 = (uint32_t)f2h(o[dt][2] * inv) | ((uint32_t)f2h(o[dt][3] * inv) << 16);
+    *reinterpret_cast<uint2*>(dst + 16 * dt) = make_uint2(lo2, hi2);
+  }
+}
+
+template <int PER>
+void launch_resnorm_per(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
+                        const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st) {
+  hipLaunchKernelGGL((k_resnorm_rows<PER>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps);
+}
+
+}  // namespace
+
+int launch_embed_rows(const Q6Mat& E, const uint32_t* ids, int M, float mult, float* h, uint16_t* xhl, hipStream_t st) {
+  if (M < 1) return e4b_fail(E4B_EINVAL, "embed rows: M = %d", M);
+  hipLaunchKernelGGL(k_embed_rows, dim3((E.nseg + 255) / 256, M), dim3(256), 0, st, E, ids, M, mult, h, xhl);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_ple_prep_rows(const float* proj, int64_t slice, const uint8_t* table, const float* w_pn,
+                         const uint32_t* ids, int M, int L, float proj_scale, float* ple, float eps, hipStream_t st) {
+  hipLaunchKernelGGL(k_ple_prep_rows, dim3(L, M), dim3(256), 0, st, proj, slice, table, w_pn, ids, L, proj_scale, ple,
+                     eps);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_resnorm_rows(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
+                        const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st) {
+  if (H < 1 || H > 256 * kMaxPer) return e4b_fail(E4B_EINVAL, "resnorm rows: hidden %d outside 1..%d", H, 256 * kMaxPer);
+  if (a && (na < 1 || !w1)) return e4b_fail(E4B_EINVAL, "resnorm rows: %d residual slices", na);
+  if (H <= 256)
+    launch_resnorm_per<1>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
+  else if (H <= 512)
+    launch_resnorm_per<2>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
+  else if (H <= 1024)
+    launch_resnorm_per<4>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
+  else if (H <= 2048)
+    launch_resnorm_per<8>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
+  else
+    launch_resnorm_per<kMaxPer>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* qw, const float* kw,
+                         const float* inv_freq, int angles, uint16_t* kc, uint16_t* vc, int slots, bool ring,
+                         uint32_t p0, int M, float* q, int qh, int kvh, float eps, hipStream_t st) {
+  if (qh != 4 * kvh) return e4b_fail(E4B_EINVAL, "headprep rows: %d q heads for %d kv heads", qh, kvh);
+  if (!ring && (int64_t)p0 + M > slots)
+    return e4b_fail(E4B_ERANGE, "headprep rows: positions [%u, %lld) beyond %d slots", p0, (long long)p0 + M, slots);
+  hipLaunchKernelGGL(k_headprep_rows, dim3(qh + 2 * kvh, M), dim3(64), 0, st, qkv, ks, slice, qw, kw, inv_freq, angles,
+                     kc, vc, slots, ring ? 1 : 0, p0, q, qh, kvh, eps);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t st) {
+  if (a.qh != 4 * a.kvh) return e4b_fail(E4B_EINVAL, "prefill attention: %d q heads for %d kv heads", a.qh, a.kvh);
+  if (a.M < 1) return e4b_fail(E4B_EINVAL, "prefill attention: M = %d", a.M);
+  if (a.window > 0) {
+    // every key a query of the chunk needs must still own its ring slot
+    // after the chunk's own writes: slots >= window + M - 1 (the Complete
+    // condition of specs/KVRing.tla with C = M)
+    if ((int64_t)a.slots < (int64_t)a.window + a.M - 1)
+      return e4b_fail(E4B_EINVAL, "prefill attention: %d ring slots < window %d + chunk %d - 1", a.slots, a.window,
+                      a.M);
+  } else if ((int64_t)a.p0 + a.M > a.slots) {
+    return e4b_fail(E4B_ERANGE, "prefill attention: positions beyond %d slots", a.slots);
+  }
+  hipLaunchKernelGGL(k_attn_prefill, dim3(a.kvh, (a.M + 15) / 16), dim3(256), 0, st, a);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}

@@ -100,6 +100,27 @@ bool q40_prologue_supported(int H);
 // batched q4_0 GEMM on the matrix cores (k_gemm.hip): Y f32 [M][rows], or
 // with Yh the GeGLU over [gate; up] rows to f16 [M][ff]
 int launch_q40_gemm(const Q40Mat& W, const uint16_t* X, int M, float* Y, uint16_t* Yh, int64_t ff, hipStream_t st);
+enum GemmEpi {
+  GEMM_F32 = 0,       // Y[(z M + m) rows + n]: split-K slice z of ks (ks = 1: the product)
+  GEMM_GLU = 1,       // rows [0,ff) gate, [ff,2ff) up: Yh[m ff + i] = f16(gelu(g) * u)
+  GEMM_GELU_MUL = 2,  // Yh[m rows + n] = f16(gelu(y) * mul[m mul_ld + n])
+};
+struct GemmArgs {
+  Q40Mat W;
+  const uint16_t* X;  // f16 [M][ldx], 16-byte aligned rows
+  int M, ldx;
+  int epi;
+  float* Y;
+  uint16_t* Yh;
+  int64_t ff;
+  const float* mul;
+  int64_t mul_ld;
+  int ks;             // split-K slices (GEMM_F32)
+};
+int launch_q40_gemm(const GemmArgs& a, hipStream_t st);
+// the largest split-K slice count <= want that cuts nb blocks into whole
+// slices (what GemmArgs::ks must be)
+int q40_gemm_kslices(int nb, int want);
 int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi, const GemvOut& o, int ks,
                hipStream_t st, const ProArgs* pro = nullptr);
 int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, float* y, hipStream_t st);

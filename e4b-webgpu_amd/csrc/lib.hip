@@ -256,6 +256,26 @@ extern "C" int e4b_rope_inv_freq(float theta, int head_dim, int angles, float* o
   return E4B_OK;
 }
 
+extern "C" int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc, void* out, int m, int q_heads,
+                                  int kv_heads, int slots, int window, uint32_t p0, void* stream) {
+  if (!q || !kc || !vc || !out || m <= 0 || q_heads <= 0 || kv_heads <= 0 || slots <= 0 || window < 0)
+    return e4b_fail(E4B_EINVAL, "e4b_k_attn_prefill: bad arguments");
+  if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out))
+    return e4b_fail(E4B_EINVAL, "e4b_k_attn_prefill: buffers must be 16-byte aligned");
+  PrefillAttnArgs a;
+  a.q = q;
+  a.kc = (const uint16_t*)kc;
+  a.vc = (const uint16_t*)vc;
+  a.out = (uint16_t*)out;
+  a.M = m;
+  a.qh = q_heads;
+  a.kvh = kv_heads;
+  a.slots = slots;
+  a.window = window;
+  a.p0 = p0;
+  return launch_attn_prefill(a, (hipStream_t)stream);
+}
+
 extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const float* k_norm, const float* inv_freq,
                                  int rope_angles, void* k_cache, void* v_cache, int q_heads, int kv_heads,
                                  int head_dim, int slots, int window, uint32_t pos, float eps, int chunk,

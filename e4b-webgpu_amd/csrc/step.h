@@ -52,3 +52,30 @@ int launch_ple_prep(const float* proj, const uint8_t* table, const float* w_pn, 
                     const float* w_attn0, uint16_t* xn, int H, float eps, hipStream_t st);
 int launch_feedback(const uint2* part, int nparts, uint32_t* amax, uint32_t* params, uint32_t* tok_ring, int ring_cap,
                     hipStream_t st);
+
+// ---- batched prefill (k_prefill.hip) -----------------------------------------
+// h[m] = E[ids[m]] * mult; xhl = [hi][M][H] then [lo][M][H] f16 split of h
+int launch_embed_rows(const Q6Mat& E, const uint32_t* ids, int M, float mult, float* h, uint16_t* xhl, hipStream_t st);
+// proj: two partial slices [M][L*256] at distance `slice`
+int launch_ple_prep_rows(const float* proj, int64_t slice, const uint8_t* table, const float* w_pn,
+                         const uint32_t* ids, int M, int L, float proj_scale, float* ple, float eps, hipStream_t st);
+// per token: h = (h + rms(sum of na slices of a) * w1) * scale (a may be
+// null); x = f16(rms(h) * w2) (w2 null: f16(h)); xlo (may be null) = the low
+// half of the exact f16 split of the same value
+int launch_resnorm_rows(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
+                        const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st);
+// qkv: ks partial slices [M][(qh + 2 kvh) 256]; q out [M][qh][256] f32; K/V
+// rows of positions p0 .. p0 + M - 1 written to the caches (ring: slot p % slots)
+int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* qw, const float* kw,
+                         const float* inv_freq, int angles, uint16_t* kc, uint16_t* vc, int slots, bool ring,
+                         uint32_t p0, int M, float* q, int qh, int kvh, float eps, hipStream_t st);
+struct PrefillAttnArgs {
+  const float* q;     // [M][qh][256] prepped queries of positions p0 .. p0 + M - 1
+  const uint16_t* kc; // [kvh][slots][256]
+  const uint16_t* vc;
+  uint16_t* out;      // [M][qh * 256] f16
+  int M, qh, kvh, slots;
+  int window;         // 0 = global layer
+  uint32_t p0;
+};
+int launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t st);

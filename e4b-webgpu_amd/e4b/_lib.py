@@ -90,6 +90,7 @@ SIGNATURES = [
     ("e4b_k_moe_layer", _i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     ("e4b_k_attn_decode", _i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _u32, _f32,
                                  _i32, _vp, _vp]),
+    ("e4b_k_attn_prefill", _i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _u32, _vp]),
     ("e4b_create", _vp, [_vp]),
     ("e4b_set_tensor", _i32, [_vp, C.c_char_p, _i32, _P(_i64), _i32, _vp, _sz]),
     ("e4b_finalize", _i32, [_vp]),
@@ -119,6 +120,7 @@ class ConfigC(C.Structure):
 
 
 FLAG_NO_GRAPH = 1
+FLAG_STEP_PREFILL = 2
 
 
 class MoeWeightsC(C.Structure):

@@ -182,6 +182,22 @@ class AttnLayer:
         return self.out.download(np.float16, self.qh * self.hd)
 
 
+def attn_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, window: int, p0: int) -> np.ndarray:
+    """Causal attention of a prefill chunk (e4b_k_attn_prefill): q f32
+    [m][q_heads][256] at positions p0 .. p0 + m - 1, caches f16
+    [kv_heads][slots][256] holding every key needed; returns f16 [m][q_heads * 256]."""
+    q = np.ascontiguousarray(q, np.float32)
+    m, qh, hd = q.shape
+    kvh, slots, _ = k_cache.shape
+    qd = DeviceBuffer.from_array(q)
+    kd = DeviceBuffer.from_array(np.ascontiguousarray(k_cache, np.float16))
+    vd = DeviceBuffer.from_array(np.ascontiguousarray(v_cache, np.float16))
+    od = DeviceBuffer(m * qh * hd * 2)
+    check(lib.e4b_k_attn_prefill(_vp(qd), _vp(kd), _vp(vd), _vp(od), m, qh, kvh, slots, window, p0, _vp(None)),
+          "e4b_k_attn_prefill")
+    return od.download(np.float16, m * qh * hd).reshape(m, qh * hd)
+
+
 class MoeLayer:
     """An A4B-style MoE FFN half-layer resident on the device.
 

@@ -218,6 +218,18 @@ int e4b_k_router_top8(const e4b_moe_weights* w, const float* h, uint32_t* topk_i
 int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* h_out, uint32_t* topk_idx,
                     float* topk_w, float* dense_out, float* moe_out, void* stream);
 
+/* Causal attention of a prefill chunk (attnB / attnOSB of the reference's
+ * batched prefill, src/engine-a4b.js:476-477; per query the arithmetic of
+ * kernels/attnf32.wgsl:21-105 and kernels/attnos.wgsl:22-98, scale 1.0):
+ *   q    f32[m][q_heads][256], prepped queries of positions p0 .. p0 + m - 1
+ *   kc/vc f16[kv_heads][slots][256] caches already holding every key the
+ *        queries attend to (position p in slot p % slots when window > 0)
+ *   out  f16[m][q_heads * 256]
+ * window > 0: keys (p - window, p] of a ring with slots >= window + m - 1;
+ * window == 0: keys [0, p], p0 + m <= slots.  q_heads = 4 * kv_heads. */
+int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc, void* out, int m, int q_heads, int kv_heads,
+                       int slots, int window, uint32_t p0, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Engine: the per-token batch-1 decode step of an E4B-shaped decoder
  * (35 layers, 4 sliding : 1 global, GeGLU FFN, per-layer embeddings, q4_0
@@ -255,6 +267,9 @@ typedef struct e4b_config {
 /* launch the step's kernels directly each token instead of replaying the
  * captured hipGraph (same kernels; for profilers that do not follow graphs) */
 #define E4B_FLAG_NO_GRAPH 1u
+/* prefill token by token through the decode step (one graph replay per
+ * prompt token) instead of the batched prefill */
+#define E4B_FLAG_STEP_PREFILL 2u
 
 /* tensor names follow the GGUF naming of the E4B family:
  *   token_embd.weight (Q6_K [vocab][hidden], tied lm-head), output_norm.weight,
@@ -272,8 +287,14 @@ int  e4b_finalize(e4b_ctx* ctx);              /* allocates KV/activations, captu
 /* one token at `pos` (positions must be fed in order from 0); logits may be
  * NULL; argmax_out may be NULL */
 int  e4b_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, float* logits_or_null, uint32_t* argmax_out);
-/* token-by-token prefill of ids[0..n) from position 0; argmax_out = greedy
- * continuation of the last prompt token */
+/* prefill of ids[0..n) from position 0 (prefill, src/engine-a4b.js:550-584):
+ * chunks of up to 512 tokens (and at most ring - window + 1, so every key a
+ * chunk's queries need keeps its ring slot), each layer as batched q4_0
+ * GEMMs on the matrix cores plus per-token head prep, causal attention and
+ * norms; the lm-head runs once, for the last token.  argmax_out = greedy
+ * continuation of the last prompt token, which is also fed back as the next
+ * e4b_decode input.  E4B_FLAG_STEP_PREFILL runs the prompt through the decode
+ * step instead. */
 int  e4b_prefill(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* argmax_out);
 /* GPU-fed greedy decode of `count` tokens starting at start_pos, fed with the
  * previous step's argmax; tokens_out[count] */

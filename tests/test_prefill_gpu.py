@@ -1,0 +1,160 @@
+"""GPU parity of the batched prefill (MFMA GEMMs + per-token kernels) with the
+CPU oracle.
+
+Attention kernel (e4b_k_attn_prefill): each query of a chunk at position p
+against orc.attn_linear (global layer, keys [0, p]) or orc.attn_ring
+(sliding ring with slot-scan position recovery, kernels/attnf32.wgsl) over the
+same cache, including slots that already hold the chunk's later positions --
+the ring is sized so every live key keeps its slot (ring >= window + M - 1),
+and the recovered position of a later key is never live.  Tolerance: within
+ATTN_TOL of max|out| (f16 output, as the decode attention test).
+
+Engine: e4b_prefill (batched, several chunks when the prompt exceeds
+ring - window + 1) in lock-step with the oracle's token-by-token step
+(tests/test_engine_gpu.py tolerances: greedy tokens bit-exact outside
+near-ties, logits within 1e-3 of the logit range, KV caches within 1e-2 max /
+1e-3 mean relative), and against the engine's own token-by-token prefill
+(E4B_FLAG_STEP_PREFILL) at E4B width with a 512-token prompt.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from e4b._lib import FLAG_STEP_PREFILL
+from e4b.engine import Engine
+from e4b.kernels import attn_prefill
+from e4b.model import E4BConfig, norm_weights_random, synth_tensors, tiny_config
+from tests.test_engine_gpu import KV_MAX_TOL, KV_MEAN_TOL, LOGIT_TOL, TIE_TOL, build, lockstep
+from tests.util import top2_margin
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 2e-3
+HD = 256
+
+
+@pytest.mark.parametrize("kvh,slots,window,p0,m,seed", [
+    (2, 4096, 0, 0, 512, 1),      # c4 prompt, global layer
+    (2, 4096, 0, 1000, 100, 2),   # a later chunk of a global layer
+    (2, 1024, 512, 0, 513, 3),    # the largest chunk a 1024-slot ring allows
+    (2, 1024, 512, 900, 200, 4),  # ring wraps inside the chunk
+    (2, 1024, 512, 3000, 37, 5),  # ragged chunk deep in the ring
+    (1, 64, 32, 100, 33, 6),      # small ring at its chunk limit, one KV group
+    (2, 1024, 512, 7, 1, 7),      # a single token
+])
+def test_attn_prefill(kvh, slots, window, p0, m, seed):
+    qh = 4 * kvh
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((m, qh, HD)).astype(np.float32)
+    k = (0.25 * rng.standard_normal((kvh, slots, HD))).astype(np.float16)
+    v = rng.standard_normal((kvh, slots, HD)).astype(np.float16)
+    got = attn_prefill(q, k, v, window, p0).astype(np.float64)
+    ko = np.ascontiguousarray(k.transpose(1, 0, 2)).view(np.uint16)  # oracle layout [slot][kvh][hd]
+    vo = np.ascontiguousarray(v.transpose(1, 0, 2)).view(np.uint16)
+    worst = 0.0
+    for i in range(m):
+        pos = p0 + i
+        if window:
+            want = orc.attn_ring(q[i].ravel(), ko, vo, qh, kvh, HD, slots, window, pos)
+        else:
+            want = orc.attn_linear(q[i].ravel(), ko, vo, qh, kvh, HD, pos + 1)
+        want = want.view(np.float16).astype(np.float64)
+        err = np.abs(got[i] - want).max() / np.abs(want).max()
+        worst = max(worst, err)
+        assert err < ATTN_TOL, f"query {i} (pos {pos}): rel err {err:.3e}"
+    print(f"attn prefill kvh={kvh} slots={slots} window={window} p0={p0} m={m}: worst rel err {worst:.2e}")
+
+
+def test_attn_prefill_rejects_short_ring():
+    q = np.zeros((40, 8, HD), np.float32)
+    k = np.zeros((2, 64, HD), np.float16)
+    with pytest.raises(Exception):
+        attn_prefill(q, k, k, 32, 0)  # 64 slots < 32 + 40 - 1
+
+
+def _kv_check(eng, om, cfg, layer):
+    k, v = eng.read_kv(layer)
+    slots = k.shape[1]
+    ok = om.kcache(layer, slots * cfg.kv_heads * cfg.head_dim).reshape(slots, cfg.kv_heads, cfg.head_dim)
+    ov = om.vcache(layer, slots * cfg.kv_heads * cfg.head_dim).reshape(slots, cfg.kv_heads, cfg.head_dim)
+    ok, ov = ok.transpose(1, 0, 2), ov.transpose(1, 0, 2)
+    assert np.array_equal(np.any(k != 0, axis=(0, 2)), np.any(ok != 0, axis=(0, 2))), f"layer {layer}: written slots"
+    for a, b in ((k, ok), (v, ov)):
+        fa = a.view(np.float16).astype(np.float64)
+        fb = b.view(np.float16).astype(np.float64)
+        d = np.abs(fa - fb)
+        assert d.max() <= KV_MAX_TOL * np.abs(fb).max(), f"layer {layer} cache values (max)"
+        assert d.mean() <= KV_MEAN_TOL * np.abs(fb).mean(), f"layer {layer} cache values (mean)"
+
+
+@pytest.mark.parametrize("n_prompt", [1, 9, 40])
+def test_tiny_batched_prefill_lockstep(n_prompt):
+    # tiny config: window 8, ring 16 -> chunks of 9 tokens; 40 tokens = five
+    # chunks with the ring wrapping twice
+    cfg = tiny_config()
+    eng, om = build(cfg, 31 + n_prompt)
+    prompt = np.random.default_rng(n_prompt).integers(0, cfg.vocab, n_prompt)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 10)
+    print(f"tiny batched prefill {n_prompt}: near-ties {ties}")
+    assert len(ties) == 0
+    err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
+    assert err < LOGIT_TOL
+    for layer in range(cfg.layers):
+        _kv_check(eng, om, cfg, layer)
+
+
+def test_tiny_batched_prefill_hidden_and_logits():
+    # after the prefill alone: the last token's hidden state and logits
+    cfg = tiny_config(layers=3, layer_global=[0, 1, 0])
+    eng, om = build(cfg, 77)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 23)
+    g = eng.prefill(prompt)
+    for i, t in enumerate(prompt):
+        o_tok, o_lg, o_h = om.step(int(t), i, want_logits=True, want_hidden=True)
+    lg = eng.read_logits()
+    err = float(np.max(np.abs(lg - o_lg)) / np.max(np.abs(o_lg)))
+    herr = float(np.max(np.abs(eng.read_hidden() - o_h)) / np.max(np.abs(o_h)))
+    print(f"tiny prefill-only logits err {err:.2e} hidden err {herr:.2e}")
+    assert err < LOGIT_TOL and herr < LOGIT_TOL
+    assert g == o_tok or top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max()
+    assert eng.argmax_fast() == g
+
+
+def test_tiny_no_ple_batched_prefill():
+    cfg = tiny_config(ple_dim=0)
+    eng, om = build(cfg, 55)
+    prompt = np.random.default_rng(6).integers(0, cfg.vocab, 20)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 6)
+    assert len(ties) == 0
+    for layer in range(cfg.layers):
+        _kv_check(eng, om, cfg, layer)
+
+
+def test_c4_width_prefill_matches_step_prefill():
+    # E4B width (5 layers, one global): 512-token prompt through the batched
+    # prefill and through the decode step; same continuation, logits and KV
+    cfg = E4BConfig(layers=5, max_seq=1024, layer_global=[0, 0, 0, 0, 1])
+    tensors = norm_weights_random(synth_tensors(cfg, 13), 14)
+    a = Engine(cfg, tensors)
+    b = Engine(E4BConfig(layers=5, max_seq=1024, layer_global=[0, 0, 0, 0, 1], flags=FLAG_STEP_PREFILL), tensors)
+    prompt = np.random.default_rng(15).integers(0, cfg.vocab, 512)
+    ga, gb = a.prefill(prompt), b.prefill(prompt)
+    la, lb = a.read_logits(), b.read_logits()
+    err = float(np.max(np.abs(la - lb)) / np.max(np.abs(lb)))
+    print(f"c4-width 512-token prefill: batched {ga} step {gb}, logits err {err:.2e}")
+    assert err < LOGIT_TOL
+    assert ga == gb or top2_margin(lb) < TIE_TOL * np.abs(lb).max()
+    for layer in range(cfg.layers):
+        ka, va = a.read_kv(layer)
+        kb, vb = b.read_kv(layer)
+        for x, y in ((ka, kb), (va, vb)):
+            fx = x.view(np.float16).astype(np.float64)
+            fy = y.view(np.float16).astype(np.float64)
+            d = np.abs(fx - fy)
+            assert d.max() <= KV_MAX_TOL * np.abs(fy).max(), f"layer {layer} cache (max)"
+            assert d.mean() <= KV_MEAN_TOL * np.abs(fy).mean(), f"layer {layer} cache (mean)"
+    # the decode continuation from both
+    ta = a.decode_chunk(512, 8)
+    tb = b.decode_chunk(512, 8)
+    print(f"continuations {ta.tolist()} / {tb.tolist()}")
+    assert np.array_equal(ta, tb)
