@@ -1,6 +1,6 @@
 """Benchmark of the batch-1 decode path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c1|c0] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c1|c0|prefill] [--no-cpu]
 
 Prints ONE JSON line (rank 0).  Workloads:
   c0  one q4_0 GEMV 16384x2048 (x f32), weights rotated over >512 MB so the
@@ -8,7 +8,10 @@ Prints ONE JSON line (rank 0).  Workloads:
   c1  Q6_K lm-head 262144x2048 + softcap + argmax; a step = one launch.
   c3  A4B-style MoE half-layer (hidden 2816, 128 experts top-8); a step =
       one layer (4 launches), weights rotated over 3 copies.
-  c4  the E4B-shaped decode loop; a step = one greedy decode token.
+  c4  the E4B-shaped decode loop; a step = one greedy decode token (the
+      config also reports the batched prefill of the 512-token prompt).
+  prefill  the 512-token c4 prompt through the batched prefill (MFMA
+      GEMMs); a step = one whole prefill.
 `roofline` is measured live with HIP events on the launch stream; the CPU
 baseline times the oracle (the C restatement, OpenMP) on a bounded sample.
 """
@@ -241,6 +244,66 @@ def _time_geglu(cfg, steps: int) -> dict:
     return {"us": us, "algo": algo, "gbs": algo / (us * 1e-6) / 1e9}
 
 
+def prefill_flops(cfg, n: int) -> dict:
+    """Algorithmic flops of a batched prefill of n tokens from position 0:
+    2 per weight element per token over every layer GEMM and the PLE model
+    projection (counted once, though it runs as two f16 passes), and 4 x
+    keys x head_dim per query head of causal attention (q.k and p.v)."""
+    H, F, PD, L = cfg.hidden, cfg.ffn, cfg.ple_dim, cfg.layers
+    qkv = (cfg.q_heads + 2 * cfg.kv_heads) * cfg.head_dim
+    per_layer = qkv * H + H * cfg.q_heads * cfg.head_dim + 2 * F * H + H * F + (2 * PD * H if PD else 0)
+    gemm = 2 * n * (L * per_layer + L * PD * H)
+    attn = 0
+    for g in cfg.layer_global:
+        keys = sum(p + 1 if g else min(p + 1, cfg.window) for p in range(n))
+        attn += 4 * cfg.q_heads * cfg.head_dim * keys
+    return {"gemm": gemm, "attn": attn}
+
+
+def time_prefill(eng, prompt, reps: int = 3) -> float:
+    """Best wall time (s) of `reps` warm batched prefills (e4b_prefill is
+    synchronous: it returns after the last token's argmax is read back)."""
+    eng.prefill(prompt)
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        eng.prefill(prompt)
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def bench_prefill(steps: int, warmup: int, cpu: bool) -> dict:
+    """The c4 prompt (512 uniform-random token ids) through the batched
+    prefill, `steps` times after `warmup` (for profiling the prefill kernels)."""
+    from e4b import formats
+    from e4b.engine import Engine
+    from e4b.model import E4BConfig, synth_tensors
+
+    prompt_len = 512
+    cfg = E4BConfig(max_seq=1024)
+    eng = Engine(cfg, synth_tensors(cfg, seed=0))
+    prompt = formats.synth_uniform_u32(7, prompt_len, 0, cfg.vocab)
+    for _ in range(warmup):
+        eng.prefill(prompt)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.prefill(prompt)
+    dt = (time.perf_counter() - t0) / steps
+    fl = prefill_flops(cfg, prompt_len)
+    tf = (fl["gemm"] + fl["attn"]) / dt / 1e12
+    eng.close()
+    return {
+        "metric": "batched prefill tokens/s (E4B-shape q4_0, 512-token prompt)", "value": round(prompt_len / dt, 1),
+        "unit": "tokens/s", "ms_per_step": dt * 1e3,
+        "dtype": "q4_0 weights x f16 activations on f16 MFMA, f32 accumulate",
+        "config": {"workload": "prefill of the c4 prompt (512 tokens) on the E4B-shaped model",
+                   "prompt_tokens": prompt_len, "flops": fl["gemm"] + fl["attn"]},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tf / 2500.0, 4), "traffic": None,
+                     "kernel": "whole prefill (GEMMs + attention + per-token kernels)"},
+    }
+
+
 def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict:
     from e4b import formats
     from e4b._lib import FLAG_NO_GRAPH
@@ -256,9 +319,8 @@ def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict
     eng = Engine(cfg, tensors)
     t_load = time.perf_counter() - t0
     prompt = formats.synth_uniform_u32(7, prompt_len, 0, cfg.vocab)
-    t0 = time.perf_counter()
-    eng.prefill(prompt)
-    t_prefill = time.perf_counter() - t0
+    t_prefill = time_prefill(eng, prompt)
+    fl = prefill_flops(cfg, prompt_len)
     eng.time_decode(prompt_len, warmup)
     ms = eng.time_decode(prompt_len + warmup, steps)
     ms_tok = ms / steps
@@ -276,6 +338,8 @@ def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict
                    "bytes_per_token": int(bytes_tok), "step_hbm_gbs": round(step_gbs, 1),
                    "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
                    "prefill_tokens_per_s": round(prompt_len / t_prefill, 1),
+                   "prefill_ms": round(t_prefill * 1e3, 3),
+                   "prefill_tflops": round((fl["gemm"] + fl["attn"]) / t_prefill / 1e12, 2),
                    "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEGLU_TRAFFIC_BYTES,
@@ -302,7 +366,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c4"])
+    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c4", "prefill"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
@@ -315,9 +379,9 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
               "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
-    fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c4": bench_c4}[a.workload]
-    steps = a.steps if a.steps is not None else (240 if a.workload == "c4" else 200)
-    warmup = a.warmup if a.warmup is not None else (16 if a.workload == "c4" else 20)
+    fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "prefill": bench_prefill}[a.workload]
+    steps = a.steps if a.steps is not None else {"c4": 240, "prefill": 10}.get(a.workload, 200)
+    warmup = a.warmup if a.warmup is not None else {"c4": 16, "prefill": 2}.get(a.workload, 20)
     if a.workload == "c4" and a.kernel_only:
         from e4b.model import E4BConfig
         dom = _time_geglu(E4BConfig(), steps)

@@ -162,7 +162,10 @@ int record_step(e4b_ctx* c);
 // batched prefill: tokens per chunk at most, and split-K slices of the
 // o and down projection GEMMs (their consumers sum the slices)
 constexpr int kPfMaxChunk = 512;
-constexpr int kPfKs = 4;
+constexpr int kPfKsO = 4;    // o projection
+constexpr int kPfKs = 8;     // down projection (the most slices; sizes the partial buffer)
+constexpr int kPfKsQkv = 2;  // qkv (the head prep sums the slices)
+constexpr int kPfKsPle = 8;  // PLE gate (256 rows; the GELU-multiply kernel sums the slices)
 
 }  // namespace
 
@@ -387,7 +390,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
     const size_t M = (size_t)cap, NPs = (size_t)NP;
     if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
         (rc = dalloc_t(c, &c->pf_proj, 2 * M * NPs)) || (rc = dalloc_t(c, &c->pf_ple, M * NPs)) ||
-        (rc = dalloc_t(c, &c->pf_qkv, M * (size_t)c->qkv_rows)) || (rc = dalloc_t(c, &c->pf_q, M * QH * HD)) ||
+        (rc = dalloc_t(c, &c->pf_qkv, kPfKsQkv * M * (size_t)c->qkv_rows)) || (rc = dalloc_t(c, &c->pf_q, M * QH * HD)) ||
         (rc = dalloc_t(c, &c->pf_y, (size_t)kPfKs * M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
         (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * HD)) ||
         (rc = dalloc_t(c, &c->pf_gg, M * FF)) || (rc = dalloc_t(c, &c->pf_gp, M * (size_t)(PD ? PD : 1))))
@@ -613,13 +616,14 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
   if ((rc = launch_resnorm_rows(M, c->pf_h, nullptr, 0, 0, nullptr, 1.0f, c->L[0].attn_norm, c->pf_xn, nullptr, H,
                                 k.eps, st)))
     return rc;
-  const int ks_o = q40_gemm_kslices(QH * HD / 32, kPfKs), ks_d = q40_gemm_kslices(FF / 32, kPfKs);
+  const int ks_o = q40_gemm_kslices(QH * HD / 32, kPfKsO), ks_d = q40_gemm_kslices(FF / 32, kPfKs);
+  const int ks_qkv = q40_gemm_kslices(H / 32, kPfKsQkv), ks_pg = q40_gemm_kslices(H / 32, kPfKsPle);
   for (int l = 0; l < Lc; ++l) {
     const Layer& ly = c->L[l];
     // attention block
-    if ((rc = gemm(q40_view(ly.qkv, c->qkv_rows, H), c->pf_xn, H, GEMM_F32, c->pf_qkv, nullptr, 0, nullptr, 0, 1)))
+    if ((rc = gemm(q40_view(ly.qkv, c->qkv_rows, H), c->pf_xn, H, GEMM_F32, c->pf_qkv, nullptr, 0, nullptr, 0, ks_qkv)))
       return rc;
-    if ((rc = launch_headprep_rows(c->pf_qkv, 1, 0, ly.q_norm, ly.k_norm, ly.global ? c->inv_global : c->inv_local,
+    if ((rc = launch_headprep_rows(c->pf_qkv, ks_qkv, (int64_t)M * c->qkv_rows, ly.q_norm, ly.k_norm, ly.global ? c->inv_global : c->inv_local,
                                    k.rope_angles, ly.kc, ly.vc, ly.slots, !ly.global, p0, M, c->pf_q, QH, KVH, k.eps,
                                    st)))
       return rc;
@@ -656,8 +660,9 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
       // projection; post-PLE residual and layer scalar
       if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_d, MH, ly.post_ffw, 1.0f, nullptr, c->pf_xn, nullptr, H,
                                     k.eps, st)) ||
-          (rc = gemm(q40_view(ly.pg, PD, H), c->pf_xn, H, GEMM_GELU_MUL, nullptr, c->pf_gp, 0, c->pf_ple + (int64_t)l * PD,
-                     NP, 1)) ||
+          (rc = gemm(q40_view(ly.pg, PD, H), c->pf_xn, H, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, ks_pg)) ||
+          (rc = launch_gelu_mul_rows(c->pf_y, ks_pg, (int64_t)M * PD, M, PD, c->pf_ple + (int64_t)l * PD, NP, c->pf_gp,
+                                     st)) ||
           (rc = gemm(q40_view(ly.pp_rm, H, PD), c->pf_gp, PD, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, 1)) ||
           (rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, 1, 0, ly.post_norm, ly.scale, w_next, x_next, xlo_next, H,
                                     k.eps, st)))

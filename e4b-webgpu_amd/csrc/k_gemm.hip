@@ -56,7 +56,9 @@ template <int T, int EPI>
 __global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
   constexpr int NT = EPI == GEMM_GLU ? 2 : 1;  // weight tiles per wave (gate, up)
   constexpr int TOK = 32 * T;                  // tokens per workgroup
-  __shared__ __align__(16) uint4 xs[TOK][KB * 4];  // KB blocks x 64 B per token
+  // KB blocks x 64 B per token, plus one 16-byte pad so that the 16-byte
+  // reads of 8 consecutive token rows hit distinct LDS bank groups
+  __shared__ __align__(16) uint4 xs[TOK][KB * 4 + 1];
   const Q40Mat& W = a.W;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -199,10 +201,12 @@ int launch_q40_gemm(const GemmArgs& a, hipStream_t st) {
   if (kslices != ks)
     return e4b_fail(E4B_EINVAL, "q4_0 GEMM: %d blocks do not split into %d slices (use q40_gemm_kslices)", W.nb, ks);
   // the widest token tile (4 x 32 tokens per wave: the weight-word
-  // conversion is shared by 4 MFMA pairs) that still gives >= 256 workgroups
+  // conversion is shared by 4 MFMA pairs) that still gives >= 512 workgroups
+  // (two per CU: a stage's load latency is hidden by the other workgroup's
+  // MFMAs; measured best for the E4B prefill shapes at 512 tokens)
   const int64_t rt = (units + 127) / 128;
   int T = 4;
-  while (T > 1 && rt * ((a.M + 32 * T - 1) / (32 * T)) * kslices < 256) T >>= 1;
+  while (T > 1 && rt * ((a.M + 32 * T - 1) / (32 * T)) * kslices < 512) T >>= 1;
   const dim3 grid((unsigned)rt, (unsigned)((a.M + 32 * T - 1) / (32 * T)), (unsigned)kslices);
   if (a.epi == GEMM_GLU)
     launch_t<GEMM_GLU>(T, a, grid, K, nbs, st);

@@ -145,6 +145,19 @@ __global__ __launch_bounds__(256) void k_resnorm_rows(float* __restrict__ h, con
   }
 }
 
+// y[m][n] = f16(gelu(sum of ks partial slices) * mul[m mul_ld + n]) for the
+// PLE gate of every token (kernels/plegatemv.wgsl:20-60 per token)
+__global__ __launch_bounds__(256) void k_gelu_mul_rows(const float* __restrict__ part, int ks, int64_t slice,
+                                                       int64_t n, const float* __restrict__ mul, int64_t mul_ld,
+                                                       uint16_t* __restrict__ y) {
+  const int m = blockIdx.y;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float v = part[(int64_t)m * n + i];
+    for (int z = 1; z < ks; ++z) v += part[z * slice + (int64_t)m * n + i];
+    y[(int64_t)m * n + i] = f2h(gelu_tanh(v) * mul[(int64_t)m * mul_ld + i]);
+  }
+}
+
 // one wave per (head row hh, token m): the qkv row is the sum of ks partial
 // slices; q heads -> q[m][hh] (f32), k heads -> key cache, v heads -> value
 // cache, at the slot of position p0 + m (ring slot for a sliding layer)
@@ -368,6 +381,14 @@ int launch_ple_prep_rows(const float* proj, int64_t slice, const uint8_t* table,
                          const uint32_t* ids, int M, int L, float proj_scale, float* ple, float eps, hipStream_t st) {
   hipLaunchKernelGGL(k_ple_prep_rows, dim3(L, M), dim3(256), 0, st, proj, slice, table, w_pn, ids, L, proj_scale, ple,
                      eps);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_gelu_mul_rows(const float* part, int ks, int64_t slice, int M, int64_t n, const float* mul, int64_t mul_ld,
+                         uint16_t* y, hipStream_t st) {
+  const unsigned gx = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(k_gelu_mul_rows, dim3(gx, M), dim3(256), 0, st, part, ks, slice, n, mul, mul_ld, y);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

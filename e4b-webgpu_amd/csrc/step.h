@@ -64,6 +64,9 @@ int launch_ple_prep_rows(const float* proj, int64_t slice, const uint8_t* table,
 // half of the exact f16 split of the same value
 int launch_resnorm_rows(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
                         const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st);
+// y[m][i] = f16(gelu(sum of ks slices of part[m][i]) * mul[m mul_ld + i]), i < n
+int launch_gelu_mul_rows(const float* part, int ks, int64_t slice, int M, int64_t n, const float* mul, int64_t mul_ld,
+                         uint16_t* y, hipStream_t st);
 // qkv: ks partial slices [M][(qh + 2 kvh) 256]; q out [M][qh][256] f32; K/V
 // rows of positions p0 .. p0 + M - 1 written to the caches (ring: slot p % slots)
 int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* qw, const float* kw,
