@@ -1,6 +1,6 @@
 """Benchmark of the batch-1 decode path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c1|c0|prefill] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c3p|c1|c0|prefill] [--no-cpu]
 
 Prints ONE JSON line (rank 0).  Workloads:
   c0  one q4_0 GEMV 16384x2048 (x f32), weights rotated over >512 MB so the
@@ -12,12 +12,15 @@ Prints ONE JSON line (rank 0).  Workloads:
       config also reports the batched prefill of the 512-token prompt).
   prefill  the 512-token c4 prompt through the batched prefill (MFMA
       GEMMs); a step = one whole prefill.
+  c3p the c3 MoE half-layer over a 512-token chunk (expert-grouped
+      GEMMs); a step = one layer.
 `roofline` is measured live with HIP events on the launch stream; the CPU
 baseline times the oracle (the C restatement, OpenMP) on a bounded sample.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -201,6 +204,52 @@ def bench_c3(steps: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
+def bench_c3p(steps: int, warmup: int, cpu: bool) -> dict:
+    """The c3 MoE half-layer over a 512-token prompt chunk (the batched
+    prefill: expert-grouped MFMA GEMMs); a step = one layer over 512 tokens."""
+    from e4b import formats
+    from e4b._lib import check, lib
+    from e4b.device import DeviceBuffer, Event
+    from e4b.kernels import MoeLayer, _vp
+
+    H, E, FF, FF2, M = 2816, 128, 704, 2112, 512
+    q = lambda rows, cols, s: formats.synth_q40(s, rows, cols, 0.02)  # noqa: E731
+    ones = np.ones(H, np.float32)
+    t = {"ffn_norm": ones, "router_scale": ones, "pre_ffw2": ones, "post_ffw1": ones, "post_ffw2": ones,
+         "post_ffw": ones, "router_w": formats.synth_normal(10, E * H, 0.0, 0.02).reshape(E, H),
+         "pes": np.ones(E, np.float32), "dense_gate": q(FF2, H, 1), "dense_up": q(FF2, H, 2),
+         "dense_down": q(H, FF2, 3), "exp_gate_up": q(E * 2 * FF, H, 4), "exp_down": q(E * H, FF, 5)}
+    L = MoeLayer(H, E, FF, FF2, t)
+    hd = DeviceBuffer.from_array(formats.synth_normal(77, M * H))
+    ho = DeviceBuffer(M * H * 4)
+
+    def run():
+        check(lib.e4b_k_moe_prefill(C.byref(L.w), _vp(hd), M, _vp(ho), None, None, None, None, None),
+              "e4b_k_moe_prefill")
+
+    for _ in range(warmup):
+        run()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    # algorithmic flops: router (f32) + dense GeGLU and down + 8 expert GeGLU
+    # and down per token
+    flops = 2 * M * (E * H + 2 * FF2 * H + H * FF2 + 8 * (2 * FF * H + H * FF))
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "MoE prefill tokens/s per layer (config c3 shapes, 512-token chunk)",
+        "value": round(M / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": ms,
+        "dtype": "q4_0 x f16 on f16 MFMA (f32 accumulate), f32 router",
+        "config": {"workload": "c3 MoE half-layer over 512 tokens: router, top-8, expert-grouped gate/up and down "
+                               "GEMMs, dense branch GEMMs, combine, tail", "tokens": M, "flops": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tf / 2500.0, 4), "traffic": None, "kernel": "whole MoE prefill layer"},
+    }
+
+
 def _time_geglu(cfg, steps: int) -> dict:
     """Dominant kernel of the c4 step: the FFN input GEMV exactly as the step
     launches it -- fused residual + RMSNorm prologue, gate/up q4_0 GEMV
@@ -366,7 +415,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c4", "prefill"])
+    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c3p", "c4", "prefill"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
@@ -379,7 +428,8 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
               "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
-    fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "prefill": bench_prefill}[a.workload]
+    fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c3p": bench_c3p, "c4": bench_c4,
+          "prefill": bench_prefill}[a.workload]
     steps = a.steps if a.steps is not None else {"c4": 240, "prefill": 10}.get(a.workload, 200)
     warmup = a.warmup if a.warmup is not None else {"c4": 16, "prefill": 2}.get(a.workload, 20)
     if a.workload == "c4" and a.kernel_only:

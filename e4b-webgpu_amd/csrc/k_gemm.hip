@@ -52,7 +52,7 @@ DEV h8 nib_word_f16(uint32_t w) {
   return r;
 }
 
-template <int T, int EPI>
+template <int T, int EPI, bool GRP = false>
 __global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
   constexpr int NT = EPI == GEMM_GLU ? 2 : 1;  // weight tiles per wave (gate, up)
   constexpr int TOK = 32 * T;                  // tokens per workgroup
@@ -64,14 +64,26 @@ __global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
   const int l32 = lane & 31, hi = lane >> 5;
   const int nb = K / 32;
   const int M = a.M;
-  const int64_t units = EPI == GEMM_GLU ? a.ff : W.rows;  // output columns
+  // output columns, and the weight rows of this workgroup's group
+  const int64_t units = EPI == GEMM_GLU ? a.ff : (GRP ? a.group_rows : W.rows);
+  int tok0, nrows;
+  int64_t wbase = 0;
+  if constexpr (GRP) {
+    if ((int)blockIdx.y >= *a.ntiles) return;  // the grid is sized for the most tiles
+    const int4 tl = a.tiles[blockIdx.y];
+    wbase = (int64_t)tl.x * a.group_rows;
+    tok0 = tl.y;
+    nrows = tl.z;
+  } else {
+    tok0 = blockIdx.y * TOK;
+    nrows = M - tok0;
+  }
   const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * 32;  // first output column of this wave
-  const int tok0 = blockIdx.y * TOK;
   const int kz = blockIdx.z;
   const int kbeg = kz * nbs, kend = min(nb, kbeg + nbs);  // this slice's blocks
   // this lane's weight rows (clamped: tiles past the end compute duplicates, never stored)
   int64_t wrow[NT];
-  wrow[0] = min(n0 + l32, units - 1);
+  wrow[0] = wbase + min(n0 + l32, units - 1);
   if constexpr (EPI == GEMM_GLU) wrow[1] = a.ff + wrow[0];
   f16v acc[NT][T];
 #pragma unroll
@@ -101,7 +113,11 @@ __global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
       const int m = i / (KB * 4), q = i % (KB * 4);
       const int kq = kb0 * 32 + q * 8;  // first k of this 16-byte piece
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (tok0 + m < M && kq < kend * 32) v = *reinterpret_cast<const uint4*>(a.X + (int64_t)(tok0 + m) * a.ldx + kq);
+      if (m < nrows && kq < kend * 32) {
+        int64_t xr = tok0 + m;
+        if constexpr (GRP) xr = a.gather ? (int64_t)(a.gather[xr] / (uint32_t)a.gather_div) : xr;
+        v = *reinterpret_cast<const uint4*>(a.X + xr * a.ldx + kq);
+      }
       xs[m][q] = v;
     }
     lds_sync();
@@ -137,20 +153,25 @@ __global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
   for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = tok0 + 32 * t + 8 * (r / 4) + 4 * hi + (r % 4);
-      if (m < M) {
+      const int ml = 32 * t + 8 * (r / 4) + 4 * hi + (r % 4);
+      const int m = tok0 + ml;
+      if (ml < nrows) {
         if constexpr (EPI == GEMM_GLU)
           a.Yh[(int64_t)m * a.ff + n] = f2h(gelu_tanh(acc[0][t][r]) * acc[1][t][r]);
         else if constexpr (EPI == GEMM_GELU_MUL)
-          a.Yh[(int64_t)m * W.rows + n] = f2h(gelu_tanh(acc[0][t][r]) * a.mul[(int64_t)m * a.mul_ld + n]);
+          a.Yh[(int64_t)m * units + n] = f2h(gelu_tanh(acc[0][t][r]) * a.mul[(int64_t)m * a.mul_ld + n]);
         else
-          a.Y[((int64_t)kz * M + m) * W.rows + n] = acc[0][t][r];
+          a.Y[((int64_t)kz * M + m) * units + n] = acc[0][t][r];
       }
     }
 }
 
 template <int EPI>
 void launch_t(int T, const GemmArgs& a, dim3 grid, int K, int nbs, hipStream_t st) {
+  if (a.tiles) {
+    hipLaunchKernelGGL((k_q40_gemm<1, EPI, true>), grid, dim3(256), 0, st, a, K, nbs);
+    return;
+  }
   if (T == 4)
     hipLaunchKernelGGL((k_q40_gemm<4, EPI>), grid, dim3(256), 0, st, a, K, nbs);
   else if (T == 2)
@@ -180,13 +201,18 @@ int launch_q40_gemm(const GemmArgs& a, hipStream_t st) {
   const int ks = a.ks > 0 ? a.ks : 1;
   if (ks > 1 && a.epi != GEMM_F32) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: split-K needs the f32 epilogue");
   if (ks > W.nb) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: %d K slices for %d blocks", ks, W.nb);
-  int64_t units = W.rows;
+  const bool grp = a.tiles != nullptr;
+  if (grp && (!a.ntiles || a.max_tiles < 1 || a.group_rows < 1 || W.rows % a.group_rows || ks != 1 ||
+              (a.gather && a.gather_div < 1)))
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMM: bad grouped-mode arguments");
+  int64_t units = grp ? a.group_rows : W.rows;
   switch (a.epi) {
     case GEMM_F32:
       if (!a.Y) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: null output");
       break;
     case GEMM_GLU:
-      if (!a.Yh || a.ff < 1 || 2 * a.ff != W.rows) return e4b_fail(E4B_EINVAL, "q4_0 GEMM: GeGLU needs 2*ff rows");
+      if (!a.Yh || a.ff < 1 || 2 * a.ff != (grp ? a.group_rows : W.rows))
+        return e4b_fail(E4B_EINVAL, "q4_0 GEMM: GeGLU needs 2*ff rows");
       units = a.ff;
       break;
     case GEMM_GELU_MUL:
@@ -207,7 +233,9 @@ int launch_q40_gemm(const GemmArgs& a, hipStream_t st) {
   const int64_t rt = (units + 127) / 128;
   int T = 4;
   while (T > 1 && rt * ((a.M + 32 * T - 1) / (32 * T)) * kslices < 512) T >>= 1;
-  const dim3 grid((unsigned)rt, (unsigned)((a.M + 32 * T - 1) / (32 * T)), (unsigned)kslices);
+  if (grp) T = 1;  // tiles of <= 32 rows
+  const unsigned gy = grp ? (unsigned)a.max_tiles : (unsigned)((a.M + 32 * T - 1) / (32 * T));
+  const dim3 grid((unsigned)rt, gy, (unsigned)kslices);
   if (a.epi == GEMM_GLU)
     launch_t<GEMM_GLU>(T, a, grid, K, nbs, st);
   else if (a.epi == GEMM_GELU_MUL)

@@ -51,6 +51,11 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
 constexpr int kRouterMaxH4 = 768;  // H <= 3072
 
 __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
+  // token row y of a batch (the batched prefill); y = 0 in the decode step
+  A.h += (int64_t)blockIdx.y * A.H;
+  A.xd += (int64_t)blockIdx.y * A.H;
+  A.xm += (int64_t)blockIdx.y * A.H;
+  A.scores += (int64_t)blockIdx.y * A.E;
   __shared__ __align__(16) float4 xr[kRouterMaxH4];
   __shared__ float red[2];
   constexpr int PT = kRouterMaxH4 / 128;  // float4 per thread
@@ -181,6 +186,10 @@ DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__
 }
 
 __global__ __launch_bounds__(64) void k_moe_topk(MoeArgs A) {
+  // token row blockIdx.x of a batch (one block in the decode step)
+  A.scores += (int64_t)blockIdx.x * A.E;
+  A.topk_idx += (int64_t)blockIdx.x * K;
+  A.topk_w += (int64_t)blockIdx.x * K;
   const TopK t = select_topk<true>(A.scores, A.pes, A.E);
   const int lane = threadIdx.x;
 #pragma unroll
@@ -455,6 +464,12 @@ constexpr int kTailPer = 12;  // elements per thread, H <= 3072
 __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
   __shared__ float red[4];
   const int H = A.H;
+  // token row blockIdx.x of a batch (one block in the decode step)
+  const int64_t ro = (int64_t)blockIdx.x * H;
+  A.h += ro;
+  A.dense_out += ro;
+  A.moe_out += ro;
+  A.h_out += ro;
   // every input requested before the first reduction waits
   float d[kTailPer], m[kTailPer], w1[kTailPer], w2[kTailPer], hv[kTailPer], wp[kTailPer];
 #pragma unroll
@@ -518,6 +533,27 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
   const int nbd = (dd_tiles + 3) / 4, nbe = (de_tiles + 3) / 4;
   hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A, nbd);
   hipLaunchKernelGGL(k_moe_tail, dim3(1), dim3(256), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_moe_router_rows(const MoeArgs& A, int M, hipStream_t st) {
+  if (A.H % 4 || A.H / 4 > kRouterMaxH4 || M < 1) return e4b_fail(E4B_EINVAL, "router rows: H=%d M=%d", A.H, M);
+  hipLaunchKernelGGL(k_moe_router, dim3((A.E + 1) / 2, M), dim3(128), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_moe_topk_rows(const MoeArgs& A, int M, hipStream_t st) {
+  if (A.E < K || A.E > 256 || M < 1) return e4b_fail(E4B_EINVAL, "top-8 rows: E=%d M=%d", A.E, M);
+  hipLaunchKernelGGL(k_moe_topk, dim3(M), dim3(64), 0, st, A);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_moe_tail_rows(const MoeArgs& A, int M, hipStream_t st) {
+  if (A.H > 256 * kTailPer || M < 1) return e4b_fail(E4B_EINVAL, "MoE tail rows: H=%d M=%d", A.H, M);
+  hipLaunchKernelGGL(k_moe_tail, dim3(M), dim3(256), 0, st, A);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -116,6 +116,18 @@ struct GemmArgs {
   const float* mul;
   int64_t mul_ld;
   int ks;             // split-K slices (GEMM_F32)
+  // grouped mode (the expert-indexed MoE prefill; tiles != null): blockIdx.y
+  // picks tiles[y] = (group g, first row r0, rows n <= 32) of the M sorted
+  // rows, y < *ntiles; the weights are rows [g group_rows, (g+1) group_rows)
+  // of W (GLU: group_rows = 2 ff, gate then up); X row r is gather[r] /
+  // gather_div (gather null: row r); outputs are rows r0 .. r0 + n - 1 of an
+  // [M][group_rows] (GLU: [M][ff]) matrix
+  const int4* tiles;
+  const int* ntiles;
+  int max_tiles;
+  int64_t group_rows;
+  const uint32_t* gather;
+  int gather_div;
 };
 int launch_q40_gemm(const GemmArgs& a, hipStream_t st);
 // the largest split-K slice count <= want that cuts nb blocks into whole

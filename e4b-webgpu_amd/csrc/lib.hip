@@ -387,6 +387,28 @@ extern "C" int e4b_k_router_top8(const e4b_moe_weights* w, const float* h, uint3
   return launch_moe_topk(a, (hipStream_t)stream);
 }
 
+extern "C" int e4b_k_moe_prefill(const e4b_moe_weights* w, const float* h, int m, float* h_out, uint32_t* topk_idx,
+                                 float* topk_w, float* dense_out, float* moe_out, void* stream) {
+  if (!h_out || m < 1 || m > 1024) return e4b_fail(E4B_EINVAL, "e4b_k_moe_prefill: null h_out or m=%d outside 1..1024", m);
+  MoeArgs a;
+  Workspace ws;
+  int rc = moe_setup(w, h, &a, &ws);  // validates the weights (its scratch is not used)
+  if (rc) return rc;
+  const size_t bytes = moe_prefill_scratch(a, m, nullptr, nullptr);
+  if ((rc = e4b_workspace(bytes, &ws))) return rc;
+  MoePrefillBufs b;
+  moe_prefill_scratch(a, m, &b, ws.buf);
+  a.h_out = h_out;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = launch_moe_prefill(a, m, b, st))) return rc;
+  const size_t P = (size_t)m * kMoeTopK * 4, HB = (size_t)m * a.H * 4;
+  if (topk_idx) E4B_HIP(hipMemcpyAsync(topk_idx, b.topk_idx, P, hipMemcpyDeviceToDevice, st));
+  if (topk_w) E4B_HIP(hipMemcpyAsync(topk_w, b.topk_w, P, hipMemcpyDeviceToDevice, st));
+  if (dense_out) E4B_HIP(hipMemcpyAsync(dense_out, b.dense_out, HB, hipMemcpyDeviceToDevice, st));
+  if (moe_out) E4B_HIP(hipMemcpyAsync(moe_out, b.moe_out, HB, hipMemcpyDeviceToDevice, st));
+  return E4B_OK;
+}
+
 extern "C" int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* h_out, uint32_t* topk_idx,
                                float* topk_w, float* dense_out, float* moe_out, void* stream) {
   if (!h_out) return e4b_fail(E4B_EINVAL, "e4b_k_moe_layer: null h_out");

@@ -43,3 +43,30 @@ int launch_moe_router(const MoeArgs& a, hipStream_t st);
 int launch_moe_topk(const MoeArgs& a, hipStream_t st);
 // the whole half-layer: router, gate/up, down, tail
 int launch_moe_ffn(const MoeArgs& a, hipStream_t st);
+// the same router / top-8 / tail kernels over M token rows (row y of h, xd,
+// xm, dense_out, moe_out, h_out at y * H, of scores at y * E, of topk at y * 8)
+int launch_moe_router_rows(const MoeArgs& a, int M, hipStream_t st);
+int launch_moe_topk_rows(const MoeArgs& a, int M, hipStream_t st);
+int launch_moe_tail_rows(const MoeArgs& a, int M, hipStream_t st);
+
+// ---- batched prefill of the half-layer (k_moe_prefill.hip) -----------------
+struct MoePrefillBufs {
+  float* scores;       // [M][E]
+  uint16_t *xd, *xm;   // [M][H] f16 branch inputs
+  uint32_t* topk_idx;  // [M][8]
+  float* topk_w;       // [M][8]
+  uint32_t* list;      // [M*8] draws (m*8 + k) sorted by expert
+  uint32_t* pos;       // [M*8] sorted position of each draw
+  int4* tiles;         // [max_tiles] (expert, first sorted row, rows)
+  int* ntiles;
+  int max_tiles;
+  uint16_t* g_sorted;  // [M*8][FF] f16 expert GeGLU outputs, sorted
+  float* d_sorted;     // [M*8][H] expert down outputs, sorted
+  uint16_t* g_dense;   // [M][FF2]
+  float* dense_out;    // [M][H]
+  float* moe_out;      // [M][H]
+};
+// bytes of scratch for M tokens; with base != null also fills b from it
+size_t moe_prefill_scratch(const MoeArgs& a, int M, MoePrefillBufs* b, uint8_t* base);
+// h_out[m] (a.h_out, rows of H) for the M token rows of a.h
+int launch_moe_prefill(const MoeArgs& a, int M, const MoePrefillBufs& b, hipStream_t st);

@@ -88,6 +88,7 @@ SIGNATURES = [
     ("e4b_rope_inv_freq", _i32, [_f32, _i32, _i32, _vp]),
     ("e4b_k_router_top8", _i32, [_vp, _vp, _vp, _vp, _vp]),
     ("e4b_k_moe_layer", _i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    ("e4b_k_moe_prefill", _i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     ("e4b_k_attn_decode", _i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _u32, _f32,
                                  _i32, _vp, _vp]),
     ("e4b_k_attn_prefill", _i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _u32, _vp]),

@@ -244,6 +244,21 @@ class MoeLayer:
                 "topk_w": self.wts.download(np.float32, 8), "dense_out": self.dense.download(np.float32, self.H),
                 "moe_out": self.moe.download(np.float32, self.H)}
 
+    def prefill(self, h: np.ndarray) -> dict:
+        """The half-layer over m token rows (e4b_k_moe_prefill): h f32 [m][H]."""
+        h = np.ascontiguousarray(h, np.float32)
+        m = h.shape[0]
+        hd = DeviceBuffer.from_array(h)
+        ho, dn, mo = DeviceBuffer(m * self.H * 4), DeviceBuffer(m * self.H * 4), DeviceBuffer(m * self.H * 4)
+        ix, wt = DeviceBuffer(m * 32), DeviceBuffer(m * 32)
+        check(lib.e4b_k_moe_prefill(C.byref(self.w), _vp(hd), m, _vp(ho), _vp(ix), _vp(wt), _vp(dn), _vp(mo), None),
+              "e4b_k_moe_prefill")
+        r = lambda b, dt, n: b.download(dt, n)  # noqa: E731
+        return {"h_out": r(ho, np.float32, m * self.H).reshape(m, self.H),
+                "topk_idx": r(ix, np.uint32, m * 8).reshape(m, 8), "topk_w": r(wt, np.float32, m * 8).reshape(m, 8),
+                "dense_out": r(dn, np.float32, m * self.H).reshape(m, self.H),
+                "moe_out": r(mo, np.float32, m * self.H).reshape(m, self.H)}
+
     def router_top8(self, h: np.ndarray):
         self.h.upload(np.ascontiguousarray(h, np.float32))
         check(lib.e4b_k_router_top8(C.byref(self.w), _vp(self.h), _vp(self.idx), _vp(self.wts), None),

@@ -218,6 +218,17 @@ int e4b_k_router_top8(const e4b_moe_weights* w, const float* h, uint32_t* topk_i
 int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* h_out, uint32_t* topk_idx,
                     float* topk_w, float* dense_out, float* moe_out, void* stream);
 
+/* The half-layer over m prompt tokens (the reference's batched prefill of
+ * the MoE layer, src/engine-a4b.js:478-549: routerTopB, expGroup +
+ * guGsg32 / downGsg32 + waccB, kernels/expgroup.wgsl:15-50,
+ * kernels/q40gugrp.wgsl:47-103): per token the e4b_k_moe_layer arithmetic;
+ * the m*8 expert draws are sorted by expert and each expert's weight rows
+ * are read once per tile of up to 32 draws (MFMA GEMMs).  h, h_out
+ * f32[m][hidden]; topk_idx u32[m][8], topk_w f32[m][8], dense_out /
+ * moe_out f32[m][hidden] may be NULL.  1 <= m <= 1024. */
+int e4b_k_moe_prefill(const e4b_moe_weights* w, const float* h, int m, float* h_out, uint32_t* topk_idx,
+                      float* topk_w, float* dense_out, float* moe_out, void* stream);
+
 /* Causal attention of a prefill chunk (attnB / attnOSB of the reference's
  * batched prefill, src/engine-a4b.js:476-477; per query the arithmetic of
  * kernels/attnf32.wgsl:21-105 and kernels/attnos.wgsl:22-98, scale 1.0):

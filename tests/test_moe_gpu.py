@@ -115,3 +115,31 @@ def test_router_ties_pick_lowest_index():
     widx = orc.router_topk(xr.astype(np.float32), t["router_w"], t["pes"], 8)[0]
     np.testing.assert_array_equal(idx, widx)
     assert list(idx[:3]) == [3, 10, 77]
+
+
+@pytest.mark.parametrize("m,seed,random_norms", [(1, 3, False), (37, 4, True), (256, 5, False)])
+def test_moe_prefill_rows(m, seed, random_norms):
+    # the batched (expert-grouped) half-layer over m token rows: every row
+    # against the oracle's single-token half-layer, the same tolerances, and
+    # the top-8 ids bit-identical to the decode kernel's on the same row
+    t = _weights(100 * seed, random_norms)
+    hs = formats.synth_normal(seed + 900, m * H).reshape(m, H)
+    L = MoeLayer(H, E, FF, FF2, t, eps=1e-6, layer_scale=0.9)
+    got = L.prefill(hs)
+    mdl = dict(t, hidden=H, n_experts=E, top_k=8, expert_ffn=FF, dense_ffn=FF2, eps=1e-6, layer_scale=0.9)
+    rows = range(m) if m <= 40 else list(range(0, m, 17)) + [m - 1]
+    worst = {"dense": 0.0, "moe": 0.0, "h_out": 0.0}
+    for r in rows:
+        idx, w, dense, moe, hout = orc.moe_ffn(mdl, hs[r])
+        _check_topk(got["topk_idx"][r], idx, _scores(t, hs[r]), f"prefill m={m} row {r}")
+        dec = L.forward(hs[r])
+        np.testing.assert_array_equal(got["topk_idx"][r], dec["topk_idx"])
+        if np.array_equal(got["topk_idx"][r], idx):
+            np.testing.assert_allclose(got["topk_w"][r], w, rtol=1e-5)
+        for name, g, wnt, tol in (("dense", got["dense_out"][r], dense, BRANCH_TOL),
+                                  ("moe", got["moe_out"][r], moe, BRANCH_TOL),
+                                  ("h_out", got["h_out"][r], hout, HOUT_TOL)):
+            err = np.abs(g.astype(np.float64) - wnt).max() / np.abs(wnt).max()
+            worst[name] = max(worst[name], err)
+            assert err < tol, f"row {r} {name}: {err:.3e}"
+    print(f"moe prefill m={m}: worst errors {worst}")
