@@ -1,0 +1,105 @@
+// engine.js -- the JS host of the MI355X decode engine.  loadEngine(path)
+// opens a GGUF file (gguf.js), uploads every tensor through the N-API addon
+// into libe4b.so (which repacks and owns the device copies) and returns an
+// object with the surface of the one loadEngineA4B returns
+// (src/engine-a4b.js:854-856): step(token, pos), argmaxFast(),
+// decodeChunk(startPos, count, ringBase), generateFast(ids, maxNew, eosIds),
+// prefill(ids), readHidden(); plus readLogits(), reset() and close().
+//
+// The GPU work runs in libe4b.so; the async functions resolve when the call
+// has returned (every library call that returns results is synchronous).
+"use strict";
+const path = require("path");
+const { openGGUF } = require("./gguf");
+
+const addon = require(path.join(__dirname, "e4b_napi.node"));
+
+// GGUF metadata keys of the E4B-shaped model (architecture prefix "e4b")
+const KV = {
+  hidden: "embedding_length", layers: "block_count", qHeads: "attention.head_count",
+  kvHeads: "attention.head_count_kv", headDim: "attention.key_length", ffn: "feed_forward_length",
+  pleDim: "embedding_length_per_layer_input", vocab: "vocab_size", window: "attention.sliding_window",
+  ropeAngles: "rope.dimension_count_half", thetaLocal: "rope.freq_base_swa", thetaGlobal: "rope.freq_base",
+  eps: "attention.layer_norm_rms_epsilon", softcap: "final_logit_softcapping",
+};
+const DEFAULTS = { ring: 1024, maxSeq: 4096, attnChunk: 0, maxPrompt: 0, flags: 0 };
+const FLAG_NO_GRAPH = 1, FLAG_STEP_PREFILL = 2;
+
+function configFromKV(kv, overrides = {}) {
+  const arch = kv["general.architecture"] || "e4b";
+  const C = Object.assign({}, DEFAULTS);
+  for (const [f, k] of Object.entries(KV)) {
+    const key = `${arch}.${k}`;
+    if (kv[key] !== undefined) C[f] = kv[key];
+  }
+  const pat = kv[`${arch}.attention.sliding_window_pattern`];
+  if (pat !== undefined) C.layerGlobal = pat.map((s) => (s ? 0 : 1));
+  Object.assign(C, overrides);
+  if (!C.layerGlobal) C.layerGlobal = Array.from({ length: C.layers }, (_, i) => (i % 5 === 4 ? 1 : 0));
+  return C;
+}
+
+async function loadEngine(file, overrides = {}) {
+  const g = openGGUF(file);
+  const C = configFromKV(g.kv, overrides);
+  const ctx = addon.create(C);
+  try {
+    for (const name of Object.keys(g.tensors)) {
+      const t = await g.fetch(name);
+      addon.setTensor(ctx, name, t.type, t.dims, t.buf);
+    }
+    addon.finalize(ctx);
+  } catch (e) {
+    addon.destroy(ctx);
+    throw e;
+  } finally {
+    g.close();
+  }
+  const tokRing = [];
+
+  async function step(token, pos) {
+    return addon.step(ctx, token, pos, false).argmax;
+  }
+  async function argmaxFast() {
+    return addon.argmax(ctx);
+  }
+  // GPU-fed greedy decode of `count` tokens from startPos, each fed with the
+  // previous argmax; the tokens land in the host token ring at ringBase
+  function decodeChunk(startPos, count, ringBase = 0) {
+    const toks = addon.decode(ctx, startPos, count);
+    for (let i = 0; i < count; i++) tokRing[ringBase + i] = toks[i];
+    return toks;
+  }
+  async function prefill(inputIds) {
+    return addon.prefill(ctx, Uint32Array.from(inputIds));
+  }
+  // src/engine-a4b.js:826-848: prompt, then GPU-fed chunks of <= 8 tokens
+  // with an EOS check after each chunk's readback
+  async function generateFast(inputIds, maxNew, eosIds = new Set([106, 1])) {
+    const g0 = await prefill(inputIds);
+    const out = [g0];
+    if (eosIds.has(g0)) return out;
+    let pos = inputIds.length, done = 1;
+    while (done < maxNew) {
+      const n = Math.min(8, maxNew - done);
+      const toks = decodeChunk(pos, n, done - 1);
+      pos += n;
+      let stop = false;
+      for (let k = 0; k < n; k++) {
+        out.push(toks[k]);
+        if (eosIds.has(toks[k])) { stop = true; break; }
+      }
+      done += n;
+      if (stop) break;
+    }
+    return out.slice(0, maxNew);
+  }
+  async function readHidden() { return addon.readHidden(ctx); }
+  async function readLogits() { return addon.readLogits(ctx); }
+  function reset() { addon.reset(ctx); }
+  function close() { addon.destroy(ctx); }
+
+  return { C, step, argmaxFast, decodeChunk, generateFast, prefill, readHidden, readLogits, reset, close, tokRing };
+}
+
+module.exports = { loadEngine, configFromKV, addon, FLAG_NO_GRAPH, FLAG_STEP_PREFILL };

@@ -1,0 +1,109 @@
+"""The JS host (N-API addon + engine.js, Node) over the same C ABI.
+
+CPU: the addon loads and exports the engine surface; the Node GGUF reader
+parses a file written by e4b.gguf.write_gguf into the same metadata, tensor
+table and tensor bytes as the Python reader (open_gguf, itself the
+restatement of src/gguf.js).
+
+GPU: a tiny model written to GGUF, loaded once by the Python host
+(Engine.from_gguf) and once by the JS host (node run_greedy.js); greedy
+generation (batched prefill + GPU-fed decode) and the step API give the
+same tokens on both (the same library and inputs: bit-identical).
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from e4b.engine import Engine, config_to_kv
+from e4b.gguf import open_gguf, write_gguf
+from e4b.model import norm_weights_random, synth_tensors, tiny_config
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+JS = os.path.join(ROOT, "e4b-webgpu_amd", "js")
+NODE = shutil.which("node")
+
+pytestmark = pytest.mark.skipif(NODE is None or not os.path.exists(os.path.join(JS, "e4b_napi.node")),
+                                reason="node or the N-API addon is missing (build() makes the addon)")
+
+
+def _node(code: str) -> str:
+    return subprocess.run([NODE, "-e", code], cwd=JS, check=True, capture_output=True, text=True,
+                          timeout=120).stdout
+
+
+def _write_model(path, cfg, seed):
+    tensors = norm_weights_random(synth_tensors(cfg, seed), seed + 1)
+    write_gguf(str(path), config_to_kv(cfg), [(t.name, t.ggml_type, t.dims, t.data) for t in tensors.values()])
+    return tensors
+
+
+def test_addon_exports_engine_surface():
+    out = _node("const a = require('./e4b_napi.node'); console.log(JSON.stringify(Object.keys(a).sort()), a.version())")
+    keys = json.loads(out.split()[0])
+    for k in ("create", "setTensor", "finalize", "step", "prefill", "decode", "argmax", "readHidden", "readLogits",
+              "reset", "destroy", "lastError", "deviceCount", "version"):
+        assert k in keys
+    assert "gfx950" in out
+
+
+def test_node_gguf_reader_matches_python(tmp_path):
+    cfg = tiny_config(layers=2, layer_global=[0, 1])
+    path = tmp_path / "m.gguf"
+    _write_model(path, cfg, 3)
+    g = open_gguf(str(path))
+    code = f"""
+const {{ openGGUF }} = require('./gguf');
+(async () => {{
+  const g = openGGUF({json.dumps(str(path))});
+  const out = {{ kv: g.kv, dataStart: g.dataStart, tensors: {{}} }};
+  for (const n of Object.keys(g.tensors)) {{
+    const t = await g.fetch(n);
+    let h = 0; for (const b of t.buf) h = (h * 31 + b) >>> 0;
+    out.tensors[n] = {{ dims: t.dims, type: t.type, offset: t.offset, n: t.buf.length, h }};
+  }}
+  g.close();
+  console.log(JSON.stringify(out));
+}})();
+"""
+    js = json.loads(_node(code))
+    assert js["dataStart"] == g.data_start
+    for k, v in g.kv.items():
+        jv = js["kv"][k]
+        if isinstance(v, float):
+            assert abs(jv - v) <= 1e-6 * max(1.0, abs(v))
+        else:
+            assert jv == v, k
+    assert set(js["tensors"]) == set(g.tensors)
+    for n, t in g.tensors.items():
+        buf = np.asarray(g.fetch(n)["buf"])
+        h = 0
+        for b in buf.tobytes():
+            h = (h * 31 + b) & 0xFFFFFFFF
+        jt = js["tensors"][n]
+        assert jt["dims"] == list(t["dims"]) and jt["type"] == t["type"] and jt["offset"] == t["offset"]
+        assert jt["n"] == buf.size and jt["h"] == h, n
+
+
+@pytest.mark.gpu
+def test_js_host_matches_python_host(tmp_path):
+    cfg = tiny_config()
+    path = tmp_path / "tiny.gguf"
+    _write_model(path, cfg, 41)
+    prompt = [int(x) for x in np.random.default_rng(41).integers(0, cfg.vocab, 12)]
+    over = {"ring": cfg.ring, "maxSeq": cfg.max_seq}
+    r = subprocess.run([NODE, os.path.join(JS, "run_greedy.js"), str(path), ",".join(map(str, prompt)), "24",
+                        json.dumps(over)], check=True, capture_output=True, text=True, timeout=300)
+    js = json.loads(r.stdout.strip().splitlines()[-1])
+    eng = Engine.from_gguf(str(path), ring=cfg.ring, max_seq=cfg.max_seq)
+    gen = eng.generate_fast(prompt, 24, eos=())
+    eng.reset()
+    steps = [eng.step(t, i) for i, t in enumerate(prompt)]
+    h = eng.read_hidden()
+    print(f"js host: generate {js['generate'][:8]}..., python {gen[:8]}...")
+    assert js["generate"] == gen
+    assert js["steps"] == steps
+    assert abs(js["hidden_l2"] - float(np.sqrt((h.astype(np.float64) ** 2).sum()))) <= 1e-5 * js["hidden_l2"]
