@@ -166,25 +166,197 @@ __global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
     }
 }
 
+// ---- LDS-staged variant ---------------------------------------------------
+// The workgroup's weight tile (128 rows; GeGLU: 128 gate + 128 up rows) is
+// loaded cooperatively, KBL contiguous blocks (64 bytes) per row and thread
+// group, instead of 16 bytes of 32 rows per wave instruction; the next
+// stage's weights, scales and activations are requested into registers
+// before the current stage's MFMAs and written to LDS after them, so each
+// stage's load latency overlaps the previous stage's math.
+constexpr int KBL = 4;            // q4_0 blocks per stage (128 k)
+constexpr int WSL = KBL + 1;      // uint4 per staged weight row (+1 pad: conflict-free 16-byte reads)
+constexpr int SSL = KBL + 2;      // f16 scales per staged row (+2 pad)
+constexpr int XSL = KBL * 4 + 1;  // uint4 per staged token row (+1 pad)
+
+template <int T, int EPI, bool GRP>
+__global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs) {
+  constexpr int NT = EPI == GEMM_GLU ? 2 : 1;
+  constexpr int TOK = 32 * T;
+  constexpr int RW = 128 * NT;                 // staged weight rows
+  constexpr int WP = RW * KBL / 256;           // nibble pieces per thread and stage
+  constexpr int SP = RW * KBL / 256;           // scales per thread and stage
+  constexpr int XP = TOK * KBL * 4 / 256;      // activation pieces per thread and stage
+  static_assert(WP >= 1 && SP >= 1 && XP >= 1, "whole pieces per thread");
+  __shared__ __align__(16) uint4 wl[RW][WSL];
+  __shared__ uint16_t sl[RW][SSL];
+  __shared__ __align__(16) uint4 xs[TOK][XSL];
+  const Q40Mat& W = a.W;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int nb = K / 32;
+  const int M = a.M;
+  const int64_t units = EPI == GEMM_GLU ? a.ff : (GRP ? a.group_rows : W.rows);
+  int tok0, nrows;
+  int64_t wbase = 0;
+  if constexpr (GRP) {
+    if ((int)blockIdx.y >= *a.ntiles) return;  // the grid is sized for the most tiles
+    const int4 tl = a.tiles[blockIdx.y];
+    wbase = (int64_t)tl.x * a.group_rows;
+    tok0 = tl.y;
+    nrows = tl.z;
+  } else {
+    tok0 = blockIdx.y * TOK;
+    nrows = M - tok0;
+  }
+  const int64_t c0 = (int64_t)blockIdx.x * 128;  // first output column of the workgroup
+  const int kz = blockIdx.z;
+  const int kbeg = kz * nbs, kend = min(nb, kbeg + nbs);
+  // global weight row of staged row r (clamped: rows past the end are loaded
+  // from a valid row and never stored)
+  auto grow = [&](int r) -> int64_t {
+    if constexpr (EPI == GEMM_GLU)
+      return wbase + (r >= 128 ? a.ff : 0) + min(c0 + (r & 127), units - 1);
+    else
+      return wbase + min(c0 + r, units - 1);
+  };
+  uint4 wr[WP];
+  uint16_t sr[SP];
+  uint4 xr[XP];
+  auto issue = [&](int kb0) {
+#pragma unroll
+    for (int j = 0; j < WP; ++j) {
+      const int p = threadIdx.x + 256 * j;
+      const int r = p / KBL, b = p % KBL;
+      const uint32_t e = (uint32_t)grow(r) * (uint32_t)nb + (uint32_t)min(kb0 + b, nb - 1);
+      wr[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(W.nib) + e * 16u);
+    }
+#pragma unroll
+    for (int j = 0; j < SP; ++j) {
+      const int q = threadIdx.x + 256 * j;
+      const int r = q / KBL, b = q % KBL;
+      // blocks past the row end repeat the last block's scale (they meet zero activations)
+      const uint32_t e = (uint32_t)grow(r) * (uint32_t)nb + (uint32_t)min(kb0 + b, nb - 1);
+      sr[j] = W.sc[e];
+    }
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      const int m = i / (KBL * 4), q = i % (KBL * 4);
+      const int kq = kb0 * 32 + q * 8;
+      const bool in = m < nrows && kq < kend * 32;
+      int64_t xrow = tok0 + m;
+      if constexpr (GRP) xrow = a.gather ? (int64_t)(a.gather[in ? xrow : tok0] / (uint32_t)a.gather_div) : xrow;
+      const uint4 v = *reinterpret_cast<const uint4*>(a.X + (in ? xrow * a.ldx + kq : 0));
+      xr[j] = in ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int j = 0; j < WP; ++j) {
+      const int p = threadIdx.x + 256 * j;
+      wl[p / KBL][p % KBL] = wr[j];
+    }
+#pragma unroll
+    for (int j = 0; j < SP; ++j) {
+      const int q = threadIdx.x + 256 * j;
+      sl[q / KBL][q % KBL] = sr[j];
+    }
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      xs[i / (KBL * 4)][i % (KBL * 4)] = xr[j];
+    }
+  };
+
+  f16v acc[NT][T];
+#pragma unroll
+  for (int u = 0; u < NT; ++u)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[u][t][r] = 0.f;
+  // this wave's staged rows: tile u = rows 128 u + 32 wave + l32
+  int lrow[NT];
+#pragma unroll
+  for (int u = 0; u < NT; ++u) lrow[u] = 128 * u + 32 * wave + l32;
+
+  issue(kbeg);
+  store();
+  lds_sync();
+  for (int kb0 = kbeg; kb0 < kend; kb0 += KBL) {
+    // the next stage (the last iteration repeats its own, unused): the loop
+    // body stays one basic block
+    issue(kb0 + KBL < kend ? kb0 + KBL : kb0);
+#pragma unroll
+    for (int b = 0; b < KBL; ++b) {
+      h8 bw[NT][2];
+      float dsc[NT];
+#pragma unroll
+      for (int u = 0; u < NT; ++u) {
+        const uint4 w4 = wl[lrow[u]][b];
+        bw[u][0] = nib_word_f16(hi ? w4.y : w4.x);
+        bw[u][1] = nib_word_f16(hi ? w4.w : w4.z);
+        dsc[u] = h2f(sl[lrow[u]][b]);
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint4 a0 = xs[32 * t + l32][4 * b + hi];
+        const uint4 a1 = xs[32 * t + l32][4 * b + 2 + hi];
+        const h8 av0 = __builtin_bit_cast(h8, a0), av1 = __builtin_bit_cast(h8, a1);
+#pragma unroll
+        for (int u = 0; u < NT; ++u) {
+          f16v d = {};
+          d = __builtin_amdgcn_mfma_f32_32x32x16_f16(av0, bw[u][0], d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_32x32x16_f16(av1, bw[u][1], d, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[u][t][r] = fmaf(dsc[u], d[r], acc[u][t][r]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_sync();
+    store();
+    lds_sync();
+  }
+  // store: lane owns column c0 + 32 wave + l32, tokens 32 t + 8 (r / 4) + 4 hi + r % 4
+  const int64_t n = c0 + 32 * wave + l32;
+  if (n >= units) return;
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ml = 32 * t + 8 * (r / 4) + 4 * hi + (r % 4);
+      const int m = tok0 + ml;
+      if (ml < nrows) {
+        if constexpr (EPI == GEMM_GLU)
+          a.Yh[(int64_t)m * a.ff + n] = f2h(gelu_tanh(acc[0][t][r]) * acc[1][t][r]);
+        else if constexpr (EPI == GEMM_GELU_MUL)
+          a.Yh[(int64_t)m * units + n] = f2h(gelu_tanh(acc[0][t][r]) * a.mul[(int64_t)m * a.mul_ld + n]);
+        else
+          a.Y[((int64_t)kz * M + m) * units + n] = acc[0][t][r];
+      }
+    }
+}
+
 template <int EPI>
 void launch_t(int T, const GemmArgs& a, dim3 grid, int K, int nbs, hipStream_t st) {
   if (a.tiles) {
-    hipLaunchKernelGGL((k_q40_gemm<1, EPI, true>), grid, dim3(256), 0, st, a, K, nbs);
+    hipLaunchKernelGGL((k_q40_gemm_lds<1, EPI, true>), grid, dim3(256), 0, st, a, K, nbs);
     return;
   }
   if (T == 4)
-    hipLaunchKernelGGL((k_q40_gemm<4, EPI>), grid, dim3(256), 0, st, a, K, nbs);
+    hipLaunchKernelGGL((k_q40_gemm_lds<4, EPI, false>), grid, dim3(256), 0, st, a, K, nbs);
   else if (T == 2)
-    hipLaunchKernelGGL((k_q40_gemm<2, EPI>), grid, dim3(256), 0, st, a, K, nbs);
+    hipLaunchKernelGGL((k_q40_gemm_lds<2, EPI, false>), grid, dim3(256), 0, st, a, K, nbs);
   else
-    hipLaunchKernelGGL((k_q40_gemm<1, EPI>), grid, dim3(256), 0, st, a, K, nbs);
+    hipLaunchKernelGGL((k_q40_gemm_lds<1, EPI, false>), grid, dim3(256), 0, st, a, K, nbs);
 }
 
 }  // namespace
 
 int q40_gemm_kslices(int nb, int want) {
   for (int ks = want < 1 ? 1 : want; ks > 1; --ks) {
-    const int nbs = ((nb + ks - 1) / ks + KB - 1) / KB * KB;
+    const int nbs = ((nb + ks - 1) / ks + KBL - 1) / KBL * KBL;
     if ((nb + nbs - 1) / nbs == ks) return ks;
   }
   return 1;
@@ -222,7 +394,7 @@ int launch_q40_gemm(const GemmArgs& a, hipStream_t st) {
   }
   // blocks per split-K slice, a multiple of the LDS stage; the consumer sums
   // exactly `ks` slices, so every slice must hold blocks
-  const int nbs = ((W.nb + ks - 1) / ks + KB - 1) / KB * KB;
+  const int nbs = ((W.nb + ks - 1) / ks + KBL - 1) / KBL * KBL;
   const int kslices = (W.nb + nbs - 1) / nbs;
   if (kslices != ks)
     return e4b_fail(E4B_EINVAL, "q4_0 GEMM: %d blocks do not split into %d slices (use q40_gemm_kslices)", W.nb, ks);
