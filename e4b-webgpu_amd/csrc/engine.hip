@@ -483,8 +483,11 @@ int record_step(e4b_ctx* c) {
     }
     if (rc) return rc;
     // 2. attention (head prep, KV write, split-K); the combine is the o
-    //    projection's prologue when the projection has 2048 columns
-    const bool fuse_combine = QH * HD == kProAttnH;
+    //    projection's prologue when the projection has 2048 columns and the
+    //    layer's live span fits the prologue's 64 chunks per head (global
+    //    layers of contexts beyond 4096 positions use the combine launch)
+    const int gch_layer = attn_chunks(ly.global ? ly.slots : k.window, c->chunk);
+    const bool fuse_combine = QH * HD == kProAttnH && gch_layer <= kProAttnMaxChunks;
     AttnLaunch a;
     a.qkv = c->qkv;
     a.qw = ly.q_norm;
@@ -518,7 +521,7 @@ int record_step(e4b_ctx* c) {
       pa.params = c->params;
       pa.window = a.window;
       pa.chunk_shift = c->chunk == 64 ? 6 : 5;
-      pa.gch = attn_chunks(a.window > 0 ? a.window : a.slots, c->chunk);
+      pa.gch = gch_layer;
       rc = launch_q40(Wo, nullptr, nullptr, EPI_F32, oo, 1, st, &pa);
     } else {
       rc = launch_q40(Wo, (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st);

@@ -73,6 +73,7 @@ struct GemvOut {
 //    an o projection of 2048 columns (8 heads of 256).
 constexpr int kMaxPartials = 8;
 constexpr int kProAttnH = 2048;  // columns of an o projection with the attention prologue (8 heads of 256)
+constexpr int kProAttnMaxChunks = 64;  // split-K chunks per head the attention prologue merges (one lane each)
 struct ProArgs {
   const float* hin;
   float* hout;       // may be null

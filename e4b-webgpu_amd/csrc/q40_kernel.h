@@ -112,7 +112,7 @@ DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB, NA>& r) {
 // further passes (U = kProAttnFirst).
 constexpr int kProAttn = -1;
 constexpr int kProAttnFirst = 8;
-constexpr int kProAttnMaxCh = 64;  // chunks per head the prologue supports (one lane each)
+constexpr int kProAttnMaxCh = kProAttnMaxChunks;  // chunks per head the prologue supports (one lane each)
 constexpr int kProAttnNH = kProAttnH / 256;
 static_assert(kProAttnNH == 8, "two heads per wave");
 // thread t merges head t/32, dims 8 (t % 32) .. 8 (t % 32) + 7 (two 16-byte

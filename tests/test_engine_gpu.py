@@ -192,3 +192,39 @@ def test_c4_width_256_forced_tokens_argmax():
     err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
     print(f"c4-width forced 256: near-ties {ties}, final logits err {err:.2e}")
     assert err < LOGIT_TOL
+
+
+def test_unfused_attention_combine_lockstep():
+    # 32-position chunks over a 4096-slot global cache = 128 chunks per head,
+    # more than the o projection's fused combine prologue merges (64): the
+    # global layer takes the separate combine launch + plain o GEMV path
+    cfg = tiny_config(attn_chunk=32, max_seq=4096)
+    eng, om = build(cfg, 61)
+    prompt = np.random.default_rng(61).integers(0, cfg.vocab, 12)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 12)
+    print(f"unfused combine: near-ties {ties}")
+    assert len(ties) == 0
+    err = float(np.max(np.abs(eng.read_logits() - o_lg)) / np.max(np.abs(o_lg)))
+    assert err < LOGIT_TOL
+
+
+def test_context_beyond_4096_positions():
+    # an 8192-position global cache (128 chunks of 64 per head): a 4300-token
+    # prompt through the batched prefill (chunks of 512) against the same
+    # prompt through the decode step, then GPU-fed decode past position 4096
+    from e4b._lib import FLAG_STEP_PREFILL
+    kw = dict(hidden=256, layers=2, ffn=512, vocab=1000, window=512, ring=1024, max_seq=8192, layer_global=[0, 1])
+    cfg = tiny_config(**kw)
+    tensors = norm_weights_random(synth_tensors(cfg, 71), 72)
+    a = Engine(cfg, tensors)
+    b = Engine(tiny_config(flags=FLAG_STEP_PREFILL, **kw), tensors)
+    prompt = np.random.default_rng(73).integers(0, cfg.vocab, 4300)
+    ga, gb = a.prefill(prompt), b.prefill(prompt)
+    la, lb = a.read_logits(), b.read_logits()
+    err = float(np.max(np.abs(la - lb)) / np.max(np.abs(lb)))
+    print(f"4300-token prompt: batched {ga} step {gb}, logits err {err:.2e}")
+    assert err < LOGIT_TOL
+    assert ga == gb or top2_margin(lb) < TIE_TOL * np.abs(lb).max()
+    ta, tb = a.decode_chunk(4300, 16), b.decode_chunk(4300, 16)
+    print(f"continuations {ta.tolist()} / {tb.tolist()}")
+    assert np.array_equal(ta, tb)
