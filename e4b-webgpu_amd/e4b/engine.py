@@ -57,6 +57,33 @@ def config_from_kv(kv: dict, **overrides) -> E4BConfig:
     return E4BConfig(**args)
 
 
+def gguf_config(path: str, **overrides) -> E4BConfig:
+    """The engine configuration of a GGUF file as the library reads it
+    (e4b_gguf_config); fields the file cannot hold (ring, max_seq, ...) come
+    from the E4BConfig defaults or `overrides`."""
+    base = E4BConfig(**overrides)
+    c = ConfigC()
+    for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
+              "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags"):
+        setattr(c, f, int(getattr(base, f)))
+    for f in ("theta_local", "theta_global", "eps", "softcap"):
+        setattr(c, f, float(getattr(base, f)))
+    lg = np.zeros(4096, np.uint8)
+    check(lib.e4b_gguf_config(path.encode(), C.byref(c), _p(lg), lg.size), "e4b_gguf_config")
+    args = {f: getattr(c, f) for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim",
+                                          "vocab", "window", "ring", "max_seq", "rope_angles", "attn_chunk",
+                                          "max_prompt", "flags")}
+    args.update({f: float(getattr(c, f)) for f in ("theta_local", "theta_global", "eps", "softcap")})
+    if c.layer_global:
+        args["layer_global"] = [int(x) for x in lg[:c.layers]]
+    elif "layer_global" in overrides:
+        args["layer_global"] = list(overrides["layer_global"])
+    for k, v in overrides.items():
+        if k in ("ring", "max_seq", "attn_chunk", "max_prompt", "flags"):
+            args[k] = v
+    return E4BConfig(**args)
+
+
 class Engine:
     def __init__(self, cfg: E4BConfig, tensors=None):
         self.cfg = cfg
@@ -86,6 +113,17 @@ class Engine:
 
     def finalize(self) -> None:
         check(lib.e4b_finalize(self.ctx), "e4b_finalize")
+
+    @classmethod
+    def load_native(cls, path: str, **overrides) -> "Engine":
+        """Load through the library's own GGUF loader (e4b_gguf_config +
+        e4b_load_gguf: the file is memory-mapped and uploaded tensor by
+        tensor without passing through Python)."""
+        cfg = gguf_config(path, **overrides)
+        eng = cls(cfg)
+        check(lib.e4b_load_gguf(eng.ctx, path.encode()), "e4b_load_gguf")
+        eng.finalize()
+        return eng
 
     @classmethod
     def from_gguf(cls, path: str, **overrides) -> "Engine":

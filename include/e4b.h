@@ -320,6 +320,27 @@ void e4b_destroy(e4b_ctx* ctx);
 /* timing: run `count` GPU-fed steps and return the elapsed device ms */
 int  e4b_time_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, float* ms_out);
 
+/* GGUF loading on the C ABI (openGGUF, src/gguf.js:17-83, and the tensor
+ * loop of loadEngineA4B, src/engine-a4b.js:121-214): the file is
+ * memory-mapped; tokenizer.* metadata is skipped; the data start is aligned
+ * to general.alignment (default 32).
+ *   e4b_gguf_config: reads <arch>.embedding_length, block_count,
+ *     attention.head_count(_kv), attention.key_length, feed_forward_length,
+ *     embedding_length_per_layer_input, vocab_size, attention.sliding_window,
+ *     rope.dimension_count_half, rope.freq_base(_swa),
+ *     attention.layer_norm_rms_epsilon, final_logit_softcapping and
+ *     attention.sliding_window_pattern (true = sliding) into cfg; fields the
+ *     file lacks keep the caller's values (ring, max_seq, attn_chunk,
+ *     max_prompt and flags are never in the file); the layer pattern is
+ *     written to layer_global[cap] and cfg->layer_global points to it.
+ *   e4b_load_gguf: e4b_set_tensor for every tensor of the file (call
+ *     e4b_finalize afterwards).
+ *   e4b_open_gguf: config (from `base`, or ring 1024 / max_seq 4096 when
+ *     NULL) + create + load + finalize in one call; NULL on error. */
+int  e4b_gguf_config(const char* path, e4b_config* cfg, uint8_t* layer_global, int cap);
+int  e4b_load_gguf(e4b_ctx* ctx, const char* path);
+e4b_ctx* e4b_open_gguf(const char* path, const e4b_config* base);
+
 #ifdef __cplusplus
 }
 #endif

@@ -130,3 +130,33 @@ def test_rope_table_matches_oracle():
     from e4b.kernels import rope_inv_freq
     for theta in (1e4, 1e6):
         np.testing.assert_array_equal(rope_inv_freq(theta, 256, 128), orc.rope_inv_freq(theta, 256, 128))
+
+
+def test_native_gguf_config_matches_metadata(tmp_path):
+    # e4b_gguf_config (the library's C++ reader) returns the configuration
+    # written by config_to_kv; missing, non-GGUF and truncated files fail
+    from e4b._lib import E4BError
+    from e4b.engine import config_to_kv, gguf_config
+    from e4b.gguf import write_gguf
+    from e4b.model import synth_tensors, tiny_config
+    cfg = tiny_config(layers=3, layer_global=[0, 1, 0], theta_local=12345.0, softcap=25.0)
+    path = tmp_path / "m.gguf"
+    t = synth_tensors(cfg, 5)
+    write_gguf(str(path), config_to_kv(cfg), [(x.name, x.ggml_type, x.dims, x.data) for x in t.values()])
+    got = gguf_config(str(path), ring=cfg.ring, max_seq=cfg.max_seq)
+    for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window",
+              "rope_angles", "ring", "max_seq"):
+        assert getattr(got, f) == getattr(cfg, f), f
+    for f in ("theta_local", "theta_global", "eps", "softcap"):
+        assert abs(getattr(got, f) - getattr(cfg, f)) <= 1e-6 * abs(getattr(cfg, f)), f
+    assert got.layer_global == [0, 1, 0]
+    with pytest.raises(E4BError):
+        gguf_config(str(tmp_path / "absent.gguf"))
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"NOPE" + bytes(60))
+    with pytest.raises(E4BError):
+        gguf_config(str(bad))
+    trunc = tmp_path / "trunc.gguf"
+    trunc.write_bytes(path.read_bytes()[:200])
+    with pytest.raises(E4BError):
+        gguf_config(str(trunc))

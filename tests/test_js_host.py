@@ -26,7 +26,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 JS = os.path.join(ROOT, "e4b-webgpu_amd", "js")
 NODE = shutil.which("node")
 
-pytestmark = pytest.mark.skipif(NODE is None or not os.path.exists(os.path.join(JS, "e4b_napi.node")),
+_needs_node = pytest.mark.skipif(NODE is None or not os.path.exists(os.path.join(JS, "e4b_napi.node")),
                                 reason="node or the N-API addon is missing (build() makes the addon)")
 
 
@@ -41,6 +41,7 @@ def _write_model(path, cfg, seed):
     return tensors
 
 
+@_needs_node
 def test_addon_exports_engine_surface():
     out = _node("const a = require('./e4b_napi.node'); console.log(JSON.stringify(Object.keys(a).sort()), a.version())")
     keys = json.loads(out.split()[0])
@@ -50,6 +51,7 @@ def test_addon_exports_engine_surface():
     assert "gfx950" in out
 
 
+@_needs_node
 def test_node_gguf_reader_matches_python(tmp_path):
     cfg = tiny_config(layers=2, layer_global=[0, 1])
     path = tmp_path / "m.gguf"
@@ -88,6 +90,7 @@ const {{ openGGUF }} = require('./gguf');
         assert jt["n"] == buf.size and jt["h"] == h, n
 
 
+@_needs_node
 @pytest.mark.gpu
 def test_js_host_matches_python_host(tmp_path):
     cfg = tiny_config()
@@ -107,3 +110,18 @@ def test_js_host_matches_python_host(tmp_path):
     assert js["generate"] == gen
     assert js["steps"] == steps
     assert abs(js["hidden_l2"] - float(np.sqrt((h.astype(np.float64) ** 2).sum()))) <= 1e-5 * js["hidden_l2"]
+
+
+@pytest.mark.gpu
+def test_native_gguf_loader_matches_python_loader(tmp_path):
+    # the library's own mmap loader (e4b_gguf_config + e4b_load_gguf) and the
+    # Python reader feeding e4b_set_tensor build the same engine
+    cfg = tiny_config(layers=3, layer_global=[0, 0, 1])
+    path = tmp_path / "m.gguf"
+    _write_model(path, cfg, 52)
+    prompt = [int(x) for x in np.random.default_rng(52).integers(0, cfg.vocab, 10)]
+    a = Engine.load_native(str(path), ring=cfg.ring, max_seq=cfg.max_seq)
+    b = Engine.from_gguf(str(path), ring=cfg.ring, max_seq=cfg.max_seq)
+    ga, gb = a.generate_fast(prompt, 16, eos=()), b.generate_fast(prompt, 16, eos=())
+    assert ga == gb
+    assert np.array_equal(a.read_logits(), b.read_logits())
