@@ -19,13 +19,15 @@
 // scaled by the row's block scale, as the decode GEMV does, so the products
 // are exact and only the f32 summation order differs.
 //
-// Workgroup: 4 waves x 32 rows (x2 for GeGLU: gate and up tiles), T token
-// tiles of 32 per wave; the X slice of KB blocks for the workgroup's 32 T
-// tokens is staged in LDS and shared by the 4 waves.  blockIdx.z selects a
-// split-K slice.  Row tiles are blockIdx.x, so the workgroups that share a
-// weight tile (same x, different token tiles) sit a multiple of 8 apart in
-// dispatch order when the row-tile count is a multiple of 8: the same XCD and
-// its L2.
+// Workgroup: 4 waves x 32 output columns (GeGLU: a gate and an up tile), T
+// token tiles of 32 per wave.  Per stage of KBL blocks (128 k) the weight
+// tile (128 rows; GeGLU 256), its block scales and the activations of the
+// workgroup's 32 T tokens are staged in LDS with row-contiguous cooperative
+// loads and shared by the 4 waves; the next stage is requested into
+// registers before the current stage's MFMAs.  blockIdx.z selects a split-K
+// slice.  Row tiles are blockIdx.x, so the workgroups that share a weight
+// tile (same x, different token tiles) sit a multiple of 8 apart in dispatch
+// order when the row-tile count is a multiple of 8: the same XCD and its L2.
 #include "../../include/e4b.h"
 #include "kernels.h"
 #include "util.h"
@@ -34,8 +36,6 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
-
-constexpr int KB = 2;  // q4_0 blocks per LDS stage (64 k)
 
 // 8 exact f16 values (n - 8) of one repacked nibble word, in element order
 DEV h8 nib_word_f16(uint32_t w) {
@@ -52,127 +52,10 @@ DEV h8 nib_word_f16(uint32_t w) {
   return r;
 }
 
-template <int T, int EPI, bool GRP = false>
-__global__ __launch_bounds__(256) void k_q40_gemm(GemmArgs a, int K, int nbs) {
-  constexpr int NT = EPI == GEMM_GLU ? 2 : 1;  // weight tiles per wave (gate, up)
-  constexpr int TOK = 32 * T;                  // tokens per workgroup
-  // KB blocks x 64 B per token, plus one 16-byte pad so that the 16-byte
-  // reads of 8 consecutive token rows hit distinct LDS bank groups
-  __shared__ __align__(16) uint4 xs[TOK][KB * 4 + 1];
-  const Q40Mat& W = a.W;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int nb = K / 32;
-  const int M = a.M;
-  // output columns, and the weight rows of this workgroup's group
-  const int64_t units = EPI == GEMM_GLU ? a.ff : (GRP ? a.group_rows : W.rows);
-  int tok0, nrows;
-  int64_t wbase = 0;
-  if constexpr (GRP) {
-    if ((int)blockIdx.y >= *a.ntiles) return;  // the grid is sized for the most tiles
-    const int4 tl = a.tiles[blockIdx.y];
-    wbase = (int64_t)tl.x * a.group_rows;
-    tok0 = tl.y;
-    nrows = tl.z;
-  } else {
-    tok0 = blockIdx.y * TOK;
-    nrows = M - tok0;
-  }
-  const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * 32;  // first output column of this wave
-  const int kz = blockIdx.z;
-  const int kbeg = kz * nbs, kend = min(nb, kbeg + nbs);  // this slice's blocks
-  // this lane's weight rows (clamped: tiles past the end compute duplicates, never stored)
-  int64_t wrow[NT];
-  wrow[0] = wbase + min(n0 + l32, units - 1);
-  if constexpr (EPI == GEMM_GLU) wrow[1] = a.ff + wrow[0];
-  f16v acc[NT][T];
-#pragma unroll
-  for (int u = 0; u < NT; ++u)
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[u][t][r] = 0.f;
-
-  for (int kb0 = kbeg; kb0 < kend; kb0 += KB) {
-    // this lane's weight words and scales for the stage, requested first
-    uint32_t wv[NT][KB][2];
-    float dsc[NT][KB];
-#pragma unroll
-    for (int u = 0; u < NT; ++u)
-#pragma unroll
-      for (int b = 0; b < KB; ++b) {
-        const int kb = min(kb0 + b, nb - 1);
-        const uint32_t e = (uint32_t)wrow[u] * (uint32_t)nb + (uint32_t)kb;
-        const uint4 w4 = ld_nt_u4_off(W.nib, e);
-        wv[u][b][0] = hi ? w4.y : w4.x;  // step 0: word (l / 32)
-        wv[u][b][1] = hi ? w4.w : w4.z;  // step 1: word 2 + (l / 32)
-        dsc[u][b] = kb0 + b < kend ? scale_of(ld_scale_pair_off(W.sc, e), e & 1) : 0.f;
-      }
-    // stage X[tok0 .. tok0+TOK)[32 kb0 .. 32 (kb0+KB)) (zeros past M or the slice)
-    for (int i = threadIdx.x; i < TOK * KB * 4; i += 256) {
-      const int m = i / (KB * 4), q = i % (KB * 4);
-      const int kq = kb0 * 32 + q * 8;  // first k of this 16-byte piece
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (m < nrows && kq < kend * 32) {
-        int64_t xr = tok0 + m;
-        if constexpr (GRP) xr = a.gather ? (int64_t)(a.gather[xr] / (uint32_t)a.gather_div) : xr;
-        v = *reinterpret_cast<const uint4*>(a.X + xr * a.ldx + kq);
-      }
-      xs[m][q] = v;
-    }
-    lds_sync();
-#pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      h8 bw[NT][2];
-#pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        bw[u][0] = nib_word_f16(wv[u][b][0]);
-        bw[u][1] = nib_word_f16(wv[u][b][1]);
-      }
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const uint4 a0 = xs[32 * t + l32][4 * b + hi];
-        const uint4 a1 = xs[32 * t + l32][4 * b + 2 + hi];
-        const h8 av0 = __builtin_bit_cast(h8, a0), av1 = __builtin_bit_cast(h8, a1);
-#pragma unroll
-        for (int u = 0; u < NT; ++u) {
-          f16v d = {};
-          d = __builtin_amdgcn_mfma_f32_32x32x16_f16(av0, bw[u][0], d, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_32x32x16_f16(av1, bw[u][1], d, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[u][t][r] = fmaf(dsc[u][b], d[r], acc[u][t][r]);
-        }
-      }
-    }
-    lds_sync();
-  }
-  // store: lane owns column n0 + l32, tokens 32 t + 8 (r / 4) + 4 hi + r % 4
-  const int64_t n = n0 + l32;
-  if (n >= units) return;
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int ml = 32 * t + 8 * (r / 4) + 4 * hi + (r % 4);
-      const int m = tok0 + ml;
-      if (ml < nrows) {
-        if constexpr (EPI == GEMM_GLU)
-          a.Yh[(int64_t)m * a.ff + n] = f2h(gelu_tanh(acc[0][t][r]) * acc[1][t][r]);
-        else if constexpr (EPI == GEMM_GELU_MUL)
-          a.Yh[(int64_t)m * units + n] = f2h(gelu_tanh(acc[0][t][r]) * a.mul[(int64_t)m * a.mul_ld + n]);
-        else
-          a.Y[((int64_t)kz * M + m) * units + n] = acc[0][t][r];
-      }
-    }
-}
-
-// ---- LDS-staged variant ---------------------------------------------------
-// The workgroup's weight tile (128 rows; GeGLU: 128 gate + 128 up rows) is
-// loaded cooperatively, KBL contiguous blocks (64 bytes) per row and thread
-// group, instead of 16 bytes of 32 rows per wave instruction; the next
-// stage's weights, scales and activations are requested into registers
-// before the current stage's MFMAs and written to LDS after them, so each
-// stage's load latency overlaps the previous stage's math.
+// The weight tile is loaded cooperatively, KBL contiguous blocks (64 bytes)
+// per row and thread group -- a wave that loaded its own B fragments would
+// touch 32 rows with 16 bytes each per instruction, which measured 1.5-2.3x
+// slower -- and each stage's loads overlap the previous stage's math.
 constexpr int KBL = 4;            // q4_0 blocks per stage (128 k)
 constexpr int WSL = KBL + 1;      // uint4 per staged weight row (+1 pad: conflict-free 16-byte reads)
 constexpr int SSL = KBL + 2;      // f16 scales per staged row (+2 pad)
