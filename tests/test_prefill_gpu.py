@@ -158,3 +158,26 @@ def test_c4_width_prefill_matches_step_prefill():
     tb = b.decode_chunk(512, 8)
     print(f"continuations {ta.tolist()} / {tb.tolist()}")
     assert np.array_equal(ta, tb)
+
+
+@pytest.mark.parametrize("n2", [9, 18, 19])
+def test_prefill_again_after_decode_matches_fresh_engine(n2):
+    # a second prefill (positions restart at 0) over caches that still hold
+    # the first prompt and its decode: every key a query reads is rewritten
+    # first, so tokens, logits and the written cache rows equal a fresh
+    # engine's; n2 covers one chunk exactly (9 = ring - window + 1), two, and
+    # two plus one token
+    cfg = tiny_config()
+    tensors = norm_weights_random(synth_tensors(cfg, 83), 84)
+    a, b = Engine(cfg, tensors), Engine(cfg, tensors)
+    rng = np.random.default_rng(n2)
+    p1 = rng.integers(0, cfg.vocab, 30)
+    p2 = rng.integers(0, cfg.vocab, n2)
+    a.prefill(p1)
+    a.decode_chunk(30, 10)
+    ga, gb = a.prefill(p2), b.prefill(p2)
+    assert ga == gb
+    assert np.array_equal(a.read_logits(), b.read_logits())
+    ta, tb = a.decode_chunk(n2, 8), b.decode_chunk(n2, 8)
+    assert np.array_equal(ta, tb)
+    assert np.array_equal(a.read_logits(), b.read_logits())
