@@ -91,39 +91,96 @@ __global__ __launch_bounds__(256) void k_ple_prep_rows(const float* __restrict__
   ple[o] = (pv * inv * wn + idv) * 0.70710678118654752f;
 }
 
+// N contiguous floats at p (aligned to min(N, 4) floats) with the widest loads
+template <int N>
+DEV void ld_row(const float* p, float (&v)[N]) {
+  if constexpr (N == 1) {
+    v[0] = p[0];
+  } else if constexpr (N == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+  } else {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const float4 t = reinterpret_cast<const float4*>(p)[q];
+      v[4 * q] = t.x;
+      v[4 * q + 1] = t.y;
+      v[4 * q + 2] = t.z;
+      v[4 * q + 3] = t.w;
+    }
+  }
+}
+template <int N>
+DEV void st_row(float* p, const float (&v)[N]) {
+  if constexpr (N == 1) {
+    p[0] = v[0];
+  } else if constexpr (N == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q)
+      reinterpret_cast<float4*>(p)[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+  }
+}
+// N f16 values (N >= 2: 4-byte aligned) in one store per 8
+template <int N>
+DEV void st_halves(uint16_t* p, const uint16_t (&v)[N]) {
+  if constexpr (N == 1) {
+    p[0] = v[0];
+  } else {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) w[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+    if constexpr (N == 2) {
+      *reinterpret_cast<uint32_t*>(p) = w[0];
+    } else if constexpr (N == 4) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < N / 8; ++q)
+        reinterpret_cast<uint4*>(p)[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    }
+  }
+}
+
 // one workgroup per token m:
 //   h = (h + rms(a) * w1) * scale, a = sum of na partial slices (a may be null)
 //   w2 != null: x = f16(rms(h) * w2), else x = f16(h); with xlo the value is
 //   stored as the exact split x = f16(y), xlo = f16(y - x) (the lm-head input)
-template <int PER>
+// H = 256 PER; thread t owns elements [PER t, PER t + PER).  NAM = 0: no
+// residual input; else na <= NAM slices, all requested before the first use
+// (slice indices past na repeat the last one and are not added), summed in
+// slice order.
+template <int PER, int NAM>
 __global__ __launch_bounds__(256) void k_resnorm_rows(float* __restrict__ h, const float* __restrict__ a, int na,
                                                       int64_t slice, const float* __restrict__ w1, float scale,
                                                       const float* __restrict__ w2, uint16_t* __restrict__ x,
                                                       uint16_t* __restrict__ xlo, int H, float eps) {
   __shared__ float red[4];
   const int m = blockIdx.x;
-  float* hm = h + (int64_t)m * H;
-  float hv[PER], av[PER];
-  float ss = 0.f;
+  const int i0 = threadIdx.x * PER;
+  const int64_t row = (int64_t)m * H + i0;
+  float hv[PER];
+  ld_row<PER>(h + row, hv);
+  float av[NAM > 0 ? NAM : 1][PER], w1v[PER];
+  if constexpr (NAM > 0) {
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    hv[k] = i < H ? hm[i] : 0.f;
-    float s = 0.f;
-    if (a && i < H) {
-      s = a[(int64_t)m * H + i];
-      for (int z = 1; z < na; ++z) s += a[z * slice + (int64_t)m * H + i];
-    }
-    av[k] = s;
-    ss = fmaf(s, s, ss);
-  }
-  if (a) {
-    const float inv1 = rms_inv(block_sum(ss, red), H, eps);
+    for (int z = 0; z < NAM; ++z) ld_row<PER>(a + (int64_t)min(z, na - 1) * slice + row, av[z]);
+    ld_row<PER>(w1 + i0, w1v);
+    float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      hv[k] = i < H ? hv[k] + av[k] * inv1 * w1[i] : 0.f;
+      float s = av[0][k];
+#pragma unroll
+      for (int z = 1; z < NAM; ++z)
+        if (z < na) s += av[z][k];
+      av[0][k] = s;
+      ss = fmaf(s, s, ss);
     }
+    const float inv1 = rms_inv(block_sum(ss, red), H, eps);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) hv[k] = hv[k] + av[0][k] * inv1 * w1v[k];
   }
   float s2 = 0.f;
 #pragma unroll
@@ -131,18 +188,29 @@ __global__ __launch_bounds__(256) void k_resnorm_rows(float* __restrict__ h, con
     hv[k] *= scale;
     s2 = fmaf(hv[k], hv[k], s2);
   }
-  const float inv2 = w2 ? rms_inv(block_sum(s2, red), H, eps) : 1.f;
+  st_row<PER>(h + row, hv);
+  uint16_t xv[PER], xl[PER];
+  if (w2) {
+    float w2v[PER];
+    ld_row<PER>(w2 + i0, w2v);
+    const float inv2 = rms_inv(block_sum(s2, red), H, eps);
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    if (i < H) {
-      hm[i] = hv[k];
-      const float y = w2 ? hv[k] * inv2 * w2[i] : hv[k];
+    for (int k = 0; k < PER; ++k) {
+      const float y = hv[k] * inv2 * w2v[k];
       const _Float16 yh = (_Float16)y;
-      x[(int64_t)m * H + i] = __builtin_bit_cast(uint16_t, yh);
-      if (xlo) xlo[(int64_t)m * H + i] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)yh));
+      xv[k] = __builtin_bit_cast(uint16_t, yh);
+      xl[k] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)yh));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const _Float16 yh = (_Float16)hv[k];
+      xv[k] = __builtin_bit_cast(uint16_t, yh);
+      xl[k] = __builtin_bit_cast(uint16_t, (_Float16)(hv[k] - (float)yh));
     }
   }
+  st_halves<PER>(x + row, xv);
+  if (xlo) st_halves<PER>(xlo + row, xl);
 }
 
 // y[m][n] = f16(gelu(sum of ks partial slices) * mul[m mul_ld + n]) for the
@@ -365,7 +433,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
 template <int PER>
 void launch_resnorm_per(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
                         const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st) {
-  hipLaunchKernelGGL((k_resnorm_rows<PER>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps);
+  const int nam = !a ? 0 : na == 1 ? 1 : na <= 2 ? 2 : na <= 4 ? 4 : 8;
+  switch (nam) {
+    case 0: hipLaunchKernelGGL((k_resnorm_rows<PER, 0>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps); break;
+    case 1: hipLaunchKernelGGL((k_resnorm_rows<PER, 1>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps); break;
+    case 2: hipLaunchKernelGGL((k_resnorm_rows<PER, 2>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps); break;
+    case 4: hipLaunchKernelGGL((k_resnorm_rows<PER, 4>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps); break;
+    default: hipLaunchKernelGGL((k_resnorm_rows<PER, 8>), dim3(M), dim3(256), 0, st, h, a, na, slice, w1, scale, w2, x, xlo, H, eps); break;
+  }
 }
 
 }  // namespace
@@ -395,18 +470,18 @@ int launch_gelu_mul_rows(const float* part, int ks, int64_t slice, int M, int64_
 
 int launch_resnorm_rows(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
                         const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st) {
-  if (H < 1 || H > 256 * kMaxPer) return e4b_fail(E4B_EINVAL, "resnorm rows: hidden %d outside 1..%d", H, 256 * kMaxPer);
-  if (a && (na < 1 || !w1)) return e4b_fail(E4B_EINVAL, "resnorm rows: %d residual slices", na);
-  if (H <= 256)
-    launch_resnorm_per<1>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
-  else if (H <= 512)
-    launch_resnorm_per<2>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
-  else if (H <= 1024)
-    launch_resnorm_per<4>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
-  else if (H <= 2048)
-    launch_resnorm_per<8>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
-  else
-    launch_resnorm_per<kMaxPer>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st);
+  const int per = H / 256;
+  if (H % 256 || (per != 1 && per != 2 && per != 4 && per != 8 && per != kMaxPer))
+    return e4b_fail(E4B_EINVAL, "resnorm rows: hidden %d is not 256, 512, 1024, 2048 or 4096", H);
+  if (M < 1) return e4b_fail(E4B_EINVAL, "resnorm rows: M = %d", M);
+  if (a && (na < 1 || na > kMaxPartials || !w1)) return e4b_fail(E4B_EINVAL, "resnorm rows: %d residual slices", na);
+  switch (per) {
+    case 1: launch_resnorm_per<1>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st); break;
+    case 2: launch_resnorm_per<2>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st); break;
+    case 4: launch_resnorm_per<4>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st); break;
+    case 8: launch_resnorm_per<8>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st); break;
+    default: launch_resnorm_per<kMaxPer>(M, h, a, na, slice, w1, scale, w2, x, xlo, H, eps, st); break;
+  }
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }
