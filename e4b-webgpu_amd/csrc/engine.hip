@@ -83,6 +83,8 @@ struct e4b_ctx {
         *pf_y = nullptr;       // [cap][H], [2][cap][L PD], [cap][L PD], [cap][QKV], [cap][QH HD], [kPfKs][cap][H]
   uint16_t *pf_xhl = nullptr, *pf_xn = nullptr, *pf_attn = nullptr, *pf_gg = nullptr,
            *pf_gp = nullptr;   // [2][cap][H], [cap][H], [cap][QH HD], [cap][FF], [cap][PD]
+  float* pf_apart = nullptr;   // split-key attention partials (attn_prefill_part_bytes)
+  size_t pf_apart_bytes = 0;
 };
 
 namespace {
@@ -395,6 +397,8 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
         (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * HD)) ||
         (rc = dalloc_t(c, &c->pf_gg, M * FF)) || (rc = dalloc_t(c, &c->pf_gp, M * (size_t)(PD ? PD : 1))))
       return rc;
+    c->pf_apart_bytes = attn_prefill_part_bytes(cap, KVH);
+    if ((rc = dalloc(c, (void**)&c->pf_apart, c->pf_apart_bytes))) return rc;
   }
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
@@ -641,6 +645,8 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
     pa.slots = ly.slots;
     pa.window = ly.global ? 0 : k.window;
     pa.p0 = p0;
+    pa.part = c->pf_apart;
+    pa.part_bytes = c->pf_apart_bytes;
     if ((rc = launch_attn_prefill(pa, st))) return rc;
     if ((rc = gemm(q40_view(ly.o, H, (int64_t)QH * HD), c->pf_attn, QH * HD, GEMM_F32, c->pf_y, nullptr, 0, nullptr,
                    0, ks_o)))

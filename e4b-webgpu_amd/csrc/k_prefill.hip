@@ -15,6 +15,8 @@
 //                     the cache (kernels/attnf32.wgsl:21-105 /
 //                     kernels/attnos.wgsl:22-98 per query) on the matrix
 //                     cores
+#include <algorithm>
+
 #include "../../include/e4b.h"
 #include "attn_prep.h"
 #include "kernels.h"
@@ -266,10 +268,14 @@ __global__ __launch_bounds__(64) void k_headprep_rows(const float* __restrict__ 
 
 // ---- causal attention of a prefill chunk on the matrix cores ----------------
 //
-// Workgroup (KV group g, tile of 16 queries); wave w = q head 4g + w, so the
-// four heads of a group share each K/V tile staged in LDS.  Key tiles of 32
-// positions walk the union of the tile's windows; per query the live keys
-// are (qp - W, qp] (sliding) or [0, qp] (global), scale 1.0.
+// Workgroup (KV group g, tile of 16 queries, key split s); wave w = q head
+// 4g + w, so the four heads of a group share each K/V tile staged in LDS.
+// Key tiles of 32 positions walk the union of the tile's windows; per query
+// the live keys are (qp - W, qp] (sliding) or [0, qp] (global), scale 1.0.
+// With ns > 1 splits the union is cut into runs of kspl keys (a multiple of
+// the tile), one workgroup each, which write unnormalised partials (O, max,
+// sum) that k_attn_prefill_combine merges by log-sum-exp: the causal tiles
+// late in the chunk no longer serialise on one CU.
 //
 // v_mfma_f32_16x16x32_f16 (lane l: A[l % 16][8 (l / 16) + t], B[8 (l / 16) +
 // t][l % 16], D[4 (l / 16) + r][l % 16]):
@@ -288,6 +294,8 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kKT = 32;            // keys per tile
 constexpr int kKsStride = 256 + 8; // halfs per K row in LDS
 constexpr int kVtStride = kKT + 8; // halfs per transposed V row in LDS
+constexpr int kPfAttnMaxSplits = 8;  // key splits per query tile
+constexpr int kPfAttnMinSplit = 128; // keys per split at least (a multiple of kKT)
 
 DEV void split8(const float (&v)[8], h8v& hi, h8v& lo) {
 #pragma unroll
@@ -313,6 +321,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
   const int klo = W > 0 ? max(0, P0 - W + 1) : 0;
   const uint16_t* kc = A.kc + (int64_t)g * A.slots * 256;
   const uint16_t* vc = A.vc + (int64_t)g * A.slots * 256;
+  const int NS = gridDim.z, sp = blockIdx.z;
+  const int kstart = NS > 1 ? klo + sp * A.kspl : klo;
+  if (kstart > P1) return;  // this tile needs fewer splits (uniform per workgroup)
+  const int kend = NS > 1 ? min(P1, kstart + A.kspl - 1) : P1;
 
   // Q^T as the B operand: step s covers dims 32 s + 8 qq .. + 8
   h8v qh_[8], ql_[8];
@@ -331,7 +343,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
   for (int dt = 0; dt < 16; ++dt) o[dt] = f4v{0.f, 0.f, 0.f, 0.f};
   float mrun = -3.0e38f, lrun = 0.f;
 
-  for (int kb = klo; kb <= P1; kb += kKT) {
+  for (int kb = kstart; kb <= kend; kb += kKT) {
     // stage keys kb .. kb + 31 (rows past P1 repeat row P1; they are masked)
     lds_sync();
     {
@@ -420,6 +432,19 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
     }
   }
   if (qi >= M) return;
+  if (NS > 1) {
+    // partials of unit (g, tile, split), head w, query j: O [256] and (max, sum)
+    const int64_t u = ((int64_t)(g * gridDim.y + blockIdx.y) * NS + sp) * 4 + wave;
+    float* po = A.part + (u * 16 + j) * 256 + 4 * qq;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt)
+      *reinterpret_cast<float4*>(po + 16 * dt) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+    if (qq == 0) {
+      float* ml = A.part + (int64_t)gridDim.x * gridDim.y * NS * 4 * 16 * 256;
+      *reinterpret_cast<float2*>(ml + (u * 16 + j) * 2) = make_float2(mrun, lrun);
+    }
+    return;
+  }
   const float inv = 1.f / lrun;
   uint16_t* dst = A.out + ((int64_t)qi * A.qh + head) * 256 + 4 * qq;
 #pragma unroll
@@ -428,6 +453,51 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
     const uint32_t hi2 = (uint32_t)f2h(o[dt][2] * inv) | ((uint32_t)f2h(o[dt][3] * inv) << 16);
     *reinterpret_cast<uint2*>(dst + 16 * dt) = make_uint2(lo2, hi2);
   }
+}
+
+// log-sum-exp merge of the key splits of one (head, query): block (h, m),
+// thread t = dims 4t .. 4t + 3.  A split in which the query has no live key
+// left max -3e38 and sum 0 and drops out (its weight underflows to 0); the
+// split that holds the query's own position is always live.
+__global__ __launch_bounds__(64) void k_attn_prefill_combine(PrefillAttnArgs A) {
+  const int h = blockIdx.x, qi = blockIdx.y, t = threadIdx.x;
+  const int g = h >> 2, w = h & 3, qt = qi >> 4, j = qi & 15;
+  const int nqt = (A.M + 15) >> 4;
+  const int P0 = (int)A.p0 + 16 * qt, P1 = (int)A.p0 + min(16 * qt + 16, A.M) - 1;
+  const int klo = A.window > 0 ? max(0, P0 - A.window + 1) : 0;
+  const int nspl = (P1 - klo + A.kspl) / A.kspl;  // splits of this tile (<= ns)
+  const int64_t u0 = (int64_t)(g * nqt + qt) * A.ns;
+  const float* ml = A.part + (int64_t)A.kvh * nqt * A.ns * 4 * 16 * 256;
+  float m[kPfAttnMaxSplits], l[kPfAttnMaxSplits];
+  float4 ov[kPfAttnMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kPfAttnMaxSplits; ++s) {
+    const int64_t u = ((u0 + min(s, nspl - 1)) * 4 + w) * 16 + j;
+    const float2 v = *reinterpret_cast<const float2*>(ml + u * 2);
+    m[s] = v.x;
+    l[s] = v.y;
+    ov[s] = *reinterpret_cast<const float4*>(A.part + u * 256 + 4 * t);
+  }
+  float M = m[0];
+#pragma unroll
+  for (int s = 1; s < kPfAttnMaxSplits; ++s)
+    if (s < nspl) M = fmaxf(M, m[s]);
+  float den = 0.f, a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+  for (int s = 0; s < kPfAttnMaxSplits; ++s) {
+    if (s < nspl) {
+      const float f = __expf(m[s] - M);
+      den = fmaf(l[s], f, den);
+      a0 = fmaf(ov[s].x, f, a0);
+      a1 = fmaf(ov[s].y, f, a1);
+      a2 = fmaf(ov[s].z, f, a2);
+      a3 = fmaf(ov[s].w, f, a3);
+    }
+  }
+  const float inv = 1.f / den;
+  uint16_t* dst = A.out + ((int64_t)qi * A.qh + h) * 256 + 4 * t;
+  *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)f2h(a0 * inv) | ((uint32_t)f2h(a1 * inv) << 16),
+                                             (uint32_t)f2h(a2 * inv) | ((uint32_t)f2h(a3 * inv) << 16));
 }
 
 template <int PER>
@@ -498,7 +568,11 @@ int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* q
   return E4B_OK;
 }
 
-int launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t st) {
+size_t attn_prefill_part_bytes(int M, int kvh) {
+  return (size_t)kvh * (size_t)((M + 15) / 16) * kPfAttnMaxSplits * 4 * 16 * (256 + 2) * sizeof(float);
+}
+
+int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
   if (a.qh != 4 * a.kvh) return e4b_fail(E4B_EINVAL, "prefill attention: %d q heads for %d kv heads", a.qh, a.kvh);
   if (a.M < 1) return e4b_fail(E4B_EINVAL, "prefill attention: M = %d", a.M);
   if (a.window > 0) {
@@ -511,7 +585,28 @@ int launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t st) {
   } else if ((int64_t)a.p0 + a.M > a.slots) {
     return e4b_fail(E4B_ERANGE, "prefill attention: positions beyond %d slots", a.slots);
   }
-  hipLaunchKernelGGL(k_attn_prefill, dim3(a.kvh, (a.M + 15) / 16), dim3(256), 0, st, a);
+  // the widest key range of a query tile sets the split length: at least
+  // kPfAttnMinSplit keys, at most kPfAttnMaxSplits splits
+  const int nqt = (a.M + 15) / 16;
+  int maxspan = 0;
+  for (int t = 0; t < nqt; ++t) {
+    const int P0 = (int)a.p0 + 16 * t, P1 = (int)a.p0 + std::min(16 * t + 16, a.M) - 1;
+    const int klo = a.window > 0 ? std::max(0, P0 - a.window + 1) : 0;
+    maxspan = std::max(maxspan, P1 - klo + 1);
+  }
+  int kspl = (maxspan + kPfAttnMaxSplits - 1) / kPfAttnMaxSplits;
+  kspl = std::max(kPfAttnMinSplit, (kspl + kKT - 1) / kKT * kKT);
+  int ns = (maxspan + kspl - 1) / kspl;
+  if (!a.part) ns = 1;
+  if (ns > 1) {
+    const size_t need = (size_t)a.kvh * nqt * ns * 4 * 16 * (256 + 2) * sizeof(float);
+    if (a.part_bytes < need)
+      return e4b_fail(E4B_EINVAL, "prefill attention: %zu partial bytes, %zu needed", a.part_bytes, need);
+  }
+  a.kspl = kspl;
+  a.ns = ns;
+  hipLaunchKernelGGL(k_attn_prefill, dim3(a.kvh, nqt, ns), dim3(256), 0, st, a);
+  if (ns > 1) hipLaunchKernelGGL(k_attn_prefill_combine, dim3(a.qh, a.M), dim3(64), 0, st, a);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -273,6 +273,11 @@ extern "C" int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc
   a.slots = slots;
   a.window = window;
   a.p0 = p0;
+  Workspace ws;
+  int rc = e4b_workspace(attn_prefill_part_bytes(m, kv_heads), &ws);
+  if (rc) return rc;
+  a.part = (float*)ws.buf;
+  a.part_bytes = ws.cap;
   return launch_attn_prefill(a, (hipStream_t)stream);
 }
 
