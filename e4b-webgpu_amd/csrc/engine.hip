@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <string>
+#include <algorithm>
 #include <vector>
 
 #include "../../include/e4b.h"
@@ -44,6 +45,7 @@ struct Layer {
   uint16_t *kc = nullptr, *vc = nullptr;
   int slots = 0;
   uint32_t have = 0;
+  float* score = nullptr;  // full layers with E4B_FLAG_KV_SCORE: [QH][slots] attention mass
 };
 
 }  // namespace
@@ -71,6 +73,12 @@ struct e4b_ctx {
   uint16_t *h_hl = nullptr, *xn = nullptr, *attn = nullptr, *xf = nullptr, *gg = nullptr, *xg = nullptr,
            *gp = nullptr, *xo_hl = nullptr;
   uint2* amax_part = nullptr;
+  // full-layer entry count (host mirror of params[4]) and the scoring /
+  // compaction buffers (E4B_FLAG_KV_SCORE)
+  uint32_t kv_count = 0;
+  float* raw = nullptr;                     // [QH][max_seq] raw scores of the current layer
+  uint32_t* keep = nullptr;                 // [max_seq] compaction keep list
+  uint16_t *kv_sk = nullptr, *kv_sv = nullptr;  // [KVH][max_seq][HD] gather scratch
   int nch = 0, chunk = 64, ring_cap = 0, max_prompt = 0, amax_parts = 0;
   int64_t qkv_rows = 0;
   hipGraph_t graph = nullptr;
@@ -400,6 +408,14 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
     c->pf_apart_bytes = attn_prefill_part_bytes(cap, KVH);
     if ((rc = dalloc(c, (void**)&c->pf_apart, c->pf_apart_bytes))) return rc;
   }
+  if (k.flags & E4B_FLAG_KV_SCORE) {
+    const size_t S = (size_t)k.max_seq;
+    for (Layer& ly : c->L)
+      if (ly.global && (rc = dalloc_t(c, &ly.score, (size_t)QH * S))) return rc;
+    if ((rc = dalloc_t(c, &c->raw, (size_t)QH * S)) || (rc = dalloc_t(c, &c->keep, S)) ||
+        (rc = dalloc_t(c, &c->kv_sk, (size_t)KVH * S * HD)) || (rc = dalloc_t(c, &c->kv_sv, (size_t)KVH * S * HD)))
+      return rc;
+  }
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
   if (k.flags & E4B_FLAG_NO_GRAPH) return E4B_OK;
@@ -514,7 +530,11 @@ int record_step(e4b_ctx* c) {
     a.chunk = c->chunk;
     a.combine = !fuse_combine;
     a.eps = k.eps;
+    a.kv_idx = 4;  // full layers: params[4] = the token's slot
+    a.raw = ly.score ? c->raw : nullptr;
     if ((rc = launch_attn(a, st))) return rc;
+    if (ly.score && (rc = launch_attn_score(c->part_ml, c->raw, c->params, 4, QH, ly.slots, c->chunk, ly.score, st)))
+      return rc;
     // 3. o projection
     GemvOut oo = {c->o, nullptr, nullptr, 0};
     const Q40Mat Wo = q40_view(ly.o, H, (int64_t)QH * HD);
@@ -523,6 +543,7 @@ int record_step(e4b_ctx* c) {
       pa.part_o = c->part_o;
       pa.part_ml = c->part_ml;
       pa.params = c->params;
+      pa.kv_idx = 4;
       pa.window = a.window;
       pa.chunk_shift = c->chunk == 64 ? 6 : 5;
       pa.gch = gch_layer;
@@ -705,8 +726,10 @@ int prefill_batched(e4b_ctx* c, const uint32_t* ids, uint32_t n) {
   if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)(c->pf_xhl + last), (const uint32_t*)(c->pf_xhl + MH + last),
                                    k.softcap, c->logits, nullptr, c->amax_part, c->st)))
     return rc;
-  const uint32_t p[4] = {n - 1, 0u, 0u, 0u};
-  if ((rc = put_params(c, p, 0, 4))) return rc;
+  // the feedback advances params[0] and params[4] to n: decode continues at
+  // position n, full-layer slot n
+  const uint32_t p[5] = {n - 1, 0u, 0u, 0u, n - 1};
+  if ((rc = put_params(c, p, 0, 5))) return rc;
   if ((rc = launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, c->st)))
     return rc;
   float* hdst = c->h_final ? c->h_final : c->h;
@@ -746,15 +769,27 @@ int put_params(e4b_ctx* c, const uint32_t* v, int first, int count) {
   return E4B_OK;
 }
 
+int zero_scores(e4b_ctx* c) {
+  for (const Layer& ly : c->L)
+    if (ly.score) E4B_HIP(hipMemsetAsync(ly.score, 0, (size_t)c->cfg.q_heads * ly.slots * 4, c->st));
+  return E4B_OK;
+}
+
 }  // namespace
 
 extern "C" int e4b_step(e4b_ctx* c, uint32_t token, uint32_t pos, float* logits, uint32_t* argmax_out) {
   int rc = ready(c, "e4b_step");
   if (rc) return rc;
   if (token >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_step: token %u >= vocab %d", token, c->cfg.vocab);
-  if (pos >= (uint32_t)c->cfg.max_seq) return e4b_fail(E4B_ERANGE, "e4b_step: pos %u >= max_seq %d", pos, c->cfg.max_seq);
-  const uint32_t p[4] = {pos, token, 0u, 0u};
-  if ((rc = put_params(c, p, 0, 4)) || (rc = launch_token(c))) return rc;
+  // positions only rotate q/k and index the sliding rings (modulo); the full
+  // layers' limit is their entry count
+  if (pos >= 0x7fffffffu) return e4b_fail(E4B_ERANGE, "e4b_step: pos %u >= 2^31 - 1", pos);
+  const uint32_t kv = pos == 0 ? 0u : c->kv_count;  // src/engine-a4b.js:695-699
+  if (kv >= (uint32_t)c->cfg.max_seq)
+    return e4b_fail(E4B_ERANGE, "e4b_step: %u full-layer entries fill max_seq %d (compact first)", kv, c->cfg.max_seq);
+  const uint32_t p[5] = {pos, token, 0u, 0u, kv};
+  if ((rc = put_params(c, p, 0, 5)) || (rc = launch_token(c))) return rc;
+  c->kv_count = kv + 1;
   uint32_t am[2] = {0, 0};
   E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
   if (logits) E4B_HIP(hipMemcpyAsync(logits, c->logits, (size_t)c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->st));
@@ -773,13 +808,17 @@ extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t
     if (ids[i] >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_prefill: ids[%u] = %u >= vocab", i, ids[i]);
   if (c->cfg.flags & E4B_FLAG_STEP_PREFILL) {
     E4B_HIP(hipMemcpyAsync(c->prompt, ids, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
-    const uint32_t p[4] = {0u, 0u, 0u, n};
-    if ((rc = put_params(c, p, 0, 4))) return rc;
+    const uint32_t p[5] = {0u, 0u, 0u, n, 0u};
+    if ((rc = put_params(c, p, 0, 5))) return rc;
     for (uint32_t i = 0; i < n; ++i)
       if ((rc = launch_token(c))) return rc;
   } else if ((rc = prefill_batched(c, ids, n))) {
     return rc;
   }
+  // the full layers hold the n prompt entries; the prefill leaves no mass
+  // (src/engine-a4b.js:555-563: scores zeroed, batched attention unscored)
+  c->kv_count = n;
+  if ((rc = zero_scores(c))) return rc;
   uint32_t am[2] = {0, 0};
   E4B_HIP(hipMemcpyAsync(am, c->amax, 8, hipMemcpyDeviceToHost, c->st));
   if ((rc = check_status(c))) return rc;
@@ -788,15 +827,20 @@ extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t
 }
 
 static int decode_launch(e4b_ctx* c, uint32_t start_pos, uint32_t count) {
-  if ((uint64_t)start_pos + count > (uint64_t)c->cfg.max_seq)
-    return e4b_fail(E4B_ERANGE, "decode: positions [%u, %u) exceed max_seq %d", start_pos, start_pos + count,
-                    c->cfg.max_seq);
+  if ((uint64_t)start_pos + count >= 0x7fffffffu)
+    return e4b_fail(E4B_ERANGE, "decode: positions [%u, %u) reach 2^31 - 1", start_pos, start_pos + count);
   if (count > (uint32_t)c->ring_cap) return e4b_fail(E4B_ERANGE, "decode: %u tokens exceed the token ring", count);
-  const uint32_t p0 = start_pos, z[2] = {0u, 0u};
+  if ((uint64_t)c->kv_count + count > (uint64_t)c->cfg.max_seq)
+    return e4b_fail(E4B_ERANGE, "decode: %u full-layer entries + %u exceed max_seq %d (compact first)", c->kv_count,
+                    count, c->cfg.max_seq);
+  // the entry count continues from the last step (decodeChunk,
+  // src/engine-a4b.js:786-795); the feedback advances it with the position
+  const uint32_t p0 = start_pos, z[3] = {0u, 0u, c->kv_count};
   int rc;
-  if ((rc = put_params(c, &p0, 0, 1)) || (rc = put_params(c, z, 2, 2))) return rc;
+  if ((rc = put_params(c, &p0, 0, 1)) || (rc = put_params(c, z, 2, 3))) return rc;
   for (uint32_t i = 0; i < count; ++i)
     if ((rc = launch_token(c))) return rc;
+  c->kv_count += count;
   return E4B_OK;
 }
 
@@ -887,8 +931,80 @@ extern "C" int e4b_reset(e4b_ctx* c) {
   E4B_HIP(hipMemsetAsync(c->params, 0, 16 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->status, 0, 4 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->amax, 0, 4 * 4, c->st));
+  if ((rc = zero_scores(c))) return rc;
+  c->kv_count = 0;
   E4B_HIP(hipStreamSynchronize(c->st));
   return E4B_OK;
+}
+
+extern "C" int e4b_kv_count(e4b_ctx* c) {
+  int rc = ready(c, "e4b_kv_count");
+  if (rc) return rc;
+  return (int)c->kv_count;
+}
+
+extern "C" int e4b_read_scores(e4b_ctx* c, int layer, float* out) {
+  int rc = ready(c, "e4b_read_scores");
+  if (rc) return rc;
+  if (layer < 0 || layer >= c->cfg.layers) return e4b_fail(E4B_EINVAL, "e4b_read_scores: layer %d", layer);
+  const Layer& ly = c->L[layer];
+  if (!ly.score)
+    return e4b_fail(E4B_ESTATE, "e4b_read_scores: layer %d keeps no scores (a full layer with E4B_FLAG_KV_SCORE)",
+                    layer);
+  if (!out) return e4b_fail(E4B_EINVAL, "e4b_read_scores: null output");
+  E4B_HIP(hipMemcpyAsync(out, ly.score, (size_t)c->cfg.q_heads * ly.slots * 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_kv_compact(e4b_ctx* c, int budget, int protect) {
+  int rc = ready(c, "e4b_kv_compact");
+  if (rc) return rc;
+  if (!(c->cfg.flags & E4B_FLAG_KV_SCORE))
+    return e4b_fail(E4B_ESTATE, "e4b_kv_compact: the context was created without E4B_FLAG_KV_SCORE");
+  if (budget < 0 || protect < 0) return e4b_fail(E4B_EINVAL, "e4b_kv_compact: budget %d, protect %d", budget, protect);
+  const int QH = c->cfg.q_heads, KVH = c->cfg.kv_heads, HD = c->cfg.head_dim;
+  const int64_t n = c->kv_count;
+  const int64_t prot = std::min<int64_t>(protect, n), nc = n - prot;
+  const int64_t want = std::max<int64_t>(0, std::min<int64_t>(budget - prot, nc));
+  std::vector<float> sc;
+  std::vector<double> mass((size_t)std::max<int64_t>(n, 1));
+  std::vector<uint32_t> cand((size_t)std::max<int64_t>(nc, 1)), keep;
+  E4B_HIP(hipStreamSynchronize(c->st));
+  for (Layer& ly : c->L) {
+    if (!ly.global) continue;
+    sc.resize((size_t)QH * ly.slots);
+    E4B_HIP(hipMemcpy(sc.data(), ly.score, sc.size() * 4, hipMemcpyDeviceToHost));
+    // mass per slot, summed over heads in head order (f64)
+    std::fill(mass.begin(), mass.end(), 0.0);
+    for (int h = 0; h < QH; ++h)
+      for (int64_t t = 0; t < n; ++t) mass[(size_t)t] += (double)sc[(size_t)h * ly.slots + (size_t)t];
+    // candidates by decreasing mass, equal masses in slot order (the stable
+    // sort of an ascending list), then the protected newest entries
+    for (int64_t t = 0; t < nc; ++t) cand[(size_t)t] = (uint32_t)t;
+    std::stable_sort(cand.begin(), cand.begin() + nc,
+                     [&](uint32_t a, uint32_t b) { return mass[a] > mass[b]; });
+    keep.assign(cand.begin(), cand.begin() + want);
+    for (int64_t t = nc; t < n; ++t) keep.push_back((uint32_t)t);
+    std::sort(keep.begin(), keep.end());
+    const int cnt = (int)keep.size();
+    if (cnt > 0) {
+      E4B_HIP(hipMemcpyAsync(c->keep, keep.data(), keep.size() * 4, hipMemcpyHostToDevice, c->st));
+      if ((rc = launch_kv_gather(c->keep, cnt, ly.kc, ly.vc, KVH, ly.slots, c->kv_sk, c->kv_sv, ly.slots, c->st)))
+        return rc;
+      // rows [0, cnt) of every head back into the cache
+      for (int g = 0; g < KVH; ++g) {
+        const size_t off = (size_t)g * ly.slots * HD, bytes = (size_t)cnt * HD * 2;
+        E4B_HIP(hipMemcpyAsync(ly.kc + off, c->kv_sk + off, bytes, hipMemcpyDeviceToDevice, c->st));
+        E4B_HIP(hipMemcpyAsync(ly.vc + off, c->kv_sv + off, bytes, hipMemcpyDeviceToDevice, c->st));
+      }
+    }
+    E4B_HIP(hipMemsetAsync(ly.score, 0, sc.size() * 4, c->st));
+    // keep is the host vector the copies read: finish before its next use
+    E4B_HIP(hipStreamSynchronize(c->st));
+    c->kv_count = (uint32_t)cnt;
+  }
+  return (int)c->kv_count;
 }
 
 extern "C" void e4b_destroy(e4b_ctx* c) {

@@ -45,8 +45,10 @@ struct AttnArgs {
   uint16_t* vc;
   const uint32_t* params;
   uint32_t pos;
+  int kv_idx;          // full layers: params[kv_idx] = the slot of this token (entries before it)
   float* part_o;
   float* part_ml;
+  float* raw;          // full layers, may be null: raw scores [qh][slots] of the live slots
   uint16_t* out;
   int qh, kvh, angles, slots, window;
   float eps;
@@ -81,7 +83,7 @@ DEV float xmax32(float v) {
 // half of V, which spreads a chunk's memory traffic over two CUs.  V is read
 // as 16 B per lane, 8 dims each, 64/LV positions per load (LV = lanes per
 // position).
-template <int CS, int NS>
+template <int CS, int NS, bool RAW = false>
 __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   constexpr int NW = 8;
   constexpr int KP = CS / 32;      // score passes per wave (4 positions each)
@@ -100,9 +102,13 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   const int g = blockIdx.x, c = blockIdx.y, zs = NS == 1 ? 0 : (int)blockIdx.z;
   // 32-bit position arithmetic throughout (positions < 2^31): a 64-bit
   // modulo is a long software sequence on this ISA
+  // `pos` rotates q and k; `cur` is the token's index in the cache's own
+  // numbering: the position for sliding rings, the entry count for full
+  // layers (equal to the position until a compaction moves entries)
   const int pos = (int)(A.params ? A.params[0] : A.pos);
-  const int lo = (A.window > 0 && pos + 1 > A.window) ? pos + 1 - A.window : 0;
-  const int n = pos + 1 - lo;
+  const int cur = A.window > 0 ? pos : (int)(A.params ? A.params[A.kv_idx] : A.pos);
+  const int lo = (A.window > 0 && cur + 1 > A.window) ? cur + 1 - A.window : 0;
+  const int n = cur + 1 - lo;
   const int nch = (n + CS - 1) / CS;  // live chunks; the rest of the grid idles
   if (c >= nch) return;
   const int c_lo = lo + c * CS;
@@ -150,7 +156,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
 
   // 1. head prep: waves 0-3 prep q heads 4g..4g+3, wave 4 the new k, wave 5
   //    the new v (f16-rounded, as stored); the chunk owning `pos` stores them
-  const bool owner = pos < c_lo + m;  // the last live chunk holds pos, at j = m - 1
+  const bool owner = cur < c_lo + m;  // the last live chunk holds cur, at j = m - 1
   if (wave < 6) {
     float x[4] = {xin.x, xin.y, xin.z, xin.w};
     const float w[4] = {win.x, win.y, win.z, win.w};
@@ -186,7 +192,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
     for (int s = 0; s < KP; ++s) {
       const int j = wave + NW * (4 * s + sub);
       uint4 ka = kr[s][0], kb = kr[s][1];
-      if (c_lo + j == pos) {
+      if (c_lo + j == cur) {
         ka = *reinterpret_cast<const uint4*>(knew + 8 * dl);
         kb = *reinterpret_cast<const uint4*>(knew + 128 + 8 * dl);
       }
@@ -201,6 +207,10 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
         t[h] = a;
       }
       sc[s] = j < m ? reduce_rows<16, GQA>(t) : -3.0e38f;
+      // raw scores for the mass of a scored full layer (lane dl % 4 == 0 of
+      // each head; one V slice writes them)
+      if (RAW && zs == 0 && j < m && (dl & 3) == 0)
+        A.raw[(int64_t)(g * GQA + (dl >> 2)) * A.slots + slot_at(j)] = sc[s];
     }
   }
 
@@ -234,7 +244,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       const int j = wave + NW * i;
       // a position past m reads a clamped, possibly stale row: zero it, so
       // its zero weight cannot meet a non-finite value
-      const uint4 vv = (c_lo + j == pos) ? vn : (j < m ? vr[q] : make_uint4(0u, 0u, 0u, 0u));
+      const uint4 vv = (c_lo + j == cur) ? vn : (j < m ? vr[q] : make_uint4(0u, 0u, 0u, 0u));
       float vf[8];
       const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
@@ -326,12 +336,12 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
 template <int CS>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
                                                       const float* __restrict__ part_ml, const uint32_t* params,
-                                                      uint32_t pos_imm, int window, int gch,
+                                                      uint32_t pos_imm, int kv_idx, int window, int gch,
                                                       uint16_t* __restrict__ out) {
   __shared__ float wt[kAttnMaxChunks];
   __shared__ float red[4];
   const int h = blockIdx.x, d = threadIdx.x;
-  const int pos = (int)(params ? params[0] : pos_imm);
+  const int pos = (int)(params ? params[window > 0 ? 0 : kv_idx] : pos_imm);
   const int lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
   const int nch = (pos + 1 - lo + CS - 1) / CS;
   const float* ml = part_ml + (int64_t)h * gch * 2;
@@ -354,7 +364,71 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
   out[h * HD + d] = f2h(acc / den);
 }
 
+// attention mass of a scored full layer (kernels/attnos.wgsl:78-92, SCORE =
+// 1): score[h][t] += e^(s_t - M) / den for the live slots t <= cur, where M
+// and den = sum_c l_c e^(m_c - M) merge the split-K statistics of head h --
+// the normalisation the combine applies.  Block (h, b) covers slots [256 b,
+// 256 b + 256); the grid is sized for the capacity and blocks past the live
+// slots exit.
+template <int CS>
+__global__ __launch_bounds__(256) void k_attn_score(const float* __restrict__ part_ml, const float* __restrict__ raw,
+                                                    const uint32_t* params, int kv_idx, int gch, int slots,
+                                                    float* __restrict__ score) {
+  __shared__ float red[4];
+  const int h = blockIdx.x, t = blockIdx.y * 256 + threadIdx.x;
+  const int cur = (int)params[kv_idx];
+  if ((int)blockIdx.y * 256 > cur) return;
+  const int nch = (cur + 1 + CS - 1) / CS;
+  const float* ml = part_ml + (int64_t)h * gch * 2;
+  float M = -3.0e38f;
+  for (int c = threadIdx.x; c < nch; c += 256) M = fmaxf(M, ml[2 * c]);
+  M = block_max(M, red);
+  float den = 0.f;
+  for (int c = threadIdx.x; c < nch; c += 256) den = fmaf(ml[2 * c + 1], __expf(ml[2 * c] - M), den);
+  den = block_sum(den, red);
+  if (t <= cur) {
+    const int64_t o = (int64_t)h * slots + t;
+    score[o] = score[o] + __expf(raw[o] - M) / den;
+  }
+}
+
+// compaction gather (kernels/kvgather.wgsl): dst[g][i] = src[g][keep[i]] for
+// K and V, block (i, g), 256 dims per row as 32 threads x 16 bytes
+__global__ __launch_bounds__(64) void k_kv_gather(const uint32_t* __restrict__ keep, const uint16_t* __restrict__ kc,
+                                                  const uint16_t* __restrict__ vc, int slots, uint16_t* __restrict__ dk,
+                                                  uint16_t* __restrict__ dv, int dslots) {
+  const int i = blockIdx.x, g = blockIdx.y, t = threadIdx.x & 31;
+  const int64_t src = ((int64_t)g * slots + keep[i]) * HD + 8 * t;
+  const int64_t dst = ((int64_t)g * dslots + i) * HD + 8 * t;
+  if (threadIdx.x < 32)
+    *reinterpret_cast<uint4*>(dk + dst) = *reinterpret_cast<const uint4*>(kc + src);
+  else
+    *reinterpret_cast<uint4*>(dv + dst) = *reinterpret_cast<const uint4*>(vc + src);
+}
+
 }  // namespace
+
+int launch_attn_score(const float* part_ml, const float* raw, const uint32_t* params, int kv_idx, int qh, int slots,
+                      int chunk, float* score, hipStream_t st) {
+  if (chunk != 32 && chunk != 64) return e4b_fail(E4B_EINVAL, "attention score: chunk %d", chunk);
+  const int gch = attn_chunks(slots, chunk);
+  const dim3 grid(qh, (slots + 255) / 256);
+  if (chunk == 64)
+    hipLaunchKernelGGL(k_attn_score<64>, grid, dim3(256), 0, st, part_ml, raw, params, kv_idx, gch, slots, score);
+  else
+    hipLaunchKernelGGL(k_attn_score<32>, grid, dim3(256), 0, st, part_ml, raw, params, kv_idx, gch, slots, score);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_kv_gather(const uint32_t* keep, int n, const uint16_t* kc, const uint16_t* vc, int kvh, int slots,
+                     uint16_t* dk, uint16_t* dv, int dslots, hipStream_t st) {
+  if (n <= 0) return E4B_OK;
+  if (n > dslots) return e4b_fail(E4B_EINVAL, "kv gather: %d rows into %d", n, dslots);
+  hipLaunchKernelGGL(k_kv_gather, dim3(n, kvh), dim3(64), 0, st, keep, kc, vc, slots, dk, dv, dslots);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
 
 int attn_chunks(int max_positions, int chunk) { return (max_positions + chunk - 1) / chunk; }
 
@@ -379,8 +453,10 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.vc = a.vc;
   A.params = a.params;
   A.pos = a.pos;
+  A.kv_idx = a.kv_idx;
   A.part_o = a.part_o;
   A.part_ml = a.part_ml;
+  A.raw = a.window > 0 ? nullptr : a.raw;
   A.out = a.out;
   A.qh = a.qh;
   A.kvh = a.kvh;
@@ -389,15 +465,21 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.window = a.window;
   A.eps = a.eps;
   if (a.chunk == 64) {
-    hipLaunchKernelGGL((k_attn_split<64, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
+    if (A.raw)
+      hipLaunchKernelGGL((k_attn_split<64, 2, true>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
+    else
+      hipLaunchKernelGGL((k_attn_split<64, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
     if (a.combine)
       hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
-                         a.window, nch, a.out);
+                         a.kv_idx, a.window, nch, a.out);
   } else {
-    hipLaunchKernelGGL((k_attn_split<32, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
+    if (A.raw)
+      hipLaunchKernelGGL((k_attn_split<32, 2, true>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
+    else
+      hipLaunchKernelGGL((k_attn_split<32, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
     if (a.combine)
       hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
-                         a.window, nch, a.out);
+                         a.kv_idx, a.window, nch, a.out);
   }
   E4B_HIP(hipGetLastError());
   return E4B_OK;

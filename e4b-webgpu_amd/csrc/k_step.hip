@@ -224,6 +224,7 @@ __global__ __launch_bounds__(256) void k_feedback(const uint2* __restrict__ part
     params[1] = si[0];
     params[2] = r + 1;
     params[0] = params[0] + 1;
+    params[4] = params[4] + 1;  // full-layer entries: the next token's slot
   }
 }
 

@@ -88,6 +88,7 @@ struct ProArgs {
   const float* part_o;     // [heads][gch][256]
   const float* part_ml;    // [heads][gch][2]
   const uint32_t* params;  // params[0] = position
+  int kv_idx;              // full layers: params[kv_idx] = the token's slot (0: the position)
   int window;              // 0 = global layer
   int chunk_shift;         // log2 of the positions per chunk
   int gch;                 // chunks allocated per head

@@ -127,7 +127,7 @@ struct AttnRegs {
 template <int U>
 DEV void attn_issue(const ProArgs& p, AttnRegs<U>& r) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  r.pos = p.params[0];
+  r.pos = p.params[p.window > 0 ? 0 : p.kv_idx];
   const int c = min(lane, p.gch - 1);
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {

@@ -14,6 +14,8 @@ struct AttnLaunch {
   uint16_t* vc;            // [kvh][slots][hd] f16 value cache
   const uint32_t* params;  // params[0] = position of the current token (device), or
   uint32_t pos;            //   this position when params is null
+  int kv_idx = 0;          // full layers: params[kv_idx] = the token's slot (0: the position)
+  float* raw = nullptr;    // full layers, may be null: raw scores [qh][slots] for the mass
   float* part_o;           // [qh][attn_chunks(span, chunk)][hd] split-K partial outputs
   float* part_ml;          // [qh][attn_chunks(span, chunk)][2]  (chunk max, chunk sum)
   uint16_t* out;           // [qh][hd] f16 attention output
@@ -26,6 +28,13 @@ struct AttnLaunch {
 };
 
 int launch_attn(const AttnLaunch& a, hipStream_t st);
+// score[h][t] += normalised attention weight of live slot t (after launch_attn
+// with raw set); slots = the layer's capacity (score and raw row stride)
+int launch_attn_score(const float* part_ml, const float* raw, const uint32_t* params, int kv_idx, int qh, int slots,
+                      int chunk, float* score, hipStream_t st);
+// dst[g][i] = src[g][keep[i]] (K and V) for i < n; dst rows per head: dslots
+int launch_kv_gather(const uint32_t* keep, int n, const uint16_t* kc, const uint16_t* vc, int kvh, int slots,
+                     uint16_t* dk, uint16_t* dv, int dslots, hipStream_t st);
 constexpr int kAttnMaxChunks = 512;
 // split-K chunks a layer of `max_positions` live positions needs
 int attn_chunks(int max_positions, int chunk);

@@ -106,6 +106,9 @@ SIGNATURES = [
     ("e4b_reset", _i32, [_vp]),
     ("e4b_destroy", None, [_vp]),
     ("e4b_time_decode", _i32, [_vp, _u32, _u32, _P(_f32)]),
+    ("e4b_kv_count", _i32, [_vp]),
+    ("e4b_read_scores", _i32, [_vp, _i32, _vp]),
+    ("e4b_kv_compact", _i32, [_vp, _i32, _i32]),
     ("e4b_gguf_config", _i32, [C.c_char_p, _vp, _vp, _i32]),
     ("e4b_load_gguf", _i32, [_vp, C.c_char_p]),
     ("e4b_open_gguf", _vp, [C.c_char_p, _vp]),
@@ -125,6 +128,7 @@ class ConfigC(C.Structure):
 
 FLAG_NO_GRAPH = 1
 FLAG_STEP_PREFILL = 2
+FLAG_KV_SCORE = 4
 
 
 class MoeWeightsC(C.Structure):

@@ -84,6 +84,12 @@ def gguf_config(path: str, **overrides) -> E4BConfig:
     return E4BConfig(**args)
 
 
+# long-context constants of the reference (src/engine-a4b.js:18-20)
+KV_BUDGET = 640   # full-layer entries after a compaction
+KV_DECAP = 768    # decode recompaction threshold
+KV_PROTECT = 64   # newest entries always kept
+
+
 class Engine:
     def __init__(self, cfg: E4BConfig, tensors=None):
         self.cfg = cfg
@@ -173,6 +179,60 @@ class Engine:
             return out
         pos, done = len(ids), 1
         while done < max_new:
+            n = min(8, max_new - done)
+            toks = self.decode_chunk(pos, n)
+            pos += n
+            stop = False
+            for t in toks.tolist():
+                out.append(int(t))
+                if t in eos:
+                    stop = True
+                    break
+            done += n
+            if stop:
+                break
+        return out[:max_new]
+
+    # ---- full-layer KV budget (src/engine-a4b.js:587-657) ------------------------
+    def kv_count(self) -> int:
+        """Entries in the full layers' caches (the reference's kvCount)."""
+        return check(lib.e4b_kv_count(self.ctx), "e4b_kv_count")
+
+    def read_scores(self, layer: int) -> np.ndarray:
+        """Accumulated attention mass [q_heads][max_seq] of a full layer
+        (needs FLAG_KV_SCORE)."""
+        out = np.empty((self.cfg.q_heads, self.cfg.max_seq), np.float32)
+        check(lib.e4b_read_scores(self.ctx, int(layer), _p(out)), "e4b_read_scores")
+        return out
+
+    def compact(self, budget: int = KV_BUDGET, protect: int = KV_PROTECT) -> int:
+        """compactAll (src/engine-a4b.js:587-617); returns the new entry count."""
+        return check(lib.e4b_kv_compact(self.ctx, int(budget), int(protect)), "e4b_kv_compact")
+
+    def generate_long(self, ids, max_new: int, eos=(106, 1), budget: int = KV_BUDGET, protect: int = KV_PROTECT,
+                      decap: int = KV_DECAP) -> list:
+        """generateLong (src/engine-a4b.js:620-657): prefill; when the full
+        layers hold more than `decap` entries, one scored probe step on the
+        whole cache, then compaction to `budget`; then GPU-fed chunks of <= 8,
+        compacting again before a chunk would pass `decap`.  Needs
+        FLAG_KV_SCORE."""
+        eos = set(eos)
+        g0 = self.prefill(ids)
+        out = [g0]
+        if g0 in eos:
+            return out
+        pos, done = len(ids), 1
+        if self.kv_count() > decap:
+            t = int(self.decode_chunk(pos, 1)[0])
+            pos += 1
+            out.append(t)
+            done = 2
+            self.compact(budget, protect)
+            if t in eos:
+                return out
+        while done < max_new:
+            if self.kv_count() + 8 > decap:
+                self.compact(budget, protect)
             n = min(8, max_new - done)
             toks = self.decode_chunk(pos, n)
             pos += n

@@ -97,7 +97,7 @@ napi_value make_typed(napi_env env, napi_typedarray_type t, size_t count, size_t
 
 struct Ctx {
   e4b_ctx* c;
-  int32_t vocab, hidden;
+  int32_t vocab, hidden, q_heads, max_seq;
 };
 
 void finalize_ctx(napi_env, void* data, void*) {
@@ -209,7 +209,7 @@ napi_value create(napi_env env, napi_callback_info info) {
   }
   e4b_ctx* c = e4b_create(&cfg);  // copies the config (and the layer pattern)
   if (!c) return throw_lib(env, "create", -1);
-  Ctx* x = new Ctx{c, cfg.vocab, cfg.hidden};
+  Ctx* x = new Ctx{c, cfg.vocab, cfg.hidden, cfg.q_heads, cfg.max_seq};
   napi_value ext;
   if (napi_create_external(env, x, finalize_ctx, nullptr, &ext) != napi_ok) {
     e4b_destroy(c);
@@ -357,6 +357,52 @@ napi_value read_f32(napi_env env, napi_callback_info info, bool hidden) {
 napi_value read_hidden(napi_env env, napi_callback_info info) { return read_f32(env, info, true); }
 napi_value read_logits(napi_env env, napi_callback_info info) { return read_f32(env, info, false); }
 
+// full-layer KV budget (src/engine-a4b.js:587-617): kvCount(ctx) -> entries;
+// readScores(ctx, layer) -> Float32Array [qHeads * maxSeq];
+// kvCompact(ctx, budget, protect) -> entries after compactAll
+napi_value kv_count(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  Ctx* x = ctx_of(env, argv[0]);
+  if (!x) return throw_msg(env, "kvCount: not an engine context");
+  const int n = e4b_kv_count(x->c);
+  if (n < 0) return throw_lib(env, "kvCount", n);
+  napi_value v;
+  CHECK_NAPI(napi_create_int32(env, n, &v));
+  return v;
+}
+
+napi_value read_scores(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  Ctx* x = ctx_of(env, argv[0]);
+  if (!x) return throw_msg(env, "readScores: not an engine context");
+  int64_t layer = 0;
+  if (!get_i64(env, argv[1], &layer)) return throw_msg(env, "readScores(ctx, layer)");
+  void* d = nullptr;
+  napi_value arr = make_typed(env, napi_float32_array, (size_t)x->q_heads * (size_t)x->max_seq, 4, &d);
+  if (!arr) return throw_msg(env, "readScores: cannot allocate");
+  const int rc = e4b_read_scores(x->c, (int)layer, (float*)d);
+  if (rc) return throw_lib(env, "readScores", rc);
+  return arr;
+}
+
+napi_value kv_compact(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  get_args(env, info, 3, argv);
+  Ctx* x = ctx_of(env, argv[0]);
+  if (!x) return throw_msg(env, "kvCompact: not an engine context");
+  int64_t budget = 0, protect = 0;
+  if (!get_i64(env, argv[1], &budget) || !get_i64(env, argv[2], &protect) || budget < 0 || protect < 0 ||
+      budget > INT32_MAX || protect > INT32_MAX)
+    return throw_msg(env, "kvCompact(ctx, budget, protect)");
+  const int n = e4b_kv_compact(x->c, (int)budget, (int)protect);
+  if (n < 0) return throw_lib(env, "kvCompact", n);
+  napi_value v;
+  CHECK_NAPI(napi_create_int32(env, n, &v));
+  return v;
+}
+
 napi_value reset(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   get_args(env, info, 1, argv);
@@ -397,6 +443,9 @@ napi_value init(napi_env env, napi_value exports) {
       {"argmax", nullptr, argmax, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"readHidden", nullptr, read_hidden, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"readLogits", nullptr, read_logits, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"kvCount", nullptr, kv_count, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"readScores", nullptr, read_scores, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"kvCompact", nullptr, kv_compact, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"reset", nullptr, reset, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"destroy", nullptr, destroy, nullptr, nullptr, nullptr, kMethod, nullptr},
   };

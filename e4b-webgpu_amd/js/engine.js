@@ -4,7 +4,9 @@
 // object with the surface of the one loadEngineA4B returns
 // (src/engine-a4b.js:854-856): step(token, pos), argmaxFast(),
 // decodeChunk(startPos, count, ringBase), generateFast(ids, maxNew, eosIds),
-// prefill(ids), readHidden(); plus readLogits(), reset() and close().
+// prefill(ids), readHidden(); the long-context pair compactAll() and
+// generateLong(ids, maxNew, eosIds) (src/engine-a4b.js:587-657, with
+// FLAG_KV_SCORE); plus readLogits(), kvCount(), reset() and close().
 //
 // The GPU work runs in libe4b.so; the async functions resolve when the call
 // has returned (every library call that returns results is synchronous).
@@ -23,7 +25,9 @@ const KV = {
   eps: "attention.layer_norm_rms_epsilon", softcap: "final_logit_softcapping",
 };
 const DEFAULTS = { ring: 1024, maxSeq: 4096, attnChunk: 0, maxPrompt: 0, flags: 0 };
-const FLAG_NO_GRAPH = 1, FLAG_STEP_PREFILL = 2;
+const FLAG_NO_GRAPH = 1, FLAG_STEP_PREFILL = 2, FLAG_KV_SCORE = 4;
+// long-context constants (src/engine-a4b.js:18-20)
+const KV_BUDGET = 640, KV_DECAP = 768, KV_PROTECT = 64;
 
 function configFromKV(kv, overrides = {}) {
   const arch = kv["general.architecture"] || "e4b";
@@ -94,12 +98,53 @@ async function loadEngine(file, overrides = {}) {
     }
     return out.slice(0, maxNew);
   }
+  // budget compaction of the full layers (src/engine-a4b.js:587-617): the
+  // library ranks the accumulated attention mass, keeps the top entries plus
+  // the newest `protect`, gathers them and zeroes the scores
+  async function compactAll(budget = KV_BUDGET, protect = KV_PROTECT) {
+    return addon.kvCompact(ctx, budget, protect);
+  }
+  // src/engine-a4b.js:620-657: prefill; past `decap` entries one scored
+  // probe step on the whole cache, then compaction; budget-maintained decode
+  // in chunks of <= 8, recompacting before a chunk would pass `decap`
+  async function generateLong(inputIds, maxNew, eosIds = new Set([106, 1]),
+                              { budget = KV_BUDGET, protect = KV_PROTECT, decap = KV_DECAP } = {}) {
+    const g0 = await prefill(inputIds);
+    const out = [g0];
+    if (eosIds.has(g0)) return out;
+    let pos = inputIds.length, done = 1;
+    if (addon.kvCount(ctx) > decap) {
+      const t = decodeChunk(pos, 1, 0)[0];
+      pos += 1;
+      out.push(t);
+      done = 2;
+      await compactAll(budget, protect);
+      if (eosIds.has(t)) return out;
+    }
+    while (done < maxNew) {
+      if (addon.kvCount(ctx) + 8 > decap) await compactAll(budget, protect);
+      const n = Math.min(8, maxNew - done);
+      const toks = decodeChunk(pos, n, done - 1);
+      pos += n;
+      let stop = false;
+      for (let k = 0; k < n; k++) {
+        out.push(toks[k]);
+        if (eosIds.has(toks[k])) { stop = true; break; }
+      }
+      done += n;
+      if (stop) break;
+    }
+    return out.slice(0, maxNew);
+  }
+  function kvCount() { return addon.kvCount(ctx); }
   async function readHidden() { return addon.readHidden(ctx); }
   async function readLogits() { return addon.readLogits(ctx); }
   function reset() { addon.reset(ctx); }
   function close() { addon.destroy(ctx); }
 
-  return { C, step, argmaxFast, decodeChunk, generateFast, prefill, readHidden, readLogits, reset, close, tokRing };
+  return { C, step, argmaxFast, decodeChunk, generateFast, prefill, compactAll, generateLong, kvCount, readHidden,
+           readLogits, reset, close, tokRing };
 }
 
-module.exports = { loadEngine, configFromKV, addon, FLAG_NO_GRAPH, FLAG_STEP_PREFILL };
+module.exports = { loadEngine, configFromKV, addon, FLAG_NO_GRAPH, FLAG_STEP_PREFILL, FLAG_KV_SCORE, KV_BUDGET,
+                   KV_DECAP, KV_PROTECT };

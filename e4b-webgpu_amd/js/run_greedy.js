@@ -1,13 +1,15 @@
 // run_greedy.js -- command-line driver of the JS host:
-//   node run_greedy.js <model.gguf> <id,id,...> <maxNew> ['{"ring":16,...}']
+//   node run_greedy.js <model.gguf> <id,id,...> <maxNew> ['{"ring":16,...}'] ['{"budget":16,...}']
 // loads the model through engine.js, runs generateFast (batched prefill then
 // GPU-fed decode), then the step API on the same prompt after a reset, and
-// prints one JSON line: {generate, steps, hidden_l2, logits_max}.
+// prints one JSON line: {generate, steps, hidden_l2, logits_max}; with the
+// fifth argument (generateLong options; the model needs flags FLAG_KV_SCORE)
+// also generate_long and kv_count after a generateLong of maxNew tokens.
 "use strict";
 const { loadEngine } = require("./engine");
 
 async function main() {
-  const [file, idsArg, maxNewArg, ovArg] = process.argv.slice(2);
+  const [file, idsArg, maxNewArg, ovArg, longArg] = process.argv.slice(2);
   if (!file || !idsArg || !maxNewArg) {
     console.error("usage: node run_greedy.js model.gguf id,id,... maxNew [overrides-json]");
     process.exit(2);
@@ -25,8 +27,14 @@ async function main() {
   let l2 = 0, lmax = -Infinity;
   for (const v of hidden) l2 += v * v;
   for (const v of logits) lmax = Math.max(lmax, v);
+  const res = { generate, steps, hidden_l2: Math.sqrt(l2), logits_max: lmax };
+  if (longArg) {
+    eng.reset();
+    res.generate_long = await eng.generateLong(ids, maxNew, new Set(), JSON.parse(longArg));
+    res.kv_count = eng.kvCount();
+  }
   eng.close();
-  console.log(JSON.stringify({ generate, steps, hidden_l2: Math.sqrt(l2), logits_max: lmax }));
+  console.log(JSON.stringify(res));
 }
 
 main().catch((e) => {

@@ -281,6 +281,11 @@ typedef struct e4b_config {
 /* prefill token by token through the decode step (one graph replay per
  * prompt token) instead of the batched prefill */
 #define E4B_FLAG_STEP_PREFILL 2u
+/* full-layer KV budget (src/engine-a4b.js:587-657): every decode step adds
+ * each live full-layer slot's normalised attention weight to a per-head
+ * score (attnos SCORE = 1, kernels/attnos.wgsl:78-92), which e4b_kv_compact
+ * ranks; costs one small kernel per full layer and token */
+#define E4B_FLAG_KV_SCORE 4u
 
 /* tensor names follow the GGUF naming of the E4B family:
  *   token_embd.weight (Q6_K [vocab][hidden], tied lm-head), output_norm.weight,
@@ -319,6 +324,26 @@ int  e4b_reset(e4b_ctx* ctx);                           /* zero KV caches and st
 void e4b_destroy(e4b_ctx* ctx);
 /* timing: run `count` GPU-fed steps and return the elapsed device ms */
 int  e4b_time_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, float* ms_out);
+
+/* Full-layer KV budget.  Full (global) layers count their cache entries
+ * apart from positions (kvCount, src/engine-a4b.js:217; CACHEMODE 2): the
+ * token of a step goes to slot kvCount and attends to slots [0, kvCount];
+ * e4b_step at position 0 and e4b_prefill restart the count, e4b_decode
+ * continues it.  Until a compaction the count equals the position.
+ *   e4b_kv_count: entries of the full layers (>= 0), or a negative error.
+ *   e4b_read_scores: the accumulated mass of full layer `layer`, [q_heads]
+ *     [max_seq] f32 (E4B_FLAG_KV_SCORE; zeroed by e4b_prefill, e4b_reset and
+ *     compaction).
+ *   e4b_kv_compact: compactAll (src/engine-a4b.js:587-617): per full layer,
+ *     mass[t] = sum over heads of score[h][t]; keep the budget - protect
+ *     older entries of largest mass (ties: lower slot first) and the
+ *     min(protect, n) newest, in slot order; gather their K/V rows to slots
+ *     0.. (kernels/kvgather.wgsl); zero the scores.  Returns the new count
+ *     (min(n, budget) when protect <= budget), or a negative error; needs
+ *     E4B_FLAG_KV_SCORE. */
+int  e4b_kv_count(e4b_ctx* ctx);
+int  e4b_read_scores(e4b_ctx* ctx, int layer, float* out);
+int  e4b_kv_compact(e4b_ctx* ctx, int budget, int protect);
 
 /* GGUF loading on the C ABI (openGGUF, src/gguf.js:17-83, and the tensor
  * loop of loadEngineA4B, src/engine-a4b.js:121-214): the file is

@@ -55,6 +55,13 @@ _sigs = {
     "orc_kv_slot": (_i64, [_vp, _i32, _u32]),
     "orc_state_kcache": (_vp, [_vp, _i32]),
     "orc_state_vcache": (_vp, [_vp, _i32]),
+    "orc_state_set_scoring": (None, [_vp, _i32]),
+    "orc_state_kv_count": (_i64, [_vp]),
+    "orc_state_score": (_vp, [_vp, _i32]),
+    "orc_kv_keep": (_i64, [_vp, _i32, _i64, _i64, _i32, _i32, _vp]),
+    "orc_kv_compact": (_i64, [_vp, _vp, _i32, _i32]),
+    "orc_kv_gather_layer": (None, [_vp, _vp, _i32, _vp, _i64]),
+    "orc_state_set_kv_count": (None, [_vp, _i64]),
 }
 for _n, (_r, _a) in _sigs.items():
     _f = getattr(_lib, _n)
@@ -195,6 +202,16 @@ def attn_combine(po, pme, qh, hd, n_chunks, chunks):
     return out
 
 
+def kv_keep(score: np.ndarray, n: int, budget: int, protect: int) -> np.ndarray:
+    """compactAll's keep list (src/engine-a4b.js:590-603) for one full layer
+    from its [q_heads][scap] f32 score buffer over the first n slots."""
+    sc = _f32(score)
+    qh, scap = sc.shape
+    keep = np.empty(max(n, 1), np.uint32)
+    cnt = int(_lib.orc_kv_keep(_p(sc), qh, scap, n, budget, protect, _p(keep)))
+    return keep[:cnt].copy()
+
+
 def kvring_recover(t: int, mw: int, ring: int) -> int:
     return int(_lib.orc_kvring_recover(t, mw, ring))
 
@@ -331,6 +348,33 @@ class OracleModel:
         hd = np.empty(int(self.cfg["hidden"]), np.float32) if want_hidden else None
         tok = int(_lib.orc_step(C.byref(self._m), self._state, token, pos, _p(lg), _p(hd)))
         return tok, lg, hd
+
+    def set_scoring(self, on: bool) -> None:
+        _lib.orc_state_set_scoring(self._state, int(bool(on)))
+
+    def kv_count(self) -> int:
+        return int(_lib.orc_state_kv_count(self._state))
+
+    def score(self, layer: int) -> np.ndarray:
+        """[q_heads][max_seq] accumulated attention mass of a full layer."""
+        qh, ms = int(self.cfg["q_heads"]), int(self.cfg["max_seq"])
+        p = _lib.orc_state_score(self._state, layer)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(qh, ms)).copy()
+
+    def compact(self, budget: int, protect: int) -> int:
+        """compactAll on every full layer; returns the new entry count."""
+        return int(_lib.orc_kv_compact(C.byref(self._m), self._state, budget, protect))
+
+    def compact_with(self, keeps: dict) -> None:
+        """The gather of compactAll with given keep lists {layer: slots}
+        (every full layer), then kv_count = their common length."""
+        cnt = None
+        for layer, keep in keeps.items():
+            k = np.ascontiguousarray(np.asarray(keep, np.uint32))
+            _lib.orc_kv_gather_layer(C.byref(self._m), self._state, int(layer), _p(k), int(k.size))
+            cnt = int(k.size)
+        if cnt is not None:
+            _lib.orc_state_set_kv_count(self._state, cnt)
 
     def kv_slot(self, is_global: bool, pos: int) -> int:
         return int(_lib.orc_kv_slot(C.byref(self._m), int(is_global), pos))

@@ -318,8 +318,10 @@ int64_t orc_kvring_recover(int64_t t, int64_t mw, int64_t ring) {
 /* Softmax attention of one q head over a list of (slot) rows; scale 1.0    */
 /* (NOTES/arch-spec.md:383-392).  Dead rows are skipped: their contribution */
 /* is exactly 0 (the reference multiplies 0*v, kernels/attnf32.wgsl:89-90). */
-static void attn_rows(const float* q, const uint16_t* kc, const uint16_t* vc, int kvh, int h_kv,
-                      int hd, const int64_t* slots, int64_t n, uint16_t* out) {
+/* probs (may be NULL) receives each row's normalised weight e^(s-m)/den,   */
+/* the quantity attnos.wgsl's SCORE pass adds to the slot's mass (:78-92).  */
+static void attn_rows_p(const float* q, const uint16_t* kc, const uint16_t* vc, int kvh, int h_kv,
+                        int hd, const int64_t* slots, int64_t n, uint16_t* out, double* probs) {
   double* s = (double*)malloc(sizeof(double) * (size_t)(n > 0 ? n : 1));
   double m = -3.0e38;
   for (int64_t i = 0; i < n; ++i) {
@@ -339,7 +341,13 @@ static void attn_rows(const float* q, const uint16_t* kc, const uint16_t* vc, in
     for (int d = 0; d < hd; ++d) acc[d] += e * (double)orc_h2f(v[d]);
   }
   for (int d = 0; d < hd; ++d) out[d] = orc_f2h((float)(acc[d] / den));
+  if (probs)
+    for (int64_t i = 0; i < n; ++i) probs[i] = exp(s[i] - m) / den;
   free(s);
+}
+static void attn_rows(const float* q, const uint16_t* kc, const uint16_t* vc, int kvh, int h_kv,
+                      int hd, const int64_t* slots, int64_t n, uint16_t* out) {
+  attn_rows_p(q, kc, vc, kvh, h_kv, hd, slots, n, out, NULL);
 }
 
 /* attnf32 CACHEMODE 1 decode (kernels/attnf32.wgsl:21-105): qp = maxW = pos, */
@@ -572,11 +580,20 @@ void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* to
 /* the lm-head is the tied Q6_K embedding with softcap, then argmax          */
 /* (src/engine-a4b.js:683-693).                                             */
 /* ------------------------------------------------------------------------ */
+/* Full (global) layers are "counted" (src/engine-a4b.js:217, :695-699,    */
+/* CACHEMODE 2): the new row goes to slot kv_count and attention reads      */
+/* slots [0, kv_count]; kv_count restarts at 0 when pos == 0 and equals     */
+/* pos until a compaction.  With scoring on, every step adds each live      */
+/* slot's normalised attention weight to score[l][h][slot] in f32 (attnos    */
+/* SCORE = 1, kernels/attnos.wgsl:78-92).                                   */
 struct orc_state {
   int layers;
   uint16_t** kc;
   uint16_t** vc;
   float* ple; /* [layers][ple_dim] per-layer inputs of the current token */
+  int64_t kv_count;
+  int scoring;
+  float** score; /* global layers: [q_heads][max_seq] */
 };
 
 static int64_t slots_of(const orc_model* m, int l) {
@@ -594,6 +611,9 @@ orc_state* orc_state_new(const orc_model* m) {
     s->vc[l] = calloc(n, sizeof(uint16_t));
   }
   s->ple = calloc((size_t)m->layers * (m->ple_dim > 0 ? m->ple_dim : 1), sizeof(float));
+  s->score = calloc((size_t)m->layers, sizeof(float*));
+  for (int l = 0; l < m->layers; ++l)
+    if (m->layer_global[l]) s->score[l] = calloc((size_t)m->q_heads * m->max_seq, sizeof(float));
   return s;
 }
 void orc_state_free(orc_state* s) {
@@ -605,7 +625,77 @@ void orc_state_free(orc_state* s) {
   free(s->kc);
   free(s->vc);
   free(s->ple);
+  for (int l = 0; l < s->layers; ++l) free(s->score[l]);
+  free(s->score);
   free(s);
+}
+void orc_state_set_scoring(orc_state* s, int on) { s->scoring = on; }
+int64_t orc_state_kv_count(const orc_state* s) { return s->kv_count; }
+const float* orc_state_score(const orc_state* s, int layer) { return s->score[layer]; }
+
+/* compactAll's selection (src/engine-a4b.js:587-617) for one full layer:    */
+/* mass[t] = sum over heads of score[h][t] (f64, head order); the candidates */
+/* [0, n - prot) sorted by mass, largest first, ties in index order (the     */
+/* stable Array.prototype.sort over an ascending list); keep the first       */
+/* budget - prot of them and the prot = min(protect, n) newest slots, in     */
+/* slot order.  Returns the number kept (<= n).                             */
+int64_t orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int budget, int protect,
+                    uint32_t* keep) {
+  double* mass = calloc((size_t)(n > 0 ? n : 1), sizeof(double));
+  for (int h = 0; h < qh; ++h)
+    for (int64_t t = 0; t < n; ++t) mass[t] += (double)score[h * scap + t];
+  const int64_t prot = protect < n ? protect : n;
+  const int64_t nc = n - prot;
+  int64_t want = budget - prot;
+  if (want < 0) want = 0;
+  if (want > nc) want = nc;
+  /* selection of the `want` largest by repeated scans: the first candidate  */
+  /* (lowest index) among equal masses wins, as the stable sort orders them */
+  char* taken = calloc((size_t)(nc > 0 ? nc : 1), 1);
+  int64_t cnt = 0;
+  for (int64_t k = 0; k < want; ++k) {
+    int64_t best = -1;
+    for (int64_t t = 0; t < nc; ++t)
+      if (!taken[t] && (best < 0 || mass[t] > mass[best])) best = t;
+    taken[best] = 1;
+  }
+  for (int64_t t = 0; t < nc; ++t)
+    if (taken[t]) keep[cnt++] = (uint32_t)t;
+  for (int64_t t = nc; t < n; ++t) keep[cnt++] = (uint32_t)t;
+  free(taken);
+  free(mass);
+  return cnt;
+}
+
+/* kvgather (kernels/kvgather.wgsl) of one full layer: slot i <- slot        */
+/* keep[i] for K and V, then its scores zeroed (src/engine-a4b.js:604-614).  */
+void orc_kv_gather_layer(const orc_model* m, orc_state* s, int layer, const uint32_t* keep, int64_t cnt) {
+  const int64_t row = (int64_t)m->kv_heads * m->head_dim;
+  uint16_t* tmp = malloc(sizeof(uint16_t) * (size_t)((cnt > 0 ? cnt : 1) * row));
+  uint16_t* caches[2] = {s->kc[layer], s->vc[layer]};
+  for (int c = 0; c < 2; ++c) {
+    for (int64_t i = 0; i < cnt; ++i) memcpy(tmp + i * row, caches[c] + (int64_t)keep[i] * row, sizeof(uint16_t) * row);
+    memcpy(caches[c], tmp, sizeof(uint16_t) * (size_t)(cnt * row));
+  }
+  memset(s->score[layer], 0, sizeof(float) * (size_t)m->q_heads * m->max_seq);
+  free(tmp);
+}
+void orc_state_set_kv_count(orc_state* s, int64_t n) { s->kv_count = n; }
+
+/* compactAll (src/engine-a4b.js:587-617) on every full layer: the keep list */
+/* of orc_kv_keep, the gather, zeroed scores; kv_count = the number kept.    */
+int64_t orc_kv_compact(const orc_model* m, orc_state* s, int budget, int protect) {
+  const int64_t n = s->kv_count;
+  uint32_t* keep = malloc(sizeof(uint32_t) * (size_t)(n > 0 ? n : 1));
+  int64_t cnt = n;
+  for (int l = 0; l < m->layers; ++l) {
+    if (!m->layer_global[l]) continue;
+    cnt = orc_kv_keep(s->score[l], m->q_heads, m->max_seq, n, budget, protect, keep);
+    orc_kv_gather_layer(m, s, l, keep, cnt);
+  }
+  s->kv_count = cnt;
+  free(keep);
+  return cnt;
 }
 const uint16_t* orc_state_kcache(const orc_state* s, int layer) { return s->kc[layer]; }
 const uint16_t* orc_state_vcache(const orc_state* s, int layer) { return s->vc[layer]; }
@@ -636,6 +726,8 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
   float* inv_g = malloc(sizeof(float) * HD);
   orc_rope_inv_freq(m->theta_local, HD, m->rope_angles, inv_l);
   orc_rope_inv_freq(m->theta_global, HD, m->rope_angles, inv_g);
+  if (pos == 0) st->kv_count = 0;
+  const int64_t kv = st->kv_count; /* full-layer slot of this token */
 
   /* embedding row * sqrt(H) (kernels/q6k.wgsl:37-73, MULT = sqrt(hidden)) */
   orc_q6k_dequant_row(m->tok_embd, H, token, (float)sqrt((double)H), h);
@@ -669,13 +761,27 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
     orc_q40_gemv(ly->wq, QH * HD, H, x, qkv);
     orc_q40_gemv(ly->wk, KVH * HD, H, x, qkv + QH * HD);
     orc_q40_gemv(ly->wv, KVH * HD, H, x, qkv + (QH + KVH) * HD);
-    int64_t slot = orc_kv_slot(m, glob, pos);
+    int64_t slot = glob ? kv : orc_kv_slot(m, glob, pos);
     orc_headprep(qkv, QH, KVH, HD, m->rope_angles, glob ? inv_g : inv_l, ly->q_norm, ly->k_norm,
                  m->eps, pos, qp, st->kc[l] + slot * KVH * HD, st->vc[l] + slot * KVH * HD);
-    if (glob)
-      orc_attn_linear(qp, st->kc[l], st->vc[l], QH, KVH, HD, pos + 1, ao);
-    else
+    if (glob) {
+      /* slots [0, kv]; with scoring, each slot's weight joins its mass */
+      const int64_t len = kv + 1;
+      int64_t* sl = malloc(sizeof(int64_t) * (size_t)len);
+      double* pr = malloc(sizeof(double) * (size_t)len);
+      for (int64_t t = 0; t < len; ++t) sl[t] = t;
+      for (int hh = 0; hh < QH; ++hh) {
+        attn_rows_p(qp + hh * HD, st->kc[l], st->vc[l], KVH, hh / (QH / KVH), HD, sl, len, ao + hh * HD,
+                    st->scoring ? pr : NULL);
+        if (st->scoring)
+          for (int64_t t = 0; t < len; ++t)
+            st->score[l][hh * m->max_seq + t] = st->score[l][hh * m->max_seq + t] + (float)pr[t];
+      }
+      free(sl);
+      free(pr);
+    } else {
       orc_attn_ring(qp, st->kc[l], st->vc[l], QH, KVH, HD, m->ring, m->window, pos, ao);
+    }
     orc_h2f_n(ao, QH * HD, a);
     orc_q40_gemv(ly->wo, H, QH * HD, a, o);
     /* h1 = h + rms(o) w_pa; x = f16(rms(h1) w_ffn) (kernels/rmsacc3.wgsl:36-53) */
@@ -721,5 +827,6 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
   if (!logits) free(lg);
   free(h); free(x); free(qkv); free(qp); free(ao); free(a); free(o); free(gu); free(gg);
   free(inv_l); free(inv_g);
+  st->kv_count = kv + 1;
   return am[0];
 }

@@ -133,6 +133,15 @@ uint32_t   orc_step(const orc_model* m, orc_state* s, uint32_t token, uint32_t p
 int64_t    orc_kv_slot(const orc_model* m, int is_global, uint32_t pos);
 const uint16_t* orc_state_kcache(const orc_state* s, int layer);
 const uint16_t* orc_state_vcache(const orc_state* s, int layer);
+/* full-layer KV budget (src/engine-a4b.js:587-617) */
+void       orc_state_set_scoring(orc_state* s, int on);
+int64_t    orc_state_kv_count(const orc_state* s);
+const float* orc_state_score(const orc_state* s, int layer);
+int64_t    orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int budget, int protect,
+                       uint32_t* keep);
+int64_t    orc_kv_compact(const orc_model* m, orc_state* s, int budget, int protect);
+void       orc_kv_gather_layer(const orc_model* m, orc_state* s, int layer, const uint32_t* keep, int64_t cnt);
+void       orc_state_set_kv_count(orc_state* s, int64_t n);
 
 #ifdef __cplusplus
 }

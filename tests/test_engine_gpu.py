@@ -112,8 +112,10 @@ def test_tiny_engine_step_api_and_reset():
     assert eng.argmax_fast() == b[-1]
     with pytest.raises(Exception):
         eng.step(cfg.vocab, 0)  # token out of range
+    # the full layers hold max_seq entries: fill them, then one more step
+    eng.decode_chunk(len(ids), cfg.max_seq - len(ids))
     with pytest.raises(Exception):
-        eng.step(1, cfg.max_seq)  # position beyond the cache
+        eng.step(1, cfg.max_seq)
 
 
 def test_generate_fast_matches_step_loop():

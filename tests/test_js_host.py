@@ -46,7 +46,7 @@ def test_addon_exports_engine_surface():
     out = _node("const a = require('./e4b_napi.node'); console.log(JSON.stringify(Object.keys(a).sort()), a.version())")
     keys = json.loads(out.split()[0])
     for k in ("create", "setTensor", "finalize", "step", "prefill", "decode", "argmax", "readHidden", "readLogits",
-              "reset", "destroy", "lastError", "deviceCount", "version"):
+              "kvCount", "readScores", "kvCompact", "reset", "destroy", "lastError", "deviceCount", "version"):
         assert k in keys
     assert "gfx950" in out
 
@@ -110,6 +110,27 @@ def test_js_host_matches_python_host(tmp_path):
     assert js["generate"] == gen
     assert js["steps"] == steps
     assert abs(js["hidden_l2"] - float(np.sqrt((h.astype(np.float64) ** 2).sum()))) <= 1e-5 * js["hidden_l2"]
+
+
+@_needs_node
+@pytest.mark.gpu
+def test_js_generate_long_matches_python_host(tmp_path):
+    # generateLong (src/engine-a4b.js:620-657) on both hosts with a small
+    # budget: probe step, compaction and recompactions take the same path
+    from e4b._lib import FLAG_KV_SCORE
+    cfg = tiny_config(layers=2, layer_global=[0, 1], max_seq=128)  # room for the driver's generateFast leg
+    path = tmp_path / "long.gguf"
+    _write_model(path, cfg, 61)
+    prompt = [int(x) for x in np.random.default_rng(61).integers(0, cfg.vocab, 30)]
+    over = {"ring": cfg.ring, "maxSeq": cfg.max_seq, "flags": FLAG_KV_SCORE}
+    opts = {"budget": 16, "protect": 4, "decap": 24}
+    r = subprocess.run([NODE, os.path.join(JS, "run_greedy.js"), str(path), ",".join(map(str, prompt)), "40",
+                        json.dumps(over), json.dumps(opts)], check=True, capture_output=True, text=True, timeout=300)
+    js = json.loads(r.stdout.strip().splitlines()[-1])
+    eng = Engine.from_gguf(str(path), ring=cfg.ring, max_seq=cfg.max_seq, flags=FLAG_KV_SCORE)
+    out = eng.generate_long(prompt, 40, eos=(), **opts)
+    assert js["generate_long"] == out
+    assert js["kv_count"] == eng.kv_count() <= opts["decap"]
 
 
 @pytest.mark.gpu

@@ -582,3 +582,101 @@ def test_moe_identical_experts_reduce_to_one_expert():
     ge = np.array([orc.gelu_tanh(float(a)) for a in g[:FF]]) * g[FF:]
     one = orc.q40_gemv(dn1, H, FF, ge.astype(np.float16).astype(np.float32)).astype(np.float64)
     np.testing.assert_allclose(moe, one, rtol=0, atol=2e-6 * np.abs(one).max())
+
+
+# --------------------------------------------------------------------------
+# Full-layer KV budget (src/engine-a4b.js:587-617 compactAll, attnos SCORE)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("masses,budget,protect,want", [
+    ([0.1, 0.5, 0.2, 0.5, 0.3, 0.0], 4, 1, [1, 3, 4, 5]),   # tie at 0.5: both fit
+    ([0.5, 0.5, 0.5, 0.5, 0.1, 0.2], 3, 2, [0, 4, 5]),      # four-way tie: lowest index first
+    ([0.9, 0.1, 0.8], 8, 1, [0, 1, 2]),                     # budget >= n: everything kept
+    ([0.9, 0.1, 0.8, 0.7], 1, 2, [2, 3]),                   # budget < protect: only the newest
+    ([0.3, 0.2], 2, 5, [0, 1]),                             # protect > n
+    ([], 4, 1, []),                                         # empty cache
+])
+def test_kv_keep_hand_cases(masses, budget, protect, want):
+    sc = np.array([masses], np.float32).reshape(1, -1) if masses else np.zeros((1, 1), np.float32)
+    got = orc.kv_keep(sc, len(masses), budget, protect)
+    assert got.tolist() == want
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_kv_keep_equals_stable_sort_over_head_sums(seed):
+    # an independent route to the same list: Python's stable sort of the
+    # candidates by decreasing f64 head-sum, quantised masses so ties occur
+    rng = np.random.default_rng(seed)
+    qh, scap, n = 8, 300, 257
+    sc = (rng.integers(0, 6, (qh, scap)) / 8.0).astype(np.float32)
+    budget, protect = 96, 16
+    got = orc.kv_keep(sc, n, budget, protect)
+    mass = [sum(float(sc[h, t]) for h in range(qh)) for t in range(n)]
+    cand = sorted(range(n - protect), key=lambda t: -mass[t])
+    want = sorted(cand[:budget - protect] + list(range(n - protect, n)))
+    assert got.tolist() == want
+    # the invariant a wrong comparator or off-by-one breaks: every kept
+    # candidate outweighs every dropped one
+    kept = set(got.tolist())
+    lo = min(mass[t] for t in kept if t < n - protect)
+    hi = max(mass[t] for t in range(n - protect) if t not in kept)
+    assert lo >= hi
+
+
+def _tiny_scored_model(seed, **kw):
+    from e4b.model import norm_weights_random, synth_tensors, tiny_config
+    cfg = tiny_config(**kw)
+    t = norm_weights_random(synth_tensors(cfg, seed), seed + 1)
+    om = orc.OracleModel(cfg.as_dict(), {n: x.data for n, x in t.items()})
+    return cfg, om
+
+
+def test_scores_are_attention_weights_summing_to_one_per_step():
+    # every scored step adds a probability distribution over slots [0, kv]
+    # per head: after k steps each head's row sums to k, slots beyond the
+    # live range stay 0, and slot t only gathers mass from steps >= t
+    cfg, om = _tiny_scored_model(3, layers=2, layer_global=[0, 1])
+    om.set_scoring(True)
+    k = 12
+    for p in range(k):
+        om.step(int(5 + 7 * p) % cfg.vocab, p)
+    sc = om.score(1).astype(np.float64)
+    np.testing.assert_allclose(sc.sum(axis=1), k, rtol=1e-5)
+    assert np.all(sc[:, k:] == 0)
+    assert np.all(sc >= 0)
+    # slot k-1 is live only in the last step: its mass is below 1 per head
+    assert np.all(sc[:, k - 1] <= 1.0 + 1e-6)
+    assert om.kv_count() == k
+
+
+def test_compaction_gathers_rows_and_resets_scores():
+    cfg, om = _tiny_scored_model(4, layers=2, layer_global=[0, 1], max_seq=64)
+    om.set_scoring(True)
+    n = 20
+    for p in range(n):
+        om.step(int(11 + 3 * p) % cfg.vocab, p)
+    row = cfg.kv_heads * cfg.head_dim
+    k_before = om.kcache(1, cfg.max_seq * row).reshape(cfg.max_seq, row)
+    v_before = om.vcache(1, cfg.max_seq * row).reshape(cfg.max_seq, row)
+    want_keep = orc.kv_keep(om.score(1), n, 8, 3)
+    assert om.compact(8, 3) == 8 and om.kv_count() == 8
+    k_after = om.kcache(1, cfg.max_seq * row).reshape(cfg.max_seq, row)
+    v_after = om.vcache(1, cfg.max_seq * row).reshape(cfg.max_seq, row)
+    assert np.array_equal(k_after[:8], k_before[want_keep])
+    assert np.array_equal(v_after[:8], v_before[want_keep])
+    assert np.all(om.score(1) == 0)
+    # decoding continues at slot 8 while the position keeps counting
+    om.step(7, n)
+    assert om.kv_count() == 9
+    assert np.any(om.kcache(1, cfg.max_seq * row).reshape(cfg.max_seq, row)[8] != k_after[8])
+
+
+def test_counted_slots_equal_positions_without_compaction():
+    # kv_count restarts with position 0 and tracks the position: the global
+    # layer writes slot p at position p, as before counting was introduced
+    cfg, om = _tiny_scored_model(5, layers=2, layer_global=[0, 1])
+    for p in range(6):
+        om.step(9, p)
+    assert om.kv_count() == 6
+    om.step(9, 0)
+    assert om.kv_count() == 1
