@@ -1,6 +1,6 @@
 """Benchmark of the batch-1 decode path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c3p|c1|c0|prefill] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c3p|c1|c0|prefill|long] [--no-cpu]
 
 Prints ONE JSON line (rank 0).  Workloads:
   c0  one q4_0 GEMV 16384x2048 (x f32), weights rotated over >512 MB so the
@@ -14,6 +14,9 @@ Prints ONE JSON line (rank 0).  Workloads:
       GEMMs); a step = one whole prefill.
   c3p the c3 MoE half-layer over a 512-token chunk (expert-grouped
       GEMMs); a step = one layer.
+  long  the c4 model at an 8192-token context: decode on the whole cache,
+      then after compaction of the full layers to the 640-entry budget
+      (generateLong's schedule); a step = one decode token after compaction.
 `roofline` is measured live with HIP events on the launch stream; the CPU
 baseline times the oracle (the C restatement, OpenMP) on a bounded sample.
 """
@@ -353,6 +356,64 @@ def bench_prefill(steps: int, warmup: int, cpu: bool) -> dict:
     }
 
 
+def _decode_bytes(cfg, sliding_live: int, global_live: int) -> int:
+    """Algorithmic bytes of one decode step with the given live K/V rows per
+    sliding and per full layer (cfg.bytes_per_token with the KV term replaced)."""
+    kv_row = 2 * cfg.kv_heads * cfg.head_dim * 2
+    base = cfg.bytes_per_token(0) - len(cfg.layer_global) * kv_row  # position 0: one live row per layer
+    return base + sum((global_live if g else sliding_live) * kv_row for g in cfg.layer_global)
+
+
+def bench_long(steps: int, warmup: int, cpu: bool) -> dict:
+    """Long-context decode (src/engine-a4b.js:587-657): an 8192-token prompt
+    on the E4B-shaped model with 8320 full-layer slots (KV_PRECAP), decode on
+    the whole cache, then after compaction to the 640-entry budget (protect
+    64); the full-cache decode is also timed on an engine without scoring."""
+    from e4b import formats
+    from e4b._lib import FLAG_KV_SCORE
+    from e4b.engine import KV_BUDGET, KV_PROTECT, Engine
+    from e4b.model import E4BConfig, synth_tensors
+
+    n = 8192
+    cfg = E4BConfig(max_seq=8320, max_prompt=n, flags=FLAG_KV_SCORE)
+    tensors = synth_tensors(cfg, seed=0)
+    prompt = formats.synth_uniform_u32(7, n, 0, cfg.vocab)
+    eng = Engine(cfg, tensors)
+    t_prefill = time_prefill(eng, prompt, reps=1)
+    eng.time_decode(n, warmup)
+    ms_full = eng.time_decode(n + warmup, steps) / steps
+    pos = n + warmup + steps
+    kept = eng.compact(KV_BUDGET, KV_PROTECT)
+    eng.time_decode(pos, warmup)
+    ms_budget = eng.time_decode(pos + warmup, steps) / steps
+    kv_mid = kept + warmup + steps // 2
+    eng.close()
+    plain = Engine(E4BConfig(max_seq=8320, max_prompt=n), tensors)
+    plain.prefill(prompt)
+    plain.time_decode(n, warmup)
+    ms_plain = plain.time_decode(n + warmup, steps) / steps
+    plain.close()
+    b_budget = _decode_bytes(cfg, cfg.window, kv_mid)
+    b_full = _decode_bytes(cfg, cfg.window, n + warmup + steps // 2)
+    gbs = b_budget / (ms_budget * 1e-3) / 1e9
+    return {
+        "metric": "batch-1 decode tokens/s at 8192-token context, 640-entry full-layer KV budget (E4B-shape q4_0)",
+        "value": round(1e3 / ms_budget, 2), "unit": "tokens/s", "ms_per_step": ms_budget,
+        "dtype": "q4_0/q6_K weights, f16 activations and KV, f32 accumulate",
+        "config": {"workload": "generateLong schedule on the c4 model: 8192-token prompt, full-layer slots 8320, "
+                               "compaction to 640 (protect 64); scored decode",
+                   "prompt_tokens": n, "prefill_ms": round(t_prefill * 1e3, 1),
+                   "decode_ms_full_cache_scored": round(ms_full, 4),
+                   "decode_ms_full_cache_unscored": round(ms_plain, 4),
+                   "decode_ms_budget_scored": round(ms_budget, 4),
+                   "speedup_budget_vs_full_unscored": round(ms_plain / ms_budget, 3),
+                   "bytes_per_token_full": b_full, "bytes_per_token_budget": b_budget},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole decode step (graph replay) after compaction"},
+    }
+
+
 def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict:
     from e4b import formats
     from e4b._lib import FLAG_NO_GRAPH
@@ -415,7 +476,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c3p", "c4", "prefill"])
+    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c3p", "c4", "prefill", "long"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
@@ -429,9 +490,9 @@ def main() -> int:
               "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
     fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c3p": bench_c3p, "c4": bench_c4,
-          "prefill": bench_prefill}[a.workload]
-    steps = a.steps if a.steps is not None else {"c4": 240, "prefill": 10}.get(a.workload, 200)
-    warmup = a.warmup if a.warmup is not None else {"c4": 16, "prefill": 2}.get(a.workload, 20)
+          "prefill": bench_prefill, "long": bench_long}[a.workload]
+    steps = a.steps if a.steps is not None else {"c4": 240, "prefill": 10, "long": 64}.get(a.workload, 200)
+    warmup = a.warmup if a.warmup is not None else {"c4": 16, "prefill": 2, "long": 8}.get(a.workload, 20)
     if a.workload == "c4" and a.kernel_only:
         from e4b.model import E4BConfig
         dom = _time_geglu(E4BConfig(), steps)
