@@ -102,6 +102,19 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
     else
       return wbase + min(c0 + r, units - 1);
   };
+  // activation row and validity of this thread's XP pieces: fixed for the
+  // whole K loop (grouped mode: the gathered row index, one load and one
+  // division per piece here instead of a dependent load chain per stage)
+  int64_t xrow_of[XP];
+  bool mrow_in[XP];
+#pragma unroll
+  for (int j = 0; j < XP; ++j) {
+    const int m = (threadIdx.x + 256 * j) / (KBL * 4);
+    mrow_in[j] = m < nrows;
+    int64_t xrow = tok0 + m;
+    if constexpr (GRP) xrow = a.gather ? (int64_t)(a.gather[mrow_in[j] ? xrow : tok0] / (uint32_t)a.gather_div) : xrow;
+    xrow_of[j] = xrow;
+  }
   uint4 wr[WP];
   uint16_t sr[SP];
   uint4 xr[XP];
@@ -123,13 +136,10 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
     }
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
-      const int i = threadIdx.x + 256 * j;
-      const int m = i / (KBL * 4), q = i % (KBL * 4);
+      const int q = (threadIdx.x + 256 * j) % (KBL * 4);
       const int kq = kb0 * 32 + q * 8;
-      const bool in = m < nrows && kq < kend * 32;
-      int64_t xrow = tok0 + m;
-      if constexpr (GRP) xrow = a.gather ? (int64_t)(a.gather[in ? xrow : tok0] / (uint32_t)a.gather_div) : xrow;
-      const uint4 v = *reinterpret_cast<const uint4*>(a.X + (in ? xrow * a.ldx + kq : 0));
+      const bool in = mrow_in[j] && kq < kend * 32;
+      const uint4 v = *reinterpret_cast<const uint4*>(a.X + (in ? xrow_of[j] * a.ldx + kq : 0));
       xr[j] = in ? v : make_uint4(0u, 0u, 0u, 0u);
     }
   };
