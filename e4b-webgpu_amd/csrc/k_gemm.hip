@@ -56,13 +56,18 @@ DEV h8 nib_word_f16(uint32_t w) {
 // per row and thread group -- a wave that loaded its own B fragments would
 // touch 32 rows with 16 bytes each per instruction, which measured 1.5-2.3x
 // slower -- and each stage's loads overlap the previous stage's math.
-constexpr int KBL = 4;            // q4_0 blocks per stage (128 k)
-constexpr int WSL = KBL + 1;      // uint4 per staged weight row (+1 pad: conflict-free 16-byte reads)
-constexpr int SSL = KBL + 2;      // f16 scales per staged row (+2 pad)
-constexpr int XSL = KBL * 4 + 1;  // uint4 per staged token row (+1 pad)
+constexpr int KBL = 4;            // q4_0 blocks per stage (128 k); split-K slices are multiples of it
 
-template <int T, int EPI, bool GRP>
+// KB blocks per stage (KBL, or 8 for the grouped expert GEMMs: their weight
+// rows are read once per 32-row tile, and 8 blocks make each row's stage
+// one whole 128-byte line)
+template <int T, int EPI, bool GRP, int KB = KBL>
 __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs) {
+  constexpr int KBL = KB;
+  constexpr int WSL = KBL + 1;      // uint4 per staged weight row (+1 pad: conflict-free 16-byte reads)
+  constexpr int SSL = KBL + 2;      // f16 scales per staged row (+2 pad)
+  constexpr int XSL = KBL * 4 + 1;  // uint4 per staged token row (+1 pad)
+  static_assert(KBL == 4 || KBL == 8, "4 or 8 blocks per stage");
   constexpr int NT = EPI == GEMM_GLU ? 2 : 1;
   constexpr int TOK = 32 * T;
   constexpr int RW = 128 * NT;                 // staged weight rows
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
 template <int EPI>
 void launch_t(int T, const GemmArgs& a, dim3 grid, int K, int nbs, hipStream_t st) {
   if (a.tiles) {
-    hipLaunchKernelGGL((k_q40_gemm_lds<1, EPI, true>), grid, dim3(256), 0, st, a, K, nbs);
+    hipLaunchKernelGGL((k_q40_gemm_lds<1, EPI, true, 8>), grid, dim3(256), 0, st, a, K, nbs);
     return;
   }
   if (T == 4)
