@@ -161,7 +161,7 @@ def test_q6k_scale_groups_are_16_contiguous_elements():
 
 
 def test_q6k_gemv_equals_rowwise_mode0_and_refold():
-    # survey invariant: MODE 1 == row-wise MODE 0 . x; plus the reference's
+    # invariant: MODE 1 == row-wise MODE 0 . x; plus the reference's
     # 255*bacc - 32*gsum refold (kernels/q6k.wgsl:113-124) evaluated exactly
     rng = np.random.default_rng(2)
     rows, cols = 9, 512
