@@ -965,31 +965,18 @@ extern "C" int e4b_kv_compact(e4b_ctx* c, int budget, int protect) {
   if (budget < 0 || protect < 0) return e4b_fail(E4B_EINVAL, "e4b_kv_compact: budget %d, protect %d", budget, protect);
   const int QH = c->cfg.q_heads, KVH = c->cfg.kv_heads, HD = c->cfg.head_dim;
   const int64_t n = c->kv_count;
-  const int64_t prot = std::min<int64_t>(protect, n), nc = n - prot;
-  const int64_t want = std::max<int64_t>(0, std::min<int64_t>(budget - prot, nc));
   std::vector<float> sc;
-  std::vector<double> mass((size_t)std::max<int64_t>(n, 1));
-  std::vector<uint32_t> cand((size_t)std::max<int64_t>(nc, 1)), keep;
+  std::vector<uint32_t> keep((size_t)std::max<int64_t>(n, 1));
   E4B_HIP(hipStreamSynchronize(c->st));
   for (Layer& ly : c->L) {
     if (!ly.global) continue;
     sc.resize((size_t)QH * ly.slots);
     E4B_HIP(hipMemcpy(sc.data(), ly.score, sc.size() * 4, hipMemcpyDeviceToHost));
-    // mass per slot, summed over heads in head order (f64)
-    std::fill(mass.begin(), mass.end(), 0.0);
-    for (int h = 0; h < QH; ++h)
-      for (int64_t t = 0; t < n; ++t) mass[(size_t)t] += (double)sc[(size_t)h * ly.slots + (size_t)t];
-    // candidates by decreasing mass, equal masses in slot order (the stable
-    // sort of an ascending list), then the protected newest entries
-    for (int64_t t = 0; t < nc; ++t) cand[(size_t)t] = (uint32_t)t;
-    std::stable_sort(cand.begin(), cand.begin() + nc,
-                     [&](uint32_t a, uint32_t b) { return mass[a] > mass[b]; });
-    keep.assign(cand.begin(), cand.begin() + want);
-    for (int64_t t = nc; t < n; ++t) keep.push_back((uint32_t)t);
-    std::sort(keep.begin(), keep.end());
-    const int cnt = (int)keep.size();
+    const int64_t sel = e4b_kv_select(sc.data(), QH, ly.slots, n, budget, protect, keep.data());
+    if (sel < 0) return (int)sel;
+    const int cnt = (int)sel;
     if (cnt > 0) {
-      E4B_HIP(hipMemcpyAsync(c->keep, keep.data(), keep.size() * 4, hipMemcpyHostToDevice, c->st));
+      E4B_HIP(hipMemcpyAsync(c->keep, keep.data(), (size_t)cnt * 4, hipMemcpyHostToDevice, c->st));
       if ((rc = launch_kv_gather(c->keep, cnt, ly.kc, ly.vc, KVH, ly.slots, c->kv_sk, c->kv_sv, ly.slots, c->st)))
         return rc;
       // rows [0, cnt) of every head back into the cache

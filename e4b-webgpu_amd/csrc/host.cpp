@@ -4,6 +4,9 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "../../include/e4b.h"
 #include "common.h"
 #include "util.h"
@@ -211,4 +214,30 @@ extern "C" int e4b_synth_q6k(uint64_t seed, int64_t rows, int64_t cols, float si
 // ---------------------------------------------------------------------------
 void rope_inv_freq(float theta, int head_dim, int angles, float* out) {
   for (int p = 0; p < angles; ++p) out[p] = (float)pow((double)theta, -2.0 * (double)p / (double)head_dim);
+}
+
+// ---------------------------------------------------------------------------
+// compactAll's selection (src/engine-a4b.js:590-603) for one full layer:
+// mass[t] = sum over heads of score[h][t] in f64, head order; the candidates
+// [0, n - prot) by decreasing mass, equal masses in slot order (the stable
+// Array.prototype.sort of an ascending list); the first budget - prot of them
+// plus the prot = min(protect, n) newest slots, ascending.
+// ---------------------------------------------------------------------------
+extern "C" int64_t e4b_kv_select(const float* score, int q_heads, int64_t stride, int64_t n, int budget, int protect,
+                                 uint32_t* keep_out) {
+  if (!score || !keep_out || q_heads < 1 || n < 0 || stride < n || budget < 0 || protect < 0)
+    return e4b_fail(E4B_EINVAL, "e4b_kv_select: bad arguments");
+  std::vector<double> mass((size_t)std::max<int64_t>(n, 1), 0.0);
+  for (int h = 0; h < q_heads; ++h)
+    for (int64_t t = 0; t < n; ++t) mass[(size_t)t] += (double)score[(size_t)h * (size_t)stride + (size_t)t];
+  const int64_t prot = std::min<int64_t>(protect, n), nc = n - prot;
+  const int64_t want = std::max<int64_t>(0, std::min<int64_t>(budget - prot, nc));
+  std::vector<uint32_t> cand((size_t)nc);
+  for (int64_t t = 0; t < nc; ++t) cand[(size_t)t] = (uint32_t)t;
+  std::stable_sort(cand.begin(), cand.end(), [&](uint32_t a, uint32_t b) { return mass[a] > mass[b]; });
+  std::vector<uint32_t> keep(cand.begin(), cand.begin() + want);
+  for (int64_t t = nc; t < n; ++t) keep.push_back((uint32_t)t);
+  std::sort(keep.begin(), keep.end());
+  std::copy(keep.begin(), keep.end(), keep_out);
+  return (int64_t)keep.size();
 }

@@ -344,6 +344,11 @@ int  e4b_time_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, float* ms
 int  e4b_kv_count(e4b_ctx* ctx);
 int  e4b_read_scores(e4b_ctx* ctx, int layer, float* out);
 int  e4b_kv_compact(e4b_ctx* ctx, int budget, int protect);
+/* the selection e4b_kv_compact applies to one full layer (host only, no
+ * device): score [q_heads][stride] over slots [0, n); writes the kept slots,
+ * ascending, to keep_out[n] and returns their number, or a negative error */
+int64_t e4b_kv_select(const float* score, int q_heads, int64_t stride, int64_t n, int budget, int protect,
+                      uint32_t* keep_out);
 
 /* GGUF loading on the C ABI (openGGUF, src/gguf.js:17-83, and the tensor
  * loop of loadEngineA4B, src/engine-a4b.js:121-214): the file is

@@ -160,3 +160,38 @@ def test_native_gguf_config_matches_metadata(tmp_path):
     trunc.write_bytes(path.read_bytes()[:200])
     with pytest.raises(E4BError):
         gguf_config(str(trunc))
+
+
+def _kv_select(score, n, budget, protect):
+    import ctypes as C
+    sc = np.ascontiguousarray(score, np.float32)
+    keep = np.empty(max(n, 1), np.uint32)
+    cnt = _lib.check(_lib.lib.e4b_kv_select(sc.ctypes.data_as(C.c_void_p), sc.shape[0], sc.shape[1], n, budget,
+                                            protect, keep.ctypes.data_as(C.c_void_p)), "e4b_kv_select")
+    return keep[:cnt]
+
+
+@pytest.mark.parametrize("seed,n,budget,protect", [(0, 257, 96, 16), (1, 64, 64, 8), (2, 40, 10, 0), (3, 9, 2, 5),
+                                                   (4, 0, 4, 1), (5, 300, 640, 64)])
+def test_kv_select_matches_oracle(seed, n, budget, protect):
+    # the library's host selection (used by e4b_kv_compact) against the
+    # oracle's restatement of compactAll, on quantised scores so that equal
+    # masses occur and the tie order is exercised
+    rng = np.random.default_rng(seed)
+    sc = (rng.integers(0, 5, (8, max(n, 1) + 7)) / 4.0).astype(np.float32)
+    got = _kv_select(sc, n, budget, protect)
+    want = orc.kv_keep(sc, n, budget, protect)
+    assert np.array_equal(got, want)
+    assert np.all(np.diff(got.astype(np.int64)) > 0)
+
+
+def test_kv_select_rejects_bad_arguments():
+    import ctypes as C
+    sc = np.zeros((2, 4), np.float32)
+    keep = np.empty(8, np.uint32)
+    p = sc.ctypes.data_as(C.c_void_p)
+    k = keep.ctypes.data_as(C.c_void_p)
+    sel = _lib.lib.e4b_kv_select
+    assert sel(p, 2, 4, 8, 2, 1, k) < 0   # n beyond the stride
+    assert sel(p, 2, 4, 4, -1, 1, k) < 0  # negative budget
+    assert sel(None, 2, 4, 4, 2, 1, k) < 0
