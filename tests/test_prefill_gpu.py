@@ -41,6 +41,7 @@ HD = 256
     (2, 1024, 512, 3000, 37, 5),  # ragged chunk deep in the ring
     (1, 64, 32, 100, 33, 6),      # small ring at its chunk limit, one KV group
     (2, 1024, 512, 7, 1, 7),      # a single token
+    (2, 8320, 0, 8000, 64, 8),    # deep global chunk: 8 key splits of 1024
 ])
 def test_attn_prefill(kvh, slots, window, p0, m, seed):
     qh = 4 * kvh
@@ -181,3 +182,31 @@ def test_prefill_again_after_decode_matches_fresh_engine(n2):
     ta, tb = a.decode_chunk(n2, 8), b.decode_chunk(n2, 8)
     assert np.array_equal(ta, tb)
     assert np.array_equal(a.read_logits(), b.read_logits())
+
+
+def test_long_prompt_batched_equals_step_prefill():
+    # 2000 tokens through 223 ring-limited chunks of 9; the global layer's
+    # later chunks split their up to 2000 keys over 8 workgroups.  The batched
+    # prefill and the token-by-token prefill of the same engine agree on the
+    # continuation, the logits and every cache.
+    cfg = tiny_config(layers=3, layer_global=[0, 1, 0], max_seq=2048)
+    tensors = norm_weights_random(synth_tensors(cfg, 91), 92)
+    a = Engine(cfg, tensors)
+    b = Engine(tiny_config(layers=3, layer_global=[0, 1, 0], max_seq=2048, flags=FLAG_STEP_PREFILL), tensors)
+    prompt = np.random.default_rng(93).integers(0, cfg.vocab, 2000)
+    ga, gb = a.prefill(prompt), b.prefill(prompt)
+    la, lb = a.read_logits(), b.read_logits()
+    err = float(np.max(np.abs(la - lb)) / np.max(np.abs(lb)))
+    print(f"2000-token prompt: batched {ga} step {gb}, logits err {err:.2e}")
+    assert err < LOGIT_TOL
+    assert ga == gb or top2_margin(lb) < TIE_TOL * np.abs(lb).max()
+    for layer in range(cfg.layers):
+        ka, va = a.read_kv(layer)
+        kb, vb = b.read_kv(layer)
+        for x, y in ((ka, kb), (va, vb)):
+            fx = x.view(np.float16).astype(np.float64)
+            fy = y.view(np.float16).astype(np.float64)
+            d = np.abs(fx - fy)
+            assert d.max() <= KV_MAX_TOL * np.abs(fy).max(), f"layer {layer} cache (max)"
+            assert d.mean() <= KV_MEAN_TOL * np.abs(fy).mean(), f"layer {layer} cache (mean)"
+    assert np.array_equal(a.decode_chunk(2000, 8), b.decode_chunk(2000, 8))
