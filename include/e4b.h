@@ -263,7 +263,7 @@ typedef struct e4b_config {
   int32_t vocab;          /* 262144 */
   int32_t window;         /* sliding window, 512 */
   int32_t ring;           /* sliding-layer ring slots (>= window), 1024 */
-  int32_t max_seq;        /* global-layer cache capacity (positions) */
+  int32_t max_seq;        /* global-layer cache capacity (entries; see e4b_kv_count) */
   int32_t rope_angles;    /* rotated pairs per head, 128 */
   float theta_local;      /* 1e4 */
   float theta_global;     /* 1e6 */
