@@ -396,6 +396,9 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
     if (cap > c->max_prompt) cap = c->max_prompt;
     if (cap > k.max_seq) cap = k.max_seq;
     if (any_sliding && cap > k.ring - k.window + 1) cap = k.ring - k.window + 1;
+    // whole 128-token GEMM tiles: a 513-token chunk (ring 1024, window 512)
+    // would run a fifth token tile for one token
+    if (cap > 128) cap = cap / 128 * 128;
     c->pf_cap = cap;
     const size_t M = (size_t)cap, NPs = (size_t)NP;
     if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||

@@ -304,7 +304,8 @@ int  e4b_finalize(e4b_ctx* ctx);              /* allocates KV/activations, captu
  * NULL; argmax_out may be NULL */
 int  e4b_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, float* logits_or_null, uint32_t* argmax_out);
 /* prefill of ids[0..n) from position 0 (prefill, src/engine-a4b.js:550-584):
- * chunks of up to 512 tokens (and at most ring - window + 1, so every key a
+ * chunks of up to 512 tokens (and at most ring - window + 1, rounded down
+ * to a multiple of 128 above 128, so every key a
  * chunk's queries need keeps its ring slot), each layer as batched q4_0
  * GEMMs on the matrix cores plus per-token head prep, causal attention and
  * norms; the lm-head runs once, for the last token.  argmax_out = greedy
