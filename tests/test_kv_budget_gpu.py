@@ -201,3 +201,24 @@ def test_decode_refuses_to_overrun_the_full_layer_cache():
     eng.compact(16, 4)
     assert eng.kv_count() == 16
     assert len(eng.decode_chunk(32, 8)) == 8
+
+
+def test_position_gap_appends_to_the_next_full_layer_slot():
+    # counted full layers (src/engine-a4b.js:695-699): after positions 0..4 a
+    # step at position 40 rotates by 40 but writes full-layer slot 5 and
+    # attends to slots 0..5; the sliding ring still indexes by position.
+    # Host-fed steps on the engine and the oracle agree token by token.
+    cfg, eng, om = _build(77, flags=0)
+    toks = [11, 22, 33, 44, 55]
+    for i, t in enumerate(toks):
+        a = eng.step(t, i)
+        b, _, _ = om.step(t, i)
+        assert a == b
+    for pos, t in ((40, 66), (41, 77), (42, 88)):
+        a, lg = eng.step(t, pos, want_logits=True)
+        b, o_lg, _ = om.step(t, pos, want_logits=True)
+        assert a == b or top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max()
+        assert float(np.abs(lg - o_lg).max() / np.abs(o_lg).max()) < LOGIT_TOL
+    assert eng.kv_count() == om.kv_count() == 8
+    k, _ = eng.read_kv(GLOBAL)
+    assert np.any(k[:, 7] != 0) and np.all(k[:, 8:] == 0)
