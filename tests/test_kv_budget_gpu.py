@@ -222,3 +222,18 @@ def test_position_gap_appends_to_the_next_full_layer_slot():
     assert eng.kv_count() == om.kv_count() == 8
     k, _ = eng.read_kv(GLOBAL)
     assert np.any(k[:, 7] != 0) and np.all(k[:, 8:] == 0)
+
+
+def test_compaction_below_the_budget_keeps_everything():
+    # fewer entries than the budget: every entry is kept in place, the
+    # scores are zeroed and decoding continues at the same slot
+    cfg, eng, om = _build(88)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, 12)
+    g0 = eng.prefill(prompt)
+    toks = eng.decode_chunk(12, 6).tolist()
+    k_before, v_before = eng.read_kv(GLOBAL)
+    assert eng.compact(64, 4) == 18 == eng.kv_count()
+    k_after, v_after = eng.read_kv(GLOBAL)
+    assert np.array_equal(k_after, k_before) and np.array_equal(v_after, v_before)
+    assert np.all(eng.read_scores(GLOBAL) == 0)
+    assert len(eng.decode_chunk(18, 4)) == 4 and eng.kv_count() == 22

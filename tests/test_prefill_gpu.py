@@ -14,7 +14,7 @@ ring - window + 1) in lock-step with the oracle's token-by-token step
 (tests/test_engine_gpu.py tolerances: greedy tokens bit-exact outside
 near-ties, logits within 1e-3 of the logit range, KV caches within 1e-2 max /
 1e-3 mean relative), and against the engine's own token-by-token prefill
-(E4B_FLAG_STEP_PREFILL) at E4B width with a 512-token prompt.
+(E4B_FLAG_STEP_PREFILL) at E4B width with 512- and 520-token prompts.
 """
 import numpy as np
 import pytest
@@ -131,18 +131,20 @@ def test_tiny_no_ple_batched_prefill():
         _kv_check(eng, om, cfg, layer)
 
 
-def test_c4_width_prefill_matches_step_prefill():
-    # E4B width (5 layers, one global): 512-token prompt through the batched
-    # prefill and through the decode step; same continuation, logits and KV
+@pytest.mark.parametrize("n", [512, 520])
+def test_c4_width_prefill_matches_step_prefill(n):
+    # E4B width (5 layers, one global): a 512-token prompt (one chunk) and a
+    # 520-token one (chunks of 512 and 8) through the batched prefill and
+    # through the decode step; same continuation, logits and KV
     cfg = E4BConfig(layers=5, max_seq=1024, layer_global=[0, 0, 0, 0, 1])
     tensors = norm_weights_random(synth_tensors(cfg, 13), 14)
     a = Engine(cfg, tensors)
     b = Engine(E4BConfig(layers=5, max_seq=1024, layer_global=[0, 0, 0, 0, 1], flags=FLAG_STEP_PREFILL), tensors)
-    prompt = np.random.default_rng(15).integers(0, cfg.vocab, 512)
+    prompt = np.random.default_rng(15).integers(0, cfg.vocab, n)
     ga, gb = a.prefill(prompt), b.prefill(prompt)
     la, lb = a.read_logits(), b.read_logits()
     err = float(np.max(np.abs(la - lb)) / np.max(np.abs(lb)))
-    print(f"c4-width 512-token prefill: batched {ga} step {gb}, logits err {err:.2e}")
+    print(f"c4-width {n}-token prefill: batched {ga} step {gb}, logits err {err:.2e}")
     assert err < LOGIT_TOL
     assert ga == gb or top2_margin(lb) < TIE_TOL * np.abs(lb).max()
     for layer in range(cfg.layers):
@@ -155,8 +157,8 @@ def test_c4_width_prefill_matches_step_prefill():
             assert d.max() <= KV_MAX_TOL * np.abs(fy).max(), f"layer {layer} cache (max)"
             assert d.mean() <= KV_MEAN_TOL * np.abs(fy).mean(), f"layer {layer} cache (mean)"
     # the decode continuation from both
-    ta = a.decode_chunk(512, 8)
-    tb = b.decode_chunk(512, 8)
+    ta = a.decode_chunk(n, 8)
+    tb = b.decode_chunk(n, 8)
     print(f"continuations {ta.tolist()} / {tb.tolist()}")
     assert np.array_equal(ta, tb)
 
