@@ -1,11 +1,13 @@
 """Benchmark of the batch-1 decode path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c3p|c1|c0|prefill|long] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c3p|c2|c1|c0|prefill|long] [--no-cpu]
 
 Prints ONE JSON line (rank 0).  Workloads:
   c0  one q4_0 GEMV 16384x2048 (x f32), weights rotated over >512 MB so the
       256 MB MALL cannot serve them; a step = one GEMV.
   c1  Q6_K lm-head 262144x2048 + softcap + argmax; a step = one launch.
+  c2  one layer's decode attention: global at 4096 positions, sliding
+      (window 512, ring 1024) at positions 4095 and 300; a step = one layer.
   c3  A4B-style MoE half-layer (hidden 2816, 128 experts top-8); a step =
       one layer (4 launches), weights rotated over 3 copies.
   c4  the E4B-shaped decode loop; a step = one greedy decode token (the
@@ -143,6 +145,81 @@ def bench_c1(steps: int, warmup: int, cpu: bool) -> dict:
         dt = (time.perf_counter() - t0) / n
         out["cpu_baseline"] = {"value": round(algo / dt / 1e9, 3), "unit": "GB/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"{n} oracle lm-heads 262144x2048 (~10 s)"}
+    return out
+
+
+def bench_c2(steps: int, warmup: int, cpu: bool) -> dict:
+    """One layer's decode attention (e4b_k_attn_decode: head prep + RoPE, K/V
+    row write, split-K partials, then the log-sum-exp combine launch) at the
+    three c2 points: a global layer at position 4095 over 4096 cached
+    positions (theta 1e6), and a sliding layer (window 512, 1024-slot ring,
+    theta 1e4) at position 4095 (wrapped ring) and 300.  Each case rotates
+    over enough cache copies (>= 512 MB) that the 256 MB MALL cannot serve
+    the next launch; a step = one layer's attention.  Algorithmic bytes per
+    layer: the live K/V rows (2 KB a position) + the raw qkv f32 (12 KB) +
+    the f16 output (4 KB) + the new K/V row (2 KB)."""
+    from e4b.device import Event
+    from e4b.kernels import AttnLayer
+
+    QH, KVH, HD = 8, 2, 256
+    rng = np.random.default_rng(0)
+    qw = (1.0 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    kw = (0.25 * (1.0 + 0.1 * rng.standard_normal(HD))).astype(np.float32)
+    qkv = rng.standard_normal((QH + 2 * KVH) * HD).astype(np.float32)
+    cases = [("global", 4096, 0, 1e6, 4095), ("sliding", 1024, 512, 1e4, 4095), ("sliding", 1024, 512, 1e4, 300)]
+    res = []
+    for kind, slots, window, theta, pos in cases:
+        cache_bytes = 2 * KVH * slots * HD * 2
+        ncopy = max(2, (2 * MALL_BYTES) // cache_bytes + 1)
+        k = (0.25 * rng.standard_normal((KVH, slots, HD))).astype(np.float16)
+        v = rng.standard_normal((KVH, slots, HD)).astype(np.float16)
+        layers = []
+        for _ in range(ncopy):
+            L = AttnLayer(QH, KVH, HD, slots, window, theta, 128, qw, kw)
+            L.load_cache(k, v)
+            L.qkv.upload(qkv)
+            layers.append(L)
+        live = min(pos + 1, window) if window else pos + 1
+        algo = live * KVH * HD * 2 * 2 + qkv.size * 4 + QH * HD * 2 + KVH * HD * 2 * 2
+        for i in range(warmup):
+            layers[i % ncopy].step_dev(pos)
+        e0, e1 = Event(), Event()
+        e0.record()
+        for i in range(steps):
+            layers[i % ncopy].step_dev(pos)
+        e1.record()
+        ms = e0.elapsed_ms(e1) / steps
+        res.append({"layer": kind, "pos": pos, "live_positions": live, "algorithmic_bytes": algo,
+                    "us_per_layer": round(ms * 1e3, 3), "gbs": round(algo / (ms * 1e-3) / 1e9, 1),
+                    "cache_copies_rotated": ncopy})
+        del layers
+    g = res[0]
+    out = {
+        "metric": "decode attention GB/s, global layer at 4096 positions (config c2)", "value": g["gbs"],
+        "unit": "GB/s", "ms_per_step": g["us_per_layer"] / 1e3, "dtype": "f16 KV, f32 softmax and accumulate",
+        "config": {"workload": "c2: GQA 8q/2kv x 256, split-K 64-position chunks + combine; global 4096 "
+                               "positions (theta 1e6), sliding window 512 / ring 1024 (theta 1e4)",
+                   "cases": res},
+        "roofline": {"bound": "hbm", "achieved": g["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_attn_split + k_attn_combine (global layer, pos 4095)",
+                     "algorithmic_bytes_per_launch": g["algorithmic_bytes"]},
+    }
+    if cpu:
+        import oracle as orc
+        inv = orc.rope_inv_freq(1e6, HD, 128)
+        kc = (0.25 * rng.standard_normal((4096, KVH, HD))).astype(np.float16).view(np.uint16)
+        vc = rng.standard_normal((4096, KVH, HD)).astype(np.float16).view(np.uint16)
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 10.0:
+            q, _, _ = orc.headprep(qkv, QH, KVH, HD, 128, inv, qw, kw, 1e-6, 4095)
+            orc.attn_linear(q, kc, vc, QH, KVH, HD, 4096)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        out["cpu_baseline"] = {"value": round(g["algorithmic_bytes"] / dt / 1e9, 3), "unit": "GB/s",
+                               "cores": _cpu_cores(), "kind": "port",
+                               "sample": f"{n} oracle global-layer attentions at 4096 positions (~10 s)"}
     return out
 
 
@@ -476,7 +553,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c3", "c3p", "c4", "prefill", "long"])
+    ap.add_argument("--workload", default="c4", choices=["c0", "c1", "c2", "c3", "c3p", "c4", "prefill", "long"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
@@ -489,7 +566,7 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
               "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
-    fn = {"c0": bench_c0, "c1": bench_c1, "c3": bench_c3, "c3p": bench_c3p, "c4": bench_c4,
+    fn = {"c0": bench_c0, "c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c3p": bench_c3p, "c4": bench_c4,
           "prefill": bench_prefill, "long": bench_long}[a.workload]
     steps = a.steps if a.steps is not None else {"c4": 240, "prefill": 10, "long": 64}.get(a.workload, 200)
     warmup = a.warmup if a.warmup is not None else {"c4": 16, "prefill": 2, "long": 8}.get(a.workload, 20)

@@ -606,7 +606,7 @@ int record_step(e4b_ctx* c) {
 // every layer as batched GEMMs on the matrix cores plus per-token kernels
 // (src/engine-a4b.js:465-563 encodeLayerPre / prefill, with the E4B layer
 // recipe of record_step).  Leaves the K/V rows of the chunk in the caches and,
-// in pf_xhl, the final-norm input of every token as an exact f16 hi/lo split.
+// in pf_xhl, the final-norm input of every token as an f16 hi/lo pair.
 int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
   const e4b_config& k = c->cfg;
   const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
@@ -682,7 +682,7 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
         (rc = gemm(q40_view(ly.down, H, FF), c->pf_gg, FF, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, ks_d)))
       return rc;
     // the last residual of the layer is followed by the next layer's input
-    // norm, or after the last layer by the final norm (as an exact hi/lo
+    // norm, or after the last layer by the final norm (as an f16 hi/lo
     // split for the lm-head)
     const bool lastl = l + 1 == Lc;
     const float* w_next = lastl ? c->out_norm : c->L[l + 1].attn_norm;

@@ -2,8 +2,10 @@
 // dequant, argmax and the f32 -> hi/lo f16 split for gfx950 (wave64).  The
 // q4_0 GEMV lives in q40_kernel.h.
 //
-// f32 activations are carried as an exact hi/lo f16 split (x = hi + lo), so a
-// v_dot2_f32_f16 product over both halves is as accurate as an f32 dot.
+// f32 activations are carried as an f16 pair hi = f16(x), lo = f16(x - hi)
+// whose sum is within max(2^-22 |x|, 2^-25) of x (22 of f32's 24 significant
+// bits; lo is subnormal below |x| = 2^-3); v_dot2_f32_f16 over both halves
+// then accumulates the products in f32.
 #include "../../include/e4b.h"
 #include "kernels.h"
 #include "util.h"

@@ -3,8 +3,8 @@
 // (src/engine-a4b.js:465-585 encodeLayerPre: "per-token math identical to
 // encodeLayer").  The GEMMs between them are k_gemm.hip.
 //
-//   k_embed_rows      token rows of the Q6_K table * sqrt(H), plus the exact
-//                     f16 hi/lo split for the PLE model projection
+//   k_embed_rows      token rows of the Q6_K table * sqrt(H), plus the
+//                     f16 hi/lo pair for the PLE model projection
 //                     (kernels/q6k.wgsl:37-73 per token)
 //   k_ple_prep_rows   per-layer inputs of every token (kernels/pleprep.wgsl:15-46)
 //   k_resnorm_rows    residual + RMSNorm, one workgroup per token
@@ -149,7 +149,8 @@ DEV void st_halves(uint16_t* p, const uint16_t (&v)[N]) {
 // one workgroup per token m:
 //   h = (h + rms(a) * w1) * scale, a = sum of na partial slices (a may be null)
 //   w2 != null: x = f16(rms(h) * w2), else x = f16(h); with xlo the value is
-//   stored as the exact split x = f16(y), xlo = f16(y - x) (the lm-head input)
+//   stored as the pair x = f16(y), xlo = f16(y - x), x + xlo within
+//   max(2^-22 |y|, 2^-25) of y (the lm-head input)
 // H = 256 PER; thread t owns elements [PER t, PER t + PER).  NAM = 0: no
 // residual input; else na <= NAM slices, all requested before the first use
 // (slice indices past na repeat the last one and are not added), summed in
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(64) void k_headprep_rows(const float* __restrict__ 
 // v_mfma_f32_16x16x32_f16 (lane l: A[l % 16][8 (l / 16) + t], B[8 (l / 16) +
 // t][l % 16], D[4 (l / 16) + r][l % 16]):
 //   S^T (16 keys x 16 queries) = K . Q^T over 8 steps of 32 dims; Q (f32) is
-//   an exact-sum f16 pair hi + lo, K is f16, so two MFMAs give q.k to ~2^-22.
+//   an f16 pair hi + lo (within max(2^-22 |q|, 2^-25) of q), K is f16, so two MFMAs give q.k to ~2^-22.
 //   After the online-softmax update each lane holds P^T for its query
 //   (column l % 16) and 8 keys: 4 (l / 16) + r of sub-tile 0 and 16 + 4 (l /
 //   16) + r of sub-tile 1 -- exactly a B operand of a 32-key MFMA when the A

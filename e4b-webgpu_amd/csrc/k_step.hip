@@ -16,8 +16,8 @@ constexpr int kMaxPer = 16;  // elements per thread in the one-block kernels (H 
 
 // Last residual of the step and the final norm: p = the sum of `np` partial
 // PLE projections (or the down projection when there is no PLE);
-// h = (h + rms(p) * w_post) * scale; xo = rms(h) * w_out stored as an exact
-// f16 hi/lo split for the lm-head (kernels/a4btail.wgsl:26-71 with the
+// h = (h + rms(p) * w_post) * scale; xo = rms(h) * w_out stored as an
+// f16 hi/lo pair for the lm-head (hi + lo within max(2^-22 |xo|, 2^-25) of xo) (kernels/a4btail.wgsl:26-71 with the
 // reference's f32 final norm, src/engine-a4b.js:688).
 template <int NP, int PER>
 __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float* __restrict__ p,
@@ -72,8 +72,8 @@ __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float
 }
 
 // token embedding: h = E[token] * sqrt(H) from the packed Q6_K lm-head planes
-// (kernels/q6k.wgsl:37-73 with the TOKSRC feedback folded in), plus the exact
-// hi/lo split of h for the PLE model projection.  The token is prompt[pos]
+// (kernels/q6k.wgsl:37-73 with the TOKSRC feedback folded in), plus the
+// f16 hi/lo pair of h for the PLE model projection.  The token is prompt[pos]
 // while pos < params[3], else params[1] (GPU-fed greedy decode).  Block 0 also
 // evaluates the step's RoPE table (cos, sin)(pos * inv_freq[p]) for local and
 // global layers, the same expression the attention kernel would evaluate.

@@ -70,7 +70,8 @@ int launch_ple_prep_rows(const float* proj, int64_t slice, const uint8_t* table,
                          const uint32_t* ids, int M, int L, float proj_scale, float* ple, float eps, hipStream_t st);
 // per token: h = (h + rms(sum of na slices of a) * w1) * scale (a may be
 // null); x = f16(rms(h) * w2) (w2 null: f16(h)); xlo (may be null) = the low
-// half of the exact f16 split of the same value
+// half of the f16 hi/lo pair of the same value (hi + lo within
+// max(2^-22 |y|, 2^-25) of y)
 int launch_resnorm_rows(int M, float* h, const float* a, int na, int64_t slice, const float* w1, float scale,
                         const float* w2, uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st);
 // y[m][i] = f16(gelu(sum of ks slices of part[m][i]) * mul[m mul_ld + i]), i < n

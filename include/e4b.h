@@ -41,8 +41,9 @@ extern "C" {
 /* activation dtypes for kernel-level entry points */
 #define E4B_DT_F32 0     /* f32[n]                                              */
 #define E4B_DT_F16 1     /* f16[n]                                              */
-#define E4B_DT_F32_HL 2  /* an f32 vector pre-split as f16 hi[n] then f16 lo[n], */
-                         /* x = hi + lo exactly (see e4b_split_f32)              */
+#define E4B_DT_F32_HL 2  /* an f32 vector pre-split as f16 hi[n] then f16 lo[n]   */
+                         /* (e4b_split_f32): hi + lo is within                   */
+                         /* max(2^-22 |x|, 2^-25) of x, |x| < 65520              */
 
 /* ---------------------------------------------------------------------------
  * Library / device plumbing (replaces src/gpu.js:4-50 initDevice, upload,
@@ -68,7 +69,10 @@ int   e4b_event_record(void* event, void* stream);
 int   e4b_event_elapsed_ms(void* start, void* end, float* ms); /* waits for end */
 int   e4b_event_destroy(void* event);
 
-/* f32 -> (hi, lo) f16 split on the device: hi = f16(x), lo = f16(x - hi). */
+/* f32 -> (hi, lo) f16 split on the device: hi = f16(x), lo = f16(x - hi) (both
+ * round to nearest even; x - hi is exact in f32).  |x - (hi + lo)| <=
+ * max(2^-22 |x|, 2^-25): 22 of f32's 24 significant bits, and lo is an f16
+ * subnormal (absolute step 2^-24) below |x| = 2^-3.  |x| must be < 65520. */
 int   e4b_split_f32(const float* x, int64_t n, void* hl_out, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -126,6 +126,36 @@ def test_tensor_bytes_matches_gguf_js():
         formats.tensor_bytes(_lib.GGML_Q4_0, [33])
 
 
+def _split_hl(x):
+    """The f32 -> f16 pair of e4b_split_f32 / k_tail / k_embed: hi = f16(x),
+    lo = f16(x - hi), both round-to-nearest-even (numpy's f32 -> f16 cast)."""
+    x = np.asarray(x, np.float32)
+    hi = x.astype(np.float16)
+    lo = (x - hi.astype(np.float32)).astype(np.float16)
+    return hi, lo
+
+
+def test_hilo_split_bound():
+    # the bound the header states: |x - (hi + lo)| <= max(2^-22 |x|, 2^-25);
+    # x - hi is exact in f32 (Sterbenz), so the error is lo's rounding alone
+    rng = np.random.default_rng(0)
+    xs = [rng.standard_normal(1_000_000).astype(np.float32)]
+    for mag in (1e-4, 1e-3, 1e-2):
+        xs.append((mag * rng.uniform(0.5, 2.0, 200_000) * rng.choice([-1, 1], 200_000)).astype(np.float32))
+    xs.append(np.float32([0.0, 2.0 ** -25, 2.0 ** -14, 0.125, 65504.0, -3.0e4]))
+    for x in xs:
+        hi, lo = _split_hl(x)
+        r = x.astype(np.float64) - hi.astype(np.float64)
+        assert np.array_equal(r, (x - hi.astype(np.float32)).astype(np.float64))  # exact residual
+        err = np.abs(x.astype(np.float64) - hi.astype(np.float64) - lo.astype(np.float64))
+        bound = np.maximum(2.0 ** -22 * np.abs(x.astype(np.float64)), 2.0 ** -25)
+        assert np.all(err <= bound), float(np.max(err / bound))
+    # the bound is attained in order of magnitude: the split is not exact
+    hi, lo = _split_hl(xs[0])
+    exact = np.mean(xs[0].astype(np.float64) == hi.astype(np.float64) + lo.astype(np.float64))
+    assert 0.4 < exact < 0.8, exact
+
+
 def test_rope_table_matches_oracle():
     from e4b.kernels import rope_inv_freq
     for theta in (1e4, 1e6):

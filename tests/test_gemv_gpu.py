@@ -71,6 +71,12 @@ def test_q40_gemv_prepared_split_matches_f32():
     from e4b._lib import DT_F32, DT_F32_HL, check, lib
     import ctypes as C
     check(lib.e4b_split_f32(C.c_void_p(xd.ptr), cols, C.c_void_p(hl.ptr), None), "split")
+    # the device split is bit-identical to hi = f16(x), lo = f16(x - hi) (RNE)
+    got = hl.download(np.uint16)
+    hi = x.astype(np.float16)
+    lo = (x - hi.astype(np.float32)).astype(np.float16)
+    np.testing.assert_array_equal(got[:cols], hi.view(np.uint16))
+    np.testing.assert_array_equal(got[cols:], lo.view(np.uint16))
     y1, y2 = DeviceBuffer(rows * 4), DeviceBuffer(rows * 4)
     M.gemv_dev(xd, DT_F32, y1)
     M.gemv_dev(hl, DT_F32_HL, y2)
