@@ -93,6 +93,12 @@ struct e4b_ctx {
            *pf_gp = nullptr;   // [2][cap][H], [cap][H], [cap][QH HD], [cap][FF], [cap][PD]
   float* pf_apart = nullptr;   // split-key attention partials (attn_prefill_part_bytes)
   size_t pf_apart_bytes = 0;
+  // per-dispatch profiling (e4b_profile_step / e4b_profile_prefill): while
+  // prof_on, every launch of a directly launched step or prefill chunk is
+  // followed by an event on the context stream, labelled by the kernel role
+  bool prof_on = false;
+  std::vector<hipEvent_t> prof_ev;       // event pool, grown on first use
+  std::vector<const char*> prof_label;   // label of the dispatch ending at event i (i >= 1)
 };
 
 namespace {
@@ -106,6 +112,21 @@ int dalloc(e4b_ctx* c, void** p, size_t bytes) {
 template <typename T>
 int dalloc_t(e4b_ctx* c, T** p, size_t count) {
   return dalloc(c, reinterpret_cast<void**>(p), count * sizeof(T));
+}
+
+// profiling mark after a launch (no-op unless a profile call is running;
+// never active during graph capture)
+int tick(e4b_ctx* c, const char* label) {
+  if (!c->prof_on) return E4B_OK;
+  const size_t i = c->prof_label.size();
+  if (i >= c->prof_ev.size()) {
+    hipEvent_t e;
+    E4B_HIP(hipEventCreate(&e));
+    c->prof_ev.push_back(e);
+  }
+  E4B_HIP(hipEventRecord(c->prof_ev[i], c->st));
+  c->prof_label.push_back(label);
+  return E4B_OK;
 }
 
 // pack `rows` q4_0 rows and place them at row offset `row_off` of a packed
@@ -472,15 +493,18 @@ int record_step(e4b_ctx* c) {
     return p;
   };
   if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, c->inv_local,
-                         c->inv_global, HD / 2, c->rope, st)))
+                         c->inv_global, HD / 2, c->rope, st)) ||
+      (rc = tick(c, "embed")))
     return rc;
   if (PD) {
     GemvOut po = {c->proj, nullptr, nullptr, 0};
     if ((rc = launch_q40(q40_view(c->ple_proj, (int64_t)Lc * PD, H), (const uint32_t*)c->h_hl,
-                         (const uint32_t*)(c->h_hl + H), EPI_F32, po, 1, st)))
+                         (const uint32_t*)(c->h_hl + H), EPI_F32, po, 1, st)) ||
+        (rc = tick(c, "ple_model_proj")))
       return rc;
     if ((rc = launch_ple_prep(c->proj, c->ple_tab, c->ple_norm, c->params, c->prompt, Lc, k.vocab,
-                              1.0f / sqrtf((float)H), c->ple, c->h, c->L[0].attn_norm, c->xn, H, k.eps, st)))
+                              1.0f / sqrtf((float)H), c->ple, c->h, c->L[0].attn_norm, c->xn, H, k.eps, st)) ||
+        (rc = tick(c, "ple_prep")))
       return rc;
   }
   for (int l = 0; l < Lc; ++l) {
@@ -504,7 +528,7 @@ int record_step(e4b_ctx* c) {
       rc = launch_q40(Wqkv, nullptr, nullptr, EPI_F32, oq, 1, st, &p);
       swap_h();
     }
-    if (rc) return rc;
+    if (rc || (rc = tick(c, "qkv"))) return rc;
     // 2. attention (head prep, KV write, split-K); the combine is the o
     //    projection's prologue when the projection has 2048 columns and the
     //    layer's live span fits the prologue's 64 chunks per head (global
@@ -535,8 +559,9 @@ int record_step(e4b_ctx* c) {
     a.eps = k.eps;
     a.kv_idx = 4;  // full layers: params[4] = the token's slot
     a.raw = ly.score ? c->raw : nullptr;
-    if ((rc = launch_attn(a, st))) return rc;
-    if (ly.score && (rc = launch_attn_score(c->part_ml, c->raw, c->params, 4, QH, ly.slots, c->chunk, ly.score, st)))
+    if ((rc = launch_attn(a, st)) || (rc = tick(c, ly.global ? "attn_global" : "attn_sliding"))) return rc;
+    if (ly.score && ((rc = launch_attn_score(c->part_ml, c->raw, c->params, 4, QH, ly.slots, c->chunk, ly.score, st)) ||
+                     (rc = tick(c, "attn_score"))))
       return rc;
     // 3. o projection
     GemvOut oo = {c->o, nullptr, nullptr, 0};
@@ -554,12 +579,13 @@ int record_step(e4b_ctx* c) {
     } else {
       rc = launch_q40(Wo, (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st);
     }
-    if (rc) return rc;
+    if (rc || (rc = tick(c, "o_proj"))) return rc;
     // 4. gate/up + GeGLU; prologue: post-attention residual + FFN input norm
     {
       const ProArgs p = pro(hnext, c->o, ly.post_attn, ly.ffn_norm, 1.0f);
       GemvOut og = {nullptr, c->gg, nullptr, FF};
-      if ((rc = launch_q40(q40_view(ly.gu, 2 * (int64_t)FF, H), nullptr, nullptr, EPI_GEGLU, og, 1, st, &p)))
+      if ((rc = launch_q40(q40_view(ly.gu, 2 * (int64_t)FF, H), nullptr, nullptr, EPI_GEGLU, og, 1, st, &p)) ||
+          (rc = tick(c, "gate_up_geglu")))
         return rc;
       swap_h();
     }
@@ -568,7 +594,8 @@ int record_step(e4b_ctx* c) {
     //    GeGLU-vector reads per workgroup; the PLE prologue adds the slices
     GemvOut od = {c->dn, nullptr, nullptr, 0};
     const int dks = (PD && (FF / 32) % 8 == 0) ? 2 : 1;
-    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, dks, st)))
+    if ((rc = launch_q40(q40_view(ly.down, H, FF), (const uint32_t*)c->gg, nullptr, EPI_F32, od, dks, st)) ||
+        (rc = tick(c, "down")))
       return rc;
     if (PD) {
       // 6. PLE branch in one launch: post-FFN residual prologue, gate x GELU x
@@ -584,7 +611,7 @@ int record_step(e4b_ctx* c) {
       pl.part = c->pp;
       pl.H = H;
       pl.PD = PD;
-      if ((rc = launch_ple(pl, p, st))) return rc;
+      if ((rc = launch_ple(pl, p, st)) || (rc = tick(c, "ple"))) return rc;
       swap_h();
     }
   }
@@ -594,12 +621,15 @@ int record_step(e4b_ctx* c) {
     rc = launch_tail(hcur, c->pp, PD / 32, last.post_norm, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
   else
     rc = launch_tail(hcur, c->dn, 1, last.post_ffw, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
-  if (rc) return rc;
+  if (rc || (rc = tick(c, "final_norm"))) return rc;
   c->h_final = hcur;
   if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
-                                   c->logits, nullptr, c->amax_part, st)))
+                                   c->logits, nullptr, c->amax_part, st)) ||
+      (rc = tick(c, "lm_head")))
     return rc;
-  return launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st);
+  if ((rc = launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st)))
+    return rc;
+  return tick(c, "argmax_feedback");
 }
 
 // One prefill chunk: tokens pf_ids[0..M) at positions p0 .. p0 + M - 1,
@@ -632,31 +662,39 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
     return launch_q40_gemm(g, st);
   };
   const Q6Mat E = q6_view(c->embd, k.vocab, H);
-  if ((rc = launch_embed_rows(E, c->pf_ids, M, sqrtf((float)H), c->pf_h, c->pf_xhl, st))) return rc;
+  if ((rc = launch_embed_rows(E, c->pf_ids, M, sqrtf((float)H), c->pf_h, c->pf_xhl, st)) ||
+      (rc = tick(c, "embed_rows")))
+    return rc;
   if (PD) {
     // PLE model projection of the f32 embedding as two f16 GEMMs (hi, lo)
     const Q40Mat Wpm = q40_view(c->ple_proj, NP, H);
     const int64_t slice = (int64_t)M * NP;
     if ((rc = gemm(Wpm, c->pf_xhl, H, GEMM_F32, c->pf_proj, nullptr, 0, nullptr, 0, 1)) ||
+        (rc = tick(c, "gemm_ple_model_proj")) ||
         (rc = gemm(Wpm, c->pf_xhl + MH, H, GEMM_F32, c->pf_proj + slice, nullptr, 0, nullptr, 0, 1)) ||
+        (rc = tick(c, "gemm_ple_model_proj")) ||
         (rc = launch_ple_prep_rows(c->pf_proj, slice, c->ple_tab, c->ple_norm, c->pf_ids, M, Lc,
-                                   1.0f / sqrtf((float)H), c->pf_ple, k.eps, st)))
+                                   1.0f / sqrtf((float)H), c->pf_ple, k.eps, st)) ||
+        (rc = tick(c, "ple_prep_rows")))
       return rc;
   }
   // layer 0 input norm
   if ((rc = launch_resnorm_rows(M, c->pf_h, nullptr, 0, 0, nullptr, 1.0f, c->L[0].attn_norm, c->pf_xn, nullptr, H,
-                                k.eps, st)))
+                                k.eps, st)) ||
+      (rc = tick(c, "resnorm_rows")))
     return rc;
   const int ks_o = q40_gemm_kslices(QH * HD / 32, kPfKsO), ks_d = q40_gemm_kslices(FF / 32, kPfKs);
   const int ks_qkv = q40_gemm_kslices(H / 32, kPfKsQkv), ks_pg = q40_gemm_kslices(H / 32, kPfKsPle);
   for (int l = 0; l < Lc; ++l) {
     const Layer& ly = c->L[l];
     // attention block
-    if ((rc = gemm(q40_view(ly.qkv, c->qkv_rows, H), c->pf_xn, H, GEMM_F32, c->pf_qkv, nullptr, 0, nullptr, 0, ks_qkv)))
+    if ((rc = gemm(q40_view(ly.qkv, c->qkv_rows, H), c->pf_xn, H, GEMM_F32, c->pf_qkv, nullptr, 0, nullptr, 0, ks_qkv)) ||
+        (rc = tick(c, "gemm_qkv")))
       return rc;
     if ((rc = launch_headprep_rows(c->pf_qkv, ks_qkv, (int64_t)M * c->qkv_rows, ly.q_norm, ly.k_norm, ly.global ? c->inv_global : c->inv_local,
                                    k.rope_angles, ly.kc, ly.vc, ly.slots, !ly.global, p0, M, c->pf_q, QH, KVH, k.eps,
-                                   st)))
+                                   st)) ||
+        (rc = tick(c, "headprep_rows")))
       return rc;
     PrefillAttnArgs pa;
     pa.q = c->pf_q;
@@ -671,15 +709,19 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
     pa.p0 = p0;
     pa.part = c->pf_apart;
     pa.part_bytes = c->pf_apart_bytes;
-    if ((rc = launch_attn_prefill(pa, st))) return rc;
+    if ((rc = launch_attn_prefill(pa, st)) || (rc = tick(c, "attn_prefill"))) return rc;
     if ((rc = gemm(q40_view(ly.o, H, (int64_t)QH * HD), c->pf_attn, QH * HD, GEMM_F32, c->pf_y, nullptr, 0, nullptr,
-                   0, ks_o)))
+                   0, ks_o)) ||
+        (rc = tick(c, "gemm_o")))
       return rc;
     // post-attention residual + FFN norm; gate/up + GeGLU; down
     if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_o, MH, ly.post_attn, 1.0f, ly.ffn_norm, c->pf_xn, nullptr,
                                   H, k.eps, st)) ||
+        (rc = tick(c, "resnorm_rows")) ||
         (rc = gemm(q40_view(ly.gu, 2 * (int64_t)FF, H), c->pf_xn, H, GEMM_GLU, nullptr, c->pf_gg, FF, nullptr, 0, 1)) ||
-        (rc = gemm(q40_view(ly.down, H, FF), c->pf_gg, FF, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, ks_d)))
+        (rc = tick(c, "gemm_gate_up_geglu")) ||
+        (rc = gemm(q40_view(ly.down, H, FF), c->pf_gg, FF, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, ks_d)) ||
+        (rc = tick(c, "gemm_down")))
       return rc;
     // the last residual of the layer is followed by the next layer's input
     // norm, or after the last layer by the final norm (as an f16 hi/lo
@@ -693,16 +735,22 @@ int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
       // projection; post-PLE residual and layer scalar
       if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_d, MH, ly.post_ffw, 1.0f, nullptr, c->pf_xn, nullptr, H,
                                     k.eps, st)) ||
+          (rc = tick(c, "resnorm_rows")) ||
           (rc = gemm(q40_view(ly.pg, PD, H), c->pf_xn, H, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, ks_pg)) ||
+          (rc = tick(c, "gemm_ple_gate")) ||
           (rc = launch_gelu_mul_rows(c->pf_y, ks_pg, (int64_t)M * PD, M, PD, c->pf_ple + (int64_t)l * PD, NP, c->pf_gp,
                                      st)) ||
+          (rc = tick(c, "gelu_mul_rows")) ||
           (rc = gemm(q40_view(ly.pp_rm, H, PD), c->pf_gp, PD, GEMM_F32, c->pf_y, nullptr, 0, nullptr, 0, 1)) ||
+          (rc = tick(c, "gemm_ple_proj")) ||
           (rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, 1, 0, ly.post_norm, ly.scale, w_next, x_next, xlo_next, H,
-                                    k.eps, st)))
+                                    k.eps, st)) ||
+          (rc = tick(c, "resnorm_rows")))
         return rc;
     } else {
       if ((rc = launch_resnorm_rows(M, c->pf_h, c->pf_y, ks_d, MH, ly.post_ffw, ly.scale, w_next, x_next, xlo_next, H,
-                                    k.eps, st)))
+                                    k.eps, st)) ||
+          (rc = tick(c, "resnorm_rows")))
         return rc;
     }
   }
@@ -801,15 +849,16 @@ extern "C" int e4b_step(e4b_ctx* c, uint32_t token, uint32_t pos, float* logits,
   return E4B_OK;
 }
 
-extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
-  int rc = ready(c, "e4b_prefill");
+static int prefill_common(e4b_ctx* c, const char* fn, const uint32_t* ids, uint32_t n, uint32_t* argmax_out,
+                          bool steps) {
+  int rc = ready(c, fn);
   if (rc) return rc;
-  if (!ids || n == 0) return e4b_fail(E4B_EINVAL, "e4b_prefill: empty prompt");
+  if (!ids || n == 0) return e4b_fail(E4B_EINVAL, "%s: empty prompt", fn);
   if (n > (uint32_t)c->max_prompt || n > (uint32_t)c->cfg.max_seq)
-    return e4b_fail(E4B_ERANGE, "e4b_prefill: %u tokens exceeds the prompt capacity %d", n, c->max_prompt);
+    return e4b_fail(E4B_ERANGE, "%s: %u tokens exceeds the prompt capacity %d", fn, n, c->max_prompt);
   for (uint32_t i = 0; i < n; ++i)
-    if (ids[i] >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "e4b_prefill: ids[%u] = %u >= vocab", i, ids[i]);
-  if (c->cfg.flags & E4B_FLAG_STEP_PREFILL) {
+    if (ids[i] >= (uint32_t)c->cfg.vocab) return e4b_fail(E4B_ERANGE, "%s: ids[%u] = %u >= vocab", fn, i, ids[i]);
+  if (steps) {
     E4B_HIP(hipMemcpyAsync(c->prompt, ids, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
     const uint32_t p[5] = {0u, 0u, 0u, n, 0u};
     if ((rc = put_params(c, p, 0, 5))) return rc;
@@ -827,6 +876,15 @@ extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t
   if ((rc = check_status(c))) return rc;
   if (argmax_out) *argmax_out = am[0];
   return E4B_OK;
+}
+
+extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
+  return prefill_common(c, "e4b_prefill", ids, n, argmax_out,
+                        c && (c->cfg.flags & E4B_FLAG_STEP_PREFILL) != 0);
+}
+
+extern "C" int e4b_prefill_steps(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
+  return prefill_common(c, "e4b_prefill_steps", ids, n, argmax_out, true);
 }
 
 static int decode_launch(e4b_ctx* c, uint32_t start_pos, uint32_t count) {
@@ -874,6 +932,83 @@ extern "C" int e4b_time_decode(e4b_ctx* c, uint32_t start_pos, uint32_t count, f
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   return rc ? rc : check_status(c);
+}
+
+// ---- per-dispatch profiles (profileStep / profilePrefill) -----------------------
+namespace {
+
+// run `body` with a mark before it and after each of its launches, then sum
+// the times between consecutive marks per label, labels in order of first use
+template <typename F>
+int profile_run(e4b_ctx* c, e4b_prof_entry* out, int cap, F body) {
+  if (cap < 0 || (cap > 0 && !out)) return e4b_fail(E4B_EINVAL, "profile: bad output array");
+  E4B_HIP(hipStreamSynchronize(c->st));
+  c->prof_label.clear();
+  c->prof_on = true;
+  int rc = tick(c, nullptr);
+  if (rc == E4B_OK) rc = body();
+  c->prof_on = false;
+  if (rc) return rc;
+  E4B_HIP(hipStreamSynchronize(c->st));
+  std::vector<std::string> names;
+  std::vector<double> us;
+  std::vector<int> cnt;
+  for (size_t i = 1; i < c->prof_label.size(); ++i) {
+    float ms = 0.f;
+    E4B_HIP(hipEventElapsedTime(&ms, c->prof_ev[i - 1], c->prof_ev[i]));
+    const std::string nm(c->prof_label[i]);
+    size_t j = 0;
+    while (j < names.size() && names[j] != nm) ++j;
+    if (j == names.size()) {
+      names.push_back(nm);
+      us.push_back(0.0);
+      cnt.push_back(0);
+    }
+    us[j] += 1000.0 * ms;
+    cnt[j] += 1;
+  }
+  for (size_t j = 0; j < names.size() && (int)j < cap; ++j) {
+    memset(out[j].name, 0, sizeof(out[j].name));
+    strncpy(out[j].name, names[j].c_str(), sizeof(out[j].name) - 1);
+    out[j].us = (float)us[j];
+    out[j].n = cnt[j];
+  }
+  return (int)names.size();
+}
+
+}  // namespace
+
+extern "C" int e4b_profile_step(e4b_ctx* c, uint32_t token, uint32_t pos, e4b_prof_entry* out, int cap) {
+  int rc = ready(c, "e4b_profile_step");
+  if (rc) return rc;
+  if (token >= (uint32_t)c->cfg.vocab)
+    return e4b_fail(E4B_ERANGE, "e4b_profile_step: token %u >= vocab %d", token, c->cfg.vocab);
+  if (pos >= 0x7fffffffu) return e4b_fail(E4B_ERANGE, "e4b_profile_step: pos %u >= 2^31 - 1", pos);
+  const uint32_t kv = pos == 0 ? 0u : c->kv_count;
+  if (kv >= (uint32_t)c->cfg.max_seq)
+    return e4b_fail(E4B_ERANGE, "e4b_profile_step: %u full-layer entries fill max_seq %d", kv, c->cfg.max_seq);
+  const uint32_t p[5] = {pos, token, 0u, 0u, kv};
+  if ((rc = put_params(c, p, 0, 5))) return rc;
+  const int n = profile_run(c, out, cap, [&]() { return record_step(c); });
+  if (n < 0) return n;
+  c->kv_count = kv + 1;
+  if ((rc = check_status(c))) return rc;
+  return n;
+}
+
+extern "C" int e4b_profile_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, e4b_prof_entry* out, int cap) {
+  int rc = ready(c, "e4b_profile_prefill");
+  if (rc) return rc;
+  if (!ids || n == 0) return e4b_fail(E4B_EINVAL, "e4b_profile_prefill: empty prompt");
+  const int M = (int)(n < (uint32_t)c->pf_cap ? n : (uint32_t)c->pf_cap);
+  for (int i = 0; i < M; ++i)
+    if (ids[i] >= (uint32_t)c->cfg.vocab)
+      return e4b_fail(E4B_ERANGE, "e4b_profile_prefill: ids[%d] = %u >= vocab", i, ids[i]);
+  E4B_HIP(hipMemcpyAsync(c->pf_ids, ids, (size_t)M * 4, hipMemcpyHostToDevice, c->st));
+  const int cnt = profile_run(c, out, cap, [&]() { return prefill_chunk(c, 0, M); });
+  if (cnt < 0) return cnt;
+  c->kv_count = (uint32_t)M;
+  return cnt;
 }
 
 extern "C" int e4b_argmax(e4b_ctx* c, uint32_t* token_out) {
@@ -1002,6 +1137,7 @@ extern "C" void e4b_destroy(e4b_ctx* c) {
   if (c->st) (void)hipStreamSynchronize(c->st);
   if (c->exec) (void)hipGraphExecDestroy(c->exec);
   if (c->graph) (void)hipGraphDestroy(c->graph);
+  for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
   for (void* p : c->allocs) (void)hipFree(p);
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;

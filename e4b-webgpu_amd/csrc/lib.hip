@@ -281,45 +281,63 @@ extern "C" int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc
   return launch_attn_prefill(a, (hipStream_t)stream);
 }
 
+// Argument checks and launch description shared by the two decode-attention
+// entry points; *part_bytes receives the size of the split-K partials
+// ([q_heads][chunks][head_dim] f32 outputs at offset 0, then the
+// [q_heads][chunks][2] (max, sum) pairs at *ml_off).
+static int attn_decode_prepare(const char* fn, const float* qkv, const float* q_norm, const float* k_norm,
+                               const float* inv_freq, int rope_angles, void* k_cache, void* v_cache, int q_heads,
+                               int kv_heads, int head_dim, int slots, int window, uint32_t pos, float eps, int chunk,
+                               void* out_f16, AttnLaunch* a, size_t* part_bytes, size_t* ml_off) {
+  if (!qkv || !q_norm || !k_norm || (rope_angles > 0 && !inv_freq) || !k_cache || !v_cache || !out_f16 ||
+      q_heads <= 0 || kv_heads <= 0 || slots <= 0 || window < 0 || rope_angles < 0 || rope_angles > head_dim / 2)
+    return e4b_fail(E4B_EINVAL, "%s: bad arguments", fn);
+  if (window == 0 && pos >= (uint32_t)slots)
+    return e4b_fail(E4B_ERANGE, "%s: position %u beyond the %d-position global cache", fn, pos, slots);
+  if (chunk == 0) chunk = 64;
+  if (chunk != 32 && chunk != 64) return e4b_fail(E4B_EINVAL, "%s: chunk %d is not 32 or 64", fn, chunk);
+  const int span = window > 0 ? window : slots;
+  const int nch = attn_chunks(span, chunk);
+  *ml_off = E4B_ALIGN256((size_t)q_heads * nch * head_dim * sizeof(float));
+  *part_bytes = *ml_off + (size_t)q_heads * nch * 2 * sizeof(float);
+  a->qkv = qkv;
+  a->qw = q_norm;
+  a->kw = k_norm;
+  a->inv_freq = inv_freq;
+  a->rope = nullptr;
+  a->kc = (uint16_t*)k_cache;
+  a->vc = (uint16_t*)v_cache;
+  a->params = nullptr;
+  a->pos = pos;
+  a->part_o = nullptr;
+  a->part_ml = nullptr;
+  a->out = (uint16_t*)out_f16;
+  a->qh = q_heads;
+  a->kvh = kv_heads;
+  a->hd = head_dim;
+  a->angles = rope_angles;
+  a->slots = slots;
+  a->window = window;
+  a->chunk = chunk;
+  a->combine = true;
+  a->eps = eps;
+  return E4B_OK;
+}
+
 extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const float* k_norm, const float* inv_freq,
                                  int rope_angles, void* k_cache, void* v_cache, int q_heads, int kv_heads,
                                  int head_dim, int slots, int window, uint32_t pos, float eps, int chunk,
                                  void* out_f16, void* stream) {
-  if (!qkv || !q_norm || !k_norm || (rope_angles > 0 && !inv_freq) || !k_cache || !v_cache || !out_f16 ||
-      q_heads <= 0 || kv_heads <= 0 || slots <= 0 || window < 0 || rope_angles < 0 || rope_angles > head_dim / 2)
-    return e4b_fail(E4B_EINVAL, "e4b_k_attn_decode: bad arguments");
-  if (window == 0 && pos >= (uint32_t)slots)
-    return e4b_fail(E4B_ERANGE, "e4b_k_attn_decode: position %u beyond the %d-position global cache", pos, slots);
-  if (chunk == 0) chunk = 64;
-  const int span = window > 0 ? window : slots;
-  const int nch = attn_chunks(span, chunk > 0 ? chunk : 64);
-  Workspace ws;
-  const size_t ob = E4B_ALIGN256((size_t)q_heads * nch * head_dim * sizeof(float));
-  const size_t mb = (size_t)q_heads * nch * 2 * sizeof(float);
-  int rc = e4b_workspace(ob + mb, &ws);
-  if (rc) return rc;
   AttnLaunch a;
-  a.qkv = qkv;
-  a.qw = q_norm;
-  a.kw = k_norm;
-  a.inv_freq = inv_freq;
-  a.rope = nullptr;
-  a.kc = (uint16_t*)k_cache;
-  a.vc = (uint16_t*)v_cache;
-  a.params = nullptr;
-  a.pos = pos;
+  size_t need = 0, ml_off = 0;
+  int rc = attn_decode_prepare("e4b_k_attn_decode", qkv, q_norm, k_norm, inv_freq, rope_angles, k_cache, v_cache,
+                               q_heads, kv_heads, head_dim, slots, window, pos, eps, chunk, out_f16, &a, &need,
+                               &ml_off);
+  if (rc) return rc;
+  Workspace ws;
+  if ((rc = e4b_workspace(need, &ws))) return rc;
   a.part_o = (float*)ws.buf;
-  a.part_ml = (float*)(ws.buf + ob);
-  a.out = (uint16_t*)out_f16;
-  a.qh = q_heads;
-  a.kvh = kv_heads;
-  a.hd = head_dim;
-  a.angles = rope_angles;
-  a.slots = slots;
-  a.window = window;
-  a.chunk = chunk;
-  a.combine = true;
-  a.eps = eps;
+  a.part_ml = (float*)(ws.buf + ml_off);
   return launch_attn(a, (hipStream_t)stream);
 }
 

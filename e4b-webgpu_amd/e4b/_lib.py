@@ -97,6 +97,9 @@ SIGNATURES = [
     ("e4b_finalize", _i32, [_vp]),
     ("e4b_step", _i32, [_vp, _u32, _u32, _vp, _vp]),
     ("e4b_prefill", _i32, [_vp, _vp, _u32, _vp]),
+    ("e4b_prefill_steps", _i32, [_vp, _vp, _u32, _vp]),
+    ("e4b_profile_step", _i32, [_vp, _u32, _u32, _vp, _i32]),
+    ("e4b_profile_prefill", _i32, [_vp, _vp, _u32, _vp, _i32]),
     ("e4b_decode", _i32, [_vp, _u32, _u32, _vp]),
     ("e4b_argmax", _i32, [_vp, _vp]),
     ("e4b_read_hidden", _i32, [_vp, _vp]),
@@ -125,6 +128,12 @@ class ConfigC(C.Structure):
         ("rope_angles", _i32), ("theta_local", _f32), ("theta_global", _f32), ("eps", _f32), ("softcap", _f32),
         ("layer_global", _vp), ("attn_chunk", _i32), ("max_prompt", _i32), ("flags", _u32),
     ]
+
+
+class ProfEntryC(C.Structure):
+    """struct e4b_prof_entry (include/e4b.h)."""
+
+    _fields_ = [("name", C.c_char * 40), ("us", _f32), ("n", _i32)]
 
 
 FLAG_NO_GRAPH = 1

@@ -2,7 +2,10 @@
 
 Mirrors the object returned by loadEngineA4B (src/engine-a4b.js:854-856):
 ``step(token, pos)``, ``argmax_fast()``, ``decode_chunk(start_pos, count)``,
-``generate_fast(ids, max_new, eos)``, ``prefill(ids)``, ``read_hidden()``.
+``generate_fast(ids, max_new, eos)``, ``prefill(ids)``,
+``generate_prefill(ids, max_new, eos)``, ``profile_step(token, pos)``,
+``profile_prefill(ids)``, ``compact()``, ``generate_long(...)``,
+``read_hidden()``.
 The compute runs in libe4b.so (HIP, gfx950); this module only moves tensors
 and calls the C ABI.
 """
@@ -12,7 +15,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import ConfigC, check, lib
+from ._lib import ConfigC, ProfEntryC, check, lib
 from .gguf import open_gguf
 from .model import E4BConfig, Tensor
 
@@ -169,15 +172,31 @@ class Engine:
         check(lib.e4b_decode(self.ctx, int(start_pos), int(count), _p(out)), "e4b_decode")
         return out
 
+    def prefill_steps(self, ids) -> int:
+        """The prompt token by token through the decode step (generateFast's
+        prompt loop, src/engine-a4b.js:826-829), GPU-side between tokens."""
+        ids = np.ascontiguousarray(np.asarray(ids, np.uint32))
+        am = C.c_uint32(0)
+        check(lib.e4b_prefill_steps(self.ctx, _p(ids), ids.size, C.byref(am)), "e4b_prefill_steps")
+        return int(am.value)
+
     def generate_fast(self, ids, max_new: int, eos=(106, 1)) -> list:
-        """src/engine-a4b.js:826-848: prompt, then GPU-fed chunks of <= 8 with
-        an EOS check after each chunk readback."""
+        """generateFast (src/engine-a4b.js:826-848): the prompt through the
+        decode step token by token, then GPU-fed chunks of <= 8 with an EOS
+        check after each chunk readback."""
+        return self._generate(self.prefill_steps(ids), len(ids), max_new, eos)
+
+    def generate_prefill(self, ids, max_new: int, eos=(106, 1)) -> list:
+        """generatePrefill (src/engine-a4b.js:659-681): the batched prefill,
+        then the same GPU-fed decode loop as generate_fast."""
+        return self._generate(self.prefill(ids), len(ids), max_new, eos)
+
+    def _generate(self, g0: int, n_prompt: int, max_new: int, eos) -> list:
         eos = set(eos)
-        g0 = self.prefill(ids)
         out = [g0]
         if g0 in eos:
             return out
-        pos, done = len(ids), 1
+        pos, done = n_prompt, 1
         while done < max_new:
             n = min(8, max_new - done)
             toks = self.decode_chunk(pos, n)
@@ -192,6 +211,24 @@ class Engine:
             if stop:
                 break
         return out[:max_new]
+
+    # ---- per-dispatch profiles (src/engine-a4b.js:707-779) ---------------------
+    def _profile(self, fn, *args) -> dict:
+        out = (ProfEntryC * 64)()
+        n = check(fn(self.ctx, *args, out, 64), fn.__name__)
+        return {out[i].name.decode(): {"us": float(out[i].us), "n": int(out[i].n)} for i in range(min(n, 64))}
+
+    def profile_step(self, token: int, pos: int) -> dict:
+        """profileStep: one step with a timed span per dispatch, summed per
+        kernel role -> {role: {"us", "n"}} (ranking only).  Runs a real step."""
+        return self._profile(lib.e4b_profile_step, int(token), int(pos))
+
+    def profile_prefill(self, ids) -> dict:
+        """profilePrefill: one batched-prefill chunk (the first <= 512 tokens)
+        with a timed span per dispatch, summed per role.  Leaves the caches
+        holding the chunk; prefill again before decoding."""
+        ids = np.ascontiguousarray(np.asarray(ids, np.uint32))
+        return self._profile(lib.e4b_profile_prefill, _p(ids), ids.size)
 
     # ---- full-layer KV budget (src/engine-a4b.js:587-657) ------------------------
     def kv_count(self) -> int:

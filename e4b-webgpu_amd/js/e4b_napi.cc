@@ -287,26 +287,86 @@ napi_value step(napi_env env, napi_callback_info info) {
   return out;
 }
 
-// prefill(ctx, Uint32Array ids) -> argmax
-napi_value prefill(napi_env env, napi_callback_info info) {
+// a Uint32Array argument as (data, length)
+bool get_u32s(napi_env env, napi_value v, const uint32_t** data, size_t* n) {
+  napi_typedarray_type t;
+  size_t off = 0;
+  void* d = nullptr;
+  napi_value ab;
+  bool is = false;
+  if (napi_is_typedarray(env, v, &is) != napi_ok || !is ||
+      napi_get_typedarray_info(env, v, &t, n, &d, &ab, &off) != napi_ok || t != napi_uint32_array)
+    return false;
+  *data = (const uint32_t*)d;
+  return true;
+}
+
+// prefill(ctx, Uint32Array ids) -> argmax: the batched prefill;
+// prefillSteps(ctx, Uint32Array ids) -> argmax: token by token through the step
+napi_value prefill_impl(napi_env env, napi_callback_info info, bool steps) {
   napi_value argv[2];
   get_args(env, info, 2, argv);
   Ctx* x = ctx_of(env, argv[0]);
   if (!x) return throw_msg(env, "prefill: not an engine context");
-  napi_typedarray_type t;
-  size_t n = 0, off = 0;
-  void* d = nullptr;
-  napi_value ab;
-  bool is = false;
-  if (napi_is_typedarray(env, argv[1], &is) != napi_ok || !is ||
-      napi_get_typedarray_info(env, argv[1], &t, &n, &d, &ab, &off) != napi_ok || t != napi_uint32_array)
-    return throw_msg(env, "prefill(ctx, Uint32Array ids)");
+  const uint32_t* d = nullptr;
+  size_t n = 0;
+  if (!get_u32s(env, argv[1], &d, &n)) return throw_msg(env, "prefill(ctx, Uint32Array ids)");
   uint32_t am = 0;
-  const int rc = e4b_prefill(x->c, (const uint32_t*)d, (uint32_t)n, &am);
-  if (rc) return throw_lib(env, "prefill", rc);
+  const int rc = steps ? e4b_prefill_steps(x->c, d, (uint32_t)n, &am) : e4b_prefill(x->c, d, (uint32_t)n, &am);
+  if (rc) return throw_lib(env, steps ? "prefillSteps" : "prefill", rc);
   napi_value v;
   CHECK_NAPI(napi_create_uint32(env, am, &v));
   return v;
+}
+napi_value prefill(napi_env env, napi_callback_info info) { return prefill_impl(env, info, false); }
+napi_value prefill_steps(napi_env env, napi_callback_info info) { return prefill_impl(env, info, true); }
+
+// the library's per-role profile entries as [{name, us, n}, ...]
+napi_value prof_array(napi_env env, const e4b_prof_entry* e, int n) {
+  napi_value arr;
+  CHECK_NAPI(napi_create_array_with_length(env, (size_t)n, &arr));
+  for (int i = 0; i < n; ++i) {
+    napi_value o, nm, us, cnt;
+    CHECK_NAPI(napi_create_object(env, &o));
+    CHECK_NAPI(napi_create_string_utf8(env, e[i].name, NAPI_AUTO_LENGTH, &nm));
+    CHECK_NAPI(napi_create_double(env, (double)e[i].us, &us));
+    CHECK_NAPI(napi_create_int32(env, e[i].n, &cnt));
+    CHECK_NAPI(napi_set_named_property(env, o, "name", nm));
+    CHECK_NAPI(napi_set_named_property(env, o, "us", us));
+    CHECK_NAPI(napi_set_named_property(env, o, "n", cnt));
+    CHECK_NAPI(napi_set_element(env, arr, (uint32_t)i, o));
+  }
+  return arr;
+}
+
+// profileStep(ctx, token, pos) -> [{name, us, n}]
+napi_value profile_step(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  get_args(env, info, 3, argv);
+  Ctx* x = ctx_of(env, argv[0]);
+  if (!x) return throw_msg(env, "profileStep: not an engine context");
+  int64_t tok = 0, pos = 0;
+  if (!get_i64(env, argv[1], &tok) || !get_i64(env, argv[2], &pos) || tok < 0 || pos < 0)
+    return throw_msg(env, "profileStep(ctx, token, pos)");
+  e4b_prof_entry e[64];
+  const int n = e4b_profile_step(x->c, (uint32_t)tok, (uint32_t)pos, e, 64);
+  if (n < 0) return throw_lib(env, "profileStep", n);
+  return prof_array(env, e, n < 64 ? n : 64);
+}
+
+// profilePrefill(ctx, Uint32Array ids) -> [{name, us, n}]
+napi_value profile_prefill(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  Ctx* x = ctx_of(env, argv[0]);
+  if (!x) return throw_msg(env, "profilePrefill: not an engine context");
+  const uint32_t* d = nullptr;
+  size_t len = 0;
+  if (!get_u32s(env, argv[1], &d, &len)) return throw_msg(env, "profilePrefill(ctx, Uint32Array ids)");
+  e4b_prof_entry e[64];
+  const int n = e4b_profile_prefill(x->c, d, (uint32_t)len, e, 64);
+  if (n < 0) return throw_lib(env, "profilePrefill", n);
+  return prof_array(env, e, n < 64 ? n : 64);
 }
 
 // decode(ctx, startPos, count) -> Uint32Array tokens
@@ -439,6 +499,9 @@ napi_value init(napi_env env, napi_value exports) {
       {"finalize", nullptr, finalize, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"step", nullptr, step, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"prefill", nullptr, prefill, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"prefillSteps", nullptr, prefill_steps, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"profileStep", nullptr, profile_step, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"profilePrefill", nullptr, profile_prefill, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"decode", nullptr, decode, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"argmax", nullptr, argmax, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"readHidden", nullptr, read_hidden, nullptr, nullptr, nullptr, kMethod, nullptr},

@@ -4,7 +4,8 @@
 // object with the surface of the one loadEngineA4B returns
 // (src/engine-a4b.js:854-856): step(token, pos), argmaxFast(),
 // decodeChunk(startPos, count, ringBase), generateFast(ids, maxNew, eosIds),
-// prefill(ids), readHidden(); the long-context pair compactAll() and
+// prefill(ids), generatePrefill(ids, maxNew, eosIds), profileStep(token,
+// pos), profilePrefill(ids), readHidden(); the long-context pair compactAll() and
 // generateLong(ids, maxNew, eosIds) (src/engine-a4b.js:587-657, with
 // FLAG_KV_SCORE); plus readLogits(), kvCount(), reset() and close().
 //
@@ -77,13 +78,31 @@ async function loadEngine(file, overrides = {}) {
   async function prefill(inputIds) {
     return addon.prefill(ctx, Uint32Array.from(inputIds));
   }
-  // src/engine-a4b.js:826-848: prompt, then GPU-fed chunks of <= 8 tokens
-  // with an EOS check after each chunk's readback
+  // src/engine-a4b.js:826-848: the prompt through the decode step token by
+  // token, then GPU-fed chunks of <= 8 tokens with an EOS check after each
+  // chunk's readback
   async function generateFast(inputIds, maxNew, eosIds = new Set([106, 1])) {
-    const g0 = await prefill(inputIds);
+    return decodeLoop(addon.prefillSteps(ctx, Uint32Array.from(inputIds)), inputIds.length, maxNew, eosIds);
+  }
+  // src/engine-a4b.js:659-681: the batched prefill, then the same loop
+  async function generatePrefill(inputIds, maxNew, eosIds = new Set([106, 1])) {
+    return decodeLoop(await prefill(inputIds), inputIds.length, maxNew, eosIds);
+  }
+  // per-dispatch GPU budget, summed per kernel role (ranking only):
+  // profileStep (src/engine-a4b.js:707-741) runs a real step,
+  // profilePrefill (:743-779) one batched-prefill chunk of the first <= 512
+  // tokens; both return a Map role -> {us, n} as the reference does
+  const toMap = (arr) => new Map(arr.map((e) => [e.name, { us: e.us, n: e.n }]));
+  async function profileStep(token, pos) {
+    return toMap(addon.profileStep(ctx, token, pos));
+  }
+  async function profilePrefill(inputIds) {
+    return toMap(addon.profilePrefill(ctx, Uint32Array.from(inputIds)));
+  }
+  function decodeLoop(g0, nPrompt, maxNew, eosIds) {
     const out = [g0];
     if (eosIds.has(g0)) return out;
-    let pos = inputIds.length, done = 1;
+    let pos = nPrompt, done = 1;
     while (done < maxNew) {
       const n = Math.min(8, maxNew - done);
       const toks = decodeChunk(pos, n, done - 1);
@@ -142,8 +161,8 @@ async function loadEngine(file, overrides = {}) {
   function reset() { addon.reset(ctx); }
   function close() { addon.destroy(ctx); }
 
-  return { C, step, argmaxFast, decodeChunk, generateFast, prefill, compactAll, generateLong, kvCount, readHidden,
-           readLogits, reset, close, tokRing };
+  return { C, step, argmaxFast, decodeChunk, generateFast, prefill, generatePrefill, profileStep, profilePrefill,
+           compactAll, generateLong, kvCount, readHidden, readLogits, reset, close, tokRing };
 }
 
 module.exports = { loadEngine, configFromKV, addon, FLAG_NO_GRAPH, FLAG_STEP_PREFILL, FLAG_KV_SCORE, KV_BUDGET,

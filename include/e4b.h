@@ -317,6 +317,11 @@ int  e4b_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, float* logits_or_null,
  * e4b_decode input.  E4B_FLAG_STEP_PREFILL runs the prompt through the decode
  * step instead. */
 int  e4b_prefill(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* argmax_out);
+/* the prompt token by token through the decode step (the prompt loop of
+ * generateFast, src/engine-a4b.js:826-829: step(t, pos) per prompt token,
+ * then argmaxFast), with no host round trip between tokens; the same state
+ * and result as e4b_prefill under E4B_FLAG_STEP_PREFILL */
+int  e4b_prefill_steps(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* argmax_out);
 /* GPU-fed greedy decode of `count` tokens starting at start_pos, fed with the
  * previous step's argmax; tokens_out[count] */
 int  e4b_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, uint32_t* tokens_out);
@@ -329,6 +334,25 @@ int  e4b_reset(e4b_ctx* ctx);                           /* zero KV caches and st
 void e4b_destroy(e4b_ctx* ctx);
 /* timing: run `count` GPU-fed steps and return the elapsed device ms */
 int  e4b_time_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, float* ms_out);
+
+/* Per-dispatch GPU time of one step or one prefill chunk, summed per kernel
+ * role (profileStep, src/engine-a4b.js:707-741, and profilePrefill,
+ * :743-779: one timed pass per dispatch, for ranking).  The step's kernels
+ * (or the first min(n, 512) prompt tokens' prefill chunk, without its
+ * lm-head) are launched directly with a HIP event after each; an entry's time
+ * is the span between the events around its launches.  Writes up to `cap`
+ * entries in order of first launch and returns the number of roles, or a
+ * negative error.  Both run a real step / chunk: e4b_profile_step is
+ * e4b_step(token, pos); e4b_profile_prefill leaves the caches holding the
+ * chunk's rows and the full layers' count at the chunk's length (decode
+ * from a fresh e4b_prefill). */
+typedef struct e4b_prof_entry {
+  char name[40];  /* kernel role, e.g. "gate_up_geglu", "attn_sliding", "gemm_qkv" */
+  float us;       /* summed microseconds */
+  int32_t n;      /* dispatches */
+} e4b_prof_entry;
+int  e4b_profile_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, e4b_prof_entry* out, int cap);
+int  e4b_profile_prefill(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, e4b_prof_entry* out, int cap);
 
 /* Full-layer KV budget.  Full (global) layers count their cache entries
  * apart from positions (kvCount, src/engine-a4b.js:217; CACHEMODE 2): the

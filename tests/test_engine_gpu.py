@@ -137,6 +137,49 @@ def test_generate_fast_matches_step_loop():
     assert gen == ref
 
 
+def test_generate_prefill_and_profiles():
+    # generatePrefill (batched prefill + GPU-fed decode) and generateFast
+    # (prompt through the step) against the oracle's chain fed with the GPU's
+    # tokens; profileStep / profilePrefill time every kernel role
+    cfg = tiny_config(layers=3, layer_global=[0, 0, 1])
+    eng, om = build(cfg, 21)
+    prompt = [int(x) for x in np.random.default_rng(21).integers(0, cfg.vocab, 12)]
+    gp = eng.generate_prefill(prompt, 12, eos=())
+    lg_p = eng.read_logits()
+    eng.reset()
+    gf = eng.generate_fast(prompt, 12, eos=())
+    for i, t in enumerate(prompt):
+        o_tok, o_lg, _ = om.step(t, i, want_logits=True)
+    ties = []
+    for k in range(len(gp)):
+        if gp[k] != o_tok:
+            assert top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max(), (k, gp[k], o_tok)
+            ties.append(k)
+        if k + 1 < len(gp):
+            o_tok, o_lg, _ = om.step(gp[k], len(prompt) + k, want_logits=True)
+    err = float(np.abs(lg_p - o_lg).max() / np.abs(o_lg).max())
+    print(f"generate_prefill {gp}, generate_fast {gf}, near-ties {ties}, logits err {err:.2e}")
+    assert err < LOGIT_TOL
+    assert gf == gp or ties
+    eng.reset()
+    ps = eng.profile_step(prompt[0], 0)
+    for role, n in (("embed", 1), ("ple_model_proj", 1), ("ple_prep", 1), ("qkv", 3), ("attn_sliding", 2),
+                    ("attn_global", 1), ("o_proj", 3), ("gate_up_geglu", 3), ("down", 3), ("ple", 3),
+                    ("final_norm", 1), ("lm_head", 1), ("argmax_feedback", 1)):
+        assert ps[role]["n"] == n and ps[role]["us"] > 0, (role, ps.get(role))
+    # the profiled step is a real step: its argmax is the oracle's at position 0
+    om.reset()
+    o0, o_lg0, _ = om.step(prompt[0], 0, want_logits=True)
+    assert eng.argmax_fast() == o0 or top2_margin(o_lg0) < TIE_TOL * np.abs(o_lg0).max()
+    pp = eng.profile_prefill(prompt)
+    for role in ("embed_rows", "gemm_ple_model_proj", "ple_prep_rows", "gemm_qkv", "headprep_rows", "attn_prefill",
+                 "gemm_o", "gemm_gate_up_geglu", "gemm_down", "gemm_ple_gate", "gelu_mul_rows", "gemm_ple_proj",
+                 "resnorm_rows"):
+        assert pp[role]["us"] > 0, role
+    assert pp["gemm_qkv"]["n"] == 3 and pp["resnorm_rows"]["n"] == 1 + 3 * 3
+    print("profile_step:", {k: round(v["us"], 1) for k, v in ps.items()})
+
+
 def test_c4_width_five_layers():
     cfg = E4BConfig(layers=5, max_seq=256, layer_global=[0, 0, 0, 0, 1])
     eng, om = build(cfg, 3)

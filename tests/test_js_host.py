@@ -45,8 +45,9 @@ def _write_model(path, cfg, seed):
 def test_addon_exports_engine_surface():
     out = _node("const a = require('./e4b_napi.node'); console.log(JSON.stringify(Object.keys(a).sort()), a.version())")
     keys = json.loads(out.split()[0])
-    for k in ("create", "setTensor", "finalize", "step", "prefill", "decode", "argmax", "readHidden", "readLogits",
-              "kvCount", "readScores", "kvCompact", "reset", "destroy", "lastError", "deviceCount", "version"):
+    for k in ("create", "setTensor", "finalize", "step", "prefill", "prefillSteps", "decode", "argmax", "readHidden",
+              "readLogits", "kvCount", "readScores", "kvCompact", "profileStep", "profilePrefill", "reset", "destroy",
+              "lastError", "deviceCount", "version"):
         assert k in keys
     assert "gfx950" in out
 
@@ -114,6 +115,52 @@ def test_js_host_matches_python_host(tmp_path):
 
 @_needs_node
 @pytest.mark.gpu
+def test_js_host_oracle_lockstep(tmp_path):
+    # the JS host against the CPU oracle directly: generateFast's tokens are
+    # replayed through orc_step (each oracle step fed the JS host's previous
+    # token), every token equal to the oracle's argmax unless the oracle's
+    # top-2 margin is a near-tie, final logits within 1e-3 of their range;
+    # generatePrefill (batched prefill) yields the same tokens; both profiles
+    # name the step's and the prefill chunk's kernel roles
+    import oracle as orc
+    from tests.util import top2_margin
+    cfg = tiny_config(layers=3, layer_global=[0, 0, 1])
+    path = tmp_path / "lock.gguf"
+    tensors = _write_model(path, cfg, 47)
+    prompt = [int(x) for x in np.random.default_rng(47).integers(0, cfg.vocab, 10)]
+    over = {"ring": cfg.ring, "maxSeq": cfg.max_seq}
+    lg_path = tmp_path / "logits.f32"
+    env = dict(os.environ, E4B_LOGITS_OUT=str(lg_path))
+    r = subprocess.run([NODE, os.path.join(JS, "run_greedy.js"), str(path), ",".join(map(str, prompt)), "20",
+                        json.dumps(over)], check=True, capture_output=True, text=True, timeout=300, env=env)
+    js = json.loads(r.stdout.strip().splitlines()[-1])
+    toks = js["generate"]
+    om = orc.OracleModel(cfg.as_dict(), {n: t.data for n, t in tensors.items()})
+    for i, t in enumerate(prompt):
+        o_tok, o_lg, _ = om.step(t, i, want_logits=True)
+    ties = []
+    for k in range(len(toks)):
+        if toks[k] != o_tok:
+            assert top2_margin(o_lg) < 2e-3 * np.abs(o_lg).max(), f"token {k}: js {toks[k]} vs oracle {o_tok}"
+            ties.append(k)
+        if k + 1 < len(toks):
+            o_tok, o_lg, _ = om.step(toks[k], len(prompt) + k, want_logits=True)
+    js_lg = np.fromfile(lg_path, np.float32)
+    err = float(np.abs(js_lg - o_lg).max() / np.abs(o_lg).max())
+    print(f"js host vs oracle: {len(toks)} tokens compared, near-ties {ties}, final logits err {err:.2e}")
+    assert err < 1e-3
+    assert js["generate_prefill"] == toks or ties
+    for key, want in (("profile_step", ("embed", "qkv", "attn_sliding", "attn_global", "o_proj", "gate_up_geglu",
+                                          "down", "ple", "lm_head")),
+                      ("profile_prefill", ("embed_rows", "gemm_qkv", "attn_prefill", "gemm_gate_up_geglu"))):
+        roles = {name: (n, pos) for name, n, pos in js[key]}
+        for role in want:
+            assert role in roles and roles[role][1], (key, role)
+    assert dict((n, c) for n, c, _ in js["profile_step"])["qkv"] == cfg.layers
+
+
+@_needs_node
+@pytest.mark.gpu
 def test_js_generate_long_matches_python_host(tmp_path):
     # generateLong (src/engine-a4b.js:620-657) on both hosts with a small
     # budget: probe step, compaction and recompactions take the same path
@@ -131,6 +178,24 @@ def test_js_generate_long_matches_python_host(tmp_path):
     out = eng.generate_long(prompt, 40, eos=(), **opts)
     assert js["generate_long"] == out
     assert js["kv_count"] == eng.kv_count() <= opts["decap"]
+
+
+@pytest.mark.gpu
+def test_native_gguf_engine_oracle_lockstep(tmp_path):
+    # an engine loaded through the library's own GGUF loader (e4b_load_gguf)
+    # against the CPU oracle built from the same file's tensors
+    import oracle as orc
+    from tests.test_engine_gpu import lockstep
+    cfg = tiny_config(layers=3, layer_global=[0, 1, 0])
+    path = tmp_path / "native.gguf"
+    tensors = _write_model(path, cfg, 57)
+    eng = Engine.load_native(str(path), ring=cfg.ring, max_seq=cfg.max_seq)
+    om = orc.OracleModel(cfg.as_dict(), {n: t.data for n, t in tensors.items()})
+    prompt = np.random.default_rng(57).integers(0, cfg.vocab, 11)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 16)
+    err = float(np.abs(eng.read_logits() - o_lg).max() / np.abs(o_lg).max())
+    print(f"native gguf engine vs oracle: near-ties {ties}, logits err {err:.2e}")
+    assert not ties and err < 1e-3
 
 
 @pytest.mark.gpu
