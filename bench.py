@@ -46,6 +46,13 @@ MALL_BYTES = 256 << 20
 # on a 256 MiB copy kernel: x2.000 and x1.000); commands and raw values in
 # profiles/geglu_dominant_traffic.md.  Re-measure when the kernel changes.
 GEGLU_TRAFFIC_BYTES = int(18633.0 * 1024 * 2.0 + 40.0 * 1024 * 1.0)
+# The same two counter runs for the other configs' timed kernels (per launch
+# or per layer; commands and raw values in profiles/gemv_c0.md,
+# profiles/lmhead_c1.md, profiles/attn_c2.md and profiles/moe_c3.md).
+C0_TRAFFIC_BYTES = int(9283.5 * 1024 * 2.0 + 64.0 * 1024)
+C1_TRAFFIC_BYTES = int(215623.7 * 1024 * 2.0 + 1088.6 * 1024)
+C2_GLOBAL_TRAFFIC_BYTES = int((4214.8 + 277.0) * 1024 * 2.0 + (530.0 + 4.0) * 1024)
+C3_TRAFFIC_BYTES = int(19183.2 * 1024 * 2.0 + 79.3 * 1024)
 
 
 def _cpu_cores() -> int:
@@ -88,7 +95,7 @@ def bench_c0(steps: int, warmup: int, cpu: bool) -> dict:
         "ms_per_step": ms, "dtype": "q4_0 x f32 (f32 accumulate)",
         "config": {"workload": "c0: q4_0 GEMV 16384x2048, x f32", "weight_copies_rotated": ncopy},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C0_TRAFFIC_BYTES,
                      "kernel": "k_q40_gemv", "algorithmic_bytes_per_launch": algo},
     }
     if cpu:
@@ -132,7 +139,7 @@ def bench_c1(steps: int, warmup: int, cpu: bool) -> dict:
         "ms_per_step": ms, "dtype": "q6_K x f32 (f32 accumulate)",
         "config": {"workload": "c1: Q6_K lm-head 262144x2048 + softcap 30 + argmax"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C1_TRAFFIC_BYTES,
                      "kernel": "k_q6k_gemv_argmax", "algorithmic_bytes_per_launch": algo},
     }
     if cpu:
@@ -201,7 +208,7 @@ def bench_c2(steps: int, warmup: int, cpu: bool) -> dict:
                                "positions (theta 1e6), sliding window 512 / ring 1024 (theta 1e4)",
                    "cases": res},
         "roofline": {"bound": "hbm", "achieved": g["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": C2_GLOBAL_TRAFFIC_BYTES,
                      "kernel": "k_attn_split + k_attn_combine (global layer, pos 4095)",
                      "algorithmic_bytes_per_launch": g["algorithmic_bytes"]},
     }
@@ -265,7 +272,7 @@ def bench_c3(steps: int, warmup: int, cpu: bool) -> dict:
         "config": {"workload": "c3: A4B-style MoE half-layer, hidden 2816, 128 experts top-8, expert ffn 704, "
                                "dense ffn 2112", "algorithmic_bytes_per_layer": algo},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C3_TRAFFIC_BYTES,
                      "kernel": "k_moe_router + k_moe_gu + k_moe_down + k_moe_tail (one layer)",
                      "algorithmic_bytes_per_launch": algo},
     }
@@ -491,14 +498,15 @@ def bench_long(steps: int, warmup: int, cpu: bool) -> dict:
     }
 
 
-def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict:
+def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False, persistent: bool = False) -> dict:
     from e4b import formats
-    from e4b._lib import FLAG_NO_GRAPH
+    from e4b._lib import FLAG_NO_GRAPH, FLAG_PERSISTENT
     from e4b.engine import Engine
     from e4b.model import E4BConfig, synth_tensors
 
     prompt_len = 512
-    cfg = E4BConfig(max_seq=max(1024, prompt_len + warmup + steps + 8), flags=FLAG_NO_GRAPH if no_graph else 0)
+    flags = (FLAG_NO_GRAPH if no_graph else 0) | (FLAG_PERSISTENT if persistent else 0)
+    cfg = E4BConfig(max_seq=max(1024, prompt_len + warmup + steps + 8), flags=flags)
     t0 = time.perf_counter()
     tensors = synth_tensors(cfg, seed=0)
     t_synth = time.perf_counter() - t0
@@ -526,6 +534,7 @@ def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict
                    "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
                    "prefill_tokens_per_s": round(prompt_len / t_prefill, 1),
                    "prefill_ms": round(t_prefill * 1e3, 3),
+                   "layer_loop": "one persistent kernel" if persistent else "six kernels a layer",
                    "prefill_tflops": round((fl["gemm"] + fl["attn"]) / t_prefill / 1e12, 2),
                    "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -559,6 +568,8 @@ def main() -> int:
                     help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device-to-device copy (the byte scale for rocprof FETCH/WRITE_SIZE)")
+    ap.add_argument("--persistent", action="store_true",
+                    help="c4: run the layer loop as one persistent cooperative kernel (E4B_FLAG_PERSISTENT)")
     ap.add_argument("--no-graph", action="store_true",
                     help="c4: launch the step kernels directly instead of replaying the hipGraph (for profilers)")
     a = ap.parse_args()
@@ -578,7 +589,7 @@ def main() -> int:
                           "algorithmic_bytes_per_launch": dom["algo"], "gbs": round(dom["gbs"], 1)}))
         res = None
     elif a.workload == "c4":
-        res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph)
+        res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph, a.persistent)
     else:
         res = fn(steps, warmup, not a.no_cpu)
     if a.copy_probe:

@@ -16,6 +16,7 @@
 
 #include "../../include/e4b.h"
 #include "kernels.h"
+#include "persist.h"
 #include "step.h"
 #include "util.h"
 
@@ -96,6 +97,16 @@ struct e4b_ctx {
   // per-dispatch profiling (e4b_profile_step / e4b_profile_prefill): while
   // prof_on, every launch of a directly launched step or prefill chunk is
   // followed by an event on the context stream, labelled by the kernel role
+  // persistent layer loop (E4B_FLAG_PERSISTENT): the per-layer descriptors
+  // on the device, two sets of tagged hand-off words, the abort word
+  bool persist = false;
+  int pblocks = 0;
+  PersistLayer* d_layers = nullptr;
+  unsigned long long* ll = nullptr;
+  size_t ll_words = 0;
+  int* pabort = nullptr;
+  PersistArgs pargs{};
+  unsigned long long* ptrace = nullptr;  // phase trace of e4b_profile_step (allocated on first use)
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;       // event pool, grown on first use
   std::vector<const char*> prof_label;   // label of the dispatch ending at event i (i >= 1)
@@ -440,6 +451,85 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
         (rc = dalloc_t(c, &c->kv_sk, (size_t)KVH * S * HD)) || (rc = dalloc_t(c, &c->kv_sv, (size_t)KVH * S * HD)))
       return rc;
   }
+  if (k.flags & E4B_FLAG_PERSISTENT) {
+    if (!persist_supported(H, FF, QH, KVH, PD) || (k.flags & E4B_FLAG_KV_SCORE))
+      return e4b_fail(E4B_EINVAL,
+                      "E4B_FLAG_PERSISTENT: unsupported configuration (hidden %d, ffn %d, %d/%d heads, ple_dim %d, "
+                      "or E4B_FLAG_KV_SCORE set)", H, FF, QH, KVH, PD);
+    c->pblocks = persist_blocks(H, FF, c->chunk);
+    if (c->pblocks <= 0)
+      return e4b_fail(E4B_EINVAL, "E4B_FLAG_PERSISTENT: %d blocks of %d threads cannot be co-resident on this device",
+                      H / 8, kPersistThreads);
+    const size_t QKVW = (size_t)c->qkv_rows;
+    const size_t pm = (size_t)QH * c->nch * (HD + 2);
+    const size_t set = (size_t)H + QKVW + pm + (size_t)QH * HD / 2 + (size_t)H + (size_t)FF / 2 + (size_t)H + (size_t)PD / 2;
+    c->ll_words = 2 * set;
+    if ((rc = dalloc_t(c, &c->ll, c->ll_words)) || (rc = dalloc_t(c, &c->pabort, 4)) ||
+        (rc = dalloc_t(c, &c->d_layers, (size_t)k.layers)))
+      return rc;
+    std::vector<PersistLayer> pl((size_t)k.layers);
+    for (int l = 0; l < k.layers; ++l) {
+      const Layer& ly = c->L[l];
+      PersistLayer& d = pl[(size_t)l];
+      d.qkv = q40_view(ly.qkv, c->qkv_rows, H);
+      d.o = q40_view(ly.o, H, (int64_t)QH * HD);
+      d.gu = q40_view(ly.gu, 2 * (int64_t)FF, H);
+      d.down = q40_view(ly.down, H, FF);
+      d.pg = q40_view(ly.pg, PD, H);
+      d.pp = q40_view(ly.pp_rm, H, PD);
+      d.attn_norm = ly.attn_norm;
+      d.q_norm = ly.q_norm;
+      d.k_norm = ly.k_norm;
+      d.post_attn = ly.post_attn;
+      d.ffn_norm = ly.ffn_norm;
+      d.post_ffw = ly.post_ffw;
+      d.post_norm = ly.post_norm;
+      d.scale = ly.scale;
+      d.global = ly.global ? 1 : 0;
+      d.kc = ly.kc;
+      d.vc = ly.vc;
+      d.slots = ly.slots;
+      unsigned long long* w = c->ll + (size_t)(l & 1) * set;
+      d.ll_p = w;
+      w += H;
+      d.ll_qkv = w;
+      w += QKVW;
+      d.ll_pm = w;
+      w += pm;
+      d.ll_att = w;
+      w += (size_t)QH * HD / 2;
+      d.ll_o = w;
+      w += H;
+      d.ll_gg = w;
+      w += (size_t)FF / 2;
+      d.ll_dn = w;
+      w += H;
+      d.ll_g = w;
+    }
+    E4B_HIP(hipMemcpy(c->d_layers, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
+    PersistArgs& a = c->pargs;
+    a.L = c->d_layers;
+    a.layers = k.layers;
+    a.H = H;
+    a.FF = FF;
+    a.QH = QH;
+    a.KVH = KVH;
+    a.PD = PD;
+    a.window = k.window;
+    a.nch_max = c->nch;
+    a.eps = k.eps;
+    a.params = c->params;
+    a.epoch = c->params + 8;
+    a.h_in = c->h;
+    a.ple = c->ple;
+    a.rope = c->rope;
+    a.abort = c->pabort;
+    a.h_out = c->hb;
+    a.xo_hl = c->xo_hl;
+    a.out_norm = c->out_norm;
+    c->persist = true;
+    c->h_final = c->hb;
+  }
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
   if (k.flags & E4B_FLAG_NO_GRAPH) return E4B_OK;
@@ -448,6 +538,14 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   rc = record_step(c);
   hipGraph_t g = nullptr;
   hipError_t ce = hipStreamEndCapture(c->st, &g);
+  if (rc && c->persist) {
+    // a cooperative launch the runtime cannot capture: launch the step's
+    // kernels directly every token instead
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();
+    E4B_HIP(hipStreamSynchronize(c->st));
+    return E4B_OK;
+  }
   if (rc) {
     if (g) (void)hipGraphDestroy(g);
     c->finalized = false;
@@ -464,7 +562,10 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
 
 namespace {
 
+int record_step_persist(e4b_ctx* c);
+
 int record_step(e4b_ctx* c) {
+  if (c->persist) return record_step_persist(c);
   const e4b_config& k = c->cfg;
   const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
   const int Lc = k.layers;
@@ -623,6 +724,39 @@ int record_step(e4b_ctx* c) {
     rc = launch_tail(hcur, c->dn, 1, last.post_ffw, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
   if (rc || (rc = tick(c, "final_norm"))) return rc;
   c->h_final = hcur;
+  if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
+                                   c->logits, nullptr, c->amax_part, st)) ||
+      (rc = tick(c, "lm_head")))
+    return rc;
+  if ((rc = launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st)))
+    return rc;
+  return tick(c, "argmax_feedback");
+}
+
+// The step with the layer loop as one persistent kernel (k_persist.hip):
+// embedding, PLE inputs, the layers (the last residual and the final norm
+// included), lm-head + argmax, feedback.
+int record_step_persist(e4b_ctx* c) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, HD = k.head_dim, PD = k.ple_dim, Lc = k.layers;
+  hipStream_t st = c->st;
+  int rc;
+  const Q6Mat E = q6_view(c->embd, k.vocab, H);
+  if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, c->inv_local,
+                         c->inv_global, HD / 2, c->rope, st)) ||
+      (rc = tick(c, "embed")))
+    return rc;
+  GemvOut po = {c->proj, nullptr, nullptr, 0};
+  if ((rc = launch_q40(q40_view(c->ple_proj, (int64_t)Lc * PD, H), (const uint32_t*)c->h_hl,
+                       (const uint32_t*)(c->h_hl + H), EPI_F32, po, 1, st)) ||
+      (rc = tick(c, "ple_model_proj")))
+    return rc;
+  if ((rc = launch_ple_prep(c->proj, c->ple_tab, c->ple_norm, c->params, c->prompt, Lc, k.vocab,
+                            1.0f / sqrtf((float)H), c->ple, c->h, c->L[0].attn_norm, c->xn, H, k.eps, st)) ||
+      (rc = tick(c, "ple_prep")))
+    return rc;
+  if ((rc = launch_persist(c->pargs, c->pblocks, c->chunk, st)) || (rc = tick(c, "layers")))
+    return rc;
   if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
                                    c->logits, nullptr, c->amax_part, st)) ||
       (rc = tick(c, "lm_head")))
@@ -796,8 +930,16 @@ int ready(e4b_ctx* c, const char* fn) {
 
 int check_status(e4b_ctx* c) {
   uint32_t s = 0;
+  int ab = 0;
   E4B_HIP(hipMemcpyAsync(&s, c->status, 4, hipMemcpyDeviceToHost, c->st));
+  if (c->pabort) E4B_HIP(hipMemcpyAsync(&ab, c->pabort, 4, hipMemcpyDeviceToHost, c->st));
   E4B_HIP(hipStreamSynchronize(c->st));
+  if (ab) {
+    // the tagged hand-off state is unknown after an abort: start clean
+    E4B_HIP(hipMemset(c->pabort, 0, 4));
+    E4B_HIP(hipMemset(c->ll, 0, c->ll_words * 8));
+    return e4b_fail(E4B_EHIP, "persistent step: a wait for a hand-off gave up (state reset; prefill again)");
+  }
   if (s) {
     uint32_t z = 0;
     E4B_HIP(hipMemcpy(c->status, &z, 4, hipMemcpyHostToDevice));
@@ -989,10 +1131,58 @@ extern "C" int e4b_profile_step(e4b_ctx* c, uint32_t token, uint32_t pos, e4b_pr
     return e4b_fail(E4B_ERANGE, "e4b_profile_step: %u full-layer entries fill max_seq %d", kv, c->cfg.max_seq);
   const uint32_t p[5] = {pos, token, 0u, 0u, kv};
   if ((rc = put_params(c, p, 0, 5))) return rc;
-  const int n = profile_run(c, out, cap, [&]() { return record_step(c); });
+  const size_t tslots = c->persist ? (size_t)c->pblocks * c->cfg.layers * kPersistTraceSlots : 0;
+  if (c->persist) {
+    if (!c->ptrace && (rc = dalloc_t(c, &c->ptrace, tslots))) return rc;
+    E4B_HIP(hipMemsetAsync(c->ptrace, 0, tslots * 8, c->st));
+    c->pargs.trace = c->ptrace;
+  }
+  int n = profile_run(c, out, cap, [&]() { return record_step(c); });
+  c->pargs.trace = nullptr;
   if (n < 0) return n;
   c->kv_count = kv + 1;
   if ((rc = check_status(c))) return rc;
+  if (c->persist) {
+    // the layer loop's phases from the trace: per phase, the time from the
+    // previous phase finishing on every block to this one finishing on every
+    // block ("span"), and block 0's wait for its input and its own work
+    static const char* kPh[kPersistPhases] = {"qkv", "attn", "combine", "o", "gate_up", "down", "ple_gate", "ple_proj"};
+    std::vector<unsigned long long> t(tslots);
+    E4B_HIP(hipMemcpy(t.data(), c->ptrace, tslots * 8, hipMemcpyDeviceToHost));
+    int dev = 0, khz = 0;
+    E4B_HIP(hipGetDevice(&dev));
+    E4B_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    const double us_per_tick = khz > 0 ? 1000.0 / khz : 0.0;
+    const int Lc = c->cfg.layers, B = c->pblocks;
+    auto at = [&](int b, int l, int ph, int k) { return t[((size_t)b * Lc + l) * kPersistTraceSlots + ph * 3 + k]; };
+    double span[kPersistPhases] = {0}, wait0[kPersistPhases] = {0}, work0[kPersistPhases] = {0};
+    unsigned long long prev_done = 0;
+    for (int l = 0; l < Lc; ++l)
+      for (int ph = 0; ph < kPersistPhases; ++ph) {
+        unsigned long long done = 0, first = ~0ull;
+        for (int b = 0; b < B; ++b) {
+          done = std::max(done, at(b, l, ph, 2));
+          if (at(b, l, ph, 0)) first = std::min(first, at(b, l, ph, 0));
+        }
+        const unsigned long long from = prev_done ? prev_done : first;
+        if (done >= from) span[ph] += (double)(done - from) * us_per_tick;
+        prev_done = done;
+        const unsigned long long t0 = at(0, l, ph, 0), t1 = at(0, l, ph, 1) ? at(0, l, ph, 1) : t0, t2 = at(0, l, ph, 2);
+        if (t1 >= t0 && t2 >= t1) {
+          wait0[ph] += (double)(t1 - t0) * us_per_tick;
+          work0[ph] += (double)(t2 - t1) * us_per_tick;
+        }
+      }
+    for (int ph = 0; ph < kPersistPhases; ++ph)
+      for (int k = 0; k < 3; ++k) {
+        if (n >= cap) break;
+        const char* what = k == 0 ? "span" : k == 1 ? "block0_wait" : "block0_work";
+        snprintf(out[n].name, sizeof(out[n].name), "layers.%s.%s", kPh[ph], what);
+        out[n].us = (float)(k == 0 ? span[ph] : k == 1 ? wait0[ph] : work0[ph]);
+        out[n].n = Lc;
+        ++n;
+      }
+  }
   return n;
 }
 
@@ -1069,6 +1259,8 @@ extern "C" int e4b_reset(e4b_ctx* c) {
   E4B_HIP(hipMemsetAsync(c->params, 0, 16 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->status, 0, 4 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->amax, 0, 4 * 4, c->st));
+  if (c->ll) E4B_HIP(hipMemsetAsync(c->ll, 0, c->ll_words * 8, c->st));
+  if (c->pabort) E4B_HIP(hipMemsetAsync(c->pabort, 0, 4, c->st));
   if ((rc = zero_scores(c))) return rc;
   c->kv_count = 0;
   E4B_HIP(hipStreamSynchronize(c->st));

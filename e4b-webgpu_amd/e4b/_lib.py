@@ -139,6 +139,7 @@ class ProfEntryC(C.Structure):
 FLAG_NO_GRAPH = 1
 FLAG_STEP_PREFILL = 2
 FLAG_KV_SCORE = 4
+FLAG_PERSISTENT = 8
 
 
 class MoeWeightsC(C.Structure):

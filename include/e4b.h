@@ -290,6 +290,14 @@ typedef struct e4b_config {
  * score (attnos SCORE = 1, kernels/attnos.wgsl:78-92), which e4b_kv_compact
  * ranks; costs one small kernel per full layer and token */
 #define E4B_FLAG_KV_SCORE 4u
+/* run the step's layer loop as one persistent cooperative kernel (one
+ * 512-thread block per CU for hidden / 8 blocks; the layers' phases hand
+ * their vectors over through tagged words in device memory) instead of six
+ * launches per layer; same results within the engine's tolerances.  Needs
+ * ple_dim 256, hidden <= 2048, 4 q heads per KV head with q_heads * 256 <=
+ * 2048, ffn <= 16384, and not E4B_FLAG_KV_SCORE; e4b_finalize fails
+ * otherwise */
+#define E4B_FLAG_PERSISTENT 8u
 
 /* tensor names follow the GGUF naming of the E4B family:
  *   token_embd.weight (Q6_K [vocab][hidden], tied lm-head), output_norm.weight,

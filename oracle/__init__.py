@@ -62,6 +62,7 @@ _sigs = {
     "orc_kv_compact": (_i64, [_vp, _vp, _i32, _i32]),
     "orc_kv_gather_layer": (None, [_vp, _vp, _i32, _vp, _i64]),
     "orc_state_set_kv_count": (None, [_vp, _i64]),
+    "orc_state_set_kv": (None, [_vp, _vp, _i32, _vp, _vp]),
 }
 for _n, (_r, _a) in _sigs.items():
     _f = getattr(_lib, _n)
@@ -375,6 +376,15 @@ class OracleModel:
             cnt = int(k.size)
         if cnt is not None:
             _lib.orc_state_set_kv_count(self._state, cnt)
+
+    def set_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        """Overwrite a layer's caches with f16 bits laid out [slots][kvh][hd]."""
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        _lib.orc_state_set_kv(C.byref(self._m), self._state, int(layer), _p(k), _p(v))
+
+    def set_kv_count(self, n: int) -> None:
+        _lib.orc_state_set_kv_count(self._state, int(n))
 
     def kv_slot(self, is_global: bool, pos: int) -> int:
         return int(_lib.orc_kv_slot(C.byref(self._m), int(is_global), pos))

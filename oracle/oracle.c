@@ -697,6 +697,14 @@ int64_t orc_kv_compact(const orc_model* m, orc_state* s, int budget, int protect
   free(keep);
   return cnt;
 }
+/* Overwrite one layer's K and V caches ([slots][kvh][hd] f16 bits): tests */
+/* hand the oracle another implementation's caches so that one step can be  */
+/* compared from identical state.                                           */
+void orc_state_set_kv(const orc_model* m, orc_state* s, int layer, const uint16_t* k, const uint16_t* v) {
+  const size_t n = (size_t)slots_of(m, layer) * m->kv_heads * m->head_dim;
+  memcpy(s->kc[layer], k, n * sizeof(uint16_t));
+  memcpy(s->vc[layer], v, n * sizeof(uint16_t));
+}
 const uint16_t* orc_state_kcache(const orc_state* s, int layer) { return s->kc[layer]; }
 const uint16_t* orc_state_vcache(const orc_state* s, int layer) { return s->vc[layer]; }
 

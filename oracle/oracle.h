@@ -132,6 +132,7 @@ uint32_t   orc_step(const orc_model* m, orc_state* s, uint32_t token, uint32_t p
 /* ring slot index the step at `pos` writes for layer type (0 sliding, 1 global) */
 int64_t    orc_kv_slot(const orc_model* m, int is_global, uint32_t pos);
 const uint16_t* orc_state_kcache(const orc_state* s, int layer);
+void       orc_state_set_kv(const orc_model* m, orc_state* s, int layer, const uint16_t* k, const uint16_t* v);
 const uint16_t* orc_state_vcache(const orc_state* s, int layer);
 /* full-layer KV budget (src/engine-a4b.js:587-617) */
 void       orc_state_set_scoring(orc_state* s, int on);

@@ -680,3 +680,22 @@ def test_counted_slots_equal_positions_without_compaction():
     assert om.kv_count() == 6
     om.step(9, 0)
     assert om.kv_count() == 1
+
+
+def test_state_set_kv_reproduces_a_step():
+    # handing one oracle state's caches to a fresh one (set_kv + set_kv_count)
+    # makes their next step identical: the step depends on the caches, the
+    # entry count, the token and the position only
+    from e4b.model import synth_tensors, tiny_config
+    cfg = tiny_config(layers=2, layer_global=[0, 1])
+    t = {n: x.data for n, x in synth_tensors(cfg, 1).items()}
+    a, b = orc.OracleModel(cfg.as_dict(), t), orc.OracleModel(cfg.as_dict(), t)
+    for p, tok in enumerate([3, 5, 7, 9, 11, 13]):
+        a.step(tok, p)
+    for l in range(cfg.layers):
+        n = (cfg.max_seq if cfg.layer_global[l] else cfg.ring) * cfg.kv_heads * cfg.head_dim
+        b.set_kv(l, a.kcache(l, n), a.vcache(l, n))
+    b.set_kv_count(a.kv_count())
+    ta, la, _ = a.step(17, 6, want_logits=True)
+    tb, lb, _ = b.step(17, 6, want_logits=True)
+    assert ta == tb and np.array_equal(la, lb)
