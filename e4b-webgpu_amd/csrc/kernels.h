@@ -44,11 +44,15 @@ static inline Q6Mat q6_view(const void* packed, int64_t rows, int64_t cols) {
 }
 
 // Per-device library workspace (argmax and attention partials, x staging).
+// Grow-only: a call that needs more than the current capacity allocates a
+// larger buffer (never while `st` is being captured into a graph: that is an
+// error) and keeps the old one until the process ends, so work already
+// queued or captured with the old address stays valid.
 struct Workspace {
   uint8_t* buf;          // general scratch
   size_t cap;
 };
-int e4b_workspace(size_t bytes, Workspace* ws);
+int e4b_workspace(size_t bytes, Workspace* ws, hipStream_t st);
 
 // q4_0 GEMV epilogues
 enum GemvEpi {

@@ -1,6 +1,7 @@
 // lib.hip -- C-ABI plumbing (errors, device memory, workspace) and the
 // kernel-level entry points of libe4b.
 #include <mutex>
+#include <vector>
 #include <string.h>
 
 #include "../../include/e4b.h"
@@ -91,31 +92,38 @@ extern "C" int e4b_event_destroy(void* ev) {
 
 // ---- per-device workspace ---------------------------------------------------
 // One grow-only scratch buffer per device.  Calls that use it on one device
-// must not overlap (one stream at a time).
+// must not overlap (one stream at a time).  A buffer outgrown by a later call
+// is retired, not freed: a graph captured earlier, or work still queued on
+// another stream, may hold its address.
 namespace {
 struct DevWs {
   uint8_t* buf = nullptr;
   size_t cap = 0;
+  std::vector<uint8_t*> retired;
 };
 std::mutex g_ws_mu;
 DevWs g_ws[64];
 }  // namespace
 
-int e4b_workspace(size_t bytes, Workspace* out) {
+int e4b_workspace(size_t bytes, Workspace* out, hipStream_t st) {
   int dev = 0;
   E4B_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= 64) return e4b_fail(E4B_EINVAL, "device %d out of range", dev);
   std::lock_guard<std::mutex> lk(g_ws_mu);
   DevWs& w = g_ws[dev];
   if (bytes > w.cap) {
-    if (w.buf) {
-      E4B_HIP(hipDeviceSynchronize());
-      E4B_HIP(hipFree(w.buf));
-      w.buf = nullptr;
-      w.cap = 0;
-    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    E4B_HIP(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return e4b_fail(E4B_EINVAL,
+                      "the call needs %zu bytes of library workspace (%zu held), which would allocate inside a "
+                      "stream capture: make the same call once before capturing",
+                      bytes, w.cap);
     const size_t cap = E4B_ALIGN256(bytes < (1u << 20) ? (1u << 20) : bytes);
-    E4B_HIP(hipMalloc(&w.buf, cap));
+    uint8_t* nb = nullptr;
+    E4B_HIP(hipMalloc(&nb, cap));
+    if (w.buf) w.retired.push_back(w.buf);
+    w.buf = nb;
     w.cap = cap;
   }
   out->buf = w.buf;
@@ -141,7 +149,7 @@ extern "C" int e4b_k_q40_gemv(const void* w_packed, int64_t rows, int64_t cols, 
   if (x_dtype != E4B_DT_F32) return e4b_fail(E4B_EINVAL, "e4b_k_q40_gemv: x_dtype %d", x_dtype);
   Workspace ws;
   const size_t half = E4B_ALIGN256((size_t)cols * 2);
-  int rc = e4b_workspace(2 * half, &ws);
+  int rc = e4b_workspace(2 * half, &ws, st);
   if (rc) return rc;
   uint16_t* hi = (uint16_t*)ws.buf;
   uint16_t* lo = (uint16_t*)(ws.buf + half);
@@ -222,7 +230,7 @@ extern "C" int e4b_k_q6k_gemv_argmax(const void* w_packed, int64_t rows, int64_t
   Workspace ws;
   const size_t half = E4B_ALIGN256((size_t)cols * 2);
   const size_t partb = 2048 * sizeof(uint2);
-  int rc = e4b_workspace(2 * half + partb, &ws);
+  int rc = e4b_workspace(2 * half + partb, &ws, st);
   if (rc) return rc;
   uint16_t* hi = (uint16_t*)ws.buf;
   uint16_t* lo = (uint16_t*)(ws.buf + half);
@@ -243,7 +251,7 @@ extern "C" int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, i
 extern "C" int e4b_k_argmax(const float* x, int64_t n, uint32_t* amax, void* stream) {
   if (!x || !amax || n <= 0 || n > 0xffffffffLL) return e4b_fail(E4B_EINVAL, "e4b_k_argmax: bad arguments");
   Workspace ws;
-  int rc = e4b_workspace(1024 * sizeof(uint2), &ws);
+  int rc = e4b_workspace(1024 * sizeof(uint2), &ws, (hipStream_t)stream);
   if (rc) return rc;
   return launch_argmax(x, n, amax, (uint2*)ws.buf, (hipStream_t)stream);
 }
@@ -274,7 +282,7 @@ extern "C" int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc
   a.window = window;
   a.p0 = p0;
   Workspace ws;
-  int rc = e4b_workspace(attn_prefill_part_bytes(m, kv_heads), &ws);
+  int rc = e4b_workspace(attn_prefill_part_bytes(m, kv_heads), &ws, (hipStream_t)stream);
   if (rc) return rc;
   a.part = (float*)ws.buf;
   a.part_bytes = ws.cap;
@@ -335,14 +343,14 @@ extern "C" int e4b_k_attn_decode(const float* qkv, const float* q_norm, const fl
                                &ml_off);
   if (rc) return rc;
   Workspace ws;
-  if ((rc = e4b_workspace(need, &ws))) return rc;
+  if ((rc = e4b_workspace(need, &ws, (hipStream_t)stream))) return rc;
   a.part_o = (float*)ws.buf;
   a.part_ml = (float*)(ws.buf + ml_off);
   return launch_attn(a, (hipStream_t)stream);
 }
 
 // ---- MoE half-layer ----------------------------------------------------------
-static int moe_setup(const e4b_moe_weights* w, const float* h, MoeArgs* A, Workspace* ws) {
+static int moe_setup(const e4b_moe_weights* w, const float* h, MoeArgs* A, Workspace* ws, hipStream_t st) {
   if (!w || !h || !w->ffn_norm || !w->router_scale || !w->pre_ffw2 || !w->router_w || !w->pes || !w->dense_gate_up ||
       !w->exp_gate_up || !w->dense_down || !w->exp_down || !w->post_ffw1 || !w->post_ffw2 || !w->post_ffw)
     return e4b_fail(E4B_EINVAL, "MoE layer: null pointer argument");
@@ -361,7 +369,7 @@ static int moe_setup(const e4b_moe_weights* w, const float* h, MoeArgs* A, Works
     off[i] = cur;
     cur += E4B_ALIGN256(sz[i]);
   }
-  int rc = e4b_workspace(cur, ws);
+  int rc = e4b_workspace(cur, ws, st);
   if (rc) return rc;
   MoeArgs& a = *A;
   a = MoeArgs{};
@@ -403,7 +411,7 @@ extern "C" int e4b_k_router_top8(const e4b_moe_weights* w, const float* h, uint3
   if (!topk_idx || !topk_w) return e4b_fail(E4B_EINVAL, "e4b_k_router_top8: null output");
   MoeArgs a;
   Workspace ws;
-  int rc = moe_setup(w, h, &a, &ws);
+  int rc = moe_setup(w, h, &a, &ws, (hipStream_t)stream);
   if (rc) return rc;
   a.topk_idx = topk_idx;
   a.topk_w = topk_w;
@@ -415,10 +423,10 @@ extern "C" int e4b_k_moe_prefill(const e4b_moe_weights* w, const float* h, int m
   if (!h_out || m < 1 || m > 1024) return e4b_fail(E4B_EINVAL, "e4b_k_moe_prefill: null h_out or m=%d outside 1..1024", m);
   MoeArgs a;
   Workspace ws;
-  int rc = moe_setup(w, h, &a, &ws);  // validates the weights (its scratch is not used)
+  int rc = moe_setup(w, h, &a, &ws, (hipStream_t)stream);  // validates the weights (its scratch is not used)
   if (rc) return rc;
   const size_t bytes = moe_prefill_scratch(a, m, nullptr, nullptr);
-  if ((rc = e4b_workspace(bytes, &ws))) return rc;
+  if ((rc = e4b_workspace(bytes, &ws, (hipStream_t)stream))) return rc;
   MoePrefillBufs b;
   moe_prefill_scratch(a, m, &b, ws.buf);
   a.h_out = h_out;
@@ -437,7 +445,7 @@ extern "C" int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* 
   if (!h_out) return e4b_fail(E4B_EINVAL, "e4b_k_moe_layer: null h_out");
   MoeArgs a;
   Workspace ws;
-  int rc = moe_setup(w, h, &a, &ws);
+  int rc = moe_setup(w, h, &a, &ws, (hipStream_t)stream);
   if (rc) return rc;
   a.h_out = h_out;
   if (topk_idx) a.topk_idx = topk_idx;

@@ -13,6 +13,15 @@
  * are asynchronous on that stream; engine calls that return results are
  * synchronous.
  *
+ * Workspace: kernel-level entry points that need scratch (split-K and argmax
+ * partials, f16 staging of an f32 x) share one grow-only buffer per device.
+ * A call that needs more than it holds allocates a larger one (hipMalloc,
+ * no device synchronisation; the outgrown buffer is kept until the process
+ * ends, so queued or captured work that holds it stays valid).  Inside a
+ * stream capture such a call fails with E4B_EINVAL instead: make the same
+ * call once before capturing.  Calls on one device that use the workspace
+ * must be ordered (one stream at a time).
+ *
  * Citations name the reference interface each entry point replaces
  * (paths relative to the Verilean/e4b-webgpu checkout).
  */
