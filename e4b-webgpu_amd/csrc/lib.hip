@@ -240,6 +240,70 @@ extern "C" int e4b_k_q6k_gemv_argmax(const void* w_packed, int64_t rows, int64_t
                                 logits, amax, part, st);
 }
 
+// ---- allocation-free lm-head --------------------------------------------------
+// e4b_k_q6k_gemv_argmax_noalloc keeps its scratch in a file-scope device array
+// instead of the workspace: the f16 hi and lo halves of x (cols <= 4096) and
+// the argmax partials of at most 2048 workgroups.  Each device holds its own
+// copy; host code addresses it only through the pointer hipGetSymbolAddress
+// returns for the current device.
+constexpr size_t kNoAllocHalf = 4096 * sizeof(uint16_t);
+constexpr size_t kNoAllocPart = 2048 * sizeof(uint2);
+constexpr size_t kNoAllocBytes = 2 * kNoAllocHalf + kNoAllocPart;  // 32 KiB
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_dev[64];  // per device: the device address of `scratch`
+}  // namespace
+
+// The device address of `scratch` on the current device, looked up once per
+// device (no allocation).
+static int scratch_address(uint8_t** out) {
+  int dev = 0;
+  E4B_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return e4b_fail(E4B_EINVAL, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return e4b_fail(E4B_EHIP, "hipGetSymbolAddress(scratch) on device %d -> %s", dev, hipGetErrorString(e));
+    g_scratch_dev[dev] = (uint8_t*)ptr;
+  }
+  *out = g_scratch_dev[dev];
+  return E4B_OK;
+}
+
+extern "C" int e4b_k_q6k_gemv_argmax_noalloc(const void* w_packed, int64_t rows, int64_t cols, const float* x,
+                                             float softcap, float* logits, uint32_t* amax, void* stream) {
+  if (!w_packed || !x || !amax || rows <= 0 || rows > 0xffffffffLL || cols <= 0 || cols % 256)
+    return e4b_fail(E4B_EINVAL, "e4b_k_q6k_gemv_argmax_noalloc: bad arguments (rows=%lld cols=%lld)",
+                    (long long)rows, (long long)cols);
+  if ((size_t)cols * sizeof(uint16_t) > kNoAllocHalf)
+    return e4b_fail(E4B_ERANGE,
+                    "e4b_k_q6k_gemv_argmax_noalloc: %lld columns exceed the %zu-column maximum of its %zu-byte "
+                    "scratch",
+                    (long long)cols, kNoAllocHalf / sizeof(uint16_t), kNoAllocBytes);
+  if ((size_t)q6k_gemv_grid(rows) * sizeof(uint2) > kNoAllocPart)
+    return e4b_fail(E4B_ERANGE, "e4b_k_q6k_gemv_argmax_noalloc: %d argmax partials exceed the scratch",
+                    q6k_gemv_grid(rows));
+  if (!aligned16(w_packed))
+    return e4b_fail(E4B_EINVAL, "e4b_k_q6k_gemv_argmax_noalloc: weight must be 16-byte aligned");
+  uint8_t* sp = nullptr;
+  int rc = scratch_address(&sp);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  // every byte read below is written earlier in the same call: the split
+  // writes hi/lo[0, cols), each GEMV workgroup writes its own partial and
+  // the fold reads only the partials of this launch's workgroups
+  uint16_t* hi = (uint16_t*)sp;
+  uint16_t* lo = (uint16_t*)(sp + kNoAllocHalf);
+  uint2* part = (uint2*)(sp + 2 * kNoAllocHalf);
+  if ((rc = launch_split_f32(x, cols, hi, lo, st))) return rc;
+  return launch_q6k_gemv_argmax(q6_view(w_packed, rows, cols), (const uint32_t*)hi, (const uint32_t*)lo, softcap,
+                                logits, amax, part, st);
+}
+
 extern "C" int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row, float mult, float* out,
                              void* stream) {
   if (!w_packed || !out || rows <= 0 || cols <= 0 || cols % 256 || row < 0 || row >= rows)

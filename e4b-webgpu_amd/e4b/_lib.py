@@ -83,6 +83,7 @@ SIGNATURES = [
     ("e4b_k_q40_gemm_geglu", _i32, [_vp, _i64, _i64, _vp, _i32, _vp, _vp]),
     ("e4b_k_q40_geglu_prenorm", _i32, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _f32, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_gemv_argmax", _i32, [_vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp]),
+    ("e4b_k_q6k_gemv_argmax_noalloc", _i32, [_vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp]),
     ("e4b_k_q6k_row", _i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),
     ("e4b_k_argmax", _i32, [_vp, _i64, _vp, _vp]),
     ("e4b_rope_inv_freq", _i32, [_f32, _i32, _i32, _vp]),

@@ -156,6 +156,18 @@ int e4b_k_q40_geglu_prenorm(const void* w_packed, int64_t ff, int64_t cols, cons
 int e4b_k_q6k_gemv_argmax(const void* w_packed, int64_t rows, int64_t cols, const float* x,
                           float softcap, float* logits, uint32_t* amax, void* stream);
 
+/* e4b_k_q6k_gemv_argmax without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as e4b_k_q6k_gemv_argmax; its scratch
+ * (f16 halves of x and the argmax partials) is a fixed 32 KiB device array
+ * per GPU, held until the process ends, so cols must be <= 4096 (E4B_ERANGE
+ * otherwise).  It calls no hipMalloc/hipFree.  Every call on one GPU shares
+ * that array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be ordered by the caller. */
+int e4b_k_q6k_gemv_argmax_noalloc(const void* w_packed, int64_t rows, int64_t cols, const float* x,
+                                  float softcap, float* logits, uint32_t* amax, void* stream);
+
 /* Q6_K row dequant * mult (kernels/q6k.wgsl:37-73 MODE 0): out f32[cols]. */
 int e4b_k_q6k_row(const void* w_packed, int64_t rows, int64_t cols, int64_t row, float mult,
                   float* out, void* stream);
