@@ -457,9 +457,12 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
                       "E4B_FLAG_PERSISTENT: unsupported configuration (hidden %d, ffn %d, %d/%d heads, ple_dim %d, "
                       "or E4B_FLAG_KV_SCORE set)", H, FF, QH, KVH, PD);
     c->pblocks = persist_blocks(H, FF, c->chunk);
-    if (c->pblocks <= 0)
-      return e4b_fail(E4B_EINVAL, "E4B_FLAG_PERSISTENT: %d blocks of %d threads cannot be co-resident on this device",
-                      H / 8, kPersistThreads);
+    if (c->pblocks < 0)
+      return e4b_fail(E4B_EHIP, "E4B_FLAG_PERSISTENT: occupancy query -> %s",
+                      hipGetErrorString((hipError_t)-c->pblocks));
+    if (c->pblocks == 0)
+      return e4b_fail(E4B_EINVAL, "E4B_FLAG_PERSISTENT: %d blocks of %d threads cannot be co-resident on this device (%s)",
+                      H / 8, kPersistThreads, persist_why());
     const size_t QKVW = (size_t)c->qkv_rows;
     const size_t pm = (size_t)QH * c->nch * (HD + 2);
     const size_t set = (size_t)H + QKVW + pm + (size_t)QH * HD / 2 + (size_t)H + (size_t)FF / 2 + (size_t)H + (size_t)PD / 2;

@@ -966,16 +966,32 @@ static const void* persist_pick(int FF, int chunk) {
 // of the o and down projections, so every block publishes words in every
 // layer that every block waits for.  That chain is what makes rewriting a
 // hand-off buffer one layer later safe: no block can still be reading it.
+static char g_persist_why[256];
+
 int persist_blocks(int H, int FF, int chunk) {
   const void* fn = persist_pick(FF, chunk);
   if (!fn) return 0;
+  // an error an earlier call left pending would be returned by the queries
+  // below instead of their own status
+  (void)hipGetLastError();
   int dev = 0, cus = 0, per = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, NT, 0) != hipSuccess || per < 1) return 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, NT, 0);
+  if (e != hipSuccess) return -(int)e;
   const int want = H / NW;
-  return want <= cus ? want : 0;
+  if (per >= 1 && want <= cus) return want;
+  hipFuncAttributes at{};
+  int lds = 0;
+  (void)hipFuncGetAttributes(&at, fn);
+  (void)hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
+  snprintf(g_persist_why, sizeof(g_persist_why),
+           "occupancy %d block(s) per CU of %d threads (%d registers, %zu B LDS of %d), %d of %d CUs wanted", per, NT,
+           at.numRegs, at.sharedSizeBytes, lds, want, cus);
+  return 0;
 }
+
+const char* persist_why() { return g_persist_why; }
 
 int launch_persist(const PersistArgs& a, int blocks, int chunk, hipStream_t st) {
   const void* fn = persist_pick(a.FF, chunk);

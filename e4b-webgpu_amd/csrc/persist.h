@@ -47,6 +47,9 @@ constexpr int kPersistTraceSlots = kPersistPhases * 3;
 // launch on `st` (cooperative, one block per CU); chunk 32 or 64 positions
 int launch_persist(const PersistArgs& a, int blocks, int chunk, hipStream_t st);
 // blocks the launch uses on the current device (H / 8, one per CU; 0 when
-// that many cannot be co-resident), and whether a configuration is supported
+// that many cannot be co-resident, -hipError_t when the query failed), and
+// whether a configuration is supported
 int persist_blocks(int H, int FF, int chunk);
 bool persist_supported(int H, int FF, int QH, int KVH, int PD);
+// why the last persist_blocks call returned 0
+const char* persist_why();

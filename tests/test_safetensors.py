@@ -4,6 +4,11 @@ f32Scalar, src/loader.js:4-36): e4b.safetensors (Python) and js/loader.js
 `safetensors` package (0.8.0 in this image): files written by it are read by
 both hosts byte for byte, and files written by write_safetensors load in it;
 bf16ToF32 against torch's bfloat16 -> float32 conversion.  CPU only.
+
+torch is imported when a test runs, not when the module is collected: a
+pytest session of GPU tests collects this module too, and torch's own HIP
+runtime loaded next to the one libe4b.so already uses makes that runtime's
+occupancy queries (the persistent step's co-residency check) answer 0.
 """
 import json
 import os
@@ -12,8 +17,6 @@ import subprocess
 
 import numpy as np
 import pytest
-import torch
-from safetensors.torch import load_file, save_file
 
 from e4b.safetensors import SafetensorsError, bf16_to_f32, f32_scalar, open_safetensors, write_safetensors
 
@@ -22,7 +25,23 @@ JS = os.path.join(ROOT, "e4b-webgpu_amd", "js")
 NODE = shutil.which("node")
 
 
+def _torch():
+    import torch
+    return torch
+
+
+def save_file(*a, **kw):
+    from safetensors.torch import save_file as f
+    return f(*a, **kw)
+
+
+def load_file(*a, **kw):
+    from safetensors.torch import load_file as f
+    return f(*a, **kw)
+
+
 def _tensors(seed=0):
+    torch = _torch()
     g = torch.Generator().manual_seed(seed)
     return {
         "model.layers.0.input_layernorm.weight": torch.randn(64, generator=g).to(torch.bfloat16),
@@ -34,11 +53,13 @@ def _tensors(seed=0):
     }
 
 
-_DT = {torch.bfloat16: "BF16", torch.int8: "I8", torch.float32: "F32", torch.float16: "F16"}
+def _dt(t):
+    torch = _torch()
+    return {torch.bfloat16: "BF16", torch.int8: "I8", torch.float32: "F32", torch.float16: "F16"}[t.dtype]
 
 
 def _raw(t):
-    return t.contiguous().view(torch.uint8).numpy().tobytes() if t.numel() else b""
+    return t.contiguous().view(_torch().uint8).numpy().tobytes() if t.numel() else b""
 
 
 def test_reads_files_written_by_the_safetensors_package(tmp_path):
@@ -49,7 +70,7 @@ def test_reads_files_written_by_the_safetensors_package(tmp_path):
     assert set(f.index) == set(ts) and "__metadata__" not in f.index
     for name, t in ts.items():
         got = f.fetch(name)
-        assert got["dtype"] == _DT[t.dtype] and got["shape"] == list(t.shape)
+        assert got["dtype"] == _dt(t) and got["shape"] == list(t.shape)
         assert got["buf"].tobytes() == _raw(t), name
         assert f.has(name) and f.info(name)["data_offsets"] == got["data_offsets"]
     assert not f.has("missing")
@@ -64,15 +85,16 @@ def test_reads_files_written_by_the_safetensors_package(tmp_path):
 def test_written_files_load_in_the_safetensors_package(tmp_path):
     ts = _tensors(2)
     p = str(tmp_path / "ours.safetensors")
-    write_safetensors(p, {n: (_DT[t.dtype], list(t.shape), _raw(t)) for n, t in ts.items()}, {"k": "v"})
+    write_safetensors(p, {n: (_dt(t), list(t.shape), _raw(t)) for n, t in ts.items()}, {"k": "v"})
     back = load_file(p)
     for name, t in ts.items():
-        assert back[name].dtype == t.dtype and torch.equal(back[name], t), name
+        assert back[name].dtype == t.dtype and _torch().equal(back[name], t), name
 
 
 def test_bf16_widening_exhaustive():
     bits = np.arange(65536, dtype=np.uint16)
     got = bf16_to_f32(bits)
+    torch = _torch()
     want = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
     same = (got == want) | (np.isnan(got) & np.isnan(want))
     assert same.all()
