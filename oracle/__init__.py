@@ -56,6 +56,9 @@ _sigs = {
     "orc_state_kcache": (_vp, [_vp, _i32]),
     "orc_state_vcache": (_vp, [_vp, _i32]),
     "orc_state_set_scoring": (None, [_vp, _i32]),
+    "orc_state_set_keep_rows": (None, [_vp, _i32]),
+    "orc_state_krow": (_vp, [_vp, _i32, _i32]),
+    "orc_state_vrow": (_vp, [_vp, _i32, _i32]),
     "orc_state_kv_count": (_i64, [_vp]),
     "orc_state_score": (_vp, [_vp, _i32]),
     "orc_kv_keep": (_i64, [_vp, _i32, _i64, _i64, _i32, _i32, _vp]),
@@ -355,6 +358,21 @@ class OracleModel:
 
     def kv_count(self) -> int:
         return int(_lib.orc_state_kv_count(self._state))
+
+    def set_keep_rows(self, on: bool) -> None:
+        """With keep_rows the step attends to the K/V row handed over (set_kv)
+        for the current token instead of writing its own there; its own rows
+        are still computed and returned by rows()."""
+        _lib.orc_state_set_keep_rows(self._state, int(bool(on)))
+
+    def rows(self, layer: int):
+        """(k, v) rows the last step computed for a layer, f16 bits [kv_heads][head_dim]."""
+        kvh, hd = int(self.cfg["kv_heads"]), int(self.cfg["head_dim"])
+        out = []
+        for fn in (_lib.orc_state_krow, _lib.orc_state_vrow):
+            p = fn(self._state, layer, kvh * hd)
+            out.append(np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(kvh * hd,)).copy().reshape(kvh, hd))
+        return out[0], out[1]
 
     def score(self, layer: int) -> np.ndarray:
         """[q_heads][max_seq] accumulated attention mass of a full layer."""

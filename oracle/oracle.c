@@ -594,6 +594,13 @@ struct orc_state {
   int64_t kv_count;
   int scoring;
   float** score; /* global layers: [q_heads][max_seq] */
+  /* this step's own K/V rows per layer [layers][kv_heads][head_dim] (f16  */
+  /* bits); with keep_rows the step leaves the cache slot of the current  */
+  /* token as it was handed over (orc_state_set_kv) and attends to that   */
+  /* row, so a test can start a step from another implementation's rows  */
+  int keep_rows;
+  uint16_t* krow;
+  uint16_t* vrow;
 };
 
 static int64_t slots_of(const orc_model* m, int l) {
@@ -611,6 +618,8 @@ orc_state* orc_state_new(const orc_model* m) {
     s->vc[l] = calloc(n, sizeof(uint16_t));
   }
   s->ple = calloc((size_t)m->layers * (m->ple_dim > 0 ? m->ple_dim : 1), sizeof(float));
+  s->krow = calloc((size_t)m->layers * m->kv_heads * m->head_dim, sizeof(uint16_t));
+  s->vrow = calloc((size_t)m->layers * m->kv_heads * m->head_dim, sizeof(uint16_t));
   s->score = calloc((size_t)m->layers, sizeof(float*));
   for (int l = 0; l < m->layers; ++l)
     if (m->layer_global[l]) s->score[l] = calloc((size_t)m->q_heads * m->max_seq, sizeof(float));
@@ -625,11 +634,16 @@ void orc_state_free(orc_state* s) {
   free(s->kc);
   free(s->vc);
   free(s->ple);
+  free(s->krow);
+  free(s->vrow);
   for (int l = 0; l < s->layers; ++l) free(s->score[l]);
   free(s->score);
   free(s);
 }
 void orc_state_set_scoring(orc_state* s, int on) { s->scoring = on; }
+void orc_state_set_keep_rows(orc_state* s, int on) { s->keep_rows = on; }
+const uint16_t* orc_state_krow(const orc_state* s, int layer, int row_len) { return s->krow + (size_t)layer * row_len; }
+const uint16_t* orc_state_vrow(const orc_state* s, int layer, int row_len) { return s->vrow + (size_t)layer * row_len; }
 int64_t orc_state_kv_count(const orc_state* s) { return s->kv_count; }
 const float* orc_state_score(const orc_state* s, int layer) { return s->score[layer]; }
 
@@ -770,8 +784,14 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
     orc_q40_gemv(ly->wk, KVH * HD, H, x, qkv + QH * HD);
     orc_q40_gemv(ly->wv, KVH * HD, H, x, qkv + (QH + KVH) * HD);
     int64_t slot = glob ? kv : orc_kv_slot(m, glob, pos);
+    uint16_t* krow = st->krow + (size_t)l * KVH * HD;
+    uint16_t* vrow = st->vrow + (size_t)l * KVH * HD;
     orc_headprep(qkv, QH, KVH, HD, m->rope_angles, glob ? inv_g : inv_l, ly->q_norm, ly->k_norm,
-                 m->eps, pos, qp, st->kc[l] + slot * KVH * HD, st->vc[l] + slot * KVH * HD);
+                 m->eps, pos, qp, krow, vrow);
+    if (!st->keep_rows) {
+      memcpy(st->kc[l] + slot * KVH * HD, krow, sizeof(uint16_t) * (size_t)KVH * HD);
+      memcpy(st->vc[l] + slot * KVH * HD, vrow, sizeof(uint16_t) * (size_t)KVH * HD);
+    }
     if (glob) {
       /* slots [0, kv]; with scoring, each slot's weight joins its mass */
       const int64_t len = kv + 1;

@@ -136,6 +136,11 @@ void       orc_state_set_kv(const orc_model* m, orc_state* s, int layer, const u
 const uint16_t* orc_state_vcache(const orc_state* s, int layer);
 /* full-layer KV budget (src/engine-a4b.js:587-617) */
 void       orc_state_set_scoring(orc_state* s, int on);
+/* keep_rows: the step attends to the cache row handed over for the current */
+/* token instead of writing its own; its own rows are kept apart           */
+void       orc_state_set_keep_rows(orc_state* s, int on);
+const uint16_t* orc_state_krow(const orc_state* s, int layer, int row_len);
+const uint16_t* orc_state_vrow(const orc_state* s, int layer, int row_len);
 int64_t    orc_state_kv_count(const orc_state* s);
 const float* orc_state_score(const orc_state* s, int layer);
 int64_t    orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int budget, int protect,

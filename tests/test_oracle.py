@@ -699,3 +699,59 @@ def test_state_set_kv_reproduces_a_step():
     ta, la, _ = a.step(17, 6, want_logits=True)
     tb, lb, _ = b.step(17, 6, want_logits=True)
     assert ta == tb and np.array_equal(la, lb)
+
+
+def test_keep_rows_attends_to_the_handed_over_row():
+    # keep_rows: the step leaves the current token's cache slot as handed over
+    # and attends to it.  Handed the caches a normal step left behind (its own
+    # rows included), a keep_rows step at the same position reproduces that
+    # step bit for bit and reports the same rows; a perturbed row in the slot
+    # changes the result, in the sliding (ring slot p % ring) and the full
+    # (counted slot) layer alike, and the cache keeps the perturbed row.
+    from e4b.model import synth_tensors, tiny_config
+    cfg = tiny_config(layers=2, layer_global=[0, 1])
+    t = {n: x.data for n, x in synth_tensors(cfg, 2).items()}
+    a, b = orc.OracleModel(cfg.as_dict(), t), orc.OracleModel(cfg.as_dict(), t)
+    for p, tok in enumerate([3, 5, 7, 9, 11, 13]):
+        a.step(tok, p)
+    pre = {}
+    for l in range(cfg.layers):
+        n = (cfg.max_seq if cfg.layer_global[l] else cfg.ring) * cfg.kv_heads * cfg.head_dim
+        pre[l] = (a.kcache(l, n), a.vcache(l, n))
+    ta, la, _ = a.step(17, 6, want_logits=True)
+    S = cfg.kv_heads * cfg.head_dim
+    b.set_keep_rows(True)
+    for l in range(cfg.layers):
+        n = pre[l][0].size
+        b.set_kv(l, a.kcache(l, n), a.vcache(l, n))
+    b.set_kv_count(6)
+    tb, lb, _ = b.step(17, 6, want_logits=True)
+    assert ta == tb and np.array_equal(la, lb)
+    for l in range(cfg.layers):
+        slot = 6 if cfg.layer_global[l] else 6 % cfg.ring
+        ka, va = a.rows(l)
+        kb, vb = b.rows(l)
+        n = pre[l][0].size
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+        assert np.array_equal(ka.reshape(-1), a.kcache(l, n).reshape(-1, S)[slot])
+        assert not np.array_equal(ka.reshape(-1), pre[l][0].reshape(-1, S)[slot])  # the step wrote it
+    # at position 0 the softmax over one key gives the current row all the
+    # weight: a perturbed V row handed over in either layer changes the step,
+    # and the cache keeps the perturbed row
+    z = orc.OracleModel(cfg.as_dict(), t)
+    _, l0, _ = z.step(17, 0, want_logits=True)
+    for l in range(cfg.layers):
+        n = (cfg.max_seq if cfg.layer_global[l] else cfg.ring) * S
+        c = orc.OracleModel(cfg.as_dict(), t)
+        c.set_keep_rows(True)
+        for j in range(cfg.layers):
+            nj = (cfg.max_seq if cfg.layer_global[j] else cfg.ring) * S
+            k, v = z.kcache(j, nj), z.vcache(j, nj).reshape(-1, S).copy()
+            if j == l:
+                v[0, :] = z.vcache(j, nj).reshape(-1, S)[0, ::-1]  # the row reversed
+            c.set_kv(j, k, v.reshape(-1))
+        c.set_kv_count(0)
+        _, lc, _ = c.step(17, 0, want_logits=True)
+        assert not np.array_equal(lc, l0), f"layer {l}: the handed-over row is not the one attended to"
+        assert np.array_equal(c.vcache(l, n).reshape(-1, S)[0], z.vcache(l, n).reshape(-1, S)[0, ::-1])
+        assert np.array_equal(c.rows(l)[1].reshape(-1), z.vcache(l, n).reshape(-1, S)[0])

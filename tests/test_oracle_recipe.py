@@ -513,3 +513,46 @@ def test_recipe_mutants():
                {"no_h_inv": True}, {"post_attn_w": tens[p + "ffn_norm.weight"]}):
         err = float(np.max(np.abs(recipe(**kw) - got)))
         assert err > 100 * tol, (kw, err, tol)
+
+
+def test_one_ulp_perturbation_jumps_at_f16_rounding_points():
+    # The recipe rounds to f16 at fixed points (GEMV inputs, the K/V rows,
+    # the GeGLU and attention outputs), so the decode step is piecewise
+    # constant in tiny input changes: nudging one norm-weight vector by one
+    # f32 ulp (relative 2^-23 ~ 1.2e-7) leaves most steps bit-identical and
+    # moves others by a jump hundreds of times larger, wherever a rounding
+    # it feeds flips and the flip travels through the scale-1.0 attention.
+    # Two implementations that differ by f32-vs-double rounding (the GPU and
+    # this oracle) therefore differ by sums of such jumps; the engine
+    # tests' logit tolerances are stated against this (at the c4 workload a
+    # single such nudge of layer 0 moves the oracle's logits by up to
+    # ~7e-4 of max |logit| at some positions and by 0 at most).
+    from e4b.model import E4BConfig, norm_weights_random, synth_tensors
+    cfg = E4BConfig(layers=5, vocab=4096, max_seq=128, layer_global=[0, 0, 0, 0, 1])
+    tens = {n: t.data for n, t in norm_weights_random(synth_tensors(cfg, 5), 6).items()}
+    pert = dict(tens)
+    w = np.asarray(tens["blk.0.attn_norm.weight"], np.float32)
+    pert["blk.0.attn_norm.weight"] = np.nextafter(w, np.float32(np.inf)).astype(np.float32)
+    a = orc.OracleModel(cfg.as_dict(), tens)
+    b = orc.OracleModel(cfg.as_dict(), pert)
+    b.set_keep_rows(True)
+    rng = np.random.default_rng(12)
+    prompt, forced = rng.integers(0, cfg.vocab, 32), rng.integers(0, cfg.vocab, 32)
+    for i, t in enumerate(prompt):
+        a.step(int(t), i)
+    S = cfg.kv_heads * cfg.head_dim
+    jumps = []
+    for k, t in enumerate(forced):
+        pos = len(prompt) + k
+        _, la, _ = a.step(int(t), pos, want_logits=True)
+        for l in range(cfg.layers):
+            n = (cfg.max_seq if cfg.layer_global[l] else cfg.ring) * S
+            b.set_kv(l, a.kcache(l, n), a.vcache(l, n))
+        b.set_kv_count(pos)
+        _, lb, _ = b.step(int(t), pos, want_logits=True)
+        jumps.append(float(np.abs(la.astype(np.float64) - lb).max() / np.abs(la).max()))
+    jumps = np.array(jumps)
+    print(f"one-ulp nudge: {int((jumps == 0).sum())} of {jumps.size} steps bit-identical, largest jump "
+          f"{jumps.max():.2e} of max |logit|")
+    assert (jumps == 0).sum() >= jumps.size // 2
+    assert jumps.max() > 100 * 2.0 ** -23
