@@ -1,0 +1,45 @@
+// a4b.h -- launchers of the A4B-recipe step kernels (k_a4b.hip): the parts
+// of the reference's live engine (src/engine-a4b.js:424-463) that the E4B
+// kernels do not cover -- hidden sizes that are not a power-of-two multiple
+// of 256, KV heads per layer, head dim 512 with a quarter of the pairs
+// rotated, and V taken from the raw K projection on full layers.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "kernels.h"
+
+// h_out = (h_in + rms(a) * w1) * scale (a null: h_in * scale; h_out null: not
+// stored, h_in and h_out may alias); x (null: none) = f16(rms(h_out) * w2)
+// (w2 null: f16(h_out)); xlo (null: none) = f16(y - f16(y)), the low half of
+// the hi/lo pair of the same value.  H <= 4096.  One workgroup.
+int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
+                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st);
+
+struct HeadPrepGen {
+  const float* qkv;        // raw q [qh][hd] | k [kvh][hd] | v [kvh][hd] (no v rows when keqv)
+  const float* qw;         // [hd] q head-norm weight
+  const float* kw;         // [hd] k head-norm weight
+  const float* inv_freq;   // [hd / 2] THETA^(-2p/hd), f32
+  const uint32_t* params;  // [0] position, [kv_idx] the full layers' slot
+  float* q;                // [qh][hd] prepped queries
+  uint16_t* kc;            // [kvh][slots][hd]
+  uint16_t* vc;
+  int qh, kvh, hd, angles, slots, window, kv_idx;
+  bool keqv;               // V = the raw K slice (kernels/headprep.wgsl:23)
+  float eps;
+};
+int launch_headprep_gen(const HeadPrepGen& a, hipStream_t st);
+
+struct AttnGen {
+  const float* q;          // [qh][hd] prepped queries
+  const uint16_t* kc;      // [kvh][slots][hd]
+  const uint16_t* vc;
+  const uint32_t* params;  // [0] position, [kv_idx] the full layers' slot
+  float* part_o;           // [qh][gch][hd] unnormalised chunk outputs
+  float* part_ml;          // [qh][gch][2] (chunk max, chunk sum)
+  uint16_t* out;           // [qh][hd] f16 attention output (the merge)
+  int qh, kvh, hd, slots, window, kv_idx, gch;
+};
+constexpr int kAttnGenChunk = 64;  // positions per split-K chunk
+// split-K partials over the live chunks, then their log-sum-exp merge
+int launch_attn_gen(const AttnGen& a, hipStream_t st);

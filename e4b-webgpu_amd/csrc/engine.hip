@@ -15,21 +15,35 @@
 #include <vector>
 
 #include "../../include/e4b.h"
+#include "a4b.h"
 #include "kernels.h"
+#include "moe.h"
 #include "persist.h"
 #include "step.h"
 #include "util.h"
 
 namespace {
 
+// per-layer tensors: the E4B recipe's, then the A4B recipe's MoE half
+// (src/engine-a4b.js:150-199)
 enum LayerPart {
   P_ATTN_NORM, P_Q, P_K, P_V, P_Q_NORM, P_K_NORM, P_O, P_POST_ATTN, P_FFN_NORM, P_GATE, P_UP, P_DOWN,
-  P_POST_FFW, P_INP_GATE, P_PROJ, P_POST_NORM, P_SCALE, P_COUNT
+  P_POST_FFW, P_INP_GATE, P_PROJ, P_POST_NORM, P_SCALE,
+  P_PRE_FFW2, P_POST_FFW1, P_POST_FFW2, P_ROUTER_W, P_ROUTER_SCALE, P_PES, P_EXP_GU, P_EXP_DOWN, P_COUNT
 };
 const char* kPartNames[P_COUNT] = {
-    "attn_norm", "attn_q", "attn_k", "attn_v", "attn_q_norm", "attn_k_norm", "attn_output", "post_attention_norm",
-    "ffn_norm", "ffn_gate", "ffn_up", "ffn_down", "post_ffw_norm", "inp_gate", "proj", "post_norm",
-    "layer_output_scale"};
+    "attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_q_norm.weight",
+    "attn_k_norm.weight", "attn_output.weight", "post_attention_norm.weight", "ffn_norm.weight", "ffn_gate.weight",
+    "ffn_up.weight", "ffn_down.weight", "post_ffw_norm.weight", "inp_gate.weight", "proj.weight",
+    "post_norm.weight", "layer_output_scale.weight", "pre_ffw_norm_2.weight", "post_ffw_norm_1.weight",
+    "post_ffw_norm_2.weight", "ffn_gate_inp.weight", "ffn_gate_inp.scale", "ffn_down_exps.scale",
+    "ffn_gate_up_exps.weight", "ffn_down_exps.weight"};
+constexpr uint32_t bit(int p) { return 1u << p; }
+// the parts each recipe needs (attn_v only on layers with their own V)
+constexpr uint32_t kNeedE4B = (bit(P_SCALE) - 1u) & ~(bit(P_INP_GATE) | bit(P_PROJ) | bit(P_POST_NORM));
+constexpr uint32_t kPleParts = bit(P_INP_GATE) | bit(P_PROJ) | bit(P_POST_NORM);
+constexpr uint32_t kNeedA4B = ((bit(P_POST_FFW) << 1) - 1u) | bit(P_PRE_FFW2) | bit(P_POST_FFW1) | bit(P_POST_FFW2) |
+                              bit(P_ROUTER_W) | bit(P_ROUTER_SCALE) | bit(P_PES) | bit(P_EXP_GU) | bit(P_EXP_DOWN);
 
 struct Layer {
   bool global = false;
@@ -47,6 +61,16 @@ struct Layer {
   int slots = 0;
   uint32_t have = 0;
   float* score = nullptr;  // full layers with E4B_FLAG_KV_SCORE: [QH][slots] attention mass
+  // attention shape of the layer: KV heads, head dim, rotated pairs, V = K
+  // (the A4B recipe's full layers), rows of the q|k(|v) matrix, split-K
+  // chunks its partials hold
+  int kvh = 0, hd = 0, angles = 0, gch = 0;
+  bool keqv = false;
+  int64_t qkv_rows = 0;
+  // A4B recipe: the MoE half (gu / down above hold the dense branch)
+  float *pre_ffw2 = nullptr, *post_ffw1 = nullptr, *post_ffw2 = nullptr, *router_w = nullptr,
+        *router_scale = nullptr, *pes = nullptr;
+  uint8_t *exp_gu = nullptr, *exp_down = nullptr;  // q4_0 [E 2 FE][H], [E H][FE]
 };
 
 }  // namespace
@@ -107,6 +131,9 @@ struct e4b_ctx {
   int* pabort = nullptr;
   PersistArgs pargs{};
   unsigned long long* ptrace = nullptr;  // phase trace of e4b_profile_step (allocated on first use)
+  // A4B recipe: prepped queries, the MoE half's scratch
+  float* qp = nullptr;
+  MoeArgs moe{};
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;       // event pool, grown on first use
   std::vector<const char*> prof_label;   // label of the dispatch ending at event i (i >= 1)
@@ -190,12 +217,13 @@ int64_t nelems(const int64_t* dims, int nd) {
   return n;
 }
 
-int expect(const char* name, int type, int want_type, const int64_t* dims, int nd, int64_t cols, int64_t rows) {
+int expect(const char* name, int type, int want_type, const int64_t* dims, int nd, int64_t cols, int64_t rows,
+           int64_t mats = 1) {
   if (type != want_type) return e4b_fail(E4B_EINVAL, "%s: ggml type %d, expected %d", name, type, want_type);
-  const int64_t d0 = nd > 0 ? dims[0] : 1, d1 = nd > 1 ? dims[1] : 1;
-  if (d0 != cols || d1 != rows || nd > 2)
-    return e4b_fail(E4B_EINVAL, "%s: dims [%lld, %lld], expected [%lld, %lld]", name, (long long)d0, (long long)d1,
-                    (long long)cols, (long long)rows);
+  const int64_t d0 = nd > 0 ? dims[0] : 1, d1 = nd > 1 ? dims[1] : 1, d2 = nd > 2 ? dims[2] : 1;
+  if (d0 != cols || d1 != rows || d2 != mats || nd > 3)
+    return e4b_fail(E4B_EINVAL, "%s: dims [%lld, %lld, %lld], expected [%lld, %lld, %lld]", name, (long long)d0,
+                    (long long)d1, (long long)d2, (long long)cols, (long long)rows, (long long)mats);
   return E4B_OK;
 }
 
@@ -212,16 +240,61 @@ constexpr int kPfKsPle = 8;  // PLE gate (256 rows; the GELU-multiply kernel sum
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// The A4B recipe's shape limits: the MoE kernels (hidden a multiple of 256
+// up to 3072, experts 8..256, expert FFN up to 768, dense FFN up to 3072),
+// the general head prep / attention (head dims 256 and 512, any KV heads
+// dividing the q heads)
+static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
+  auto bad = [&](const char* m) {
+    snprintf(why, n, "%s", m);
+    return false;
+  };
+  if (k.hidden <= 0 || k.hidden % 256 || k.hidden > 3072) return bad("hidden must be a multiple of 256 up to 3072");
+  if (k.head_dim != 256) return bad("head_dim (sliding layers) must be 256");
+  const int hdf = k.head_dim_full ? k.head_dim_full : k.head_dim;
+  if (hdf != 256 && hdf != 512) return bad("head_dim_full must be 256 or 512");
+  if (k.q_heads <= 0) return bad("q_heads must be positive");
+  for (int l = 0; l < k.layers; ++l) {
+    const int kvh = k.layer_kv_heads ? k.layer_kv_heads[l] : k.kv_heads;
+    if (kvh <= 0 || k.q_heads % kvh) return bad("every layer's KV heads must divide q_heads");
+  }
+  if (k.ple_dim != 0) return bad("ple_dim must be 0 (no per-layer embeddings)");
+  if (k.ffn <= 0 || k.ffn % 32 || k.ffn > 3072) return bad("ffn (the dense branch) must be a multiple of 32 up to 3072");
+  if (k.n_experts < 8 || k.n_experts > 256) return bad("n_experts must be 8..256");
+  if (k.expert_ffn <= 0 || k.expert_ffn % 32 || k.expert_ffn > 768)
+    return bad("expert_ffn must be a multiple of 32 up to 768");
+  const int af = k.rope_angles_full ? k.rope_angles_full : k.rope_angles;
+  if (k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || af < 0 || af > hdf / 2)
+    return bad("rotated pairs beyond half the head dim");
+  if (k.flags & (E4B_FLAG_PERSISTENT | E4B_FLAG_KV_SCORE))
+    return bad("E4B_FLAG_PERSISTENT and E4B_FLAG_KV_SCORE are E4B-recipe features");
+  return true;
+}
+
 extern "C" e4b_ctx* e4b_create(const e4b_config* cfg) {
   if (!cfg) {
     e4b_fail(E4B_EINVAL, "e4b_create: null config");
     return nullptr;
   }
   const e4b_config& k = *cfg;
-  if (!q40_prologue_supported(k.hidden) || k.layers <= 0 || k.head_dim != 256 || k.kv_heads <= 0 ||
-      k.q_heads != 4 * k.kv_heads || k.ffn <= 0 || k.ffn % 32 || k.vocab <= 0 ||
-      (k.ple_dim != 0 && k.ple_dim != 256) || k.window <= 0 || k.ring < k.window || k.max_seq <= 0 ||
-      k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || (k.attn_chunk != 0 && k.attn_chunk != 32 && k.attn_chunk != 64) || k.max_prompt < 0) {
+  if (k.recipe != E4B_RECIPE_E4B && k.recipe != E4B_RECIPE_A4B) {
+    e4b_fail(E4B_EINVAL, "e4b_create: unknown recipe %d", k.recipe);
+    return nullptr;
+  }
+  if (k.layers <= 0 || k.vocab <= 0 || k.window <= 0 || k.ring < k.window || k.max_seq <= 0 || k.max_prompt < 0 ||
+      (k.attn_chunk != 0 && k.attn_chunk != 32 && k.attn_chunk != 64)) {
+    e4b_fail(E4B_EINVAL, "e4b_create: unsupported config (layers, vocab, window <= ring, max_seq, attn_chunk 32/64)");
+    return nullptr;
+  }
+  if (k.recipe == E4B_RECIPE_A4B) {
+    char why[160];
+    if (!a4b_config_ok(k, why, sizeof(why))) {
+      e4b_fail(E4B_EINVAL, "e4b_create: unsupported A4B config: %s", why);
+      return nullptr;
+    }
+  } else if (!q40_prologue_supported(k.hidden) || k.head_dim != 256 || k.kv_heads <= 0 ||
+             k.q_heads != 4 * k.kv_heads || k.ffn <= 0 || k.ffn % 32 || (k.ple_dim != 0 && k.ple_dim != 256) ||
+             k.rope_angles < 0 || k.rope_angles > k.head_dim / 2) {
     e4b_fail(E4B_EINVAL,
              "e4b_create: unsupported config (hidden %d not 256, 512, 1024 or 2048, or: head_dim 256, q_heads = 4 * "
              "kv_heads, ple_dim 0 or 256, ring >= window)",
@@ -233,9 +306,20 @@ extern "C" e4b_ctx* e4b_create(const e4b_config* cfg) {
   c->lglobal.resize(k.layers);
   for (int i = 0; i < k.layers; ++i) c->lglobal[i] = k.layer_global ? (k.layer_global[i] != 0) : (i % 5 == 4);
   c->cfg.layer_global = nullptr;
+  c->cfg.layer_kv_heads = nullptr;
   c->L.resize(k.layers);
-  for (int i = 0; i < k.layers; ++i) c->L[i].global = c->lglobal[i] != 0;
-  c->qkv_rows = (int64_t)(k.q_heads + 2 * k.kv_heads) * k.head_dim;
+  const bool a4b = k.recipe == E4B_RECIPE_A4B;
+  for (int i = 0; i < k.layers; ++i) {
+    Layer& ly = c->L[i];
+    ly.global = c->lglobal[i] != 0;
+    ly.kvh = (a4b && k.layer_kv_heads) ? k.layer_kv_heads[i] : k.kv_heads;
+    const bool full = a4b && ly.global;
+    ly.hd = (full && k.head_dim_full) ? k.head_dim_full : k.head_dim;
+    ly.angles = (full && k.rope_angles_full) ? k.rope_angles_full : k.rope_angles;
+    ly.keqv = full;  // src/engine-a4b.js:155 (full layers: V = K projection)
+    ly.qkv_rows = (int64_t)(k.q_heads + (ly.keqv ? 1 : 2) * ly.kvh) * ly.hd;
+    if (ly.qkv_rows > c->qkv_rows) c->qkv_rows = ly.qkv_rows;
+  }
   hipError_t e = hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking);
   if (e != hipSuccess) {
     e4b_fail(E4B_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
@@ -293,18 +377,21 @@ extern "C" int e4b_set_tensor(e4b_ctx* c, const char* name, int type, const int6
     if ((rc = expect(name, type, E4B_GGML_F32, dims, nd, PD, 1)) || (rc = check_bytes((size_t)PD * 4))) return rc;
     return upload_f32(c, &c->ple_norm, bytes, PD);
   }
-  // blk.N.part.weight
+  // blk.N.<part>.weight / blk.N.<part>.scale
   int li = -1, used = 0;
-  char part[64] = {0};
-  if (sscanf(name, "blk.%d.%63[a-z_0-9].weight%n", &li, part, &used) != 2 || (size_t)used != nm.size() || li < 0 ||
-      li >= k.layers)
+  if (sscanf(name, "blk.%d.%n", &li, &used) != 1 || used <= 0 || li < 0 || li >= k.layers)
     return e4b_fail(E4B_EINVAL, "e4b_set_tensor: unknown tensor '%s'", name);
   int pi = -1;
   for (int i = 0; i < P_COUNT; ++i)
-    if (strcmp(part, kPartNames[i]) == 0) pi = i;
+    if (strcmp(name + used, kPartNames[i]) == 0) pi = i;
   if (pi < 0) return e4b_fail(E4B_EINVAL, "e4b_set_tensor: unknown tensor '%s'", name);
+  const bool a4b = k.recipe == E4B_RECIPE_A4B;
+  if (a4b && (bit(pi) & kPleParts))
+    return e4b_fail(E4B_EINVAL, "e4b_set_tensor: '%s' is not part of the A4B recipe (no per-layer embeddings)", name);
+  if (!a4b && pi >= P_PRE_FFW2)
+    return e4b_fail(E4B_EINVAL, "e4b_set_tensor: '%s' belongs to the A4B recipe's MoE half (recipe is E4B)", name);
   Layer& ly = c->L[li];
-  const int64_t QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn;
+  const int64_t QH = k.q_heads, KVH = ly.kvh, HD = ly.hd, FF = k.ffn, E = k.n_experts, FE = k.expert_ffn;
   auto q40 = [&](uint8_t** dst, int64_t total_rows, int64_t cols, int64_t row_off, int64_t rows) -> int {
     int r2;
     if ((r2 = expect(name, type, E4B_GGML_Q4_0, dims, nd, cols, rows)) ||
@@ -320,9 +407,14 @@ extern "C" int e4b_set_tensor(e4b_ctx* c, const char* name, int type, const int6
   };
   switch (pi) {
     case P_ATTN_NORM: rc = f32v(&ly.attn_norm, H); break;
-    case P_Q: rc = q40(&ly.qkv, c->qkv_rows, H, 0, QH * HD); break;
-    case P_K: rc = q40(&ly.qkv, c->qkv_rows, H, QH * HD, KVH * HD); break;
-    case P_V: rc = q40(&ly.qkv, c->qkv_rows, H, (QH + KVH) * HD, KVH * HD); break;
+    case P_Q: rc = q40(&ly.qkv, ly.qkv_rows, H, 0, QH * HD); break;
+    case P_K: rc = q40(&ly.qkv, ly.qkv_rows, H, QH * HD, KVH * HD); break;
+    case P_V:
+      // a V = K layer reads V from the K rows; the reference does not load
+      // this tensor there (src/engine-a4b.js:202), nor does the library
+      if (ly.keqv) return E4B_OK;
+      rc = q40(&ly.qkv, ly.qkv_rows, H, (QH + KVH) * HD, KVH * HD);
+      break;
     case P_Q_NORM: rc = f32v(&ly.q_norm, HD); break;
     case P_K_NORM: rc = f32v(&ly.k_norm, HD); break;
     case P_O: rc = q40(&ly.o, H, QH * HD, 0, H); break;
@@ -351,11 +443,100 @@ extern "C" int e4b_set_tensor(e4b_ctx* c, const char* name, int type, const int6
       memcpy(&ly.scale, bytes, 4);
       rc = E4B_OK;
       break;
+    case P_PRE_FFW2: rc = f32v(&ly.pre_ffw2, H); break;
+    case P_POST_FFW1: rc = f32v(&ly.post_ffw1, H); break;
+    case P_POST_FFW2: rc = f32v(&ly.post_ffw2, H); break;
+    case P_ROUTER_SCALE: rc = f32v(&ly.router_scale, H); break;
+    case P_PES: rc = f32v(&ly.pes, E); break;
+    case P_ROUTER_W:  // f32 [E][H]
+      if ((rc = expect(name, type, E4B_GGML_F32, dims, nd, H, E)) || (rc = check_bytes((size_t)(E * H) * 4))) return rc;
+      rc = upload_f32(c, &ly.router_w, bytes, E * H);
+      break;
+    case P_EXP_GU:  // q4_0 [E][2 FE][H]: per expert the gate rows, then the up rows
+      if ((rc = expect(name, type, E4B_GGML_Q4_0, dims, nd, H, 2 * FE, E)) ||
+          (rc = check_bytes((size_t)(E * 2 * FE * H / 32) * 18)))
+        return rc;
+      if (!ly.exp_gu && (rc = dalloc(c, (void**)&ly.exp_gu, e4b_q40_packed_bytes(E * 2 * FE, H)))) return rc;
+      rc = upload_q40_rows(ly.exp_gu, E * 2 * FE, H, 0, bytes, E * 2 * FE);
+      break;
+    case P_EXP_DOWN:  // q4_0 [E][H][FE]
+      if ((rc = expect(name, type, E4B_GGML_Q4_0, dims, nd, FE, H, E)) ||
+          (rc = check_bytes((size_t)(E * H * FE / 32) * 18)))
+        return rc;
+      if (!ly.exp_down && (rc = dalloc(c, (void**)&ly.exp_down, e4b_q40_packed_bytes(E * H, FE)))) return rc;
+      rc = upload_q40_rows(ly.exp_down, E * H, FE, 0, bytes, E * H);
+      break;
     default: rc = e4b_fail(E4B_EINVAL, "unhandled part %d", pi);
   }
   if (rc == E4B_OK) ly.have |= 1u << pi;
   return rc;
 }
+
+namespace {
+
+int missing_parts(const e4b_ctx* c, int l, uint32_t need) {
+  const uint32_t miss = need & ~c->L[l].have;
+  for (int i = 0; i < P_COUNT; ++i)
+    if (miss & bit(i)) return e4b_fail(E4B_ENOTENSOR, "missing blk.%d.%s", l, kPartNames[i]);
+  return E4B_OK;
+}
+
+// The A4B recipe's device state: per-layer caches of the layer's KV heads and
+// head dim, the split-K partials of the widest layer, the MoE half's scratch.
+// Prompts run through the decode step (no batched prefill buffers).
+int finalize_a4b(e4b_ctx* c) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, QH = k.q_heads, FF = k.ffn, E = k.n_experts, FE = k.expert_ffn;
+  int rc;
+  for (int l = 0; l < k.layers; ++l)
+    if ((rc = missing_parts(c, l, kNeedA4B & ~(c->L[l].keqv ? bit(P_V) : 0u)))) return rc;
+  // RoPE inverse frequencies THETA^(-2p/hd) with each layer type's head dim
+  const int hd_s = k.head_dim, hd_f = k.head_dim_full ? k.head_dim_full : k.head_dim;
+  {
+    std::vector<float> il(hd_s / 2), ig(hd_f / 2);
+    rope_inv_freq(k.theta_local, hd_s, hd_s / 2, il.data());
+    rope_inv_freq(k.theta_global, hd_f, hd_f / 2, ig.data());
+    if ((rc = upload_f32(c, &c->inv_local, il.data(), hd_s / 2)) ||
+        (rc = upload_f32(c, &c->inv_global, ig.data(), hd_f / 2)))
+      return rc;
+  }
+  c->chunk = kAttnGenChunk;
+  c->ring_cap = k.max_seq;
+  c->max_prompt = k.max_prompt > 0 ? k.max_prompt : k.max_seq;
+  c->amax_parts = q6k_gemv_grid(k.vocab);
+  c->pf_cap = 0;
+  size_t part = 0, ml = 0;
+  int hd_max = 0;
+  for (int l = 0; l < k.layers; ++l) {
+    Layer& ly = c->L[l];
+    ly.slots = ly.global ? k.max_seq : k.ring;
+    ly.gch = attn_chunks(ly.global ? k.max_seq : k.window, kAttnGenChunk);
+    const size_t n = (size_t)ly.kvh * ly.slots * ly.hd;
+    if ((rc = dalloc_t(c, &ly.kc, n)) || (rc = dalloc_t(c, &ly.vc, n))) return rc;
+    part = std::max(part, (size_t)QH * ly.gch * ly.hd);
+    ml = std::max(ml, (size_t)QH * ly.gch * 2);
+    hd_max = std::max(hd_max, ly.hd);
+  }
+  MoeArgs& m = c->moe;
+  if ((rc = dalloc_t(c, &c->params, 16)) || (rc = dalloc_t(c, &c->prompt, (size_t)c->max_prompt)) ||
+      (rc = dalloc_t(c, &c->tok_ring, (size_t)c->ring_cap)) || (rc = dalloc_t(c, &c->amax, 4)) ||
+      (rc = dalloc_t(c, &c->status, 4)) || (rc = dalloc_t(c, &c->h, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->hb, (size_t)H)) || (rc = dalloc_t(c, &c->rope, (size_t)hd_s)) ||
+      (rc = dalloc_t(c, &c->h_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->xn, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) || (rc = dalloc_t(c, &c->qp, (size_t)QH * hd_max)) ||
+      (rc = dalloc_t(c, &c->part_o, part)) || (rc = dalloc_t(c, &c->part_ml, ml)) ||
+      (rc = dalloc_t(c, &c->attn, (size_t)QH * hd_max)) || (rc = dalloc_t(c, &c->o, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) ||
+      (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)) || (rc = dalloc_t(c, &m.scores, (size_t)E)) ||
+      (rc = dalloc_t(c, &m.xd, (size_t)H)) || (rc = dalloc_t(c, &m.xm, (size_t)H)) ||
+      (rc = dalloc_t(c, &m.topk_idx, (size_t)kMoeTopK)) || (rc = dalloc_t(c, &m.topk_w, (size_t)kMoeTopK)) ||
+      (rc = dalloc_t(c, &m.g_dense, (size_t)FF)) || (rc = dalloc_t(c, &m.g_slots, (size_t)kMoeTopK * FE)) ||
+      (rc = dalloc_t(c, &m.dense_out, (size_t)H)) || (rc = dalloc_t(c, &m.moe_out, (size_t)H)))
+    return rc;
+  return E4B_OK;
+}
+
+}  // namespace
 
 extern "C" int e4b_finalize(e4b_ctx* c) {
   if (!c) return e4b_fail(E4B_EINVAL, "e4b_finalize: null");
@@ -364,19 +545,14 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
   if (!c->embd) return e4b_fail(E4B_ENOTENSOR, "missing token_embd.weight");
   if (!c->out_norm) return e4b_fail(E4B_ENOTENSOR, "missing output_norm.weight");
+  int rc;
+  if (k.recipe == E4B_RECIPE_A4B) {
+    if ((rc = finalize_a4b(c))) return rc;
+  } else {
   if (PD && (!c->ple_tab || !c->ple_proj || !c->ple_norm))
     return e4b_fail(E4B_ENOTENSOR, "missing per_layer_token_embd / per_layer_model_proj / per_layer_proj_norm");
-  uint32_t need = 0;
-  for (int i = 0; i < P_COUNT; ++i) need |= 1u << i;
-  need &= ~(1u << P_SCALE);
-  if (!PD) need &= ~((1u << P_INP_GATE) | (1u << P_PROJ) | (1u << P_POST_NORM));
-  for (int l = 0; l < k.layers; ++l) {
-    const uint32_t miss = need & ~c->L[l].have;
-    if (miss)
-      for (int i = 0; i < P_COUNT; ++i)
-        if (miss & (1u << i)) return e4b_fail(E4B_ENOTENSOR, "missing blk.%d.%s.weight", l, kPartNames[i]);
-  }
-  int rc;
+  for (int l = 0; l < k.layers; ++l)
+    if ((rc = missing_parts(c, l, kNeedE4B | (PD ? kPleParts : 0u)))) return rc;
   // RoPE inverse frequencies THETA^(-2p/HD), rounded once to f32
   {
     std::vector<float> il(HD / 2), ig(HD / 2);
@@ -533,6 +709,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
     c->persist = true;
     c->h_final = c->hb;
   }
+  }  // E4B recipe
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
   if (k.flags & E4B_FLAG_NO_GRAPH) return E4B_OK;
@@ -567,7 +744,111 @@ namespace {
 
 int record_step_persist(e4b_ctx* c);
 
+// One token of the A4B recipe (the reference's encodeForward / encodeLayer,
+// src/engine-a4b.js:424-463, 683-693): embedding; per layer the input norm,
+// q|k(|v), head prep with the K/V write, split-K attention and its merge,
+// o, the attention residual, then the MoE half (router + top-8, dense and
+// expert gate/up + GeGLU, dense and expert down, a4btail); final norm,
+// lm-head + argmax, feedback.  The residual stream is c->h at layer
+// boundaries and c->hb after the attention residual.
+int record_step_a4b(e4b_ctx* c) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, QH = k.q_heads, E = k.n_experts, FE = k.expert_ffn, FF = k.ffn;
+  hipStream_t st = c->st;
+  int rc;
+  const Q6Mat Em = q6_view(c->embd, k.vocab, H);
+  if ((rc = launch_embed(Em, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, c->inv_local,
+                         c->inv_global, k.head_dim / 2, c->rope, st)) ||
+      (rc = tick(c, "embed")))
+    return rc;
+  for (int l = 0; l < k.layers; ++l) {
+    const Layer& ly = c->L[l];
+    const int window = ly.global ? 0 : k.window;
+    GemvOut oq = {c->qkv, nullptr, nullptr, 0};
+    if ((rc = launch_rownorm(c->h, nullptr, nullptr, nullptr, 1.f, ly.attn_norm, c->xn, nullptr, H, k.eps, st)) ||
+        (rc = tick(c, "attn_norm")) ||
+        (rc = launch_q40(q40_view(ly.qkv, ly.qkv_rows, H), (const uint32_t*)c->xn, nullptr, EPI_F32, oq, 1, st)) ||
+        (rc = tick(c, "qkv")))
+      return rc;
+    HeadPrepGen hp;
+    hp.qkv = c->qkv;
+    hp.qw = ly.q_norm;
+    hp.kw = ly.k_norm;
+    hp.inv_freq = ly.global ? c->inv_global : c->inv_local;
+    hp.params = c->params;
+    hp.q = c->qp;
+    hp.kc = ly.kc;
+    hp.vc = ly.vc;
+    hp.qh = QH;
+    hp.kvh = ly.kvh;
+    hp.hd = ly.hd;
+    hp.angles = ly.angles;
+    hp.slots = ly.slots;
+    hp.window = window;
+    hp.kv_idx = 4;  // full layers: params[4] = the token's slot
+    hp.keqv = ly.keqv;
+    hp.eps = k.eps;
+    AttnGen ag;
+    ag.q = c->qp;
+    ag.kc = ly.kc;
+    ag.vc = ly.vc;
+    ag.params = c->params;
+    ag.part_o = c->part_o;
+    ag.part_ml = c->part_ml;
+    ag.out = c->attn;
+    ag.qh = QH;
+    ag.kvh = ly.kvh;
+    ag.hd = ly.hd;
+    ag.slots = ly.slots;
+    ag.window = window;
+    ag.kv_idx = 4;
+    ag.gch = ly.gch;
+    GemvOut oo = {c->o, nullptr, nullptr, 0};
+    if ((rc = launch_headprep_gen(hp, st)) || (rc = tick(c, "headprep")) || (rc = launch_attn_gen(ag, st)) ||
+        (rc = tick(c, ly.global ? "attn_global" : "attn_sliding")) ||
+        (rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * ly.hd), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1,
+                         st)) ||
+        (rc = tick(c, "o_proj")) ||
+        (rc = launch_rownorm(c->h, c->hb, c->o, ly.post_attn, 1.f, nullptr, nullptr, nullptr, H, k.eps, st)) ||
+        (rc = tick(c, "attn_residual")))
+      return rc;
+    MoeArgs a = c->moe;
+    a.h = c->hb;
+    a.ffn_norm = ly.ffn_norm;
+    a.router_scale = ly.router_scale;
+    a.router_mult = 1.0f / sqrtf((float)H);
+    a.pre_ffw2 = ly.pre_ffw2;
+    a.router_w = ly.router_w;
+    a.pes = ly.pes;
+    a.dense_gu = q40_view(ly.gu, 2 * (int64_t)FF, H);
+    a.exp_gu = q40_view(ly.exp_gu, (int64_t)E * 2 * FE, H);
+    a.dense_down = q40_view(ly.down, H, FF);
+    a.exp_down = q40_view(ly.exp_down, (int64_t)E * H, FE);
+    a.post_ffw1 = ly.post_ffw1;
+    a.post_ffw2 = ly.post_ffw2;
+    a.post_ffw = ly.post_ffw;
+    a.layer_scale = ly.scale;
+    a.eps = k.eps;
+    a.H = H;
+    a.E = E;
+    a.FF = FE;
+    a.FF2 = FF;
+    a.h_out = c->h;
+    if ((rc = launch_moe_ffn(a, st)) || (rc = tick(c, "moe_ffn"))) return rc;
+  }
+  c->h_final = c->h;
+  if ((rc = launch_rownorm(c->h, nullptr, nullptr, nullptr, 1.f, c->out_norm, c->xo_hl, c->xo_hl + H, H, k.eps, st)) ||
+      (rc = tick(c, "final_norm")) ||
+      (rc = launch_q6k_gemv_argmax(Em, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
+                                   c->logits, nullptr, c->amax_part, st)) ||
+      (rc = tick(c, "lm_head")) ||
+      (rc = launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st)))
+    return rc;
+  return tick(c, "argmax_feedback");
+}
+
 int record_step(e4b_ctx* c) {
+  if (c->cfg.recipe == E4B_RECIPE_A4B) return record_step_a4b(c);
   if (c->persist) return record_step_persist(c);
   const e4b_config& k = c->cfg;
   const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
@@ -1024,8 +1305,9 @@ static int prefill_common(e4b_ctx* c, const char* fn, const uint32_t* ids, uint3
 }
 
 extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
+  // the A4B recipe has no batched prefill: its prompt runs through the step
   return prefill_common(c, "e4b_prefill", ids, n, argmax_out,
-                        c && (c->cfg.flags & E4B_FLAG_STEP_PREFILL) != 0);
+                        c && ((c->cfg.flags & E4B_FLAG_STEP_PREFILL) != 0 || c->cfg.recipe == E4B_RECIPE_A4B));
 }
 
 extern "C" int e4b_prefill_steps(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
@@ -1193,6 +1475,9 @@ extern "C" int e4b_profile_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, 
   int rc = ready(c, "e4b_profile_prefill");
   if (rc) return rc;
   if (!ids || n == 0) return e4b_fail(E4B_EINVAL, "e4b_profile_prefill: empty prompt");
+  if (c->pf_cap <= 0)
+    return e4b_fail(E4B_ESTATE, "e4b_profile_prefill: this recipe has no batched prefill (its prompts run through "
+                                "the decode step; profile that with e4b_profile_step)");
   const int M = (int)(n < (uint32_t)c->pf_cap ? n : (uint32_t)c->pf_cap);
   for (int i = 0; i < M; ++i)
     if (ids[i] >= (uint32_t)c->cfg.vocab)
@@ -1244,7 +1529,7 @@ extern "C" int e4b_read_kv(e4b_ctx* c, int layer, uint16_t* k_out, uint16_t* v_o
   if (rc) return rc;
   if (layer < 0 || layer >= c->cfg.layers) return e4b_fail(E4B_EINVAL, "layer %d", layer);
   const Layer& ly = c->L[layer];
-  const size_t n = (size_t)c->cfg.kv_heads * ly.slots * c->cfg.head_dim * 2;
+  const size_t n = (size_t)ly.kvh * ly.slots * ly.hd * 2;
   if (k_out) E4B_HIP(hipMemcpyAsync(k_out, ly.kc, n, hipMemcpyDeviceToHost, c->st));
   if (v_out) E4B_HIP(hipMemcpyAsync(v_out, ly.vc, n, hipMemcpyDeviceToHost, c->st));
   E4B_HIP(hipStreamSynchronize(c->st));
@@ -1255,7 +1540,7 @@ extern "C" int e4b_reset(e4b_ctx* c) {
   int rc = ready(c, "e4b_reset");
   if (rc) return rc;
   for (const Layer& ly : c->L) {
-    const size_t n = (size_t)c->cfg.kv_heads * ly.slots * c->cfg.head_dim * 2;
+    const size_t n = (size_t)ly.kvh * ly.slots * ly.hd * 2;
     E4B_HIP(hipMemsetAsync(ly.kc, 0, n, c->st));
     E4B_HIP(hipMemsetAsync(ly.vc, 0, n, c->st));
   }

@@ -20,6 +20,8 @@ E4B_EHIP = -3
 E4B_ESTATE = -4
 E4B_ENOTENSOR = -5
 E4B_ERANGE = -6
+RECIPE_E4B = 0
+RECIPE_A4B = 1
 
 DT_F32 = 0
 DT_F16 = 1
@@ -128,6 +130,8 @@ class ConfigC(C.Structure):
         ("ffn", _i32), ("ple_dim", _i32), ("vocab", _i32), ("window", _i32), ("ring", _i32), ("max_seq", _i32),
         ("rope_angles", _i32), ("theta_local", _f32), ("theta_global", _f32), ("eps", _f32), ("softcap", _f32),
         ("layer_global", _vp), ("attn_chunk", _i32), ("max_prompt", _i32), ("flags", _u32),
+        ("recipe", _i32), ("head_dim_full", _i32), ("rope_angles_full", _i32), ("n_experts", _i32),
+        ("expert_ffn", _i32), ("layer_kv_heads", _vp),
     ]
 
 

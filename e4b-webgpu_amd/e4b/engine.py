@@ -98,12 +98,17 @@ class Engine:
         self.cfg = cfg
         c = ConfigC()
         for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
-                  "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags"):
+                  "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags", "recipe", "head_dim_full",
+                  "rope_angles_full", "n_experts", "expert_ffn"):
             setattr(c, f, int(getattr(cfg, f)))
         for f in ("theta_local", "theta_global", "eps", "softcap"):
             setattr(c, f, float(getattr(cfg, f)))
         self._lg = np.ascontiguousarray(np.asarray(cfg.layer_global, np.uint8))
         c.layer_global = _p(self._lg)
+        self._kvh = None
+        if cfg.layer_kv_heads:
+            self._kvh = np.ascontiguousarray(np.asarray(cfg.layer_kv_heads, np.int32))
+            c.layer_kv_heads = _p(self._kvh)
         ctx = lib.e4b_create(C.byref(c))
         if not ctx:
             check(-1, "e4b_create")
@@ -306,7 +311,8 @@ class Engine:
     def read_kv(self, layer: int):
         """(k, v) caches of a layer as uint16 (f16 bits) [kv_heads][slots][head_dim]."""
         slots = self.kv_slots(layer)
-        shape = (self.cfg.kv_heads, slots, self.cfg.head_dim)
+        kvh, hd, _, _ = self.cfg.layer_shape(layer)
+        shape = (kvh, slots, hd)
         k = np.empty(shape, np.uint16)
         v = np.empty(shape, np.uint16)
         check(lib.e4b_read_kv(self.ctx, layer, _p(k), _p(v)), "e4b_read_kv")

@@ -298,7 +298,20 @@ typedef struct e4b_config {
   int32_t attn_chunk;     /* positions per split-K attention chunk: 32 or 64, 0 = 64 */
   int32_t max_prompt;     /* prompt buffer capacity, 0 = max_seq */
   uint32_t flags;         /* E4B_FLAG_* */
+  /* E4B_RECIPE_A4B (src/engine-a4b.js:100-116): the model loadEngineA4B
+   * loads -- no per-layer embeddings, a MoE FFN half per layer, full layers
+   * with their own head dim and rotated pairs and V = K */
+  int32_t recipe;              /* E4B_RECIPE_E4B (0) or E4B_RECIPE_A4B (1) */
+  int32_t head_dim_full;       /* A4B: full layers' head dim (512), 0 = head_dim */
+  int32_t rope_angles_full;    /* A4B: full layers' rotated pairs (64 = 0.25 * 512 / 2), 0 = rope_angles */
+  int32_t n_experts;           /* A4B: 128 */
+  int32_t expert_ffn;          /* A4B: 704 (ffn above is the dense branch, 2112) */
+  const int32_t* layer_kv_heads; /* A4B: [layers] KV heads per layer; NULL = kv_heads */
 } e4b_config;
+
+/* the layer recipe of e4b_config.recipe */
+#define E4B_RECIPE_E4B 0  /* dense GeGLU FFN + per-layer embeddings (BASELINE config c4) */
+#define E4B_RECIPE_A4B 1  /* MoE FFN half (BASELINE config c3's layer), src/engine-a4b.js:424-463 */
 
 /* launch the step's kernels directly each token instead of replaying the
  * captured hipGraph (same kernels; for profilers that do not follow graphs) */

@@ -57,8 +57,8 @@ _sigs = {
     "orc_state_vcache": (_vp, [_vp, _i32]),
     "orc_state_set_scoring": (None, [_vp, _i32]),
     "orc_state_set_keep_rows": (None, [_vp, _i32]),
-    "orc_state_krow": (_vp, [_vp, _i32, _i32]),
-    "orc_state_vrow": (_vp, [_vp, _i32, _i32]),
+    "orc_state_krow": (_vp, [_vp, _i32]),
+    "orc_state_vrow": (_vp, [_vp, _i32]),
     "orc_state_kv_count": (_i64, [_vp]),
     "orc_state_score": (_vp, [_vp, _i32]),
     "orc_kv_keep": (_i64, [_vp, _i32, _i64, _i64, _i32, _i32, _vp]),
@@ -270,7 +270,7 @@ class LayerC(C.Structure):
         ("attn_norm", _vp), ("q_norm", _vp), ("k_norm", _vp), ("post_attn_norm", _vp), ("ffn_norm", _vp),
         ("post_ffw_norm", _vp), ("post_norm", _vp), ("layer_scale", _cf),
         ("wq", _vp), ("wk", _vp), ("wv", _vp), ("wo", _vp), ("wgate", _vp), ("wup", _vp), ("wdown", _vp),
-        ("inp_gate", _vp), ("proj", _vp),
+        ("inp_gate", _vp), ("proj", _vp), ("moe", MoeC),
     ]
 
 
@@ -281,11 +281,15 @@ class ModelC(C.Structure):
         ("rope_angles", _i32), ("theta_local", _cf), ("theta_global", _cf), ("eps", _cf), ("softcap", _cf),
         ("layer_global", _vp), ("tok_embd", _vp), ("out_norm", _vp), ("ple_tab", _vp), ("ple_proj", _vp),
         ("ple_proj_norm", _vp), ("L", _vp),
+        ("recipe", _i32), ("head_dim_full", _i32), ("rope_angles_full", _i32), ("layer_kv_heads", _vp),
     ]
 
 
 class OracleModel:
-    """Full E4B-shaped decode step on the CPU over ggml-format tensors.
+    """Full decode step on the CPU over ggml-format tensors: the E4B recipe
+    (dense GeGLU FFN, per-layer embeddings) or, with cfg["recipe"] == 1, the
+    A4B recipe (MoE FFN half, per-layer KV heads, full layers with
+    head_dim_full, rope_angles_full and V = K).
 
     ``tensors`` maps GGUF tensor names (the ones e4b.engine uses) to numpy
     arrays: q4_0 / Q6_K as uint8 block bytes, norms as float32.
@@ -338,6 +342,34 @@ class OracleModel:
                             ("wgate", "ffn_gate"), ("wup", "ffn_up"), ("wdown", "ffn_down"),
                             ("inp_gate", "inp_gate"), ("proj", "proj")):
                 setattr(ly, fld, t(p + nm + ".weight", "u"))
+        recipe = int(cfg.get("recipe", 0))
+        m.recipe = recipe
+        if recipe == 1:
+            m.head_dim_full = int(cfg.get("head_dim_full") or cfg["head_dim"])
+            m.rope_angles_full = int(cfg.get("rope_angles_full") or cfg["rope_angles"])
+            kvh = cfg.get("layer_kv_heads")
+            if kvh is not None:
+                kv = np.ascontiguousarray(np.asarray(kvh, dtype=np.int32))
+                self._keep.append(kv)
+                m.layer_kv_heads = _p(kv)
+            H = int(cfg["hidden"])
+            for i in range(int(cfg["layers"])):
+                p = f"blk.{i}."
+                mo = L[i].moe
+                mo.hidden, mo.n_experts, mo.top_k = H, int(cfg["n_experts"]), 8
+                mo.expert_ffn, mo.dense_ffn = int(cfg["expert_ffn"]), int(cfg["ffn"])
+                mo.eps, mo.layer_scale = float(cfg["eps"]), L[i].layer_scale
+                mo.ffn_norm = L[i].ffn_norm
+                mo.router_scale = t(p + "ffn_gate_inp.scale", "f")
+                mo.pre_ffw2 = t(p + "pre_ffw_norm_2.weight", "f")
+                mo.router_w = t(p + "ffn_gate_inp.weight", "f")
+                mo.pes = t(p + "ffn_down_exps.scale", "f")
+                mo.dense_gate, mo.dense_up, mo.dense_down = L[i].wgate, L[i].wup, L[i].wdown
+                mo.exp_gate_up = t(p + "ffn_gate_up_exps.weight", "u")
+                mo.exp_down = t(p + "ffn_down_exps.weight", "u")
+                mo.post_ffw1 = t(p + "post_ffw_norm_1.weight", "f")
+                mo.post_ffw2 = t(p + "post_ffw_norm_2.weight", "f")
+                mo.post_ffw = L[i].post_ffw_norm
         self._keep.append(L)
         m.L = C.cast(L, C.c_void_p)
         self._m = m
@@ -365,12 +397,22 @@ class OracleModel:
         are still computed and returned by rows()."""
         _lib.orc_state_set_keep_rows(self._state, int(bool(on)))
 
+    def layer_shape(self, layer: int):
+        """(kv_heads, head_dim) of a layer's caches."""
+        c = self.cfg
+        if int(c.get("recipe", 0)) == 1:
+            kvh = c.get("layer_kv_heads")
+            kvh = int(kvh[layer]) if kvh is not None else int(c["kv_heads"])
+            glob = bool(c["layer_global"][layer])
+            return kvh, int(c.get("head_dim_full") or c["head_dim"]) if glob else int(c["head_dim"])
+        return int(c["kv_heads"]), int(c["head_dim"])
+
     def rows(self, layer: int):
         """(k, v) rows the last step computed for a layer, f16 bits [kv_heads][head_dim]."""
-        kvh, hd = int(self.cfg["kv_heads"]), int(self.cfg["head_dim"])
+        kvh, hd = self.layer_shape(layer)
         out = []
         for fn in (_lib.orc_state_krow, _lib.orc_state_vrow):
-            p = fn(self._state, layer, kvh * hd)
+            p = fn(self._state, layer)
             out.append(np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(kvh * hd,)).copy().reshape(kvh, hd))
         return out[0], out[1]
 

@@ -601,10 +601,29 @@ struct orc_state {
   int keep_rows;
   uint16_t* krow;
   uint16_t* vrow;
+  int64_t row_stride; /* krow/vrow entries per layer: the largest kv_heads * head_dim */
 };
 
 static int64_t slots_of(const orc_model* m, int l) {
   return m->layer_global[l] ? m->max_seq : m->ring;
+}
+/* per-layer attention shape: the A4B recipe's full layers use head_dim_full, */
+/* rope_angles_full and V = K (src/engine-a4b.js:152-156, 330-334)            */
+static int lay_hd(const orc_model* m, int l) {
+  return (m->recipe == 1 && m->layer_global[l] && m->head_dim_full > 0) ? m->head_dim_full : m->head_dim;
+}
+static int lay_kvh(const orc_model* m, int l) {
+  return (m->recipe == 1 && m->layer_kv_heads) ? m->layer_kv_heads[l] : m->kv_heads;
+}
+static int lay_angles(const orc_model* m, int l) {
+  return (m->recipe == 1 && m->layer_global[l]) ? m->rope_angles_full : m->rope_angles;
+}
+static int lay_keqv(const orc_model* m, int l) { return m->recipe == 1 && m->layer_global[l]; }
+static int64_t row_max(const orc_model* m) {
+  int64_t r = 0;
+  for (int l = 0; l < m->layers; ++l)
+    if ((int64_t)lay_kvh(m, l) * lay_hd(m, l) > r) r = (int64_t)lay_kvh(m, l) * lay_hd(m, l);
+  return r;
 }
 
 orc_state* orc_state_new(const orc_model* m) {
@@ -613,13 +632,14 @@ orc_state* orc_state_new(const orc_model* m) {
   s->kc = calloc((size_t)m->layers, sizeof(uint16_t*));
   s->vc = calloc((size_t)m->layers, sizeof(uint16_t*));
   for (int l = 0; l < m->layers; ++l) {
-    size_t n = (size_t)slots_of(m, l) * m->kv_heads * m->head_dim;
+    size_t n = (size_t)slots_of(m, l) * lay_kvh(m, l) * lay_hd(m, l);
     s->kc[l] = calloc(n, sizeof(uint16_t));
     s->vc[l] = calloc(n, sizeof(uint16_t));
   }
   s->ple = calloc((size_t)m->layers * (m->ple_dim > 0 ? m->ple_dim : 1), sizeof(float));
-  s->krow = calloc((size_t)m->layers * m->kv_heads * m->head_dim, sizeof(uint16_t));
-  s->vrow = calloc((size_t)m->layers * m->kv_heads * m->head_dim, sizeof(uint16_t));
+  s->krow = calloc((size_t)m->layers * row_max(m), sizeof(uint16_t));
+  s->vrow = calloc((size_t)m->layers * row_max(m), sizeof(uint16_t));
+  s->row_stride = row_max(m);
   s->score = calloc((size_t)m->layers, sizeof(float*));
   for (int l = 0; l < m->layers; ++l)
     if (m->layer_global[l]) s->score[l] = calloc((size_t)m->q_heads * m->max_seq, sizeof(float));
@@ -642,8 +662,8 @@ void orc_state_free(orc_state* s) {
 }
 void orc_state_set_scoring(orc_state* s, int on) { s->scoring = on; }
 void orc_state_set_keep_rows(orc_state* s, int on) { s->keep_rows = on; }
-const uint16_t* orc_state_krow(const orc_state* s, int layer, int row_len) { return s->krow + (size_t)layer * row_len; }
-const uint16_t* orc_state_vrow(const orc_state* s, int layer, int row_len) { return s->vrow + (size_t)layer * row_len; }
+const uint16_t* orc_state_krow(const orc_state* s, int layer) { return s->krow + (size_t)layer * s->row_stride; }
+const uint16_t* orc_state_vrow(const orc_state* s, int layer) { return s->vrow + (size_t)layer * s->row_stride; }
 int64_t orc_state_kv_count(const orc_state* s) { return s->kv_count; }
 const float* orc_state_score(const orc_state* s, int layer) { return s->score[layer]; }
 
@@ -684,7 +704,7 @@ int64_t orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int bud
 /* kvgather (kernels/kvgather.wgsl) of one full layer: slot i <- slot        */
 /* keep[i] for K and V, then its scores zeroed (src/engine-a4b.js:604-614).  */
 void orc_kv_gather_layer(const orc_model* m, orc_state* s, int layer, const uint32_t* keep, int64_t cnt) {
-  const int64_t row = (int64_t)m->kv_heads * m->head_dim;
+  const int64_t row = (int64_t)lay_kvh(m, layer) * lay_hd(m, layer);
   uint16_t* tmp = malloc(sizeof(uint16_t) * (size_t)((cnt > 0 ? cnt : 1) * row));
   uint16_t* caches[2] = {s->kc[layer], s->vc[layer]};
   for (int c = 0; c < 2; ++c) {
@@ -715,7 +735,7 @@ int64_t orc_kv_compact(const orc_model* m, orc_state* s, int budget, int protect
 /* hand the oracle another implementation's caches so that one step can be  */
 /* compared from identical state.                                           */
 void orc_state_set_kv(const orc_model* m, orc_state* s, int layer, const uint16_t* k, const uint16_t* v) {
-  const size_t n = (size_t)slots_of(m, layer) * m->kv_heads * m->head_dim;
+  const size_t n = (size_t)slots_of(m, layer) * lay_kvh(m, layer) * lay_hd(m, layer);
   memcpy(s->kc[layer], k, n * sizeof(uint16_t));
   memcpy(s->vc[layer], v, n * sizeof(uint16_t));
 }
@@ -728,6 +748,59 @@ int64_t orc_kv_slot(const orc_model* m, int is_global, uint32_t pos) {
 
 static void round_f16(float* x, int64_t n) {
   for (int64_t i = 0; i < n; ++i) x[i] = orc_h2f(orc_f2h(x[i]));
+}
+
+/* One layer of the A4B recipe (src/engine-a4b.js:424-463): attn_norm -> q|k|v */
+/* GEMVs on the f16 input (full layers have no V projection: V is the raw K  */
+/* slice, KEQV, kernels/headprep.wgsl:23) -> headprep with the layer's head   */
+/* dim and rotated pairs (src/engine-a4b.js:330-334) -> ring or counted       */
+/* attention -> o -> h1 = h + rms(o) post_attention_norm (rmsacc3,             */
+/* kernels/rmsacc3.wgsl:36-53) -> the MoE FFN half on h1 (orc_moe_ffn:        */
+/* rmsacc3's branch inputs, routertop, q40gu, q40moedown, a4btail).          */
+static void a4b_layer(const orc_model* m, orc_state* st, int l, float* h, uint32_t pos, int64_t kv) {
+  const orc_layer* ly = &m->L[l];
+  const int H = m->hidden, QH = m->q_heads, glob = m->layer_global[l];
+  const int HD = lay_hd(m, l), KVH = lay_kvh(m, l), ANG = lay_angles(m, l), keqv = lay_keqv(m, l);
+  float* x = malloc(sizeof(float) * H);
+  float* qkv = malloc(sizeof(float) * (size_t)(QH + 2 * KVH) * HD);
+  float* qp = malloc(sizeof(float) * (size_t)QH * HD);
+  uint16_t* ao = malloc(sizeof(uint16_t) * (size_t)QH * HD);
+  float* a = malloc(sizeof(float) * (size_t)QH * HD);
+  float* o = malloc(sizeof(float) * H);
+  float* inv = malloc(sizeof(float) * (size_t)(HD / 2));
+  orc_rope_inv_freq(glob ? m->theta_global : m->theta_local, HD, ANG, inv);
+  orc_rmsnorm(h, ly->attn_norm, H, m->eps, x);
+  round_f16(x, H);
+  orc_q40_gemv(ly->wq, QH * HD, H, x, qkv);
+  orc_q40_gemv(ly->wk, KVH * HD, H, x, qkv + QH * HD);
+  if (keqv)
+    memcpy(qkv + (size_t)(QH + KVH) * HD, qkv + (size_t)QH * HD, sizeof(float) * (size_t)KVH * HD);
+  else
+    orc_q40_gemv(ly->wv, KVH * HD, H, x, qkv + (size_t)(QH + KVH) * HD);
+  const int64_t slot = glob ? kv : orc_kv_slot(m, glob, pos);
+  uint16_t* krow = st->krow + (size_t)l * st->row_stride;
+  uint16_t* vrow = st->vrow + (size_t)l * st->row_stride;
+  orc_headprep(qkv, QH, KVH, HD, ANG, inv, ly->q_norm, ly->k_norm, m->eps, pos, qp, krow, vrow);
+  if (!st->keep_rows) {
+    memcpy(st->kc[l] + slot * KVH * HD, krow, sizeof(uint16_t) * (size_t)KVH * HD);
+    memcpy(st->vc[l] + slot * KVH * HD, vrow, sizeof(uint16_t) * (size_t)KVH * HD);
+  }
+  if (glob)
+    orc_attn_linear(qp, st->kc[l], st->vc[l], QH, KVH, HD, (uint32_t)(kv + 1), ao);
+  else
+    orc_attn_ring(qp, st->kc[l], st->vc[l], QH, KVH, HD, m->ring, m->window, pos, ao);
+  orc_h2f_n(ao, (int64_t)QH * HD, a);
+  orc_q40_gemv(ly->wo, H, QH * HD, a, o);
+  double io = rms_inv(o, H, m->eps);
+  for (int i = 0; i < H; ++i) h[i] = (float)((double)h[i] + (double)o[i] * io * (double)ly->post_attn_norm[i]);
+  float* dn = malloc(sizeof(float) * H);
+  float* mo = malloc(sizeof(float) * H);
+  float* ho = malloc(sizeof(float) * H);
+  uint32_t idx[64];
+  float w[64];
+  orc_moe_ffn(&ly->moe, h, idx, w, dn, mo, ho);
+  memcpy(h, ho, sizeof(float) * H);
+  free(x); free(qkv); free(qp); free(ao); free(a); free(o); free(inv); free(dn); free(mo); free(ho);
 }
 
 uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t pos, float* logits,
@@ -775,6 +848,10 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
   }
 
   for (int l = 0; l < L; ++l) {
+    if (m->recipe == 1) {
+      a4b_layer(m, st, l, h, pos, kv);
+      continue;
+    }
     const orc_layer* ly = &m->L[l];
     const int glob = m->layer_global[l];
     /* attention block */
@@ -784,8 +861,8 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
     orc_q40_gemv(ly->wk, KVH * HD, H, x, qkv + QH * HD);
     orc_q40_gemv(ly->wv, KVH * HD, H, x, qkv + (QH + KVH) * HD);
     int64_t slot = glob ? kv : orc_kv_slot(m, glob, pos);
-    uint16_t* krow = st->krow + (size_t)l * KVH * HD;
-    uint16_t* vrow = st->vrow + (size_t)l * KVH * HD;
+    uint16_t* krow = st->krow + (size_t)l * st->row_stride;
+    uint16_t* vrow = st->vrow + (size_t)l * st->row_stride;
     orc_headprep(qkv, QH, KVH, HD, m->rope_angles, glob ? inv_g : inv_l, ly->q_norm, ly->k_norm,
                  m->eps, pos, qp, krow, vrow);
     if (!st->keep_rows) {

@@ -108,6 +108,7 @@ typedef struct {
   const uint8_t *wq, *wk, *wv, *wo;          /* q4_0 */
   const uint8_t *wgate, *wup, *wdown;        /* q4_0 */
   const uint8_t *inp_gate, *proj;            /* q4_0 PLE gate [PD][H], proj [H][PD] */
+  orc_moe moe;  /* A4B recipe: the layer's MoE FFN half (wgate/wup/wdown are the dense branch) */
 } orc_layer;
 
 typedef struct {
@@ -121,6 +122,12 @@ typedef struct {
   const uint8_t* ple_proj;     /* q4_0 [layers*ple_dim][hidden] */
   const float* ple_proj_norm;  /* [ple_dim] */
   const orc_layer* L;          /* [layers] */
+  /* recipe 1 = the A4B engine's layer (src/engine-a4b.js:424-463): no PLE, */
+  /* MoE FFN half (orc_moe_ffn); full layers use head_dim_full, rotate     */
+  /* rope_angles_full pairs and take V from the raw K projection (KEQV);   */
+  /* layer_kv_heads (may be NULL) gives each layer's KV heads               */
+  int recipe, head_dim_full, rope_angles_full;
+  const int* layer_kv_heads;
 } orc_model;
 
 typedef struct orc_state orc_state;
@@ -139,8 +146,8 @@ void       orc_state_set_scoring(orc_state* s, int on);
 /* keep_rows: the step attends to the cache row handed over for the current */
 /* token instead of writing its own; its own rows are kept apart           */
 void       orc_state_set_keep_rows(orc_state* s, int on);
-const uint16_t* orc_state_krow(const orc_state* s, int layer, int row_len);
-const uint16_t* orc_state_vrow(const orc_state* s, int layer, int row_len);
+const uint16_t* orc_state_krow(const orc_state* s, int layer);  /* [layer's kv_heads][head_dim] */
+const uint16_t* orc_state_vrow(const orc_state* s, int layer);
 int64_t    orc_state_kv_count(const orc_state* s);
 const float* orc_state_score(const orc_state* s, int layer);
 int64_t    orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int budget, int protect,

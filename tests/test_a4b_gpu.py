@@ -1,0 +1,178 @@
+"""The A4B recipe (the model the reference's live engine loads,
+src/engine-a4b.js:100-199, 424-463) through the C-ABI engine, against the
+CPU oracle's A4B layer (oracle/oracle.c a4b_layer).
+
+Per layer: input norm, q|k(|v) GEMV, head prep with the layer's KV heads and
+head dim (full layers: head dim 512, a quarter of the pairs rotated, V from
+the raw K projection), ring (sliding) or counted (full) split-K attention,
+o projection, attention residual, MoE half (router + top-8, dense and
+expert GeGLU, down projections, a4btail).  The prompt runs through the
+decode step (this recipe has no batched prefill).
+
+The recipe is piecewise constant in small input changes (f16 rounding
+points, and the top-8 expert selection on top of the E4B recipe's;
+tests/test_oracle_recipe.py shows the jumps), so the tests compare each
+step from the GPU's own state, as the c4 stated-workload test does
+(tests/test_engine_gpu.py): an oracle handed the GPU's caches, the current
+token's rows included (keep_rows), must give logits within SYNC_TOL = 2e-3
+of its logit range, the same argmax unless a near-tie (top-2 margin below
+2e-3 of max |logit|), and the GPU's new K/V rows within 2^-9 (layer 0) or
+1e-2 (later layers) of its row max.  A free-running oracle follows too:
+logits within 1e-2 of the range, an argmax difference only where its top-2
+margin is within twice that step's logit difference; written KV slot sets
+bit-exact at the end.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from e4b.engine import Engine
+from e4b.model import a4b_config, norm_weights_random, synth_tensors, tiny_a4b_config
+from tests.test_engine_gpu import KV_MAX_TOL, KV_MEAN_TOL, LOGIT_TOL, TIE_TOL, lockstep
+from tests.util import top2_margin
+
+pytestmark = pytest.mark.gpu
+
+SYNC_TOL = 2e-3
+DRIFT_TOL = 1e-2
+
+
+def _models(cfg, seed):
+    tensors = norm_weights_random(synth_tensors(cfg, seed), seed + 1)
+    tens = {n: t.data for n, t in tensors.items()}
+    eng = Engine(cfg, tensors)
+    return eng, orc.OracleModel(cfg.as_dict(), tens), orc.OracleModel(cfg.as_dict(), tens)
+
+
+def _kv_close(eng, om, cfg, layer):
+    k, v = eng.read_kv(layer)  # [kvh][slots][hd]
+    kvh, slots, hd = k.shape
+    assert (kvh, hd) == cfg.layer_shape(layer)[:2]
+    n = slots * kvh * hd
+    ok = om.kcache(layer, n).reshape(slots, kvh, hd).transpose(1, 0, 2)
+    ov = om.vcache(layer, n).reshape(slots, kvh, hd).transpose(1, 0, 2)
+    assert np.array_equal(np.any(k != 0, axis=(0, 2)), np.any(ok != 0, axis=(0, 2))), f"layer {layer}: slots"
+    errs = []
+    for a, b in ((k, ok), (v, ov)):
+        fa, fb = a.view(np.float16).astype(np.float64), b.view(np.float16).astype(np.float64)
+        d = np.abs(fa - fb)
+        errs.append(d.max() / np.abs(fb).max())
+        assert d.max() <= KV_MAX_TOL * np.abs(fb).max(), f"layer {layer} (max)"
+        assert d.mean() <= KV_MEAN_TOL * np.abs(fb).mean(), f"layer {layer} (mean)"
+    return errs
+
+
+def _f16(a):
+    return a.view(np.float16).astype(np.float64)
+
+
+def synced_steps(eng, om, osync, cfg, tokens, start):
+    """Host-fed steps at positions start, start + 1, ...; every step compared
+    with the synced and the free-running oracle.  Returns the per-step
+    (synced error of range, free error of range) and the near-ties."""
+    osync.set_keep_rows(True)
+    out, ties = [], []
+    for k, t in enumerate(tokens):
+        pos = start + k
+        g, lg = eng.step(int(t), pos, want_logits=True)
+        o_tok, o_lg, _ = om.step(int(t), pos, want_logits=True)
+        rows = []
+        for layer in range(cfg.layers):
+            kg, vg = eng.read_kv(layer)
+            osync.set_kv(layer, kg.transpose(1, 0, 2), vg.transpose(1, 0, 2))
+            slot = pos if cfg.layer_global[layer] else pos % kg.shape[1]
+            rows.append((kg[:, slot, :], vg[:, slot, :]))
+        osync.set_kv_count(pos)
+        s_tok, s_lg, s_h = osync.step(int(t), pos, want_logits=True, want_hidden=True)
+        d = np.abs(lg.astype(np.float64) - s_lg)
+        sr = float(d.max() / (s_lg.max() - s_lg.min()))
+        fr = float(np.abs(lg.astype(np.float64) - o_lg).max() / (o_lg.max() - o_lg.min()))
+        herr = float(np.abs(eng.read_hidden() - s_h).max() / np.abs(s_h).max())
+        assert sr < SYNC_TOL and herr < SYNC_TOL, f"pos {pos}: synced logits {sr:.2e}, hidden {herr:.2e}"
+        assert fr < DRIFT_TOL, f"pos {pos}: free-running logits {fr:.2e}"
+        if g != s_tok:
+            assert top2_margin(s_lg) < TIE_TOL * np.abs(s_lg).max(), f"pos {pos}: gpu {g} vs synced oracle {s_tok}"
+            ties.append((pos, "synced"))
+        if g != o_tok:
+            assert top2_margin(o_lg) <= 2 * float(np.abs(lg.astype(np.float64) - o_lg).max()), f"pos {pos}: free"
+            ties.append((pos, "free"))
+        for layer, (kg, vg) in enumerate(rows):
+            for a, b in zip((kg, vg), osync.rows(layer)):
+                e = np.abs(_f16(a) - _f16(b)).max() / np.abs(_f16(b)).max()
+                assert e <= (2.0 ** -9 if layer == 0 else KV_MAX_TOL), f"pos {pos} layer {layer}: new row {e:.2e}"
+        out.append((sr, fr))
+    return np.array(out), ties
+
+
+def _written_slots_match(eng, om, cfg):
+    for layer in range(cfg.layers):
+        k, _ = eng.read_kv(layer)
+        kvh, slots, hd = k.shape
+        ok = om.kcache(layer, slots * kvh * hd).reshape(slots, kvh, hd)
+        assert np.array_equal(np.any(k != 0, axis=(0, 2)), np.any(ok != 0, axis=(1, 2))), f"layer {layer}: slots"
+
+
+def test_tiny_a4b_synced_steps():
+    # 4 layers (KV heads 4, 2, 4 and 1; the last a full layer with head dim
+    # 512 and V = K), window 8 in a 16-slot ring: a 12-token prompt through
+    # the step, then 48 forced tokens (positions 12..59 wrap the ring)
+    cfg = tiny_a4b_config()
+    eng, om, osync = _models(cfg, 31)
+    rng = np.random.default_rng(4)
+    prompt, forced = rng.integers(0, cfg.vocab, 12), rng.integers(0, cfg.vocab, 48)
+    g0 = eng.prefill(prompt)
+    for i, t in enumerate(prompt):
+        o_tok, o_lg, _ = om.step(int(t), i, want_logits=True)
+    assert g0 == o_tok or top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max()
+    errs, ties = synced_steps(eng, om, osync, cfg, forced, len(prompt))
+    print(f"tiny A4B: synced err of range median {np.median(errs[:, 0]):.2e} max {errs[:, 0].max():.2e}; "
+          f"free median {np.median(errs[:, 1]):.2e} max {errs[:, 1].max():.2e}; near-ties {ties}")
+    _written_slots_match(eng, om, cfg)
+
+
+def test_tiny_a4b_layer_mix_synced_steps():
+    # two full layers with 1 and 2 KV heads between sliding layers with 2
+    # and 8 (GQA 8, 4, 4 and 1 over the 8 q heads), from position 0
+    cfg = tiny_a4b_config(layer_global=[0, 1, 0, 1], layer_kv_heads=[2, 1, 8, 2])
+    eng, om, osync = _models(cfg, 41)
+    errs, ties = synced_steps(eng, om, osync, cfg, np.random.default_rng(5).integers(0, cfg.vocab, 32), 0)
+    print(f"A4B layer mix: synced err of range median {np.median(errs[:, 0]):.2e} max {errs[:, 0].max():.2e}; "
+          f"free max {errs[:, 1].max():.2e}; near-ties {ties}")
+    _written_slots_match(eng, om, cfg)
+
+
+def _pair(cfg, seed):
+    tensors = norm_weights_random(synth_tensors(cfg, seed), seed + 1)
+    eng = Engine(cfg, tensors)
+    om = orc.OracleModel(cfg.as_dict(), {n: t.data for n, t in tensors.items()})
+    return eng, om
+
+
+def test_a4b_width_layers_lockstep():
+    # the reference model's layer shapes (hidden 2816, 16 q heads, head dims
+    # 256 / 512, dense FFN 2112, 128 experts of 704), two sliding layers with
+    # 8 KV heads and one full layer with 2, a reduced vocabulary
+    cfg = a4b_config(layers=3, vocab=4096, max_seq=256, window=64, ring=128, layer_global=[0, 1, 0],
+                     layer_kv_heads=[8, 2, 8])
+    eng, om = _pair(cfg, 51)
+    prompt = np.random.default_rng(6).integers(0, cfg.vocab, 70)
+    toks, ties, o_lg = lockstep(eng, om, prompt, 8)
+    err = float(np.abs(eng.read_logits() - o_lg).max() / np.abs(o_lg).max())
+    print(f"A4B width: tokens {toks}, near-ties {ties}, logits err {err:.2e}")
+    assert err < LOGIT_TOL
+    for layer in range(cfg.layers):
+        _kv_close(eng, om, cfg, layer)
+
+
+def test_a4b_engine_is_graph_replayed_and_gpu_fed():
+    # GPU-fed decode (one graph replay per token) equals the host-fed step loop
+    cfg = tiny_a4b_config()
+    tensors = norm_weights_random(synth_tensors(cfg, 61), 62)
+    a, b = Engine(cfg, tensors), Engine(cfg, tensors)
+    prompt = np.random.default_rng(7).integers(0, cfg.vocab, 9)
+    fed = [a.prefill(prompt)] + a.decode_chunk(len(prompt), 12).tolist()
+    b.prefill(prompt)
+    step = [fed[0]]
+    for i in range(12):
+        step.append(b.step(step[-1], len(prompt) + i))
+    assert fed == step
