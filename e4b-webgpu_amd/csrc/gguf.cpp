@@ -201,9 +201,47 @@ double num_or(const File& f, const std::string& k, double dflt, bool* found = nu
   return (v && v->type != 8 && v->type != 9) ? v->num : dflt;
 }
 
+// the A4B recipe of a gemma4 MoE file, read as loadEngineA4B reads it
+// (src/engine-a4b.js:100-116, 150-156, 330-334): sliding layers of head dim
+// key_length_swa rotating every pair with theta 1e4, full layers of head dim
+// key_length rotating floor(0.25 * key_length / 2) pairs with theta 1e6 and
+// V = K, KV heads per layer, a MoE half of expert_count experts (top 8) of
+// expert_feed_forward_length beside the dense feed_forward_length branch,
+// the ring window + 512 slots; theta 1e4 / 1e6 as the recipe fixes them
+// (src/engine-a4b.js:329)
+int gguf_config_a4b(const File& f, const std::string& p, e4b_config* cfg, int32_t* layer_kv_heads, int cap) {
+  cfg->recipe = E4B_RECIPE_A4B;
+  cfg->ple_dim = 0;
+  const int used = (int)num_or(f, p + "expert_used_count", 8);
+  if (used != 8) return e4b_fail(E4B_EINVAL, "GGUF: expert_used_count %d (the MoE kernels select 8)", used);
+  cfg->n_experts = (int32_t)num_or(f, p + "expert_count", cfg->n_experts);
+  cfg->expert_ffn = (int32_t)num_or(f, p + "expert_feed_forward_length", cfg->expert_ffn);
+  cfg->head_dim_full = (int32_t)num_or(f, p + "attention.key_length", cfg->head_dim_full);
+  cfg->head_dim = (int32_t)num_or(f, p + "attention.key_length_swa", cfg->head_dim);
+  cfg->rope_angles = cfg->head_dim / 2;
+  cfg->rope_angles_full = (int32_t)(0.25 * cfg->head_dim_full / 2);
+  cfg->theta_local = 10000.0f;  // fixed by the recipe, not read from the file
+  cfg->theta_global = 1000000.0f;
+  if (cfg->ring < cfg->window + 512) cfg->ring = cfg->window + 512;
+  if (const Value* kvh = f.find(p + "attention.head_count_kv")) {
+    if (kvh->type == 9) {
+      if ((int)kvh->arr.size() != cfg->layers)
+        return e4b_fail(E4B_EINVAL, "GGUF: attention.head_count_kv lists %zu layers, not %d", kvh->arr.size(),
+                        cfg->layers);
+      if (!layer_kv_heads || cap < cfg->layers)
+        return e4b_fail(E4B_EINVAL, "e4b_gguf_config: layer_kv_heads needs room for %d layers", cfg->layers);
+      for (int i = 0; i < cfg->layers; ++i) layer_kv_heads[i] = (int32_t)kvh->arr[(size_t)i];
+      cfg->layer_kv_heads = layer_kv_heads;
+      cfg->kv_heads = layer_kv_heads[0];
+    }
+  }
+  return E4B_OK;
+}
+
 }  // namespace
 
-extern "C" int e4b_gguf_config(const char* path, e4b_config* cfg, uint8_t* layer_global, int cap) {
+extern "C" int e4b_gguf_config(const char* path, e4b_config* cfg, uint8_t* layer_global, int32_t* layer_kv_heads,
+                               int cap) {
   if (!cfg) return e4b_fail(E4B_EINVAL, "e4b_gguf_config: null config");
   File f;
   int rc = open_file(path, &f);
@@ -227,6 +265,11 @@ extern "C" int e4b_gguf_config(const char* path, e4b_config* cfg, uint8_t* layer
   } flts[] = {{"rope.freq_base_swa", &cfg->theta_local}, {"rope.freq_base", &cfg->theta_global},
               {"attention.layer_norm_rms_epsilon", &cfg->eps}, {"final_logit_softcapping", &cfg->softcap}};
   for (const FloatKey& k : flts) *k.dst = (float)num_or(f, p + k.key, *k.dst);
+  // the vocabulary of a file without vocab_size: the embedding's row count
+  if (!f.find(p + "vocab_size"))
+    for (const TensorInfo& t : f.tensors)
+      if (t.name == "token_embd.weight" && t.nd >= 2) cfg->vocab = (int32_t)t.dims[1];
+  if (f.find(p + "expert_count") && (rc = gguf_config_a4b(f, p, cfg, layer_kv_heads, cap))) return rc;
   if (const Value* pat = f.find(p + "attention.sliding_window_pattern")) {
     if (pat->type != 9 || (int)pat->arr.size() != cfg->layers)
       return e4b_fail(E4B_EINVAL, "GGUF: sliding_window_pattern must list %d layers", cfg->layers);
@@ -264,7 +307,8 @@ extern "C" e4b_ctx* e4b_open_gguf(const char* path, const e4b_config* base) {
     cfg.max_seq = 4096;
   }
   std::vector<uint8_t> lg(4096);
-  if (e4b_gguf_config(path, &cfg, lg.data(), (int)lg.size())) return nullptr;
+  std::vector<int32_t> kvh(4096);
+  if (e4b_gguf_config(path, &cfg, lg.data(), kvh.data(), (int)lg.size())) return nullptr;
   e4b_ctx* c = e4b_create(&cfg);
   if (!c) return nullptr;
   if (e4b_load_gguf(c, path) || e4b_finalize(c)) {

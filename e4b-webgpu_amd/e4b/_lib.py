@@ -116,7 +116,7 @@ SIGNATURES = [
     ("e4b_read_scores", _i32, [_vp, _i32, _vp]),
     ("e4b_kv_compact", _i32, [_vp, _i32, _i32]),
     ("e4b_kv_select", _i64, [_vp, _i32, _i64, _i64, _i32, _i32, _vp]),
-    ("e4b_gguf_config", _i32, [C.c_char_p, _vp, _vp, _i32]),
+    ("e4b_gguf_config", _i32, [C.c_char_p, _vp, _vp, _vp, _i32]),
     ("e4b_load_gguf", _i32, [_vp, C.c_char_p]),
     ("e4b_open_gguf", _vp, [C.c_char_p, _vp]),
 ]

@@ -33,9 +33,29 @@ _KV = {
     "eps": "attention.layer_norm_rms_epsilon", "softcap": "final_logit_softcapping",
 }
 ARCH = "e4b"
+# the gemma4 MoE keys loadEngineA4B reads (src/engine-a4b.js:100-116); the
+# full layers' head dim is key_length, the sliding layers' key_length_swa,
+# head_count_kv is a per-layer array
+_KV_A4B = {
+    "hidden": "embedding_length", "layers": "block_count", "q_heads": "attention.head_count",
+    "ffn": "feed_forward_length", "expert_ffn": "expert_feed_forward_length", "n_experts": "expert_count",
+    "window": "attention.sliding_window", "eps": "attention.layer_norm_rms_epsilon",
+    "softcap": "final_logit_softcapping", "head_dim_full": "attention.key_length",
+    "head_dim": "attention.key_length_swa", "vocab": "vocab_size",
+}
+ARCH_A4B = "gemma4"
+TOP_K = 8  # expert_used_count the MoE kernels select
 
 
 def config_to_kv(cfg: E4BConfig) -> dict:
+    if cfg.recipe == 1:
+        kv = {"general.architecture": ARCH_A4B}
+        for f, k in _KV_A4B.items():
+            kv[f"{ARCH_A4B}.{k}"] = getattr(cfg, f)
+        kv[f"{ARCH_A4B}.expert_used_count"] = TOP_K
+        kv[f"{ARCH_A4B}.attention.head_count_kv"] = [int(cfg.layer_shape(i)[0]) for i in range(cfg.layers)]
+        kv[f"{ARCH_A4B}.attention.sliding_window_pattern"] = [not bool(g) for g in cfg.layer_global]
+        return kv
     kv = {"general.architecture": ARCH}
     for f, k in _KV.items():
         kv[f"{ARCH}.{k}"] = getattr(cfg, f)
@@ -43,8 +63,34 @@ def config_to_kv(cfg: E4BConfig) -> dict:
     return kv
 
 
+def _a4b_from_kv(kv: dict, arch: str, overrides: dict) -> E4BConfig:
+    """The A4B recipe of a gemma4 key set, as e4b_gguf_config derives it."""
+    args = {f: kv[f"{arch}.{k}"] for f, k in _KV_A4B.items() if f"{arch}.{k}" in kv}
+    if int(kv.get(f"{arch}.expert_used_count", TOP_K)) != TOP_K:
+        raise ValueError(f"expert_used_count {kv[f'{arch}.expert_used_count']} (the MoE kernels select {TOP_K})")
+    args.update(recipe=1, ple_dim=0)
+    kvh = kv.get(f"{arch}.attention.head_count_kv")
+    if isinstance(kvh, (list, tuple)):
+        args["layer_kv_heads"] = [int(x) for x in kvh]
+        args["kv_heads"] = int(kvh[0])
+    pat = kv.get(f"{arch}.attention.sliding_window_pattern")
+    if pat is not None:
+        args["layer_global"] = [0 if s else 1 for s in pat]
+    args.update(overrides)
+    hd = int(args.get("head_dim", E4BConfig.head_dim))
+    hdf = int(args.get("head_dim_full", 512))
+    args.update(rope_angles=hd // 2, rope_angles_full=int(0.25 * hdf / 2), theta_local=1e4, theta_global=1e6)
+    args["ring"] = max(int(args.get("ring", E4BConfig.ring)), int(args.get("window", E4BConfig.window)) + 512)
+    for f in ("eps", "softcap"):
+        if f in args:
+            args[f] = float(args[f])
+    return E4BConfig(**args)
+
+
 def config_from_kv(kv: dict, **overrides) -> E4BConfig:
     arch = kv.get("general.architecture", ARCH)
+    if f"{arch}.expert_count" in kv:
+        return _a4b_from_kv(kv, arch, overrides)
     args = {}
     for f, k in _KV.items():
         key = f"{arch}.{k}"
@@ -60,30 +106,35 @@ def config_from_kv(kv: dict, **overrides) -> E4BConfig:
     return E4BConfig(**args)
 
 
+_INT_FIELDS = ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
+               "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags", "recipe", "head_dim_full",
+               "rope_angles_full", "n_experts", "expert_ffn")
+_FLOAT_FIELDS = ("theta_local", "theta_global", "eps", "softcap")
+
+
 def gguf_config(path: str, **overrides) -> E4BConfig:
     """The engine configuration of a GGUF file as the library reads it
     (e4b_gguf_config); fields the file cannot hold (ring, max_seq, ...) come
     from the E4BConfig defaults or `overrides`."""
     base = E4BConfig(**overrides)
     c = ConfigC()
-    for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
-              "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags"):
+    for f in _INT_FIELDS:
         setattr(c, f, int(getattr(base, f)))
-    for f in ("theta_local", "theta_global", "eps", "softcap"):
+    for f in _FLOAT_FIELDS:
         setattr(c, f, float(getattr(base, f)))
     lg = np.zeros(4096, np.uint8)
-    check(lib.e4b_gguf_config(path.encode(), C.byref(c), _p(lg), lg.size), "e4b_gguf_config")
-    args = {f: getattr(c, f) for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim",
-                                          "vocab", "window", "ring", "max_seq", "rope_angles", "attn_chunk",
-                                          "max_prompt", "flags")}
-    args.update({f: float(getattr(c, f)) for f in ("theta_local", "theta_global", "eps", "softcap")})
+    kvh = np.zeros(4096, np.int32)
+    check(lib.e4b_gguf_config(path.encode(), C.byref(c), _p(lg), _p(kvh), lg.size), "e4b_gguf_config")
+    args = {f: getattr(c, f) for f in _INT_FIELDS}
+    args.update({f: float(getattr(c, f)) for f in _FLOAT_FIELDS})
     if c.layer_global:
         args["layer_global"] = [int(x) for x in lg[:c.layers]]
     elif "layer_global" in overrides:
         args["layer_global"] = list(overrides["layer_global"])
-    for k, v in overrides.items():
-        if k in ("ring", "max_seq", "attn_chunk", "max_prompt", "flags"):
-            args[k] = v
+    if c.layer_kv_heads:
+        args["layer_kv_heads"] = [int(x) for x in kvh[:c.layers]]
+    elif "layer_kv_heads" in overrides:
+        args["layer_kv_heads"] = list(overrides["layer_kv_heads"])
     return E4BConfig(**args)
 
 
@@ -97,11 +148,9 @@ class Engine:
     def __init__(self, cfg: E4BConfig, tensors=None):
         self.cfg = cfg
         c = ConfigC()
-        for f in ("hidden", "layers", "q_heads", "kv_heads", "head_dim", "ffn", "ple_dim", "vocab", "window", "ring",
-                  "max_seq", "rope_angles", "attn_chunk", "max_prompt", "flags", "recipe", "head_dim_full",
-                  "rope_angles_full", "n_experts", "expert_ffn"):
+        for f in _INT_FIELDS:
             setattr(c, f, int(getattr(cfg, f)))
-        for f in ("theta_local", "theta_global", "eps", "softcap"):
+        for f in _FLOAT_FIELDS:
             setattr(c, f, float(getattr(cfg, f)))
         self._lg = np.ascontiguousarray(np.asarray(cfg.layer_global, np.uint8))
         c.layer_global = _p(self._lg)
@@ -142,6 +191,10 @@ class Engine:
     @classmethod
     def from_gguf(cls, path: str, **overrides) -> "Engine":
         g = open_gguf(path)
+        arch = g.kv.get("general.architecture", ARCH)
+        emb = g.tensors.get("token_embd.weight")
+        if f"{arch}.vocab_size" not in g.kv and emb is not None and len(emb["dims"]) >= 2:
+            overrides.setdefault("vocab", int(emb["dims"][1]))  # the embedding's row count
         cfg = config_from_kv(g.kv, **overrides)
         eng = cls(cfg)
         for name in g.tensors:

@@ -149,7 +149,9 @@ napi_value create(napi_env env, napi_callback_info info) {
               {"kvHeads", &cfg.kv_heads}, {"headDim", &cfg.head_dim}, {"ffn", &cfg.ffn},
               {"pleDim", &cfg.ple_dim}, {"vocab", &cfg.vocab}, {"window", &cfg.window},
               {"ring", &cfg.ring}, {"maxSeq", &cfg.max_seq}, {"ropeAngles", &cfg.rope_angles},
-              {"attnChunk", &cfg.attn_chunk}, {"maxPrompt", &cfg.max_prompt}};
+              {"attnChunk", &cfg.attn_chunk}, {"maxPrompt", &cfg.max_prompt}, {"recipe", &cfg.recipe},
+              {"headDimFull", &cfg.head_dim_full}, {"ropeAnglesFull", &cfg.rope_angles_full},
+              {"nExperts", &cfg.n_experts}, {"expertFfn", &cfg.expert_ffn}};
   for (const IntField& f : ints) {
     napi_value v;
     bool has = false;
@@ -207,7 +209,28 @@ napi_value create(napi_env env, napi_callback_info info) {
       cfg.layer_global = lg.data();
     }
   }
-  e4b_ctx* c = e4b_create(&cfg);  // copies the config (and the layer pattern)
+  std::vector<int32_t> kvh;  // KV heads per layer (the A4B recipe)
+  {
+    bool has = false;
+    CHECK_NAPI(napi_has_named_property(env, argv[0], "layerKvHeads", &has));
+    if (has) {
+      napi_value arr;
+      CHECK_NAPI(napi_get_named_property(env, argv[0], "layerKvHeads", &arr));
+      uint32_t n = 0;
+      if (napi_get_array_length(env, arr, &n) != napi_ok) return throw_msg(env, "create: layerKvHeads must be an array");
+      kvh.resize(n);
+      for (uint32_t i = 0; i < n; ++i) {
+        napi_value e;
+        CHECK_NAPI(napi_get_element(env, arr, i, &e));
+        int64_t x = 0;
+        if (!get_i64(env, e, &x)) return throw_msg(env, "create: layerKvHeads entries must be integers");
+        kvh[i] = (int32_t)x;
+      }
+      if ((int32_t)n != cfg.layers) return throw_msg(env, "create: layerKvHeads length must equal layers");
+      cfg.layer_kv_heads = kvh.data();
+    }
+  }
+  e4b_ctx* c = e4b_create(&cfg);  // copies the config (and the per-layer arrays)
   if (!c) return throw_lib(env, "create", -1);
   Ctx* x = new Ctx{c, cfg.vocab, cfg.hidden, cfg.q_heads, cfg.max_seq};
   napi_value ext;

@@ -30,8 +30,46 @@ const FLAG_NO_GRAPH = 1, FLAG_STEP_PREFILL = 2, FLAG_KV_SCORE = 4;
 // long-context constants (src/engine-a4b.js:18-20)
 const KV_BUDGET = 640, KV_DECAP = 768, KV_PROTECT = 64;
 
+// the gemma4 MoE keys loadEngineA4B reads (src/engine-a4b.js:100-116): the
+// A4B recipe (recipe 1) -- head dims key_length (full) / key_length_swa
+// (sliding), KV heads per layer, a quarter of the full layers' pairs
+// rotated, theta 1e4 / 1e6 (:329), the ring window + 512 slots (:198)
+const KV_A4B = {
+  hidden: "embedding_length", layers: "block_count", qHeads: "attention.head_count",
+  ffn: "feed_forward_length", expertFfn: "expert_feed_forward_length", nExperts: "expert_count",
+  window: "attention.sliding_window", eps: "attention.layer_norm_rms_epsilon", softcap: "final_logit_softcapping",
+  headDimFull: "attention.key_length", headDim: "attention.key_length_swa", vocab: "vocab_size",
+};
+const RECIPE_A4B = 1, TOP_K = 8;
+
+function configFromKVA4B(kv, arch, overrides) {
+  const C = Object.assign({}, DEFAULTS, { recipe: RECIPE_A4B, pleDim: 0 });
+  for (const [f, k] of Object.entries(KV_A4B)) {
+    const key = `${arch}.${k}`;
+    if (kv[key] !== undefined) C[f] = kv[key];
+  }
+  const used = kv[`${arch}.expert_used_count`];
+  if (used !== undefined && used !== TOP_K) throw new Error(`expert_used_count ${used} (the MoE kernels select ${TOP_K})`);
+  const kvh = kv[`${arch}.attention.head_count_kv`];
+  if (Array.isArray(kvh)) {
+    C.layerKvHeads = kvh.map(Number);
+    C.kvHeads = C.layerKvHeads[0];
+  }
+  const pat = kv[`${arch}.attention.sliding_window_pattern`];
+  if (pat !== undefined) C.layerGlobal = pat.map((s) => (s ? 0 : 1));
+  Object.assign(C, overrides);
+  C.ropeAngles = C.headDim / 2;
+  C.ropeAnglesFull = Math.floor((0.25 * C.headDimFull) / 2);
+  C.thetaLocal = 10000.0;
+  C.thetaGlobal = 1000000.0;
+  C.ring = Math.max(C.ring, C.window + 512);
+  if (!C.layerGlobal) C.layerGlobal = Array.from({ length: C.layers }, (_, i) => (i % 6 === 5 ? 1 : 0));
+  return C;
+}
+
 function configFromKV(kv, overrides = {}) {
   const arch = kv["general.architecture"] || "e4b";
+  if (kv[`${arch}.expert_count`] !== undefined) return configFromKVA4B(kv, arch, overrides);
   const C = Object.assign({}, DEFAULTS);
   for (const [f, k] of Object.entries(KV)) {
     const key = `${arch}.${k}`;
@@ -46,6 +84,10 @@ function configFromKV(kv, overrides = {}) {
 
 async function loadEngine(file, overrides = {}) {
   const g = openGGUF(file);
+  const arch = g.kv["general.architecture"] || "e4b";
+  const emb = g.tensors["token_embd.weight"];
+  if (g.kv[`${arch}.vocab_size`] === undefined && emb && emb.dims.length >= 2 && overrides.vocab === undefined)
+    overrides = Object.assign({}, overrides, { vocab: Number(emb.dims[1]) });  // the embedding's row count
   const C = configFromKV(g.kv, overrides);
   const ctx = addon.create(C);
   try {

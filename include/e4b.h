@@ -432,13 +432,24 @@ int64_t e4b_kv_select(const float* score, int q_heads, int64_t stride, int64_t n
  *     attention.layer_norm_rms_epsilon, final_logit_softcapping and
  *     attention.sliding_window_pattern (true = sliding) into cfg; fields the
  *     file lacks keep the caller's values (ring, max_seq, attn_chunk,
- *     max_prompt and flags are never in the file); the layer pattern is
- *     written to layer_global[cap] and cfg->layer_global points to it.
+ *     max_prompt and flags are never in the file); a file without
+ *     vocab_size takes the row count of token_embd.weight; the layer
+ *     pattern is written to layer_global[cap] and cfg->layer_global points
+ *     to it.  A file with <arch>.expert_count (the gemma4 26B-A4B MoE that
+ *     loadEngineA4B loads, src/engine-a4b.js:100-116) selects
+ *     E4B_RECIPE_A4B: head_dim = attention.key_length_swa, head_dim_full =
+ *     attention.key_length, rope_angles = head_dim / 2, rope_angles_full =
+ *     floor(0.25 * head_dim_full / 2), theta 1e4 / 1e6 whatever the file
+ *     says (the recipe fixes them, src/engine-a4b.js:329), n_experts /
+ *     expert_ffn from expert_count / expert_feed_forward_length
+ *     (expert_used_count must be 8), ple_dim 0, ring >= window + 512, and
+ *     the per-layer attention.head_count_kv array into layer_kv_heads[cap]
+ *     (cfg->layer_kv_heads points to it).
  *   e4b_load_gguf: e4b_set_tensor for every tensor of the file (call
  *     e4b_finalize afterwards).
  *   e4b_open_gguf: config (from `base`, or ring 1024 / max_seq 4096 when
  *     NULL) + create + load + finalize in one call; NULL on error. */
-int  e4b_gguf_config(const char* path, e4b_config* cfg, uint8_t* layer_global, int cap);
+int  e4b_gguf_config(const char* path, e4b_config* cfg, uint8_t* layer_global, int32_t* layer_kv_heads, int cap);
 int  e4b_load_gguf(e4b_ctx* ctx, const char* path);
 e4b_ctx* e4b_open_gguf(const char* path, const e4b_config* base);
 

@@ -176,3 +176,43 @@ def test_a4b_engine_is_graph_replayed_and_gpu_fed():
     for i in range(12):
         step.append(b.step(step[-1], len(prompt) + i))
     assert fed == step
+
+
+def test_a4b_gguf_loaders_and_js_host_agree(tmp_path):
+    # an A4B-recipe model written as a gemma4 GGUF file, loaded by the Python
+    # reader (Engine.from_gguf), the library's own loader (load_native) and
+    # the JS host (node run_greedy.js): the same configuration and, over the
+    # same library, the same greedy tokens as the engine built from the
+    # tensors directly
+    import json
+    import os
+    import subprocess
+
+    from e4b.engine import config_to_kv
+    from e4b.gguf import write_gguf
+    from tests.test_js_host import JS, NODE
+    cfg = tiny_a4b_config(ring=8 + 512)  # the ring a gemma4 file gets: window + 512
+    tensors = norm_weights_random(synth_tensors(cfg, 71), 72)
+    path = tmp_path / "a4b.gguf"
+    write_gguf(str(path), config_to_kv(cfg), [(t.name, t.ggml_type, t.dims, t.data) for t in tensors.values()])
+    prompt = [int(x) for x in np.random.default_rng(71).integers(0, cfg.vocab, 10)]
+    ref = Engine(cfg, tensors)
+    want = ref.generate_fast(prompt, 16, eos=())
+    ref.reset()
+    steps = [ref.step(t, i) for i, t in enumerate(prompt)]
+    for eng in (Engine.from_gguf(str(path), ring=cfg.ring, max_seq=cfg.max_seq),
+                Engine.load_native(str(path), ring=cfg.ring, max_seq=cfg.max_seq)):
+        for f in ("recipe", "layers", "head_dim", "head_dim_full", "rope_angles_full", "n_experts", "ring",
+                  "layer_global", "layer_kv_heads"):
+            assert getattr(eng.cfg, f) == getattr(cfg, f), f
+        assert eng.generate_fast(prompt, 16, eos=()) == want
+    if NODE is None or not os.path.exists(os.path.join(JS, "e4b_napi.node")):
+        pytest.skip("node or the N-API addon is missing")
+    over = {"ring": cfg.ring, "maxSeq": cfg.max_seq}
+    r = subprocess.run([NODE, os.path.join(JS, "run_greedy.js"), str(path), ",".join(map(str, prompt)), "16",
+                        json.dumps(over)], check=True, capture_output=True, text=True, timeout=300)
+    js = json.loads(r.stdout.strip().splitlines()[-1])
+    print(f"A4B gguf: tokens {want[:8]}..., js {js['generate'][:8]}...")
+    assert js["generate"] == want and js["generate_prefill"] == want and js["steps"] == steps
+    roles = {name for name, _, _ in js["profile_step"]}
+    assert {"headprep", "attn_sliding", "attn_global", "moe_ffn", "lm_head"} <= roles

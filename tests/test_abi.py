@@ -225,3 +225,46 @@ def test_kv_select_rejects_bad_arguments():
     assert sel(p, 2, 4, 8, 2, 1, k) < 0   # n beyond the stride
     assert sel(p, 2, 4, 4, -1, 1, k) < 0  # negative budget
     assert sel(None, 2, 4, 4, 2, 1, k) < 0
+
+
+def test_native_gguf_config_a4b(tmp_path):
+    # a gemma4 MoE key set (src/engine-a4b.js:100-116) selects the A4B recipe
+    # in both readers: head dims from key_length(_swa), per-layer KV heads
+    # from the head_count_kv array, the recipe's theta and rotated pairs, the
+    # ring widened to window + 512, the vocabulary from the embedding's rows
+    # when vocab_size is absent; a head_count_kv array of the wrong length
+    # and an expert_used_count other than 8 are refused
+    from e4b._lib import E4BError
+    from e4b.engine import config_from_kv, config_to_kv, gguf_config
+    from e4b.gguf import write_gguf
+    from e4b.model import synth_tensors, tiny_a4b_config
+    cfg = tiny_a4b_config(layer_global=[0, 1, 0, 1], layer_kv_heads=[2, 1, 8, 2], window=8, ring=24)
+    t = [(x.name, x.ggml_type, x.dims, x.data) for x in synth_tensors(cfg, 5).values()]
+    kv = config_to_kv(cfg)
+    assert kv["general.architecture"] == "gemma4" and kv["gemma4.attention.key_length"] == 512
+    del kv["gemma4.vocab_size"]
+    kv["gemma4.rope.freq_base"] = 5.0  # the recipe fixes theta whatever the file says
+    path = tmp_path / "a4b.gguf"
+    write_gguf(str(path), kv, t)
+    for got in (gguf_config(str(path), ring=cfg.ring, max_seq=cfg.max_seq),
+                config_from_kv(kv, vocab=cfg.vocab, ring=cfg.ring, max_seq=cfg.max_seq)):
+        for f in ("recipe", "hidden", "layers", "q_heads", "head_dim", "head_dim_full", "rope_angles",
+                  "rope_angles_full", "ffn", "n_experts", "expert_ffn", "ple_dim", "vocab", "window", "max_seq"):
+            assert getattr(got, f) == getattr(cfg, f), f
+        assert got.ring == cfg.window + 512  # the reference's kvSlots (src/engine-a4b.js:198)
+        assert (got.theta_local, got.theta_global) == (1e4, 1e6)
+        assert got.layer_global == [0, 1, 0, 1] and got.layer_kv_heads == [2, 1, 8, 2]
+        assert [got.layer_shape(i) for i in range(4)] == [cfg.layer_shape(i) for i in range(4)]
+    assert gguf_config(str(path), ring=4096).ring == 4096  # a larger ring is kept
+    bad = dict(kv)
+    bad["gemma4.attention.head_count_kv"] = [2, 1, 8]
+    write_gguf(str(tmp_path / "kvh.gguf"), bad, t)
+    with pytest.raises(E4BError, match="head_count_kv"):
+        gguf_config(str(tmp_path / "kvh.gguf"))
+    bad = dict(kv)
+    bad["gemma4.expert_used_count"] = 4
+    write_gguf(str(tmp_path / "topk.gguf"), bad, t)
+    with pytest.raises(E4BError, match="expert_used_count"):
+        gguf_config(str(tmp_path / "topk.gguf"))
+    with pytest.raises(ValueError, match="expert_used_count"):
+        config_from_kv(bad)

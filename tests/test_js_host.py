@@ -211,3 +211,38 @@ def test_native_gguf_loader_matches_python_loader(tmp_path):
     ga, gb = a.generate_fast(prompt, 16, eos=()), b.generate_fast(prompt, 16, eos=())
     assert ga == gb
     assert np.array_equal(a.read_logits(), b.read_logits())
+
+
+@_needs_node
+def test_node_config_a4b_matches_python(tmp_path):
+    # the JS loader's configFromKV reads a gemma4 key set (src/engine-a4b.js
+    # :100-116) into the same A4B configuration as the Python and native
+    # readers, the vocabulary from the embedding's rows when absent
+    from e4b.engine import gguf_config
+    from e4b.model import tiny_a4b_config
+    cfg = tiny_a4b_config(layer_global=[0, 1, 0, 1], layer_kv_heads=[2, 1, 8, 2])
+    kv = config_to_kv(cfg)
+    del kv["gemma4.vocab_size"]
+    path = tmp_path / "a4b.gguf"
+    write_gguf(str(path), kv, [(t.name, t.ggml_type, t.dims, t.data) for t in synth_tensors(cfg, 3).values()])
+    code = f"""
+const {{ openGGUF }} = require('./gguf');
+const {{ configFromKV }} = require('./engine');
+const g = openGGUF({json.dumps(str(path))});
+const emb = g.tensors['token_embd.weight'];
+console.log(JSON.stringify(configFromKV(g.kv, {{ vocab: emb.dims[1], maxSeq: {cfg.max_seq} }})));
+g.close();
+"""
+    js = json.loads(_node(code))
+    nat = gguf_config(str(path), max_seq=cfg.max_seq)
+    for jf, pf in (("recipe", "recipe"), ("hidden", "hidden"), ("layers", "layers"), ("qHeads", "q_heads"),
+                   ("kvHeads", "kv_heads"), ("headDim", "head_dim"), ("headDimFull", "head_dim_full"),
+                   ("ropeAngles", "rope_angles"), ("ropeAnglesFull", "rope_angles_full"), ("ffn", "ffn"),
+                   ("nExperts", "n_experts"), ("expertFfn", "expert_ffn"), ("pleDim", "ple_dim"), ("vocab", "vocab"),
+                   ("window", "window"), ("ring", "ring"), ("maxSeq", "max_seq"), ("layerGlobal", "layer_global"),
+                   ("layerKvHeads", "layer_kv_heads")):
+        assert js[jf] == getattr(nat, pf), jf
+    for jf, pf in (("thetaLocal", "theta_local"), ("thetaGlobal", "theta_global"), ("eps", "eps"),
+                   ("softcap", "softcap")):
+        assert abs(js[jf] - getattr(nat, pf)) <= 1e-6 * abs(getattr(nat, pf)), jf
+    assert nat.vocab == cfg.vocab and nat.layer_kv_heads == [2, 1, 8, 2]
