@@ -745,12 +745,14 @@ namespace {
 int record_step_persist(e4b_ctx* c);
 
 // One token of the A4B recipe (the reference's encodeForward / encodeLayer,
-// src/engine-a4b.js:424-463, 683-693): embedding; per layer the input norm,
-// q|k(|v), head prep with the K/V write, split-K attention and its merge,
-// o, the attention residual, then the MoE half (router + top-8, dense and
-// expert gate/up + GeGLU, dense and expert down, a4btail); final norm,
-// lm-head + argmax, feedback.  The residual stream is c->h at layer
-// boundaries and c->hb after the attention residual.
+// src/engine-a4b.js:424-463, 683-693): embedding; per layer the q|k(|v)
+// GEMV (whose prologue runs the previous layer's MoE tail and this layer's
+// input norm), head prep with the K/V write, split-K attention and its
+// merge, o, then the MoE half (router with the attention residual, top-8,
+// dense and expert gate/up + GeGLU, dense and expert down); after the last
+// layer its tail, the final norm, lm-head + argmax, feedback.  The residual
+// stream is c->h at layer boundaries and c->hb (h1) after the attention
+// residual.
 int record_step_a4b(e4b_ctx* c) {
   const e4b_config& k = c->cfg;
   const int H = k.hidden, QH = k.q_heads, E = k.n_experts, FE = k.expert_ffn, FF = k.ffn;
@@ -764,10 +766,29 @@ int record_step_a4b(e4b_ctx* c) {
   for (int l = 0; l < k.layers; ++l) {
     const Layer& ly = c->L[l];
     const int window = ly.global ? 0 : k.window;
+    // 1. q|k(|v) GEMV; its prologue finishes the previous layer (the MoE
+    //    tail over h1 in hb, written to h) and applies this layer's input norm
     GemvOut oq = {c->qkv, nullptr, nullptr, 0};
-    if ((rc = launch_rownorm(c->h, nullptr, nullptr, nullptr, 1.f, ly.attn_norm, c->xn, nullptr, H, k.eps, st)) ||
-        (rc = tick(c, "attn_norm")) ||
-        (rc = launch_q40(q40_view(ly.qkv, ly.qkv_rows, H), (const uint32_t*)c->xn, nullptr, EPI_F32, oq, 1, st)) ||
+    ProArgs pq{};
+    pq.tail = 1;
+    pq.H = H;
+    pq.eps = k.eps;
+    pq.w2 = ly.attn_norm;
+    pq.scale = 1.f;
+    if (l == 0) {
+      pq.hin = c->h;
+    } else {
+      const Layer& pv = c->L[l - 1];
+      pq.hin = c->hb;
+      pq.hout = c->h;
+      pq.a = c->moe.dense_out;
+      pq.a2 = c->moe.moe_out;
+      pq.w1 = pv.post_ffw1;
+      pq.w1b = pv.post_ffw2;
+      pq.wp = pv.post_ffw;
+      pq.scale = pv.scale;
+    }
+    if ((rc = launch_q40(q40_view(ly.qkv, ly.qkv_rows, H), nullptr, nullptr, EPI_F32, oq, 1, st, &pq)) ||
         (rc = tick(c, "qkv")))
       return rc;
     HeadPrepGen hp;
@@ -808,12 +829,16 @@ int record_step_a4b(e4b_ctx* c) {
         (rc = tick(c, ly.global ? "attn_global" : "attn_sliding")) ||
         (rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * ly.hd), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1,
                          st)) ||
-        (rc = tick(c, "o_proj")) ||
-        (rc = launch_rownorm(c->h, c->hb, c->o, ly.post_attn, 1.f, nullptr, nullptr, nullptr, H, k.eps, st)) ||
-        (rc = tick(c, "attn_residual")))
+        (rc = tick(c, "o_proj")))
       return rc;
+    // 2. MoE half; its router forms the attention residual h1 = h +
+    //    rms(o) post_attn into hb; the tail runs in the next layer's qkv
+    //    prologue, after the last layer in its own launch (h = the output)
     MoeArgs a = c->moe;
-    a.h = c->hb;
+    a.h = c->h;
+    a.attn_o = c->o;
+    a.post_attn = ly.post_attn;
+    a.h1 = c->hb;
     a.ffn_norm = ly.ffn_norm;
     a.router_scale = ly.router_scale;
     a.router_mult = 1.0f / sqrtf((float)H);
@@ -833,7 +858,7 @@ int record_step_a4b(e4b_ctx* c) {
     a.E = E;
     a.FF = FE;
     a.FF2 = FF;
-    a.h_out = c->h;
+    a.h_out = l == k.layers - 1 ? c->h : nullptr;
     if ((rc = launch_moe_ffn(a, st)) || (rc = tick(c, "moe_ffn"))) return rc;
   }
   c->h_final = c->h;

@@ -47,8 +47,19 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
 // grid ceil(E/2) x 128: wave w of block b scores expert 2b + w.  Every block
 // computes the rms of h itself and stages x_r = h * inv * scale * mult in LDS
 // once; each wave then streams only its expert's row.  Block b also writes
-// its slice of the two f16 GEMV inputs.
+// its slice of the two f16 GEMV inputs.  With attn_o set, every block first
+// forms the attention residual h1 = h + rms(attn_o) post_attn
+// (kernels/rmsacc3.wgsl:36-53) from its own loads, stages it in LDS for the
+// branch inputs, and block 0 writes it to h1.
 constexpr int kRouterMaxH4 = 768;  // H <= 3072
+
+DEV float4 f4_fma(float4 a, float s, float4 w, float4 b) {
+  return make_float4(fmaf(a.x * s, w.x, b.x), fmaf(a.y * s, w.y, b.y), fmaf(a.z * s, w.z, b.z),
+                     fmaf(a.w * s, w.w, b.w));
+}
+DEV float f4_ss(float4 v, float acc) {
+  return fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, acc))));
+}
 
 __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
   // token row y of a batch (the batched prefill); y = 0 in the decode step
@@ -57,24 +68,53 @@ __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
   A.xm += (int64_t)blockIdx.y * A.H;
   A.scores += (int64_t)blockIdx.y * A.E;
   __shared__ __align__(16) float4 xr[kRouterMaxH4];
+  __shared__ __align__(16) float4 h1s[kRouterMaxH4];
   __shared__ float red[2];
   constexpr int PT = kRouterMaxH4 / 128;  // float4 per thread
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int H = A.H, H4 = H / 4;
+  const bool res = A.attn_o != nullptr;
   const float4* h4 = reinterpret_cast<const float4*>(A.h);
   const float4* rs4 = reinterpret_cast<const float4*>(A.router_scale);
+  // absent residual inputs read h instead (always valid) and go unused
+  const float4* o4 = reinterpret_cast<const float4*>(res ? A.attn_o : A.h);
+  const float4* pa4 = reinterpret_cast<const float4*>(res ? A.post_attn : A.h);
   const int e = min((int)blockIdx.x * 2 + wave, A.E - 1);
   const float4* w4 = reinterpret_cast<const float4*>(A.router_w + (int64_t)e * H);
-  // every load up front: h and the scale (thread-strided), the expert row
-  float4 hv[PT], sv[PT], wv[kRouterMaxH4 / 64];
+  // every load up front: h, the scale and the residual inputs
+  // (thread-strided), the expert row
+  float4 hv[PT], sv[PT], ov[PT], pv[PT], wv[kRouterMaxH4 / 64];
 #pragma unroll
   for (int k = 0; k < PT; ++k) {
     const int i = min((int)threadIdx.x + 128 * k, H4 - 1);
     hv[k] = h4[i];
     sv[k] = rs4[i];
+    ov[k] = o4[i];
+    pv[k] = pa4[i];
   }
 #pragma unroll
   for (int k = 0; k < kRouterMaxH4 / 64; ++k) wv[k] = w4[min(lane + 64 * k, H4 - 1)];
+  if (res) {
+    float so = 0.f;
+#pragma unroll
+    for (int k = 0; k < PT; ++k)
+      if ((int)threadIdx.x + 128 * k < H4) so = f4_ss(ov[k], so);
+    so = wave_sum(so);
+    if (lane == 0) red[wave] = so;
+    lds_sync();
+    const float io = rms_inv(red[0] + red[1], H, A.eps);
+    lds_sync();  // red is reused below
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+      const int i = (int)threadIdx.x + 128 * k;
+      hv[k] = f4_fma(ov[k], io, pv[k], hv[k]);
+      if (i < H4) {
+        h1s[i] = hv[k];
+        if (writer) reinterpret_cast<float4*>(A.h1)[i] = hv[k];
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < PT; ++k)
@@ -105,8 +145,9 @@ __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
   if (lane == 0 && (int)blockIdx.x * 2 + wave < A.E) A.scores[e] = acc;
   // this block's slice of the f16 branch inputs
   const int per = (H + gridDim.x - 1) / gridDim.x;
+  const float* h1f = reinterpret_cast<const float*>(h1s);
   for (int i = blockIdx.x * per + threadIdx.x; i < min(H, (int)(blockIdx.x + 1) * per); i += 128) {
-    const float v = A.h[i] * inv;
+    const float v = (res ? h1f[i] : A.h[i]) * inv;
     A.xd[i] = f2h(v * A.ffn_norm[i]);
     A.xm[i] = f2h(v * A.pre_ffw2[i]);
   }
@@ -466,7 +507,7 @@ __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
   const int H = A.H;
   // token row blockIdx.x of a batch (one block in the decode step)
   const int64_t ro = (int64_t)blockIdx.x * H;
-  A.h += ro;
+  A.h = (A.attn_o ? A.h1 : A.h) + ro;
   A.dense_out += ro;
   A.moe_out += ro;
   A.h_out += ro;
@@ -524,6 +565,8 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
                     "MoE layer: unsupported shape (H=%d multiple of 256 <= 3072, FF2=%d <= 3072, FF=%d <= 768, "
                     "8 <= E=%d <= 256)",
                     A.H, A.FF2, A.FF, A.E);
+  if (A.attn_o && (!A.post_attn || !A.h1 || A.h1 == A.h))
+    return e4b_fail(E4B_EINVAL, "MoE layer: the attention residual needs post_attn and an h1 buffer apart from h");
   int rc = launch_moe_router(A, st);
   if (rc) return rc;
   const int64_t gu_tiles = (A.FF2 + (int64_t)K * A.FF) / 2;
@@ -532,7 +575,7 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
   const int dd_tiles = (A.H + 2 * DD_R - 1) / (2 * DD_R), de_tiles = (A.H + DE_R - 1) / DE_R;
   const int nbd = (dd_tiles + 3) / 4, nbe = (de_tiles + 3) / 4;
   hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A, nbd);
-  hipLaunchKernelGGL(k_moe_tail, dim3(1), dim3(256), 0, st, A);
+  if (A.h_out) hipLaunchKernelGGL(k_moe_tail, dim3(1), dim3(256), 0, st, A);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -27,6 +27,11 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
         pro->chunk_shift < 0 || pro->chunk_shift > 10 || pro->gch < 1 || pro->gch > q40k::kProAttnMaxCh)
       return e4b_fail(E4B_EINVAL, "q4_0 GEMV: the attention prologue needs an f32 GEMV of %d columns (got %d)",
                       kProAttnH, W.nb * 32);
+  } else if (pro && pro->tail) {
+    if (xl || ks != 1 || epi != EPI_F32 || pro->H != W.nb * 32 || pro->H % 4 || pro->H > q40k::kProTailMaxH ||
+        !pro->hin || !pro->w2 || (pro->a && (!pro->a2 || !pro->w1 || !pro->w1b || !pro->wp)))
+      return e4b_fail(E4B_EINVAL, "q4_0 GEMV: the layer-boundary prologue needs an f32 GEMV of H <= %d columns "
+                      "(multiple of 4; got %d) and all its vectors", q40k::kProTailMaxH, W.nb * 32);
   } else if (pro && (xl || ks != 1 || pro->H != W.nb * 32 || !q40_prologue_supported(pro->H) || !pro->hin ||
                      (pro->a && !pro->w1) || (pro->na > 1 && (pro->na != kMaxPartials || epi != EPI_F32)))) {
     return e4b_fail(E4B_EINVAL, "q4_0 GEMV: prologue needs f16 input of a full 256/512/1024/2048 row (H=%d, cols=%d)",
@@ -42,7 +47,20 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
   L.nbk = nbk;
   L.pa = pro ? *pro : ProArgs{};
   L.st = st;
-  const q40k::Cfg c = q40k::pick(nbk, L.units, epi, pro != nullptr, ks, pro && pro->part_o);
+  q40k::Cfg c = q40k::pick(nbk, L.units, epi, pro != nullptr, ks, pro && pro->part_o);
+  if (pro && pro->tail) {
+    // lanes: one block each up to 64-block rows, else 32 lanes x 2-3 blocks
+    // (H <= 3072); every workgroup repeats the prologue's seven vector
+    // reads, so tiles grow (up to 4 rows per lane group) while >= 256
+    // workgroups remain
+    c.kw = 1;
+    c.nwv = 4;
+    c.lpr = nbk <= 8 ? 8 : nbk <= 16 ? 16 : nbk <= 32 ? 32 : nbk <= 64 ? 64 : 32;
+    c.bpl = nbk <= 64 ? 1 : (nbk + 31) / 32;
+    c.r = 1;
+    const int64_t per_wg = 4 * (64 / c.lpr);
+    while (c.r < 4 && (L.units + per_wg * 2 * c.r - 1) / (per_wg * 2 * c.r) >= 256) c.r *= 2;
+  }
   if (c.bpl > 8 || c.lpr * c.bpl * c.kw < nbk)
     return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per slice exceeds the 2048-block (65536-column) maximum", nbk);
   bool ok;

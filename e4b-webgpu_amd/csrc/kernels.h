@@ -96,6 +96,14 @@ struct ProArgs {
   int window;              // 0 = global layer
   int chunk_shift;         // log2 of the positions per chunk
   int gch;                 // chunks allocated per head
+  // A4B layer boundary (tail != 0; any H <= 3072 divisible by 4): the
+  // previous layer's MoE tail, then this layer's input norm:
+  //   h = (hin + rms(rms(a) w1 + rms(a2) w1b) wp) * scale; x = f16(rms(h) w2)
+  // a == null (the first layer): h = hin * scale
+  int tail;
+  const float* a2;
+  const float* w1b;
+  const float* wp;
 };
 bool q40_prologue_supported(int H);
 

@@ -34,7 +34,13 @@ struct MoeArgs {
   uint16_t* g_slots;          // [8][FF] f16
   float* dense_out;           // [H]
   float* moe_out;             // [H]
-  float* h_out;               // [H]
+  float* h_out;               // [H]; null: no tail launch (a consumer's prologue finishes the layer)
+  // optional attention residual folded into the router (decode step only):
+  // h1 = h + rms(attn_o) post_attn is the FFN half's input, written to h1
+  // (a buffer other than h) by router block 0 and read by the tail
+  const float* attn_o;        // [H] o projection output, or null
+  const float* post_attn;     // [H]
+  float* h1;                  // [H]
 };
 
 // router scores (+ the f16 branch inputs)

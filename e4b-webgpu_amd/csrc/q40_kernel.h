@@ -189,6 +189,106 @@ DEV void attn_finish(const ProArgs& p, AttnRegs<U>& r, uint16_t* xs, float* wts)
   lds_sync();
 }
 
+// A4B layer-boundary prologue (ProArgs.tail): the previous layer's MoE tail
+// (kernels/a4btail.wgsl:26-71) and this layer's input norm
+// (kernels/rmsnorm.wgsl:13-51), for any H <= 3072 divisible by 4:
+//   comb = rms(a) w1 + rms(a2) w1b;  h = (hin + rms(comb) wp) * scale;
+//   x = f16(rms(h) w2); block (0,0) writes h to hout
+// with a == null (the first layer) h = hin * scale.  Thread t owns the
+// float4 groups q = t + 256 k (k < 3); groups past H/4 read the last one and
+// are masked to zero.
+constexpr int kProTail = -2;
+constexpr int kProTailK = 3;
+constexpr int kProTailMaxH = 4 * 256 * kProTailK;
+
+struct TailRegs {
+  // element 4 k + c of each vector: component c of the thread's float4 group k
+  float h[4 * kProTailK], a[4 * kProTailK], a2[4 * kProTailK], w1[4 * kProTailK], w1b[4 * kProTailK],
+      wp[4 * kProTailK], w2[4 * kProTailK];
+};
+
+DEV void ld4(const float* p, int q, float* d) {
+  const float4 t = reinterpret_cast<const float4*>(p)[q];
+  d[0] = t.x;
+  d[1] = t.y;
+  d[2] = t.z;
+  d[3] = t.w;
+}
+
+DEV void tail_issue(const ProArgs& p, TailRegs& r) {
+  const int H4 = p.H >> 2;
+  // absent vectors (the first layer) read hin instead and are masked
+  const bool has_a = p.a != nullptr;
+  const float* a = has_a ? p.a : p.hin;
+  const float* a2 = has_a ? p.a2 : p.hin;
+  const float* w1 = has_a ? p.w1 : p.hin;
+  const float* w1b = has_a ? p.w1b : p.hin;
+  const float* wp = has_a ? p.wp : p.hin;
+#pragma unroll
+  for (int k = 0; k < kProTailK; ++k) {
+    const int q = min((int)threadIdx.x + 256 * k, H4 - 1);
+    ld4(p.hin, q, r.h + 4 * k);
+    ld4(a, q, r.a + 4 * k);
+    ld4(a2, q, r.a2 + 4 * k);
+    ld4(w1, q, r.w1 + 4 * k);
+    ld4(w1b, q, r.w1b + 4 * k);
+    ld4(wp, q, r.wp + 4 * k);
+    ld4(p.w2, q, r.w2 + 4 * k);
+  }
+}
+
+DEV void tail_finish(const ProArgs& p, TailRegs& r, uint16_t* xs, float* red) {
+  constexpr int NE = 4 * kProTailK;
+  const int H4 = p.H >> 2;
+  const bool has_a = p.a != nullptr;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const bool in = (int)threadIdx.x + 256 * (e >> 2) < H4;
+    r.h[e] = in ? r.h[e] : 0.f;
+    r.a[e] = (in && has_a) ? r.a[e] : 0.f;
+    r.a2[e] = (in && has_a) ? r.a2[e] : 0.f;
+  }
+  // rms of the two branch outputs, then of their normed sum (every reduction
+  // runs, the first layer's on zeros: no branch between loads and use)
+  float sa = 0.f, sb = 0.f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    sa = fmaf(r.a[e], r.a[e], sa);
+    sb = fmaf(r.a2[e], r.a2[e], sb);
+  }
+  const float ia = rms_inv(block_sum_n<4>(sa, red), p.H, p.eps);
+  const float ib = rms_inv(block_sum_n<4>(sb, red), p.H, p.eps);
+  float sc = 0.f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    r.a[e] = fmaf(r.a[e] * ia, r.w1[e], r.a2[e] * ib * r.w1b[e]);  // comb
+    sc = fmaf(r.a[e], r.a[e], sc);
+  }
+  const float ic = has_a ? rms_inv(block_sum_n<4>(sc, red), p.H, p.eps) : 0.f;
+  float sh = 0.f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const float w = has_a ? r.wp[e] : 0.f;
+    r.h[e] = (r.h[e] + r.a[e] * ic * w) * p.scale;
+    sh = fmaf(r.h[e], r.h[e], sh);
+  }
+  const float ih = rms_inv(block_sum_n<4>(sh, red), p.H, p.eps);
+  const bool writer = p.hout && blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+  for (int k = 0; k < kProTailK; ++k) {
+    const int q = (int)threadIdx.x + 256 * k;
+    if (q < H4) {
+      const float* h = r.h + 4 * k;
+      const float* w = r.w2 + 4 * k;
+      const uint2 pk = make_uint2((uint32_t)f2h(h[0] * ih * w[0]) | ((uint32_t)f2h(h[1] * ih * w[1]) << 16),
+                                  (uint32_t)f2h(h[2] * ih * w[2]) | ((uint32_t)f2h(h[3] * ih * w[3]) << 16));
+      *reinterpret_cast<uint2*>(xs + 4 * q) = pk;
+      if (writer) reinterpret_cast<float4*>(p.hout)[q] = make_float4(h[0], h[1], h[2], h[3]);
+    }
+  }
+  lds_sync();
+}
+
 // h = (hin + rms(a) * w1) * scale; x = w2 ? f16(rms(h) * w2) : f16(h)
 // (kernels/rmsacc3.wgsl:36-53, kernels/a4btail.wgsl:54-71,
 // kernels/rmsacc.wgsl:10-26 folded into the consumer GEMV)
@@ -252,13 +352,14 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  static_assert(PROK >= kProAttn, "prologue kind");
-  static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1), "attention prologue: f32 o projection");
+  static_assert(PROK >= kProTail, "prologue kind");
+  static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1 && NWV == 4), "attention / tail prologue: f32, KW = 1");
   static_assert(R * BPL <= 64, "scale parity bits");
-  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK < 0 ? kProAttnH : 8];
+  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK == kProAttn ? kProAttnH
+                                                                  : PROK == kProTail ? kProTailMaxH : 8];
   __shared__ float red[NWV];
   __shared__ float part[KW == 4 ? 4 * SLOTS : 1];
-  __shared__ float mls[PROK < 0 ? (kProAttnH / 256) * kProAttnMaxCh : 1];
+  __shared__ float mls[PROK == kProAttn ? (kProAttnH / 256) * kProAttnMaxCh : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
@@ -275,7 +376,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   ProRegs<PROK, TPB, NA> pr;
   if constexpr (PROK > 0) pro_issue<PROK, NA, TPB>(pa, pr);
   AttnRegs<kProAttnFirst> ar;
-  if constexpr (PROK < 0) attn_issue(pa, ar);
+  if constexpr (PROK == kProAttn) attn_issue(pa, ar);
+  TailRegs tr;
+  if constexpr (PROK == kProTail) tail_issue(pa, tr);
 
   // weight tile: rows and blocks clamped into range (slots past the end are
   // computed on duplicate data and never stored; blocks past the range end
@@ -313,7 +416,8 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   uint32_t xq[BPL][XLO ? 16 : 1];
   float xs8[BPL];
   if constexpr (PROK > 0) pro_finish<PROK, TPB, NA>(pa, pr, xs_lds, red);
-  if constexpr (PROK < 0) attn_finish(pa, ar, xs_lds, mls);
+  if constexpr (PROK == kProAttn) attn_finish(pa, ar, xs_lds, mls);
+  if constexpr (PROK == kProTail) tail_finish(pa, tr, xs_lds, red);
 #pragma unroll
   for (int k = 0; k < BPL; ++k) {
     const int jb = l + LPR * k;
@@ -512,6 +616,34 @@ bool launch_plain(const Cfg& c, const Launch& L) {
 inline bool launch_pro_attn(const Cfg& c, const Launch& L) {
   if (c.bpl != 1 || c.lpr != 64) return false;
   return launch_r<64, 1, 1, false, EPI_F32, kProAttn>(c, L);
+}
+
+// A4B boundary prologue (the x vector comes from LDS): lane splits
+// (8|16|32|64, 1) and (32, 2|3), 1, 2 or 4 rows per lane group
+template <int LPR, int BPL>
+bool launch_pro_tail_r(const Cfg& c, const Launch& L) {
+  switch (c.r) {
+    case 1: launch<LPR, BPL, 1, 1, false, EPI_F32, kProTail>(L); return true;
+    case 2: launch<LPR, BPL, 2, 1, false, EPI_F32, kProTail>(L); return true;
+    case 4: launch<LPR, BPL, 4, 1, false, EPI_F32, kProTail>(L); return true;
+  }
+  return false;
+}
+inline bool launch_pro_tail(const Cfg& c, const Launch& L) {
+  if (c.kw != 1 || c.nwv != 4) return false;
+  if (c.bpl == 1) {
+    switch (c.lpr) {
+      case 8: return launch_pro_tail_r<8, 1>(c, L);
+      case 16: return launch_pro_tail_r<16, 1>(c, L);
+      case 32: return launch_pro_tail_r<32, 1>(c, L);
+      case 64: return launch_pro_tail_r<64, 1>(c, L);
+    }
+    return false;
+  }
+  if (c.lpr != 32) return false;
+  if (c.bpl == 2) return launch_pro_tail_r<32, 2>(c, L);
+  if (c.bpl == 3) return launch_pro_tail_r<32, 3>(c, L);
+  return false;
 }
 
 // fused prologue: H = 256 PROK, one block per lane (LPR = H / 32); NA
