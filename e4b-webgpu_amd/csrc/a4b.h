@@ -15,31 +15,23 @@
 int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
                    uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st);
 
-struct HeadPrepGen {
+struct AttnGen {
   const float* qkv;        // raw q [qh][hd] | k [kvh][hd] | v [kvh][hd] (no v rows when keqv)
   const float* qw;         // [hd] q head-norm weight
   const float* kw;         // [hd] k head-norm weight
   const float* inv_freq;   // [hd / 2] THETA^(-2p/hd), f32
   const uint32_t* params;  // [0] position, [kv_idx] the full layers' slot
-  float* q;                // [qh][hd] prepped queries
   uint16_t* kc;            // [kvh][slots][hd]
   uint16_t* vc;
-  int qh, kvh, hd, angles, slots, window, kv_idx;
-  bool keqv;               // V = the raw K slice (kernels/headprep.wgsl:23)
-  float eps;
-};
-int launch_headprep_gen(const HeadPrepGen& a, hipStream_t st);
-
-struct AttnGen {
-  const float* q;          // [qh][hd] prepped queries
-  const uint16_t* kc;      // [kvh][slots][hd]
-  const uint16_t* vc;
-  const uint32_t* params;  // [0] position, [kv_idx] the full layers' slot
   float* part_o;           // [qh][gch][hd] unnormalised chunk outputs
   float* part_ml;          // [qh][gch][2] (chunk max, chunk sum)
   uint16_t* out;           // [qh][hd] f16 attention output (the merge)
-  int qh, kvh, hd, slots, window, kv_idx, gch;
+  int qh, kvh, hd, angles, slots, window, kv_idx, gch;
+  bool keqv;               // V = the raw K slice (kernels/headprep.wgsl:23)
+  float eps;
 };
 constexpr int kAttnGenChunk = 64;  // positions per split-K chunk
-// split-K partials over the live chunks, then their log-sum-exp merge
+// head prep with the K/V row write, split-K partials over the live chunks,
+// then their log-sum-exp merge (two launches); head dim 256 or 512, 1, 2, 4
+// or 8 q heads per KV head
 int launch_attn_gen(const AttnGen& a, hipStream_t st);

@@ -132,7 +132,6 @@ struct e4b_ctx {
   PersistArgs pargs{};
   unsigned long long* ptrace = nullptr;  // phase trace of e4b_profile_step (allocated on first use)
   // A4B recipe: prepped queries, the MoE half's scratch
-  float* qp = nullptr;
   MoeArgs moe{};
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;       // event pool, grown on first use
@@ -523,7 +522,7 @@ int finalize_a4b(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->status, 4)) || (rc = dalloc_t(c, &c->h, (size_t)H)) ||
       (rc = dalloc_t(c, &c->hb, (size_t)H)) || (rc = dalloc_t(c, &c->rope, (size_t)hd_s)) ||
       (rc = dalloc_t(c, &c->h_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->xn, (size_t)H)) ||
-      (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) || (rc = dalloc_t(c, &c->qp, (size_t)QH * hd_max)) ||
+      (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) ||
       (rc = dalloc_t(c, &c->part_o, part)) || (rc = dalloc_t(c, &c->part_ml, ml)) ||
       (rc = dalloc_t(c, &c->attn, (size_t)QH * hd_max)) || (rc = dalloc_t(c, &c->o, (size_t)H)) ||
       (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) ||
@@ -791,41 +790,29 @@ int record_step_a4b(e4b_ctx* c) {
     if ((rc = launch_q40(q40_view(ly.qkv, ly.qkv_rows, H), nullptr, nullptr, EPI_F32, oq, 1, st, &pq)) ||
         (rc = tick(c, "qkv")))
       return rc;
-    HeadPrepGen hp;
-    hp.qkv = c->qkv;
-    hp.qw = ly.q_norm;
-    hp.kw = ly.k_norm;
-    hp.inv_freq = ly.global ? c->inv_global : c->inv_local;
-    hp.params = c->params;
-    hp.q = c->qp;
-    hp.kc = ly.kc;
-    hp.vc = ly.vc;
-    hp.qh = QH;
-    hp.kvh = ly.kvh;
-    hp.hd = ly.hd;
-    hp.angles = ly.angles;
-    hp.slots = ly.slots;
-    hp.window = window;
-    hp.kv_idx = 4;  // full layers: params[4] = the token's slot
-    hp.keqv = ly.keqv;
-    hp.eps = k.eps;
     AttnGen ag;
-    ag.q = c->qp;
+    ag.qkv = c->qkv;
+    ag.qw = ly.q_norm;
+    ag.kw = ly.k_norm;
+    ag.inv_freq = ly.global ? c->inv_global : c->inv_local;
+    ag.params = c->params;
     ag.kc = ly.kc;
     ag.vc = ly.vc;
-    ag.params = c->params;
     ag.part_o = c->part_o;
     ag.part_ml = c->part_ml;
     ag.out = c->attn;
     ag.qh = QH;
     ag.kvh = ly.kvh;
     ag.hd = ly.hd;
+    ag.angles = ly.angles;
     ag.slots = ly.slots;
     ag.window = window;
-    ag.kv_idx = 4;
+    ag.kv_idx = 4;  // full layers: params[4] = the token's slot
     ag.gch = ly.gch;
+    ag.keqv = ly.keqv;
+    ag.eps = k.eps;
     GemvOut oo = {c->o, nullptr, nullptr, 0};
-    if ((rc = launch_headprep_gen(hp, st)) || (rc = tick(c, "headprep")) || (rc = launch_attn_gen(ag, st)) ||
+    if ((rc = launch_attn_gen(ag, st)) ||
         (rc = tick(c, ly.global ? "attn_global" : "attn_sliding")) ||
         (rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * ly.hd), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1,
                          st)) ||

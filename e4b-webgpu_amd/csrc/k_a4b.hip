@@ -1,20 +1,21 @@
 // k_a4b.hip -- step kernels of the A4B recipe (src/engine-a4b.js:424-463)
 // that the E4B kernels do not cover:
-//   k_rownorm       residual + RMSNorm of one vector, any hidden size up to
-//                   4096 (kernels/rmsacc3.wgsl:36-53, kernels/rmsnorm.wgsl
-//                   :13-51; one workgroup)
-//   k_headprep_gen  q/k weighted head-RMS + NeoX RoPE over the first
-//                   `angles` pairs, scale-less v RMS with V read from the raw
-//                   K slice on KEQV layers, K/V row write at the token's slot
-//                   (kernels/headprep.wgsl:19-87), head dim 256 or 512, any
-//                   number of KV heads
-//   k_attn_chunk    split-K partials of one (q head, chunk of 64 positions):
-//                   scale-1.0 scores, the chunk's max and exponential sum, the
-//                   unnormalised P.V (kernels/attsplit.wgsl:16-76 over the
-//                   ring of attnf32.wgsl:21-105 or the counted slots of
-//                   attnos.wgsl:22-98)
-//   k_attn_merge    log-sum-exp merge of a head's live chunks to f16
-//                   (kernels/attcomb.wgsl:10-36)
+//   k_rownorm      residual + RMSNorm of one vector, any hidden size up to
+//                  4096 (kernels/rmsacc3.wgsl:36-53, kernels/rmsnorm.wgsl
+//                  :13-51; one workgroup)
+//   k_attn_gen     one layer's decode attention for head dim 256 or 512 and
+//                  1-8 q heads per KV head: head prep (q/k weighted head-RMS +
+//                  NeoX RoPE over the first `angles` pairs, scale-less v RMS,
+//                  V from the raw K slice on KEQV layers; kernels/headprep.wgsl
+//                  :19-87) with the K/V row write at the token's slot, then
+//                  the split-K partials of one (KV group, chunk of 64
+//                  positions, 128 V dims): scale-1.0 scores of every q head
+//                  of the group, the chunk's max and exponential sum, the
+//                  unnormalised P.V (kernels/attsplit.wgsl:16-76 over the
+//                  ring of attnf32.wgsl:21-105 or the counted slots of
+//                  attnos.wgsl:22-98)
+//   k_attn_merge   log-sum-exp merge of a head's live chunks to f16
+//                  (kernels/attcomb.wgsl:10-36)
 #include "../../include/e4b.h"
 #include "a4b.h"
 #include "kernels.h"
@@ -77,58 +78,6 @@ __global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ h_in,
   }
 }
 
-// one wave per head row b: q heads [0, qh), k heads [qh, qh + kvh), v heads
-// [qh + kvh, qh + 2 kvh).  Lane l holds the PER = HD / 64 contiguous dims
-// [PER l, PER l + PER): the RoPE partner of dim p < HD / 2 (p + HD / 2) sits
-// in lane l + 32.
-template <int HD>
-__global__ __launch_bounds__(64) void k_headprep_gen(HeadPrepGen A) {
-  constexpr int PER = HD / 64;
-  const int b = blockIdx.x, lane = threadIdx.x;
-  const int QH = A.qh, KVH = A.kvh;
-  const int kind = b < QH ? 0 : b < QH + KVH ? 1 : 2;  // q, k, v
-  const int g = kind == 0 ? b : kind == 1 ? b - QH : b - QH - KVH;
-  const int src = kind == 0 ? b : kind == 1 ? QH + g : (A.keqv ? QH + g : QH + KVH + g);
-  const float* xr = A.qkv + (int64_t)src * HD + PER * lane;
-  float x[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) x[i] = xr[i];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) ss = fmaf(x[i], x[i], ss);
-  const float inv = rms_inv(wave_sum(ss), HD, A.eps);
-  const float* w = kind == 0 ? A.qw : A.kw;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) x[i] = x[i] * inv * (kind < 2 ? w[PER * lane + i] : 1.f);
-  const uint32_t pos = A.params[0];
-  if (kind < 2) {
-    const float fpos = (float)pos;
-    const bool hi = lane >= 32;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      float lo_v = x[i], hi_v = x[i];
-      swapx32(lo_v, hi_v);  // lanes < 32: hi_v = partner (dim p + HD/2); lanes >= 32: lo_v = partner (dim p)
-      const float partner = hi ? lo_v : hi_v;
-      const int p = PER * (lane & 31) + i;
-      if (p < A.angles) {
-        float sn, c;
-        sincosf(fpos * A.inv_freq[p], &sn, &c);
-        x[i] = hi ? (partner * sn + x[i] * c) : (x[i] * c - partner * sn);
-      }
-    }
-  }
-  if (kind == 0) {
-    float* q = A.q + (int64_t)b * HD + PER * lane;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) q[i] = x[i];
-    return;
-  }
-  const uint32_t slot = A.window > 0 ? pos % (uint32_t)A.slots : A.params[A.kv_idx];
-  uint16_t* dst = (kind == 1 ? A.kc : A.vc) + ((int64_t)g * A.slots + slot) * HD + PER * lane;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) dst[i] = f2h(x[i]);
-}
-
 // live positions of the layer at this step: (lo, n) with the token's index
 // `cur` in the cache's own numbering (the position on a ring, the counted
 // slot on a full layer)
@@ -144,69 +93,208 @@ DEV Live live_of(const AttnGen& A) {
   return L;
 }
 
-// block (head h, chunk c); wave w scores positions j = w + 4 i of the chunk,
-// one position per pass, each lane PER = HD / 64 dims of the key
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_chunk(AttnGen A) {
-  constexpr int CS = kAttnGenChunk, PER = HD / 64, PW = CS / 4;
-  __shared__ float qs[HD];
-  __shared__ float es[CS];
-  __shared__ float red[4];
-  const int h = blockIdx.x, c = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+// Block (KV group g, chunk c, V slice z), 8 waves.  Every load is issued
+// before any math: the head-prep rows of the wave (q heads g GQA + r, the k
+// head, the v head; 10 rows at GQA 8 take two passes of the 8 waves), the
+// K rows of the wave's positions j = w + 8 i (lane l: dims [PER l, PER l +
+// PER)), and their V dims [128 z + 2 l, 128 z + 2 l + 2).  The row of the
+// token itself is not in the cache yet: it comes from the head prep (LDS),
+// and the chunk that owns it (the last live one, slice 0) stores it.
+// Scores: per position GQA dot products reduced across the wave
+// (reduce_rows), stored to LDS; softmax statistics of head h by wave h over
+// the chunk's 64 positions; P.V with the weights broadcast from LDS, folded
+// over the 8 waves.  A chunk's K is read by all HD / 128 slices (from L2
+// after the first); V is split across them.
+template <int HD, int GQA>
+__global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
+  constexpr int NW = 8, CS = kAttnGenChunk, PER = HD / 64, PW = CS / NW, VD = 128;
+  constexpr int NR = GQA + 2, RPW = (NR + NW - 1) / NW, LPH = 64 / GQA;
+  static_assert(CS == 64 && GQA <= NW && (GQA & (GQA - 1)) == 0, "64-position chunks, GQA 1/2/4/8");
+  __shared__ __align__(16) float qs[GQA][HD];
+  __shared__ __align__(16) uint16_t knew[HD];
+  __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ float es[GQA][CS];
+  __shared__ float mls[GQA][2];
+  __shared__ __align__(16) float po[NW][GQA][VD];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = blockIdx.x, c = blockIdx.y, zs = blockIdx.z;
   const Live L = live_of(A);
   const int nch = (L.n + CS - 1) / CS;
   if (c >= nch) return;
   const int c_lo = L.lo + c * CS;
   const int m = min(CS, L.n - c * CS);
-  const int g = h / (A.qh / A.kvh);
-  const uint16_t* kc = A.kc + (int64_t)g * A.slots * HD;
-  const uint16_t* vc = A.vc + (int64_t)g * A.slots * HD;
+  uint16_t* kc = A.kc + (int64_t)g * A.slots * HD;
+  uint16_t* vc = A.vc + (int64_t)g * A.slots * HD;
+  // one modulo per block: j < m <= window <= slots, the ring wraps at most once
   const int s_lo = A.window > 0 ? c_lo % A.slots : c_lo;
   auto slot_at = [&](int j) -> int64_t {
     const int s = s_lo + j;
     return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
   };
-  // the wave's key rows, requested before the query is staged
-  uint32_t kr[PW][PER / 2];
+
+  // 0. loads: head-prep rows and weights, the wave's K rows and V dims
+  float xin[RPW][PER], win[RPW][PER];
 #pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const int j = min(wave + 4 * i, m - 1);
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(kc + slot_at(j) * HD + PER * lane);
+  for (int u = 0; u < RPW; ++u) {
+    const int r = min(wave + NW * u, NR - 1);
+    const int src = r < GQA ? g * GQA + r : r == GQA || A.keqv ? A.qh + g : A.qh + A.kvh + g;
+    const float* xr = A.qkv + (int64_t)src * HD + PER * lane;
+    const float* wr = (r == GQA ? A.kw : A.qw) + PER * lane;  // v rows use no weight
 #pragma unroll
-    for (int e = 0; e < PER / 2; ++e) kr[i][e] = row[e];
-  }
-  for (int d = t; d < HD; d += 256) qs[d] = A.q[(int64_t)h * HD + d];
-  lds_sync();
-  float qv[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) qv[e] = qs[PER * lane + e];
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    float dot = 0.f;
-#pragma unroll
-    for (int e = 0; e < PER / 2; ++e) {
-      dot = fmaf(qv[2 * e], h2f((uint16_t)(kr[i][e] & 0xffffu)), dot);
-      dot = fmaf(qv[2 * e + 1], h2f((uint16_t)(kr[i][e] >> 16)), dot);
+    for (int e = 0; e < PER; e += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(xr + e);
+      const float4 w = *reinterpret_cast<const float4*>(wr + e);
+      xin[u][e] = t.x, xin[u][e + 1] = t.y, xin[u][e + 2] = t.z, xin[u][e + 3] = t.w;
+      win[u][e] = w.x, win[u][e + 1] = w.y, win[u][e + 2] = w.z, win[u][e + 3] = w.w;
     }
-    dot = wave_sum(dot);
-    const int j = wave + 4 * i;
-    if (lane == 0 && j < m) es[j] = dot;
+  }
+  uint32_t kr[PW][PER / 2];
+  uint32_t vr[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int64_t sl = slot_at(min(wave + NW * i, m - 1));
+    const uint32_t* krow = reinterpret_cast<const uint32_t*>(kc + sl * HD + PER * lane);
+    if constexpr (PER == 4) {
+      const uint2 t = *reinterpret_cast<const uint2*>(krow);
+      kr[i][0] = t.x, kr[i][1] = t.y;
+    } else {
+      const uint4 t = *reinterpret_cast<const uint4*>(krow);
+      kr[i][0] = t.x, kr[i][1] = t.y, kr[i][2] = t.z, kr[i][3] = t.w;
+    }
+    vr[i] = *reinterpret_cast<const uint32_t*>(vc + sl * HD + VD * zs + 2 * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
+
+  // 1. head prep: weighted head-RMS (v: scale-less), RoPE on q and k over the
+  //    first `angles` pairs (p, p + HD/2) -- dim p of lane l < 32 pairs with
+  //    the same register of lane l + 32
+  const bool owner = c == nch - 1;  // the last live chunk holds the token, at j = m - 1
+  const float fpos = (float)A.params[0];
+#pragma unroll
+  for (int u = 0; u < RPW; ++u) {
+    const int r = wave + NW * u;
+    if (r >= NR) break;
+    float* x = xin[u];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) ss = fmaf(x[e], x[e], ss);
+    const float inv = rms_inv(wave_sum(ss), HD, A.eps);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) x[e] = x[e] * inv * (r <= GQA ? win[u][e] : 1.f);
+    if (r <= GQA) {
+      const bool hi = lane >= 32;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        float lo_v = x[e], hi_v = x[e];
+        swapx32(lo_v, hi_v);  // lanes < 32: hi_v = dim p + HD/2; lanes >= 32: lo_v = dim p
+        const float partner = hi ? lo_v : hi_v;
+        const int p = PER * (lane & 31) + e;
+        if (p < A.angles) {
+          float sn, cs;
+          sincosf(fpos * A.inv_freq[p], &sn, &cs);
+          x[e] = hi ? (partner * sn + x[e] * cs) : (x[e] * cs - partner * sn);
+        }
+      }
+    }
+    if (r < GQA) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) qs[r][PER * lane + e] = x[e];
+    } else {
+      uint16_t* dst = r == GQA ? knew : vnew;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) dst[PER * lane + e] = f2h(x[e]);
+      if (owner && zs == 0) {
+        uint16_t* cache = (r == GQA ? kc : vc) + slot_at(m - 1) * HD + PER * lane;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) cache[e] = f2h(x[e]);
+      }
+    }
   }
   lds_sync();
-  const float s = t < m ? es[t] : -3.0e38f;
-  const float M = block_max(s, red);
-  const float e = t < m ? __expf(s - M) : 0.f;
-  const float lsum = block_sum(e, red);
-  if (t < CS) es[t] = e;
-  lds_sync();
-  for (int d = t; d < HD; d += 256) {
-    float acc = 0.f;
-    for (int j = 0; j < m; ++j) acc = fmaf(es[j], h2f(vc[slot_at(j) * HD + d]), acc);
-    A.part_o[((int64_t)h * A.gch + c) * HD + d] = acc;
+
+  // 2. scores of the wave's positions, all GQA heads: lane l ends with head
+  //    l / LPH of position j
+  {
+    float q[GQA][PER];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) q[h][e] = qs[h][PER * lane + e];
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int j = wave + NW * i;
+      uint32_t kw[PER / 2];
+#pragma unroll
+      for (int e = 0; e < PER / 2; ++e)
+        kw[e] = (c_lo + j == L.cur) ? reinterpret_cast<const uint32_t*>(knew)[PER / 2 * lane + e] : kr[i][e];
+      float t[GQA];
+#pragma unroll
+      for (int h = 0; h < GQA; ++h) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < PER / 2; ++e) {
+          a = fmaf(q[h][2 * e], h2f((uint16_t)(kw[e] & 0xffffu)), a);
+          a = fmaf(q[h][2 * e + 1], h2f((uint16_t)(kw[e] >> 16)), a);
+        }
+        t[h] = a;
+      }
+      const float sc = reduce_rows<64, GQA>(t);
+      if ((lane % LPH) == 0 && j < m) es[lane / LPH][j] = sc;
+    }
   }
-  if (t == 0) {
-    A.part_ml[((int64_t)h * A.gch + c) * 2] = M;
-    A.part_ml[((int64_t)h * A.gch + c) * 2 + 1] = lsum;
+  lds_sync();
+
+  // 3. softmax statistics of head h (wave h, lane = position)
+  if (wave < GQA) {
+    const float sv = lane < m ? es[wave][lane] : -3.0e38f;
+    const float M = wave_max(sv);
+    const float e = lane < m ? __expf(sv - M) : 0.f;
+    const float l = wave_sum(e);
+    es[wave][lane] = e;
+    if (lane == 0) {
+      mls[wave][0] = M;
+      mls[wave][1] = l;
+    }
+  }
+  lds_sync();
+
+  // 4. P.V over the wave's positions, V dims 128 z + 2 l, 2 l + 1
+  {
+    float acc[GQA][2];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) acc[h][0] = acc[h][1] = 0.f;
+    const uint32_t vn = reinterpret_cast<const uint32_t*>(vnew)[VD / 2 * zs + lane];
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int j = wave + NW * i;
+      // positions past m read a clamped row; their weight is 0 and the row is zeroed
+      const uint32_t vv = (c_lo + j == L.cur) ? vn : (j < m ? vr[i] : 0u);
+      const float v0 = h2f((uint16_t)(vv & 0xffffu)), v1 = h2f((uint16_t)(vv >> 16));
+#pragma unroll
+      for (int h = 0; h < GQA; ++h) {
+        const float p = es[h][j];
+        acc[h][0] = fmaf(p, v0, acc[h][0]);
+        acc[h][1] = fmaf(p, v1, acc[h][1]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) *reinterpret_cast<float2*>(&po[wave][h][2 * lane]) = make_float2(acc[h][0], acc[h][1]);
+  }
+  lds_sync();
+
+  // 5. fold the 8 waves into this chunk's partials ([q head][chunk][dim],
+  //    [q head][chunk][max, sum])
+  for (int o = threadIdx.x; o < GQA * VD; o += 64 * NW) {
+    const int h = o / VD, d = o % VD;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += po[w][h][d];
+    A.part_o[((int64_t)(g * GQA + h) * A.gch + c) * HD + VD * zs + d] = v;
+  }
+  if (zs == 0 && threadIdx.x < GQA) {
+    const int64_t b = (int64_t)(g * GQA + threadIdx.x) * A.gch + c;
+    A.part_ml[2 * b] = mls[threadIdx.x][0];
+    A.part_ml[2 * b + 1] = mls[threadIdx.x][1];
   }
 }
 
@@ -243,33 +331,29 @@ int launch_rownorm(const float* h_in, float* h_out, const float* a, const float*
   return E4B_OK;
 }
 
-int launch_headprep_gen(const HeadPrepGen& a, hipStream_t st) {
-  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || a.angles < 0 || a.angles > a.hd / 2 ||
-      a.slots <= 0 || (a.window > 0 && a.slots < a.window))
-    return e4b_fail(E4B_EINVAL, "head prep: head_dim %d, %d/%d heads, %d pairs, %d slots", a.hd, a.qh, a.kvh,
-                    a.angles, a.slots);
-  const dim3 grid(a.qh + 2 * a.kvh);
-  if (a.hd == 256)
-    hipLaunchKernelGGL(k_headprep_gen<256>, grid, dim3(64), 0, st, a);
-  else
-    hipLaunchKernelGGL(k_headprep_gen<512>, grid, dim3(64), 0, st, a);
-  E4B_HIP(hipGetLastError());
-  return E4B_OK;
+template <int HD>
+static void launch_attn_hd(const AttnGen& a, hipStream_t st) {
+  const dim3 grid(a.kvh, a.gch, HD / 128);
+  switch (a.qh / a.kvh) {
+    case 1: hipLaunchKernelGGL((k_attn_gen<HD, 1>), grid, dim3(512), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_attn_gen<HD, 2>), grid, dim3(512), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_attn_gen<HD, 4>), grid, dim3(512), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_attn_gen<HD, 8>), grid, dim3(512), 0, st, a); break;
+  }
+  hipLaunchKernelGGL(k_attn_merge<HD>, dim3(a.qh), dim3(256), 0, st, a);
 }
 
 int launch_attn_gen(const AttnGen& a, hipStream_t st) {
-  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || a.slots <= 0 || a.gch <= 0 ||
-      (a.window > 0 && a.slots < a.window) || (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots))
-    return e4b_fail(E4B_EINVAL, "attention: head_dim %d, %d/%d heads, %d slots, %d chunks", a.hd, a.qh, a.kvh,
-                    a.slots, a.gch);
-  const dim3 grid(a.qh, a.gch);
-  if (a.hd == 256) {
-    hipLaunchKernelGGL(k_attn_chunk<256>, grid, dim3(256), 0, st, a);
-    hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.qh), dim3(256), 0, st, a);
-  } else {
-    hipLaunchKernelGGL(k_attn_chunk<512>, grid, dim3(256), 0, st, a);
-    hipLaunchKernelGGL(k_attn_merge<512>, dim3(a.qh), dim3(256), 0, st, a);
-  }
+  const int gqa = a.kvh > 0 ? a.qh / a.kvh : 0;
+  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
+      a.angles < 0 || a.angles > a.hd / 2 || a.slots <= 0 || a.gch <= 0 || (a.window > 0 && a.slots < a.window) ||
+      (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots))
+    return e4b_fail(E4B_EINVAL, "attention: head_dim %d, %d/%d heads (1, 2, 4 or 8 per KV head), %d pairs, %d slots, "
+                    "%d chunks", a.hd, a.qh, a.kvh, a.angles, a.slots, a.gch);
+  if (a.hd == 256)
+    launch_attn_hd<256>(a, st);
+  else
+    launch_attn_hd<512>(a, st);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

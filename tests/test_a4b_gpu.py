@@ -215,4 +215,4 @@ def test_a4b_gguf_loaders_and_js_host_agree(tmp_path):
     print(f"A4B gguf: tokens {want[:8]}..., js {js['generate'][:8]}...")
     assert js["generate"] == want and js["generate_prefill"] == want and js["steps"] == steps
     roles = {name for name, _, _ in js["profile_step"]}
-    assert {"headprep", "attn_sliding", "attn_global", "moe_ffn", "lm_head"} <= roles
+    assert {"qkv", "attn_sliding", "attn_global", "o_proj", "moe_ffn", "lm_head"} <= roles
