@@ -158,18 +158,45 @@ __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
 // returns the same 8 picks (and, with WEIGHTS, their weights).  Selection on
 // the scores equals the reference's selection on p = exp(s - max) unless some
 // of the top-8 p underflow to 0 (scores more than ~87 below the maximum).
-// Branch-free: compare-and-select only, so a wave runs it in a few hundred
-// instructions.
+// Each pick is the wave maximum of a 64-bit key (the score's bits mapped to
+// an unsigned order, then the complemented expert index, so ties go to the
+// lowest index as the strict '>' scan in index order gives), reduced with
+// lane swaps and DPP moves (six short steps, no LDS round trips); the
+// picked entry's key drops to 0, below every live key.
 struct TopK {
   int idx[K];
   float w[K];
 };
 
-DEV void amax_pick(float& bv, int& bi, float& bp, float ov, int oi, float op) {
-  const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
-  bv = take ? ov : bv;
-  bi = take ? oi : bi;
-  bp = take ? op : bp;
+// the value of lane l ^ M (bit-preserving)
+template <int M>
+DEV uint32_t lane_partner(uint32_t v) {
+  if constexpr (M == 32) {
+    float a = __uint_as_float(v), b = a;
+    swapx32(a, b);  // lanes < 32: b holds lane l + 32; lanes >= 32: a holds lane l - 32
+    return __float_as_uint((threadIdx.x & 32) ? a : b);
+  } else if constexpr (M == 16) {
+    float a = __uint_as_float(v), b = a;
+    swapx16(a, b);  // even rows: b holds lane l + 16; odd rows: a holds lane l - 16
+    return __float_as_uint((threadIdx.x & 16) ? a : b);
+  } else {
+    return __float_as_uint(lane_xor<M>(__uint_as_float(v)));
+  }
+}
+
+// unsigned order of a float (larger float, larger key); -0 counts as +0,
+// which the float compare holds equal
+DEV uint32_t score_order(float s) {
+  const uint32_t u = __float_as_uint(s + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int M>
+DEV void key_max_step(uint32_t& hi, uint32_t& lo) {
+  const uint32_t ohi = lane_partner<M>(hi), olo = lane_partner<M>(lo);
+  const bool take = (ohi > hi) | ((ohi == hi) & (olo > lo));
+  hi = take ? ohi : hi;
+  lo = take ? olo : lo;
 }
 
 template <bool WEIGHTS>
@@ -182,8 +209,13 @@ DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__
     s[j] = scores[e];
     pe[j] = WEIGHTS ? pes[e] : 0.f;
   }
+  uint32_t kh[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) s[j] = lane + 64 * j < E ? s[j] : -3.0e38f;
+  for (int j = 0; j < 4; ++j) {
+    const bool live = lane + 64 * j < E;
+    s[j] = live ? s[j] : -3.0e38f;
+    kh[j] = live ? score_order(s[j]) : 0u;  // live keys are >= 1
+  }
   float M = 0.f, S = 1.f;
   if constexpr (WEIGHTS) {
     M = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
@@ -197,27 +229,38 @@ DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__
   float pk[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    // lane candidate: strict '>' in index order keeps the lowest index
-    float bv = s[0], bp = pe[0];
-    int bi = lane;
+    // lane candidate: j ascending is index ascending, so a strict '>' keeps
+    // the lowest index of equal keys
+    uint32_t bh = kh[0], bl = ~(uint32_t)lane;
 #pragma unroll
     for (int j = 1; j < 4; ++j) {
-      const bool take = s[j] > bv;
-      bv = take ? s[j] : bv;
-      bp = take ? pe[j] : bp;
-      bi = take ? lane + 64 * j : bi;
+      const bool take = kh[j] > bh;
+      bh = take ? kh[j] : bh;
+      bl = take ? ~(uint32_t)(lane + 64 * j) : bl;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-      amax_pick(bv, bi, bp, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64), __shfl_xor(bp, off, 64));
+    key_max_step<32>(bh, bl);
+    key_max_step<16>(bh, bl);
+    key_max_step<8>(bh, bl);
+    key_max_step<4>(bh, bl);
+    key_max_step<2>(bh, bl);
+    key_max_step<1>(bh, bl);
+    const int bi = __builtin_amdgcn_readfirstlane((int)~bl);
     t.idx[k] = bi;
-    pk[k] = bp;
+    const int bj = bi >> 6, bln = bi & 63;
+    float sv = s[0], pv = pe[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+      sv = bj == j ? s[j] : sv;
+      pv = bj == j ? pe[j] : pv;
+    }
+    const float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), bln));
+    pk[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), bln));
     if constexpr (WEIGHTS) {
       t.w[k] = expf(bv - M) / S;  // p_k / sum p, as the reference stores it
       wsum += t.w[k];
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = lane + 64 * j == bi ? -3.4e38f : s[j];  // below any live score
+    for (int j = 0; j < 4; ++j) kh[j] = lane + 64 * j == bi ? 0u : kh[j];
   }
   if constexpr (WEIGHTS) {
 #pragma unroll
@@ -252,6 +295,7 @@ constexpr int kMoeMaxH = GU_LPR * GU_BPL * 32;  // 3072
 
 __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   __shared__ __align__(16) uint16_t xs[2][kMoeMaxH];
+  __shared__ int sel[K];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / GU_LPR, l = lane % GU_LPR;
@@ -273,8 +317,9 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   const uint4 xm0 = reinterpret_cast<const uint4*>(A.xm)[i0], xm1 = reinterpret_cast<const uint4*>(A.xm)[i1];
 
   // 2. weight rows: dense units are known now; expert units after the top-8
-  //    selection, which every expert wave redoes from the 128 scores (wave 0
-  //    of block 0 also stores it for the down kernel)
+  //    selection, made once per workgroup by wave 0 from the 128 scores and
+  //    handed over in LDS (wave 0 of block 0 also stores the picks and their
+  //    weights for the down kernel)
   uint4 wq[2][GU_BPL];
   uint32_t ws[2][GU_BPL], odd = 0;  // aligned scale pairs (ld_scale_pair)
   auto load_rows = [&](const Q40Mat& W, int64_t row_g, int64_t row_u) {
@@ -290,33 +335,29 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
       odd |= (uint32_t)(eu & 1) << (GU_BPL + b);
     }
   };
-  int slot = 0, j = u;
   if (dense) load_rows(A.dense_gu, u, A.FF2 + u);
-  if (blockIdx.x == 0 && wave == 0) {
-    // one wave stores the picks and weights for the down kernel
-    const TopK t = select_topk<true>(A.scores, A.pes, A.E);
+  // the block holds expert waves iff its last (clamped) tile is an expert tile
+  const bool blk_expert = 2 * min((int64_t)blockIdx.x * 4 + 3, ntiles - 1) >= A.FF2;
+  if (wave == 0 && (blk_expert || blockIdx.x == 0)) {
+    TopK t;
+    if (blockIdx.x == 0) {
+      t = select_topk<true>(A.scores, A.pes, A.E);
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if (lane == k) {
+          A.topk_idx[k] = (uint32_t)t.idx[k];
+          A.topk_w[k] = t.w[k];
+        }
+    } else {
+      t = select_topk<false>(A.scores, A.pes, A.E);
+    }
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      if (lane == k) {
-        A.topk_idx[k] = (uint32_t)t.idx[k];
-        A.topk_w[k] = t.w[k];
-      }
-  }
-  if (!dense) {
-    const TopK t = select_topk<false>(A.scores, A.pes, A.E);
-    {
-      slot = (u - A.FF2) / A.FF;
-      j = (u - A.FF2) - slot * A.FF;
-      int e = t.idx[0];
-#pragma unroll
-      for (int k = 1; k < K; ++k)
-        if (slot == k) e = t.idx[k];
-      const int64_t row_g = (int64_t)e * 2 * A.FF + j;
-      load_rows(A.exp_gu, row_g, row_g + A.FF);
-    }
+      if (lane == k) sel[k] = t.idx[k];
   }
 
-  // 3. stage the inputs, then this lane's blocks from LDS
+  // 3. stage the inputs and the picks, then the expert rows and this lane's
+  //    blocks from LDS
   if ((int)threadIdx.x < nv) {
     reinterpret_cast<uint4*>(xs[0])[threadIdx.x] = xd0;
     reinterpret_cast<uint4*>(xs[1])[threadIdx.x] = xm0;
@@ -326,6 +367,13 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     reinterpret_cast<uint4*>(xs[1])[threadIdx.x + 256] = xm1;
   }
   lds_sync();
+  int slot = 0, j = u;
+  if (!dense) {
+    slot = (u - A.FF2) / A.FF;
+    j = (u - A.FF2) - slot * A.FF;
+    const int64_t row_g = (int64_t)sel[slot] * 2 * A.FF + j;
+    load_rows(A.exp_gu, row_g, row_g + A.FF);
+  }
   const uint32_t* x = reinterpret_cast<const uint32_t*>(xs[dense ? 0 : 1]);
   uint32_t xp[GU_BPL][16];
 #pragma unroll
