@@ -501,7 +501,7 @@ def bench_long(steps: int, warmup: int, cpu: bool) -> dict:
     }
 
 
-def bench_a4b(steps: int, warmup: int, cpu: bool) -> dict:
+def bench_a4b(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict:
     """Decode of the reference's live model shape (src/engine-a4b.js:100-116,
     the Gemma-4 26B-A4B MoE its published 95.0 tok/s on an M4 Max is quoted
     on): the A4B recipe at 30 layers, hidden 2816, 16 q heads, sliding layers
@@ -513,11 +513,12 @@ def bench_a4b(steps: int, warmup: int, cpu: bool) -> dict:
     (every dense weight, the router, the 8 active experts' blocks, the live
     K/V rows, the lm-head) over the step time."""
     from e4b import formats
+    from e4b._lib import FLAG_NO_GRAPH
     from e4b.engine import Engine
     from e4b.model import a4b_config, synth_tensors
 
     prompt_len = 512
-    cfg = a4b_config(max_seq=max(1024, prompt_len + warmup + steps + 8))
+    cfg = a4b_config(max_seq=max(1024, prompt_len + warmup + steps + 8), flags=FLAG_NO_GRAPH if no_graph else 0)
     t0 = time.perf_counter()
     tensors = synth_tensors(cfg, seed=0)
     t_synth = time.perf_counter() - t0
@@ -637,7 +638,7 @@ def main() -> int:
     ap.add_argument("--persistent", action="store_true",
                     help="c4: run the layer loop as one persistent cooperative kernel (E4B_FLAG_PERSISTENT)")
     ap.add_argument("--no-graph", action="store_true",
-                    help="c4: launch the step kernels directly instead of replaying the hipGraph (for profilers)")
+                    help="c4, a4b: launch the step kernels directly instead of replaying the hipGraph (for profilers)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
@@ -656,6 +657,8 @@ def main() -> int:
         res = None
     elif a.workload == "c4":
         res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph, a.persistent)
+    elif a.workload == "a4b":
+        res = bench_a4b(steps, warmup, not a.no_cpu, a.no_graph)
     else:
         res = fn(steps, warmup, not a.no_cpu)
     if a.copy_probe:

@@ -20,6 +20,7 @@ struct AttnGen {
   const float* qw;         // [hd] q head-norm weight
   const float* kw;         // [hd] k head-norm weight
   const float* inv_freq;   // [hd / 2] THETA^(-2p/hd), f32
+  const float2* rope;      // [>= angles] (cos, sin)(pos inv_freq[p]) of this step, or null: evaluated here
   const uint32_t* params;  // [0] position, [kv_idx] the full layers' slot
   uint16_t* kc;            // [kvh][slots][hd]
   uint16_t* vc;

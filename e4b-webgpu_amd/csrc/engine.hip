@@ -256,6 +256,8 @@ static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
   for (int l = 0; l < k.layers; ++l) {
     const int kvh = k.layer_kv_heads ? k.layer_kv_heads[l] : k.kv_heads;
     if (kvh <= 0 || k.q_heads % kvh) return bad("every layer's KV heads must divide q_heads");
+    const int gqa = k.q_heads / kvh;
+    if (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) return bad("q heads per KV head must be 1, 2, 4 or 8");
   }
   if (k.ple_dim != 0) return bad("ple_dim must be 0 (no per-layer embeddings)");
   if (k.ffn <= 0 || k.ffn % 32 || k.ffn > 3072) return bad("ffn (the dense branch) must be a multiple of 32 up to 3072");
@@ -790,11 +792,13 @@ int record_step_a4b(e4b_ctx* c) {
     if ((rc = launch_q40(q40_view(ly.qkv, ly.qkv_rows, H), nullptr, nullptr, EPI_F32, oq, 1, st, &pq)) ||
         (rc = tick(c, "qkv")))
       return rc;
-    AttnGen ag;
+    AttnGen ag{};
     ag.qkv = c->qkv;
     ag.qw = ly.q_norm;
     ag.kw = ly.k_norm;
     ag.inv_freq = ly.global ? c->inv_global : c->inv_local;
+    // the step's (cos, sin) table (k_embed) holds head_dim / 2 pairs per layer type
+    ag.rope = ly.angles <= k.head_dim / 2 ? c->rope + (ly.global ? k.head_dim / 2 : 0) : nullptr;
     ag.params = c->params;
     ag.kc = ly.kc;
     ag.vc = ly.vc;

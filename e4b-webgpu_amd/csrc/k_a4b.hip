@@ -148,6 +148,13 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
       win[u][e] = w.x, win[u][e + 1] = w.y, win[u][e + 2] = w.z, win[u][e + 3] = w.w;
     }
   }
+  // the step's (cos, sin) of this lane's pairs (p = PER (l mod 32) + e),
+  // index clamped into the rotated range (absent table: any readable row)
+  const bool have_cs = A.rope != nullptr;
+  const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);
+  float2 rc[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) rc[e] = rsrc[min(PER * (lane & 31) + e, max(A.angles - 1, 0))];
   uint32_t kr[PW][PER / 2];
   uint32_t vr[PW];
 #pragma unroll
@@ -190,8 +197,8 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
         const float partner = hi ? lo_v : hi_v;
         const int p = PER * (lane & 31) + e;
         if (p < A.angles) {
-          float sn, cs;
-          sincosf(fpos * A.inv_freq[p], &sn, &cs);
+          float sn = rc[e].y, cs = rc[e].x;
+          if (!have_cs) sincosf(fpos * A.inv_freq[p], &sn, &cs);
           x[e] = hi ? (partner * sn + x[e] * cs) : (x[e] * cs - partner * sn);
         }
       }
@@ -298,26 +305,54 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
   }
 }
 
-// one block per head: out = sum_c e^(m_c - M) part_o[c] / sum_c e^(m_c - M) l_c
+// one block per head: out = sum_c e^(m_c - M) part_o[c] / sum_c e^(m_c - M) l_c.
+// Thread t: output dims t + 256 q, and the (max, sum) of chunk t.  The first
+// U chunks' outputs are requested with the statistics, before the reductions
+// wait; further chunks follow U at a time.
+constexpr int kMergeMaxChunks = 256;
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnGen A) {
-  constexpr int CS = kAttnGenChunk;
+  constexpr int CS = kAttnGenChunk, U = 16, DPT = HD / 256;
+  __shared__ float wts[kMergeMaxChunks];
   __shared__ float red[4];
   const int h = blockIdx.x, t = threadIdx.x;
   const Live L = live_of(A);
   const int nch = (L.n + CS - 1) / CS;
   const float* ml = A.part_ml + (int64_t)h * A.gch * 2;
-  float mloc = -3.0e38f;
-  for (int c = t; c < nch; c += 256) mloc = fmaxf(mloc, ml[2 * c]);
-  const float M = block_max(mloc, red);
-  float den = 0.f;
-  for (int c = t; c < nch; c += 256) den += __expf(ml[2 * c] - M) * ml[2 * c + 1];
-  den = block_sum(den, red);
-  for (int d = t; d < HD; d += 256) {
-    float acc = 0.f;
-    for (int c = 0; c < nch; ++c) acc = fmaf(__expf(ml[2 * c] - M), A.part_o[((int64_t)h * A.gch + c) * HD + d], acc);
-    A.out[(int64_t)h * HD + d] = f2h(acc / den);
+  const float* po = A.part_o + (int64_t)h * A.gch * HD + t;
+  float v[U][DPT];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int q = 0; q < DPT; ++q) v[u][q] = po[(int64_t)min(u, nch - 1) * HD + 256 * q];
+  const int tc = min(t, nch - 1);
+  const float mt = ml[2 * tc], lt = ml[2 * tc + 1];
+  __builtin_amdgcn_sched_barrier(0);
+  const float M = block_max(t < nch ? mt : -3.0e38f, red);
+  const float f = t < nch ? __expf(mt - M) : 0.f;
+  const float den = block_sum(t < nch ? lt * f : 0.f, red);
+  wts[t] = f;
+  lds_sync();
+  float acc[DPT];
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) acc[q] = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int q = 0; q < DPT; ++q) acc[q] = fmaf(wts[u], v[u][q], acc[q]);  // wts = 0 past nch
+  for (int c0 = U; c0 < nch; c0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < DPT; ++q) v[u][q] = po[(int64_t)min(c0 + u, nch - 1) * HD + 256 * q];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < DPT; ++q) acc[q] = fmaf(c0 + u < nch ? wts[c0 + u] : 0.f, v[u][q], acc[q]);
   }
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) A.out[(int64_t)h * HD + t + 256 * q] = f2h(acc[q] / den);
 }
 
 }  // namespace
@@ -347,7 +382,7 @@ int launch_attn_gen(const AttnGen& a, hipStream_t st) {
   const int gqa = a.kvh > 0 ? a.qh / a.kvh : 0;
   if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
       a.angles < 0 || a.angles > a.hd / 2 || a.slots <= 0 || a.gch <= 0 || (a.window > 0 && a.slots < a.window) ||
-      (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots))
+      (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots) || a.gch > kMergeMaxChunks)
     return e4b_fail(E4B_EINVAL, "attention: head_dim %d, %d/%d heads (1, 2, 4 or 8 per KV head), %d pairs, %d slots, "
                     "%d chunks", a.hd, a.qh, a.kvh, a.angles, a.slots, a.gch);
   if (a.hd == 256)

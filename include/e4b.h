@@ -300,7 +300,12 @@ typedef struct e4b_config {
   uint32_t flags;         /* E4B_FLAG_* */
   /* E4B_RECIPE_A4B (src/engine-a4b.js:100-116): the model loadEngineA4B
    * loads -- no per-layer embeddings, a MoE FFN half per layer, full layers
-   * with their own head dim and rotated pairs and V = K */
+   * with their own head dim and rotated pairs and V = K.  Supported: hidden
+   * a multiple of 256 up to 3072, head_dim 256, head_dim_full 256 or 512,
+   * 1, 2, 4 or 8 q heads per KV head on every layer, ffn and expert_ffn
+   * multiples of 32 (<= 3072, <= 768), 8..256 experts, ple_dim 0; not with
+   * E4B_FLAG_PERSISTENT or E4B_FLAG_KV_SCORE.  Prompts run through the
+   * decode step. */
   int32_t recipe;              /* E4B_RECIPE_E4B (0) or E4B_RECIPE_A4B (1) */
   int32_t head_dim_full;       /* A4B: full layers' head dim (512), 0 = head_dim */
   int32_t rope_angles_full;    /* A4B: full layers' rotated pairs (64 = 0.25 * 512 / 2), 0 = rope_angles */
