@@ -11,9 +11,10 @@
 // h_out = (h_in + rms(a) * w1) * scale (a null: h_in * scale; h_out null: not
 // stored, h_in and h_out may alias); x (null: none) = f16(rms(h_out) * w2)
 // (w2 null: f16(h_out)); xlo (null: none) = f16(y - f16(y)), the low half of
-// the hi/lo pair of the same value.  H <= 4096.  One workgroup.
+// the hi/lo pair of the same value.  H <= 4096.  One workgroup per row: M
+// rows at stride H in h_in, h_out, a, x and xlo (the weights are shared).
 int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
-                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st);
+                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st, int M = 1);
 
 struct AttnGen {
   const float* qkv;        // raw q [qh][hd] | k [kvh][hd] | v [kvh][hd] (no v rows when keqv)
@@ -36,3 +37,33 @@ constexpr int kAttnGenChunk = 64;  // positions per split-K chunk
 // then their log-sum-exp merge (two launches); head dim 256 or 512, 1, 2, 4
 // or 8 q heads per KV head
 int launch_attn_gen(const AttnGen& a, hipStream_t st);
+
+// ---- batched prefill of the A4B recipe (src/engine-a4b.js:465-549) ----------
+struct HeadRowsGen {
+  const float* qkv;        // [M][ld]: raw q | k (| v) rows of each token
+  int64_t ld;
+  const float* qw;
+  const float* kw;
+  const float* inv_freq;
+  uint16_t* kc;            // [kvh][slots][hd]
+  uint16_t* vc;
+  float* q;                // [M][qh][hd] prepped queries
+  int qh, kvh, hd, angles, slots, window;
+  bool keqv;
+  uint32_t p0;             // position (= full-layer slot) of token 0
+  float eps;
+};
+// head prep of M tokens: queries out, the K/V rows of positions p0 .. p0 + M - 1 into the caches
+int launch_headprep_rows_gen(const HeadRowsGen& a, int M, hipStream_t st);
+
+struct AttnRowsGen {
+  const float* q;          // [M][qh][hd]
+  const uint16_t* kc;      // [kvh][slots][hd], every position <= p0 + M - 1 written
+  const uint16_t* vc;
+  uint16_t* out;           // [M][qh hd] f16
+  int qh, kvh, hd, slots, window;
+  uint32_t p0;
+};
+// causal attention of M tokens (token m at position p0 + m over its live
+// window), one workgroup per (KV group, token)
+int launch_attn_rows_gen(const AttnRowsGen& a, int M, hipStream_t st);

@@ -131,8 +131,10 @@ struct e4b_ctx {
   int* pabort = nullptr;
   PersistArgs pargs{};
   unsigned long long* ptrace = nullptr;  // phase trace of e4b_profile_step (allocated on first use)
-  // A4B recipe: prepped queries, the MoE half's scratch
+  // A4B recipe: the MoE half's scratch; the batched prefill's MoE scratch
   MoeArgs moe{};
+  MoePrefillBufs pf_mb{};
+  uint8_t* pf_moe = nullptr;
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;       // event pool, grown on first use
   std::vector<const char*> prof_label;   // label of the dispatch ending at event i (i >= 1)
@@ -534,6 +536,36 @@ int finalize_a4b(e4b_ctx* c) {
       (rc = dalloc_t(c, &m.g_dense, (size_t)FF)) || (rc = dalloc_t(c, &m.g_slots, (size_t)kMoeTopK * FE)) ||
       (rc = dalloc_t(c, &m.dense_out, (size_t)H)) || (rc = dalloc_t(c, &m.moe_out, (size_t)H)))
     return rc;
+  // batched prefill (src/engine-a4b.js:259-295, 465-584): chunks of up to 512
+  // tokens; a chunk must leave every key its queries need in the sliding
+  // rings (ring >= window + M - 1, the Complete condition of
+  // specs/KVRing.tla with C = M), and the MoE prefill takes <= 1024 tokens
+  {
+    int cap = kPfMaxChunk;
+    bool any_sliding = false;
+    for (int l = 0; l < k.layers; ++l) any_sliding |= !c->L[l].global;
+    if (cap > c->max_prompt) cap = c->max_prompt;
+    if (cap > k.max_seq) cap = k.max_seq;
+    if (any_sliding && cap > k.ring - k.window + 1) cap = k.ring - k.window + 1;
+    if (cap > 128) cap = cap / 128 * 128;
+    if (cap >= 1) {
+      const size_t M = (size_t)cap;
+      MoeArgs shape = m;
+      shape.H = H;
+      shape.E = E;
+      shape.FF = FE;
+      shape.FF2 = FF;
+      const size_t moe_bytes = moe_prefill_scratch(shape, cap, nullptr, nullptr);
+      if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
+          (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_qkv, M * (size_t)c->qkv_rows)) ||
+          (rc = dalloc_t(c, &c->pf_q, M * QH * hd_max)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * hd_max)) ||
+          (rc = dalloc_t(c, &c->pf_y, M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
+          (rc = dalloc(c, (void**)&c->pf_moe, moe_bytes)))
+        return rc;
+      moe_prefill_scratch(shape, cap, &c->pf_mb, c->pf_moe);
+      c->pf_cap = cap;
+    }
+  }
   return E4B_OK;
 }
 
@@ -1066,12 +1098,122 @@ int record_step_persist(e4b_ctx* c) {
   return tick(c, "argmax_feedback");
 }
 
+// One prefill chunk of the A4B recipe (src/engine-a4b.js:465-549
+// encodeLayerPre, 550-584 prefill): tokens pf_ids[0..M) at positions p0 ..
+// p0 + M - 1 (= the full layers' slots: a prefill starts from an empty
+// cache), per layer the q|k(|v) GEMM, head prep of every token with the K/V
+// rows into the caches, causal attention per (KV group, token), the o GEMM,
+// the attention residual, the MoE half over the M tokens (k_moe_prefill.hip:
+// router, top-8, expert-grouped gate/up and down, dense branch, tail).  The
+// per-token arithmetic is the decode step's.  Leaves the final-norm input of
+// every token in pf_xhl as an f16 hi/lo pair.
+int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
+  const e4b_config& k = c->cfg;
+  const int H = k.hidden, QH = k.q_heads, Lc = k.layers;
+  const int64_t MH = (int64_t)M * H;
+  hipStream_t st = c->st;
+  int rc;
+  auto gemm = [&](const Q40Mat& W, const uint16_t* X, int ldx, float* Y) {
+    GemmArgs g{};
+    g.W = W;
+    g.X = X;
+    g.M = M;
+    g.ldx = ldx;
+    g.epi = GEMM_F32;
+    g.Y = Y;
+    g.ks = 1;
+    return launch_q40_gemm(g, st);
+  };
+  const Q6Mat E = q6_view(c->embd, k.vocab, H);
+  if ((rc = launch_embed_rows(E, c->pf_ids, M, sqrtf((float)H), c->pf_h, c->pf_xhl, st)) ||
+      (rc = tick(c, "embed_rows")))
+    return rc;
+  for (int l = 0; l < Lc; ++l) {
+    const Layer& ly = c->L[l];
+    const int window = ly.global ? 0 : k.window;
+    if ((rc = launch_rownorm(c->pf_h, nullptr, nullptr, nullptr, 1.f, ly.attn_norm, c->pf_xn, nullptr, H, k.eps, st,
+                             M)) ||
+        (rc = tick(c, "norm_rows")) ||
+        (rc = gemm(q40_view(ly.qkv, ly.qkv_rows, H), c->pf_xn, H, c->pf_qkv)) || (rc = tick(c, "gemm_qkv")))
+      return rc;
+    HeadRowsGen hr{};
+    hr.qkv = c->pf_qkv;
+    hr.ld = ly.qkv_rows;
+    hr.qw = ly.q_norm;
+    hr.kw = ly.k_norm;
+    hr.inv_freq = ly.global ? c->inv_global : c->inv_local;
+    hr.kc = ly.kc;
+    hr.vc = ly.vc;
+    hr.q = c->pf_q;
+    hr.qh = QH;
+    hr.kvh = ly.kvh;
+    hr.hd = ly.hd;
+    hr.angles = ly.angles;
+    hr.slots = ly.slots;
+    hr.window = window;
+    hr.keqv = ly.keqv;
+    hr.p0 = p0;
+    hr.eps = k.eps;
+    AttnRowsGen ar{};
+    ar.q = c->pf_q;
+    ar.kc = ly.kc;
+    ar.vc = ly.vc;
+    ar.out = c->pf_attn;
+    ar.qh = QH;
+    ar.kvh = ly.kvh;
+    ar.hd = ly.hd;
+    ar.slots = ly.slots;
+    ar.window = window;
+    ar.p0 = p0;
+    if ((rc = launch_headprep_rows_gen(hr, M, st)) || (rc = tick(c, "headprep_rows")) ||
+        (rc = launch_attn_rows_gen(ar, M, st)) || (rc = tick(c, "attn_rows")) ||
+        (rc = gemm(q40_view(ly.o, H, (int64_t)QH * ly.hd), c->pf_attn, QH * ly.hd, c->pf_y)) ||
+        (rc = tick(c, "gemm_o")) ||
+        // h1 = h + rms(o) post_attn, in place
+        (rc = launch_rownorm(c->pf_h, c->pf_h, c->pf_y, ly.post_attn, 1.f, nullptr, nullptr, nullptr, H, k.eps, st,
+                             M)) ||
+        (rc = tick(c, "attn_residual_rows")))
+      return rc;
+    MoeArgs a = c->moe;
+    a.h = c->pf_h;
+    a.h_out = c->pf_h;  // the tail reads each row before it writes it
+    a.attn_o = nullptr;
+    a.ffn_norm = ly.ffn_norm;
+    a.router_scale = ly.router_scale;
+    a.router_mult = 1.0f / sqrtf((float)H);
+    a.pre_ffw2 = ly.pre_ffw2;
+    a.router_w = ly.router_w;
+    a.pes = ly.pes;
+    a.dense_gu = q40_view(ly.gu, 2 * (int64_t)k.ffn, H);
+    a.exp_gu = q40_view(ly.exp_gu, (int64_t)k.n_experts * 2 * k.expert_ffn, H);
+    a.dense_down = q40_view(ly.down, H, k.ffn);
+    a.exp_down = q40_view(ly.exp_down, (int64_t)k.n_experts * H, k.expert_ffn);
+    a.post_ffw1 = ly.post_ffw1;
+    a.post_ffw2 = ly.post_ffw2;
+    a.post_ffw = ly.post_ffw;
+    a.layer_scale = ly.scale;
+    a.eps = k.eps;
+    a.H = H;
+    a.E = k.n_experts;
+    a.FF = k.expert_ffn;
+    a.FF2 = k.ffn;
+    if ((rc = launch_moe_prefill(a, M, c->pf_mb, st)) || (rc = tick(c, "moe_prefill"))) return rc;
+  }
+  // final norm as the f16 hi/lo pair of the lm-head input
+  if ((rc = launch_rownorm(c->pf_h, nullptr, nullptr, nullptr, 1.f, c->out_norm, c->pf_xhl, c->pf_xhl + MH, H, k.eps,
+                           st, M)) ||
+      (rc = tick(c, "final_norm_rows")))
+    return rc;
+  return E4B_OK;
+}
+
 // One prefill chunk: tokens pf_ids[0..M) at positions p0 .. p0 + M - 1,
 // every layer as batched GEMMs on the matrix cores plus per-token kernels
 // (src/engine-a4b.js:465-563 encodeLayerPre / prefill, with the E4B layer
 // recipe of record_step).  Leaves the K/V rows of the chunk in the caches and,
 // in pf_xhl, the final-norm input of every token as an f16 hi/lo pair.
 int prefill_chunk(e4b_ctx* c, uint32_t p0, int M) {
+  if (c->cfg.recipe == E4B_RECIPE_A4B) return prefill_chunk_a4b(c, p0, M);
   const e4b_config& k = c->cfg;
   const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
   const int Lc = k.layers;
@@ -1321,9 +1463,8 @@ static int prefill_common(e4b_ctx* c, const char* fn, const uint32_t* ids, uint3
 }
 
 extern "C" int e4b_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
-  // the A4B recipe has no batched prefill: its prompt runs through the step
   return prefill_common(c, "e4b_prefill", ids, n, argmax_out,
-                        c && ((c->cfg.flags & E4B_FLAG_STEP_PREFILL) != 0 || c->cfg.recipe == E4B_RECIPE_A4B));
+                        c && ((c->cfg.flags & E4B_FLAG_STEP_PREFILL) != 0 || c->pf_cap <= 0));
 }
 
 extern "C" int e4b_prefill_steps(e4b_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* argmax_out) {
@@ -1492,8 +1633,8 @@ extern "C" int e4b_profile_prefill(e4b_ctx* c, const uint32_t* ids, uint32_t n, 
   if (rc) return rc;
   if (!ids || n == 0) return e4b_fail(E4B_EINVAL, "e4b_profile_prefill: empty prompt");
   if (c->pf_cap <= 0)
-    return e4b_fail(E4B_ESTATE, "e4b_profile_prefill: this recipe has no batched prefill (its prompts run through "
-                                "the decode step; profile that with e4b_profile_step)");
+    return e4b_fail(E4B_ESTATE, "e4b_profile_prefill: no batched prefill buffers (max_prompt, max_seq or the ring "
+                                "leave no chunk); profile the step with e4b_profile_step");
   const int M = (int)(n < (uint32_t)c->pf_cap ? n : (uint32_t)c->pf_cap);
   for (int i = 0; i < M; ++i)
     if (ids[i] >= (uint32_t)c->cfg.vocab)

@@ -32,6 +32,13 @@ __global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ h_in,
                                                  uint16_t* __restrict__ xlo, int H, float eps) {
   __shared__ float red[4];
   const int t = threadIdx.x;
+  // row blockIdx.x of a batch (one row in the decode step)
+  const int64_t ro = (int64_t)blockIdx.x * H;
+  h_in += ro;
+  if (h_out) h_out += ro;
+  if (a) a += ro;
+  if (x) x += ro;
+  if (xlo) xlo += ro;
   float hv[kRowMax], av[kRowMax];
 #pragma unroll
   for (int k = 0; k < kRowMax; ++k) {
@@ -355,13 +362,213 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnGen A) {
   for (int q = 0; q < DPT; ++q) A.out[(int64_t)h * HD + t + 256 * q] = f2h(acc[q] / den);
 }
 
+// ---- batched prefill ----------------------------------------------------------
+// one wave per (head row r, token m): q heads [0, qh), k heads [qh, qh + kvh),
+// v heads [qh + kvh, qh + 2 kvh) (V from the K slice on KEQV layers); lane l
+// holds dims [PER l, PER l + PER), the RoPE partner of dim p < HD / 2 in lane
+// l + 32 (kernels/headprep.wgsl:19-87 per token)
+template <int HD>
+__global__ __launch_bounds__(64) void k_headprep_rows_gen(HeadRowsGen A) {
+  constexpr int PER = HD / 64;
+  const int r = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const int QH = A.qh, KVH = A.kvh;
+  const int kind = r < QH ? 0 : r < QH + KVH ? 1 : 2;  // q, k, v
+  const int g = kind == 0 ? r : kind == 1 ? r - QH : r - QH - KVH;
+  const int src = kind == 0 ? r : kind == 1 || A.keqv ? QH + g : QH + KVH + g;
+  const float* xr = A.qkv + (int64_t)m * A.ld + (int64_t)src * HD + PER * lane;
+  const float* wr = (kind == 1 ? A.kw : A.qw) + PER * lane;  // v rows use no weight
+  float x[PER], w[PER];
+#pragma unroll
+  for (int e = 0; e < PER; e += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(xr + e);
+    const float4 u = *reinterpret_cast<const float4*>(wr + e);
+    x[e] = t.x, x[e + 1] = t.y, x[e + 2] = t.z, x[e + 3] = t.w;
+    w[e] = u.x, w[e + 1] = u.y, w[e + 2] = u.z, w[e + 3] = u.w;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) ss = fmaf(x[e], x[e], ss);
+  const float inv = rms_inv(wave_sum(ss), HD, A.eps);
+#pragma unroll
+  for (int e = 0; e < PER; ++e) x[e] = x[e] * inv * (kind < 2 ? w[e] : 1.f);
+  const uint32_t pos = A.p0 + (uint32_t)m;
+  if (kind < 2) {
+    const float fpos = (float)pos;
+    const bool hi = lane >= 32;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      float lo_v = x[e], hi_v = x[e];
+      swapx32(lo_v, hi_v);  // lanes < 32: hi_v = dim p + HD/2; lanes >= 32: lo_v = dim p
+      const float partner = hi ? lo_v : hi_v;
+      const int p = PER * (lane & 31) + e;
+      if (p < A.angles) {
+        float sn, cs;
+        sincosf(fpos * A.inv_freq[p], &sn, &cs);
+        x[e] = hi ? (partner * sn + x[e] * cs) : (x[e] * cs - partner * sn);
+      }
+    }
+  }
+  if (kind == 0) {
+    float* q = A.q + ((int64_t)m * QH + r) * HD + PER * lane;
+#pragma unroll
+    for (int e = 0; e < PER; e += 4) *reinterpret_cast<float4*>(q + e) = make_float4(x[e], x[e + 1], x[e + 2], x[e + 3]);
+    return;
+  }
+  const uint32_t slot = A.window > 0 ? pos % (uint32_t)A.slots : pos;
+  uint16_t* dst = (kind == 1 ? A.kc : A.vc) + ((int64_t)g * A.slots + slot) * HD + PER * lane;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) dst[e] = f2h(x[e]);
+}
+
+// Workgroup (KV group g, token m), 4 waves.  Wave w walks the token's live
+// positions lo + w, lo + w + 4, ... in tiles of T, with its own running max,
+// sum and P.V per q head of the group (flash-style online softmax; after the
+// cross-lane reduction lane l holds the score of head l / (64 / GQA), so the
+// statistics are lane-local and the P.V weights are read out per head);
+// the four waves are folded by log-sum-exp at the end.  K and V rows come
+// from the caches, which hold every position of the chunk already.
+template <int HD, int GQA>
+__global__ __launch_bounds__(256) void k_attn_rows_gen(AttnRowsGen A) {
+  constexpr int NW = 4, PER = HD / 64, LPH = 64 / GQA, T = HD == 512 ? 4 : 8;
+  __shared__ float sml[NW][GQA][2];
+  __shared__ __align__(16) float sacc[NW - 1][GQA][HD];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = blockIdx.x, m = blockIdx.y;
+  const int cur = (int)A.p0 + m;
+  const int lo = (A.window > 0 && cur + 1 > A.window) ? cur + 1 - A.window : 0;
+  const int n = cur + 1 - lo;
+  const uint16_t* kc = A.kc + (int64_t)g * A.slots * HD + PER * lane;
+  const uint16_t* vc = A.vc + (int64_t)g * A.slots * HD + PER * lane;
+  const int s_lo = A.window > 0 ? lo % A.slots : lo;
+  auto slot_at = [&](int j) -> int64_t {  // j < n <= window <= slots: one wrap at most
+    const int s = s_lo + j;
+    return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
+  };
+  float q[GQA][PER];
+#pragma unroll
+  for (int h = 0; h < GQA; ++h) {
+    const float* qr = A.q + ((int64_t)m * A.qh + g * GQA + h) * HD + PER * lane;
+#pragma unroll
+    for (int e = 0; e < PER; e += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(qr + e);
+      q[h][e] = t.x, q[h][e + 1] = t.y, q[h][e + 2] = t.z, q[h][e + 3] = t.w;
+    }
+  }
+  float acc[GQA][PER];
+#pragma unroll
+  for (int h = 0; h < GQA; ++h)
+#pragma unroll
+    for (int e = 0; e < PER; ++e) acc[h][e] = 0.f;
+  float mrun = -3.0e38f, lrun = 0.f;  // of head lane / LPH
+  for (int base = wave; base < n; base += NW * T) {
+    uint32_t kr[T][PER / 2], vr[T][PER / 2];
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      const int64_t sl = slot_at(min(base + NW * i, n - 1)) * HD;
+#pragma unroll
+      for (int e = 0; e < PER / 2; e += 2) {
+        const uint2 a = *reinterpret_cast<const uint2*>(kc + sl + 2 * e);
+        const uint2 b = *reinterpret_cast<const uint2*>(vc + sl + 2 * e);
+        kr[i][e] = a.x, kr[i][e + 1] = a.y;
+        vr[i][e] = b.x, vr[i][e + 1] = b.y;
+      }
+    }
+    float sc[T];
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      float t[GQA];
+#pragma unroll
+      for (int h = 0; h < GQA; ++h) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < PER / 2; ++e) {
+          a = fmaf(q[h][2 * e], h2f((uint16_t)(kr[i][e] & 0xffffu)), a);
+          a = fmaf(q[h][2 * e + 1], h2f((uint16_t)(kr[i][e] >> 16)), a);
+        }
+        t[h] = a;
+      }
+      const float s = reduce_rows<64, GQA>(t);
+      sc[i] = base + NW * i < n ? s : -3.0e38f;
+    }
+    float mt = sc[0];
+#pragma unroll
+    for (int i = 1; i < T; ++i) mt = fmaxf(mt, sc[i]);
+    const float mnew = fmaxf(mrun, mt);
+    const float alpha = __expf(mrun - mnew);
+    float p[T], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      p[i] = sc[i] > -1.0e38f ? __expf(sc[i] - mnew) : 0.f;
+      ps += p[i];
+    }
+    lrun = lrun * alpha + ps;
+    mrun = mnew;
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) {
+      const float ah = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), h * LPH));
+#pragma unroll
+      for (int e = 0; e < PER; ++e) acc[h][e] *= ah;
+    }
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      float vf[PER];
+#pragma unroll
+      for (int e = 0; e < PER / 2; ++e) {
+        vf[2 * e] = h2f((uint16_t)(vr[i][e] & 0xffffu));
+        vf[2 * e + 1] = h2f((uint16_t)(vr[i][e] >> 16));
+      }
+#pragma unroll
+      for (int h = 0; h < GQA; ++h) {
+        const float ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[i]), h * LPH));
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[h][e] = fmaf(ph, vf[e], acc[h][e]);
+      }
+    }
+  }
+  // fold the four waves
+  if ((lane % LPH) == 0) {
+    sml[wave][lane / LPH][0] = mrun;
+    sml[wave][lane / LPH][1] = lrun;
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) sacc[wave - 1][h][PER * lane + e] = acc[h][e];
+  }
+  lds_sync();
+  if (wave != 0) return;
+#pragma unroll
+  for (int h = 0; h < GQA; ++h) {
+    float M = sml[0][h][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, sml[w][h][0]);
+    float f[NW], L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      f[w] = __expf(sml[w][h][0] - M);  // 0 for a wave without positions
+      L = fmaf(sml[w][h][1], f[w], L);
+    }
+    const float invL = 1.f / L;
+    uint16_t* dst = A.out + (int64_t)m * A.qh * HD + (int64_t)(g * GQA + h) * HD + PER * lane;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      float v = acc[h][e] * f[0];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) v = fmaf(sacc[w - 1][h][PER * lane + e], f[w], v);
+      dst[e] = f2h(v * invL);
+    }
+  }
+}
+
 }  // namespace
 
 int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
-                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st) {
+                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st, int M) {
   if (H <= 0 || H > 256 * kRowMax) return e4b_fail(E4B_EINVAL, "row norm: hidden %d outside 1..%d", H, 256 * kRowMax);
   if (a && !w1) return e4b_fail(E4B_EINVAL, "row norm: residual without its norm weight");
-  hipLaunchKernelGGL(k_rownorm, dim3(1), dim3(256), 0, st, h_in, h_out, a, w1, scale, w2, x, xlo, H, eps);
+  if (M < 1) return e4b_fail(E4B_EINVAL, "row norm: %d rows", M);
+  hipLaunchKernelGGL(k_rownorm, dim3(M), dim3(256), 0, st, h_in, h_out, a, w1, scale, w2, x, xlo, H, eps);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }
@@ -389,6 +596,47 @@ int launch_attn_gen(const AttnGen& a, hipStream_t st) {
     launch_attn_hd<256>(a, st);
   else
     launch_attn_hd<512>(a, st);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_headprep_rows_gen(const HeadRowsGen& a, int M, hipStream_t st) {
+  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || a.angles < 0 || a.angles > a.hd / 2 ||
+      a.slots <= 0 || (a.window > 0 && a.slots < a.window) || M < 1 || a.ld < (int64_t)(a.qh + a.kvh) * a.hd ||
+      (a.window == 0 && (int64_t)a.p0 + M > a.slots))
+    return e4b_fail(E4B_EINVAL, "head prep rows: head_dim %d, %d/%d heads, %d pairs, %d slots, %d tokens", a.hd, a.qh,
+                    a.kvh, a.angles, a.slots, M);
+  const dim3 grid(a.qh + 2 * a.kvh, M);
+  if (a.hd == 256)
+    hipLaunchKernelGGL(k_headprep_rows_gen<256>, grid, dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_headprep_rows_gen<512>, grid, dim3(64), 0, st, a);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+template <int HD>
+static void launch_attn_rows_hd(const AttnRowsGen& a, int M, hipStream_t st) {
+  const dim3 grid(a.kvh, M);
+  switch (a.qh / a.kvh) {
+    case 1: hipLaunchKernelGGL((k_attn_rows_gen<HD, 1>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_attn_rows_gen<HD, 2>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_attn_rows_gen<HD, 4>), grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_attn_rows_gen<HD, 8>), grid, dim3(256), 0, st, a); break;
+  }
+}
+
+int launch_attn_rows_gen(const AttnRowsGen& a, int M, hipStream_t st) {
+  const int gqa = a.kvh > 0 ? a.qh / a.kvh : 0;
+  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
+      a.slots <= 0 || (a.window > 0 && a.slots < a.window) || M < 1 ||
+      (a.window == 0 && (int64_t)a.p0 + M > a.slots))
+    return e4b_fail(E4B_EINVAL, "attention rows: head_dim %d, %d/%d heads, %d slots, %d tokens from %u", a.hd, a.qh,
+                    a.kvh, a.slots, M, a.p0);
+  if (a.hd == 256)
+    launch_attn_rows_hd<256>(a, M, st);
+  else
+    launch_attn_rows_hd<512>(a, M, st);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -3,8 +3,7 @@
 // loads the model through engine.js, runs generateFast (the prompt through
 // the step, then GPU-fed decode; with E4B_LOGITS_OUT set its last logits go
 // to that file as raw f32), generatePrefill (batched prefill, same decode),
-// profilePrefill (not for the A4B recipe, whose prompt runs through the
-// step), then the step API on the same prompt after a reset and one
+// profilePrefill, then the step API on the same prompt after a reset and one
 // profileStep, and prints one JSON line: {generate, generate_prefill, steps,
 // hidden_l2, logits_max, profile_step, profile_prefill}; with the
 // fifth argument (generateLong options; the model needs flags FLAG_KV_SCORE)
@@ -27,8 +26,7 @@ async function main() {
   eng.reset();
   const generatePrefill = await eng.generatePrefill(ids, maxNew, new Set());
   eng.reset();
-  // the A4B recipe (C.recipe 1) runs its prompt through the step: no prefill chunk to profile
-  const profPrefill = eng.C.recipe === 1 ? new Map() : await eng.profilePrefill(ids);
+  const profPrefill = await eng.profilePrefill(ids);
   eng.reset();
   const steps = [];
   let pos = 0;

@@ -304,8 +304,9 @@ typedef struct e4b_config {
    * a multiple of 256 up to 3072, head_dim 256, head_dim_full 256 or 512,
    * 1, 2, 4 or 8 q heads per KV head on every layer, ffn and expert_ffn
    * multiples of 32 (<= 3072, <= 768), 8..256 experts, ple_dim 0; not with
-   * E4B_FLAG_PERSISTENT or E4B_FLAG_KV_SCORE.  Prompts run through the
-   * decode step. */
+   * E4B_FLAG_PERSISTENT or E4B_FLAG_KV_SCORE.  e4b_prefill runs the
+   * batched prefill of src/engine-a4b.js:465-584 (chunks of up to 512
+   * tokens, ring - window + 1 at most). */
   int32_t recipe;              /* E4B_RECIPE_E4B (0) or E4B_RECIPE_A4B (1) */
   int32_t head_dim_full;       /* A4B: full layers' head dim (512), 0 = head_dim */
   int32_t rope_angles_full;    /* A4B: full layers' rotated pairs (64 = 0.25 * 512 / 2), 0 = rope_angles */
@@ -359,7 +360,9 @@ int  e4b_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, float* logits_or_null,
  * to a multiple of 128 above 128, so every key a
  * chunk's queries need keeps its ring slot), each layer as batched q4_0
  * GEMMs on the matrix cores plus per-token head prep, causal attention and
- * norms; the lm-head runs once, for the last token.  argmax_out = greedy
+ * norms (E4B_RECIPE_A4B: the MoE half over the chunk's tokens with
+ * expert-grouped GEMMs, src/engine-a4b.js:478-549); the lm-head runs once,
+ * for the last token.  argmax_out = greedy
  * continuation of the last prompt token, which is also fed back as the next
  * e4b_decode input.  E4B_FLAG_STEP_PREFILL runs the prompt through the decode
  * step instead. */

@@ -60,6 +60,7 @@ _sigs = {
     "orc_state_krow": (_vp, [_vp, _i32]),
     "orc_state_vrow": (_vp, [_vp, _i32]),
     "orc_state_kv_count": (_i64, [_vp]),
+    "orc_state_route_margin": (C.c_double, [_vp]),
     "orc_state_score": (_vp, [_vp, _i32]),
     "orc_kv_keep": (_i64, [_vp, _i32, _i64, _i64, _i32, _i32, _vp]),
     "orc_kv_compact": (_i64, [_vp, _vp, _i32, _i32]),
@@ -390,6 +391,11 @@ class OracleModel:
 
     def kv_count(self) -> int:
         return int(_lib.orc_state_kv_count(self._state))
+
+    def route_margin(self) -> float:
+        """A4B recipe: the smallest top-8 decision margin of the last step's
+        layers, (8th - 9th largest router score) / max |score|."""
+        return float(_lib.orc_state_route_margin(self._state))
 
     def set_keep_rows(self, on: bool) -> None:
         """With keep_rows the step attends to the K/V row handed over (set_kv)

@@ -521,8 +521,38 @@ static void geglu_rows(const uint8_t* gu, int64_t ff, int64_t in, const float* x
   free(g);
 }
 
+/* the selection's decision margin: (K-th largest score - (K+1)-th) / max |score| */
+static double route_margin_of(const float* sc, int E, int K) {
+  double mx = 0.0;
+  for (int e = 0; e < E; ++e) mx = fmax(mx, fabs((double)sc[e]));
+  if (K >= E || mx == 0.0) return 0.0;
+  /* K-th and (K+1)-th largest by repeated scans (E <= 256) */
+  double prev = INFINITY, kth = 0.0, next = 0.0;
+  int taken = 0;
+  while (taken <= K) {
+    double best = -INFINITY;
+    int cnt = 0;
+    for (int e = 0; e < E; ++e)
+      if ((double)sc[e] < prev && (double)sc[e] > best) best = (double)sc[e];
+    if (best == -INFINITY) return 0.0; /* NaN scores: no margin */
+    for (int e = 0; e < E; ++e)
+      if ((double)sc[e] == best) ++cnt;
+    for (int c = 0; c < cnt && taken <= K; ++c, ++taken) {
+      if (taken == K - 1) kth = best;
+      if (taken == K) next = best;
+    }
+    prev = best;
+  }
+  return (kth - next) / mx;
+}
+
 void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
                  float* dense_out, float* moe_out, float* h_out) {
+  orc_moe_ffn_m(m, h, topk_idx, topk_w, dense_out, moe_out, h_out, NULL);
+}
+
+void orc_moe_ffn_m(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
+                   float* dense_out, float* moe_out, float* h_out, double* margin) {
   const int H = m->hidden, E = m->n_experts, K = m->top_k, FF = m->expert_ffn, FF2 = m->dense_ffn;
   float *xd = malloc(sizeof(float) * H), *xr = malloc(sizeof(float) * H), *xm = malloc(sizeof(float) * H);
   double inv = rms_inv(h, H, m->eps);
@@ -533,7 +563,10 @@ void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* to
     xr[i] = (float)(v * (double)((float)((double)m->router_scale[i] * rs)));
     xm[i] = orc_h2f(orc_f2h((float)(v * (double)m->pre_ffw2[i])));
   }
-  orc_router_topk(xr, m->router_w, m->pes, H, E, K, topk_idx, topk_w, NULL);
+  float* sc = malloc(sizeof(float) * E);
+  orc_router_topk(xr, m->router_w, m->pes, H, E, K, topk_idx, topk_w, sc);
+  if (margin) *margin = route_margin_of(sc, E, K);
+  free(sc);
 
   /* dense branch: gate rows [0,FF2), up rows [FF2,2FF2) */
   float* gd = malloc(sizeof(float) * FF2);
@@ -602,6 +635,9 @@ struct orc_state {
   uint16_t* krow;
   uint16_t* vrow;
   int64_t row_stride; /* krow/vrow entries per layer: the largest kv_heads * head_dim */
+  /* A4B recipe: the smallest top-8 decision margin of the last step's      */
+  /* layers ((8th - 9th router score) / max |score|; orc_moe_ffn_m)        */
+  double route_margin;
 };
 
 static int64_t slots_of(const orc_model* m, int l) {
@@ -665,6 +701,7 @@ void orc_state_set_keep_rows(orc_state* s, int on) { s->keep_rows = on; }
 const uint16_t* orc_state_krow(const orc_state* s, int layer) { return s->krow + (size_t)layer * s->row_stride; }
 const uint16_t* orc_state_vrow(const orc_state* s, int layer) { return s->vrow + (size_t)layer * s->row_stride; }
 int64_t orc_state_kv_count(const orc_state* s) { return s->kv_count; }
+double orc_state_route_margin(const orc_state* s) { return s->route_margin; }
 const float* orc_state_score(const orc_state* s, int layer) { return s->score[layer]; }
 
 /* compactAll's selection (src/engine-a4b.js:587-617) for one full layer:    */
@@ -798,7 +835,9 @@ static void a4b_layer(const orc_model* m, orc_state* st, int l, float* h, uint32
   float* ho = malloc(sizeof(float) * H);
   uint32_t idx[64];
   float w[64];
-  orc_moe_ffn(&ly->moe, h, idx, w, dn, mo, ho);
+  double mg = INFINITY;
+  orc_moe_ffn_m(&ly->moe, h, idx, w, dn, mo, ho, &mg);
+  if (mg < st->route_margin) st->route_margin = mg;
   memcpy(h, ho, sizeof(float) * H);
   free(x); free(qkv); free(qp); free(ao); free(a); free(o); free(inv); free(dn); free(mo); free(ho);
 }
@@ -823,6 +862,7 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
   orc_rope_inv_freq(m->theta_global, HD, m->rope_angles, inv_g);
   if (pos == 0) st->kv_count = 0;
   const int64_t kv = st->kv_count; /* full-layer slot of this token */
+  st->route_margin = INFINITY;
 
   /* embedding row * sqrt(H) (kernels/q6k.wgsl:37-73, MULT = sqrt(hidden)) */
   orc_q6k_dequant_row(m->tok_embd, H, token, (float)sqrt((double)H), h);

@@ -94,6 +94,10 @@ typedef struct {
 } orc_moe;
 void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
                  float* dense_out, float* moe_out, float* h_out);
+/* the same, also returning the selection's decision margin (K-th minus
+ * (K+1)-th largest router score, over max |score|) when margin != NULL */
+void orc_moe_ffn_m(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
+                   float* dense_out, float* moe_out, float* h_out, double* margin);
 
 /* ---- full E4B-shaped decode step --------------------------------------- */
 typedef struct {
@@ -149,6 +153,8 @@ void       orc_state_set_keep_rows(orc_state* s, int on);
 const uint16_t* orc_state_krow(const orc_state* s, int layer);  /* [layer's kv_heads][head_dim] */
 const uint16_t* orc_state_vrow(const orc_state* s, int layer);
 int64_t    orc_state_kv_count(const orc_state* s);
+/* A4B recipe: the smallest top-8 decision margin over the last step's layers */
+double     orc_state_route_margin(const orc_state* s);
 const float* orc_state_score(const orc_state* s, int layer);
 int64_t    orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int budget, int protect,
                        uint32_t* keep);

@@ -23,12 +23,12 @@ from e4b.model import synth_tensors, tiny_a4b_config
 from tests.test_oracle_recipe import EPS, check, f16, gather, onehot_q40, rms, select, set_scale
 
 
-def a4b_model(layer_global=(1,), kvh=(2,), seed=3, q_heads=4):
+def a4b_model(layer_global=(1,), kvh=(2,), seed=3, q_heads=4, n_experts=8):
     """Tiny A4B model, every layer matrix (router included) zero, random norm
     and scale vectors, an O(1) embedding."""
     L = len(layer_global)
     cfg = tiny_a4b_config(layers=L, q_heads=q_heads, layer_global=list(layer_global), layer_kv_heads=list(kvh),
-                          vocab=64, eps=EPS, n_experts=8, expert_ffn=32, ffn=32)
+                          vocab=64, eps=EPS, n_experts=n_experts, expert_ffn=32, ffn=32)
     t = synth_tensors(cfg, seed, emb_sigma=2e-4)
     rng = np.random.default_rng(seed + 100)
     tens = {}
@@ -192,3 +192,66 @@ def test_moe_half_runs_on_the_attention_residual():
                  post_ffw=tens[p + "post_ffw_norm.weight"])
         h = orc.moe_ffn(m, h.astype(np.float32))[4].astype(np.float64)
     check(run(cfg, tens, [17]), h, "MoE halves over two layers")
+
+
+def test_route_margin_of_the_step():
+    # the smallest top-8 decision margin of a step: 0 with a zero router (all
+    # scores tie), in (0, 1] with a random one, and equal to the margin of
+    # the scores recomputed from the layer's MoE input in numpy (one layer,
+    # attention zero so the input is the embedding row itself)
+    cfg, tens = a4b_model(layer_global=(0,), kvh=(4,), seed=21, n_experts=16)
+    om = orc.OracleModel(cfg.as_dict(), tens)
+    om.step(7, 0)
+    assert om.route_margin() == 0.0
+    rng = np.random.default_rng(22)
+    H, E = cfg.hidden, cfg.n_experts
+    W = rng.normal(0, 0.5, E * H).astype(np.float32)
+    tens["blk.0.ffn_gate_inp.weight"] = W
+    om = orc.OracleModel(cfg.as_dict(), tens)
+    om.step(7, 0)
+    got = om.route_margin()
+    h = emb_row(cfg, tens, 7)
+    xr = rms(h) * (tens["blk.0.ffn_gate_inp.scale"].astype(np.float64) / math.sqrt(H))
+    sc = np.sort(W.reshape(E, H).astype(np.float64) @ xr)[::-1]
+    want = (sc[7] - sc[8]) / np.abs(sc).max()
+    assert 0.0 < got <= 1.0
+    assert abs(got - want) <= 1e-4 * abs(want) + 1e-7, (got, want)
+
+
+def test_one_ulp_nudge_jumps_in_the_a4b_recipe():
+    # the A4B recipe rounds to f16 at the same kinds of points as the E4B one
+    # (GEMV inputs, the K/V rows, the GeGLU and attention outputs, the MoE
+    # branch inputs): nudging layer 0's input-norm weights by one f32 ulp
+    # leaves most steps of the tiny model bit-identical and moves a few by a
+    # jump hundreds of times larger.  At this seed the largest reaches ~9e-4
+    # of max |h| (~5e-4 of the hidden range); the GPU tests' synced
+    # tolerance (2e-3 of the range) is stated against sums of such jumps.
+    from e4b.model import norm_weights_random
+    cfg = tiny_a4b_config()
+    tens = {n: t.data for n, t in norm_weights_random(synth_tensors(cfg, 41), 42).items()}
+    pert = dict(tens)
+    w = np.asarray(tens["blk.0.attn_norm.weight"], np.float32)
+    pert["blk.0.attn_norm.weight"] = np.nextafter(w, np.float32(np.inf)).astype(np.float32)
+    a = orc.OracleModel(cfg.as_dict(), tens)
+    b = orc.OracleModel(cfg.as_dict(), pert)
+    b.set_keep_rows(True)
+    rng = np.random.default_rng(41)
+    prompt, forced = rng.integers(0, cfg.vocab, 16), rng.integers(0, cfg.vocab, 40)
+    for i, t in enumerate(prompt):
+        a.step(int(t), i)
+    jumps = []
+    for k, t in enumerate(forced):
+        pos = len(prompt) + k
+        _, _, ha = a.step(int(t), pos, want_hidden=True)
+        for l in range(cfg.layers):
+            kvh, hd = a.layer_shape(l)[:2]
+            n = (cfg.max_seq if cfg.layer_global[l] else cfg.ring) * kvh * hd
+            b.set_kv(l, a.kcache(l, n), a.vcache(l, n))
+        b.set_kv_count(pos)
+        _, _, hb = b.step(int(t), pos, want_hidden=True)
+        jumps.append(float(np.abs(ha.astype(np.float64) - hb).max() / (ha.max() - ha.min())))
+    jumps = np.array(jumps)
+    print(f"A4B one-ulp nudge: {int((jumps == 0).sum())} of {jumps.size} steps bit-identical, largest jump "
+          f"{jumps.max():.2e} of the hidden range")
+    assert (jumps == 0).sum() >= jumps.size // 2
+    assert jumps.max() > 100 * 2.0 ** -23
