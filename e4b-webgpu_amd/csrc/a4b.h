@@ -28,6 +28,7 @@ struct AttnGen {
   float* part_o;           // [qh][gch][hd] unnormalised chunk outputs
   float* part_ml;          // [qh][gch][2] (chunk max, chunk sum)
   uint16_t* out;           // [qh][hd] f16 attention output (the merge)
+  float* raw;              // full layers, may be null: raw scores [qh][slots] of the live slots
   int qh, kvh, hd, angles, slots, window, kv_idx, gch;
   bool keqv;               // V = the raw K slice (kernels/headprep.wgsl:23)
   float eps;
@@ -67,3 +68,8 @@ struct AttnRowsGen {
 // causal attention of M tokens (token m at position p0 + m over its live
 // window), one workgroup per (KV group, token)
 int launch_attn_rows_gen(const AttnRowsGen& a, int M, hipStream_t st);
+
+// compaction gather of one layer: dst[g][i] = src[g][keep[i]] for K and V,
+// rows of hd f16 (any head dim up to 1024)
+int launch_kv_gather_gen(const uint32_t* keep, int n, const uint16_t* kc, const uint16_t* vc, int kvh, int slots,
+                         int hd, uint16_t* dk, uint16_t* dv, int dslots, hipStream_t st);

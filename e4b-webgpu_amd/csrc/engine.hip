@@ -269,8 +269,7 @@ static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
   const int af = k.rope_angles_full ? k.rope_angles_full : k.rope_angles;
   if (k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || af < 0 || af > hdf / 2)
     return bad("rotated pairs beyond half the head dim");
-  if (k.flags & (E4B_FLAG_PERSISTENT | E4B_FLAG_KV_SCORE))
-    return bad("E4B_FLAG_PERSISTENT and E4B_FLAG_KV_SCORE are E4B-recipe features");
+  if (k.flags & E4B_FLAG_PERSISTENT) return bad("E4B_FLAG_PERSISTENT is an E4B-recipe feature");
   return true;
 }
 
@@ -536,6 +535,21 @@ int finalize_a4b(e4b_ctx* c) {
       (rc = dalloc_t(c, &m.g_dense, (size_t)FF)) || (rc = dalloc_t(c, &m.g_slots, (size_t)kMoeTopK * FE)) ||
       (rc = dalloc_t(c, &m.dense_out, (size_t)H)) || (rc = dalloc_t(c, &m.moe_out, (size_t)H)))
     return rc;
+  // full-layer KV budget (src/engine-a4b.js:587-657): accumulated attention
+  // mass per full layer, the step's raw scores, the keep list and the gather
+  // scratch
+  if (k.flags & E4B_FLAG_KV_SCORE) {
+    const size_t S = (size_t)k.max_seq;
+    size_t rows = 1;
+    for (Layer& ly : c->L)
+      if (ly.global) {
+        if ((rc = dalloc_t(c, &ly.score, (size_t)QH * S))) return rc;
+        rows = std::max(rows, (size_t)ly.kvh * ly.slots * ly.hd);
+      }
+    if ((rc = dalloc_t(c, &c->raw, (size_t)QH * S)) || (rc = dalloc_t(c, &c->keep, S)) ||
+        (rc = dalloc_t(c, &c->kv_sk, rows)) || (rc = dalloc_t(c, &c->kv_sv, rows)))
+      return rc;
+  }
   // batched prefill (src/engine-a4b.js:259-295, 465-584): chunks of up to 512
   // tokens; a chunk must leave every key its queries need in the sliding
   // rings (ring >= window + M - 1, the Complete condition of
@@ -847,9 +861,12 @@ int record_step_a4b(e4b_ctx* c) {
     ag.gch = ly.gch;
     ag.keqv = ly.keqv;
     ag.eps = k.eps;
+    ag.raw = ly.score ? c->raw : nullptr;
     GemvOut oo = {c->o, nullptr, nullptr, 0};
-    if ((rc = launch_attn_gen(ag, st)) ||
-        (rc = tick(c, ly.global ? "attn_global" : "attn_sliding")) ||
+    if ((rc = launch_attn_gen(ag, st)) || (rc = tick(c, ly.global ? "attn_global" : "attn_sliding")) ||
+        (ly.score && ((rc = launch_attn_score(c->part_ml, c->raw, c->params, 4, QH, ly.slots, kAttnGenChunk, ly.score,
+                                              st)) ||
+                      (rc = tick(c, "attn_score")))) ||
         (rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * ly.hd), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1,
                          st)) ||
         (rc = tick(c, "o_proj")))
@@ -1738,7 +1755,7 @@ extern "C" int e4b_kv_compact(e4b_ctx* c, int budget, int protect) {
   if (!(c->cfg.flags & E4B_FLAG_KV_SCORE))
     return e4b_fail(E4B_ESTATE, "e4b_kv_compact: the context was created without E4B_FLAG_KV_SCORE");
   if (budget < 0 || protect < 0) return e4b_fail(E4B_EINVAL, "e4b_kv_compact: budget %d, protect %d", budget, protect);
-  const int QH = c->cfg.q_heads, KVH = c->cfg.kv_heads, HD = c->cfg.head_dim;
+  const int QH = c->cfg.q_heads;
   const int64_t n = c->kv_count;
   std::vector<float> sc;
   std::vector<uint32_t> keep((size_t)std::max<int64_t>(n, 1));
@@ -1752,7 +1769,11 @@ extern "C" int e4b_kv_compact(e4b_ctx* c, int budget, int protect) {
     const int cnt = (int)sel;
     if (cnt > 0) {
       E4B_HIP(hipMemcpyAsync(c->keep, keep.data(), (size_t)cnt * 4, hipMemcpyHostToDevice, c->st));
-      if ((rc = launch_kv_gather(c->keep, cnt, ly.kc, ly.vc, KVH, ly.slots, c->kv_sk, c->kv_sv, ly.slots, c->st)))
+      const int KVH = ly.kvh, HD = ly.hd;
+      if ((rc = HD == 256 ? launch_kv_gather(c->keep, cnt, ly.kc, ly.vc, KVH, ly.slots, c->kv_sk, c->kv_sv, ly.slots,
+                                             c->st)
+                          : launch_kv_gather_gen(c->keep, cnt, ly.kc, ly.vc, KVH, ly.slots, HD, c->kv_sk, c->kv_sv,
+                                                 ly.slots, c->st)))
         return rc;
       // rows [0, cnt) of every head back into the cache
       for (int g = 0; g < KVH; ++g) {

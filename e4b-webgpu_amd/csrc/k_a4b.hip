@@ -112,7 +112,7 @@ DEV Live live_of(const AttnGen& A) {
 // the chunk's 64 positions; P.V with the weights broadcast from LDS, folded
 // over the 8 waves.  A chunk's K is read by all HD / 128 slices (from L2
 // after the first); V is split across them.
-template <int HD, int GQA>
+template <int HD, int GQA, bool RAW>
 __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
   constexpr int NW = 8, CS = kAttnGenChunk, PER = HD / 64, PW = CS / NW, VD = 128;
   constexpr int NR = GQA + 2, RPW = (NR + NW - 1) / NW, LPH = 64 / GQA;
@@ -253,7 +253,11 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
         t[h] = a;
       }
       const float sc = reduce_rows<64, GQA>(t);
-      if ((lane % LPH) == 0 && j < m) es[lane / LPH][j] = sc;
+      if ((lane % LPH) == 0 && j < m) {
+        es[lane / LPH][j] = sc;
+        // raw scores for the mass of a scored full layer (one V slice writes them)
+        if (RAW && zs == 0) A.raw[(int64_t)(g * GQA + lane / LPH) * A.slots + slot_at(j)] = sc;
+      }
     }
   }
   lds_sync();
@@ -561,6 +565,23 @@ __global__ __launch_bounds__(256) void k_attn_rows_gen(AttnRowsGen A) {
   }
 }
 
+// compaction gather (kernels/kvgather.wgsl): block (i, g) copies row keep[i]
+// of head g to row i, K by threads [0, hd/8) and V by [hd/8, hd/4), 16 bytes each
+__global__ __launch_bounds__(256) void k_kv_gather_gen(const uint32_t* __restrict__ keep,
+                                                       const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+                                                       int slots, int hd, uint16_t* __restrict__ dk,
+                                                       uint16_t* __restrict__ dv, int dslots) {
+  const int i = blockIdx.x, g = blockIdx.y, t = threadIdx.x, nr = hd / 8;
+  if (t >= 2 * nr) return;
+  const int part = t < nr ? t : t - nr;
+  const int64_t src = ((int64_t)g * slots + keep[i]) * hd + 8 * part;
+  const int64_t dst = ((int64_t)g * dslots + i) * hd + 8 * part;
+  if (t < nr)
+    *reinterpret_cast<uint4*>(dk + dst) = *reinterpret_cast<const uint4*>(kc + src);
+  else
+    *reinterpret_cast<uint4*>(dv + dst) = *reinterpret_cast<const uint4*>(vc + src);
+}
+
 }  // namespace
 
 int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
@@ -573,15 +594,22 @@ int launch_rownorm(const float* h_in, float* h_out, const float* a, const float*
   return E4B_OK;
 }
 
-template <int HD>
-static void launch_attn_hd(const AttnGen& a, hipStream_t st) {
+template <int HD, bool RAW>
+static void launch_attn_hd_raw(const AttnGen& a, hipStream_t st) {
   const dim3 grid(a.kvh, a.gch, HD / 128);
   switch (a.qh / a.kvh) {
-    case 1: hipLaunchKernelGGL((k_attn_gen<HD, 1>), grid, dim3(512), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((k_attn_gen<HD, 2>), grid, dim3(512), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((k_attn_gen<HD, 4>), grid, dim3(512), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((k_attn_gen<HD, 8>), grid, dim3(512), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((k_attn_gen<HD, 1, RAW>), grid, dim3(512), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_attn_gen<HD, 2, RAW>), grid, dim3(512), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_attn_gen<HD, 4, RAW>), grid, dim3(512), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_attn_gen<HD, 8, RAW>), grid, dim3(512), 0, st, a); break;
   }
+}
+template <int HD>
+static void launch_attn_hd(const AttnGen& a, hipStream_t st) {
+  if (a.raw)
+    launch_attn_hd_raw<HD, true>(a, st);
+  else
+    launch_attn_hd_raw<HD, false>(a, st);
   hipLaunchKernelGGL(k_attn_merge<HD>, dim3(a.qh), dim3(256), 0, st, a);
 }
 
@@ -589,7 +617,8 @@ int launch_attn_gen(const AttnGen& a, hipStream_t st) {
   const int gqa = a.kvh > 0 ? a.qh / a.kvh : 0;
   if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
       a.angles < 0 || a.angles > a.hd / 2 || a.slots <= 0 || a.gch <= 0 || (a.window > 0 && a.slots < a.window) ||
-      (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots) || a.gch > kMergeMaxChunks)
+      (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots) || a.gch > kMergeMaxChunks ||
+      (a.raw && a.window > 0))
     return e4b_fail(E4B_EINVAL, "attention: head_dim %d, %d/%d heads (1, 2, 4 or 8 per KV head), %d pairs, %d slots, "
                     "%d chunks", a.hd, a.qh, a.kvh, a.angles, a.slots, a.gch);
   if (a.hd == 256)
@@ -637,6 +666,16 @@ int launch_attn_rows_gen(const AttnRowsGen& a, int M, hipStream_t st) {
     launch_attn_rows_hd<256>(a, M, st);
   else
     launch_attn_rows_hd<512>(a, M, st);
+  E4B_HIP(hipGetLastError());
+  return E4B_OK;
+}
+
+int launch_kv_gather_gen(const uint32_t* keep, int n, const uint16_t* kc, const uint16_t* vc, int kvh, int slots,
+                         int hd, uint16_t* dk, uint16_t* dv, int dslots, hipStream_t st) {
+  if (n <= 0) return E4B_OK;
+  if (n > dslots || hd % 8 || hd > 1024 || kvh <= 0)
+    return e4b_fail(E4B_EINVAL, "kv gather: %d rows into %d, head dim %d", n, dslots, hd);
+  hipLaunchKernelGGL(k_kv_gather_gen, dim3(n, kvh), dim3(256), 0, st, keep, kc, vc, slots, hd, dk, dv, dslots);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -822,10 +822,25 @@ static void a4b_layer(const orc_model* m, orc_state* st, int l, float* h, uint32
     memcpy(st->kc[l] + slot * KVH * HD, krow, sizeof(uint16_t) * (size_t)KVH * HD);
     memcpy(st->vc[l] + slot * KVH * HD, vrow, sizeof(uint16_t) * (size_t)KVH * HD);
   }
-  if (glob)
-    orc_attn_linear(qp, st->kc[l], st->vc[l], QH, KVH, HD, (uint32_t)(kv + 1), ao);
-  else
+  if (glob) {
+    /* slots [0, kv]; with scoring, each slot's weight joins its mass (attnos */
+    /* SCORE, kernels/attnos.wgsl:78-92), as on the E4B recipe's full layers   */
+    const int64_t len = kv + 1;
+    int64_t* sl = malloc(sizeof(int64_t) * (size_t)len);
+    double* pr = malloc(sizeof(double) * (size_t)len);
+    for (int64_t t = 0; t < len; ++t) sl[t] = t;
+    for (int hh = 0; hh < QH; ++hh) {
+      attn_rows_p(qp + (size_t)hh * HD, st->kc[l], st->vc[l], KVH, hh / (QH / KVH), HD, sl, len,
+                  ao + (size_t)hh * HD, st->scoring ? pr : NULL);
+      if (st->scoring)
+        for (int64_t t = 0; t < len; ++t)
+          st->score[l][hh * m->max_seq + t] = st->score[l][hh * m->max_seq + t] + (float)pr[t];
+    }
+    free(sl);
+    free(pr);
+  } else {
     orc_attn_ring(qp, st->kc[l], st->vc[l], QH, KVH, HD, m->ring, m->window, pos, ao);
+  }
   orc_h2f_n(ao, (int64_t)QH * HD, a);
   orc_q40_gemv(ly->wo, H, QH * HD, a, o);
   double io = rms_inv(o, H, m->eps);

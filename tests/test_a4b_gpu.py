@@ -83,15 +83,16 @@ def synced_steps(eng, om, osync, cfg, tokens, start):
     out, ties = [], []
     for k, t in enumerate(tokens):
         pos = start + k
+        kv = eng.kv_count()  # the full layers' slot of this token (its position until a compaction)
         g, lg = eng.step(int(t), pos, want_logits=True)
         o_tok, o_lg, _ = om.step(int(t), pos, want_logits=True)
         rows = []
         for layer in range(cfg.layers):
             kg, vg = eng.read_kv(layer)
             osync.set_kv(layer, kg.transpose(1, 0, 2), vg.transpose(1, 0, 2))
-            slot = pos if cfg.layer_global[layer] else pos % kg.shape[1]
+            slot = kv if cfg.layer_global[layer] else pos % kg.shape[1]
             rows.append((kg[:, slot, :], vg[:, slot, :]))
-        osync.set_kv_count(pos)
+        osync.set_kv_count(kv)
         s_tok, s_lg, s_h = osync.step(int(t), pos, want_logits=True, want_hidden=True)
         margin = osync.route_margin()
         d = np.abs(lg.astype(np.float64) - s_lg)
@@ -333,3 +334,63 @@ def test_a4b_batched_prefill_long_prompt_vs_step_prefill():
             assert d.mean() <= KV_MEAN_TOL * np.abs(fy).mean(), f"layer {layer} cache (mean)"
     ta, tb = a.decode_chunk(140, 8), b.decode_chunk(140, 8)
     print(f"continuations {ta.tolist()} / {tb.tolist()}")
+
+
+def test_a4b_kv_budget_scores_compaction_and_decode():
+    # the full-layer KV budget on the A4B recipe (src/engine-a4b.js:587-657):
+    # after a batched prefill (no mass) 9 GPU-fed decode steps accumulate the
+    # full layer's attention mass (head dim 512, 1 KV head for 8 q heads);
+    # the mass sums to the steps per head and matches the teacher-forced
+    # oracle's; compaction to 16 entries (protect 4) gathers the engine's own
+    # rows bit-exactly; decode then continues from the compacted slots,
+    # synced with the oracle step by step
+    from e4b._lib import FLAG_KV_SCORE
+    from tests.test_kv_budget_gpu import SCORE_TOL
+    cfg = tiny_a4b_config(max_seq=64, flags=FLAG_KV_SCORE)
+    full = cfg.layer_global.index(1)
+    eng, om, osync = _models(cfg, 121)
+    rng = np.random.default_rng(122)
+    prompt = rng.integers(0, cfg.vocab, 30)
+    g0 = eng.prefill(prompt)
+    assert eng.kv_count() == 30 and np.all(eng.read_scores(full) == 0)
+    om.set_scoring(False)
+    for i, t in enumerate(prompt):
+        om.step(int(t), i)
+    om.set_scoring(True)
+    toks = eng.decode_chunk(30, 9).tolist()
+    fed = [g0] + toks
+    for i in range(9):
+        om.step(int(fed[i]), 30 + i)
+    n = 39
+    sc, osc = eng.read_scores(full).astype(np.float64), om.score(full).astype(np.float64)
+    assert eng.kv_count() == n == om.kv_count()
+    np.testing.assert_allclose(sc.sum(axis=1), 9, rtol=1e-4)
+    assert np.all(sc[:, n:] == 0) and np.all(sc >= 0)
+    err = float(np.abs(sc - osc).max())
+    print(f"A4B scores: 9 steps, max |gpu - oracle| {err:.2e}")
+    assert err < SCORE_TOL * 9
+    keep = orc.kv_keep(eng.read_scores(full), n, 16, 4)
+    k_before, v_before = eng.read_kv(full)
+    assert eng.compact(16, 4) == 16 == len(keep) == eng.kv_count()
+    k_after, v_after = eng.read_kv(full)
+    assert np.array_equal(k_after[:, :16], k_before[:, keep]) and np.array_equal(v_after[:, :16], v_before[:, keep])
+    assert np.all(eng.read_scores(full) == 0)
+    om.compact_with({full: keep})
+    errs, ties = synced_steps(eng, om, osync, cfg, rng.integers(0, cfg.vocab, 12), 39)
+    assert eng.kv_count() == om.kv_count() == 28
+    print(f"A4B after compaction: synced max {errs[:, 0].max():.2e}, free max {errs[:, 1].max():.2e}; ties {ties}")
+
+
+def test_a4b_generate_long_runs_the_schedule():
+    # generateLong on the A4B recipe with a small budget: the prompt past
+    # decap takes the probe step and a compaction, later chunks recompact
+    # before passing decap; the run ends within the budget and equals a
+    # second engine's (same weights, same schedule)
+    from e4b._lib import FLAG_KV_SCORE
+    cfg = tiny_a4b_config(max_seq=64, flags=FLAG_KV_SCORE)
+    tensors = norm_weights_random(synth_tensors(cfg, 131), 132)
+    a, b = Engine(cfg, tensors), Engine(cfg, tensors)
+    prompt = np.random.default_rng(133).integers(0, cfg.vocab, 30)
+    out = a.generate_long(prompt, 40, eos=(), budget=16, protect=4, decap=24)
+    assert len(out) == 40 and a.kv_count() <= 24
+    assert b.generate_long(prompt, 40, eos=(), budget=16, protect=4, decap=24) == out

@@ -255,3 +255,28 @@ def test_one_ulp_nudge_jumps_in_the_a4b_recipe():
           f"{jumps.max():.2e} of the hidden range")
     assert (jumps == 0).sum() >= jumps.size // 2
     assert jumps.max() > 100 * 2.0 ** -23
+
+
+def test_a4b_full_layer_mass_sums_to_the_scored_steps():
+    # scoring on the A4B recipe's full layer (head dim 512, V = K): every
+    # scored step adds one normalised weight row per q head, so each head's
+    # mass sums to the number of scored steps and stays 0 past the entries;
+    # the sliding layers keep none
+    from e4b.model import norm_weights_random
+    cfg = tiny_a4b_config(max_seq=64)
+    tens = {n: t.data for n, t in norm_weights_random(synth_tensors(cfg, 61), 62).items()}
+    om = orc.OracleModel(cfg.as_dict(), tens)
+    rng = np.random.default_rng(63)
+    for i, t in enumerate(rng.integers(0, cfg.vocab, 12)):
+        om.step(int(t), i)
+    om.set_scoring(True)
+    for i, t in enumerate(rng.integers(0, cfg.vocab, 7)):
+        om.step(int(t), 12 + i)
+    full = cfg.layer_global.index(1)
+    sc = om.score(full).astype(np.float64)
+    np.testing.assert_allclose(sc.sum(axis=1), 7, rtol=1e-5)
+    assert np.all(sc[:, 19:] == 0) and np.all(sc[:, :19] > 0)
+    # compaction keeps the protected newest entries and the heaviest others
+    keep = orc.kv_keep(om.score(full), 19, 10, 3)
+    assert len(keep) == 10 and list(keep[-3:]) == [16, 17, 18]
+    assert om.compact(10, 3) == 10 == om.kv_count()
