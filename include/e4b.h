@@ -304,7 +304,7 @@ typedef struct e4b_config {
    * a multiple of 256 up to 3072, head_dim 256, head_dim_full 256 or 512,
    * 1, 2, 4 or 8 q heads per KV head on every layer, ffn and expert_ffn
    * multiples of 32 (<= 3072, <= 768), 8..256 experts, ple_dim 0; not with
-   * E4B_FLAG_PERSISTENT or E4B_FLAG_KV_SCORE.  e4b_prefill runs the
+   * E4B_FLAG_PERSISTENT.  e4b_prefill runs the
    * batched prefill of src/engine-a4b.js:465-584 (chunks of up to 512
    * tokens, ring - window + 1 at most). */
   int32_t recipe;              /* E4B_RECIPE_E4B (0) or E4B_RECIPE_A4B (1) */
