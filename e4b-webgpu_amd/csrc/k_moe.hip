@@ -286,11 +286,14 @@ __global__ __launch_bounds__(64) void k_moe_topk(MoeArgs A) {
 
 // ---- gate/up + GeGLU, dense branch and 8 expert slots ------------------------
 // 32 lanes per unit (a gate row and its up row), 3 blocks per lane (88-block
-// rows of the 2816-wide input), 2 units per wave tile.  Units [0, FF2) are
+// rows of the 2816-wide input), GU_U units per lane group and 2 GU_U per
+// wave tile (2 measured fastest at the A4B shape: c3 23.3 us per half-layer
+// against 24.3 with 1 and 24.1 with 4).  Units [0, FF2) are
 // dense, then slot k covers [FF2 + k FF, FF2 + (k+1) FF).  The block stages
 // both f16 inputs in LDS once (a block can hold dense and expert waves):
 // read per wave, the input would cost more on-chip traffic than the weights.
 constexpr int GU_LPR = 32, GU_BPL = 3;
+constexpr int GU_U = 2;  // units per lane group (a wave tile holds 2 GU_U units)
 constexpr int kMoeMaxH = GU_LPR * GU_BPL * 32;  // 3072
 
 __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
@@ -300,13 +303,13 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / GU_LPR, l = lane % GU_LPR;
   const int nb = A.H / 32;
-  // one tile (2 units) per wave; idle waves of the last workgroup repeat the
-  // last tile and store nothing
+  // one tile (2 GU_U units) per wave; idle waves of the last workgroup
+  // repeat the last tile and store nothing
   const int64_t tile_id = (int64_t)blockIdx.x * 4 + wave;
   const bool live = tile_id < ntiles;
   const int64_t tile = live ? tile_id : ntiles - 1;
-  const int u = (int)(2 * tile) + g;    // this group's unit
-  const bool dense = 2 * tile < A.FF2;  // wave-uniform: FF2 and FF are even
+  const int u = (int)(2 * GU_U * tile) + GU_U * g;  // this group's first unit
+  const bool dense = 2 * GU_U * tile < A.FF2;        // wave-uniform: FF2 and FF are multiples of 2 GU_U
 
   // 1. both inputs (independent of the routing), two 16-byte pieces per
   //    thread and input at most (H <= 3072)
@@ -320,24 +323,27 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   //    selection, made once per workgroup by wave 0 from the 128 scores and
   //    handed over in LDS (wave 0 of block 0 also stores the picks and their
   //    weights for the down kernel)
-  uint4 wq[2][GU_BPL];
-  uint32_t ws[2][GU_BPL], odd = 0;  // aligned scale pairs (ld_scale_pair)
-  auto load_rows = [&](const Q40Mat& W, int64_t row_g, int64_t row_u) {
+  // rows 2i (gate) and 2i + 1 (up) of unit u + i
+  uint4 wq[2 * GU_U][GU_BPL];
+  uint32_t ws[2 * GU_U][GU_BPL], odd = 0;  // aligned scale pairs (ld_scale_pair)
+  auto load_rows = [&](const Q40Mat& W, int64_t row_g, int64_t up_off) {
 #pragma unroll
-    for (int b = 0; b < GU_BPL; ++b) {
-      const int jb = min(l + GU_LPR * b, nb - 1);
-      const int64_t eg = row_g * nb + jb, eu = row_u * nb + jb;
-      wq[0][b] = ld_nt_u4(W.nib + eg);
-      ws[0][b] = ld_scale_pair(W.sc, eg);
-      wq[1][b] = ld_nt_u4(W.nib + eu);
-      ws[1][b] = ld_scale_pair(W.sc, eu);
-      odd |= (uint32_t)(eg & 1) << b;
-      odd |= (uint32_t)(eu & 1) << (GU_BPL + b);
-    }
+    for (int i = 0; i < GU_U; ++i)
+#pragma unroll
+      for (int b = 0; b < GU_BPL; ++b) {
+        const int jb = min(l + GU_LPR * b, nb - 1);
+        const int64_t eg = (row_g + i) * nb + jb, eu = (row_g + i + up_off) * nb + jb;
+        wq[2 * i][b] = ld_nt_u4(W.nib + eg);
+        ws[2 * i][b] = ld_scale_pair(W.sc, eg);
+        wq[2 * i + 1][b] = ld_nt_u4(W.nib + eu);
+        ws[2 * i + 1][b] = ld_scale_pair(W.sc, eu);
+        odd |= (uint32_t)(eg & 1) << (2 * i * GU_BPL + b);
+        odd |= (uint32_t)(eu & 1) << ((2 * i + 1) * GU_BPL + b);
+      }
   };
-  if (dense) load_rows(A.dense_gu, u, A.FF2 + u);
+  if (dense) load_rows(A.dense_gu, u, A.FF2);
   // the block holds expert waves iff its last (clamped) tile is an expert tile
-  const bool blk_expert = 2 * min((int64_t)blockIdx.x * 4 + 3, ntiles - 1) >= A.FF2;
+  const bool blk_expert = 2 * GU_U * min((int64_t)blockIdx.x * 4 + 3, ntiles - 1) >= A.FF2;
   if (wave == 0 && (blk_expert || blockIdx.x == 0)) {
     TopK t;
     if (blockIdx.x == 0) {
@@ -372,7 +378,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     slot = (u - A.FF2) / A.FF;
     j = (u - A.FF2) - slot * A.FF;
     const int64_t row_g = (int64_t)sel[slot] * 2 * A.FF + j;
-    load_rows(A.exp_gu, row_g, row_g + A.FF);
+    load_rows(A.exp_gu, row_g, A.FF);
   }
   const uint32_t* x = reinterpret_cast<const uint32_t*>(xs[dense ? 0 : 1]);
   uint32_t xp[GU_BPL][16];
@@ -380,7 +386,9 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   for (int b = 0; b < GU_BPL; ++b) load_x16(x, min(l + GU_LPR * b, nb - 1), xp[b]);
 
   // 4. dot products, GeGLU
-  float acc[2] = {0.f, 0.f};
+  float acc[2 * GU_U];
+#pragma unroll
+  for (int r = 0; r < 2 * GU_U; ++r) acc[r] = 0.f;
 #pragma unroll
   for (int b = 0; b < GU_BPL; ++b) {
     const bool in = l + GU_LPR * b < nb;
@@ -388,34 +396,40 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     for (int i = 0; i < 16; ++i) xp[b][i] = in ? xp[b][i] : 0u;
     const float xs8 = -8.f * xsum16(xp[b]);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < 2 * GU_U; ++r) {
       float a0 = 0.f, a1 = 0.f;
       q40_dot2(wq[r][b], xp[b], a0, a1);
       const float d = scale_of(ws[r][b], (odd >> (r * GU_BPL + b)) & 1);
       acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8)), acc[r]);
     }
   }
-  const float v = reduce_rows<GU_LPR, 2>(acc);  // lanes 0..15 gate, 16..31 up
-  const float up = __shfl_xor(v, GU_LPR / 2, 64);
-  if (live && l == 0) {
+  // lanes [SPAN r, SPAN r + SPAN) of the group hold row r: gate of unit r / 2
+  // for even r, its up row for odd r
+  constexpr int SPAN = GU_LPR / (2 * GU_U);
+  const float v = reduce_rows<GU_LPR, 2 * GU_U>(acc);
+  const float up = __shfl_xor(v, SPAN, 64);
+  const int i = l / (2 * SPAN);
+  if (live && (l % (2 * SPAN)) == 0) {
     const uint16_t y = f2h(gelu_tanh(v) * up);
     if (dense)
-      A.g_dense[u] = y;
+      A.g_dense[u + i] = y;
     else
-      A.g_slots[(int64_t)slot * A.FF + j] = y;
+      A.g_slots[(int64_t)slot * A.FF + j + i] = y;
   }
 }
 
 // ---- down projections -------------------------------------------------------
 // Blocks [0, nbd) run the dense down rows (32 lanes x 3 blocks per row of
-// FF2/32 blocks, 2 rows per group, 4 per wave tile); the rest run the expert
-// rows: for output row o the 8 lane groups are the 8 slots (8 lanes x 3
-// blocks of the FF/32 = 22-block rows), 4 output rows per wave tile, and the
-// slot results are combined with the router weights across the groups.  One
-// tile per wave; the block's f16 input (the dense GeGLU output, or the 8
-// slots' outputs) is staged in LDS once.
-constexpr int DD_LPR = 32, DD_BPL = 3, DD_R = 2;
-constexpr int DE_LPR = 8, DE_BPL = 3, DE_R = 4;
+// FF2/32 blocks, DD_R rows per group, 2 DD_R per wave tile); the rest run
+// the expert rows: for output row o the 8 lane groups are the 8 slots (8
+// lanes x 3 blocks of the FF/32 = 22-block rows), DE_R output rows per wave
+// tile, and the slot results are combined with the router weights across
+// the groups.  One tile per wave; the block's f16 input (the dense GeGLU
+// output, or the 8 slots' outputs) is staged in LDS once.  One row per
+// group and tile measured fastest at the A4B shape (c3: 22.5 us per
+// half-layer against 23.3 with 2 / 4 rows and 26.0 with 4 / 8).
+constexpr int DD_LPR = 32, DD_BPL = 3, DD_R = 1;
+constexpr int DE_LPR = 8, DE_BPL = 3, DE_R = 1;
 constexpr int kMoeMaxX = K * DE_LPR * DE_BPL * 32;  // 6144 >= FF2 and 8 FF
 
 __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
@@ -606,7 +620,7 @@ int launch_moe_router(const MoeArgs& A, hipStream_t st) {
 }
 
 int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
-  if (A.H % 256 || A.H > kMoeMaxH || A.H > 256 * kTailPer || A.FF % 32 || A.FF2 % 32 || A.FF % 2 ||
+  if (A.H % 256 || A.H > kMoeMaxH || A.H > 256 * kTailPer || A.FF % 32 || A.FF2 % 32 || A.FF % (2 * GU_U) ||
       A.FF2 / 32 > DD_LPR * DD_BPL || A.FF / 32 > DE_LPR * DE_BPL || A.FF2 > kMoeMaxX || K * A.FF > kMoeMaxX ||
       A.FF2 > 3 * 256 * 8 || K * A.FF > 3 * 256 * 8 || A.E < K || A.E > 256)
     return e4b_fail(E4B_EINVAL,
@@ -617,7 +631,7 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
     return e4b_fail(E4B_EINVAL, "MoE layer: the attention residual needs post_attn and an h1 buffer apart from h");
   int rc = launch_moe_router(A, st);
   if (rc) return rc;
-  const int64_t gu_tiles = (A.FF2 + (int64_t)K * A.FF) / 2;
+  const int64_t gu_tiles = (A.FF2 + (int64_t)K * A.FF) / (2 * GU_U);
   const int64_t gu_wgs = (gu_tiles + 3) / 4;  // one tile per wave
   hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)gu_wgs), dim3(256), 0, st, A, gu_tiles);
   const int dd_tiles = (A.H + 2 * DD_R - 1) / (2 * DD_R), de_tiles = (A.H + DE_R - 1) / DE_R;
