@@ -505,7 +505,7 @@ int finalize_a4b(e4b_ctx* c) {
   c->chunk = kAttnGenChunk;
   c->ring_cap = k.max_seq;
   c->max_prompt = k.max_prompt > 0 ? k.max_prompt : k.max_seq;
-  c->amax_parts = q6k_gemv_grid(k.vocab);
+  c->amax_parts = q6k_gemv_grid(k.vocab, k.hidden / 32);
   c->pf_cap = 0;
   size_t part = 0, ml = 0;
   int hd_max = 0;
@@ -616,7 +616,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
     return e4b_fail(E4B_EINVAL, "max_seq %d needs %d attention chunks (max %d)", k.max_seq, c->nch, kAttnMaxChunks);
   c->ring_cap = k.max_seq;
   c->max_prompt = k.max_prompt > 0 ? k.max_prompt : k.max_seq;
-  c->amax_parts = q6k_gemv_grid(k.vocab);
+  c->amax_parts = q6k_gemv_grid(k.vocab, k.hidden / 32);
   // caches
   for (int l = 0; l < k.layers; ++l) {
     Layer& ly = c->L[l];

@@ -258,23 +258,30 @@ int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipS
   return E4B_OK;
 }
 
-int q6k_gemv_grid(int64_t rows) {
-  const int64_t ntiles = (rows + kQ6Rows - 1) / kQ6Rows;
+// rows per wave tile: kQ6Rows with one segment per lane (<= 2048 columns);
+// a quarter as many with two (each row then takes 8 loads per lane: the 63 a
+// wave can keep in flight are not exceeded, and the 2816-column A4B lm-head
+// measured 177 us with 8 rows, 127 with 4, 124 with 2)
+static int q6k_rows(int nseg) { return nseg <= 64 ? kQ6Rows : kQ6Rows / 4; }
+
+int q6k_gemv_grid(int64_t rows, int nseg) {
+  const int R = q6k_rows(nseg);
+  const int64_t ntiles = (rows + R - 1) / R;
   const int64_t wgs = (ntiles + 3) / 4;
   return (int)(wgs < 2048 ? wgs : 2048);
 }
 
 int launch_q6k_gemv_argmax(const Q6Mat& W, const uint32_t* xh, const uint32_t* xl, float softcap, float* logits,
                            uint32_t* amax, uint2* part, hipStream_t st) {
-  constexpr int R = kQ6Rows;
+  const int R = q6k_rows(W.nseg);
   const int64_t ntiles = (W.rows + R - 1) / R;
-  const int64_t wgs = q6k_gemv_grid(W.rows);
+  const int64_t wgs = q6k_gemv_grid(W.rows, W.nseg);
   if (W.nseg <= 64)
-    hipLaunchKernelGGL((k_q6k_gemv_argmax<1, R>), dim3((unsigned)wgs), dim3(256), 0, st, W, xh, xl, softcap, logits,
-                       part, ntiles);
+    hipLaunchKernelGGL((k_q6k_gemv_argmax<1, kQ6Rows>), dim3((unsigned)wgs), dim3(256), 0, st, W, xh, xl, softcap,
+                       logits, part, ntiles);
   else if (W.nseg <= 128)
-    hipLaunchKernelGGL((k_q6k_gemv_argmax<2, R>), dim3((unsigned)wgs), dim3(256), 0, st, W, xh, xl, softcap, logits,
-                       part, ntiles);
+    hipLaunchKernelGGL((k_q6k_gemv_argmax<2, kQ6Rows / 4>), dim3((unsigned)wgs), dim3(256), 0, st, W, xh, xl, softcap,
+                       logits, part, ntiles);
   else
     return e4b_fail(E4B_EINVAL, "Q6_K GEMV: %d columns exceeds the 4096-column maximum", W.nseg * 32);
   if (amax) hipLaunchKernelGGL(k_amax_final, dim3(1), dim3(256), 0, st, part, (int)wgs, amax);

@@ -153,7 +153,7 @@ int launch_q40_gemv(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, flo
 int launch_split_f32(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st);
 // part: one (index, value) partial per block (<= 2048); amax may be NULL to
 // leave the fold to the caller (k_amax_final semantics)
-int q6k_gemv_grid(int64_t rows);  // number of argmax partials the lm-head writes
+int q6k_gemv_grid(int64_t rows, int nseg);  // number of argmax partials the lm-head writes (nseg = cols / 32)
 int launch_q6k_gemv_argmax(const Q6Mat& W, const uint32_t* xh, const uint32_t* xl, float softcap,
                            float* logits, uint32_t* amax, uint2* part, hipStream_t st);
 int launch_q6k_row(const Q6Mat& W, int64_t row, const uint32_t* row_dev, float mult, float* out, hipStream_t st);

@@ -284,9 +284,9 @@ extern "C" int e4b_k_q6k_gemv_argmax_noalloc(const void* w_packed, int64_t rows,
                     "e4b_k_q6k_gemv_argmax_noalloc: %lld columns exceed the %zu-column maximum of its %zu-byte "
                     "scratch",
                     (long long)cols, kNoAllocHalf / sizeof(uint16_t), kNoAllocBytes);
-  if ((size_t)q6k_gemv_grid(rows) * sizeof(uint2) > kNoAllocPart)
+  if ((size_t)q6k_gemv_grid(rows, (int)(cols / 32)) * sizeof(uint2) > kNoAllocPart)
     return e4b_fail(E4B_ERANGE, "e4b_k_q6k_gemv_argmax_noalloc: %d argmax partials exceed the scratch",
-                    q6k_gemv_grid(rows));
+                    q6k_gemv_grid(rows, (int)(cols / 32)));
   if (!aligned16(w_packed))
     return e4b_fail(E4B_EINVAL, "e4b_k_q6k_gemv_argmax_noalloc: weight must be 16-byte aligned");
   uint8_t* sp = nullptr;
