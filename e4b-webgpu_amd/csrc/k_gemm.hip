@@ -36,6 +36,20 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+// staged 16-byte pieces as a native vector: an array of HIP's uint4 struct
+// kept across the K loop is not split into registers (it stays in scratch,
+// and the next stage's loads are waited for before the current MFMAs;
+// measured 1.55x slower on the expert-grouped GEMMs)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// the prefetch registers of a stage: native vectors, except in the widest
+// GeGLU tile (4 token tiles x 2 x 32 rows per wave), whose accumulators and
+// operands already take 256 VGPRs.  There the uint4 struct array is what the
+// compiler moves to LDS (16 KB per workgroup), which keeps 2 waves per SIMD
+// (the native vectors in registers leave 1 wave and measured 16 % slower)
+template <int T, int EPI>
+using StageVec = std::conditional_t<T == 4 && EPI == GEMM_GLU, uint4, u32x4>;
+DEV u32x4 as_vec(u32x4 v) { return v; }
+DEV u32x4 as_vec(const uint4& v) { return u32x4{v.x, v.y, v.z, v.w}; }
 
 // 8 exact f16 values (n - 8) of one repacked nibble word, in element order
 DEV h8 nib_word_f16(uint32_t w) {
@@ -64,9 +78,9 @@ constexpr int KBL = 4;            // q4_0 blocks per stage (128 k); split-K slic
 template <int T, int EPI, bool GRP, int KB = KBL>
 __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs) {
   constexpr int KBL = KB;
-  constexpr int WSL = KBL + 1;      // uint4 per staged weight row (+1 pad: conflict-free 16-byte reads)
+  constexpr int WSL = KBL + 1;      // 16-byte pieces per staged weight row (+1 pad: conflict-free 16-byte reads)
   constexpr int SSL = KBL + 2;      // f16 scales per staged row (+2 pad)
-  constexpr int XSL = KBL * 4 + 1;  // uint4 per staged token row (+1 pad)
+  constexpr int XSL = KBL * 4 + 1;  // 16-byte pieces per staged token row (+1 pad)
   static_assert(KBL == 4 || KBL == 8, "4 or 8 blocks per stage");
   constexpr int NT = EPI == GEMM_GLU ? 2 : 1;
   constexpr int TOK = 32 * T;
@@ -75,9 +89,9 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
   constexpr int SP = RW * KBL / 256;           // scales per thread and stage
   constexpr int XP = TOK * KBL * 4 / 256;      // activation pieces per thread and stage
   static_assert(WP >= 1 && SP >= 1 && XP >= 1, "whole pieces per thread");
-  __shared__ __align__(16) uint4 wl[RW][WSL];
+  __shared__ __align__(16) StageVec<T, EPI> wl[RW][WSL];
   __shared__ uint16_t sl[RW][SSL];
-  __shared__ __align__(16) uint4 xs[TOK][XSL];
+  __shared__ __align__(16) StageVec<T, EPI> xs[TOK][XSL];
   const Q40Mat& W = a.W;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -120,16 +134,16 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
     if constexpr (GRP) xrow = a.gather ? (int64_t)(a.gather[mrow_in[j] ? xrow : tok0] / (uint32_t)a.gather_div) : xrow;
     xrow_of[j] = xrow;
   }
-  uint4 wr[WP];
+  StageVec<T, EPI> wr[WP];
   uint16_t sr[SP];
-  uint4 xr[XP];
+  StageVec<T, EPI> xr[XP];
   auto issue = [&](int kb0) {
 #pragma unroll
     for (int j = 0; j < WP; ++j) {
       const int p = threadIdx.x + 256 * j;
       const int r = p / KBL, b = p % KBL;
       const uint32_t e = (uint32_t)grow(r) * (uint32_t)nb + (uint32_t)min(kb0 + b, nb - 1);
-      wr[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(W.nib) + e * 16u);
+      wr[j] = *reinterpret_cast<const StageVec<T, EPI>*>(reinterpret_cast<const char*>(W.nib) + e * 16u);
     }
 #pragma unroll
     for (int j = 0; j < SP; ++j) {
@@ -144,8 +158,8 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
       const int q = (threadIdx.x + 256 * j) % (KBL * 4);
       const int kq = kb0 * 32 + q * 8;
       const bool in = mrow_in[j] && kq < kend * 32;
-      const uint4 v = *reinterpret_cast<const uint4*>(a.X + (in ? xrow_of[j] * a.ldx + kq : 0));
-      xr[j] = in ? v : make_uint4(0u, 0u, 0u, 0u);
+      const StageVec<T, EPI> v = *reinterpret_cast<const StageVec<T, EPI>*>(a.X + (in ? xrow_of[j] * a.ldx + kq : 0));
+      xr[j] = in ? v : StageVec<T, EPI>{};
     }
   };
   auto store = [&]() {
@@ -191,15 +205,15 @@ __global__ __launch_bounds__(256) void k_q40_gemm_lds(GemmArgs a, int K, int nbs
       float dsc[NT];
 #pragma unroll
       for (int u = 0; u < NT; ++u) {
-        const uint4 w4 = wl[lrow[u]][b];
+        const u32x4 w4 = as_vec(wl[lrow[u]][b]);
         bw[u][0] = nib_word_f16(hi ? w4.y : w4.x);
         bw[u][1] = nib_word_f16(hi ? w4.w : w4.z);
         dsc[u] = h2f(sl[lrow[u]][b]);
       }
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const uint4 a0 = xs[32 * t + l32][4 * b + hi];
-        const uint4 a1 = xs[32 * t + l32][4 * b + 2 + hi];
+        const u32x4 a0 = as_vec(xs[32 * t + l32][4 * b + hi]);
+        const u32x4 a1 = as_vec(xs[32 * t + l32][4 * b + 2 + hi]);
         const h8 av0 = __builtin_bit_cast(h8, a0), av1 = __builtin_bit_cast(h8, a1);
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
