@@ -153,6 +153,119 @@ __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
   }
 }
 
+// ---- router over token rows (batched prefill) -------------------------------
+// grid ceil(E / kRrE) x ceil(M / kRrT), 128 threads: block (bx, by) scores
+// experts [kRrE bx, kRrE bx + kRrE) of token rows [kRrT by, kRrT by + kRrT).
+// Each row's rms and x_r follow k_moe_router's arithmetic step for step (the
+// same 128-thread element split, fmaf chains, wave sums and two-wave sum),
+// so the scores, and the top-8 taken from them, equal the decode router's
+// bit for bit.  An expert row is read once per kRrT token rows instead of
+// once per row (the decode layout over rows re-read the whole router matrix
+// and the row's vectors in every one of its E/2 blocks).  Rows without the
+// attention residual only (the prefill forms h1 before the router).
+constexpr int kRrT = 4, kRrE = 16;
+static_assert(kRrT * kRrE / 2 <= 64, "one score per lane");
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_moe_router_rows(MoeArgs A, int M) {
+  __shared__ __align__(16) float4 xr[kRrT][kRouterMaxH4];
+  __shared__ float red[kRrT][2];
+  constexpr int PT = kRouterMaxH4 / 128;  // float4 per thread and row
+  constexpr int PW = kRouterMaxH4 / 64;   // float4 per lane of an expert row
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int H = A.H, H4 = H / 4, E = A.E;
+  const int r0 = blockIdx.y * kRrT;
+  const float4* rs4 = reinterpret_cast<const float4*>(A.router_scale);
+  const float4* fn4 = reinterpret_cast<const float4*>(A.ffn_norm);
+  const float4* pf4 = reinterpret_cast<const float4*>(A.pre_ffw2);
+  // this block writes float4 [q0, q1) of each row's f16 branch inputs
+  const int per4 = (H4 + gridDim.x - 1) / gridDim.x;
+  const int q0 = blockIdx.x * per4, q1 = min(H4, q0 + per4);
+  // every load up front (clamped, branch-free): the rows, the scale, the
+  // two branch norms
+  float4 hv[kRrT][PT], sv[PT], fv[PT], pv[PT];
+#pragma unroll
+  for (int k = 0; k < PT; ++k) {
+    const int i = min((int)threadIdx.x + 128 * k, H4 - 1);
+    sv[k] = rs4[i];
+    fv[k] = fn4[i];
+    pv[k] = pf4[i];
+#pragma unroll
+    for (int t = 0; t < kRrT; ++t)
+      hv[t][k] = reinterpret_cast<const float4*>(A.h + (int64_t)min(r0 + t, M - 1) * H)[i];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < kRrT; ++t) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+      const float4 v = hv[t][k];
+      const float nx = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+      ss = (int)threadIdx.x + 128 * k < H4 ? nx : ss;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[t][wave] = ss;
+  }
+  lds_sync();
+#pragma unroll
+  for (int t = 0; t < kRrT; ++t) {
+    const float inv = rms_inv(red[t][0] + red[t][1], H, A.eps);
+    const int64_t ro = (int64_t)(r0 + t) * H;
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+      const int i = (int)threadIdx.x + 128 * k;
+      const float4 v = hv[t][k];
+      if (i < H4)
+        xr[t][i] = make_float4(v.x * inv * (sv[k].x * A.router_mult), v.y * inv * (sv[k].y * A.router_mult),
+                               v.z * inv * (sv[k].z * A.router_mult), v.w * inv * (sv[k].w * A.router_mult));
+      if (i >= q0 && i < q1 && r0 + t < M) {
+        const float4 n = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+        uint2 d, m;
+        d.x = (uint32_t)f2h(n.x * fv[k].x) | ((uint32_t)f2h(n.y * fv[k].y) << 16);
+        d.y = (uint32_t)f2h(n.z * fv[k].z) | ((uint32_t)f2h(n.w * fv[k].w) << 16);
+        m.x = (uint32_t)f2h(n.x * pv[k].x) | ((uint32_t)f2h(n.y * pv[k].y) << 16);
+        m.y = (uint32_t)f2h(n.z * pv[k].z) | ((uint32_t)f2h(n.w * pv[k].w) << 16);
+        reinterpret_cast<uint2*>(A.xd + ro)[i] = d;
+        reinterpret_cast<uint2*>(A.xm + ro)[i] = m;
+      }
+    }
+  }
+  lds_sync();
+  // wave w scores experts e0 + w + 2 j (j < kRrE / 2); the next row is
+  // requested before the current one's dot products; lane j kRrT + t keeps
+  // the score of (expert j, row t) for one store at the end
+  const int e0 = blockIdx.x * kRrE + wave;
+  float4 wv[2][PW];
+  auto load_row = [&](float4* dst, int j) {
+    const float4* w4 = reinterpret_cast<const float4*>(A.router_w + (int64_t)min(e0 + 2 * j, E - 1) * H);
+#pragma unroll
+    for (int k = 0; k < PW; ++k) dst[k] = w4[min(lane + 64 * k, H4 - 1)];
+  };
+  load_row(wv[0], 0);
+  float mine = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRrE / 2; ++j) {
+    // the staged rows are read from LDS again for every expert: held in
+    // registers (4 x 12 float4) they leave none for the next row's loads
+    asm volatile("" ::: "memory");
+    if (j + 1 < kRrE / 2) load_row(wv[(j + 1) & 1], j + 1);
+#pragma unroll
+    for (int t = 0; t < kRrT; ++t) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < PW; ++k) {
+        const int i = lane + 64 * k;
+        const float4 x = xr[t][min(i, H4 - 1)], w = wv[j & 1][k];
+        const float nx = fmaf(x.x, w.x, fmaf(x.y, w.y, fmaf(x.z, w.z, fmaf(x.w, w.w, acc))));
+        acc = i < H4 ? nx : acc;
+      }
+      acc = wave_sum(acc);
+      mine = lane == j * kRrT + t ? acc : mine;
+    }
+  }
+  const int j = lane / kRrT, t = lane % kRrT, e = e0 + 2 * j;
+  if (lane < kRrT * kRrE / 2 && e < E && r0 + t < M) A.scores[(int64_t)(r0 + t) * E + e] = mine;
+}
+
 // ---- top-8 in one wave ----------------------------------------------------
 // lane l holds the scores of experts l + 64 j (j < 4, E <= 256); every lane
 // returns the same 8 picks (and, with WEIGHTS, their weights).  Selection on
@@ -643,8 +756,9 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
 }
 
 int launch_moe_router_rows(const MoeArgs& A, int M, hipStream_t st) {
-  if (A.H % 4 || A.H / 4 > kRouterMaxH4 || M < 1) return e4b_fail(E4B_EINVAL, "router rows: H=%d M=%d", A.H, M);
-  hipLaunchKernelGGL(k_moe_router, dim3((A.E + 1) / 2, M), dim3(128), 0, st, A);
+  if (A.H % 4 || A.H / 4 > kRouterMaxH4 || M < 1 || A.E < 1 || A.attn_o)
+    return e4b_fail(E4B_EINVAL, "router rows: H=%d M=%d E=%d (no attention residual over rows)", A.H, M, A.E);
+  hipLaunchKernelGGL(k_moe_router_rows, dim3((A.E + kRrE - 1) / kRrE, (M + kRrT - 1) / kRrT), dim3(128), 0, st, A, M);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

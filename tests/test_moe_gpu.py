@@ -134,6 +134,11 @@ def test_moe_prefill_rows(m, seed, random_norms):
         _check_topk(got["topk_idx"][r], idx, _scores(t, hs[r]), f"prefill m={m} row {r}")
         dec = L.forward(hs[r])
         np.testing.assert_array_equal(got["topk_idx"][r], dec["topk_idx"])
+        # the row router's scores equal the decode router's bit for bit: the
+        # same top-8 kernel on them gives identical weights
+        ri, rw = L.router_top8(hs[r])
+        np.testing.assert_array_equal(got["topk_idx"][r], ri)
+        np.testing.assert_array_equal(got["topk_w"][r], rw)
         if np.array_equal(got["topk_idx"][r], idx):
             np.testing.assert_allclose(got["topk_w"][r], w, rtol=1e-5)
         for name, g, wnt, tol in (("dense", got["dense_out"][r], dense, BRANCH_TOL),
