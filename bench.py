@@ -55,7 +55,7 @@ GEGLU_TRAFFIC_BYTES = int(18633.0 * 1024 * 2.0 + 40.0 * 1024 * 1.0)
 C0_TRAFFIC_BYTES = int(9283.5 * 1024 * 2.0 + 64.0 * 1024)
 C1_TRAFFIC_BYTES = int(215623.7 * 1024 * 2.0 + 1088.6 * 1024)
 C2_GLOBAL_TRAFFIC_BYTES = int((4214.8 + 277.0) * 1024 * 2.0 + (530.0 + 4.0) * 1024)
-C3_TRAFFIC_BYTES = int(19183.2 * 1024 * 2.0 + 79.3 * 1024)
+C3_TRAFFIC_BYTES = int(19466.5 * 1024 * 2.0 + 75.2 * 1024)
 
 
 def _cpu_cores() -> int:

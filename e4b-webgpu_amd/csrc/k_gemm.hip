@@ -45,7 +45,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // GeGLU tile (4 token tiles x 2 x 32 rows per wave), whose accumulators and
 // operands already take 256 VGPRs.  There the uint4 struct array is what the
 // compiler moves to LDS (16 KB per workgroup), which keeps 2 waves per SIMD
-// (the native vectors in registers leave 1 wave and measured 16 % slower)
+// (the native vectors in registers leave 1 wave: the E4B prefill measured
+// 16 % slower)
 template <int T, int EPI>
 using StageVec = std::conditional_t<T == 4 && EPI == GEMM_GLU, uint4, u32x4>;
 DEV u32x4 as_vec(u32x4 v) { return v; }
