@@ -245,6 +245,13 @@ constexpr int kPfKsPle = 8;  // PLE gate (256 rows; the GELU-multiply kernel sum
 // up to 3072, experts 8..256, expert FFN up to 768, dense FFN up to 3072),
 // the general head prep / attention (head dims 256 and 512, any KV heads
 // dividing the q heads)
+// A4B prefill layers whose attention runs on the matrix cores (the E4B
+// prefill kernel: head dim 256, 1, 2 or 4 q heads per KV head, a ring)
+static bool a4b_pf_mfma_attn(const Layer& ly, int qh) {
+  const int gqa = ly.kvh > 0 && qh % ly.kvh == 0 ? qh / ly.kvh : 0;
+  return !ly.global && ly.hd == 256 && !ly.keqv && (gqa == 1 || gqa == 2 || gqa == 4);
+}
+
 static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
   auto bad = [&](const char* m) {
     snprintf(why, n, "%s", m);
@@ -570,12 +577,20 @@ int finalize_a4b(e4b_ctx* c) {
       shape.FF = FE;
       shape.FF2 = FF;
       const size_t moe_bytes = moe_prefill_scratch(shape, cap, nullptr, nullptr);
+      // split-key partials of the matrix-core attention (sliding layers of
+      // head dim 256 with 1, 2 or 4 q heads per KV head)
+      size_t apart = 0;
+      for (int l = 0; l < k.layers; ++l)
+        if (a4b_pf_mfma_attn(c->L[l], QH))
+          apart = std::max(apart, attn_prefill_part_bytes(cap, c->L[l].kvh, QH / c->L[l].kvh));
       if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
           (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_qkv, M * (size_t)c->qkv_rows)) ||
           (rc = dalloc_t(c, &c->pf_q, M * QH * hd_max)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * hd_max)) ||
           (rc = dalloc_t(c, &c->pf_y, M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
-          (rc = dalloc(c, (void**)&c->pf_moe, moe_bytes)))
+          (rc = dalloc(c, (void**)&c->pf_moe, moe_bytes)) ||
+          (apart && (rc = dalloc(c, (void**)&c->pf_apart, apart))))
         return rc;
+      c->pf_apart_bytes = apart;
       moe_prefill_scratch(shape, cap, &c->pf_mb, c->pf_moe);
       c->pf_cap = cap;
     }
@@ -663,7 +678,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
         (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * HD)) ||
         (rc = dalloc_t(c, &c->pf_gg, M * FF)) || (rc = dalloc_t(c, &c->pf_gp, M * (size_t)(PD ? PD : 1))))
       return rc;
-    c->pf_apart_bytes = attn_prefill_part_bytes(cap, KVH);
+    c->pf_apart_bytes = attn_prefill_part_bytes(cap, KVH, QH / KVH);
     if ((rc = dalloc(c, (void**)&c->pf_apart, c->pf_apart_bytes))) return rc;
   }
   if (k.flags & E4B_FLAG_KV_SCORE) {
@@ -1171,6 +1186,23 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     hr.keqv = ly.keqv;
     hr.p0 = p0;
     hr.eps = k.eps;
+    // sliding layers of head dim 256: the matrix-core attention of the E4B
+    // prefill (split keys + combine); other layers: one workgroup per
+    // (KV group, token)
+    PrefillAttnArgs pa{};
+    pa.q = c->pf_q;
+    pa.kc = ly.kc;
+    pa.vc = ly.vc;
+    pa.out = c->pf_attn;
+    pa.M = M;
+    pa.qh = QH;
+    pa.kvh = ly.kvh;
+    pa.slots = ly.slots;
+    pa.window = window;
+    pa.p0 = p0;
+    pa.part = c->pf_apart;
+    pa.part_bytes = c->pf_apart_bytes;
+    const bool mfma_attn = a4b_pf_mfma_attn(ly, QH);
     AttnRowsGen ar{};
     ar.q = c->pf_q;
     ar.kc = ly.kc;
@@ -1183,7 +1215,8 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     ar.window = window;
     ar.p0 = p0;
     if ((rc = launch_headprep_rows_gen(hr, M, st)) || (rc = tick(c, "headprep_rows")) ||
-        (rc = launch_attn_rows_gen(ar, M, st)) || (rc = tick(c, "attn_rows")) ||
+        (rc = mfma_attn ? launch_attn_prefill(pa, st) : launch_attn_rows_gen(ar, M, st)) ||
+        (rc = tick(c, "attn_rows")) ||
         (rc = gemm(q40_view(ly.o, H, (int64_t)QH * ly.hd), c->pf_attn, QH * ly.hd, c->pf_y)) ||
         (rc = tick(c, "gemm_o")) ||
         // h1 = h + rms(o) post_attn, in place

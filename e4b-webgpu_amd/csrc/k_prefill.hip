@@ -269,9 +269,11 @@ __global__ __launch_bounds__(64) void k_headprep_rows(const float* __restrict__ 
 
 // ---- causal attention of a prefill chunk on the matrix cores ----------------
 //
-// Workgroup (KV group g, tile of 16 queries, key split s); wave w = q head
-// 4g + w, so the four heads of a group share each K/V tile staged in LDS.
-// Key tiles of 32 positions walk the union of the tile's windows; per query
+// Workgroup (KV group g, tile of 16 QS queries, key split s), GQA q heads
+// per KV group and QS = 4 / GQA: wave w takes q head GQA g + w % GQA for
+// queries 16 (w / GQA) .. + 15 of the tile, so the four waves share each
+// K/V tile staged in LDS.  Key tiles of 32 positions walk the union of the
+// tile's windows; per query
 // the live keys are (qp - W, qp] (sliding) or [0, qp] (global), scale 1.0.
 // With ns > 1 splits the union is cut into runs of kspl keys (a multiple of
 // the tile), one workgroup each, which write unnormalised partials (O, max,
@@ -307,17 +309,20 @@ DEV void split8(const float (&v)[8], h8v& hi, h8v& lo) {
   }
 }
 
+template <int GQA>
 __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
+  constexpr int QS = 4 / GQA;  // 16-query sub-tiles per workgroup
   __shared__ __align__(16) uint16_t ks[kKT * kKsStride];
   __shared__ __align__(16) uint16_t vt[256 * kVtStride];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = blockIdx.x, q0 = blockIdx.y * 16;
-  const int head = 4 * g + wave;
+  const int g = blockIdx.x, t0 = blockIdx.y * 16 * QS, q0 = t0 + 16 * (wave / GQA);
+  const int head = GQA * g + wave % GQA;
   const int j = lane & 15, qq = lane >> 4;
   const int M = A.M;
   const int qi = q0 + j;                      // this lane's query (column)
   const int qp = (int)A.p0 + min(qi, M - 1);  // its position
-  const int P0 = (int)A.p0 + q0, P1 = (int)A.p0 + min(q0 + 16, M) - 1;
+  // key range of the workgroup's queries t0 .. t0 + 16 QS - 1
+  const int P0 = (int)A.p0 + t0, P1 = (int)A.p0 + min(t0 + 16 * QS, M) - 1;
   const int W = A.window;
   const int klo = W > 0 ? max(0, P0 - W + 1) : 0;
   const uint16_t* kc = A.kc + (int64_t)g * A.slots * 256;
@@ -460,11 +465,13 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
 // thread t = dims 4t .. 4t + 3.  A split in which the query has no live key
 // left max -3e38 and sum 0 and drops out (its weight underflows to 0); the
 // split that holds the query's own position is always live.
+template <int GQA>
 __global__ __launch_bounds__(64) void k_attn_prefill_combine(PrefillAttnArgs A) {
+  constexpr int QS = 4 / GQA, TQ = 16 * QS;
   const int h = blockIdx.x, qi = blockIdx.y, t = threadIdx.x;
-  const int g = h >> 2, w = h & 3, qt = qi >> 4, j = qi & 15;
-  const int nqt = (A.M + 15) >> 4;
-  const int P0 = (int)A.p0 + 16 * qt, P1 = (int)A.p0 + min(16 * qt + 16, A.M) - 1;
+  const int g = h / GQA, qt = qi / TQ, j = qi & 15, w = ((qi % TQ) >> 4) * GQA + h % GQA;
+  const int nqt = (A.M + TQ - 1) / TQ;
+  const int P0 = (int)A.p0 + TQ * qt, P1 = (int)A.p0 + min(TQ * qt + TQ, A.M) - 1;
   const int klo = A.window > 0 ? max(0, P0 - A.window + 1) : 0;
   const int nspl = (P1 - klo + A.kspl) / A.kspl;  // splits of this tile (<= ns)
   const int64_t u0 = (int64_t)(g * nqt + qt) * A.ns;
@@ -569,12 +576,15 @@ int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* q
   return E4B_OK;
 }
 
-size_t attn_prefill_part_bytes(int M, int kvh) {
-  return (size_t)kvh * (size_t)((M + 15) / 16) * kPfAttnMaxSplits * 4 * 16 * (256 + 2) * sizeof(float);
+size_t attn_prefill_part_bytes(int M, int kvh, int gqa) {
+  const int tq = 16 * (4 / (gqa == 1 || gqa == 2 ? gqa : 4));
+  return (size_t)kvh * (size_t)((M + tq - 1) / tq) * kPfAttnMaxSplits * 4 * 16 * (256 + 2) * sizeof(float);
 }
 
 int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
-  if (a.qh != 4 * a.kvh) return e4b_fail(E4B_EINVAL, "prefill attention: %d q heads for %d kv heads", a.qh, a.kvh);
+  const int gqa = a.kvh > 0 && a.qh % a.kvh == 0 ? a.qh / a.kvh : 0;
+  if (gqa != 1 && gqa != 2 && gqa != 4)
+    return e4b_fail(E4B_EINVAL, "prefill attention: %d q heads for %d kv heads (1, 2 or 4 per group)", a.qh, a.kvh);
   if (a.M < 1) return e4b_fail(E4B_EINVAL, "prefill attention: M = %d", a.M);
   if (a.window > 0) {
     // every key a query of the chunk needs must still own its ring slot
@@ -588,10 +598,11 @@ int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
   }
   // the widest key range of a query tile sets the split length: at least
   // kPfAttnMinSplit keys, at most kPfAttnMaxSplits splits
-  const int nqt = (a.M + 15) / 16;
+  const int tq = 16 * (4 / gqa);  // queries per workgroup
+  const int nqt = (a.M + tq - 1) / tq;
   int maxspan = 0;
   for (int t = 0; t < nqt; ++t) {
-    const int P0 = (int)a.p0 + 16 * t, P1 = (int)a.p0 + std::min(16 * t + 16, a.M) - 1;
+    const int P0 = (int)a.p0 + tq * t, P1 = (int)a.p0 + std::min(tq * t + tq, a.M) - 1;
     const int klo = a.window > 0 ? std::max(0, P0 - a.window + 1) : 0;
     maxspan = std::max(maxspan, P1 - klo + 1);
   }
@@ -606,8 +617,17 @@ int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
   }
   a.kspl = kspl;
   a.ns = ns;
-  hipLaunchKernelGGL(k_attn_prefill, dim3(a.kvh, nqt, ns), dim3(256), 0, st, a);
-  if (ns > 1) hipLaunchKernelGGL(k_attn_prefill_combine, dim3(a.qh, a.M), dim3(64), 0, st, a);
+  const dim3 grid(a.kvh, nqt, ns), cgrid(a.qh, a.M);
+  if (gqa == 4) {
+    hipLaunchKernelGGL(k_attn_prefill<4>, grid, dim3(256), 0, st, a);
+    if (ns > 1) hipLaunchKernelGGL(k_attn_prefill_combine<4>, cgrid, dim3(64), 0, st, a);
+  } else if (gqa == 2) {
+    hipLaunchKernelGGL(k_attn_prefill<2>, grid, dim3(256), 0, st, a);
+    if (ns > 1) hipLaunchKernelGGL(k_attn_prefill_combine<2>, cgrid, dim3(64), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(k_attn_prefill<1>, grid, dim3(256), 0, st, a);
+    if (ns > 1) hipLaunchKernelGGL(k_attn_prefill_combine<1>, cgrid, dim3(64), 0, st, a);
+  }
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

@@ -346,7 +346,7 @@ extern "C" int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc
   a.window = window;
   a.p0 = p0;
   Workspace ws;
-  int rc = e4b_workspace(attn_prefill_part_bytes(m, kv_heads), &ws, (hipStream_t)stream);
+  int rc = e4b_workspace(attn_prefill_part_bytes(m, kv_heads, q_heads / kv_heads), &ws, (hipStream_t)stream);
   if (rc) return rc;
   a.part = (float*)ws.buf;
   a.part_bytes = ws.cap;

@@ -90,12 +90,12 @@ struct PrefillAttnArgs {
   int M, qh, kvh, slots;
   int window;         // 0 = global layer
   uint32_t p0;
-  // split-key partials (attn_prefill_part_bytes(M, kvh) bytes); null: every
+  // split-key partials (attn_prefill_part_bytes(M, kvh, qh / kvh) bytes); null: every
   // query tile walks its keys in one workgroup
   float* part = nullptr;
   size_t part_bytes = 0;
   int kspl = 0, ns = 1;  // keys per split and splits per query tile (set by the launcher)
 };
 // the partial buffer a chunk of M queries needs at most
-size_t attn_prefill_part_bytes(int M, int kvh);
+size_t attn_prefill_part_bytes(int M, int kvh, int gqa);
 int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st);

@@ -262,7 +262,7 @@ int e4b_k_moe_prefill(const e4b_moe_weights* w, const float* h, int m, float* h_
  *        queries attend to (position p in slot p % slots when window > 0)
  *   out  f16[m][q_heads * 256]
  * window > 0: keys (p - window, p] of a ring with slots >= window + m - 1;
- * window == 0: keys [0, p], p0 + m <= slots.  q_heads = 4 * kv_heads. */
+ * window == 0: keys [0, p], p0 + m <= slots.  q_heads = 1, 2 or 4 x kv_heads. */
 int e4b_k_attn_prefill(const float* q, const void* kc, const void* vc, void* out, int m, int q_heads, int kv_heads,
                        int slots, int window, uint32_t p0, void* stream);
 

@@ -33,18 +33,26 @@ ATTN_TOL = 2e-3
 HD = 256
 
 
-@pytest.mark.parametrize("kvh,slots,window,p0,m,seed", [
-    (2, 4096, 0, 0, 512, 1),      # c4 prompt, global layer
-    (2, 4096, 0, 1000, 100, 2),   # a later chunk of a global layer
-    (2, 1024, 512, 0, 513, 3),    # the largest chunk a 1024-slot ring allows
-    (2, 1024, 512, 900, 200, 4),  # ring wraps inside the chunk
-    (2, 1024, 512, 3000, 37, 5),  # ragged chunk deep in the ring
-    (1, 64, 32, 100, 33, 6),      # small ring at its chunk limit, one KV group
-    (2, 1024, 512, 7, 1, 7),      # a single token
-    (2, 8320, 0, 8000, 64, 8),    # deep global chunk: 8 key splits of 1024
+@pytest.mark.parametrize("gqa,kvh,slots,window,p0,m,seed", [
+    (4, 2, 4096, 0, 0, 512, 1),      # c4 prompt, global layer
+    (4, 2, 4096, 0, 1000, 100, 2),   # a later chunk of a global layer
+    (4, 2, 1024, 512, 0, 513, 3),    # the largest chunk a 1024-slot ring allows
+    (4, 2, 1024, 512, 900, 200, 4),  # ring wraps inside the chunk
+    (4, 2, 1024, 512, 3000, 37, 5),  # ragged chunk deep in the ring
+    (4, 1, 64, 32, 100, 33, 6),      # small ring at its chunk limit, one KV group
+    (4, 2, 1024, 512, 7, 1, 7),      # a single token
+    (4, 2, 8320, 0, 8000, 64, 8),    # deep global chunk: 8 key splits of 1024
+    # two q heads per KV group (the A4B sliding layers: 16 q / 8 KV heads,
+    # window 1024, ring 1536) and one: 32- and 64-query workgroup tiles
+    (2, 8, 1536, 1024, 0, 512, 9),   # the A4B prompt
+    (2, 8, 1536, 1024, 1300, 237, 10),  # ring wraps, ragged last tile
+    (2, 3, 64, 32, 100, 33, 11),     # small ring at its chunk limit
+    (2, 2, 1024, 512, 5, 1, 12),     # a single token
+    (2, 2, 4096, 0, 2000, 90, 13),   # global layer
+    (1, 4, 1024, 512, 600, 77, 14),  # one q head per KV head
 ])
-def test_attn_prefill(kvh, slots, window, p0, m, seed):
-    qh = 4 * kvh
+def test_attn_prefill(gqa, kvh, slots, window, p0, m, seed):
+    qh = gqa * kvh
     rng = np.random.default_rng(seed)
     q = rng.standard_normal((m, qh, HD)).astype(np.float32)
     k = (0.25 * rng.standard_normal((kvh, slots, HD))).astype(np.float16)
@@ -63,7 +71,7 @@ def test_attn_prefill(kvh, slots, window, p0, m, seed):
         err = np.abs(got[i] - want).max() / np.abs(want).max()
         worst = max(worst, err)
         assert err < ATTN_TOL, f"query {i} (pos {pos}): rel err {err:.3e}"
-    print(f"attn prefill kvh={kvh} slots={slots} window={window} p0={p0} m={m}: worst rel err {worst:.2e}")
+    print(f"attn prefill gqa={gqa} kvh={kvh} slots={slots} window={window} p0={p0} m={m}: worst rel err {worst:.2e}")
 
 
 def test_attn_prefill_rejects_short_ring():
