@@ -13,8 +13,11 @@
 // (w2 null: f16(h_out)); xlo (null: none) = f16(y - f16(y)), the low half of
 // the hi/lo pair of the same value.  H <= 4096.  One workgroup per row: M
 // rows at stride H in h_in, h_out, a, x and xlo (the weights are shared).
+// na > 1 (<= 4): a is the sum of na split-K slices at stride a_slice, added in
+// slice order.
 int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
-                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st, int M = 1);
+                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st, int M = 1, int na = 1,
+                   int64_t a_slice = 0);
 
 struct AttnGen {
   const float* qkv;        // raw q [qh][hd] | k [kvh][hd] | v [kvh][hd] (no v rows when keqv)

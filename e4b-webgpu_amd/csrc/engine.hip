@@ -237,6 +237,7 @@ constexpr int kPfKsO = 4;    // o projection
 constexpr int kPfKs = 8;     // down projection (the most slices; sizes the partial buffer)
 constexpr int kPfKsQkv = 2;  // qkv (the head prep sums the slices)
 constexpr int kPfKsPle = 8;  // PLE gate (256 rows; the GELU-multiply kernel sums the slices)
+constexpr int kPfA4bOKs = 4;  // A4B o projection (the attention-residual row norm sums the slices)
 
 }  // namespace
 
@@ -586,7 +587,7 @@ int finalize_a4b(e4b_ctx* c) {
       if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
           (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_qkv, M * (size_t)c->qkv_rows)) ||
           (rc = dalloc_t(c, &c->pf_q, M * QH * hd_max)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * hd_max)) ||
-          (rc = dalloc_t(c, &c->pf_y, M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
+          (rc = dalloc_t(c, &c->pf_y, (size_t)kPfA4bOKs * M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
           (rc = dalloc(c, (void**)&c->pf_moe, moe_bytes)) ||
           (apart && (rc = dalloc(c, (void**)&c->pf_apart, apart))))
         return rc;
@@ -1145,7 +1146,7 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
   const int64_t MH = (int64_t)M * H;
   hipStream_t st = c->st;
   int rc;
-  auto gemm = [&](const Q40Mat& W, const uint16_t* X, int ldx, float* Y) {
+  auto gemm = [&](const Q40Mat& W, const uint16_t* X, int ldx, float* Y, int ks_want = 1) {
     GemmArgs g{};
     g.W = W;
     g.X = X;
@@ -1153,9 +1154,12 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     g.ldx = ldx;
     g.epi = GEMM_F32;
     g.Y = Y;
-    g.ks = 1;
+    g.ks = q40_gemm_kslices(W.nb, ks_want);
     return launch_q40_gemm(g, st);
   };
+  // the o projection's K slices (its 2816 output rows alone give too few
+  // workgroups): what q40_gemm_kslices makes of kPfA4bOKs for the layer
+  auto ok_slices = [&](const Layer& ly) { return q40_gemm_kslices(QH * ly.hd / 32, kPfA4bOKs); };
   const Q6Mat E = q6_view(c->embd, k.vocab, H);
   if ((rc = launch_embed_rows(E, c->pf_ids, M, sqrtf((float)H), c->pf_h, c->pf_xhl, st)) ||
       (rc = tick(c, "embed_rows")))
@@ -1217,11 +1221,11 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     if ((rc = launch_headprep_rows_gen(hr, M, st)) || (rc = tick(c, "headprep_rows")) ||
         (rc = mfma_attn ? launch_attn_prefill(pa, st) : launch_attn_rows_gen(ar, M, st)) ||
         (rc = tick(c, "attn_rows")) ||
-        (rc = gemm(q40_view(ly.o, H, (int64_t)QH * ly.hd), c->pf_attn, QH * ly.hd, c->pf_y)) ||
+        (rc = gemm(q40_view(ly.o, H, (int64_t)QH * ly.hd), c->pf_attn, QH * ly.hd, c->pf_y, kPfA4bOKs)) ||
         (rc = tick(c, "gemm_o")) ||
-        // h1 = h + rms(o) post_attn, in place
+        // h1 = h + rms(o) post_attn, in place (o: the sum of the K slices)
         (rc = launch_rownorm(c->pf_h, c->pf_h, c->pf_y, ly.post_attn, 1.f, nullptr, nullptr, nullptr, H, k.eps, st,
-                             M)) ||
+                             M, ok_slices(ly), MH)) ||
         (rc = tick(c, "attn_residual_rows")))
       return rc;
     MoeArgs a = c->moe;

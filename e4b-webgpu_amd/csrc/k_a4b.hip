@@ -24,12 +24,14 @@
 namespace {
 
 constexpr int kRowMax = 16;  // elements per thread of k_rownorm: H <= 16 * 256
+constexpr int kRowSlices = 4;  // split-K slices k_rownorm sums at most
 
 // thread t owns the elements i = t + 256 k
 __global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ h_in, float* __restrict__ h_out,
                                                  const float* __restrict__ a, const float* __restrict__ w1, float scale,
                                                  const float* __restrict__ w2, uint16_t* __restrict__ x,
-                                                 uint16_t* __restrict__ xlo, int H, float eps) {
+                                                 uint16_t* __restrict__ xlo, int H, float eps, int na,
+                                                 int64_t a_slice) {
   __shared__ float red[4];
   const int t = threadIdx.x;
   // row blockIdx.x of a batch (one row in the decode step)
@@ -45,6 +47,23 @@ __global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ h_in,
     const int i = t + 256 * k;
     hv[k] = i < H ? h_in[i] : 0.f;
     av[k] = (a && i < H) ? a[i] : 0.f;
+  }
+  if (a && na > 1) {
+    // slices 1 .. kRowSlices - 1 requested together (clamped to the last
+    // slice, added only below na)
+    float sv[kRowSlices - 1][kRowMax];
+#pragma unroll
+    for (int s = 1; s < kRowSlices; ++s)
+#pragma unroll
+      for (int k = 0; k < kRowMax; ++k) {
+        const int i = min(t + 256 * k, H - 1);
+        sv[s - 1][k] = a[min(s, na - 1) * a_slice + i];
+      }
+#pragma unroll
+    for (int s = 1; s < kRowSlices; ++s)
+#pragma unroll
+      for (int k = 0; k < kRowMax; ++k)
+        if (s < na && t + 256 * k < H) av[k] += sv[s - 1][k];
   }
   if (a) {
     float ss = 0.f;
@@ -585,11 +604,12 @@ __global__ __launch_bounds__(256) void k_kv_gather_gen(const uint32_t* __restric
 }  // namespace
 
 int launch_rownorm(const float* h_in, float* h_out, const float* a, const float* w1, float scale, const float* w2,
-                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st, int M) {
+                   uint16_t* x, uint16_t* xlo, int H, float eps, hipStream_t st, int M, int na, int64_t a_slice) {
   if (H <= 0 || H > 256 * kRowMax) return e4b_fail(E4B_EINVAL, "row norm: hidden %d outside 1..%d", H, 256 * kRowMax);
   if (a && !w1) return e4b_fail(E4B_EINVAL, "row norm: residual without its norm weight");
-  if (M < 1) return e4b_fail(E4B_EINVAL, "row norm: %d rows", M);
-  hipLaunchKernelGGL(k_rownorm, dim3(M), dim3(256), 0, st, h_in, h_out, a, w1, scale, w2, x, xlo, H, eps);
+  if (M < 1 || na < 1 || na > kRowSlices || (na > 1 && (!a || a_slice < (int64_t)M * H)))
+    return e4b_fail(E4B_EINVAL, "row norm: %d rows, %d slices", M, na);
+  hipLaunchKernelGGL(k_rownorm, dim3(M), dim3(256), 0, st, h_in, h_out, a, w1, scale, w2, x, xlo, H, eps, na, a_slice);
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }
