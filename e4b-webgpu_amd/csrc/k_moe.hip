@@ -163,7 +163,10 @@ __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
 // once per row (the decode layout over rows re-read the whole router matrix
 // and the row's vectors in every one of its E/2 blocks).  Rows without the
 // attention residual only (the prefill forms h1 before the router).
-constexpr int kRrT = 4, kRrE = 16;
+// 2 rows x 16 experts per workgroup: 24 KB of LDS, 6 workgroups per CU
+// (measured against 4 x 16, 4 x 8 and 2 x 8: 367.7 us for the c3 layer over
+// 512 rows against 377.9, 375.5 and 372.7)
+constexpr int kRrT = 2, kRrE = 16;
 static_assert(kRrT * kRrE / 2 <= 64, "one score per lane");
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_moe_router_rows(MoeArgs A, int M) {
   __shared__ __align__(16) float4 xr[kRrT][kRouterMaxH4];
