@@ -10,7 +10,8 @@
 //   grouped GEMMs       expert gate/up + GeGLU and expert down on the matrix
 //                       cores (k_gemm.hip grouped mode): each tile reads its
 //                       expert's rows once for up to 32 draws
-//   dense branch        GeGLU GEMM + down GEMM over all M tokens
+//   dense branch        gate|up GEMM in K slices, k_geglu_rows, down GEMM over
+//                       all M tokens
 //   k_moe_combine_rows  moe[m] = sum_k w_k down_sorted[pos(m, k)], in k order
 //   tail                the decode tail over token rows
 #include "../../include/e4b.h"
@@ -61,6 +62,22 @@ __global__ __launch_bounds__(1024) void k_moe_group(const uint32_t* __restrict__
       tiles[toff[e] + j] = make_int4(e, off[e] + j * kTileRows, min(kTileRows, cnt[e] - j * kTileRows), 0);
 }
 
+// out[m][j] = f16(gelu(gate) * up) of the dense branch, gate and up each the
+// sum of the ks split-K slices of the gate|up GEMM (rows j and FF + j), in
+// slice order; the arithmetic of the GEMM's GeGLU epilogue after that sum
+__global__ __launch_bounds__(256) void k_geglu_rows(const float* __restrict__ part, int ks, int64_t slice, int FF,
+                                                    uint16_t* __restrict__ out) {
+  const int m = blockIdx.y, j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= FF) return;
+  const float* p = part + (int64_t)m * 2 * FF + j;
+  float g = p[0], u = p[FF];
+  for (int s = 1; s < ks; ++s) {
+    g += p[s * slice];
+    u += p[s * slice + FF];
+  }
+  out[(int64_t)m * FF + j] = f2h(gelu_tanh(g) * u);
+}
+
 // moe[m][i] = sum_k w[m][k] * down[pos[m K + k]][i], in slot order
 __global__ __launch_bounds__(256) void k_moe_combine_rows(const float* __restrict__ down,
                                                           const uint32_t* __restrict__ pos,
@@ -99,6 +116,7 @@ size_t moe_prefill_scratch(const MoeArgs& a, int M, MoePrefillBufs* b, uint8_t* 
   uint8_t* p_g = take(P * FF * 2);
   uint8_t* p_d = take(P * H * 4);
   uint8_t* p_gd = take((size_t)M * FF2 * 2);
+  uint8_t* p_gdp = take((size_t)kMoePfDenseKs * M * 2 * FF2 * 4);
   uint8_t* p_dense = take((size_t)M * H * 4);
   uint8_t* p_moe = take((size_t)M * H * 4);
   if (b) {
@@ -115,6 +133,7 @@ size_t moe_prefill_scratch(const MoeArgs& a, int M, MoePrefillBufs* b, uint8_t* 
     b->g_sorted = (uint16_t*)p_g;
     b->d_sorted = (float*)p_d;
     b->g_dense = (uint16_t*)p_gd;
+    b->gd_part = (float*)p_gdp;
     b->dense_out = (float*)p_dense;
     b->moe_out = (float*)p_moe;
   }
@@ -167,24 +186,25 @@ int launch_moe_prefill(const MoeArgs& base, int M, const MoePrefillBufs& b, hipS
   g.gather = nullptr;
   g.gather_div = 1;
   if ((rc = launch_q40_gemm(g, st))) return rc;
-  // dense branch over all tokens
+  // dense branch over all tokens: gate|up in K slices, then the GeGLU rows
   GemmArgs d{};
   d.W = a.dense_gu;
   d.X = b.xd;
   d.M = M;
   d.ldx = H;
-  d.epi = GEMM_GLU;
-  d.Yh = b.g_dense;
-  d.ff = FF2;
-  d.ks = 1;
+  d.epi = GEMM_F32;
+  d.Y = b.gd_part;
+  d.ks = q40_gemm_kslices(a.dense_gu.nb, kMoePfDenseKs);
   if ((rc = launch_q40_gemm(d, st))) return rc;
+  hipLaunchKernelGGL(k_geglu_rows, dim3((FF2 + 255) / 256, M), dim3(256), 0, st, b.gd_part, d.ks,
+                     (int64_t)M * 2 * FF2, FF2, b.g_dense);
+  E4B_HIP(hipGetLastError());
   d.W = a.dense_down;
   d.X = b.g_dense;
   d.ldx = FF2;
   d.epi = GEMM_F32;
   d.Y = b.dense_out;
-  d.Yh = nullptr;
-  d.ff = 0;
+  d.ks = 1;
   if ((rc = launch_q40_gemm(d, st))) return rc;
   hipLaunchKernelGGL(k_moe_combine_rows, dim3((H + 255) / 256, M), dim3(256), 0, st, b.d_sorted, b.pos, b.topk_w, H,
                      b.moe_out);

@@ -69,9 +69,13 @@ struct MoePrefillBufs {
   uint16_t* g_sorted;  // [M*8][FF] f16 expert GeGLU outputs, sorted
   float* d_sorted;     // [M*8][H] expert down outputs, sorted
   uint16_t* g_dense;   // [M][FF2]
+  float* gd_part;      // [kMoePfDenseKs][M][2 FF2] dense gate|up split-K partials
   float* dense_out;    // [M][H]
   float* moe_out;      // [M][H]
 };
+// K slices of the dense gate|up GEMM over the prompt rows (its 2 x 2112 rows
+// give too few workgroups for one slice); k_geglu_rows sums them
+constexpr int kMoePfDenseKs = 2;
 // bytes of scratch for M tokens; with base != null also fills b from it
 size_t moe_prefill_scratch(const MoeArgs& a, int M, MoePrefillBufs* b, uint8_t* base);
 // h_out[m] (a.h_out, rows of H) for the M token rows of a.h
