@@ -10,9 +10,10 @@
 //   grouped GEMMs       expert gate/up + GeGLU and expert down on the matrix
 //                       cores (k_gemm.hip grouped mode): each tile reads its
 //                       expert's rows once for up to 32 draws
-//   dense branch        gate|up GEMM in K slices, k_geglu_rows, down GEMM over
-//                       all M tokens
-//   k_moe_combine_rows  moe[m] = sum_k w_k down_sorted[pos(m, k)], in k order
+//   dense branch        gate|up GEMM in K slices, k_geglu_rows, down GEMM in
+//                       K slices over all M tokens
+//   k_moe_combine_rows  moe[m] = sum_k w_k down_sorted[pos(m, k)], in k order,
+//                       and the dense down's K slices summed
 //   tail                the decode tail over token rows
 #include "../../include/e4b.h"
 #include "kernels.h"
@@ -79,17 +80,24 @@ __global__ __launch_bounds__(256) void k_geglu_rows(const float* __restrict__ pa
 }
 
 // moe[m][i] = sum_k w[m][k] * down[pos[m K + k]][i], in slot order
+// (and dense[m] = the sum of the dense down GEMM's dks K slices of row m, in
+// slice order)
 __global__ __launch_bounds__(256) void k_moe_combine_rows(const float* __restrict__ down,
                                                           const uint32_t* __restrict__ pos,
                                                           const float* __restrict__ topk_w, int H,
-                                                          float* __restrict__ moe) {
+                                                          float* __restrict__ moe, const float* __restrict__ dpart,
+                                                          int dks, int64_t dslice, float* __restrict__ dense) {
   const int m = blockIdx.y;
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= H) return;
+  const int64_t o = (int64_t)m * H + i;
+  float ds = dpart[o];
+  for (int s = 1; s < dks; ++s) ds += dpart[s * dslice + o];
   float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < K; ++k) acc = fmaf(topk_w[m * K + k], down[(int64_t)pos[m * K + k] * H + i], acc);
-  moe[(int64_t)m * H + i] = acc;
+  moe[o] = acc;
+  dense[o] = ds;
 }
 
 }  // namespace
@@ -116,7 +124,7 @@ size_t moe_prefill_scratch(const MoeArgs& a, int M, MoePrefillBufs* b, uint8_t* 
   uint8_t* p_g = take(P * FF * 2);
   uint8_t* p_d = take(P * H * 4);
   uint8_t* p_gd = take((size_t)M * FF2 * 2);
-  uint8_t* p_gdp = take((size_t)kMoePfDenseKs * M * 2 * FF2 * 4);
+  uint8_t* p_gdp = take((size_t)kMoePfDenseKs * M * (2 * FF2 > H ? 2 * FF2 : H) * 4);
   uint8_t* p_dense = take((size_t)M * H * 4);
   uint8_t* p_moe = take((size_t)M * H * 4);
   if (b) {
@@ -203,11 +211,11 @@ int launch_moe_prefill(const MoeArgs& base, int M, const MoePrefillBufs& b, hipS
   d.X = b.g_dense;
   d.ldx = FF2;
   d.epi = GEMM_F32;
-  d.Y = b.dense_out;
-  d.ks = 1;
+  d.Y = b.gd_part;  // the down's K slices reuse the gate|up partials' space
+  d.ks = q40_gemm_kslices(a.dense_down.nb, kMoePfDenseKs);
   if ((rc = launch_q40_gemm(d, st))) return rc;
   hipLaunchKernelGGL(k_moe_combine_rows, dim3((H + 255) / 256, M), dim3(256), 0, st, b.d_sorted, b.pos, b.topk_w, H,
-                     b.moe_out);
+                     b.moe_out, b.gd_part, d.ks, (int64_t)M * H, b.dense_out);
   E4B_HIP(hipGetLastError());
   return launch_moe_tail_rows(a, M, st);
 }

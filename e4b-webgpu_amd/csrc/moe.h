@@ -70,6 +70,7 @@ struct MoePrefillBufs {
   float* d_sorted;     // [M*8][H] expert down outputs, sorted
   uint16_t* g_dense;   // [M][FF2]
   float* gd_part;      // [kMoePfDenseKs][M][2 FF2] dense gate|up split-K partials
+                       // (then the dense down's, [kMoePfDenseKs][M][H]; sized for both)
   float* dense_out;    // [M][H]
   float* moe_out;      // [M][H]
 };
