@@ -56,6 +56,9 @@ C0_TRAFFIC_BYTES = int(9283.5 * 1024 * 2.0 + 64.0 * 1024)
 C1_TRAFFIC_BYTES = int(215623.7 * 1024 * 2.0 + 1088.6 * 1024)
 C2_GLOBAL_TRAFFIC_BYTES = int((4214.8 + 277.0) * 1024 * 2.0 + (530.0 + 4.0) * 1024)
 C3_TRAFFIC_BYTES = int(19466.5 * 1024 * 2.0 + 75.2 * 1024)
+# A4B whole decode step at positions 513-530 (profiles/decode_a4b_traffic.md):
+# FETCH_SIZE 1,270,208.5 KiB x 2.0 + WRITE_SIZE 11,299.5 KiB per token
+A4B_STEP_TRAFFIC_BYTES = int(1270208.5 * 1024 * 2.0 + 11299.5 * 1024)
 
 
 def _cpu_cores() -> int:
@@ -548,7 +551,7 @@ def bench_a4b(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dic
                                           "26B-A4B q4_0 GGUF, 2.38 GB/token",
                    "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": A4B_STEP_TRAFFIC_BYTES,
                      "kernel": "whole decode step (graph replay)"},
     }
     eng.close()
