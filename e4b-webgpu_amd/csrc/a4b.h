@@ -56,6 +56,8 @@ struct HeadRowsGen {
   bool keqv;
   uint32_t p0;             // position (= full-layer slot) of token 0
   float eps;
+  int ks = 1;              // qkv = the sum of ks split-K slices at stride slice
+  int64_t slice = 0;
 };
 // head prep of M tokens: queries out, the K/V rows of positions p0 .. p0 + M - 1 into the caches
 int launch_headprep_rows_gen(const HeadRowsGen& a, int M, hipStream_t st);

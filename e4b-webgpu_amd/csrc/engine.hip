@@ -237,7 +237,8 @@ constexpr int kPfKsO = 4;    // o projection
 constexpr int kPfKs = 8;     // down projection (the most slices; sizes the partial buffer)
 constexpr int kPfKsQkv = 2;  // qkv (the head prep sums the slices)
 constexpr int kPfKsPle = 8;  // PLE gate (256 rows; the GELU-multiply kernel sums the slices)
-constexpr int kPfA4bOKs = 4;  // A4B o projection (the attention-residual row norm sums the slices)
+constexpr int kPfA4bOKs = 4;
+constexpr int kPfA4bQkvKs = 2;  // A4B q|k|v projection (the head prep sums the slices)  // A4B o projection (the attention-residual row norm sums the slices)
 
 }  // namespace
 
@@ -585,7 +586,7 @@ int finalize_a4b(e4b_ctx* c) {
         if (a4b_pf_mfma_attn(c->L[l], QH))
           apart = std::max(apart, attn_prefill_part_bytes(cap, c->L[l].kvh, QH / c->L[l].kvh));
       if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
-          (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_qkv, M * (size_t)c->qkv_rows)) ||
+          (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_qkv, (size_t)kPfA4bQkvKs * M * c->qkv_rows)) ||
           (rc = dalloc_t(c, &c->pf_q, M * QH * hd_max)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * hd_max)) ||
           (rc = dalloc_t(c, &c->pf_y, (size_t)kPfA4bOKs * M * H)) || (rc = dalloc_t(c, &c->pf_xhl, 2 * M * H)) ||
           (rc = dalloc(c, (void**)&c->pf_moe, moe_bytes)) ||
@@ -1170,7 +1171,8 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     if ((rc = launch_rownorm(c->pf_h, nullptr, nullptr, nullptr, 1.f, ly.attn_norm, c->pf_xn, nullptr, H, k.eps, st,
                              M)) ||
         (rc = tick(c, "norm_rows")) ||
-        (rc = gemm(q40_view(ly.qkv, ly.qkv_rows, H), c->pf_xn, H, c->pf_qkv)) || (rc = tick(c, "gemm_qkv")))
+        (rc = gemm(q40_view(ly.qkv, ly.qkv_rows, H), c->pf_xn, H, c->pf_qkv, kPfA4bQkvKs)) ||
+        (rc = tick(c, "gemm_qkv")))
       return rc;
     HeadRowsGen hr{};
     hr.qkv = c->pf_qkv;
@@ -1190,6 +1192,8 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     hr.keqv = ly.keqv;
     hr.p0 = p0;
     hr.eps = k.eps;
+    hr.ks = q40_gemm_kslices(H / 32, kPfA4bQkvKs);
+    hr.slice = (int64_t)M * ly.qkv_rows;
     // sliding layers of head dim 256: the matrix-core attention of the E4B
     // prefill (split keys + combine); other layers: one workgroup per
     // (KV group, token)

@@ -408,6 +408,12 @@ __global__ __launch_bounds__(64) void k_headprep_rows_gen(HeadRowsGen A) {
     x[e] = t.x, x[e + 1] = t.y, x[e + 2] = t.z, x[e + 3] = t.w;
     w[e] = u.x, w[e + 1] = u.y, w[e + 2] = u.z, w[e + 3] = u.w;
   }
+  for (int s = 1; s < A.ks; ++s)  // the GEMM's K slices, in slice order
+#pragma unroll
+    for (int e = 0; e < PER; e += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(xr + s * A.slice + e);
+      x[e] += t.x, x[e + 1] += t.y, x[e + 2] += t.z, x[e + 3] += t.w;
+    }
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < PER; ++e) ss = fmaf(x[e], x[e], ss);
