@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c3|c3p|c2|c1|c0|prefill|long|a4b] [--no-cpu]
 
-Prints ONE JSON line (rank 0).  Workloads:
+Prints ONE JSON line (rank 0).  Workloads (the benchmark configs):
   c0  one q4_0 GEMV 16384x2048 (x f32), weights rotated over >512 MB so the
       256 MB MALL cannot serve them; a step = one GEMV.
   c1  Q6_K lm-head 262144x2048 + softcap + argmax; a step = one launch.

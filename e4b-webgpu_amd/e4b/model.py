@@ -1,6 +1,6 @@
 """Model descriptions and seeded random-init tensors.
 
-The BASELINE "E4B-shaped q4_0" model combines Gemma-3n-E4B shapes (35 layers,
+The benchmark's "E4B-shaped q4_0" model combines Gemma-3n-E4B shapes (35 layers,
 hidden 2048, GeGLU FFN 16384, 4 sliding : 1 global, per-layer embeddings of
 256) with the A4B engine's formats (q4_0 linears, Q6_K tied embedding /
 lm-head, f16 KV ring).  recipe = 1 describes the model the reference's live
@@ -147,7 +147,7 @@ class Tensor:
 
 
 def synth_tensors(cfg: E4BConfig, seed: int = 0, lin_sigma: float = 0.02, emb_sigma: float = 1e-3):
-    """Random-init tensors of the E4B-shaped model (BASELINE config c4):
+    """Random-init tensors of the E4B-shaped model (benchmark config c4):
     q4_0 linears with d = f16(|N(0, lin_sigma)|/8), Q6_K embedding / PLE table
     with d = f16(|N(0, emb_sigma)|), norm weights 1, layer scalars 1."""
     H, F, PD, L, V = cfg.hidden, cfg.ffn, cfg.ple_dim, cfg.layers, cfg.vocab
@@ -204,7 +204,7 @@ def synth_tensors(cfg: E4BConfig, seed: int = 0, lin_sigma: float = 0.02, emb_si
 
 def _synth_a4b_layers(cfg, out, sub, q40, ones, lin_sigma):
     """Layers of the A4B recipe: per-layer q|k(|v) widths, the dense branch,
-    the router (f32 [E][H] ~ N(0, 0.02), as BASELINE config c3), its input
+    the router (f32 [E][H] ~ N(0, 0.02), as benchmark config c3), its input
     scale and the per-expert output scales (1), the expert tensors (3-d, one
     [2 FE][H] gate|up and one [H][FE] down matrix per expert) and the
     branch norms."""

@@ -86,7 +86,7 @@ int   e4b_split_f32(const float* x, int64_t n, void* hl_out, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic data (portable counter-based splitmix64; identical bytes
- * from any caller).  Distributions follow BASELINE configs: q4_0 d =
+ * from any caller).  Distributions follow benchmark configs: q4_0 d =
  * f16(|N(0,sigma)|/8), nibbles U{0..15}; Q6_K d = f16(|N(0,sigma)|), scales
  * U{-32..31}, quants U{0..63}.
  * ------------------------------------------------------------------------- */
@@ -316,8 +316,8 @@ typedef struct e4b_config {
 } e4b_config;
 
 /* the layer recipe of e4b_config.recipe */
-#define E4B_RECIPE_E4B 0  /* dense GeGLU FFN + per-layer embeddings (BASELINE config c4) */
-#define E4B_RECIPE_A4B 1  /* MoE FFN half (BASELINE config c3's layer), src/engine-a4b.js:424-463 */
+#define E4B_RECIPE_E4B 0  /* dense GeGLU FFN + per-layer embeddings (benchmark config c4) */
+#define E4B_RECIPE_A4B 1  /* MoE FFN half (benchmark config c3's layer), src/engine-a4b.js:424-463 */
 
 /* launch the step's kernels directly each token instead of replaying the
  * captured hipGraph (same kernels; for profilers that do not follow graphs) */

@@ -194,7 +194,7 @@ def test_c4_width_five_layers():
 
 @pytest.mark.slow
 def test_c4_full_model_lockstep():
-    cfg = E4BConfig(max_seq=1024)  # BASELINE config c4 shapes (35 layers)
+    cfg = E4BConfig(max_seq=1024)  # benchmark config c4 shapes (35 layers)
     eng, om = build(cfg, 0)
     prompt = np.random.default_rng(2).integers(0, cfg.vocab, 8)
     toks, ties, o_lg = lockstep(eng, om, prompt, 16)
@@ -222,7 +222,7 @@ def test_c4_greedy_256_steps():
 @pytest.mark.slow
 @pytest.mark.timeout(900)
 def test_c4_stated_workload_teacher_forced(capsys):
-    # BASELINE config c4 at its stated workload: the 35-layer E4B shape, a
+    # benchmark config c4 at its stated workload: the 35-layer E4B shape, a
     # 512-token prompt through the batched prefill (e4b_prefill), then 256
     # decode steps fed with seeded random tokens (teacher forcing), so every
     # step's argmax is a decision on a different input and positions 512-767

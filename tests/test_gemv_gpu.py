@@ -38,7 +38,7 @@ def test_fdot2_subnormal_pairs_exact():
 
 @pytest.mark.parametrize("seed", [0, 1])
 def test_q40_gemv_c0_f32(seed):
-    rows, cols = 16384, 2048  # BASELINE config c0
+    rows, cols = 16384, 2048  # benchmark config c0
     w = formats.synth_q40(seed, rows, cols, 0.02)
     x = formats.synth_normal(1000 + seed, cols)
     y = Q40Matrix(w, rows, cols).gemv(x)
@@ -104,7 +104,7 @@ def _check_lmhead(rows, cols, seed, softcap):
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_q6k_lmhead_argmax_c1(seed):
-    _check_lmhead(262144, 2048, seed, 30.0)  # BASELINE config c1
+    _check_lmhead(262144, 2048, seed, 30.0)  # benchmark config c1
 
 
 @pytest.mark.parametrize("rows,cols", [(1000, 256), (4099, 2816 // 256 * 256), (77, 4096)])
