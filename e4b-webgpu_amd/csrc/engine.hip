@@ -247,11 +247,11 @@ constexpr int kPfA4bQkvKs = 2;  // A4B q|k|v projection (the head prep sums the 
 // up to 3072, experts 8..256, expert FFN up to 768, dense FFN up to 3072),
 // the general head prep / attention (head dims 256 and 512, any KV heads
 // dividing the q heads)
-// A4B prefill layers whose attention runs on the matrix cores (the E4B
-// prefill kernel: head dim 256, 1, 2 or 4 q heads per KV head, a ring)
+// A4B prefill layers whose attention runs on the matrix cores (the prefill
+// kernel: head dim 256 with 1, 2 or 4 q heads per KV head, or 512 with 8)
 static bool a4b_pf_mfma_attn(const Layer& ly, int qh) {
   const int gqa = ly.kvh > 0 && qh % ly.kvh == 0 ? qh / ly.kvh : 0;
-  return !ly.global && ly.hd == 256 && !ly.keqv && (gqa == 1 || gqa == 2 || gqa == 4);
+  return (ly.hd == 256 && (gqa == 1 || gqa == 2 || gqa == 4)) || (ly.hd == 512 && gqa == 8);
 }
 
 static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
@@ -584,7 +584,7 @@ int finalize_a4b(e4b_ctx* c) {
       size_t apart = 0;
       for (int l = 0; l < k.layers; ++l)
         if (a4b_pf_mfma_attn(c->L[l], QH))
-          apart = std::max(apart, attn_prefill_part_bytes(cap, c->L[l].kvh, QH / c->L[l].kvh));
+          apart = std::max(apart, attn_prefill_part_bytes(cap, c->L[l].kvh, QH / c->L[l].kvh, c->L[l].hd));
       if ((rc = dalloc_t(c, &c->pf_ids, M)) || (rc = dalloc_t(c, &c->pf_h, M * H)) ||
           (rc = dalloc_t(c, &c->pf_xn, M * H)) || (rc = dalloc_t(c, &c->pf_qkv, (size_t)kPfA4bQkvKs * M * c->qkv_rows)) ||
           (rc = dalloc_t(c, &c->pf_q, M * QH * hd_max)) || (rc = dalloc_t(c, &c->pf_attn, M * QH * hd_max)) ||
@@ -1194,9 +1194,8 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     hr.eps = k.eps;
     hr.ks = q40_gemm_kslices(H / 32, kPfA4bQkvKs);
     hr.slice = (int64_t)M * ly.qkv_rows;
-    // sliding layers of head dim 256: the matrix-core attention of the E4B
-    // prefill (split keys + combine); other layers: one workgroup per
-    // (KV group, token)
+    // the matrix-core attention of the prefill (split keys + combine); other
+    // head shapes: one workgroup per (KV group, token)
     PrefillAttnArgs pa{};
     pa.q = c->pf_q;
     pa.kc = ly.kc;
@@ -1206,6 +1205,7 @@ int prefill_chunk_a4b(e4b_ctx* c, uint32_t p0, int M) {
     pa.qh = QH;
     pa.kvh = ly.kvh;
     pa.slots = ly.slots;
+    pa.hd = ly.hd;
     pa.window = window;
     pa.p0 = p0;
     pa.part = c->pf_apart;

@@ -295,7 +295,7 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 32;            // keys per tile
-constexpr int kKsStride = 256 + 8; // halfs per K row in LDS
+// halfs per K row in LDS: the head dim + 8
 constexpr int kVtStride = kKT + 8; // halfs per transposed V row in LDS
 constexpr int kPfAttnMaxSplits = 8;  // key splits per query tile
 constexpr int kPfAttnMinSplit = 128; // keys per split at least (a multiple of kKT)
@@ -309,14 +309,25 @@ DEV void split8(const float (&v)[8], h8v& hi, h8v& lo) {
   }
 }
 
-template <int GQA>
+// Head dim 512 (GQA 8, the A4B full layers): blockIdx.x also picks one of
+// the two sets of 4 heads and one of the two 256-dim halves of V, so a
+// workgroup holds 4 heads' O for 256 dims; both V halves compute the scores.
+template <int GQA, int HD = 256>
 __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
-  constexpr int QS = 4 / GQA;  // 16-query sub-tiles per workgroup
-  __shared__ __align__(16) uint16_t ks[kKT * kKsStride];
+  static_assert((HD == 256 && GQA <= 4) || (HD == 512 && GQA == 8), "head dim 256 (GQA <= 4) or 512 (GQA 8)");
+  constexpr int QS = GQA >= 4 ? 1 : 4 / GQA;  // 16-query sub-tiles per workgroup
+  constexpr int NVH = HD / 256;               // 256-dim V halves
+  constexpr int NHS = GQA > 4 ? GQA / 4 : 1;  // sets of 4 heads
+  constexpr int WG = GQA > 4 ? GQA : 4;       // partial units per (group, tile, split)
+  constexpr int KST = HD + 8;                 // halfs per K row in LDS
+  __shared__ __align__(16) uint16_t ks[kKT * KST];
   __shared__ __align__(16) uint16_t vt[256 * kVtStride];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = blockIdx.x, t0 = blockIdx.y * 16 * QS, q0 = t0 + 16 * (wave / GQA);
-  const int head = GQA * g + wave % GQA;
+  const int g = blockIdx.x / (NHS * NVH), hs = (blockIdx.x / NVH) % NHS, vh = blockIdx.x % NVH;
+  const int t0 = blockIdx.y * 16 * QS, q0 = t0 + 16 * (GQA >= 4 ? 0 : wave / GQA);
+  const int hg = GQA >= 4 ? 4 * hs + wave : wave % GQA;  // head within the group
+  const int wid = GQA >= 4 ? hg : wave;                  // partial unit of this wave
+  const int head = GQA * g + hg;
   const int j = lane & 15, qq = lane >> 4;
   const int M = A.M;
   const int qi = q0 + j;                      // this lane's query (column)
@@ -325,19 +336,20 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
   const int P0 = (int)A.p0 + t0, P1 = (int)A.p0 + min(t0 + 16 * QS, M) - 1;
   const int W = A.window;
   const int klo = W > 0 ? max(0, P0 - W + 1) : 0;
-  const uint16_t* kc = A.kc + (int64_t)g * A.slots * 256;
-  const uint16_t* vc = A.vc + (int64_t)g * A.slots * 256;
+  const uint16_t* kc = A.kc + (int64_t)g * A.slots * HD;
+  const uint16_t* vc = A.vc + (int64_t)g * A.slots * HD + 256 * vh;
   const int NS = gridDim.z, sp = blockIdx.z;
   const int kstart = NS > 1 ? klo + sp * A.kspl : klo;
   if (kstart > P1) return;  // this tile needs fewer splits (uniform per workgroup)
   const int kend = NS > 1 ? min(P1, kstart + A.kspl - 1) : P1;
 
   // Q^T as the B operand: step s covers dims 32 s + 8 qq .. + 8
-  h8v qh_[8], ql_[8];
+  constexpr int QST = HD / 32;  // score steps
+  h8v qh_[QST], ql_[QST];
   {
-    const float* qrow = A.q + ((int64_t)min(qi, M - 1) * A.qh + head) * 256;
+    const float* qrow = A.q + ((int64_t)min(qi, M - 1) * A.qh + head) * HD;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int s = 0; s < QST; ++s) {
       const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * s + 8 * qq);
       const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * s + 8 * qq + 4);
       const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -354,21 +366,21 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
     lds_sync();
     {
       const int t = threadIdx.x;
-      // K: 8 threads per row, 64 bytes each
+      // K: 8 threads per row, HD / 8 halfs each
       const int kr = t >> 3, part = t & 7;
       const int kp = min(kb + kr, P1);
       const int64_t sk = W > 0 ? (int64_t)(kp % A.slots) : (int64_t)kp;
-      const uint4* srck = reinterpret_cast<const uint4*>(kc + sk * 256 + 32 * part);
-      uint4* dstk = reinterpret_cast<uint4*>(ks + kr * kKsStride + 32 * part);
+      const uint4* srck = reinterpret_cast<const uint4*>(kc + sk * HD + (HD / 8) * part);
+      uint4* dstk = reinterpret_cast<uint4*>(ks + kr * KST + (HD / 8) * part);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dstk[i] = srck[i];
+      for (int i = 0; i < HD / 64; ++i) dstk[i] = srck[i];
       // V: thread (key pair kp2, dim chunk dc) transposes 2 keys x 16 dims
       const int kp2 = t >> 4, dc = t & 15;
       const int pa = min(kb + 2 * kp2, P1), pb = min(kb + 2 * kp2 + 1, P1);
       const int64_t sa = W > 0 ? (int64_t)(pa % A.slots) : (int64_t)pa;
       const int64_t sb = W > 0 ? (int64_t)(pb % A.slots) : (int64_t)pb;
-      const uint4* va = reinterpret_cast<const uint4*>(vc + sa * 256 + 16 * dc);
-      const uint4* vb = reinterpret_cast<const uint4*>(vc + sb * 256 + 16 * dc);
+      const uint4* va = reinterpret_cast<const uint4*>(vc + sa * HD + 16 * dc);
+      const uint4* vb = reinterpret_cast<const uint4*>(vc + sb * HD + 16 * dc);
       const uint4 a0 = va[0], a1 = va[1], b0 = vb[0], b1 = vb[1];
       const uint32_t aw[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
       const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
@@ -386,9 +398,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       f4v d = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = ks + (16 * kt + j) * kKsStride + 8 * qq;
+      const uint16_t* krow = ks + (16 * kt + j) * KST + 8 * qq;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < QST; ++s) {
         const h8v ka = __builtin_bit_cast(h8v, *reinterpret_cast<const uint4*>(krow + 32 * s));
         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh_[s], d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql_[s], d, 0, 0, 0);
@@ -439,20 +451,21 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
   }
   if (qi >= M) return;
   if (NS > 1) {
-    // partials of unit (g, tile, split), head w, query j: O [256] and (max, sum)
-    const int64_t u = ((int64_t)(g * gridDim.y + blockIdx.y) * NS + sp) * 4 + wave;
-    float* po = A.part + (u * 16 + j) * 256 + 4 * qq;
+    // partials of unit (g, tile, split), wave unit wid, query j: O [HD] (this
+    // workgroup's 256 V dims) and (max, sum)
+    const int64_t u = ((int64_t)(g * gridDim.y + blockIdx.y) * NS + sp) * WG + wid;
+    float* po = A.part + (u * 16 + j) * HD + 256 * vh + 4 * qq;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt)
       *reinterpret_cast<float4*>(po + 16 * dt) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
-    if (qq == 0) {
-      float* ml = A.part + (int64_t)gridDim.x * gridDim.y * NS * 4 * 16 * 256;
+    if (qq == 0 && vh == 0) {
+      float* ml = A.part + (int64_t)(gridDim.x / (NHS * NVH)) * gridDim.y * NS * WG * 16 * HD;
       *reinterpret_cast<float2*>(ml + (u * 16 + j) * 2) = make_float2(mrun, lrun);
     }
     return;
   }
   const float inv = 1.f / lrun;
-  uint16_t* dst = A.out + ((int64_t)qi * A.qh + head) * 256 + 4 * qq;
+  uint16_t* dst = A.out + ((int64_t)qi * A.qh + head) * HD + 256 * vh + 4 * qq;
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt) {
     const uint32_t lo2 = (uint32_t)f2h(o[dt][0] * inv) | ((uint32_t)f2h(o[dt][1] * inv) << 16);
@@ -465,26 +478,28 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs A) {
 // thread t = dims 4t .. 4t + 3.  A split in which the query has no live key
 // left max -3e38 and sum 0 and drops out (its weight underflows to 0); the
 // split that holds the query's own position is always live.
-template <int GQA>
-__global__ __launch_bounds__(64) void k_attn_prefill_combine(PrefillAttnArgs A) {
-  constexpr int QS = 4 / GQA, TQ = 16 * QS;
+// (HD / 4 threads: thread t = dims 4t .. 4t + 3)
+template <int GQA, int HD = 256>
+__global__ __launch_bounds__(128) void k_attn_prefill_combine(PrefillAttnArgs A) {
+  constexpr int QS = GQA >= 4 ? 1 : 4 / GQA, TQ = 16 * QS, WG = GQA > 4 ? GQA : 4;
   const int h = blockIdx.x, qi = blockIdx.y, t = threadIdx.x;
-  const int g = h / GQA, qt = qi / TQ, j = qi & 15, w = ((qi % TQ) >> 4) * GQA + h % GQA;
+  const int g = h / GQA, qt = qi / TQ, j = qi & 15;
+  const int w = GQA >= 4 ? h % GQA : ((qi % TQ) >> 4) * GQA + h % GQA;
   const int nqt = (A.M + TQ - 1) / TQ;
   const int P0 = (int)A.p0 + TQ * qt, P1 = (int)A.p0 + min(TQ * qt + TQ, A.M) - 1;
   const int klo = A.window > 0 ? max(0, P0 - A.window + 1) : 0;
   const int nspl = (P1 - klo + A.kspl) / A.kspl;  // splits of this tile (<= ns)
   const int64_t u0 = (int64_t)(g * nqt + qt) * A.ns;
-  const float* ml = A.part + (int64_t)A.kvh * nqt * A.ns * 4 * 16 * 256;
+  const float* ml = A.part + (int64_t)A.kvh * nqt * A.ns * WG * 16 * HD;
   float m[kPfAttnMaxSplits], l[kPfAttnMaxSplits];
   float4 ov[kPfAttnMaxSplits];
 #pragma unroll
   for (int s = 0; s < kPfAttnMaxSplits; ++s) {
-    const int64_t u = ((u0 + min(s, nspl - 1)) * 4 + w) * 16 + j;
+    const int64_t u = ((u0 + min(s, nspl - 1)) * WG + w) * 16 + j;
     const float2 v = *reinterpret_cast<const float2*>(ml + u * 2);
     m[s] = v.x;
     l[s] = v.y;
-    ov[s] = *reinterpret_cast<const float4*>(A.part + u * 256 + 4 * t);
+    ov[s] = *reinterpret_cast<const float4*>(A.part + u * HD + 4 * t);
   }
   float M = m[0];
 #pragma unroll
@@ -503,7 +518,7 @@ __global__ __launch_bounds__(64) void k_attn_prefill_combine(PrefillAttnArgs A) 
     }
   }
   const float inv = 1.f / den;
-  uint16_t* dst = A.out + ((int64_t)qi * A.qh + h) * 256 + 4 * t;
+  uint16_t* dst = A.out + ((int64_t)qi * A.qh + h) * HD + 4 * t;
   *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)f2h(a0 * inv) | ((uint32_t)f2h(a1 * inv) << 16),
                                              (uint32_t)f2h(a2 * inv) | ((uint32_t)f2h(a3 * inv) << 16));
 }
@@ -576,15 +591,17 @@ int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* q
   return E4B_OK;
 }
 
-size_t attn_prefill_part_bytes(int M, int kvh, int gqa) {
-  const int tq = 16 * (4 / (gqa == 1 || gqa == 2 ? gqa : 4));
-  return (size_t)kvh * (size_t)((M + tq - 1) / tq) * kPfAttnMaxSplits * 4 * 16 * (256 + 2) * sizeof(float);
+size_t attn_prefill_part_bytes(int M, int kvh, int gqa, int hd) {
+  const int tq = 16 * (gqa == 1 || gqa == 2 ? 4 / gqa : 1), units = gqa > 4 ? gqa : 4;
+  return (size_t)kvh * (size_t)((M + tq - 1) / tq) * kPfAttnMaxSplits * units * 16 * (hd + 2) * sizeof(float);
 }
 
 int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
   const int gqa = a.kvh > 0 && a.qh % a.kvh == 0 ? a.qh / a.kvh : 0;
-  if (gqa != 1 && gqa != 2 && gqa != 4)
-    return e4b_fail(E4B_EINVAL, "prefill attention: %d q heads for %d kv heads (1, 2 or 4 per group)", a.qh, a.kvh);
+  if (!(a.hd == 256 && (gqa == 1 || gqa == 2 || gqa == 4)) && !(a.hd == 512 && gqa == 8))
+    return e4b_fail(E4B_EINVAL,
+                    "prefill attention: head dim %d with %d q heads for %d kv heads (256: 1, 2 or 4 per group; "
+                    "512: 8)", a.hd, a.qh, a.kvh);
   if (a.M < 1) return e4b_fail(E4B_EINVAL, "prefill attention: M = %d", a.M);
   if (a.window > 0) {
     // every key a query of the chunk needs must still own its ring slot
@@ -598,7 +615,7 @@ int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
   }
   // the widest key range of a query tile sets the split length: at least
   // kPfAttnMinSplit keys, at most kPfAttnMaxSplits splits
-  const int tq = 16 * (4 / gqa);  // queries per workgroup
+  const int tq = 16 * (gqa < 4 ? 4 / gqa : 1);  // queries per workgroup
   const int nqt = (a.M + tq - 1) / tq;
   int maxspan = 0;
   for (int t = 0; t < nqt; ++t) {
@@ -611,14 +628,18 @@ int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st) {
   int ns = (maxspan + kspl - 1) / kspl;
   if (!a.part) ns = 1;
   if (ns > 1) {
-    const size_t need = (size_t)a.kvh * nqt * ns * 4 * 16 * (256 + 2) * sizeof(float);
+    const size_t need = (size_t)a.kvh * nqt * ns * (gqa > 4 ? gqa : 4) * 16 * (a.hd + 2) * sizeof(float);
     if (a.part_bytes < need)
       return e4b_fail(E4B_EINVAL, "prefill attention: %zu partial bytes, %zu needed", a.part_bytes, need);
   }
   a.kspl = kspl;
   a.ns = ns;
   const dim3 grid(a.kvh, nqt, ns), cgrid(a.qh, a.M);
-  if (gqa == 4) {
+  if (a.hd == 512) {
+    // two sets of 4 heads x two 256-dim V halves per KV group
+    hipLaunchKernelGGL((k_attn_prefill<8, 512>), dim3(4 * a.kvh, nqt, ns), dim3(256), 0, st, a);
+    if (ns > 1) hipLaunchKernelGGL((k_attn_prefill_combine<8, 512>), cgrid, dim3(128), 0, st, a);
+  } else if (gqa == 4) {
     hipLaunchKernelGGL(k_attn_prefill<4>, grid, dim3(256), 0, st, a);
     if (ns > 1) hipLaunchKernelGGL(k_attn_prefill_combine<4>, cgrid, dim3(64), 0, st, a);
   } else if (gqa == 2) {

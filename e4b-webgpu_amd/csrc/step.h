@@ -83,19 +83,20 @@ int launch_headprep_rows(const float* qkv, int ks, int64_t slice, const float* q
                          const float* inv_freq, int angles, uint16_t* kc, uint16_t* vc, int slots, bool ring,
                          uint32_t p0, int M, float* q, int qh, int kvh, float eps, hipStream_t st);
 struct PrefillAttnArgs {
-  const float* q;     // [M][qh][256] prepped queries of positions p0 .. p0 + M - 1
-  const uint16_t* kc; // [kvh][slots][256]
+  const float* q;     // [M][qh][hd] prepped queries of positions p0 .. p0 + M - 1
+  const uint16_t* kc; // [kvh][slots][hd]
   const uint16_t* vc;
-  uint16_t* out;      // [M][qh * 256] f16
+  uint16_t* out;      // [M][qh * hd] f16
   int M, qh, kvh, slots;
+  int hd = 256;       // 256 (1, 2 or 4 q heads per KV head) or 512 (8)
   int window;         // 0 = global layer
   uint32_t p0;
-  // split-key partials (attn_prefill_part_bytes(M, kvh, qh / kvh) bytes); null: every
+  // split-key partials (attn_prefill_part_bytes(M, kvh, qh / kvh, hd) bytes); null: every
   // query tile walks its keys in one workgroup
   float* part = nullptr;
   size_t part_bytes = 0;
   int kspl = 0, ns = 1;  // keys per split and splits per query tile (set by the launcher)
 };
 // the partial buffer a chunk of M queries needs at most
-size_t attn_prefill_part_bytes(int M, int kvh, int gqa);
+size_t attn_prefill_part_bytes(int M, int kvh, int gqa, int hd = 256);
 int launch_attn_prefill(PrefillAttnArgs a, hipStream_t st);
