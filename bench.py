@@ -569,14 +569,14 @@ def bench_a4b(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dic
     return out
 
 
-def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False, persistent: bool = False) -> dict:
+def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False) -> dict:
     from e4b import formats
-    from e4b._lib import FLAG_NO_GRAPH, FLAG_PERSISTENT
+    from e4b._lib import FLAG_NO_GRAPH
     from e4b.engine import Engine
     from e4b.model import E4BConfig, synth_tensors
 
     prompt_len = 512
-    flags = (FLAG_NO_GRAPH if no_graph else 0) | (FLAG_PERSISTENT if persistent else 0)
+    flags = FLAG_NO_GRAPH if no_graph else 0
     cfg = E4BConfig(max_seq=max(1024, prompt_len + warmup + steps + 8), flags=flags)
     t0 = time.perf_counter()
     tensors = synth_tensors(cfg, seed=0)
@@ -605,7 +605,7 @@ def bench_c4(steps: int, warmup: int, cpu: bool, no_graph: bool = False, persist
                    "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
                    "prefill_tokens_per_s": round(prompt_len / t_prefill, 1),
                    "prefill_ms": round(t_prefill * 1e3, 3),
-                   "layer_loop": "one persistent kernel" if persistent else "six kernels a layer",
+                   "layer_loop": "six kernels a layer",
                    "prefill_tflops": round((fl["gemm"] + fl["attn"]) / t_prefill / 1e12, 2),
                    "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)}},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -639,8 +639,6 @@ def main() -> int:
                     help="c4: time only the dominant kernel (for counter runs; prints its own line, not the bench line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one 256 MiB device-to-device copy (the byte scale for rocprof FETCH/WRITE_SIZE)")
-    ap.add_argument("--persistent", action="store_true",
-                    help="c4: run the layer loop as one persistent cooperative kernel (E4B_FLAG_PERSISTENT)")
     ap.add_argument("--no-graph", action="store_true",
                     help="c4, a4b: launch the step kernels directly instead of replaying the hipGraph (for profilers)")
     a = ap.parse_args()
@@ -660,7 +658,7 @@ def main() -> int:
                           "algorithmic_bytes_per_launch": dom["algo"], "gbs": round(dom["gbs"], 1)}))
         res = None
     elif a.workload == "c4":
-        res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph, a.persistent)
+        res = bench_c4(steps, warmup, not a.no_cpu, a.no_graph)
     elif a.workload == "a4b":
         res = bench_a4b(steps, warmup, not a.no_cpu, a.no_graph)
     else:

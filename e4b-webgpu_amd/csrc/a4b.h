@@ -37,6 +37,7 @@ struct AttnGen {
   float eps;
 };
 constexpr int kAttnGenChunk = 64;  // positions per split-K chunk
+constexpr int kAttnGenMaxChunks = 256;  // chunks per head the merge holds (max_seq <= 16384)
 // head prep with the K/V row write, split-K partials over the live chunks,
 // then their log-sum-exp merge (two launches); head dim 256 or 512, 1, 2, 4
 // or 8 q heads per KV head

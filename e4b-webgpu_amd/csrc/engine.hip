@@ -16,9 +16,20 @@
 
 #include "../../include/e4b.h"
 #include "a4b.h"
+
+// decode attention split of the E4B recipe (compile-time, for A/B builds):
+// sliding layers' chunk and V slices, full layers' V slices
+#ifndef E4B_TUNE_CHUNK_SW
+#define E4B_TUNE_CHUNK_SW 32
+#endif
+#ifndef E4B_TUNE_VS_SW
+#define E4B_TUNE_VS_SW 4
+#endif
+#ifndef E4B_TUNE_VS_GL
+#define E4B_TUNE_VS_GL 4
+#endif
 #include "kernels.h"
 #include "moe.h"
-#include "persist.h"
 #include "step.h"
 #include "util.h"
 
@@ -105,6 +116,12 @@ struct e4b_ctx {
   uint32_t* keep = nullptr;                 // [max_seq] compaction keep list
   uint16_t *kv_sk = nullptr, *kv_sv = nullptr;  // [KVH][max_seq][HD] gather scratch
   int nch = 0, chunk = 64, ring_cap = 0, max_prompt = 0, amax_parts = 0;
+  // E4B recipe decode attention: split-K chunk and V slices of the sliding
+  // and of the full layers (chunk = the full layers' chunk)
+  int chunk_sw = 32, vs_sw = E4B_TUNE_VS_SW, vs_gl = E4B_TUNE_VS_GL;
+  // E4B_FLAG_LAYER_HIDDEN: the residual stream after each layer of the last
+  // decode step ([layers][hidden]; the last layer's is h_final)
+  float* lh = nullptr;
   int64_t qkv_rows = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -121,16 +138,6 @@ struct e4b_ctx {
   // per-dispatch profiling (e4b_profile_step / e4b_profile_prefill): while
   // prof_on, every launch of a directly launched step or prefill chunk is
   // followed by an event on the context stream, labelled by the kernel role
-  // persistent layer loop (E4B_FLAG_PERSISTENT): the per-layer descriptors
-  // on the device, two sets of tagged hand-off words, the abort word
-  bool persist = false;
-  int pblocks = 0;
-  PersistLayer* d_layers = nullptr;
-  unsigned long long* ll = nullptr;
-  size_t ll_words = 0;
-  int* pabort = nullptr;
-  PersistArgs pargs{};
-  unsigned long long* ptrace = nullptr;  // phase trace of e4b_profile_step (allocated on first use)
   // A4B recipe: the MoE half's scratch; the batched prefill's MoE scratch
   MoeArgs moe{};
   MoePrefillBufs pf_mb{};
@@ -271,6 +278,8 @@ static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
     if (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) return bad("q heads per KV head must be 1, 2, 4 or 8");
   }
   if (k.ple_dim != 0) return bad("ple_dim must be 0 (no per-layer embeddings)");
+  if (k.max_seq > kAttnGenMaxChunks * kAttnGenChunk)
+    return bad("max_seq beyond 16384: the full layers' attention merge holds 256 chunks of 64 positions");
   if (k.ffn <= 0 || k.ffn % 32 || k.ffn > 3072) return bad("ffn (the dense branch) must be a multiple of 32 up to 3072");
   if (k.n_experts < 8 || k.n_experts > 256) return bad("n_experts must be 8..256");
   if (k.expert_ffn <= 0 || k.expert_ffn % 32 || k.expert_ffn > 768)
@@ -278,7 +287,6 @@ static bool a4b_config_ok(const e4b_config& k, char* why, size_t n) {
   const int af = k.rope_angles_full ? k.rope_angles_full : k.rope_angles;
   if (k.rope_angles < 0 || k.rope_angles > k.head_dim / 2 || af < 0 || af > hdf / 2)
     return bad("rotated pairs beyond half the head dim");
-  if (k.flags & E4B_FLAG_PERSISTENT) return bad("E4B_FLAG_PERSISTENT is an E4B-recipe feature");
   return true;
 }
 
@@ -290,6 +298,10 @@ extern "C" e4b_ctx* e4b_create(const e4b_config* cfg) {
   const e4b_config& k = *cfg;
   if (k.recipe != E4B_RECIPE_E4B && k.recipe != E4B_RECIPE_A4B) {
     e4b_fail(E4B_EINVAL, "e4b_create: unknown recipe %d", k.recipe);
+    return nullptr;
+  }
+  if (k.flags & ~E4B_FLAGS_KNOWN) {
+    e4b_fail(E4B_EINVAL, "e4b_create: unknown flags 0x%x", k.flags & ~E4B_FLAGS_KNOWN);
     return nullptr;
   }
   if (k.layers <= 0 || k.vocab <= 0 || k.window <= 0 || k.ring < k.window || k.max_seq <= 0 || k.max_prompt < 0 ||
@@ -540,7 +552,9 @@ int finalize_a4b(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) ||
       (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)) || (rc = dalloc_t(c, &m.scores, (size_t)E)) ||
       (rc = dalloc_t(c, &m.xd, (size_t)H)) || (rc = dalloc_t(c, &m.xm, (size_t)H)) ||
-      (rc = dalloc_t(c, &m.topk_idx, (size_t)kMoeTopK)) || (rc = dalloc_t(c, &m.topk_w, (size_t)kMoeTopK)) ||
+      (rc = dalloc_t(c, &m.topk_idx, (size_t)kMoeTopK * k.layers)) ||
+      (rc = dalloc_t(c, &m.topk_w, (size_t)kMoeTopK * k.layers)) ||
+      ((k.flags & E4B_FLAG_LAYER_HIDDEN) && (rc = dalloc_t(c, &c->lh, (size_t)k.layers * H))) ||
       (rc = dalloc_t(c, &m.g_dense, (size_t)FF)) || (rc = dalloc_t(c, &m.g_slots, (size_t)kMoeTopK * FE)) ||
       (rc = dalloc_t(c, &m.dense_out, (size_t)H)) || (rc = dalloc_t(c, &m.moe_out, (size_t)H)))
     return rc;
@@ -627,8 +641,13 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   }
   // split-K attention: chunks of `chunk` positions; partials sized for the
   // layer with the most live positions
+  // The sliding layers use 32-position chunks (16 for a 512 window) in 4 V
+  // slices, so a window's K/V rows are spread over 128 blocks, and the o
+  // projection's prologue merges their 16 chunks in one pass; the full
+  // layers use attn_chunk (default 64) in 4 V slices.
   c->chunk = k.attn_chunk ? k.attn_chunk : 64;
-  c->nch = attn_chunks(k.max_seq > k.window ? k.max_seq : k.window, c->chunk);
+  c->chunk_sw = k.attn_chunk == 64 ? 64 : E4B_TUNE_CHUNK_SW;
+  c->nch = std::max(attn_chunks(k.max_seq, c->chunk), attn_chunks(k.window, c->chunk_sw));
   if (c->nch > kAttnMaxChunks)
     return e4b_fail(E4B_EINVAL, "max_seq %d needs %d attention chunks (max %d)", k.max_seq, c->nch, kAttnMaxChunks);
   c->ring_cap = k.max_seq;
@@ -656,7 +675,8 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->xg, (size_t)H)) || (rc = dalloc_t(c, &c->gp, (size_t)(PD ? PD : 1))) ||
       (rc = dalloc_t(c, &c->pp, (size_t)(PD ? PD / 32 : 1) * H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
-      (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)))
+      (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) || (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)) ||
+      ((k.flags & E4B_FLAG_LAYER_HIDDEN) && (rc = dalloc_t(c, &c->lh, (size_t)k.layers * H))))
     return rc;
   // batched prefill buffers: a chunk of M tokens must leave every key its
   // queries need in the sliding rings (ring >= window + M - 1, the Complete
@@ -691,88 +711,6 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
         (rc = dalloc_t(c, &c->kv_sk, (size_t)KVH * S * HD)) || (rc = dalloc_t(c, &c->kv_sv, (size_t)KVH * S * HD)))
       return rc;
   }
-  if (k.flags & E4B_FLAG_PERSISTENT) {
-    if (!persist_supported(H, FF, QH, KVH, PD) || (k.flags & E4B_FLAG_KV_SCORE))
-      return e4b_fail(E4B_EINVAL,
-                      "E4B_FLAG_PERSISTENT: unsupported configuration (hidden %d, ffn %d, %d/%d heads, ple_dim %d, "
-                      "or E4B_FLAG_KV_SCORE set)", H, FF, QH, KVH, PD);
-    c->pblocks = persist_blocks(H, FF, c->chunk);
-    if (c->pblocks < 0)
-      return e4b_fail(E4B_EHIP, "E4B_FLAG_PERSISTENT: occupancy query -> %s",
-                      hipGetErrorString((hipError_t)-c->pblocks));
-    if (c->pblocks == 0)
-      return e4b_fail(E4B_EINVAL, "E4B_FLAG_PERSISTENT: %d blocks of %d threads cannot be co-resident on this device (%s)",
-                      H / 8, kPersistThreads, persist_why());
-    const size_t QKVW = (size_t)c->qkv_rows;
-    const size_t pm = (size_t)QH * c->nch * (HD + 2);
-    const size_t set = (size_t)H + QKVW + pm + (size_t)QH * HD / 2 + (size_t)H + (size_t)FF / 2 + (size_t)H + (size_t)PD / 2;
-    c->ll_words = 2 * set;
-    if ((rc = dalloc_t(c, &c->ll, c->ll_words)) || (rc = dalloc_t(c, &c->pabort, 4)) ||
-        (rc = dalloc_t(c, &c->d_layers, (size_t)k.layers)))
-      return rc;
-    std::vector<PersistLayer> pl((size_t)k.layers);
-    for (int l = 0; l < k.layers; ++l) {
-      const Layer& ly = c->L[l];
-      PersistLayer& d = pl[(size_t)l];
-      d.qkv = q40_view(ly.qkv, c->qkv_rows, H);
-      d.o = q40_view(ly.o, H, (int64_t)QH * HD);
-      d.gu = q40_view(ly.gu, 2 * (int64_t)FF, H);
-      d.down = q40_view(ly.down, H, FF);
-      d.pg = q40_view(ly.pg, PD, H);
-      d.pp = q40_view(ly.pp_rm, H, PD);
-      d.attn_norm = ly.attn_norm;
-      d.q_norm = ly.q_norm;
-      d.k_norm = ly.k_norm;
-      d.post_attn = ly.post_attn;
-      d.ffn_norm = ly.ffn_norm;
-      d.post_ffw = ly.post_ffw;
-      d.post_norm = ly.post_norm;
-      d.scale = ly.scale;
-      d.global = ly.global ? 1 : 0;
-      d.kc = ly.kc;
-      d.vc = ly.vc;
-      d.slots = ly.slots;
-      unsigned long long* w = c->ll + (size_t)(l & 1) * set;
-      d.ll_p = w;
-      w += H;
-      d.ll_qkv = w;
-      w += QKVW;
-      d.ll_pm = w;
-      w += pm;
-      d.ll_att = w;
-      w += (size_t)QH * HD / 2;
-      d.ll_o = w;
-      w += H;
-      d.ll_gg = w;
-      w += (size_t)FF / 2;
-      d.ll_dn = w;
-      w += H;
-      d.ll_g = w;
-    }
-    E4B_HIP(hipMemcpy(c->d_layers, pl.data(), pl.size() * sizeof(PersistLayer), hipMemcpyHostToDevice));
-    PersistArgs& a = c->pargs;
-    a.L = c->d_layers;
-    a.layers = k.layers;
-    a.H = H;
-    a.FF = FF;
-    a.QH = QH;
-    a.KVH = KVH;
-    a.PD = PD;
-    a.window = k.window;
-    a.nch_max = c->nch;
-    a.eps = k.eps;
-    a.params = c->params;
-    a.epoch = c->params + 8;
-    a.h_in = c->h;
-    a.ple = c->ple;
-    a.rope = c->rope;
-    a.abort = c->pabort;
-    a.h_out = c->hb;
-    a.xo_hl = c->xo_hl;
-    a.out_norm = c->out_norm;
-    c->persist = true;
-    c->h_final = c->hb;
-  }
   }  // E4B recipe
   c->finalized = true;
   if ((rc = e4b_reset(c))) return rc;
@@ -782,14 +720,6 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
   rc = record_step(c);
   hipGraph_t g = nullptr;
   hipError_t ce = hipStreamEndCapture(c->st, &g);
-  if (rc && c->persist) {
-    // a cooperative launch the runtime cannot capture: launch the step's
-    // kernels directly every token instead
-    if (g) (void)hipGraphDestroy(g);
-    (void)hipGetLastError();
-    E4B_HIP(hipStreamSynchronize(c->st));
-    return E4B_OK;
-  }
   if (rc) {
     if (g) (void)hipGraphDestroy(g);
     c->finalized = false;
@@ -806,7 +736,6 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
 
 namespace {
 
-int record_step_persist(e4b_ctx* c);
 
 // One token of the A4B recipe (the reference's encodeForward / encodeLayer,
 // src/engine-a4b.js:424-463, 683-693): embedding; per layer the q|k(|v)
@@ -851,6 +780,7 @@ int record_step_a4b(e4b_ctx* c) {
       pq.w1b = pv.post_ffw2;
       pq.wp = pv.post_ffw;
       pq.scale = pv.scale;
+      if (c->lh) pq.hsnap = c->lh + (size_t)(l - 1) * H;  // E4B_FLAG_LAYER_HIDDEN: the stream after layer l - 1
     }
     if ((rc = launch_q40(q40_view(ly.qkv, ly.qkv_rows, H), nullptr, nullptr, EPI_F32, oq, 1, st, &pq)) ||
         (rc = tick(c, "qkv")))
@@ -916,6 +846,8 @@ int record_step_a4b(e4b_ctx* c) {
     a.FF = FE;
     a.FF2 = FF;
     a.h_out = l == k.layers - 1 ? c->h : nullptr;
+    a.topk_idx = c->moe.topk_idx + (size_t)kMoeTopK * l;  // each layer's picks stay readable (e4b_read_topk)
+    a.topk_w = c->moe.topk_w + (size_t)kMoeTopK * l;
     if ((rc = launch_moe_ffn(a, st)) || (rc = tick(c, "moe_ffn"))) return rc;
   }
   c->h_final = c->h;
@@ -931,7 +863,6 @@ int record_step_a4b(e4b_ctx* c) {
 
 int record_step(e4b_ctx* c) {
   if (c->cfg.recipe == E4B_RECIPE_A4B) return record_step_a4b(c);
-  if (c->persist) return record_step_persist(c);
   const e4b_config& k = c->cfg;
   const int H = k.hidden, QH = k.q_heads, KVH = k.kv_heads, HD = k.head_dim, FF = k.ffn, PD = k.ple_dim;
   const int Lc = k.layers;
@@ -992,6 +923,7 @@ int record_step(e4b_ctx* c) {
       ProArgs p = PD ? pro(hnext, c->pp, pv.post_norm, ly.attn_norm, pv.scale)
                      : pro(hnext, c->dn, pv.post_ffw, ly.attn_norm, pv.scale);
       if (PD) p.na = PD / 32;  // the PLE branch leaves PD/32 partial projections
+      if (c->lh) p.hsnap = c->lh + (size_t)(l - 1) * H;  // E4B_FLAG_LAYER_HIDDEN: the stream after layer l - 1
       rc = launch_q40(Wqkv, nullptr, nullptr, EPI_F32, oq, 1, st, &p);
       swap_h();
     }
@@ -1000,7 +932,8 @@ int record_step(e4b_ctx* c) {
     //    projection's prologue when the projection has 2048 columns and the
     //    layer's live span fits the prologue's 64 chunks per head (global
     //    layers of contexts beyond 4096 positions use the combine launch)
-    const int gch_layer = attn_chunks(ly.global ? ly.slots : k.window, c->chunk);
+    const int chunk_l = ly.global ? c->chunk : c->chunk_sw;
+    const int gch_layer = attn_chunks(ly.global ? ly.slots : k.window, chunk_l);
     const bool fuse_combine = QH * HD == kProAttnH && gch_layer <= kProAttnMaxChunks;
     AttnLaunch a;
     a.qkv = c->qkv;
@@ -1021,7 +954,8 @@ int record_step(e4b_ctx* c) {
     a.angles = k.rope_angles;
     a.slots = ly.slots;
     a.window = ly.global ? 0 : k.window;
-    a.chunk = c->chunk;
+    a.chunk = chunk_l;
+    a.vslices = ly.global ? c->vs_gl : c->vs_sw;
     a.combine = !fuse_combine;
     a.eps = k.eps;
     a.kv_idx = 4;  // full layers: params[4] = the token's slot
@@ -1040,7 +974,7 @@ int record_step(e4b_ctx* c) {
       pa.params = c->params;
       pa.kv_idx = 4;
       pa.window = a.window;
-      pa.chunk_shift = c->chunk == 64 ? 6 : 5;
+      pa.chunk_shift = chunk_l == 64 ? 6 : 5;
       pa.gch = gch_layer;
       rc = launch_q40(Wo, nullptr, nullptr, EPI_F32, oo, 1, st, &pa);
     } else {
@@ -1090,39 +1024,6 @@ int record_step(e4b_ctx* c) {
     rc = launch_tail(hcur, c->dn, 1, last.post_ffw, last.scale, c->out_norm, c->xo_hl, H, k.eps, st);
   if (rc || (rc = tick(c, "final_norm"))) return rc;
   c->h_final = hcur;
-  if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
-                                   c->logits, nullptr, c->amax_part, st)) ||
-      (rc = tick(c, "lm_head")))
-    return rc;
-  if ((rc = launch_feedback(c->amax_part, c->amax_parts, c->amax, c->params, c->tok_ring, c->ring_cap, st)))
-    return rc;
-  return tick(c, "argmax_feedback");
-}
-
-// The step with the layer loop as one persistent kernel (k_persist.hip):
-// embedding, PLE inputs, the layers (the last residual and the final norm
-// included), lm-head + argmax, feedback.
-int record_step_persist(e4b_ctx* c) {
-  const e4b_config& k = c->cfg;
-  const int H = k.hidden, HD = k.head_dim, PD = k.ple_dim, Lc = k.layers;
-  hipStream_t st = c->st;
-  int rc;
-  const Q6Mat E = q6_view(c->embd, k.vocab, H);
-  if ((rc = launch_embed(E, c->params, c->prompt, sqrtf((float)H), c->h, c->h_hl, c->status, c->inv_local,
-                         c->inv_global, HD / 2, c->rope, st)) ||
-      (rc = tick(c, "embed")))
-    return rc;
-  GemvOut po = {c->proj, nullptr, nullptr, 0};
-  if ((rc = launch_q40(q40_view(c->ple_proj, (int64_t)Lc * PD, H), (const uint32_t*)c->h_hl,
-                       (const uint32_t*)(c->h_hl + H), EPI_F32, po, 1, st)) ||
-      (rc = tick(c, "ple_model_proj")))
-    return rc;
-  if ((rc = launch_ple_prep(c->proj, c->ple_tab, c->ple_norm, c->params, c->prompt, Lc, k.vocab,
-                            1.0f / sqrtf((float)H), c->ple, c->h, c->L[0].attn_norm, c->xn, H, k.eps, st)) ||
-      (rc = tick(c, "ple_prep")))
-    return rc;
-  if ((rc = launch_persist(c->pargs, c->pblocks, c->chunk, st)) || (rc = tick(c, "layers")))
-    return rc;
   if ((rc = launch_q6k_gemv_argmax(E, (const uint32_t*)c->xo_hl, (const uint32_t*)(c->xo_hl + H), k.softcap,
                                    c->logits, nullptr, c->amax_part, st)) ||
       (rc = tick(c, "lm_head")))
@@ -1430,16 +1331,8 @@ int ready(e4b_ctx* c, const char* fn) {
 
 int check_status(e4b_ctx* c) {
   uint32_t s = 0;
-  int ab = 0;
   E4B_HIP(hipMemcpyAsync(&s, c->status, 4, hipMemcpyDeviceToHost, c->st));
-  if (c->pabort) E4B_HIP(hipMemcpyAsync(&ab, c->pabort, 4, hipMemcpyDeviceToHost, c->st));
   E4B_HIP(hipStreamSynchronize(c->st));
-  if (ab) {
-    // the tagged hand-off state is unknown after an abort: start clean
-    E4B_HIP(hipMemset(c->pabort, 0, 4));
-    E4B_HIP(hipMemset(c->ll, 0, c->ll_words * 8));
-    return e4b_fail(E4B_EHIP, "persistent step: a wait for a hand-off gave up (state reset; prefill again)");
-  }
   if (s) {
     uint32_t z = 0;
     E4B_HIP(hipMemcpy(c->status, &z, 4, hipMemcpyHostToDevice));
@@ -1631,58 +1524,10 @@ extern "C" int e4b_profile_step(e4b_ctx* c, uint32_t token, uint32_t pos, e4b_pr
     return e4b_fail(E4B_ERANGE, "e4b_profile_step: %u full-layer entries fill max_seq %d", kv, c->cfg.max_seq);
   const uint32_t p[5] = {pos, token, 0u, 0u, kv};
   if ((rc = put_params(c, p, 0, 5))) return rc;
-  const size_t tslots = c->persist ? (size_t)c->pblocks * c->cfg.layers * kPersistTraceSlots : 0;
-  if (c->persist) {
-    if (!c->ptrace && (rc = dalloc_t(c, &c->ptrace, tslots))) return rc;
-    E4B_HIP(hipMemsetAsync(c->ptrace, 0, tslots * 8, c->st));
-    c->pargs.trace = c->ptrace;
-  }
   int n = profile_run(c, out, cap, [&]() { return record_step(c); });
-  c->pargs.trace = nullptr;
   if (n < 0) return n;
   c->kv_count = kv + 1;
   if ((rc = check_status(c))) return rc;
-  if (c->persist) {
-    // the layer loop's phases from the trace: per phase, the time from the
-    // previous phase finishing on every block to this one finishing on every
-    // block ("span"), and block 0's wait for its input and its own work
-    static const char* kPh[kPersistPhases] = {"qkv", "attn", "combine", "o", "gate_up", "down", "ple_gate", "ple_proj"};
-    std::vector<unsigned long long> t(tslots);
-    E4B_HIP(hipMemcpy(t.data(), c->ptrace, tslots * 8, hipMemcpyDeviceToHost));
-    int dev = 0, khz = 0;
-    E4B_HIP(hipGetDevice(&dev));
-    E4B_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
-    const double us_per_tick = khz > 0 ? 1000.0 / khz : 0.0;
-    const int Lc = c->cfg.layers, B = c->pblocks;
-    auto at = [&](int b, int l, int ph, int k) { return t[((size_t)b * Lc + l) * kPersistTraceSlots + ph * 3 + k]; };
-    double span[kPersistPhases] = {0}, wait0[kPersistPhases] = {0}, work0[kPersistPhases] = {0};
-    unsigned long long prev_done = 0;
-    for (int l = 0; l < Lc; ++l)
-      for (int ph = 0; ph < kPersistPhases; ++ph) {
-        unsigned long long done = 0, first = ~0ull;
-        for (int b = 0; b < B; ++b) {
-          done = std::max(done, at(b, l, ph, 2));
-          if (at(b, l, ph, 0)) first = std::min(first, at(b, l, ph, 0));
-        }
-        const unsigned long long from = prev_done ? prev_done : first;
-        if (done >= from) span[ph] += (double)(done - from) * us_per_tick;
-        prev_done = done;
-        const unsigned long long t0 = at(0, l, ph, 0), t1 = at(0, l, ph, 1) ? at(0, l, ph, 1) : t0, t2 = at(0, l, ph, 2);
-        if (t1 >= t0 && t2 >= t1) {
-          wait0[ph] += (double)(t1 - t0) * us_per_tick;
-          work0[ph] += (double)(t2 - t1) * us_per_tick;
-        }
-      }
-    for (int ph = 0; ph < kPersistPhases; ++ph)
-      for (int k = 0; k < 3; ++k) {
-        if (n >= cap) break;
-        const char* what = k == 0 ? "span" : k == 1 ? "block0_wait" : "block0_work";
-        snprintf(out[n].name, sizeof(out[n].name), "layers.%s.%s", kPh[ph], what);
-        out[n].us = (float)(k == 0 ? span[ph] : k == 1 ? wait0[ph] : work0[ph]);
-        out[n].n = Lc;
-        ++n;
-      }
-  }
   return n;
 }
 
@@ -1720,6 +1565,33 @@ extern "C" int e4b_read_hidden(e4b_ctx* c, float* out) {
   if (rc) return rc;
   E4B_HIP(hipMemcpyAsync(out, c->h_final ? c->h_final : c->h, (size_t)c->cfg.hidden * 4, hipMemcpyDeviceToHost,
                          c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_read_layer_hidden(e4b_ctx* c, int layer, float* out) {
+  int rc = ready(c, "e4b_read_layer_hidden");
+  if (rc) return rc;
+  if (!out) return e4b_fail(E4B_EINVAL, "e4b_read_layer_hidden: null output");
+  if (layer < 0 || layer >= c->cfg.layers)
+    return e4b_fail(E4B_ERANGE, "e4b_read_layer_hidden: layer %d of %d", layer, c->cfg.layers);
+  if (!c->lh && layer < c->cfg.layers - 1)
+    return e4b_fail(E4B_ESTATE, "e4b_read_layer_hidden: the engine was created without E4B_FLAG_LAYER_HIDDEN");
+  const float* src = layer == c->cfg.layers - 1 ? (c->h_final ? c->h_final : c->h) : c->lh + (size_t)layer * c->cfg.hidden;
+  E4B_HIP(hipMemcpyAsync(out, src, (size_t)c->cfg.hidden * 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipStreamSynchronize(c->st));
+  return E4B_OK;
+}
+
+extern "C" int e4b_read_topk(e4b_ctx* c, int layer, uint32_t* idx, float* w) {
+  int rc = ready(c, "e4b_read_topk");
+  if (rc) return rc;
+  if (c->cfg.recipe != E4B_RECIPE_A4B) return e4b_fail(E4B_EINVAL, "e4b_read_topk: the E4B recipe has no experts");
+  if (!idx || !w) return e4b_fail(E4B_EINVAL, "e4b_read_topk: null output");
+  if (layer < 0 || layer >= c->cfg.layers)
+    return e4b_fail(E4B_ERANGE, "e4b_read_topk: layer %d of %d", layer, c->cfg.layers);
+  E4B_HIP(hipMemcpyAsync(idx, c->moe.topk_idx + (size_t)kMoeTopK * layer, kMoeTopK * 4, hipMemcpyDeviceToHost, c->st));
+  E4B_HIP(hipMemcpyAsync(w, c->moe.topk_w + (size_t)kMoeTopK * layer, kMoeTopK * 4, hipMemcpyDeviceToHost, c->st));
   E4B_HIP(hipStreamSynchronize(c->st));
   return E4B_OK;
 }
@@ -1762,8 +1634,6 @@ extern "C" int e4b_reset(e4b_ctx* c) {
   E4B_HIP(hipMemsetAsync(c->params, 0, 16 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->status, 0, 4 * 4, c->st));
   E4B_HIP(hipMemsetAsync(c->amax, 0, 4 * 4, c->st));
-  if (c->ll) E4B_HIP(hipMemsetAsync(c->ll, 0, c->ll_words * 8, c->st));
-  if (c->pabort) E4B_HIP(hipMemsetAsync(c->pabort, 0, 4, c->st));
   if ((rc = zero_scores(c))) return rc;
   c->kv_count = 0;
   E4B_HIP(hipStreamSynchronize(c->st));

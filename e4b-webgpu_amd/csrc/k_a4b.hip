@@ -20,6 +20,7 @@
 #include "a4b.h"
 #include "kernels.h"
 #include "util.h"
+#include "trace.h"
 
 namespace {
 
@@ -32,6 +33,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ h_in,
                                                  const float* __restrict__ w2, uint16_t* __restrict__ x,
                                                  uint16_t* __restrict__ xlo, int H, float eps, int na,
                                                  int64_t a_slice) {
+  E4B_TRACE_SCOPE(trace_tag(TR_ROWNORM, 0));
   __shared__ float red[4];
   const int t = threadIdx.x;
   // row blockIdx.x of a batch (one row in the decode step)
@@ -133,6 +135,7 @@ DEV Live live_of(const AttnGen& A) {
 // after the first); V is split across them.
 template <int HD, int GQA, bool RAW>
 __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
+  E4B_TRACE_SCOPE(trace_tag(TR_ATTN_GEN, HD));
   constexpr int NW = 8, CS = kAttnGenChunk, PER = HD / 64, PW = CS / NW, VD = 128;
   constexpr int NR = GQA + 2, RPW = (NR + NW - 1) / NW, LPH = 64 / GQA;
   static_assert(CS == 64 && GQA <= NW && (GQA & (GQA - 1)) == 0, "64-position chunks, GQA 1/2/4/8");
@@ -339,10 +342,11 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
 // Thread t: output dims t + 256 q, and the (max, sum) of chunk t.  The first
 // U chunks' outputs are requested with the statistics, before the reductions
 // wait; further chunks follow U at a time.
-constexpr int kMergeMaxChunks = 256;
+constexpr int kMergeMaxChunks = kAttnGenMaxChunks;
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnGen A) {
+  E4B_TRACE_SCOPE(trace_tag(TR_ATTN_MERGE, 0));
   constexpr int CS = kAttnGenChunk, U = 16, DPT = HD / 256;
   __shared__ float wts[kMergeMaxChunks];
   __shared__ float red[4];

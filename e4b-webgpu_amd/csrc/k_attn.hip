@@ -29,6 +29,7 @@
 #include "step.h"
 #include "util.h"
 #include "attn_prep.h"
+#include "trace.h"
 
 namespace {
 
@@ -74,25 +75,30 @@ DEV float xmax32(float v) {
   return fmaxf(v, t);
 }
 
-// One block of 8 waves per (KV group g, chunk c of CS positions, V slice z);
-// wave w owns the chunk's positions j = w + 8k (k < CS/8).  K is read as 16
-// lanes per position, lane dl holding dims 8dl..8dl+7 and 128+8dl..128+8dl+7
-// (two 256-byte contiguous halves per row), 4 positions per pass (lane group
-// `sub` takes k = 4s + sub).  With NS = 2 the block handles V dims
-// [128z, 128z+128) only: both slices compute the same scores, and each reads
-// half of V, which spreads a chunk's memory traffic over two CUs.  V is read
-// as 16 B per lane, 8 dims each, 64/LV positions per load (LV = lanes per
-// position).
-template <int CS, int NS, bool RAW = false>
-__global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
-  constexpr int NW = 8;
-  constexpr int KP = CS / 32;      // score passes per wave (4 positions each)
-  constexpr int VS = CS / 8;       // positions per wave
-  constexpr int VD = HD / NS;      // V dims per block
-  constexpr int LV = VD / 8;       // lanes per V row
-  constexpr int PPL = 64 / LV;     // positions per V load
-  constexpr int VQ = VS / PPL;     // V loads per lane
-  static_assert(NS == 1 || NS == 2, "one or two V slices");
+// One block of NW waves (8 or 4) per (KV group g, chunk c of CS positions, V
+// slice z); wave w owns the chunk's positions j = w + NW k (k < CS/NW).  K is
+// read as 16 lanes per position, lane dl holding dims 8dl..8dl+7 and
+// 128+8dl..128+8dl+7 (two 256-byte contiguous halves per row), 4 positions
+// per pass (lane group `sub` takes k = 4s + sub).  With NS > 1 the block
+// handles V dims [VD z, VD z + VD) only (VD = 256 / NS): every slice computes
+// the same scores and reads 1/NS of V, which spreads a chunk's memory traffic
+// over NS CUs (the grid puts a chunk's slices on one XCD, so its K rows are
+// fetched into that XCD's L2 once).  V is read as 16 B per lane, 8 dims each,
+// 64/LV positions per load (LV = lanes per position).  With NW = 8 waves 4
+// and 5 prep the new k and v rows; with NW = 4 waves 0 and 1 prep them after
+// their q heads, in the chunk that owns the token only.
+template <int CS, int NS, int NW = 8, bool RAW = false>
+__global__ __launch_bounds__(64 * NW) void k_attn_split(AttnArgs A) {
+  E4B_TRACE_SCOPE(trace_tag(TR_ATTN, A.window > 0 ? 0 : 1));
+  constexpr int KP = CS / (4 * NW);  // score passes per wave (4 positions each)
+  constexpr int VS = CS / NW;        // positions per wave
+  constexpr int VD = HD / NS;        // V dims per block
+  constexpr int LV = VD / 8;         // lanes per V row
+  constexpr int PPL = 64 / LV;       // positions per V load
+  constexpr int VQ = VS / PPL;       // V loads per lane
+  static_assert(NW == 8 || NW == 4, "8 or 4 waves");
+  static_assert(NS == 1 || NS == 2 || NS == 4, "one, two or four V slices");
+  static_assert(KP >= 1 && VQ >= 1 && VS == VQ * PPL && CS == KP * 4 * NW, "positions per wave");
   __shared__ float qs[GQA][HD];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
@@ -125,15 +131,23 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
   };
   const int sub = lane >> 4, dl = lane & 15;
   const int vsub = lane / LV, vl = lane % LV, vd0 = VD * zs + 8 * vl;
+  const bool owner = cur < c_lo + m;  // the last live chunk holds cur, at j = m - 1
 
   // 0. request everything the block reads before any math: the head-prep
   //    inputs (this wave's q/k/v row, its norm weights, the RoPE (cos, sin)
-  //    of its lane's dims; waves 6-7 repeat wave 5's row and drop it), then
-  //    the wave's K and V rows (index clamped into the chunk; the row of
-  //    `pos` is not written yet and is replaced from LDS below)
-  const int prow = wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g;
+  //    of its lane's dims; with NW = 8 waves 6-7 repeat wave 5's row and drop
+  //    it; with NW = 4 waves 0 and 1 also read the k and v rows), then the
+  //    wave's K and V rows (index clamped into the chunk; the row of `pos` is
+  //    not written yet and is replaced from LDS below)
+  const int prow = NW == 8 ? (wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g) : g * GQA + wave;
   const float4 xin = *reinterpret_cast<const float4*>(A.qkv + (int64_t)prow * HD + 4 * lane);
-  const float4 win = *reinterpret_cast<const float4*>((wave < 4 ? A.qw : A.kw) + 4 * lane);
+  const float4 win = *reinterpret_cast<const float4*>((NW == 8 && wave >= 4 ? A.kw : A.qw) + 4 * lane);
+  const int krow2 = A.qh + (wave == 0 ? 0 : A.kvh) + g;  // NW = 4: the k (wave 0) or v (wave 1) row
+  float4 xin2 = make_float4(0.f, 0.f, 0.f, 0.f), win2 = xin2;
+  if constexpr (NW == 4) {
+    xin2 = *reinterpret_cast<const float4*>(A.qkv + (int64_t)krow2 * HD + 4 * lane);
+    win2 = *reinterpret_cast<const float4*>(A.kw + 4 * lane);
+  }
   const bool have_cs = A.rope != nullptr;
   const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);  // any readable 1 KB
   const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
@@ -153,27 +167,34 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
     vr[q] = *reinterpret_cast<const uint4*>(vc + slot_at(j) * HD + vd0);
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first wait
+  E4B_TRACE_MARK(0);
 
-  // 1. head prep: waves 0-3 prep q heads 4g..4g+3, wave 4 the new k, wave 5
-  //    the new v (f16-rounded, as stored); the chunk owning `pos` stores them
-  const bool owner = cur < c_lo + m;  // the last live chunk holds cur, at j = m - 1
-  if (wave < 6) {
+  // 1. head prep: q heads 4g..4g+3 (waves 0-3), the new k and v rows
+  //    (f16-rounded, as stored; NW = 8: waves 4 and 5, NW = 4: waves 0 and 1
+  //    of the owner chunk); the chunk owning `pos` stores them
+  const float2 cs[4] = {make_float2(rc0.x, rc0.y), make_float2(rc0.z, rc0.w), make_float2(rc1.x, rc1.y),
+                        make_float2(rc1.z, rc1.w)};
+  auto prep_kv = [&](float4 xr, float4 wr, bool is_k) {
+    float x[4] = {xr.x, xr.y, xr.z, xr.w};
+    const float w[4] = {wr.x, wr.y, wr.z, wr.w};
+    prep_head_regs(x, w, is_k, cs, have_cs, A.inv_freq, A.angles, A.eps, fpos, is_k);
+    const uint2 pk = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
+                                (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
+    *reinterpret_cast<uint2*>((is_k ? knew : vnew) + 4 * lane) = pk;
+    if (owner && zs == 0) *reinterpret_cast<uint2*>((is_k ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
+  };
+  if (wave < 4) {
     float x[4] = {xin.x, xin.y, xin.z, xin.w};
     const float w[4] = {win.x, win.y, win.z, win.w};
-    const float2 cs[4] = {make_float2(rc0.x, rc0.y), make_float2(rc0.z, rc0.w), make_float2(rc1.x, rc1.y),
-                          make_float2(rc1.z, rc1.w)};
-    prep_head_regs(x, w, wave < 5, cs, have_cs, A.inv_freq, A.angles, A.eps, fpos, wave < 5);
-    if (wave < 4) {
+    prep_head_regs(x, w, true, cs, have_cs, A.inv_freq, A.angles, A.eps, fpos, true);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = x[i];
-    } else {
-      const uint2 pk = make_uint2((uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16),
-                                  (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16));
-      *reinterpret_cast<uint2*>((wave == 4 ? knew : vnew) + 4 * lane) = pk;
-      if (owner && zs == 0) *reinterpret_cast<uint2*>((wave == 4 ? kc : vc) + slot_at(m - 1) * HD + 4 * lane) = pk;
-    }
+    for (int i = 0; i < 4; ++i) qs[wave][4 * lane + i] = x[i];
+  } else if (NW == 8 && wave < 6) {
+    prep_kv(xin, win, wave == 4);
   }
+  if (NW == 4 && owner && wave < 2) prep_kv(xin2, win2, wave == 0);
   lds_sync();
+  E4B_TRACE_MARK(1);
 
   // 2. scores of the wave's positions: 16 lanes per position (16 dims each);
   //    after the reduction lane (sub, dl) holds head dl/4 of position
@@ -213,7 +234,7 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
         A.raw[(int64_t)(g * GQA + (dl >> 2)) * A.slots + slot_at(j)] = sc[s];
     }
   }
-
+  E4B_TRACE_MARK(2);
   // 3. the wave's softmax statistics per head (lanes with equal dl/4 share
   //    a head): max and sum over the passes and the four lane groups
   float mx = sc[0];
@@ -261,16 +282,22 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
           const float p0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i0 >> 2]), 16 * (i0 & 3) + 4 * h));
           const float p1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[i1 >> 2]), 16 * (i1 & 3) + 4 * h));
           pf = vsub ? p1 : p0;
-        } else {
-          // PPL = 4: position 4q + vsub lives in pass q, lane group vsub
+        } else if constexpr (PPL == 4) {
+          // position 4q + vsub lives in pass q, lane group vsub
           pf = __shfl(e[q], 16 * vsub + 4 * h, 64);
+        } else {
+          // PPL = 8: position 8q + vsub lives in pass 2q + vsub / 4, lane group vsub % 4
+          const float p0 = __shfl(e[2 * q], 16 * (vsub & 3) + 4 * h, 64);
+          const float p1 = __shfl(e[2 * q + 1], 16 * (vsub & 3) + 4 * h, 64);
+          pf = vsub < 4 ? p0 : p1;
         }
 #pragma unroll
         for (int d = 0; d < 8; ++d) acc[h][d] = fmaf(pf, vf[d], acc[h][d]);
       }
     }
     // fold the position groups: lanes < 32 keep heads 0, 1, lanes >= 32
-    // heads 2, 3; with four groups, bit 16 then picks one of the two
+    // heads 2, 3; with four or eight groups, bit 16 then picks one of the
+    // two, and with eight groups the lanes 8 apart are added
     float r[2][8];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
@@ -287,9 +314,15 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       float t[8];
 #pragma unroll
       for (int d = 0; d < 8; ++d) t[d] = tstep<16>(r[0][d], r[1][d]);
-      float4* dst = reinterpret_cast<float4*>(&po[wave][2 * (lane >> 5) + ((lane >> 4) & 1)][8 * vl]);
-      dst[0] = make_float4(t[0], t[1], t[2], t[3]);
-      dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+      if constexpr (PPL == 8) {
+#pragma unroll
+        for (int d = 0; d < 8; ++d) t[d] = xsum_step<8>(t[d]);
+      }
+      if (PPL == 4 || (lane & 8) == 0) {
+        float4* dst = reinterpret_cast<float4*>(&po[wave][2 * (lane >> 5) + ((lane >> 4) & 1)][8 * vl]);
+        dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+        dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+      }
     }
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
@@ -299,12 +332,14 @@ __global__ __launch_bounds__(512) void k_attn_split(AttnArgs A) {
       }
   }
   lds_sync();
+  E4B_TRACE_MARK(3);
 
-  // 5. fold the 8 waves (log-sum-exp) into this chunk's partials
+  // 5. fold the NW waves (log-sum-exp) into this chunk's partials
   //    ([head][chunk][dim], [head][chunk][max, sum]); GQA x VD outputs, one
   //    or two (adjacent dims) per thread
   {
     constexpr int OPT = GQA * VD / (NW * 64);  // outputs per thread
+    static_assert(OPT == 1 || OPT == 2, "outputs per thread");
     const int gch = gridDim.y;  // partial stride: chunks allocated per head
     const int h = threadIdx.x / (VD / OPT), d = OPT * (threadIdx.x % (VD / OPT));
     float M = wml[0][h][0];
@@ -464,20 +499,37 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.slots = a.slots;
   A.window = a.window;
   A.eps = a.eps;
-  if (a.chunk == 64) {
+  if (a.vslices != 2 && a.vslices != 4) return e4b_fail(E4B_EINVAL, "attention: %d V slices (2 or 4)", a.vslices);
+  const dim3 grid(a.kvh, nch, a.vslices);
+  if (a.vslices == 4) {
+    // 4 waves a block, 64-dim V slices
+    if (a.chunk == 64) {
+      if (A.raw)
+        hipLaunchKernelGGL((k_attn_split<64, 4, 4, true>), grid, dim3(256), 0, st, A);
+      else
+        hipLaunchKernelGGL((k_attn_split<64, 4, 4>), grid, dim3(256), 0, st, A);
+    } else {
+      if (A.raw)
+        hipLaunchKernelGGL((k_attn_split<32, 4, 4, true>), grid, dim3(256), 0, st, A);
+      else
+        hipLaunchKernelGGL((k_attn_split<32, 4, 4>), grid, dim3(256), 0, st, A);
+    }
+  } else if (a.chunk == 64) {
     if (A.raw)
-      hipLaunchKernelGGL((k_attn_split<64, 2, true>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
+      hipLaunchKernelGGL((k_attn_split<64, 2, 8, true>), grid, dim3(512), 0, st, A);
     else
-      hipLaunchKernelGGL((k_attn_split<64, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
-    if (a.combine)
-      hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
-                         a.kv_idx, a.window, nch, a.out);
+      hipLaunchKernelGGL((k_attn_split<64, 2, 8>), grid, dim3(512), 0, st, A);
   } else {
     if (A.raw)
-      hipLaunchKernelGGL((k_attn_split<32, 2, true>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
+      hipLaunchKernelGGL((k_attn_split<32, 2, 8, true>), grid, dim3(512), 0, st, A);
     else
-      hipLaunchKernelGGL((k_attn_split<32, 2>), dim3(a.kvh, nch, 2), dim3(512), 0, st, A);
-    if (a.combine)
+      hipLaunchKernelGGL((k_attn_split<32, 2, 8>), grid, dim3(512), 0, st, A);
+  }
+  if (a.combine) {
+    if (a.chunk == 64)
+      hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+                         a.kv_idx, a.window, nch, a.out);
+    else
       hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
                          a.kv_idx, a.window, nch, a.out);
   }

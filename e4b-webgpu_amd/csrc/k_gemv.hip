@@ -9,6 +9,7 @@
 #include "../../include/e4b.h"
 #include "kernels.h"
 #include "util.h"
+#include "trace.h"
 
 namespace {
 
@@ -113,6 +114,7 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_argmax(Q6Mat W, const uint32_t
                                                          const uint32_t* __restrict__ xl, float softcap,
                                                          float* __restrict__ logits, uint2* part,
                                                          int64_t ntiles) {
+  E4B_TRACE_SCOPE(trace_tag(TR_LMHEAD, 0));
   constexpr int SPAN = 64 / R;
   constexpr int XW = BPL * 64 * 16;  // 32-bit words of x (hi or lo) the block can hold
   __shared__ __align__(16) uint32_t xs[2][XW];

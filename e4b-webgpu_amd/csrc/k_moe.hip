@@ -25,6 +25,7 @@
 #include "kernels.h"
 #include "moe.h"
 #include "util.h"
+#include "trace.h"
 
 namespace {
 
@@ -62,6 +63,7 @@ DEV float f4_ss(float4 v, float acc) {
 }
 
 __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
+  E4B_TRACE_SCOPE(trace_tag(TR_MOE_ROUTER, 0));
   // token row y of a batch (the batched prefill); y = 0 in the decode step
   A.h += (int64_t)blockIdx.y * A.H;
   A.xd += (int64_t)blockIdx.y * A.H;
@@ -413,6 +415,7 @@ constexpr int GU_U = 2;  // units per lane group (a wave tile holds 2 GU_U units
 constexpr int kMoeMaxH = GU_LPR * GU_BPL * 32;  // 3072
 
 __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
+  E4B_TRACE_SCOPE(trace_tag(TR_MOE_GU, 0));
   __shared__ __align__(16) uint16_t xs[2][kMoeMaxH];
   __shared__ int sel[K];
   const int lane = threadIdx.x & 63;
@@ -549,6 +552,7 @@ constexpr int DE_LPR = 8, DE_BPL = 3, DE_R = 1;
 constexpr int kMoeMaxX = K * DE_LPR * DE_BPL * 32;  // 6144 >= FF2 and 8 FF
 
 __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
+  E4B_TRACE_SCOPE(trace_tag(TR_MOE_DOWN, 0));
   __shared__ __align__(16) uint16_t xs[kMoeMaxX];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -681,6 +685,7 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
 constexpr int kTailPer = 12;  // elements per thread, H <= 3072
 
 __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
+  E4B_TRACE_SCOPE(trace_tag(TR_MOE_TAIL, 0));
   __shared__ float red[4];
   const int H = A.H;
   // token row blockIdx.x of a batch (one block in the decode step)

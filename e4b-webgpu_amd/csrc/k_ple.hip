@@ -18,6 +18,7 @@
 #include "q40_kernel.h"
 #include "step.h"
 #include "util.h"
+#include "trace.h"
 
 namespace {
 
@@ -28,6 +29,7 @@ constexpr float kTwo24 = 16777216.0f;
 // quarters (blockIdx.y), PR = PROK / Q projection rows per thread.
 template <int PROK, int Q, int NA>
 __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
+  E4B_TRACE_SCOPE(trace_tag(TR_PLE, 0));
   constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK, PR = PROK / Q;
   static_assert(G * R == 8, "8 gate rows per wave");
   static_assert(PR * Q == PROK, "whole projection rows per thread");
@@ -67,7 +69,9 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
   // no row load a valid neighbour and drop it)
   const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
+  E4B_TRACE_MARK(0);
   q40k::pro_finish<PROK, 256, NA, false>(pa, pr, xs, red);
+  E4B_TRACE_MARK(1);
 
   // gate: 32 columns of x per lane (block l), R rows per group
   {
@@ -97,6 +101,7 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
     }
   }
   lds_sync();
+  E4B_TRACE_MARK(2);
 
   // projection partial: part[w][o] = d_{o,w} * sum_j (n_j - 8) g_j
   {

@@ -9,6 +9,7 @@
 #include "kernels.h"
 #include "step.h"
 #include "util.h"
+#include "trace.h"
 
 namespace {
 
@@ -24,6 +25,7 @@ __global__ __launch_bounds__(256) void k_tail(float* __restrict__ h, const float
                                               const float* __restrict__ w_post, float scale,
                                               const float* __restrict__ w_out, uint16_t* __restrict__ xo_hl, int H,
                                               float eps) {
+  E4B_TRACE_SCOPE(trace_tag(TR_TAIL, 0));
   __shared__ float red[4];
   float hv[PER];
   float pv[PER];
@@ -83,6 +85,7 @@ __global__ __launch_bounds__(256) void k_embed(Q6Mat E, const uint32_t* __restri
                                                uint32_t* __restrict__ status, const float* __restrict__ inv_local,
                                                const float* __restrict__ inv_global, int half,
                                                float2* __restrict__ rope) {
+  E4B_TRACE_SCOPE(trace_tag(TR_EMBED, 0));
   const uint32_t pos = params[0];
   if (blockIdx.x == 0)
     for (int t = threadIdx.x; t < 2 * half; t += 256) {
@@ -146,6 +149,7 @@ __global__ __launch_bounds__(256) void k_ple_prep(const float* __restrict__ proj
                                                   float proj_scale, float* __restrict__ ple,
                                                   const float* __restrict__ h, const float* __restrict__ w_attn0,
                                                   uint16_t* __restrict__ xn, int H, float eps) {
+  E4B_TRACE_SCOPE(trace_tag(TR_PLE_PREP, 0));
   __shared__ float red[4];
   const int b = blockIdx.x, t = threadIdx.x;
   if (b == L) {
@@ -185,6 +189,7 @@ __global__ __launch_bounds__(256) void k_ple_prep(const float* __restrict__ proj
 // wins (kernels/argmax2.wgsl:8-48).
 __global__ __launch_bounds__(256) void k_feedback(const uint2* __restrict__ part, int nparts, uint32_t* amax,
                                                   uint32_t* params, uint32_t* tok_ring, int ring_cap) {
+  E4B_TRACE_SCOPE(trace_tag(TR_FEEDBACK, 0));
   __shared__ float sv[4];
   __shared__ uint32_t si[4];
   float v = -3.0e38f;

@@ -81,6 +81,7 @@ constexpr int kProAttnMaxChunks = 64;  // split-K chunks per head the attention 
 struct ProArgs {
   const float* hin;
   float* hout;       // may be null
+  float* hsnap;      // may be null: block (0,0) also stores h here (the per-layer readout)
   const float* a;    // may be null
   const float* w1;
   const float* w2;   // may be null

@@ -1,5 +1,6 @@
 // lib.hip -- C-ABI plumbing (errors, device memory, workspace) and the
 // kernel-level entry points of libe4b.
+#include <algorithm>
 #include <mutex>
 #include <vector>
 #include <string.h>
@@ -517,4 +518,82 @@ extern "C" int e4b_k_moe_layer(const e4b_moe_weights* w, const float* h, float* 
   if (dense_out) a.dense_out = dense_out;
   if (moe_out) a.moe_out = moe_out;
   return launch_moe_ffn(a, (hipStream_t)stream);
+}
+
+// ---- device-side timeline (E4B_TRACE builds) -------------------------------------
+#include "trace.h"
+
+static std::vector<TraceBinder>& trace_binders() {
+  static std::vector<TraceBinder> v;
+  return v;
+}
+bool trace_register(TraceBinder b) {
+  trace_binders().push_back(b);
+  return true;
+}
+static_assert(sizeof(TraceRec) == sizeof(e4b_trace_rec), "trace record layout");
+static TraceRec* g_tr_host_buf = nullptr;
+static unsigned* g_tr_host_cnt = nullptr;
+static size_t g_tr_host_cap = 0;
+
+static int trace_bind_all(TraceRec* buf, unsigned* cnt, unsigned cap) {
+  for (TraceBinder b : trace_binders())
+    if (b(buf, cnt, cap)) return e4b_fail(E4B_EHIP, "trace: binding a unit's trace buffer failed");
+  return E4B_OK;
+}
+
+extern "C" int e4b_trace_start(size_t cap) {
+#ifndef E4B_TRACE
+  (void)cap;
+  return e4b_fail(E4B_EINVAL, "e4b_trace_start: this library was built without E4B_TRACE (use libe4b_trace.so)");
+#else
+  if (cap < kTraceXcds || cap > (1u << 26)) return e4b_fail(E4B_EINVAL, "e4b_trace_start: capacity %zu", cap);
+  int rc = e4b_trace_stop();
+  if (rc) return rc;
+  // one segment of cap / 8 records per XCD, one counter per segment
+  E4B_HIP(hipMalloc(&g_tr_host_buf, cap * sizeof(TraceRec)));
+  E4B_HIP(hipMalloc(&g_tr_host_cnt, kTraceXcds * kTraceCntStride * sizeof(unsigned)));
+  E4B_HIP(hipMemset(g_tr_host_cnt, 0, kTraceXcds * kTraceCntStride * sizeof(unsigned)));
+  g_tr_host_cap = cap / kTraceXcds;
+  E4B_HIP(hipDeviceSynchronize());
+  return trace_bind_all(g_tr_host_buf, g_tr_host_cnt, (unsigned)g_tr_host_cap);
+#endif
+}
+
+extern "C" int e4b_trace_read(e4b_trace_rec* out, size_t cap, size_t* recorded) {
+  if (!g_tr_host_buf) return e4b_fail(E4B_ESTATE, "e4b_trace_read: no trace running");
+  if (!recorded || (cap && !out)) return e4b_fail(E4B_EINVAL, "e4b_trace_read: null output");
+  E4B_HIP(hipDeviceSynchronize());
+  unsigned n[kTraceXcds * kTraceCntStride];
+  E4B_HIP(hipMemcpy(n, g_tr_host_cnt, sizeof(n), hipMemcpyDeviceToHost));
+  size_t total = 0, put = 0;
+  for (int x = 0; x < kTraceXcds; ++x) {
+    const size_t nx = n[x * kTraceCntStride];
+    total += nx;
+    const size_t m = std::min(std::min(nx, g_tr_host_cap), cap - put);
+    if (m) E4B_HIP(hipMemcpy(out + put, g_tr_host_buf + x * g_tr_host_cap, m * sizeof(TraceRec), hipMemcpyDeviceToHost));
+    put += m;
+  }
+  *recorded = total;
+  return E4B_OK;
+}
+
+extern "C" int e4b_trace_stop(void) {
+  if (!g_tr_host_buf) return E4B_OK;
+  E4B_HIP(hipDeviceSynchronize());
+  int rc = trace_bind_all(nullptr, nullptr, 0);
+  (void)hipFree(g_tr_host_buf);
+  (void)hipFree(g_tr_host_cnt);
+  g_tr_host_buf = nullptr;
+  g_tr_host_cnt = nullptr;
+  g_tr_host_cap = 0;
+  return rc;
+}
+
+extern "C" int e4b_trace_clock_khz(int* khz) {
+  if (!khz) return e4b_fail(E4B_EINVAL, "e4b_trace_clock_khz: null");
+  int dev = 0;
+  E4B_HIP(hipGetDevice(&dev));
+  E4B_HIP(hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev));
+  return E4B_OK;
 }

@@ -23,6 +23,7 @@ struct AttnLaunch {
   int slots;               // ring slots (sliding) or capacity (global)
   int window;              // sliding window; 0 = global layer (linear cache)
   int chunk;               // positions per split-K chunk: 32 or 64
+  int vslices = 4;         // V-dim slices per chunk (blocks per chunk): 4 (4 waves each) or 2 (8 waves each)
   bool combine;            // also launch the combine (false: the o projection's prologue merges)
   float eps;
 };

@@ -11,7 +11,9 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "libe4b.so"))
+# E4B_LIBRARY names another build of the same library (libe4b_trace.so, the
+# device-side timeline build); by default the in-tree libe4b.so
+LIB_PATH = os.path.normpath(os.environ.get("E4B_LIBRARY") or os.path.join(_HERE, "..", "libe4b.so"))
 
 E4B_OK = 0
 E4B_EINVAL = -1
@@ -103,9 +105,15 @@ SIGNATURES = [
     ("e4b_prefill_steps", _i32, [_vp, _vp, _u32, _vp]),
     ("e4b_profile_step", _i32, [_vp, _u32, _u32, _vp, _i32]),
     ("e4b_profile_prefill", _i32, [_vp, _vp, _u32, _vp, _i32]),
+    ("e4b_trace_start", _i32, [_sz]),
+    ("e4b_trace_read", _i32, [_vp, _sz, _P(_sz)]),
+    ("e4b_trace_stop", _i32, []),
+    ("e4b_trace_clock_khz", _i32, [_P(_i32)]),
     ("e4b_decode", _i32, [_vp, _u32, _u32, _vp]),
     ("e4b_argmax", _i32, [_vp, _vp]),
     ("e4b_read_hidden", _i32, [_vp, _vp]),
+    ("e4b_read_layer_hidden", _i32, [_vp, _i32, _vp]),
+    ("e4b_read_topk", _i32, [_vp, _i32, _vp, _vp]),
     ("e4b_read_logits", _i32, [_vp, _vp]),
     ("e4b_read_kv", _i32, [_vp, _i32, _vp, _vp]),
     ("e4b_kv_slots", _i32, [_vp, _i32]),
@@ -144,7 +152,7 @@ class ProfEntryC(C.Structure):
 FLAG_NO_GRAPH = 1
 FLAG_STEP_PREFILL = 2
 FLAG_KV_SCORE = 4
-FLAG_PERSISTENT = 8
+FLAG_LAYER_HIDDEN = 16
 
 
 class MoeWeightsC(C.Structure):

@@ -353,6 +353,20 @@ class Engine:
         check(lib.e4b_read_hidden(self.ctx, _p(out)), "e4b_read_hidden")
         return out
 
+    def read_layer_hidden(self, layer: int) -> np.ndarray:
+        """The residual stream after `layer` in the last decode step."""
+        out = np.empty(self.cfg.hidden, np.float32)
+        check(lib.e4b_read_layer_hidden(self.ctx, int(layer), _p(out)), "e4b_read_layer_hidden")
+        return out
+
+    def read_topk(self, layer: int):
+        """A4B recipe: (expert ids [8], router weights [8]) of `layer` in the
+        last decode step."""
+        idx = np.empty(8, np.uint32)
+        w = np.empty(8, np.float32)
+        check(lib.e4b_read_topk(self.ctx, int(layer), _p(idx), _p(w)), "e4b_read_topk")
+        return idx, w
+
     def read_logits(self) -> np.ndarray:
         out = np.empty(self.cfg.vocab, np.float32)
         check(lib.e4b_read_logits(self.ctx, _p(out)), "e4b_read_logits")

@@ -295,7 +295,8 @@ typedef struct e4b_config {
   float eps;              /* 1e-6 */
   float softcap;          /* 30 (0 = none) */
   const uint8_t* layer_global; /* [layers] 1 = global; NULL = (i % 5 == 4) */
-  int32_t attn_chunk;     /* positions per split-K attention chunk: 32 or 64, 0 = 64 */
+  int32_t attn_chunk;     /* E4B recipe: positions per split-K attention chunk of the full layers, 32 or
+                           * 64 (0 = 64); the sliding layers use 32 unless attn_chunk is 64 */
   int32_t max_prompt;     /* prompt buffer capacity, 0 = max_seq */
   uint32_t flags;         /* E4B_FLAG_* */
   /* E4B_RECIPE_A4B (src/engine-a4b.js:100-116): the model loadEngineA4B
@@ -303,8 +304,9 @@ typedef struct e4b_config {
    * with their own head dim and rotated pairs and V = K.  Supported: hidden
    * a multiple of 256 up to 3072, head_dim 256, head_dim_full 256 or 512,
    * 1, 2, 4 or 8 q heads per KV head on every layer, ffn and expert_ffn
-   * multiples of 32 (<= 3072, <= 768), 8..256 experts, ple_dim 0; not with
-   * E4B_FLAG_PERSISTENT.  e4b_prefill runs the
+   * multiples of 32 (<= 3072, <= 768), 8..256 experts, ple_dim 0, and
+   * max_seq <= 16384 (the full layers' merge holds 256 chunks of 64
+   * positions).  e4b_prefill runs the
    * batched prefill of src/engine-a4b.js:465-584 (chunks of up to 512
    * tokens, ring - window + 1 at most). */
   int32_t recipe;              /* E4B_RECIPE_E4B (0) or E4B_RECIPE_A4B (1) */
@@ -330,14 +332,13 @@ typedef struct e4b_config {
  * score (attnos SCORE = 1, kernels/attnos.wgsl:78-92), which e4b_kv_compact
  * ranks; costs one small kernel per full layer and token */
 #define E4B_FLAG_KV_SCORE 4u
-/* run the step's layer loop as one persistent cooperative kernel (one
- * 512-thread block per CU for hidden / 8 blocks; the layers' phases hand
- * their vectors over through tagged words in device memory) instead of six
- * launches per layer; same results within the engine's tolerances.  Needs
- * ple_dim 256, hidden <= 2048, 4 q heads per KV head with q_heads * 256 <=
- * 2048, ffn <= 16384, and not E4B_FLAG_KV_SCORE; e4b_finalize fails
- * otherwise */
-#define E4B_FLAG_PERSISTENT 8u
+/* keep the residual stream after every layer of the last decode step for
+ * e4b_read_layer_hidden (one extra store of the hidden state per layer) */
+#define E4B_FLAG_LAYER_HIDDEN 16u
+/* the flags e4b_create accepts; any other bit is an error (bit 8 named a
+ * persistent layer loop that measured slower than the kernel chain and was
+ * removed) */
+#define E4B_FLAGS_KNOWN (E4B_FLAG_NO_GRAPH | E4B_FLAG_STEP_PREFILL | E4B_FLAG_KV_SCORE | E4B_FLAG_LAYER_HIDDEN)
 
 /* tensor names follow the GGUF naming of the E4B family:
  *   token_embd.weight (Q6_K [vocab][hidden], tied lm-head), output_norm.weight,
@@ -377,6 +378,18 @@ int  e4b_prefill_steps(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* 
 int  e4b_decode(e4b_ctx* ctx, uint32_t start_pos, uint32_t count, uint32_t* tokens_out);
 int  e4b_argmax(e4b_ctx* ctx, uint32_t* token_out);     /* argmaxFast: last step's argmax */
 int  e4b_read_hidden(e4b_ctx* ctx, float* out);         /* hidden state after the last layer */
+/* The residual stream after `layer` in the last decode step (e4b_step, or
+ * the last token of e4b_decode; readHidden, src/engine-a4b.js:850-852, per
+ * layer: the per-layer state the resident harness's `stats` mode reports,
+ * resident-a4b.html:96-101).  f32 [hidden]; the last layer's equals
+ * e4b_read_hidden.  Needs E4B_FLAG_LAYER_HIDDEN for the layers before the
+ * last (E4B_ESTATE otherwise); a batched prefill does not update it. */
+int  e4b_read_layer_hidden(e4b_ctx* ctx, int layer, float* out);
+/* A4B recipe: the top-8 experts (in slot order) and their router weights
+ * (softmax over the layer's experts, renormalised over the 8, times the
+ * per-expert scale; kernels/routertop.wgsl:19-71) that `layer` used in the
+ * last decode step.  E4B_EINVAL on the E4B recipe. */
+int  e4b_read_topk(e4b_ctx* ctx, int layer, uint32_t* idx, float* w);
 int  e4b_read_logits(e4b_ctx* ctx, float* out);         /* last step's logits [vocab] */
 int  e4b_read_kv(e4b_ctx* ctx, int layer, uint16_t* k_out, uint16_t* v_out); /* [kvh][slots][hd] f16 */
 int  e4b_kv_slots(e4b_ctx* ctx, int layer);             /* slots of that layer's cache */
@@ -403,6 +416,34 @@ typedef struct e4b_prof_entry {
 } e4b_prof_entry;
 int  e4b_profile_step(e4b_ctx* ctx, uint32_t token, uint32_t pos, e4b_prof_entry* out, int cap);
 int  e4b_profile_prefill(e4b_ctx* ctx, const uint32_t* ids, uint32_t n, e4b_prof_entry* out, int cap);
+
+/* Device-side timeline (the same per-dispatch ranking as profileStep,
+ * src/engine-a4b.js:707-741, taken inside a captured hipGraph replay, which
+ * event-based timing cannot see).  Only a library built with E4B_TRACE
+ * (libe4b_trace.so, make target `trace`) records; the product library
+ * returns E4B_EINVAL from e4b_trace_start.  While a trace runs, every
+ * workgroup of every decode-step kernel writes one record: the chip's
+ * real-time counter (e4b_trace_clock_khz ticks per ms) at its first
+ * instruction and when its wave 0 exits, the kernel tag (family << 16 |
+ * variant), its linear workgroup index, wave 0's HW_ID and XCC_ID
+ * registers, and up to four phase marks inside the kernel (the GEMV: weight
+ * loads issued, input vector ready, dot products done, rows reduced; the
+ * attention: loads issued, head prep done, scores done, P.V done).  e4b_trace_start(cap) allocates room for cap records (cap / 8
+ * per XCD) and clears the counts; e4b_trace_read copies up to `cap` records
+ * (device-synchronising first; grouped by XCD, not in time order) and
+ * returns the number recorded, which may exceed what fit (the excess is
+ * dropped); e4b_trace_stop detaches and frees the buffer. */
+typedef struct e4b_trace_rec {
+  uint64_t t0, t1;
+  uint32_t tag, blk;
+  uint32_t hw_id, xcc;
+  uint32_t mark[4];  /* wave 0's phase marks (ticks after t0; 0 = none) */
+  uint32_t pad[4];
+} e4b_trace_rec;
+int  e4b_trace_start(size_t cap);
+int  e4b_trace_read(e4b_trace_rec* out, size_t cap, size_t* recorded);
+int  e4b_trace_stop(void);
+int  e4b_trace_clock_khz(int* khz);
 
 /* Full-layer KV budget.  Full (global) layers count their cache entries
  * apart from positions (kvCount, src/engine-a4b.js:217; CACHEMODE 2): the

@@ -268,3 +268,49 @@ def test_native_gguf_config_a4b(tmp_path):
         gguf_config(str(tmp_path / "topk.gguf"))
     with pytest.raises(ValueError, match="expert_used_count"):
         config_from_kv(bad)
+
+
+def test_create_validates_before_any_device_call():
+    # e4b_create checks the configuration before its first HIP call: unknown
+    # flag bits, and an A4B context longer than the full layers' attention
+    # merge holds (256 chunks of 64 positions), are refused with E4B_EINVAL
+    from e4b.engine import Engine
+    from e4b.model import a4b_config, tiny_config
+    with pytest.raises(_lib.E4BError, match="unknown flags 0x400"):
+        Engine(tiny_config(flags=1 << 10))
+    with pytest.raises(_lib.E4BError, match="max_seq beyond 16384"):
+        Engine(a4b_config(max_seq=16385))
+
+
+def test_trace_entry_points_need_the_trace_build():
+    # the product library has no device-side timeline: e4b_trace_start fails
+    # (before any device call) and names the build that has one
+    assert _lib.lib.e4b_trace_start(1 << 16) == _lib.E4B_EINVAL
+    assert "E4B_TRACE" in _lib.last_error()
+
+
+def test_timeline_splits_launches_and_names_tags():
+    # e4b.timeline's host logic on hand-made records: a launch is a maximal
+    # run of one tag in entry order; spans, gaps and per-token sums in us at
+    # a 100 MHz clock; tag names decode csrc/trace.h's variant bits
+    from e4b import timeline as tl
+    assert tl.tag_name((1 << 16) | (16 + 8) | (1 << 5) | (4 << 8) | (1 << 14)) == \
+        "q40 geglu r16 prologue H=4096 batched"
+    assert tl.tag_name((1 << 16) | (-1 + 8) | (1 << 8)) == "q40 f32 r2 attn-combine prologue"
+    assert tl.tag_name((2 << 16) | 1) == "attn global" and tl.tag_name(9 << 16 | 512) == "attn_gen hd512"
+    rec = np.zeros(7, tl.REC)
+    a, b = (1 << 16) | 8, (2 << 16)
+    # two tokens of [a x2 WGs, b x1 WG]; ticks of 10 ns
+    rows = [(0, 100, a), (5, 120, a), (220, 400, b), (1000, 1100, a), (1002, 1160, a), (1250, 1400, b),
+            (1400, 1500, b | 1)]
+    for r, (t0, t1, tag) in zip(rec, rows):
+        r["t0"], r["t1"], r["tag"] = t0, t1, tag
+    ls = tl.launches(rec)
+    assert [(l["tag"], l["wgs"], l["t0"], l["t1"]) for l in ls] == \
+        [(a, 2, 0, 120), (b, 1, 220, 400), (a, 2, 1000, 1160), (b, 1, 1250, 1400), (b | 1, 1, 1400, 1500)]
+    txt = tl.summarize(ls, 100_000, 2)
+    row_a = next(ln for ln in txt.splitlines() if ln.startswith("| q40 "))
+    # spans 1.2 and 1.6 us, gaps 0 and 6 us; median entry 0.025 / 0.02 us after the first,
+    # last exit 0.1 / 0.3 us after the median; per token (2.8 + 6.0) / 2
+    assert row_a.split(" | ")[1:8] == ["2", "1", "1.40", "3.00", "0.02", "0.20", "4.4 |"], row_a
+    assert "first entry to last exit 7.5 us" in txt
