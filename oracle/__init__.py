@@ -61,6 +61,11 @@ _sigs = {
     "orc_state_vrow": (_vp, [_vp, _i32]),
     "orc_state_kv_count": (_i64, [_vp]),
     "orc_state_route_margin": (C.c_double, [_vp]),
+    "orc_moe_ffn_f": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "orc_state_layer_hidden": (_vp, [_vp, _i32]),
+    "orc_state_layer_topk": (_vp, [_vp, _i32]),
+    "orc_state_layer_margin": (C.c_double, [_vp, _i32]),
+    "orc_state_force_topk": (None, [_vp, _i32, _vp]),
     "orc_state_score": (_vp, [_vp, _i32]),
     "orc_kv_keep": (_i64, [_vp, _i32, _i64, _i64, _i32, _i32, _vp]),
     "orc_kv_compact": (_i64, [_vp, _vp, _i32, _i32]),
@@ -237,8 +242,10 @@ class MoeC(C.Structure):
     ]
 
 
-def moe_ffn(m: dict, h: np.ndarray):
-    """m: dict of numpy arrays / ints keyed like orc_moe's fields."""
+def moe_ffn(m: dict, h: np.ndarray, force=None):
+    """m: dict of numpy arrays / ints keyed like orc_moe's fields.  force:
+    the top_k experts the expert slots use instead of the router's own picks
+    (weighted from the router's scores); the returned ids are then `force`."""
     keep = {}
 
     def arr(name, kind):
@@ -262,7 +269,11 @@ def moe_ffn(m: dict, h: np.ndarray):
     dense = np.zeros(H, np.float32)
     moe = np.zeros(H, np.float32)
     hout = np.zeros(H, np.float32)
-    _lib.orc_moe_ffn(C.byref(s), _p(h), _p(idx), _p(w), _p(dense), _p(moe), _p(hout))
+    if force is None:
+        _lib.orc_moe_ffn(C.byref(s), _p(h), _p(idx), _p(w), _p(dense), _p(moe), _p(hout))
+    else:
+        f = np.ascontiguousarray(np.asarray(force, np.uint32).reshape(K))
+        _lib.orc_moe_ffn_f(C.byref(s), _p(h), _p(f), None, _p(idx), _p(w), _p(dense), _p(moe), _p(hout), None)
     return idx, w, dense, moe, hout
 
 
@@ -396,6 +407,31 @@ class OracleModel:
         """A4B recipe: the smallest top-8 decision margin of the last step's
         layers, (8th - 9th largest router score) / max |score|."""
         return float(_lib.orc_state_route_margin(self._state))
+
+    def layer_hidden(self, layer: int) -> np.ndarray:
+        """The residual stream after `layer` in the last step (f32 [hidden])."""
+        p = _lib.orc_state_layer_hidden(self._state, int(layer))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (int(self.cfg["hidden"]),)).copy()
+
+    def layer_topk(self, layer: int) -> np.ndarray:
+        """A4B recipe: the oracle's own top-8 experts at `layer` in the last
+        step (before any forcing)."""
+        p = _lib.orc_state_layer_topk(self._state, int(layer))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint32)), (8,)).copy()
+
+    def layer_margin(self, layer: int) -> float:
+        """A4B recipe: (8th - 9th router score) / max |score| at `layer`."""
+        return float(_lib.orc_state_layer_margin(self._state, int(layer)))
+
+    def force_topk(self, layer: int, idx=None) -> None:
+        """A4B recipe: the next steps' expert slots at `layer` use the 8
+        experts `idx` (weighted from the oracle's own router scores), or the
+        oracle's own picks again when idx is None."""
+        if idx is None:
+            _lib.orc_state_force_topk(self._state, int(layer), None)
+        else:
+            a = np.ascontiguousarray(np.asarray(idx, np.uint32).reshape(8))
+            _lib.orc_state_force_topk(self._state, int(layer), _p(a))
 
     def set_keep_rows(self, on: bool) -> None:
         """With keep_rows the step attends to the K/V row handed over (set_kv)

@@ -553,6 +553,17 @@ void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* to
 
 void orc_moe_ffn_m(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
                    float* dense_out, float* moe_out, float* h_out, double* margin) {
+  orc_moe_ffn_f(m, h, NULL, NULL, topk_idx, topk_w, dense_out, moe_out, h_out, margin);
+}
+
+/* force_idx != NULL: the expert slots use those K experts instead of the     */
+/* oracle's own top-K (a test hands over the GPU's picks at a routing near-   */
+/* tie), weighted as routertop weights its picks: softmax probability over   */
+/* all E scores, renormalised over the K, times pes (kernels/routertop.wgsl:  */
+/* 19-71); own_idx (may be NULL) receives the oracle's own top-K.           */
+void orc_moe_ffn_f(const orc_moe* m, const float* h, const uint32_t* force_idx, uint32_t* own_idx,
+                   uint32_t* topk_idx, float* topk_w, float* dense_out, float* moe_out, float* h_out,
+                   double* margin) {
   const int H = m->hidden, E = m->n_experts, K = m->top_k, FF = m->expert_ffn, FF2 = m->dense_ffn;
   float *xd = malloc(sizeof(float) * H), *xr = malloc(sizeof(float) * H), *xm = malloc(sizeof(float) * H);
   double inv = rms_inv(h, H, m->eps);
@@ -566,6 +577,18 @@ void orc_moe_ffn_m(const orc_moe* m, const float* h, uint32_t* topk_idx, float* 
   float* sc = malloc(sizeof(float) * E);
   orc_router_topk(xr, m->router_w, m->pes, H, E, K, topk_idx, topk_w, sc);
   if (margin) *margin = route_margin_of(sc, E, K);
+  if (own_idx) memcpy(own_idx, topk_idx, sizeof(uint32_t) * (size_t)K);
+  if (force_idx) {
+    double mx = -3.0e38, sum = 0.0, wsum = 0.0, wk[64];
+    for (int e = 0; e < E; ++e) mx = sc[e] > mx ? sc[e] : mx;
+    for (int e = 0; e < E; ++e) sum += exp((double)sc[e] - mx);
+    for (int k = 0; k < K; ++k) {
+      topk_idx[k] = force_idx[k];
+      wk[k] = exp((double)sc[force_idx[k]] - mx) / sum;
+      wsum += wk[k];
+    }
+    for (int k = 0; k < K; ++k) topk_w[k] = (float)(wk[k] / wsum * (double)m->pes[topk_idx[k]]);
+  }
   free(sc);
 
   /* dense branch: gate rows [0,FF2), up rows [FF2,2FF2) */
@@ -620,7 +643,7 @@ void orc_moe_ffn_m(const orc_moe* m, const float* h, uint32_t* topk_idx, float* 
 /* slot's normalised attention weight to score[l][h][slot] in f32 (attnos    */
 /* SCORE = 1, kernels/attnos.wgsl:78-92).                                   */
 struct orc_state {
-  int layers;
+  int layers, hidden;
   uint16_t** kc;
   uint16_t** vc;
   float* ple; /* [layers][ple_dim] per-layer inputs of the current token */
@@ -638,6 +661,15 @@ struct orc_state {
   /* A4B recipe: the smallest top-8 decision margin of the last step's      */
   /* layers ((8th - 9th router score) / max |score|; orc_moe_ffn_m)        */
   double route_margin;
+  /* per layer of the last step: the residual stream after the layer        */
+  /* ([layers][hidden]); A4B: the oracle's own top-8 ([layers][8]), its     */
+  /* decision margin, and the experts a test forces on that layer (force[l] */
+  /* set: used instead of the own picks)                                    */
+  float* lh;
+  uint32_t* ltopk;
+  double* lmargin;
+  uint32_t* lforce;
+  uint8_t* forced;
 };
 
 static int64_t slots_of(const orc_model* m, int l) {
@@ -665,6 +697,7 @@ static int64_t row_max(const orc_model* m) {
 orc_state* orc_state_new(const orc_model* m) {
   orc_state* s = calloc(1, sizeof(orc_state));
   s->layers = m->layers;
+  s->hidden = m->hidden;
   s->kc = calloc((size_t)m->layers, sizeof(uint16_t*));
   s->vc = calloc((size_t)m->layers, sizeof(uint16_t*));
   for (int l = 0; l < m->layers; ++l) {
@@ -676,6 +709,11 @@ orc_state* orc_state_new(const orc_model* m) {
   s->krow = calloc((size_t)m->layers * row_max(m), sizeof(uint16_t));
   s->vrow = calloc((size_t)m->layers * row_max(m), sizeof(uint16_t));
   s->row_stride = row_max(m);
+  s->lh = calloc((size_t)m->layers * m->hidden, sizeof(float));
+  s->ltopk = calloc((size_t)m->layers * 8, sizeof(uint32_t));
+  s->lmargin = calloc((size_t)m->layers, sizeof(double));
+  s->lforce = calloc((size_t)m->layers * 8, sizeof(uint32_t));
+  s->forced = calloc((size_t)m->layers, 1);
   s->score = calloc((size_t)m->layers, sizeof(float*));
   for (int l = 0; l < m->layers; ++l)
     if (m->layer_global[l]) s->score[l] = calloc((size_t)m->q_heads * m->max_seq, sizeof(float));
@@ -694,6 +732,11 @@ void orc_state_free(orc_state* s) {
   free(s->vrow);
   for (int l = 0; l < s->layers; ++l) free(s->score[l]);
   free(s->score);
+  free(s->lh);
+  free(s->ltopk);
+  free(s->lmargin);
+  free(s->lforce);
+  free(s->forced);
   free(s);
 }
 void orc_state_set_scoring(orc_state* s, int on) { s->scoring = on; }
@@ -702,6 +745,13 @@ const uint16_t* orc_state_krow(const orc_state* s, int layer) { return s->krow +
 const uint16_t* orc_state_vrow(const orc_state* s, int layer) { return s->vrow + (size_t)layer * s->row_stride; }
 int64_t orc_state_kv_count(const orc_state* s) { return s->kv_count; }
 double orc_state_route_margin(const orc_state* s) { return s->route_margin; }
+const float* orc_state_layer_hidden(const orc_state* s, int layer) { return s->lh + (size_t)layer * s->hidden; }
+const uint32_t* orc_state_layer_topk(const orc_state* s, int layer) { return s->ltopk + (size_t)layer * 8; }
+double orc_state_layer_margin(const orc_state* s, int layer) { return s->lmargin[layer]; }
+void orc_state_force_topk(orc_state* s, int layer, const uint32_t* idx) {
+  s->forced[layer] = idx != NULL;
+  if (idx) memcpy(s->lforce + (size_t)layer * 8, idx, sizeof(uint32_t) * 8);
+}
 const float* orc_state_score(const orc_state* s, int layer) { return s->score[layer]; }
 
 /* compactAll's selection (src/engine-a4b.js:587-617) for one full layer:    */
@@ -851,7 +901,9 @@ static void a4b_layer(const orc_model* m, orc_state* st, int l, float* h, uint32
   uint32_t idx[64];
   float w[64];
   double mg = INFINITY;
-  orc_moe_ffn_m(&ly->moe, h, idx, w, dn, mo, ho, &mg);
+  orc_moe_ffn_f(&ly->moe, h, st->forced[l] ? st->lforce + (size_t)l * 8 : NULL, st->ltopk + (size_t)l * 8, idx, w,
+                dn, mo, ho, &mg);
+  st->lmargin[l] = mg;
   if (mg < st->route_margin) st->route_margin = mg;
   memcpy(h, ho, sizeof(float) * H);
   free(x); free(qkv); free(qp); free(ao); free(a); free(o); free(inv); free(dn); free(mo); free(ho);
@@ -905,6 +957,7 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
   for (int l = 0; l < L; ++l) {
     if (m->recipe == 1) {
       a4b_layer(m, st, l, h, pos, kv);
+      memcpy(st->lh + (size_t)l * H, h, sizeof(float) * H);
       continue;
     }
     const orc_layer* ly = &m->L[l];
@@ -975,6 +1028,7 @@ uint32_t orc_step(const orc_model* m, orc_state* st, uint32_t token, uint32_t po
     } else {
       for (int i = 0; i < H; ++i) h[i] = (float)((double)h[i] * (double)ly->layer_scale);
     }
+    memcpy(st->lh + (size_t)l * H, h, sizeof(float) * H);
   }
   if (hidden_out) memcpy(hidden_out, h, sizeof(float) * H);
 

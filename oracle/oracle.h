@@ -98,6 +98,9 @@ void orc_moe_ffn(const orc_moe* m, const float* h, uint32_t* topk_idx, float* to
  * (K+1)-th largest router score, over max |score|) when margin != NULL */
 void orc_moe_ffn_m(const orc_moe* m, const float* h, uint32_t* topk_idx, float* topk_w,
                    float* dense_out, float* moe_out, float* h_out, double* margin);
+void orc_moe_ffn_f(const orc_moe* m, const float* h, const uint32_t* force_idx, uint32_t* own_idx,
+                   uint32_t* topk_idx, float* topk_w, float* dense_out, float* moe_out, float* h_out,
+                   double* margin);
 
 /* ---- full E4B-shaped decode step --------------------------------------- */
 typedef struct {
@@ -155,6 +158,13 @@ const uint16_t* orc_state_vrow(const orc_state* s, int layer);
 int64_t    orc_state_kv_count(const orc_state* s);
 /* A4B recipe: the smallest top-8 decision margin over the last step's layers */
 double     orc_state_route_margin(const orc_state* s);
+/* per layer of the last step: the residual stream after the layer; A4B: the */
+/* oracle's own top-8 and decision margin; force_topk(idx) makes the layer's */
+/* expert slots use idx[8] (NULL: the oracle's own picks again)             */
+const float*    orc_state_layer_hidden(const orc_state* s, int layer);
+const uint32_t* orc_state_layer_topk(const orc_state* s, int layer);
+double          orc_state_layer_margin(const orc_state* s, int layer);
+void            orc_state_force_topk(orc_state* s, int layer, const uint32_t* idx);
 const float* orc_state_score(const orc_state* s, int layer);
 int64_t    orc_kv_keep(const float* score, int qh, int64_t scap, int64_t n, int budget, int protect,
                        uint32_t* keep);

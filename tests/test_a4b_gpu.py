@@ -75,10 +75,29 @@ def _f16(a):
     return a.view(np.float16).astype(np.float64)
 
 
-def synced_steps(eng, om, osync, cfg, tokens, start):
+def _resync(eng, o, cfg, kv):
+    """Hand the GPU's caches and full-layer entry count to oracle state `o`."""
+    for layer in range(cfg.layers):
+        kg, vg = eng.read_kv(layer)
+        o.set_kv(layer, kg.transpose(1, 0, 2), vg.transpose(1, 0, 2))
+    o.set_kv_count(kv)
+
+
+def synced_steps(eng, om, osync, cfg, tokens, start, max_route_frac=0.5):
     """Host-fed steps at positions start, start + 1, ...; every step compared
-    with the synced and the free-running oracle.  Returns the per-step
-    (synced error of range, free error of range) and the near-ties."""
+    with the synced and the free-running oracle.
+
+    The synced oracle starts each step from the GPU's caches (the current
+    token's rows kept) and routes every layer to the GPU's own top-8
+    (e4b_read_topk; weighted from the oracle's own router scores), so every
+    step must meet SYNC_TOL -- there is no exemption.  A layer whose picks
+    differ from the oracle's own top-8 must be a routing near-tie there (the
+    oracle's decision margin at that layer below ROUTE_TIE); such steps are
+    counted ("route" ties) and capped at max_route_frac of the steps.  The
+    free-running oracle is compared at every step where its experts agree
+    with the GPU's; after a step where they do not (a near-tie within its
+    drift) it restarts from the GPU's caches, so the comparison continues.  Returns the per-step (synced error of range, free
+    error of range) and the near-ties."""
     osync.set_keep_rows(True)
     out, ties = [], []
     for k, t in enumerate(tokens):
@@ -86,43 +105,60 @@ def synced_steps(eng, om, osync, cfg, tokens, start):
         kv = eng.kv_count()  # the full layers' slot of this token (its position until a compaction)
         g, lg = eng.step(int(t), pos, want_logits=True)
         o_tok, o_lg, _ = om.step(int(t), pos, want_logits=True)
+        picks = [eng.read_topk(layer)[0] for layer in range(cfg.layers)]
         rows = []
         for layer in range(cfg.layers):
             kg, vg = eng.read_kv(layer)
             osync.set_kv(layer, kg.transpose(1, 0, 2), vg.transpose(1, 0, 2))
             slot = kv if cfg.layer_global[layer] else pos % kg.shape[1]
             rows.append((kg[:, slot, :], vg[:, slot, :]))
+            osync.force_topk(layer, picks[layer])
         osync.set_kv_count(kv)
         s_tok, s_lg, s_h = osync.step(int(t), pos, want_logits=True, want_hidden=True)
-        margin = osync.route_margin()
+        differ = []
+        for layer in range(cfg.layers):
+            own = osync.layer_topk(layer)
+            if set(own.tolist()) != set(picks[layer].tolist()):
+                margin = osync.layer_margin(layer)
+                assert margin < ROUTE_TIE, (f"pos {pos} layer {layer}: GPU experts {sorted(picks[layer].tolist())} vs "
+                                            f"oracle {sorted(own.tolist())} at decision margin {margin:.2e}")
+                differ.append(layer)
         d = np.abs(lg.astype(np.float64) - s_lg)
         sr = float(d.max() / (s_lg.max() - s_lg.min()))
         fr = float(np.abs(lg.astype(np.float64) - o_lg).max() / (o_lg.max() - o_lg.min()))
         herr = float(np.abs(eng.read_hidden() - s_h).max() / (s_h.max() - s_h.min()))
-        routed = False
-        if not (sr < SYNC_TOL and herr < SYNC_TOL):
-            # only a routing near-tie may move the step this far
-            assert margin < ROUTE_TIE, f"pos {pos}: synced logits {sr:.2e}, hidden {herr:.2e}, route margin {margin:.2e}"
-            ties.append((pos, "route"))
-            routed = True
-        # the free-running oracle is compared until the first routing near-tie
-        # (after it the two may hold different experts' rows)
-        if not any(kind == "route" for _, kind in ties):
-            assert fr < DRIFT_TOL, f"pos {pos}: free-running logits {fr:.2e}"
-        if routed:
-            out.append((sr, fr))
-            continue
+        assert sr < SYNC_TOL and herr < SYNC_TOL, f"pos {pos}: synced logits {sr:.2e}, hidden {herr:.2e}"
         if g != s_tok:
             assert top2_margin(s_lg) < TIE_TOL * np.abs(s_lg).max(), f"pos {pos}: gpu {g} vs synced oracle {s_tok}"
             ties.append((pos, "synced"))
-        if g != o_tok:
-            assert top2_margin(o_lg) <= 2 * float(np.abs(lg.astype(np.float64) - o_lg).max()), f"pos {pos}: free"
-            ties.append((pos, "free"))
         for layer, (kg, vg) in enumerate(rows):
             for a, b in zip((kg, vg), osync.rows(layer)):
                 e = np.abs(_f16(a) - _f16(b)).max() / np.abs(_f16(b)).max()
                 assert e <= (2.0 ** -9 if layer == 0 else KV_MAX_TOL), f"pos {pos} layer {layer}: new row {e:.2e}"
+        if differ:
+            ties.append((pos, "route", tuple(differ)))
+        # the free-running oracle routed on its own (slightly drifted) state:
+        # where its experts agree with the GPU's everywhere its logits must be
+        # within the drift bound; a layer where they differ must be a near-tie
+        # within that drift, and the oracle then restarts from the GPU's state
+        # (it would hold other experts' rows from here on)
+        free_differ = [layer for layer in range(cfg.layers)
+                       if set(om.layer_topk(layer).tolist()) != set(picks[layer].tolist())]
+        if not free_differ:
+            assert fr < DRIFT_TOL, f"pos {pos}: free-running logits {fr:.2e}"
+            if g != o_tok:
+                assert top2_margin(o_lg) <= 2 * float(np.abs(lg.astype(np.float64) - o_lg).max()), f"pos {pos}: free"
+                ties.append((pos, "free"))
+        else:
+            for layer in free_differ:
+                assert om.layer_margin(layer) < DRIFT_TOL, (f"pos {pos} layer {layer}: free-running experts differ at "
+                                                            f"margin {om.layer_margin(layer):.2e}")
+            ties.append((pos, "free-route", tuple(free_differ)))
+            _resync(eng, om, cfg, kv + 1)
         out.append((sr, fr))
+    routed = sum(1 for tie in ties if tie[1] == "route")
+    print(f"synced steps: {len(tokens)} checked against the synced oracle, {routed} with a routing near-tie")
+    assert routed <= max_route_frac * len(tokens), f"{routed} of {len(tokens)} steps are routing near-ties"
     return np.array(out), ties
 
 
@@ -244,19 +280,26 @@ def test_a4b_gguf_loaders_and_js_host_agree(tmp_path):
     assert {"gemm_qkv", "headprep_rows", "attn_rows", "gemm_o", "moe_prefill"} <= roles
 
 
-def _prefill_synced(eng, om, osync, cfg, prompt):
+def _prefill_synced(eng, om, osync, cfg, prompt, positions=None, prefilled=False):
     """After eng.prefill(prompt) (every position inside the caches): each
-    prompt token m stepped by the synced oracle on the GPU's caches (entry
-    count m, the token's own rows kept), its new K/V rows against the GPU's
-    rows of position m, the last token's logits and hidden state against the
-    GPU's; the free-running oracle follows the prompt.  Returns the last
-    synced step's error of range."""
-    g = eng.prefill(prompt)
+    prompt token m (of `positions`, default all; the last always) stepped by
+    the synced oracle on the GPU's caches (entry count m, the token's own rows
+    kept), its new K/V rows against the GPU's rows of position m, the last
+    token's logits and hidden state against the GPU's; the free-running
+    oracle (unless None) follows the prompt.  With prefilled the engine
+    already holds the prompt.  Returns the last synced step's error of
+    range."""
+    g = eng.argmax_fast() if prefilled else eng.prefill(prompt)
     caches = [eng.read_kv(layer) for layer in range(cfg.layers)]
     osync.set_keep_rows(True)
     n = len(prompt)
+    excused = 0
+    check_at = set(range(n)) if positions is None else set(positions) | {n - 1}
     for m, t in enumerate(prompt):
-        om.step(int(t), m)
+        if om is not None:
+            om.step(int(t), m)
+        if m not in check_at:
+            continue
         for layer, (kg, vg) in enumerate(caches):
             osync.set_kv(layer, kg.transpose(1, 0, 2), vg.transpose(1, 0, 2))
         osync.set_kv_count(m)
@@ -270,14 +313,21 @@ def _prefill_synced(eng, om, osync, cfg, prompt):
                 if e > (2.0 ** -9 if layer == 0 else KV_MAX_TOL):
                     bad.append((layer, e))
         if bad:
-            # rows past a layer whose expert choice is a near-tie may differ
-            assert osync.route_margin() < ROUTE_TIE, f"token {m}: rows {bad}, route margin {osync.route_margin():.2e}"
+            # a layer's rows may differ only past a layer whose expert choice
+            # is a near-tie (the batched prefill's picks are not read back)
+            for layer, e in bad:
+                first_tie = min((j for j in range(layer) if osync.layer_margin(j) < ROUTE_TIE), default=None)
+                assert first_tie is not None, (f"token {m} layer {layer}: row err {e:.2e} with no routing near-tie "
+                                               f"in layers 0..{layer - 1}")
+            excused += 1
             assert not last, "the last prompt token's rows are compared with its logits"
     lg = eng.read_logits().astype(np.float64)
     sr = float(np.abs(lg - s_lg).max() / (s_lg.max() - s_lg.min()))
     herr = float(np.abs(eng.read_hidden() - s_h).max() / (s_h.max() - s_h.min()))
     assert sr < SYNC_TOL and herr < SYNC_TOL, f"prefill: synced logits {sr:.2e}, hidden {herr:.2e}"
     assert g == s_tok or top2_margin(s_lg) < TIE_TOL * np.abs(s_lg).max(), f"prefill argmax {g} vs {s_tok}"
+    print(f"prefill synced: {len(check_at)} of {n} tokens checked, {excused} with rows past a routing near-tie")
+    assert excused <= 0.25 * len(check_at), f"{excused} of {len(check_at)} prompt tokens excused by routing near-ties"
     return sr
 
 
@@ -394,3 +444,60 @@ def test_a4b_generate_long_runs_the_schedule():
     out = a.generate_long(prompt, 40, eos=(), budget=16, protect=4, decap=24)
     assert len(out) == 40 and a.kv_count() <= 24
     assert b.generate_long(prompt, 40, eos=(), budget=16, protect=4, decap=24) == out
+
+
+def test_a4b_30_layer_prefill_then_synced_steps():
+    # the reference model's depth and shapes (src/engine-a4b.js:100-116: 30
+    # layers, hidden 2816, 16 q heads, sliding 8 KV heads x 256 with window
+    # 1024 in a 1536-slot ring, every sixth layer full with 2 KV heads x 512
+    # and V = K, dense FFN 2112 beside 128 experts of 704), a reduced
+    # vocabulary: a 512-token batched prefill, checked against the engine's
+    # token-by-token prefill on the same weights (caches within the KV
+    # tolerances, last logits within the drift bound), then 64 decode steps,
+    # each against the synced oracle (the GPU's caches and per-layer experts)
+    # within SYNC_TOL, the free-running oracle restarting from the GPU's state
+    # after the prefill and after any step whose experts differ from its own
+    import time
+
+    from e4b._lib import FLAG_STEP_PREFILL
+    t0 = time.time()
+    shape = dict(vocab=8192, max_seq=1024)
+    cfg = a4b_config(**shape)
+    tensors = norm_weights_random(synth_tensors(cfg, 131), 132)
+    tens = {n: t.data for n, t in tensors.items()}
+    eng = Engine(cfg, tensors)
+    prompt = np.random.default_rng(133).integers(0, cfg.vocab, 512)
+    g = eng.prefill(prompt)
+    ref = Engine(a4b_config(flags=FLAG_STEP_PREFILL, **shape), tensors)
+    gr = ref.prefill(prompt)
+    la, lb = eng.read_logits().astype(np.float64), ref.read_logits().astype(np.float64)
+    err = float(np.abs(la - lb).max() / (lb.max() - lb.min()))
+    print(f"A4B 30 layers: batched vs token-by-token prefill of 512: argmax {g}/{gr}, logits err {err:.2e} "
+          f"({time.time() - t0:.0f} s)", flush=True)
+    assert err < DRIFT_TOL and (g == gr or top2_margin(lb) < TIE_TOL * np.abs(lb).max())
+    worst = (0.0, -1)
+    for layer in range(cfg.layers):
+        for x, y in zip(eng.read_kv(layer), ref.read_kv(layer)):
+            fx, fy = _f16(x), _f16(y)
+            assert np.array_equal(np.any(x != 0, axis=(0, 2)), np.any(y != 0, axis=(0, 2))), f"layer {layer}: slots"
+            d = np.abs(fx - fy)
+            assert d.mean() <= KV_MEAN_TOL * np.abs(fy).mean(), f"layer {layer} cache (mean)"
+            worst = max(worst, (float(d.max() / np.abs(fy).max()), layer))
+    # (the two paths may route a token to other experts at a near-tie, which
+    # moves its later layers' rows past KV_MAX_TOL; rows are held to the
+    # oracle below, token by token with the near-tie attribution)
+    print(f"A4B 30 layers: batched vs token-by-token caches, worst row max err {worst[0]:.2e} (layer {worst[1]})")
+    ref.close()
+    om, osync = orc.OracleModel(cfg.as_dict(), tens), orc.OracleModel(cfg.as_dict(), tens)
+    # the batched prefill's own K/V rows of the last 16 prompt tokens against
+    # the synced oracle (each token from the GPU's caches), the last token's
+    # logits and hidden state too
+    _prefill_synced(eng, None, osync, cfg, prompt, positions=range(len(prompt) - 16, len(prompt)), prefilled=True)
+    osync = orc.OracleModel(cfg.as_dict(), tens)
+    _resync(eng, om, cfg, len(prompt))
+    forced = np.random.default_rng(134).integers(0, cfg.vocab, 64)
+    errs, ties = synced_steps(eng, om, osync, cfg, forced, len(prompt))
+    routed = [t for t in ties if t[1] == "route"]
+    print(f"A4B 30 layers: 64 synced steps, synced err of range median {np.median(errs[:, 0]):.2e} max "
+          f"{errs[:, 0].max():.2e}; free max {errs[:, 1].max():.2e}; {len(routed)} routing near-ties {routed}; "
+          f"other ties {[t for t in ties if t[1] != 'route']} ({time.time() - t0:.0f} s)")

@@ -148,3 +148,66 @@ def test_moe_prefill_rows(m, seed, random_norms):
             worst[name] = max(worst[name], err)
             assert err < tol, f"row {r} {name}: {err:.3e}"
     print(f"moe prefill m={m}: worst errors {worst}")
+
+
+# ---------------------------------------------------------------------------
+# slot pairing against the closed form (not the oracle): distinct one-hot
+# experts and a one-hot router (tests/closed_form.py), so a kernel that pairs
+# router weight k with the wrong slot's expert, or an expert's gate/up with
+# another expert's down, fails here even if the oracle shared the mistake
+# ---------------------------------------------------------------------------
+from closed_form import moe_pairing_case, moe_pairing_expected, moe_pairing_route  # noqa: E402
+
+PAIR_TOL = 2e-3  # of max |moe|: f16 rounding points of xm and the GeGLU output
+
+
+def _pairing_layer(seed):
+    m, sels = moe_pairing_case(seed=seed)
+    t = {k: m[k] for k in ("ffn_norm", "router_scale", "pre_ffw2", "router_w", "pes", "dense_gate", "dense_up",
+                           "dense_down", "exp_gate_up", "exp_down", "post_ffw1", "post_ffw2", "post_ffw")}
+    L = MoeLayer(m["hidden"], m["n_experts"], m["expert_ffn"], m["dense_ffn"], t, eps=m["eps"], layer_scale=1.0)
+    return m, sels, L
+
+
+def _check_pairing(m, sels, h, idx, w, moe, what):
+    top, wt, margin = moe_pairing_route(m, h)
+    assert margin > 1e-3, f"{what}: margin {margin:.2e}"
+    np.testing.assert_array_equal(idx, top, err_msg=what)
+    np.testing.assert_allclose(w, wt, rtol=1e-5, err_msg=what)
+    want = moe_pairing_expected(m, sels, h, top, wt)
+    tol = PAIR_TOL * np.abs(want).max()
+    err = float(np.abs(moe.astype(np.float64) - want).max())
+    assert err <= tol, f"{what}: moe err {err:.3e} > {tol:.3e}"
+    for mut in ("weights_rolled", "down_by_slot", "down_next"):
+        bad = moe_pairing_expected(m, sels, h, top, wt, mutant=mut)
+        assert float(np.abs(bad - moe).max()) > 100 * tol, f"{what}: mutant {mut} within 100x tolerance"
+    return err / np.abs(want).max()
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_moe_slot_pairing_decode_closed_form(seed):
+    m, sels, L = _pairing_layer(seed)
+    h = np.random.default_rng(50 + seed).standard_normal(m["hidden"]).astype(np.float32)
+    got = L.forward(h)
+    assert not np.any(got["dense_out"])
+    e = _check_pairing(m, sels, h, got["topk_idx"], got["topk_w"], got["moe_out"], f"decode seed {seed}")
+    print(f"pairing decode seed {seed}: moe err {e:.2e} of max, top-8 {got['topk_idx'].tolist()}")
+
+
+def test_moe_slot_pairing_prefill_closed_form():
+    # the expert-grouped prefill (counting sort by expert, grouped GEMMs,
+    # slot-ordered combine) over 24 rows with 24 different routings
+    m, sels, L = _pairing_layer(3)
+    rng = np.random.default_rng(77)
+    rows = []
+    while len(rows) < 24:
+        h = rng.standard_normal(m["hidden"]).astype(np.float32)
+        if moe_pairing_route(m, h)[2] > 1e-3:
+            rows.append(h)
+    hs = np.stack(rows)
+    got = L.prefill(hs)
+    worst = 0.0
+    for i, h in enumerate(hs):
+        worst = max(worst, _check_pairing(m, sels, h, got["topk_idx"][i], got["topk_w"][i], got["moe_out"][i],
+                                          f"prefill row {i}"))
+    print(f"pairing prefill: 24 rows, worst moe err {worst:.2e} of max")

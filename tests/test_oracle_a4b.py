@@ -280,3 +280,48 @@ def test_a4b_full_layer_mass_sums_to_the_scored_steps():
     keep = orc.kv_keep(om.score(full), 19, 10, 3)
     assert len(keep) == 10 and list(keep[-3:]) == [16, 17, 18]
     assert om.compact(10, 3) == 10 == om.kv_count()
+
+
+def test_layer_hidden_and_forced_routing():
+    # the oracle's per-layer readouts: the residual stream after each layer
+    # (the last one equals the step's hidden output; with every matrix zero a
+    # layer only scales h by its layer scalar, so after layer l it is
+    # emb * s_0 ... s_l in f32) and, on random weights, each layer's own
+    # top-8; forcing a layer to its own picks reproduces the step bit for
+    # bit, forcing another set changes it while layer_topk still reports the
+    # oracle's own picks
+    from e4b.model import norm_weights_random
+    cfg, tens = a4b_model(layer_global=(0, 1, 0), kvh=(2, 1, 2))
+    sc = [0.75, 1.25, 0.5]
+    for l, s in enumerate(sc):
+        set_scale(tens, l, s)
+    om = orc.OracleModel(cfg.as_dict(), tens)
+    _, _, hid = om.step(5, 0, want_hidden=True)
+    h = emb_row(cfg, tens, 5).astype(np.float32)
+    for l, s in enumerate(sc):
+        h = (h.astype(np.float64) * s).astype(np.float32)
+        np.testing.assert_array_equal(om.layer_hidden(l), h)
+    np.testing.assert_array_equal(om.layer_hidden(cfg.layers - 1), hid)
+
+    cfg = tiny_a4b_config()
+    tensors = norm_weights_random(synth_tensors(cfg, 21), 22)
+    tens = {n: t.data for n, t in tensors.items()}
+    a, b, c = (orc.OracleModel(cfg.as_dict(), tens) for _ in range(3))
+    toks = np.random.default_rng(23).integers(0, cfg.vocab, 6)
+    for p, t in enumerate(toks):
+        _, lga, _ = a.step(int(t), p, want_logits=True)
+        picks = [a.layer_topk(l) for l in range(cfg.layers)]
+        for l in range(cfg.layers):
+            b.force_topk(l, picks[l])
+        _, lgb, _ = b.step(int(t), p, want_logits=True)
+        np.testing.assert_array_equal(lgb, lga)
+        for l in range(cfg.layers):
+            np.testing.assert_array_equal(b.layer_topk(l), picks[l])
+        if p == 0:
+            # another expert in layer 0's eighth slot
+            swapped = picks[0].copy()
+            swapped[7] = next(e for e in range(cfg.n_experts) if e not in picks[0])
+            c.force_topk(0, swapped)
+            _, lgc, _ = c.step(int(t), p, want_logits=True)
+            assert np.abs(lgc - lga).max() > 0
+            np.testing.assert_array_equal(c.layer_topk(0), picks[0])

@@ -37,56 +37,7 @@ import pytest
 import oracle as orc
 from e4b.model import synth_tensors, tiny_config
 
-EPS = 0.05
-SQ12 = 0.70710678118654752
-
-
-def f16(a):
-    return np.asarray(a, np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
-
-
-def f32(a):
-    return np.asarray(a, np.float64).astype(np.float32).astype(np.float64)
-
-
-def rms(v, w=None, eps=EPS):
-    v = np.asarray(v, np.float64)
-    r = v / math.sqrt(float(np.mean(v * v)) + eps)
-    return r if w is None else r * np.asarray(w, np.float64)
-
-
-def gelu(g):
-    # kernels/q40gu.wgsl:114 (tanh form, argument clamped to +-20)
-    g = np.asarray(g, np.float64)
-    return 0.5 * g * (1.0 + np.tanh(np.clip(0.7978845608028654 * (g + 0.044715 * g ** 3), -20.0, 20.0)))
-
-
-def onehot_q40(rows, cols, sel, sign):
-    """q4_0 bytes of a matrix whose row r is sign[r] * e_{sel[r]} (d = 1)."""
-    nb = cols // 32
-    blk = np.zeros((rows, nb, 18), np.uint8)
-    blk[:, :, 1] = 0x3C  # f16 1.0, little endian
-    blk[:, :, 2:] = 0x88  # every nibble 8 -> value 0
-    for r in range(rows):
-        c = int(sel[r])
-        b, j = divmod(c, 32)
-        n = 9 if sign[r] > 0 else 7
-        if j < 16:
-            blk[r, b, 2 + j] = (blk[r, b, 2 + j] & 0xF0) | n
-        else:
-            blk[r, b, 2 + j - 16] = (blk[r, b, 2 + j - 16] & 0x0F) | (n << 4)
-    return blk.reshape(-1)
-
-
-def select(rows, cols, seed):
-    rng = np.random.default_rng(seed)
-    sel = rng.integers(0, cols, rows)
-    sign = np.where(rng.random(rows) < 0.5, -1.0, 1.0)
-    return sel, sign
-
-
-def gather(x, sel, sign):
-    return sign * np.asarray(x, np.float64)[sel]
+from closed_form import EPS, SQ12, f16, f32, gather, gelu, onehot_q40, rms, select  # noqa: F401
 
 
 def base_model(layers=1, ple=True, layer_global=None, emb_sigma=2e-4, seed=3):
@@ -556,3 +507,65 @@ def test_one_ulp_perturbation_jumps_at_f16_rounding_points():
           f"{jumps.max():.2e} of max |logit|")
     assert (jumps == 0).sum() >= jumps.size // 2
     assert jumps.max() > 100 * 2.0 ** -23
+
+
+# ---------------------------------------------------------------------------
+# MoE slot pairing (kernels/q40gu.wgsl:84-87, kernels/q40moedown.wgsl:42-75,
+# kernels/routertop.wgsl:19-71): router weight k with the gate/up AND the
+# down of expert topk[k]
+# ---------------------------------------------------------------------------
+from closed_form import moe_pairing_case, moe_pairing_expected, moe_pairing_route  # noqa: E402
+
+PAIRING_MUTANTS = ("weights_rolled", "down_by_slot", "down_next")
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_moe_slot_pairing_closed_form(seed):
+    # distinct one-hot experts, strict hand-set router order: the top-8, their
+    # weights and the mixture are known in closed form; the three mutants
+    # (weights paired by the wrong slot, the down of slot k instead of
+    # expert topk[k], the down of the next slot's expert) are rejected by
+    # more than 100x the tolerance
+    m, sels = moe_pairing_case(seed=seed)
+    h = np.random.default_rng(50 + seed).standard_normal(m["hidden"]).astype(np.float32)
+    top, w, margin = moe_pairing_route(m, h)
+    assert margin > 1e-3, f"seed {seed}: top-8 decision margin {margin:.2e}"
+    assert not np.array_equal(np.sort(top), np.arange(8)), "the routed set must not be the first 8 experts"
+    idx, wo, dense, moe, _ = orc.moe_ffn(m, h)
+    np.testing.assert_array_equal(idx, top)
+    np.testing.assert_allclose(wo, w, rtol=1e-6)
+    assert not np.any(dense)
+    want = moe_pairing_expected(m, sels, h, top, w)
+    tol = 1e-6 * np.abs(want).max()
+    np.testing.assert_allclose(moe, want, rtol=0, atol=tol)
+    for mut in PAIRING_MUTANTS:
+        bad = moe_pairing_expected(m, sels, h, top, w, mutant=mut)
+        dev = float(np.abs(bad - moe).max())
+        assert dev > 100 * tol, f"mutant {mut} not rejected ({dev:.2e} vs tolerance {tol:.2e})"
+
+
+def test_moe_forced_experts_closed_form():
+    # orc_moe_ffn with forced experts (the synced A4B oracle routes a layer
+    # to the GPU's picks at a near-tie): the slots use the given experts,
+    # weighted from the router's own softmax renormalised over them, times
+    # pes; the order of the given experts does not change the mixture
+    m, sels = moe_pairing_case(seed=4)
+    h = np.random.default_rng(54).standard_normal(m["hidden"]).astype(np.float32)
+    top, w, _ = moe_pairing_route(m, h)
+    _, _, _, moe_own, _ = orc.moe_ffn(m, h)
+    idx, wf, _, moe_same, _ = orc.moe_ffn(m, h, force=top[::-1])
+    np.testing.assert_array_equal(idx, top[::-1])
+    np.testing.assert_allclose(moe_same, moe_own, rtol=0, atol=1e-6 * np.abs(moe_own).max())
+    other = np.array([int(top[0]), int(top[1])] + [e for e in range(m["n_experts"]) if e not in top][:6])
+    hd = np.asarray(h, np.float64)
+    inv = 1.0 / math.sqrt(float(np.mean(hd * hd)) + m["eps"])
+    s = 32.0 * f32(hd * inv * f32(np.asarray(m["router_scale"], np.float64) / math.sqrt(m["hidden"])))[:m["n_experts"]]
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    wo = p[other] / p[other].sum() * np.asarray(m["pes"], np.float64)[other]
+    idx, wf, _, moe_f, _ = orc.moe_ffn(m, h, force=other)
+    np.testing.assert_array_equal(idx, other)
+    np.testing.assert_allclose(wf, wo, rtol=1e-6)
+    want = moe_pairing_expected(m, sels, h, other, wo)
+    np.testing.assert_allclose(moe_f, want, rtol=0, atol=1e-6 * np.abs(want).max())
+    assert np.abs(moe_f - moe_own).max() > 0.1 * np.abs(moe_own).max()

@@ -6,9 +6,9 @@ both hosts byte for byte, and files written by write_safetensors load in it;
 bf16ToF32 against torch's bfloat16 -> float32 conversion.  CPU only.
 
 torch is imported when a test runs, not when the module is collected: a
-pytest session of GPU tests collects this module too, and torch's own HIP
-runtime loaded next to the one libe4b.so already uses makes that runtime's
-occupancy queries (the persistent step's co-residency check) answer 0.
+pytest session of GPU tests collects this module too, and a second HIP
+runtime (torch's) loaded next to the one libe4b.so already uses makes that
+runtime's occupancy queries answer 0.
 """
 import json
 import os
