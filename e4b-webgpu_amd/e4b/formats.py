@@ -84,3 +84,29 @@ def synth_q6k(seed: int, rows: int, cols: int, sigma: float = 1e-3) -> np.ndarra
     out = np.empty(rows * (cols // 256) * 210, dtype=np.uint8)
     check(lib.e4b_synth_q6k(seed, rows, cols, sigma, _ptr(out)), "e4b_synth_q6k")
     return out
+
+
+def q6k_row(ggml, cols: int, row: int) -> np.ndarray:
+    """Row `row` of a raw ggml Q6_K matrix [rows][cols] as f32 (the published
+    block_q6_K layout: per 256 weights ql[128] low nibbles, qh[64] high bit
+    pairs, 16 int8 group scales, f16 d; weight = d * scale * (q - 32), with
+    q = 4 low bits | 2 high bits << 4 in ggml's element order)."""
+    nsb = cols // 256
+    raw = np.frombuffer(memoryview(np.ascontiguousarray(ggml)).cast("B"), np.uint8)
+    blk = raw[row * nsb * 210:(row + 1) * nsb * 210].reshape(nsb, 210)
+    ql = blk[:, :128].astype(np.int32)
+    qh = blk[:, 128:192].astype(np.int32)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float32)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float32).reshape(nsb)
+    y = np.empty((nsb, 256), np.float32)
+    for half in range(2):
+        l_lo, l_hi = ql[:, 64 * half:64 * half + 32], ql[:, 64 * half + 32:64 * half + 64]
+        h = qh[:, 32 * half:32 * half + 32]
+        q = [(l_lo & 15) | ((h & 3) << 4), (l_hi & 15) | (((h >> 2) & 3) << 4),
+             (l_lo >> 4) | (((h >> 4) & 3) << 4), (l_hi >> 4) | (((h >> 6) & 3) << 4)]
+        for j in range(4):
+            for part in range(2):  # 16-element scale groups
+                g = 8 * half + 2 * j + part
+                s = slice(128 * half + 32 * j + 16 * part, 128 * half + 32 * j + 16 * part + 16)
+                y[:, s] = (d * sc[:, g])[:, None] * (q[j][:, 16 * part:16 * part + 16] - 32).astype(np.float32)
+    return y.reshape(-1)

@@ -438,6 +438,24 @@ napi_value read_f32(napi_env env, napi_callback_info info, bool hidden) {
   return arr;
 }
 napi_value read_hidden(napi_env env, napi_callback_info info) { return read_f32(env, info, true); }
+
+// readLayerHidden(ctx, layer) -> Float32Array [hidden]: the residual stream
+// after `layer` in the last decode step (the engine needs
+// FLAG_LAYER_HIDDEN for the layers before the last)
+napi_value read_layer_hidden(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  Ctx* x = ctx_of(env, argv[0]);
+  if (!x) return throw_msg(env, "readLayerHidden: not an engine context");
+  int32_t layer = 0;
+  if (napi_get_value_int32(env, argv[1], &layer) != napi_ok) return throw_msg(env, "readLayerHidden(ctx, layer)");
+  void* d = nullptr;
+  napi_value arr = make_typed(env, napi_float32_array, (size_t)x->hidden, 4, &d);
+  if (!arr) return throw_msg(env, "readLayerHidden: cannot allocate");
+  const int rc = e4b_read_layer_hidden(x->c, layer, (float*)d);
+  if (rc) return throw_lib(env, "readLayerHidden", rc);
+  return arr;
+}
 napi_value read_logits(napi_env env, napi_callback_info info) { return read_f32(env, info, false); }
 
 // full-layer KV budget (src/engine-a4b.js:587-617): kvCount(ctx) -> entries;
@@ -528,6 +546,7 @@ napi_value init(napi_env env, napi_value exports) {
       {"decode", nullptr, decode, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"argmax", nullptr, argmax, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"readHidden", nullptr, read_hidden, nullptr, nullptr, nullptr, kMethod, nullptr},
+      {"readLayerHidden", nullptr, read_layer_hidden, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"readLogits", nullptr, read_logits, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"kvCount", nullptr, kv_count, nullptr, nullptr, nullptr, kMethod, nullptr},
       {"readScores", nullptr, read_scores, nullptr, nullptr, nullptr, kMethod, nullptr},

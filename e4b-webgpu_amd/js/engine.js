@@ -5,7 +5,7 @@
 // (src/engine-a4b.js:854-856): step(token, pos), argmaxFast(),
 // decodeChunk(startPos, count, ringBase), generateFast(ids, maxNew, eosIds),
 // prefill(ids), generatePrefill(ids, maxNew, eosIds), profileStep(token,
-// pos), profilePrefill(ids), readHidden(); the long-context pair compactAll() and
+// pos), profilePrefill(ids), readHidden(), readLayerHidden(layer); the long-context pair compactAll() and
 // generateLong(ids, maxNew, eosIds) (src/engine-a4b.js:587-657, with
 // FLAG_KV_SCORE); plus readLogits(), kvCount(), reset() and close().
 //
@@ -26,7 +26,7 @@ const KV = {
   eps: "attention.layer_norm_rms_epsilon", softcap: "final_logit_softcapping",
 };
 const DEFAULTS = { ring: 1024, maxSeq: 4096, attnChunk: 0, maxPrompt: 0, flags: 0 };
-const FLAG_NO_GRAPH = 1, FLAG_STEP_PREFILL = 2, FLAG_KV_SCORE = 4;
+const FLAG_NO_GRAPH = 1, FLAG_STEP_PREFILL = 2, FLAG_KV_SCORE = 4, FLAG_LAYER_HIDDEN = 16;
 // long-context constants (src/engine-a4b.js:18-20)
 const KV_BUDGET = 640, KV_DECAP = 768, KV_PROTECT = 64;
 
@@ -199,13 +199,15 @@ async function loadEngine(file, overrides = {}) {
   }
   function kvCount() { return addon.kvCount(ctx); }
   async function readHidden() { return addon.readHidden(ctx); }
+  async function readLayerHidden(layer) { return addon.readLayerHidden(ctx, layer); }
   async function readLogits() { return addon.readLogits(ctx); }
   function reset() { addon.reset(ctx); }
   function close() { addon.destroy(ctx); }
 
   return { C, step, argmaxFast, decodeChunk, generateFast, prefill, generatePrefill, profileStep, profilePrefill,
-           compactAll, generateLong, kvCount, readHidden, readLogits, reset, close, tokRing };
+           compactAll, generateLong, kvCount, readHidden, readLayerHidden, readLogits, reset, close, tokRing };
 }
 
-module.exports = { loadEngine, configFromKV, addon, FLAG_NO_GRAPH, FLAG_STEP_PREFILL, FLAG_KV_SCORE, KV_BUDGET,
+module.exports = { loadEngine, configFromKV, addon, FLAG_NO_GRAPH, FLAG_STEP_PREFILL, FLAG_KV_SCORE, FLAG_LAYER_HIDDEN,
+                   KV_BUDGET,
                    KV_DECAP, KV_PROTECT };
