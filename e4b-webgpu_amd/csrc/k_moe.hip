@@ -273,14 +273,15 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 
 // ---- top-8 in one wave ----------------------------------------------------
 // lane l holds the scores of experts l + 64 j (j < 4, E <= 256); every lane
-// returns the same 8 picks (and, with WEIGHTS, their weights).  Selection on
-// the scores equals the reference's selection on p = exp(s - max) unless some
-// of the top-8 p underflow to 0 (scores more than ~87 below the maximum).
-// Each pick is the wave maximum of a 64-bit key (the score's bits mapped to
-// an unsigned order, then the complemented expert index, so ties go to the
-// lowest index as the strict '>' scan in index order gives), reduced with
-// lane swaps and DPP moves (six short steps, no LDS round trips); the
-// picked entry's key drops to 0, below every live key.
+// returns the same 8 picks (and, with WEIGHTS, their weights).  As in
+// kernels/routertop.wgsl:53-64 the ranking is on the f32 p = exp(s - max),
+// not on the scores: scores whose p round equal (apart by less than p's
+// spacing, or both far enough below the maximum that p is 0) tie and go to
+// the lowest index.  Each pick is the wave maximum of a 64-bit key (p's bits,
+// which order non-negative floats, plus one; then the complemented expert
+// index, so ties go to the lowest index as the strict '>' scan in index
+// order gives), reduced with lane swaps and DPP moves (six short steps, no
+// LDS round trips); the picked entry's key drops to 0, below every live key.
 struct TopK {
   int idx[K];
   float w[K];
@@ -302,13 +303,6 @@ DEV uint32_t lane_partner(uint32_t v) {
   }
 }
 
-// unsigned order of a float (larger float, larger key); -0 counts as +0,
-// which the float compare holds equal
-DEV uint32_t score_order(float s) {
-  const uint32_t u = __float_as_uint(s + 0.0f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 template <int M>
 DEV void key_max_step(uint32_t& hi, uint32_t& lo) {
   const uint32_t ohi = lane_partner<M>(hi), olo = lane_partner<M>(lo);
@@ -327,21 +321,20 @@ DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__
     s[j] = scores[e];
     pe[j] = WEIGHTS ? pes[e] : 0.f;
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s[j] = lane + 64 * j < E ? s[j] : -3.0e38f;
+  const float M = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
   uint32_t kh[4];
+  float p[4];
+  float psum = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool live = lane + 64 * j < E;
-    s[j] = live ? s[j] : -3.0e38f;
-    kh[j] = live ? score_order(s[j]) : 0u;  // live keys are >= 1
+    p[j] = live ? expf(s[j] - M) : 0.f;
+    psum += p[j];
+    kh[j] = live ? __float_as_uint(p[j]) + 1u : 0u;  // live keys are >= 1
   }
-  float M = 0.f, S = 1.f;
-  if constexpr (WEIGHTS) {
-    M = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-    float psum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) psum += lane + 64 * j < E ? expf(s[j] - M) : 0.f;
-    S = wave_sum(psum);
-  }
+  const float S = WEIGHTS ? wave_sum(psum) : 1.f;
   TopK t;
   float wsum = 0.f;
   float pk[K];
@@ -365,16 +358,16 @@ DEV TopK select_topk(const float* __restrict__ scores, const float* __restrict__
     const int bi = __builtin_amdgcn_readfirstlane((int)~bl);
     t.idx[k] = bi;
     const int bj = bi >> 6, bln = bi & 63;
-    float sv = s[0], pv = pe[0];
-#pragma unroll
-    for (int j = 1; j < 4; ++j) {
-      sv = bj == j ? s[j] : sv;
-      pv = bj == j ? pe[j] : pv;
-    }
-    const float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), bln));
-    pk[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), bln));
     if constexpr (WEIGHTS) {
-      t.w[k] = expf(bv - M) / S;  // p_k / sum p, as the reference stores it
+      float sv = p[0], pv = pe[0];
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        sv = bj == j ? p[j] : sv;
+        pv = bj == j ? pe[j] : pv;
+      }
+      const float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), bln));
+      pk[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), bln));
+      t.w[k] = bv / S;  // p_k / sum p, as the reference stores it
       wsum += t.w[k];
     }
 #pragma unroll

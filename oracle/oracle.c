@@ -220,27 +220,38 @@ float orc_gelu_tanh(float g) { return (float)gelu_d(g); }
 
 /* ------------------------------------------------------------------------ */
 /* Router + top-K (kernels/routertop.wgsl:19-71, same epilogue as           */
-/* kernels/top8.wgsl:9-29): scores = x.W_e; softmax; K rounds of a strict  */
-/* '>' scan from bv=-1 (ties -> lowest index), winner set to -2; w_k =     */
-/* p_k/sum, renormalised by sum of the K picks, times pes[idx_k].          */
+/* kernels/top8.wgsl:9-29): f32 scores s = x.W_e; f32 p = exp(s - max)     */
+/* (:53-56, the subtraction in f32, exp rounded once to f32); K rounds of  */
+/* a strict '>' scan of p from bv = -1, so p values that round equal --    */
+/* scores apart by less than the f32 spacing, or both underflowed to 0 --  */
+/* go to the lowest index (:58-64); the winner is set to -2; w_k = p_k /   */
+/* sum p, renormalised by the sum of the K picks, times pes[idx_k] (:66-68)*/
 /* ------------------------------------------------------------------------ */
+/* p[e] = f32 exp(f32(s_e - max s)) (kernels/routertop.wgsl:53-56); returns sum p */
+static double router_probs(const float* sf, int E, double* p) {
+  float mx = -3.0e38f;
+  for (int e = 0; e < E; ++e)
+    if (sf[e] > mx) mx = sf[e];
+  double sum = 0.0;
+  for (int e = 0; e < E; ++e) {
+    const float d = sf[e] - mx; /* f32 difference */
+    p[e] = (double)(float)exp((double)d);
+    sum += p[e];
+  }
+  return sum;
+}
+
 void orc_router_topk(const float* x, const float* W, const float* pes, int H, int E, int K,
                      uint32_t* idx, float* wts, float* scores) {
+  float* sf = (float*)malloc(sizeof(float) * (size_t)E);
   double* p = (double*)malloc(sizeof(double) * (size_t)E);
-  double mx = -3.0e38;
   for (int e = 0; e < E; ++e) {
     double s = 0.0;
     for (int j = 0; j < H; ++j) s += (double)x[j] * (double)W[(int64_t)e * H + j];
-    float sf = (float)s; /* the reference stores f32 scores */
-    if (scores) scores[e] = sf;
-    p[e] = sf;
-    if (p[e] > mx) mx = p[e];
+    sf[e] = (float)s; /* the reference stores f32 scores */
+    if (scores) scores[e] = sf[e];
   }
-  double sum = 0.0;
-  for (int e = 0; e < E; ++e) {
-    p[e] = exp(p[e] - mx);
-    sum += p[e];
-  }
+  const double sum = router_probs(sf, E, p);
   double wk[64], wsum = 0.0;
   for (int k = 0; k < K; ++k) {
     int bi = 0;
@@ -257,6 +268,7 @@ void orc_router_topk(const float* x, const float* W, const float* pes, int H, in
   }
   for (int k = 0; k < K; ++k) wts[k] = (float)(wk[k] / wsum * (double)pes[idx[k]]);
   free(p);
+  free(sf);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -579,15 +591,16 @@ void orc_moe_ffn_f(const orc_moe* m, const float* h, const uint32_t* force_idx, 
   if (margin) *margin = route_margin_of(sc, E, K);
   if (own_idx) memcpy(own_idx, topk_idx, sizeof(uint32_t) * (size_t)K);
   if (force_idx) {
-    double mx = -3.0e38, sum = 0.0, wsum = 0.0, wk[64];
-    for (int e = 0; e < E; ++e) mx = sc[e] > mx ? sc[e] : mx;
-    for (int e = 0; e < E; ++e) sum += exp((double)sc[e] - mx);
+    double* p = malloc(sizeof(double) * (size_t)E);
+    const double sum = router_probs(sc, E, p);
+    double wsum = 0.0, wk[64];
     for (int k = 0; k < K; ++k) {
       topk_idx[k] = force_idx[k];
-      wk[k] = exp((double)sc[force_idx[k]] - mx) / sum;
+      wk[k] = p[force_idx[k]] / sum;
       wsum += wk[k];
     }
     for (int k = 0; k < K; ++k) topk_w[k] = (float)(wk[k] / wsum * (double)m->pes[topk_idx[k]]);
+    free(p);
   }
   free(sc);
 

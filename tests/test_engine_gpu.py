@@ -263,7 +263,8 @@ def test_c4_stated_workload_teacher_forced(capsys):
     import time
     DRIFT_TOL = 1e-2
     SYNC_TOL = 2e-3
-    cfg = E4BConfig(max_seq=1024)
+    from e4b._lib import FLAG_LAYER_HIDDEN
+    cfg = E4BConfig(max_seq=1024, flags=FLAG_LAYER_HIDDEN)
     tensors = norm_weights_random(synth_tensors(cfg, 5), 6)
     eng = Engine(cfg, tensors)
     tens = {n: t.data for n, t in tensors.items()}
@@ -293,7 +294,7 @@ def test_c4_stated_workload_teacher_forced(capsys):
     print(f"after the batched prefill: logits err {err_m:.2e} of max, {err_r:.2e} of range")
     assert g0 == o_tok or top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max(), f"prefill argmax {g0} vs {o_tok}"
     assert err_m < LOGIT_TOL
-    free, sync, ties, row_same = [], [], [], []
+    free, sync, ties, row_same, layer_err = [], [], [], [], []
     argmaxes = []
     osync.set_keep_rows(True)
     for k, t in enumerate(forced):
@@ -319,6 +320,10 @@ def test_c4_stated_workload_teacher_forced(capsys):
         argmaxes.append(g)
         fm, fr = lerr(lg, o_lg)
         sm, sr = lerr(lg, s_lg)
+        # attribution: the residual stream after every layer (E4B_FLAG_LAYER_HIDDEN)
+        # against the synced oracle's, as a fraction of that layer's range
+        layer_err.append([lerr(eng.read_layer_hidden(layer), osync.layer_hidden(layer))[1]
+                          for layer in range(cfg.layers)])
         # synced: equal unless a near-tie; free-running: a different argmax
         # only where the oracle's top-2 margin is within twice that step's
         # logit difference (the flip the drift can cause)
@@ -346,6 +351,21 @@ def test_c4_stated_workload_teacher_forced(capsys):
           f"{np.percentile(fr, 90):.2e} max {fr.max():.2e} at pos {free[int(np.argmax(fr))][0]}; new K/V rows "
           f"bit-identical to the synced oracle's in {100 * np.mean(row_same):.1f} % of entries (min row "
           f"{100 * np.min(row_same):.1f} %)")
+    # where the worst steps' logit error comes from: the per-layer hidden
+    # error from the GPU's own caches, against the median step's profile
+    le = np.array(layer_err)
+    med = np.median(le, axis=0)
+    print("per-layer hidden err of range (median step), layers 0/5/10/.../34: " +
+          " ".join(f"{x:.1e}" for x in med[::5]) + f" {med[-1]:.1e}")
+    for i in np.argsort(-sr)[:6]:
+        prof = le[i]
+        ratio = prof / np.maximum(med, 1e-12)
+        jump = int(np.argmax(np.diff(np.r_[0.0, prof])))
+        print(f"  step pos {sync[i][0]}: logits err {sr[i]:.2e} of range; hidden err layer 0 {prof[0]:.1e}, "
+              f"largest rise at layer {jump} ({prof[jump - 1] if jump else 0.0:.1e} -> {prof[jump]:.1e}), "
+              f"last layer {prof[-1]:.1e} ({ratio[-1]:.1f}x the median step's); layers above 3x the median: "
+              f"{[int(x) for x in np.flatnonzero(ratio > 3)]}")
+    assert le[:, 0].max() < 1e-3, f"layer 0 hidden err {le[:, 0].max():.2e} of range"
     # KV caches after position 767: written slots identical, values close
     moved = []
     for layer in range(cfg.layers):

@@ -117,6 +117,48 @@ def test_router_ties_pick_lowest_index():
     assert list(idx[:3]) == [3, 10, 77]
 
 
+def test_router_ranks_on_f32_probabilities():
+    # kernels/routertop.wgsl:53-64 ranks p = exp(s - max) in f32: scores
+    # whose p round equal go to the lowest index.  A constant h makes every
+    # router input element the same value v, and one nonzero per router row
+    # makes each score one f32 product.  (1) Seven scores 200..194 and the
+    # rest >= 104 below them (p = 0, all tied): the 8th pick is expert 0
+    # (raw-score order would take the highest of the rest, expert 127).
+    # (2) Scores 1 and the next float (experts 5 and 9) 63 below the max:
+    # f32(s - max) rounds both to the same value, so 5 precedes 9.
+    t = _weights(9, False)
+    h = np.full(H, 0.75, np.float32)
+    xr = _router_input(t, h)
+    v = float(xr[0])
+    assert np.all(xr == xr[0])
+    sc = 0.5 + 0.01 * np.arange(E)
+    top = [100, 17, 60, 3, 90, 41, 77]
+    sc[top] = [200.0, 199.0, 198.0, 197.0, 196.0, 195.0, 194.0]
+    W = np.zeros((E, H), np.float32)
+    W[:, 0] = (sc / v).astype(np.float32)
+    t["router_w"] = W
+    idx, w = MoeLayer(H, E, FF, FF2, t).router_top8(h)
+    widx, ww = orc.router_topk(xr, W, t["pes"], 8)[:2]
+    assert widx.tolist() == top + [0]
+    np.testing.assert_array_equal(idx, widx)
+    assert w[7] == 0.0
+    # scores near 200: one f32 ulp of a score (1.5e-5) moves p = exp(s - max)
+    # by that much relative, and the GPU's v may differ from the oracle's by an ulp
+    np.testing.assert_allclose(w, ww, rtol=4e-5)
+    sc = np.full(E, -10.0)
+    sc[4], sc[5], sc[9] = 64.0, 1.0, 1.0
+    W = np.zeros((E, H), np.float32)
+    W[:, 0] = (sc / v).astype(np.float32)
+    W[9, 0] = np.nextafter(W[5, 0], np.float32(np.inf))
+    t["router_w"] = W
+    idx, w = MoeLayer(H, E, FF, FF2, t).router_top8(h)
+    widx, ww = orc.router_topk(xr, W, t["pes"], 8)[:2]
+    assert widx[:3].tolist() == [4, 5, 9]
+    np.testing.assert_array_equal(idx, widx)
+    assert w[1] == w[2]
+    np.testing.assert_allclose(w, ww, rtol=4e-5)
+
+
 @pytest.mark.parametrize("m,seed,random_norms", [(1, 3, False), (37, 4, True), (256, 5, False)])
 def test_moe_prefill_rows(m, seed, random_norms):
     # the batched (expert-grouped) half-layer over m token rows: every row

@@ -273,6 +273,39 @@ def test_router_ties_lowest_index_first():
     assert abs(float(w.sum()) - 1.0) < 1e-6
 
 
+def _router_exact(scores):
+    """x = ones, one nonzero per router row: the f32 scores are exactly `scores`."""
+    E = len(scores)
+    W = np.zeros((E, 4), np.float32)
+    W[:, 0] = np.asarray(scores, np.float32)
+    return np.ones(4, np.float32), W
+
+
+def test_router_ranks_on_f32_probabilities():
+    # routertop.wgsl:53-64 ranks p = exp(s - max) in f32, so scores whose p
+    # round equal go to the lowest index even where the scores differ.
+    # (1) f32(s - max) rounds both to -63: 1.0 and the next float 1 + 2^-23
+    # (at index 9, the higher score) keep index order 5, 9
+    sc = np.full(16, -10.0, np.float32)
+    sc[4] = 64.0
+    sc[5], sc[9] = 1.0, np.nextafter(np.float32(1.0), np.float32(2.0))
+    x, W = _router_exact(sc)
+    idx, w, got = orc.router_topk(x, W, np.ones(16, np.float32), 8)
+    np.testing.assert_array_equal(got, sc)
+    assert idx[:3].tolist() == [4, 5, 9]
+    assert w[1] == w[2] and w[1] > 0
+    # (2) p underflows to 0 for every score 104 or more below the max: the
+    # 8th pick among them is the lowest index, not the highest score
+    sc = (0.5 + 0.01 * np.arange(128)).astype(np.float32)
+    top = [100, 17, 60, 3, 90, 41, 77]
+    sc[top] = [200.0, 199.0, 198.0, 197.0, 196.0, 195.0, 194.0]
+    x, W = _router_exact(sc)
+    idx, w, _ = orc.router_topk(x, W, np.ones(128, np.float32), 8)
+    assert idx[:7].tolist() == top
+    assert idx[7] == 0 and w[7] == 0.0  # raw-score order would pick 127
+    assert abs(float(w.sum()) - 1.0) < 1e-6
+
+
 # --------------------------------------------------------------------------
 # RoPE / head prep (kernels/headprep.wgsl:19-87)
 # --------------------------------------------------------------------------
