@@ -28,6 +28,11 @@
 #ifndef E4B_TUNE_VS_GL
 #define E4B_TUNE_VS_GL 4
 #endif
+// column slices of the o projection with the attention-combine prologue (1
+// or 2; the consumer's prologue adds the slices)
+#ifndef E4B_TUNE_OKS
+#define E4B_TUNE_OKS 2
+#endif
 #include "kernels.h"
 #include "moe.h"
 #include "step.h"
@@ -671,7 +676,7 @@ extern "C" int e4b_finalize(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) ||
       (rc = dalloc_t(c, &c->part_o, (size_t)QH * c->nch * HD)) ||
       (rc = dalloc_t(c, &c->part_ml, (size_t)QH * c->nch * 2)) || (rc = dalloc_t(c, &c->attn, (size_t)QH * HD)) ||
-      (rc = dalloc_t(c, &c->o, (size_t)H)) || (rc = dalloc_t(c, &c->xf, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->o, (size_t)2 * H)) || (rc = dalloc_t(c, &c->xf, (size_t)H)) ||
       (rc = dalloc_t(c, &c->gg, (size_t)FF)) || (rc = dalloc_t(c, &c->dn, (size_t)2 * H)) ||
       (rc = dalloc_t(c, &c->xg, (size_t)H)) || (rc = dalloc_t(c, &c->gp, (size_t)(PD ? PD : 1))) ||
       (rc = dalloc_t(c, &c->pp, (size_t)(PD ? PD / 32 : 1) * H)) || (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) ||
@@ -976,14 +981,15 @@ int record_step(e4b_ctx* c) {
       pa.window = a.window;
       pa.chunk_shift = chunk_l == 64 ? 6 : 5;
       pa.gch = gch_layer;
-      rc = launch_q40(Wo, nullptr, nullptr, EPI_F32, oo, 1, st, &pa);
+      rc = launch_q40(Wo, nullptr, nullptr, EPI_F32, oo, E4B_TUNE_OKS, st, &pa);
     } else {
       rc = launch_q40(Wo, (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st);
     }
     if (rc || (rc = tick(c, "o_proj"))) return rc;
     // 4. gate/up + GeGLU; prologue: post-attention residual + FFN input norm
     {
-      const ProArgs p = pro(hnext, c->o, ly.post_attn, ly.ffn_norm, 1.0f);
+      ProArgs p = pro(hnext, c->o, ly.post_attn, ly.ffn_norm, 1.0f);
+      if (fuse_combine) p.na = E4B_TUNE_OKS;  // the o projection's column slices
       GemvOut og = {nullptr, c->gg, nullptr, FF};
       if ((rc = launch_q40(q40_view(ly.gu, 2 * (int64_t)FF, H), nullptr, nullptr, EPI_GEGLU, og, 1, st, &p)) ||
           (rc = tick(c, "gate_up_geglu")))

@@ -23,7 +23,7 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
   const int nbk = W.nb / ks;
   if (nbk < 1) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: empty row");
   if (pro && pro->part_o) {
-    if (xl || ks != 1 || epi != EPI_F32 || W.nb * 32 != kProAttnH || !pro->part_ml || !pro->params ||
+    if (xl || (ks != 1 && ks != 2) || epi != EPI_F32 || W.nb * 32 != kProAttnH || !pro->part_ml || !pro->params ||
         pro->chunk_shift < 0 || pro->chunk_shift > 10 || pro->gch < 1 || pro->gch > q40k::kProAttnMaxCh)
       return e4b_fail(E4B_EINVAL, "q4_0 GEMV: the attention prologue needs an f32 GEMV of %d columns (got %d)",
                       kProAttnH, W.nb * 32);
@@ -33,7 +33,8 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
       return e4b_fail(E4B_EINVAL, "q4_0 GEMV: the layer-boundary prologue needs an f32 GEMV of H <= %d columns "
                       "(multiple of 4; got %d) and all its vectors", q40k::kProTailMaxH, W.nb * 32);
   } else if (pro && (xl || ks != 1 || pro->H != W.nb * 32 || !q40_prologue_supported(pro->H) || !pro->hin ||
-                     (pro->a && !pro->w1) || (pro->na > 1 && (pro->na != kMaxPartials || epi != EPI_F32)))) {
+                     (pro->a && !pro->w1) ||
+                     (pro->na > 1 && !((pro->na == kMaxPartials && epi == EPI_F32) || (pro->na == 2 && epi == EPI_GEGLU))))) {
     return e4b_fail(E4B_EINVAL, "q4_0 GEMV: prologue needs f16 input of a full 256/512/1024/2048 row (H=%d, cols=%d)",
                     pro ? pro->H : 0, W.nb * 32);
   }

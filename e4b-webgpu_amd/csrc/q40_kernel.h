@@ -21,10 +21,33 @@
 // batches of the fused-prologue gate/up GeGLU tile and of the column-split
 // f32 tile of 8 rows (the down projection) (compile-time, for A/B builds)
 #ifndef E4B_TUNE_GEGLU_NB
-#define E4B_TUNE_GEGLU_NB 4
+#define E4B_TUNE_GEGLU_NB 8
 #endif
 #ifndef E4B_TUNE_KW4_NB
 #define E4B_TUNE_KW4_NB 2
+#endif
+// batches requested before the prologue (PRE) and kept in flight ahead of
+// the one being multiplied (LB) by k_q40b
+#ifndef E4B_TUNE_GEGLU_PRE
+#define E4B_TUNE_GEGLU_PRE 2
+#endif
+#ifndef E4B_TUNE_GEGLU_LB
+#define E4B_TUNE_GEGLU_LB 2
+#endif
+#ifndef E4B_TUNE_KW4_PRE
+#define E4B_TUNE_KW4_PRE 2
+#endif
+#ifndef E4B_TUNE_KW4_LB
+#define E4B_TUNE_KW4_LB 2
+#endif
+
+// fewest workgroups the row-tile choice keeps for a GEMV with the fused norm
+// prologue and with the attention-combine prologue
+#ifndef E4B_TUNE_PRO_MINWGS
+#define E4B_TUNE_PRO_MINWGS 128
+#endif
+#ifndef E4B_TUNE_ATTN_MINWGS
+#define E4B_TUNE_ATTN_MINWGS 256
 #endif
 
 namespace q40k {
@@ -127,89 +150,106 @@ DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB, NA>& r) {
 
 // attention-combine prologue of the o projection: x[h*256 + d] = f16 of the
 // log-sum-exp merge of the live split-K chunks of head h (kernels/attcomb.wgsl
-// :10-36), thread d = output dim d.  attn_issue requests, before the weight
-// tile and without waiting for the position, the (max, sum) pairs of every
-// allocated chunk (wave v: heads 2v, 2v+1, one lane per chunk) and the
-// partial outputs of the first U chunks of all 8 heads; attn_finish reduces
-// the pairs to normalised chunk weights e^(m_c - M) / sum_c l_c e^(m_c - M)
-// in LDS and accumulates.  Chunks past the first U are read 8 at a time in
-// further passes (U = kProAttnFirst).
+// :10-36).  With kProAttn the workgroup merges all 8 heads; with kProAttn2
+// the projection's columns are cut into two slices (blockIdx.y) and a
+// workgroup merges only the 4 heads of its slice, which halves the partials
+// each workgroup reads (the two partial outputs are summed by the consumer's
+// prologue).  attn_issue requests, before the weight tile and without
+// waiting for the position, the (max, sum) pairs of every allocated chunk of
+// the slice's heads (one lane per chunk) and the partial outputs of the first
+// U chunks; attn_finish reduces the pairs to normalised chunk weights
+// e^(m_c - M) / sum_c l_c e^(m_c - M) in LDS and accumulates.  Chunks past
+// the first U are read U at a time in further passes.
 constexpr int kProAttn = -1;
+constexpr int kProAttn2 = -3;
 constexpr int kProAttnFirst = 8;
 constexpr int kProAttnMaxCh = kProAttnMaxChunks;  // chunks per head the prologue supports (one lane each)
 constexpr int kProAttnNH = kProAttnH / 256;
-static_assert(kProAttnNH == 8, "two heads per wave");
-// thread t merges head t/32, dims 8 (t % 32) .. 8 (t % 32) + 7 (two 16-byte
-// loads per chunk)
-template <int U>
+static_assert(kProAttnNH == 8, "8 heads of 256");
+constexpr bool pro_attn(int k) { return k == kProAttn || k == kProAttn2; }
+// heads a workgroup merges
+constexpr int attn_hs(int k) { return k == kProAttn2 ? 4 : 8; }
+// 256 threads over HS heads: thread t merges local head t / (256 / HS), EPT
+// = HS consecutive dims (one or two 16-byte loads per chunk); wave v owns the
+// (max, sum) pairs of local heads HPW v .. HPW v + HPW - 1
+template <int U, int HS>
 struct AttnRegs {
+  static constexpr int HPW = HS / 4, EPT = HS, TPH = 256 / HS;
   uint32_t pos;
-  float m[2], l[2];
-  float v[U][8];
+  float m[HPW], l[HPW];
+  float v[U][EPT];
 };
 
-template <int U>
-DEV void attn_issue(const ProArgs& p, AttnRegs<U>& r) {
+template <int U, int HS>
+DEV void attn_issue(const ProArgs& p, AttnRegs<U, HS>& r) {
+  using R = AttnRegs<U, HS>;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int hb = HS == 8 ? 0 : HS * (int)blockIdx.y;  // the slice's first head
   r.pos = p.params[p.window > 0 ? 0 : p.kv_idx];
   const int c = min(lane, p.gch - 1);
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const float* ml = p.part_ml + (int64_t)(2 * wv + hh) * p.gch * 2;
+  for (int hh = 0; hh < R::HPW; ++hh) {
+    const float* ml = p.part_ml + (int64_t)(hb + R::HPW * wv + hh) * p.gch * 2;
     r.m[hh] = ml[2 * c];
     r.l[hh] = ml[2 * c + 1];
   }
-  const int h = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 8;
+  const int h = hb + threadIdx.x / R::TPH, d0 = (threadIdx.x % R::TPH) * R::EPT;
 #pragma unroll
-  for (int u = 0; u < U; ++u) ld_floats<8>(p.part_o + ((int64_t)h * p.gch + min(u, p.gch - 1)) * 256 + d0, r.v[u]);
+  for (int u = 0; u < U; ++u)
+    ld_floats<R::EPT>(p.part_o + ((int64_t)h * p.gch + min(u, p.gch - 1)) * 256 + d0, r.v[u]);
 }
 
-template <int U>
-DEV void attn_finish(const ProArgs& p, AttnRegs<U>& r, uint16_t* xs, float* wts) {
+template <int U, int HS>
+DEV void attn_finish(const ProArgs& p, AttnRegs<U, HS>& r, uint16_t* xs, float* wts) {
+  using R = AttnRegs<U, HS>;
   const int pos = (int)r.pos;
   const int lo = (p.window > 0 && pos + 1 > p.window) ? pos + 1 - p.window : 0;
   const int nch = (pos + 1 - lo + (1 << p.chunk_shift) - 1) >> p.chunk_shift;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int hb = HS == 8 ? 0 : HS * (int)blockIdx.y;
   const bool live = lane < nch;
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
+  for (int hh = 0; hh < R::HPW; ++hh) {
     const float m = live ? r.m[hh] : -3.0e38f;
     const float M = wave_max(m);
     const float f = live ? __expf(m - M) : 0.f;
     const float den = wave_sum(live ? r.l[hh] * f : 0.f);
-    wts[(2 * wv + hh) * kProAttnMaxCh + lane] = f / den;
+    wts[(R::HPW * wv + hh) * kProAttnMaxCh + lane] = f / den;
   }
   lds_sync();
-  const int h = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 8;
-  const float* wh = wts + h * kProAttnMaxCh;
-  float acc[8];
+  const int hl = threadIdx.x / R::TPH, h = hb + hl, d0 = (threadIdx.x % R::TPH) * R::EPT;
+  const float* wh = wts + hl * kProAttnMaxCh;
+  float acc[R::EPT];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int j = 0; j < R::EPT; ++j) acc[j] = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (u < nch) {  // chunks past the live ones may hold stale or unwritten values
       const float wu = wh[u];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = fmaf(r.v[u][j], wu, acc[j]);
+      for (int j = 0; j < R::EPT; ++j) acc[j] = fmaf(r.v[u][j], wu, acc[j]);
     }
   }
   for (int c0 = U; c0 < nch; c0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      ld_floats<8>(p.part_o + ((int64_t)h * p.gch + min(c0 + u, nch - 1)) * 256 + d0, r.v[u]);
+      ld_floats<R::EPT>(p.part_o + ((int64_t)h * p.gch + min(c0 + u, nch - 1)) * 256 + d0, r.v[u]);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (c0 + u < nch) {
         const float wu = wh[c0 + u];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = fmaf(r.v[u][j], wu, acc[j]);
+        for (int j = 0; j < R::EPT; ++j) acc[j] = fmaf(r.v[u][j], wu, acc[j]);
       }
     }
   }
-  uint32_t pk[4];
+  uint32_t pk[R::EPT / 2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) pk[j] = (uint32_t)f2h(acc[2 * j]) | ((uint32_t)f2h(acc[2 * j + 1]) << 16);
-  *reinterpret_cast<uint4*>(xs + h * 256 + d0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  for (int j = 0; j < R::EPT / 2; ++j) pk[j] = (uint32_t)f2h(acc[2 * j]) | ((uint32_t)f2h(acc[2 * j + 1]) << 16);
+  if constexpr (R::EPT == 8)
+    *reinterpret_cast<uint4*>(xs + h * 256 + d0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  else
+    *reinterpret_cast<uint2*>(xs + h * 256 + d0) = make_uint2(pk[0], pk[1]);
   lds_sync();
 }
 
@@ -381,14 +421,14 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  static_assert(PROK >= kProTail, "prologue kind");
+  static_assert(PROK >= kProAttn2, "prologue kind");
   static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1 && NWV == 4), "attention / tail prologue: f32, KW = 1");
   static_assert(R * BPL <= 64, "scale parity bits");
-  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK == kProAttn ? kProAttnH
+  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : pro_attn(PROK) ? kProAttnH
                                                                   : PROK == kProTail ? kProTailMaxH : 8];
   __shared__ float red[NWV];
   __shared__ float part[KW == 4 ? 4 * SLOTS : 1];
-  __shared__ float mls[PROK == kProAttn ? (kProAttnH / 256) * kProAttnMaxCh : 1];
+  __shared__ float mls[pro_attn(PROK) ? attn_hs(PROK) * kProAttnMaxCh : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
@@ -406,9 +446,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   if constexpr (PROK > 0) pro_issue<PROK, NA, TPB>(pa, pr);
   // the attention prologue requests its first UA chunks up front (NA names
   // UA for this prologue: 8 or 16)
-  constexpr int UA = (PROK == kProAttn && NA > 1) ? NA : kProAttnFirst;
-  AttnRegs<UA> ar;
-  if constexpr (PROK == kProAttn) attn_issue(pa, ar);
+  constexpr int UA = (pro_attn(PROK) && NA > 1) ? NA : kProAttnFirst;
+  AttnRegs<UA, attn_hs(PROK)> ar;
+  if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
 
@@ -449,7 +489,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   uint32_t xq[BPL][XLO ? 16 : 1];
   float xs8[BPL];
   if constexpr (PROK > 0) pro_finish<PROK, TPB, NA>(pa, pr, xs_lds, red);
-  if constexpr (PROK == kProAttn) attn_finish(pa, ar, xs_lds, mls);
+  if constexpr (pro_attn(PROK)) attn_finish(pa, ar, xs_lds, mls);
   if constexpr (PROK == kProTail) tail_finish(pa, tr, xs_lds, red);
   E4B_TRACE_MARK(1);
 #pragma unroll
@@ -526,7 +566,8 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
 // while the chip is still accepting the rest of the stream (on a full chip
 // the memory system takes the requests of a whole tile only over several
 // microseconds) and a prologue's block barriers wait only for batch 0.
-template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4, int NB = 2>
+template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4, int NB = 2,
+          int PRE = 1, int LB = 1>
 __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __restrict__ xh,
                                                   const uint32_t* __restrict__ xl, GemvOut o, int64_t ntiles,
                                                   int nbk, ProArgs pa) {
@@ -540,15 +581,15 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  static_assert(PROK >= kProTail, "prologue kind");
+  static_assert(PROK >= kProAttn2, "prologue kind");
   static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1 && NWV == 4), "attention / tail prologue: f32, KW = 1");
   static_assert(R * BPL <= 64, "scale parity bits");
   static_assert(R % NB == 0 && (EPI != EPI_GEGLU || RB % 2 == 0), "whole (gate, up) pairs per batch");
-  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : PROK == kProAttn ? kProAttnH
+  __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : pro_attn(PROK) ? kProAttnH
                                                                   : PROK == kProTail ? kProTailMaxH : 8];
   __shared__ float red[NWV];
   __shared__ float part[KW == 4 ? 4 * SLOTS : 1];
-  __shared__ float mls[PROK == kProAttn ? (kProAttnH / 256) * kProAttnMaxCh : 1];
+  __shared__ float mls[pro_attn(PROK) ? attn_hs(PROK) * kProAttnMaxCh : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
@@ -566,9 +607,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   if constexpr (PROK > 0) pro_issue<PROK, NA, TPB>(pa, pr);
   // the attention prologue requests its first UA chunks up front (NA names
   // UA for this prologue: 8 or 16)
-  constexpr int UA = (PROK == kProAttn && NA > 1) ? NA : kProAttnFirst;
-  AttnRegs<UA> ar;
-  if constexpr (PROK == kProAttn) attn_issue(pa, ar);
+  constexpr int UA = (pro_attn(PROK) && NA > 1) ? NA : kProAttnFirst;
+  AttnRegs<UA, attn_hs(PROK)> ar;
+  if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
 
@@ -644,7 +685,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
       }
     }
   };
-  issue_rows(0);
+  static_assert(PRE >= 0 && PRE <= LB && LB >= 1 && LB <= NB, "batches requested ahead");
+#pragma unroll
+  for (int b = 0; b < PRE; ++b) issue_rows(b * RB);
   // the epilogue multiplier of the row this lane finishes (lanes that finish
   // no row read a valid neighbour), requested with the tile
   float mulv = 0.f;
@@ -655,7 +698,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   E4B_TRACE_MARK(0);
 
   if constexpr (PROK > 0) pro_finish<PROK, TPB, NA>(pa, pr, xs_lds, red);
-  if constexpr (PROK == kProAttn) attn_finish(pa, ar, xs_lds, mls);
+  if constexpr (pro_attn(PROK)) attn_finish(pa, ar, xs_lds, mls);
   if constexpr (PROK == kProTail) tail_finish(pa, tr, xs_lds, red);
   E4B_TRACE_MARK(1);
   if constexpr (PROK == 0 && NB > 1) {
@@ -692,12 +735,18 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   }
 
   if constexpr (NB == 1) {
+    if constexpr (PRE == 0) issue_rows(0);
     dot_rows(0);
   } else {
+    if constexpr (PRE < LB) {
+#pragma unroll
+      for (int b = PRE; b < LB; ++b) issue_rows(b * RB);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      if (b + 1 < NB) {
-        issue_rows((b + 1) * RB);
+      if (b + LB < NB) {
+        issue_rows((b + LB) * RB);
         __builtin_amdgcn_sched_barrier(0);
       }
       dot_rows(b * RB);
@@ -779,7 +828,7 @@ inline Cfg pick(int nbk, int64_t units, int epi, bool pro, int ks = 1, bool attn
   // norm prologue, which every workgroup repeats; 256 with the attention
   // prologue, whose per-workgroup partial reads favour short tiles; 512 for
   // the column-split down projection) keep enough loads in flight
-  const int64_t min_wgs = attn ? 256 : pro ? 128 : c.kw == 4 ? 512 : 256;
+  const int64_t min_wgs = attn ? E4B_TUNE_ATTN_MINWGS : pro ? E4B_TUNE_PRO_MINWGS : c.kw == 4 ? 512 : 256;
   while (r > rmin && ks * ((units + per_wg * r - 1) / (per_wg * r)) < min_wgs) r >>= 1;
   if (r < rmin) r = rmin;
   c.r = r;
@@ -798,7 +847,8 @@ struct Launch {
   hipStream_t st;
 };
 
-template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4, int NB = 1>
+template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4, int NB = 1,
+          int PRE = 1, int LB = 1>
 void launch(const Launch& L) {
   constexpr int G = 64 / LPR;
   const int64_t ntiles = (L.units + G * R - 1) / (G * R);
@@ -807,7 +857,7 @@ void launch(const Launch& L) {
     hipLaunchKernelGGL((k_q40<LPR, BPL, R, KW, XLO, EPI, PROK, NA, NWV>), dim3((unsigned)wgs, (unsigned)L.ks),
                        dim3(64 * NWV), 0, L.st, L.W, L.xh, L.xl, L.o, ntiles, L.nbk, L.pa);
   else
-    hipLaunchKernelGGL((k_q40b<LPR, BPL, R, KW, XLO, EPI, PROK, NA, NWV, NB>), dim3((unsigned)wgs, (unsigned)L.ks),
+    hipLaunchKernelGGL((k_q40b<LPR, BPL, R, KW, XLO, EPI, PROK, NA, NWV, NB, PRE, LB>), dim3((unsigned)wgs, (unsigned)L.ks),
                        dim3(64 * NWV), 0, L.st, L.W, L.xh, L.xl, L.o, ntiles, L.nbk, L.pa);
 }
 
@@ -827,7 +877,7 @@ bool launch_r(const Cfg& c, const Launch& L) {
         // the column-split down projection in 2 batches of 4 rows (measured
         // on MI355X at the E4B shape: 796 tok/s against 788 unbatched, 791
         // with 4 batches; batching the qkv and o tiles measured slower)
-        launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_KW4_NB>(L);
+        launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_KW4_NB, E4B_TUNE_KW4_PRE, E4B_TUNE_KW4_LB>(L);
       } else {
         launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA>(L);
       }
@@ -836,7 +886,7 @@ bool launch_r(const Cfg& c, const Launch& L) {
       if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0) {
         // the fused-prologue GeGLU in 4 batches of 4 rows (measured on
         // MI355X at the E4B shape: 8.9 us against 9.8-10.4 us unbatched)
-        launch<LPR, BPL, 16, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_GEGLU_NB>(L);
+        launch<LPR, BPL, 16, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_GEGLU_NB, E4B_TUNE_GEGLU_PRE, E4B_TUNE_GEGLU_LB>(L);
         return true;
       }
       return false;
@@ -874,8 +924,14 @@ bool launch_plain(const Cfg& c, const Launch& L) {
 // a second pass: the loads cannot be trimmed to the live chunks without
 // waiting for the position first.)
 inline bool launch_pro_attn(const Cfg& c, const Launch& L) {
-  if (c.bpl != 1 || c.lpr != 64) return false;
   // 16 chunks (a sliding layer in 32-position chunks) in one pass
+  if (L.ks == 2) {
+    // two column slices of 4 heads (1024 columns: 32 lanes per row)
+    if (c.bpl != 1 || c.lpr != 32) return false;
+    if (L.pa.gch == 16) return launch_r<32, 1, 1, false, EPI_F32, kProAttn2, 16>(c, L);
+    return launch_r<32, 1, 1, false, EPI_F32, kProAttn2>(c, L);
+  }
+  if (c.bpl != 1 || c.lpr != 64) return false;
   if (L.pa.gch == 16) return launch_r<64, 1, 1, false, EPI_F32, kProAttn, 16>(c, L);
   return launch_r<64, 1, 1, false, EPI_F32, kProAttn>(c, L);
 }
