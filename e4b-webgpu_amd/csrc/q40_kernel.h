@@ -41,6 +41,14 @@
 #define E4B_TUNE_KW4_LB 2
 #endif
 
+// rows per wave and waves per workgroup of the fused-prologue GeGLU tile
+#ifndef E4B_TUNE_GEGLU_R
+#define E4B_TUNE_GEGLU_R 16
+#endif
+#ifndef E4B_TUNE_GEGLU_NWV
+#define E4B_TUNE_GEGLU_NWV 4
+#endif
+
 // fewest workgroups the row-tile choice keeps for a GEMV with the fused norm
 // prologue and with the attention-combine prologue
 #ifndef E4B_TUNE_PRO_MINWGS
@@ -451,6 +459,8 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
+  // the prologue's requests stay ahead of the weight requests (vmcnt drains in order)
+  __builtin_amdgcn_sched_barrier(0);
 
   // weight tile: rows and blocks clamped into range (slots past the end are
   // computed on duplicate data and never stored; blocks past the range end
@@ -643,6 +653,8 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
     }
   };
   if constexpr (PROK == 0 && NB > 1) load_x();
+  // the input requests stay ahead of the weight requests (vmcnt drains in order)
+  __builtin_amdgcn_sched_barrier(0);
 
   // weight tile: rows and blocks clamped into range (slots past the end are
   // computed on duplicate data and never stored); scales as aligned pairs
@@ -820,7 +832,7 @@ inline Cfg pick(int nbk, int64_t units, int epi, bool pro, int ks = 1, bool attn
   // the fused-prologue GeGLU reads the prologue's four vectors once per
   // workgroup: 16 rows per wave halve that on-chip traffic (measured
   // fastest at the E4B shape, 512 workgroups)
-  if (pro && epi == EPI_GEGLU && c.lpr == 64 && c.bpl == 1 && c.kw == 1 && units >= 16 * 4 * 256) r = 16;
+  if (pro && epi == EPI_GEGLU && c.lpr == 64 && c.bpl == 1 && c.kw == 1 && units >= 16 * 4 * 256) r = E4B_TUNE_GEGLU_R;
   if (r > c.lpr) r = c.lpr;
   const int rmin = (epi == EPI_GEGLU) ? 2 : 1;
   const int per_wg = (c.kw == 1 ? 4 : 1) * G;
@@ -873,7 +885,10 @@ bool launch_r(const Cfg& c, const Launch& L) {
     case 2: launch<LPR, BPL, 2, KW, XLO, EPI, PROK, NA>(L); return true;
     case 4: launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA>(L); return true;
     case 8:
-      if constexpr (KW == 4 && !XLO && EPI == EPI_F32 && PROK == 0) {
+      if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0 && E4B_TUNE_GEGLU_R == 8) {
+        launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, E4B_TUNE_GEGLU_NWV, E4B_TUNE_GEGLU_NB, E4B_TUNE_GEGLU_PRE,
+               E4B_TUNE_GEGLU_LB>(L);
+      } else if constexpr (KW == 4 && !XLO && EPI == EPI_F32 && PROK == 0) {
         // the column-split down projection in 2 batches of 4 rows (measured
         // on MI355X at the E4B shape: 796 tok/s against 788 unbatched, 791
         // with 4 batches; batching the qkv and o tiles measured slower)
@@ -886,7 +901,8 @@ bool launch_r(const Cfg& c, const Launch& L) {
       if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0) {
         // the fused-prologue GeGLU in 4 batches of 4 rows (measured on
         // MI355X at the E4B shape: 8.9 us against 9.8-10.4 us unbatched)
-        launch<LPR, BPL, 16, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_GEGLU_NB, E4B_TUNE_GEGLU_PRE, E4B_TUNE_GEGLU_LB>(L);
+        launch<LPR, BPL, 16, KW, XLO, EPI, PROK, NA, E4B_TUNE_GEGLU_NWV, E4B_TUNE_GEGLU_NB, E4B_TUNE_GEGLU_PRE,
+               E4B_TUNE_GEGLU_LB>(L);
         return true;
       }
       return false;

@@ -8,9 +8,10 @@
 // in one device buffer, so they survive hipGraph replay: the timeline of a
 // graph-replayed step, which kernel-trace profilers do not follow here, is
 // read back as is.  A workgroup takes its record slot with one atomic on its
-// XCD's own counter at entry (its latency overlaps the kernel's first
-// loads) and writes the record at exit.  In the product build every
-// E4B_TRACE_SCOPE compiles to nothing.
+// XCD's own counter at phase mark 0 (after the kernel has requested its
+// loads, so no wait for those loads also waits for the atomic's return) or,
+// in kernels without mark 0, at exit, and writes the record at exit.  In
+// the product build every E4B_TRACE_SCOPE compiles to nothing.
 #pragma once
 #include <stdint.h>
 
@@ -55,23 +56,25 @@ bool trace_register(TraceBinder b);
 #include <hip/hip_runtime.h>
 
 namespace {
-__device__ TraceRec* g_trace_buf;
-__device__ unsigned* g_trace_cnt;
-__device__ unsigned g_trace_cap;  // records per XCD segment
+__constant__ TraceRec* g_trace_buf;  // constant space: scalar loads, no wait on the vector memory counter
+__constant__ unsigned* g_trace_cnt;
+__constant__ unsigned g_trace_cap;  // records per XCD segment
 
 struct TraceScope {
   uint64_t t0;
   uint32_t tag, slot, xcc;
   uint32_t mark[kTraceMarks] = {0, 0, 0, 0};
   __device__ __forceinline__ explicit TraceScope(uint32_t t) : t0(__builtin_amdgcn_s_memrealtime()), tag(t), slot(~0u), xcc(0) {
-    if (threadIdx.x == 0 && g_trace_buf) {
-      xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // HW_REG_XCC_ID
+    xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // HW_REG_XCC_ID
+  }
+  __device__ __forceinline__ void take_slot() {
+    if (threadIdx.x == 0 && slot == ~0u && g_trace_buf)
       slot = atomicAdd(g_trace_cnt + (xcc % kTraceXcds) * kTraceCntStride, 1u);
-    }
   }
   __device__ __forceinline__ ~TraceScope() {
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    take_slot();
     if (threadIdx.x == 0 && slot < g_trace_cap) {
-      const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
       const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);  // HW_REG_HW_ID
       const uint32_t blk = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
       uint4* d = reinterpret_cast<uint4*>(g_trace_buf + (size_t)(xcc % kTraceXcds) * g_trace_cap + slot);
@@ -84,6 +87,7 @@ struct TraceScope {
   // inputs are in", "the dot products are done"
   __device__ __forceinline__ void stamp(int i) {
     if (threadIdx.x < 64) mark[i] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - t0);
+    if (i == 0) take_slot();
   }
 };
 
