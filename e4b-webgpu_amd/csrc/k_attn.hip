@@ -112,6 +112,26 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(AttnArgs A) {
   // numbering: the position for sliding rings, the entry count for full
   // layers (equal to the position until a compaction moves entries)
   const int pos = (int)(A.params ? A.params[0] : A.pos);
+  __builtin_amdgcn_sched_barrier(0);
+  // 0a. the head-prep inputs do not depend on the position: they are
+  //     requested while the position is in flight (this wave's q/k/v row,
+  //     its norm weights, the RoPE (cos, sin) of its lane's dims; with
+  //     NW = 8 waves 6-7 repeat wave 5's row and drop it; with NW = 4 waves
+  //     0 and 1 also read the k and v rows)
+  const int prow = NW == 8 ? (wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g) : g * GQA + wave;
+  const float4 xin = *reinterpret_cast<const float4*>(A.qkv + (int64_t)prow * HD + 4 * lane);
+  const float4 win = *reinterpret_cast<const float4*>((NW == 8 && wave >= 4 ? A.kw : A.qw) + 4 * lane);
+  const int krow2 = A.qh + (wave == 0 ? 0 : A.kvh) + g;  // NW = 4: the k (wave 0) or v (wave 1) row
+  float4 xin2 = make_float4(0.f, 0.f, 0.f, 0.f), win2 = xin2;
+  if constexpr (NW == 4) {
+    xin2 = *reinterpret_cast<const float4*>(A.qkv + (int64_t)krow2 * HD + 4 * lane);
+    win2 = *reinterpret_cast<const float4*>(A.kw + 4 * lane);
+  }
+  const bool have_cs = A.rope != nullptr;
+  const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);  // any readable 1 KB
+  const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
+  const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
+  __builtin_amdgcn_sched_barrier(0);
   const int cur = A.window > 0 ? pos : (int)(A.params ? A.params[A.kv_idx] : A.pos);
   const int lo = (A.window > 0 && cur + 1 > A.window) ? cur + 1 - A.window : 0;
   const int n = cur + 1 - lo;
@@ -133,25 +153,9 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(AttnArgs A) {
   const int vsub = lane / LV, vl = lane % LV, vd0 = VD * zs + 8 * vl;
   const bool owner = cur < c_lo + m;  // the last live chunk holds cur, at j = m - 1
 
-  // 0. request everything the block reads before any math: the head-prep
-  //    inputs (this wave's q/k/v row, its norm weights, the RoPE (cos, sin)
-  //    of its lane's dims; with NW = 8 waves 6-7 repeat wave 5's row and drop
-  //    it; with NW = 4 waves 0 and 1 also read the k and v rows), then the
-  //    wave's K and V rows (index clamped into the chunk; the row of `pos` is
-  //    not written yet and is replaced from LDS below)
-  const int prow = NW == 8 ? (wave < 4 ? g * GQA + wave : A.qh + (wave == 4 ? 0 : A.kvh) + g) : g * GQA + wave;
-  const float4 xin = *reinterpret_cast<const float4*>(A.qkv + (int64_t)prow * HD + 4 * lane);
-  const float4 win = *reinterpret_cast<const float4*>((NW == 8 && wave >= 4 ? A.kw : A.qw) + 4 * lane);
-  const int krow2 = A.qh + (wave == 0 ? 0 : A.kvh) + g;  // NW = 4: the k (wave 0) or v (wave 1) row
-  float4 xin2 = make_float4(0.f, 0.f, 0.f, 0.f), win2 = xin2;
-  if constexpr (NW == 4) {
-    xin2 = *reinterpret_cast<const float4*>(A.qkv + (int64_t)krow2 * HD + 4 * lane);
-    win2 = *reinterpret_cast<const float4*>(A.kw + 4 * lane);
-  }
-  const bool have_cs = A.rope != nullptr;
-  const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);  // any readable 1 KB
-  const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
-  const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
+  // 0b. the wave's K and V rows (index clamped into the chunk; the row of
+  //     `pos` is not written yet and is replaced from LDS below), all
+  //     requested before any math
   uint4 kr[KP][2];
   uint4 vr[VQ];
 #pragma unroll

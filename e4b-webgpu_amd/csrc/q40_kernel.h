@@ -21,7 +21,7 @@
 // batches of the fused-prologue gate/up GeGLU tile and of the column-split
 // f32 tile of 8 rows (the down projection) (compile-time, for A/B builds)
 #ifndef E4B_TUNE_GEGLU_NB
-#define E4B_TUNE_GEGLU_NB 8
+#define E4B_TUNE_GEGLU_NB 4
 #endif
 #ifndef E4B_TUNE_KW4_NB
 #define E4B_TUNE_KW4_NB 2
@@ -29,10 +29,10 @@
 // batches requested before the prologue (PRE) and kept in flight ahead of
 // the one being multiplied (LB) by k_q40b
 #ifndef E4B_TUNE_GEGLU_PRE
-#define E4B_TUNE_GEGLU_PRE 2
+#define E4B_TUNE_GEGLU_PRE 1
 #endif
 #ifndef E4B_TUNE_GEGLU_LB
-#define E4B_TUNE_GEGLU_LB 2
+#define E4B_TUNE_GEGLU_LB 1
 #endif
 #ifndef E4B_TUNE_KW4_PRE
 #define E4B_TUNE_KW4_PRE 2
@@ -43,10 +43,10 @@
 
 // rows per wave and waves per workgroup of the fused-prologue GeGLU tile
 #ifndef E4B_TUNE_GEGLU_R
-#define E4B_TUNE_GEGLU_R 16
+#define E4B_TUNE_GEGLU_R 8
 #endif
 #ifndef E4B_TUNE_GEGLU_NWV
-#define E4B_TUNE_GEGLU_NWV 4
+#define E4B_TUNE_GEGLU_NWV 8
 #endif
 
 // fewest workgroups the row-tile choice keeps for a GEMV with the fused norm
@@ -829,9 +829,9 @@ inline Cfg pick(int nbk, int64_t units, int epi, bool pro, int ks = 1, bool attn
   pick_lanes(nbk / c.kw, &c.lpr, &c.bpl, c.kw == 4);
   const int G = 64 / c.lpr;
   int r = c.bpl == 1 ? 8 : c.bpl == 2 ? 4 : c.bpl <= 4 ? 2 : 1;
-  // the fused-prologue GeGLU reads the prologue's four vectors once per
-  // workgroup: 16 rows per wave halve that on-chip traffic (measured
-  // fastest at the E4B shape, 512 workgroups)
+  // the fused-prologue GeGLU reads the prologue's vectors once per
+  // workgroup: 64 rows per workgroup (8 waves x 8 rows, 512 workgroups)
+  // halve that on-chip traffic against 4-wave workgroups of 8 rows
   if (pro && epi == EPI_GEGLU && c.lpr == 64 && c.bpl == 1 && c.kw == 1 && units >= 16 * 4 * 256) r = E4B_TUNE_GEGLU_R;
   if (r > c.lpr) r = c.lpr;
   const int rmin = (epi == EPI_GEGLU) ? 2 : 1;
@@ -886,12 +886,18 @@ bool launch_r(const Cfg& c, const Launch& L) {
     case 4: launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA>(L); return true;
     case 8:
       if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0 && E4B_TUNE_GEGLU_R == 8) {
+        // the fused-prologue GeGLU: 8-wave workgroups, 4 batches of 2 rows,
+        // one batch requested ahead (measured on MI355X at the E4B shape:
+        // 825 tok/s against 821 for 4-wave workgroups of 16 rows in 8
+        // batches and 797-808 for the other 8-row shapes tried)
         launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, E4B_TUNE_GEGLU_NWV, E4B_TUNE_GEGLU_NB, E4B_TUNE_GEGLU_PRE,
                E4B_TUNE_GEGLU_LB>(L);
       } else if constexpr (KW == 4 && !XLO && EPI == EPI_F32 && PROK == 0) {
-        // the column-split down projection in 2 batches of 4 rows (measured
-        // on MI355X at the E4B shape: 796 tok/s against 788 unbatched, 791
-        // with 4 batches; batching the qkv and o tiles measured slower)
+        // the column-split down projection: the whole tile requested up
+        // front, multiplied in 2 batches of 4 rows (measured on MI355X at
+        // the E4B shape: 798 tok/s against 796 with one batch ahead, 788
+        // unbatched, 791-793 with 4 batches; batching the qkv and o tiles
+        // measured slower)
         launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_KW4_NB, E4B_TUNE_KW4_PRE, E4B_TUNE_KW4_LB>(L);
       } else {
         launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA>(L);
@@ -899,8 +905,8 @@ bool launch_r(const Cfg& c, const Launch& L) {
       return true;
     case 16:
       if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0) {
-        // the fused-prologue GeGLU in 4 batches of 4 rows (measured on
-        // MI355X at the E4B shape: 8.9 us against 9.8-10.4 us unbatched)
+        // the fused-prologue GeGLU with 16 rows per wave (the 8-row shape
+        // above measured faster)
         launch<LPR, BPL, 16, KW, XLO, EPI, PROK, NA, E4B_TUNE_GEGLU_NWV, E4B_TUNE_GEGLU_NB, E4B_TUNE_GEGLU_PRE,
                E4B_TUNE_GEGLU_LB>(L);
         return true;
