@@ -48,7 +48,7 @@ MALL_BYTES = 256 << 20
 # runs (FETCH_SIZE, WRITE_SIZE per dispatch, each scaled by the same counter
 # on a 256 MiB copy kernel: x2.000 and x1.000); commands and raw values in
 # profiles/geglu_dominant_traffic.md.  Re-measure when the kernel changes.
-GEGLU_TRAFFIC_BYTES = int(18633.0 * 1024 * 2.0 + 40.0 * 1024 * 1.0)
+GEGLU_TRAFFIC_BYTES = int(18609.6 * 1024 * 2.0 + 40.0 * 1024 * 1.0)
 # The same two counter runs for the other configs' timed kernels (per launch
 # or per layer; commands and raw values in profiles/gemv_c0.md,
 # profiles/lmhead_c1.md, profiles/attn_c2.md and profiles/moe_c3.md).
