@@ -294,7 +294,7 @@ def test_c4_stated_workload_teacher_forced(capsys):
     print(f"after the batched prefill: logits err {err_m:.2e} of max, {err_r:.2e} of range")
     assert g0 == o_tok or top2_margin(o_lg) < TIE_TOL * np.abs(o_lg).max(), f"prefill argmax {g0} vs {o_tok}"
     assert err_m < LOGIT_TOL
-    free, sync, ties, row_same, layer_err = [], [], [], [], []
+    free, sync, ties, row_same, layer_err, flips = [], [], [], [], [], []
     argmaxes = []
     osync.set_keep_rows(True)
     for k, t in enumerate(forced):
@@ -311,12 +311,18 @@ def test_c4_stated_workload_teacher_forced(capsys):
             gpu_rows.append((kg[:, slot, :], vg[:, slot, :]))
         osync.set_kv_count(pos)
         s_tok, s_lg, _ = osync.step(int(t), pos, want_logits=True)
+        ulp1 = np.zeros(cfg.layers, np.int64)  # new K/V entries one f16 code apart (a rounding point straddled)
+        ulpn = np.zeros(cfg.layers, np.int64)  # ... more than one code apart
         for layer, (kg, vg) in enumerate(gpu_rows):
             for a, b in zip((kg, vg), osync.rows(layer)):
                 fa, fb = a.view(np.float16).astype(np.float64), b.view(np.float16).astype(np.float64)
                 d = np.abs(fa - fb).max() / np.abs(fb).max()
                 assert d <= (2.0 ** -9 if layer == 0 else KV_MAX_TOL), f"pos {pos} layer {layer}: new row {d:.2e}"
                 row_same.append(float(np.mean(a == b)))
+                du = np.abs(a.view(np.int16).astype(np.int32) - b.view(np.int16).astype(np.int32))
+                ulp1[layer] += int(np.sum(du == 1))
+                ulpn[layer] += int(np.sum(du > 1))
+        flips.append((ulp1, ulpn))
         argmaxes.append(g)
         fm, fr = lerr(lg, o_lg)
         sm, sr = lerr(lg, s_lg)
@@ -357,6 +363,10 @@ def test_c4_stated_workload_teacher_forced(capsys):
     med = np.median(le, axis=0)
     print("per-layer hidden err of range (median step), layers 0/5/10/.../34: " +
           " ".join(f"{x:.1e}" for x in med[::5]) + f" {med[-1]:.1e}")
+    f1 = np.array([f[0].sum() for f in flips])
+    fn = np.array([f[1].sum() for f in flips])
+    print(f"new K/V entries (35 layers x 2 x 512 a step) one f16 code apart from the synced oracle's: median "
+          f"{int(np.median(f1))} a step, more than one code apart: median {int(np.median(fn))}, max {int(fn.max())}")
     for i in np.argsort(-sr)[:6]:
         prof = le[i]
         ratio = prof / np.maximum(med, 1e-12)
@@ -364,7 +374,9 @@ def test_c4_stated_workload_teacher_forced(capsys):
         print(f"  step pos {sync[i][0]}: logits err {sr[i]:.2e} of range; hidden err layer 0 {prof[0]:.1e}, "
               f"largest rise at layer {jump} ({prof[jump - 1] if jump else 0.0:.1e} -> {prof[jump]:.1e}), "
               f"last layer {prof[-1]:.1e} ({ratio[-1]:.1f}x the median step's); layers above 3x the median: "
-              f"{[int(x) for x in np.flatnonzero(ratio > 3)]}")
+              f"{[int(x) for x in np.flatnonzero(ratio > 3)]}; K/V entries one code apart {int(f1[i])} "
+              f"(layers 0-4: {[int(x) for x in flips[i][0][:5]]}), more than one {int(fn[i])}")
+        print("    per-layer hidden err of range: " + " ".join(f"{x:.1e}" for x in prof))
     assert le[:, 0].max() < 1e-3, f"layer 0 hidden err {le[:, 0].max():.2e} of range"
     # KV caches after position 767: written slots identical, values close
     moved = []
