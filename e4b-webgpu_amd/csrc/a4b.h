@@ -34,6 +34,7 @@ struct AttnGen {
   float* raw;              // full layers, may be null: raw scores [qh][slots] of the live slots
   int qh, kvh, hd, angles, slots, window, kv_idx, gch;
   bool keqv;               // V = the raw K slice (kernels/headprep.wgsl:23)
+  bool no_merge;           // the consumer merges the partials (the o projection's prologue): no merge launch
   float eps;
 };
 constexpr int kAttnGenChunk = 64;  // positions per split-K chunk

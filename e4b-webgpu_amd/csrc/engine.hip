@@ -553,7 +553,7 @@ int finalize_a4b(e4b_ctx* c) {
       (rc = dalloc_t(c, &c->h_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->xn, (size_t)H)) ||
       (rc = dalloc_t(c, &c->qkv, (size_t)c->qkv_rows)) ||
       (rc = dalloc_t(c, &c->part_o, part)) || (rc = dalloc_t(c, &c->part_ml, ml)) ||
-      (rc = dalloc_t(c, &c->attn, (size_t)QH * hd_max)) || (rc = dalloc_t(c, &c->o, (size_t)H)) ||
+      (rc = dalloc_t(c, &c->attn, (size_t)QH * hd_max)) || (rc = dalloc_t(c, &c->o, (size_t)4 * H)) ||
       (rc = dalloc_t(c, &c->xo_hl, (size_t)2 * H)) || (rc = dalloc_t(c, &c->logits, (size_t)k.vocab)) ||
       (rc = dalloc_t(c, &c->amax_part, (size_t)c->amax_parts)) || (rc = dalloc_t(c, &m.scores, (size_t)E)) ||
       (rc = dalloc_t(c, &m.xd, (size_t)H)) || (rc = dalloc_t(c, &m.xm, (size_t)H)) ||
@@ -814,21 +814,47 @@ int record_step_a4b(e4b_ctx* c) {
     ag.keqv = ly.keqv;
     ag.eps = k.eps;
     ag.raw = ly.score ? c->raw : nullptr;
+    // the o projection merges the split-K partials in its prologue, in
+    // column slices of 4 heads (2 or 4 slices, their partial outputs summed
+    // by the router), when the layer's chunks fit the prologue's lanes;
+    // else the merge launch writes the f16 attention output
+    static_assert(kAttnGenChunk == 64, "the prologue's chunk_shift below");
+    const int oks = QH / 4;
+#ifdef E4B_TUNE_A4B_MERGE_LAUNCH  // A/B builds: the merge as its own launch
+    const bool fuse = false;
+#else
+    const bool fuse = QH % 4 == 0 && (oks == 2 || oks == 4) && ly.gch <= kProAttnMaxChunks;
+#endif
+    ag.no_merge = fuse;
     GemvOut oo = {c->o, nullptr, nullptr, 0};
+    const Q40Mat Wo = q40_view(ly.o, H, (int64_t)QH * ly.hd);
     if ((rc = launch_attn_gen(ag, st)) || (rc = tick(c, ly.global ? "attn_global" : "attn_sliding")) ||
         (ly.score && ((rc = launch_attn_score(c->part_ml, c->raw, c->params, 4, QH, ly.slots, kAttnGenChunk, ly.score,
                                               st)) ||
-                      (rc = tick(c, "attn_score")))) ||
-        (rc = launch_q40(q40_view(ly.o, H, (int64_t)QH * ly.hd), (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1,
-                         st)) ||
-        (rc = tick(c, "o_proj")))
+                      (rc = tick(c, "attn_score")))))
       return rc;
+    if (fuse) {
+      ProArgs pa{};
+      pa.part_o = c->part_o;
+      pa.part_ml = c->part_ml;
+      pa.params = c->params;
+      pa.kv_idx = 4;
+      pa.window = window;
+      pa.chunk_shift = 6;  // kAttnGenChunk = 64 positions
+      pa.gch = ly.gch;
+      pa.head_dim = ly.hd;
+      rc = launch_q40(Wo, nullptr, nullptr, EPI_F32, oo, oks, st, &pa);
+    } else {
+      rc = launch_q40(Wo, (const uint32_t*)c->attn, nullptr, EPI_F32, oo, 1, st);
+    }
+    if (rc || (rc = tick(c, "o_proj"))) return rc;
     // 2. MoE half; its router forms the attention residual h1 = h +
     //    rms(o) post_attn into hb; the tail runs in the next layer's qkv
     //    prologue, after the last layer in its own launch (h = the output)
     MoeArgs a = c->moe;
     a.h = c->h;
     a.attn_o = c->o;
+    a.attn_o_slices = fuse ? oks : 1;
     a.post_attn = ly.post_attn;
     a.h1 = c->hb;
     a.ffn_norm = ly.ffn_norm;

@@ -640,7 +640,7 @@ static void launch_attn_hd(const AttnGen& a, hipStream_t st) {
     launch_attn_hd_raw<HD, true>(a, st);
   else
     launch_attn_hd_raw<HD, false>(a, st);
-  hipLaunchKernelGGL(k_attn_merge<HD>, dim3(a.qh), dim3(256), 0, st, a);
+  if (!a.no_merge) hipLaunchKernelGGL(k_attn_merge<HD>, dim3(a.qh), dim3(256), 0, st, a);
 }
 
 int launch_attn_gen(const AttnGen& a, hipStream_t st) {

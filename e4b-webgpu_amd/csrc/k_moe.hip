@@ -62,6 +62,7 @@ DEV float f4_ss(float4 v, float acc) {
   return fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, acc))));
 }
 
+template <int NO>
 __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
   E4B_TRACE_SCOPE(trace_tag(TR_MOE_ROUTER, 0));
   // token row y of a batch (the batched prefill); y = 0 in the decode step
@@ -86,17 +87,27 @@ __global__ __launch_bounds__(128) void k_moe_router(MoeArgs A) {
   // every load up front: h, the scale and the residual inputs
   // (thread-strided), the expert row
   float4 hv[PT], sv[PT], ov[PT], pv[PT], wv[kRouterMaxH4 / 64];
+  float4 os[NO > 1 ? NO - 1 : 1][PT];  // the o projection's further column slices
 #pragma unroll
   for (int k = 0; k < PT; ++k) {
     const int i = min((int)threadIdx.x + 128 * k, H4 - 1);
     hv[k] = h4[i];
     sv[k] = rs4[i];
     ov[k] = o4[i];
+#pragma unroll
+    for (int q = 1; q < NO; ++q) os[q - 1][k] = o4[(int64_t)q * H4 + i];
     pv[k] = pa4[i];
   }
 #pragma unroll
   for (int k = 0; k < kRouterMaxH4 / 64; ++k) wv[k] = w4[min(lane + 64 * k, H4 - 1)];
   if (res) {
+    // o = the slices' sum in slice order
+#pragma unroll
+    for (int q = 1; q < NO; ++q)
+#pragma unroll
+      for (int k = 0; k < PT; ++k)
+        ov[k] = make_float4(ov[k].x + os[q - 1][k].x, ov[k].y + os[q - 1][k].y, ov[k].z + os[q - 1][k].z,
+                            ov[k].w + os[q - 1][k].w);
     float so = 0.f;
 #pragma unroll
     for (int k = 0; k < PT; ++k)
@@ -728,7 +739,13 @@ __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
 
 int launch_moe_router(const MoeArgs& A, hipStream_t st) {
   if (A.H % 4 || A.H / 4 > kRouterMaxH4) return e4b_fail(E4B_EINVAL, "router: H=%d (multiple of 4, <= 3072)", A.H);
-  hipLaunchKernelGGL(k_moe_router, dim3((A.E + 1) / 2), dim3(128), 0, st, A);
+  switch (A.attn_o ? A.attn_o_slices : 1) {
+    case 0:
+    case 1: hipLaunchKernelGGL(k_moe_router<1>, dim3((A.E + 1) / 2), dim3(128), 0, st, A); break;
+    case 2: hipLaunchKernelGGL(k_moe_router<2>, dim3((A.E + 1) / 2), dim3(128), 0, st, A); break;
+    case 4: hipLaunchKernelGGL(k_moe_router<4>, dim3((A.E + 1) / 2), dim3(128), 0, st, A); break;
+    default: return e4b_fail(E4B_EINVAL, "MoE layer: %d o-projection slices (1, 2 or 4)", A.attn_o_slices);
+  }
   E4B_HIP(hipGetLastError());
   return E4B_OK;
 }

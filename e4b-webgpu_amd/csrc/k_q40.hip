@@ -23,10 +23,13 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
   const int nbk = W.nb / ks;
   if (nbk < 1) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: empty row");
   if (pro && pro->part_o) {
-    if (xl || (ks != 1 && ks != 2) || epi != EPI_F32 || W.nb * 32 != kProAttnH || !pro->part_ml || !pro->params ||
-        pro->chunk_shift < 0 || pro->chunk_shift > 10 || pro->gch < 1 || pro->gch > q40k::kProAttnMaxCh)
-      return e4b_fail(E4B_EINVAL, "q4_0 GEMV: the attention prologue needs an f32 GEMV of %d columns (got %d)",
-                      kProAttnH, W.nb * 32);
+    // one slice of 8 heads of 256 (ks = 1) or ks slices of 4 heads of 256 or 512
+    const int hd = pro->head_dim ? pro->head_dim : 256;
+    const bool shape = ks == 1 ? (hd == 256 && W.nb * 32 == kProAttnH) : ((hd == 256 || hd == 512) && nbk * 32 == 4 * hd);
+    if (xl || !shape || epi != EPI_F32 || !pro->part_ml || !pro->params || pro->chunk_shift < 0 ||
+        pro->chunk_shift > 10 || pro->gch < 1 || pro->gch > q40k::kProAttnMaxCh)
+      return e4b_fail(E4B_EINVAL, "q4_0 GEMV: the attention prologue needs 8 heads of 256 columns or slices of 4 "
+                      "heads of 256 or 512 (got %d columns, %d slices, head dim %d)", W.nb * 32, ks, hd);
   } else if (pro && pro->tail) {
     if (xl || ks != 1 || epi != EPI_F32 || pro->H != W.nb * 32 || pro->H % 4 || pro->H > q40k::kProTailMaxH ||
         !pro->hin || !pro->w2 || (pro->a && (!pro->a2 || !pro->w1 || !pro->w1b || !pro->wp)))

@@ -97,6 +97,7 @@ struct ProArgs {
   int window;              // 0 = global layer
   int chunk_shift;         // log2 of the positions per chunk
   int gch;                 // chunks allocated per head
+  int head_dim;            // 256 or 512 (0: 256); with ks column slices of 4 heads each
   // A4B layer boundary (tail != 0; any H <= 3072 divisible by 4): the
   // previous layer's MoE tail, then this layer's input norm:
   //   h = (hin + rms(rms(a) w1 + rms(a2) w1b) wp) * scale; x = f16(rms(h) w2)

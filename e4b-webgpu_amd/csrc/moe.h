@@ -38,7 +38,8 @@ struct MoeArgs {
   // optional attention residual folded into the router (decode step only):
   // h1 = h + rms(attn_o) post_attn is the FFN half's input, written to h1
   // (a buffer other than h) by router block 0 and read by the tail
-  const float* attn_o;        // [H] o projection output, or null
+  const float* attn_o;        // [attn_o_slices][H] o projection output (column-slice partials), or null
+  int attn_o_slices;          // 1, 2 or 4 (0 = 1): attn_o = their sum, added in slice order
   const float* post_attn;     // [H]
   float* h1;                  // [H]
 };

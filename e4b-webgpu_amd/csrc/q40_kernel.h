@@ -156,43 +156,48 @@ DEV void pro_issue(const ProArgs& p, ProRegs<PROK, TPB, NA>& r) {
   if constexpr (NORM2) ld_floats<N>(w2 + i0, r.w2);
 }
 
-// attention-combine prologue of the o projection: x[h*256 + d] = f16 of the
+// attention-combine prologue of the o projection: x[h*HD + d] = f16 of the
 // log-sum-exp merge of the live split-K chunks of head h (kernels/attcomb.wgsl
-// :10-36).  With kProAttn the workgroup merges all 8 heads; with kProAttn2
-// the projection's columns are cut into two slices (blockIdx.y) and a
-// workgroup merges only the 4 heads of its slice, which halves the partials
-// each workgroup reads (the two partial outputs are summed by the consumer's
-// prologue).  attn_issue requests, before the weight tile and without
-// waiting for the position, the (max, sum) pairs of every allocated chunk of
-// the slice's heads (one lane per chunk) and the partial outputs of the first
-// U chunks; attn_finish reduces the pairs to normalised chunk weights
+// :10-36).  With kProAttn the workgroup merges all 8 heads of 256 dims;
+// with kProAttn2 (4 heads of 256) and kProAttn4w (4 heads of 512) the
+// projection's columns are cut into slices of 4 heads (blockIdx.y) and a
+// workgroup merges only its slice's heads, so each workgroup reads only
+// their partials (the consumer's prologue sums the slices' partial
+// outputs).  attn_issue requests, before the weight tile and without
+// waiting for the position, the (max, sum) pairs of every allocated chunk
+// of the slice's heads (one lane per chunk) and the partial outputs of the
+// first U chunks; attn_finish reduces the pairs to normalised chunk weights
 // e^(m_c - M) / sum_c l_c e^(m_c - M) in LDS and accumulates.  Chunks past
-// the first U are read U at a time in further passes.
+// the first U are read U at a time in further passes.  The merged slice
+// lands in LDS at offset 0 (the dot products index it from the slice's
+// first column).
 constexpr int kProAttn = -1;
 constexpr int kProAttn2 = -3;
+constexpr int kProAttn4w = -4;
 constexpr int kProAttnFirst = 8;
 constexpr int kProAttnMaxCh = kProAttnMaxChunks;  // chunks per head the prologue supports (one lane each)
-constexpr int kProAttnNH = kProAttnH / 256;
-static_assert(kProAttnNH == 8, "8 heads of 256");
-constexpr bool pro_attn(int k) { return k == kProAttn || k == kProAttn2; }
-// heads a workgroup merges
-constexpr int attn_hs(int k) { return k == kProAttn2 ? 4 : 8; }
-// 256 threads over HS heads: thread t merges local head t / (256 / HS), EPT
-// = HS consecutive dims (one or two 16-byte loads per chunk); wave v owns the
-// (max, sum) pairs of local heads HPW v .. HPW v + HPW - 1
-template <int U, int HS>
+constexpr bool pro_attn(int k) { return k == kProAttn || k == kProAttn2 || k == kProAttn4w; }
+// heads a workgroup merges, and their head dim
+constexpr int attn_hs(int k) { return k == kProAttn ? 8 : 4; }
+constexpr int attn_hd(int k) { return k == kProAttn4w ? 512 : 256; }
+static_assert(kProAttnH == 8 * 256 && kProAttnH == 4 * 512, "the merged slice fits the 2048-column LDS stage");
+// 256 threads over HS heads of HD dims: thread t merges local head
+// t / (256 / HS), EPT = HS HD / 256 consecutive dims (one or two 16-byte
+// loads per chunk); wave v owns the (max, sum) pairs of local heads HPW v ..
+// HPW v + HPW - 1
+template <int U, int HS, int HD = 256>
 struct AttnRegs {
-  static constexpr int HPW = HS / 4, EPT = HS, TPH = 256 / HS;
+  static constexpr int HPW = HS / 4, TPH = 256 / HS, EPT = HD / TPH;
   uint32_t pos;
   float m[HPW], l[HPW];
   float v[U][EPT];
 };
 
-template <int U, int HS>
-DEV void attn_issue(const ProArgs& p, AttnRegs<U, HS>& r) {
-  using R = AttnRegs<U, HS>;
+template <int U, int HS, int HD>
+DEV void attn_issue(const ProArgs& p, AttnRegs<U, HS, HD>& r) {
+  using R = AttnRegs<U, HS, HD>;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int hb = HS == 8 ? 0 : HS * (int)blockIdx.y;  // the slice's first head
+  const int hb = HS * (int)blockIdx.y;  // the slice's first head
   r.pos = p.params[p.window > 0 ? 0 : p.kv_idx];
   const int c = min(lane, p.gch - 1);
 #pragma unroll
@@ -204,17 +209,17 @@ DEV void attn_issue(const ProArgs& p, AttnRegs<U, HS>& r) {
   const int h = hb + threadIdx.x / R::TPH, d0 = (threadIdx.x % R::TPH) * R::EPT;
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    ld_floats<R::EPT>(p.part_o + ((int64_t)h * p.gch + min(u, p.gch - 1)) * 256 + d0, r.v[u]);
+    ld_floats<R::EPT>(p.part_o + ((int64_t)h * p.gch + min(u, p.gch - 1)) * HD + d0, r.v[u]);
 }
 
-template <int U, int HS>
-DEV void attn_finish(const ProArgs& p, AttnRegs<U, HS>& r, uint16_t* xs, float* wts) {
-  using R = AttnRegs<U, HS>;
+template <int U, int HS, int HD>
+DEV void attn_finish(const ProArgs& p, AttnRegs<U, HS, HD>& r, uint16_t* xs, float* wts) {
+  using R = AttnRegs<U, HS, HD>;
   const int pos = (int)r.pos;
   const int lo = (p.window > 0 && pos + 1 > p.window) ? pos + 1 - p.window : 0;
   const int nch = (pos + 1 - lo + (1 << p.chunk_shift) - 1) >> p.chunk_shift;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int hb = HS == 8 ? 0 : HS * (int)blockIdx.y;
+  const int hb = HS * (int)blockIdx.y;
   const bool live = lane < nch;
 #pragma unroll
   for (int hh = 0; hh < R::HPW; ++hh) {
@@ -241,7 +246,7 @@ DEV void attn_finish(const ProArgs& p, AttnRegs<U, HS>& r, uint16_t* xs, float* 
   for (int c0 = U; c0 < nch; c0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      ld_floats<R::EPT>(p.part_o + ((int64_t)h * p.gch + min(c0 + u, nch - 1)) * 256 + d0, r.v[u]);
+      ld_floats<R::EPT>(p.part_o + ((int64_t)h * p.gch + min(c0 + u, nch - 1)) * HD + d0, r.v[u]);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (c0 + u < nch) {
@@ -254,10 +259,11 @@ DEV void attn_finish(const ProArgs& p, AttnRegs<U, HS>& r, uint16_t* xs, float* 
   uint32_t pk[R::EPT / 2];
 #pragma unroll
   for (int j = 0; j < R::EPT / 2; ++j) pk[j] = (uint32_t)f2h(acc[2 * j]) | ((uint32_t)f2h(acc[2 * j + 1]) << 16);
-  if constexpr (R::EPT == 8)
-    *reinterpret_cast<uint4*>(xs + h * 256 + d0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-  else
-    *reinterpret_cast<uint2*>(xs + h * 256 + d0) = make_uint2(pk[0], pk[1]);
+  uint16_t* dst = xs + hl * HD + d0;  // the slice at offset 0
+#pragma unroll
+  for (int q = 0; q < R::EPT / 8; ++q)
+    reinterpret_cast<uint4*>(dst)[q] = make_uint4(pk[4 * q], pk[4 * q + 1], pk[4 * q + 2], pk[4 * q + 3]);
+  if constexpr (R::EPT == 4) *reinterpret_cast<uint2*>(dst) = make_uint2(pk[0], pk[1]);
   lds_sync();
 }
 
@@ -429,7 +435,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  static_assert(PROK >= kProAttn2, "prologue kind");
+  static_assert(PROK >= kProAttn4w, "prologue kind");
   static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1 && NWV == 4), "attention / tail prologue: f32, KW = 1");
   static_assert(R * BPL <= 64, "scale parity bits");
   __shared__ __align__(16) uint16_t xs_lds[PROK > 0 ? 256 * PROK : pro_attn(PROK) ? kProAttnH
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   // the attention prologue requests its first UA chunks up front (NA names
   // UA for this prologue: 8 or 16)
   constexpr int UA = (pro_attn(PROK) && NA > 1) ? NA : kProAttnFirst;
-  AttnRegs<UA, attn_hs(PROK)> ar;
+  AttnRegs<UA, attn_hs(PROK), attn_hd(PROK)> ar;
   if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
@@ -508,7 +514,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
     const bool in = jb < nbw;
     const int jc = in ? jb : 0;
     if constexpr (PROK != 0) {
-      const uint4* v = reinterpret_cast<const uint4*>(xs_lds) + (size_t)(jb0 + jc) * 4;
+      const uint4* v = reinterpret_cast<const uint4*>(xs_lds) + (size_t)((pro_attn(PROK) ? 0 : jb0) + jc) * 4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint4 t = v[i];
@@ -591,7 +597,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   static_assert(NWV == 4 || (KW == 1 && PROK >= 0), "wide workgroups: no column split, no attention prologue");
   static_assert(EPI != EPI_GEGLU || (R % 2 == 0), "GeGLU tiles hold (gate, up) pairs");
   static_assert(!(PROK && XLO), "the prologue produces f16 input");
-  static_assert(PROK >= kProAttn2, "prologue kind");
+  static_assert(PROK >= kProAttn4w, "prologue kind");
   static_assert(PROK >= 0 || (EPI == EPI_F32 && KW == 1 && NWV == 4), "attention / tail prologue: f32, KW = 1");
   static_assert(R * BPL <= 64, "scale parity bits");
   static_assert(R % NB == 0 && (EPI != EPI_GEGLU || RB % 2 == 0), "whole (gate, up) pairs per batch");
@@ -618,7 +624,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   // the attention prologue requests its first UA chunks up front (NA names
   // UA for this prologue: 8 or 16)
   constexpr int UA = (pro_attn(PROK) && NA > 1) ? NA : kProAttnFirst;
-  AttnRegs<UA, attn_hs(PROK)> ar;
+  AttnRegs<UA, attn_hs(PROK), attn_hd(PROK)> ar;
   if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
@@ -722,7 +728,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
       const bool in = jb < nbw;
       const int jc = in ? jb : 0;
       if constexpr (PROK != 0) {
-        const uint4* v = reinterpret_cast<const uint4*>(xs_lds) + (size_t)(jb0 + jc) * 4;
+        const uint4* v = reinterpret_cast<const uint4*>(xs_lds) + (size_t)((pro_attn(PROK) ? 0 : jb0) + jc) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint4 t = v[i];
@@ -941,21 +947,33 @@ bool launch_plain(const Cfg& c, const Launch& L) {
   return false;
 }
 
-// attention-combine prologue: 2048 columns, one block per lane.  (Reading 16
-// chunks up front for layers that allocate more than 8 measured slower than
-// a second pass: the loads cannot be trimmed to the live chunks without
-// waiting for the position first.)
+// attention-combine prologue: 1024 or 2048 columns a slice, one block per
+// lane.  (Reading 16 chunks up front for layers that allocate more than 8
+// measured slower than a second pass: the loads cannot be trimmed to the
+// live chunks without waiting for the position first.)
 inline bool launch_pro_attn(const Cfg& c, const Launch& L) {
-  // 16 chunks (a sliding layer in 32-position chunks) in one pass
-  if (L.ks == 2) {
-    // two column slices of 4 heads (1024 columns: 32 lanes per row)
-    if (c.bpl != 1 || c.lpr != 32) return false;
+  if (c.bpl != 1) return false;
+  const int hd = L.pa.head_dim ? L.pa.head_dim : 256;
+  if (L.ks == 1) {
+    // all 8 heads of 256 dims
+    if (c.lpr != 64 || hd != 256) return false;
+    // 16 chunks (a sliding layer in 32-position chunks) in one pass
+    if (L.pa.gch == 16) return launch_r<64, 1, 1, false, EPI_F32, kProAttn, 16>(c, L);
+    return launch_r<64, 1, 1, false, EPI_F32, kProAttn>(c, L);
+  }
+  if (hd == 256) {
+    // column slices of 4 heads of 256 (1024 columns: 32 lanes per row)
+    if (c.lpr != 32) return false;
+#ifndef E4B_TUNE_ATTN_U16_ANY
+    if (L.pa.gch == 16 && L.pa.chunk_shift == 5) return launch_r<32, 1, 1, false, EPI_F32, kProAttn2, 16>(c, L);
+#else
     if (L.pa.gch == 16) return launch_r<32, 1, 1, false, EPI_F32, kProAttn2, 16>(c, L);
+#endif
     return launch_r<32, 1, 1, false, EPI_F32, kProAttn2>(c, L);
   }
-  if (c.bpl != 1 || c.lpr != 64) return false;
-  if (L.pa.gch == 16) return launch_r<64, 1, 1, false, EPI_F32, kProAttn, 16>(c, L);
-  return launch_r<64, 1, 1, false, EPI_F32, kProAttn>(c, L);
+  // column slices of 4 heads of 512 (2048 columns)
+  if (c.lpr != 64) return false;
+  return launch_r<64, 1, 1, false, EPI_F32, kProAttn4w>(c, L);
 }
 
 // A4B boundary prologue (the x vector comes from LDS): lane splits

@@ -41,7 +41,9 @@ def tag_name(tag: int) -> str:
         epi = (v >> 5) & 7
         r = 1 << ((v >> 8) & 15)
         kind = {0: "f32", 1: "geglu", 2: "gelu_mul"}.get(epi, str(epi))
-        pro = {0: "", -1: " attn-combine prologue", -2: " layer-boundary prologue"}.get(prok, f" prologue H={256 * prok}")
+        pro = {0: "", -1: " attn-combine prologue", -2: " layer-boundary prologue",
+               -3: " attn-combine prologue (4 heads of 256 a slice)",
+               -4: " attn-combine prologue (4 heads of 512 a slice)"}.get(prok, f" prologue H={256 * prok}")
         extra = (" kw4" if (v >> 12) & 1 else "") + (" ksplit" if (v >> 13) & 1 else "") + \
             (" batched" if (v >> 14) & 1 else "")
         return f"q40 {kind} r{r}{pro}{extra}"
