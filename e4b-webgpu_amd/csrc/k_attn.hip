@@ -87,8 +87,25 @@ DEV float xmax32(float v) {
 // 64/LV positions per load (LV = lanes per position).  With NW = 8 waves 4
 // and 5 prep the new k and v rows; with NW = 4 waves 0 and 1 prep them after
 // their q heads, in the chunk that owns the token only.
+//
+// The leading scalar arguments repeat the fields the first requests need
+// (params, qkv, qw, kw, rope; qh | kvh << 16; pos; the index of the token's
+// slot in params: 0 on sliding layers, kv_idx on full ones): the library is built with
+// -amdgpu-kernarg-preload-count, so they arrive in SGPRs with the wave and
+// no request waits for a kernel-argument load (struct arguments are not
+// preloaded).
 template <int CS, int NS, int NW = 8, bool RAW = false>
-__global__ __launch_bounds__(64 * NW) void k_attn_split(AttnArgs A) {
+__global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams, const float* lqkv, const float* lqw,
+                                                        const float* lkw, const float2* lrope, uint32_t lheads,
+                                                        uint32_t lpos, uint32_t lcur_idx, AttnArgs A) {
+  A.params = lparams;
+  A.qkv = lqkv;
+  A.qw = lqw;
+  A.kw = lkw;
+  A.rope = lrope;
+  A.qh = (int)(lheads & 0xffffu);
+  A.kvh = (int)(lheads >> 16);
+  A.pos = lpos;
   E4B_TRACE_SCOPE(trace_tag(TR_ATTN, A.window > 0 ? 0 : 1));
   constexpr int KP = CS / (4 * NW);  // score passes per wave (4 positions each)
   constexpr int VS = CS / NW;        // positions per wave
@@ -112,6 +129,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(AttnArgs A) {
   // numbering: the position for sliding rings, the entry count for full
   // layers (equal to the position until a compaction moves entries)
   const int pos = (int)(A.params ? A.params[0] : A.pos);
+  const int cur_raw = (int)(A.params ? A.params[lcur_idx] : A.pos);
   __builtin_amdgcn_sched_barrier(0);
   // 0a. the head-prep inputs do not depend on the position: they are
   //     requested while the position is in flight (this wave's q/k/v row,
@@ -132,7 +150,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(AttnArgs A) {
   const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
   const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
   __builtin_amdgcn_sched_barrier(0);
-  const int cur = A.window > 0 ? pos : (int)(A.params ? A.params[A.kv_idx] : A.pos);
+  const int cur = A.window > 0 ? pos : cur_raw;
   const int lo = (A.window > 0 && cur + 1 > A.window) ? cur + 1 - A.window : 0;
   const int n = cur + 1 - lo;
   const int nch = (n + CS - 1) / CS;  // live chunks; the rest of the grid idles
@@ -504,30 +522,33 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   A.window = a.window;
   A.eps = a.eps;
   if (a.vslices != 2 && a.vslices != 4) return e4b_fail(E4B_EINVAL, "attention: %d V slices (2 or 4)", a.vslices);
+  if (a.qh > 0xffff || a.kvh > 0xffff) return e4b_fail(E4B_EINVAL, "attention: %d q / %d KV heads", a.qh, a.kvh);
+#define ATTN_LEAD(A) A.params, A.qkv, A.qw, A.kw, A.rope, (uint32_t)A.qh | (uint32_t)A.kvh << 16, A.pos, \
+                     (uint32_t)(A.window > 0 ? 0 : A.kv_idx), A
   const dim3 grid(a.kvh, nch, a.vslices);
   if (a.vslices == 4) {
     // 4 waves a block, 64-dim V slices
     if (a.chunk == 64) {
       if (A.raw)
-        hipLaunchKernelGGL((k_attn_split<64, 4, 4, true>), grid, dim3(256), 0, st, A);
+        hipLaunchKernelGGL((k_attn_split<64, 4, 4, true>), grid, dim3(256), 0, st, ATTN_LEAD(A));
       else
-        hipLaunchKernelGGL((k_attn_split<64, 4, 4>), grid, dim3(256), 0, st, A);
+        hipLaunchKernelGGL((k_attn_split<64, 4, 4>), grid, dim3(256), 0, st, ATTN_LEAD(A));
     } else {
       if (A.raw)
-        hipLaunchKernelGGL((k_attn_split<32, 4, 4, true>), grid, dim3(256), 0, st, A);
+        hipLaunchKernelGGL((k_attn_split<32, 4, 4, true>), grid, dim3(256), 0, st, ATTN_LEAD(A));
       else
-        hipLaunchKernelGGL((k_attn_split<32, 4, 4>), grid, dim3(256), 0, st, A);
+        hipLaunchKernelGGL((k_attn_split<32, 4, 4>), grid, dim3(256), 0, st, ATTN_LEAD(A));
     }
   } else if (a.chunk == 64) {
     if (A.raw)
-      hipLaunchKernelGGL((k_attn_split<64, 2, 8, true>), grid, dim3(512), 0, st, A);
+      hipLaunchKernelGGL((k_attn_split<64, 2, 8, true>), grid, dim3(512), 0, st, ATTN_LEAD(A));
     else
-      hipLaunchKernelGGL((k_attn_split<64, 2, 8>), grid, dim3(512), 0, st, A);
+      hipLaunchKernelGGL((k_attn_split<64, 2, 8>), grid, dim3(512), 0, st, ATTN_LEAD(A));
   } else {
     if (A.raw)
-      hipLaunchKernelGGL((k_attn_split<32, 2, 8, true>), grid, dim3(512), 0, st, A);
+      hipLaunchKernelGGL((k_attn_split<32, 2, 8, true>), grid, dim3(512), 0, st, ATTN_LEAD(A));
     else
-      hipLaunchKernelGGL((k_attn_split<32, 2, 8>), grid, dim3(512), 0, st, A);
+      hipLaunchKernelGGL((k_attn_split<32, 2, 8>), grid, dim3(512), 0, st, ATTN_LEAD(A));
   }
   if (a.combine) {
     if (a.chunk == 64)

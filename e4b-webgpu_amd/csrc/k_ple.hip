@@ -27,10 +27,28 @@ constexpr float kTwo24 = 16777216.0f;
 // PROK = H / 256: lanes per gate row LPR = H / 32 = 8 PROK, G = 8 / PROK
 // groups per wave, R = PROK rows per group, 8 gate rows per wave; Q row
 // quarters (blockIdx.y), PR = PROK / Q projection rows per thread.
+//
+// The leading scalar arguments repeat the pointers the first requests need
+// (the prologue's hin, a, w1; the gate and projection planes): the library
+// is built with -amdgpu-kernarg-preload-count, so they arrive in SGPRs with
+// the wave and no request waits for a kernel-argument load (struct
+// arguments are not preloaded); H and the gate's blocks per row follow from
+// PROK.
 template <int PROK, int Q, int NA>
-__global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
+__global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la, const float* lw1,
+                                             const uint4* lgnib, const uint16_t* lgsc, const uint4* lpnib,
+                                             const uint16_t* lpsc, PleLaunch A, ProArgs pa) {
   E4B_TRACE_SCOPE(trace_tag(TR_PLE, 0));
   constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK, PR = PROK / Q;
+  pa.hin = lhin;
+  pa.a = la;
+  pa.w1 = lw1;
+  pa.H = H;
+  A.gate.nib = lgnib;
+  A.gate.sc = lgsc;
+  A.gate.nb = H / 32;
+  A.proj_nib = lpnib;
+  A.proj_sc = lpsc;
   static_assert(G * R == 8, "8 gate rows per wave");
   static_assert(PR * Q == PROK, "whole projection rows per thread");
   __shared__ __align__(16) uint16_t xs[H];
@@ -66,7 +84,9 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
     podd |= (uint32_t)(e & 1) << i;
   }
   // the per-layer input of the gate row this lane finishes (lanes that finish
-  // no row load a valid neighbour and drop it)
+  // no row load a valid neighbour and drop it); requested last, as its
+  // pointer is not among the preloaded arguments
+  __builtin_amdgcn_sched_barrier(0);
   const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
   E4B_TRACE_MARK(0);
@@ -128,13 +148,14 @@ __global__ __launch_bounds__(256) void k_ple(PleLaunch A, ProArgs pa) {
 
 }  // namespace
 
+#define PLE_LEAD(A, pa) pa.hin, pa.a, pa.w1, A.gate.nib, A.gate.sc, A.proj_nib, A.proj_sc, A, pa
 template <int NA>
 static void launch_ple_na(const PleLaunch& A, const ProArgs& pa, hipStream_t st) {
   switch (A.H) {
-    case 256: hipLaunchKernelGGL((k_ple<1, 1, NA>), dim3(A.PD / 32, 1), dim3(256), 0, st, A, pa); break;
-    case 512: hipLaunchKernelGGL((k_ple<2, 2, NA>), dim3(A.PD / 32, 2), dim3(256), 0, st, A, pa); break;
-    case 1024: hipLaunchKernelGGL((k_ple<4, 4, NA>), dim3(A.PD / 32, 4), dim3(256), 0, st, A, pa); break;
-    case 2048: hipLaunchKernelGGL((k_ple<8, 8, NA>), dim3(A.PD / 32, 8), dim3(256), 0, st, A, pa); break;
+    case 256: hipLaunchKernelGGL((k_ple<1, 1, NA>), dim3(A.PD / 32, 1), dim3(256), 0, st, PLE_LEAD(A, pa)); break;
+    case 512: hipLaunchKernelGGL((k_ple<2, 2, NA>), dim3(A.PD / 32, 2), dim3(256), 0, st, PLE_LEAD(A, pa)); break;
+    case 1024: hipLaunchKernelGGL((k_ple<4, 4, NA>), dim3(A.PD / 32, 4), dim3(256), 0, st, PLE_LEAD(A, pa)); break;
+    case 2048: hipLaunchKernelGGL((k_ple<8, 8, NA>), dim3(A.PD / 32, 8), dim3(256), 0, st, PLE_LEAD(A, pa)); break;
   }
 }
 

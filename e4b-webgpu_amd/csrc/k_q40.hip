@@ -22,6 +22,8 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
                     W.nb);
   const int nbk = W.nb / ks;
   if (nbk < 1) return e4b_fail(E4B_EINVAL, "q4_0 GEMV: empty row");
+  if (W.nb > 0xffff)  // the kernels take nb and nbk packed in 16 bits each (Q40_LEAD_PARAMS)
+    return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per row exceeds 65535", W.nb);
   if (pro && pro->part_o) {
     // one slice of 8 heads of 256 (ks = 1) or ks slices of 4 heads of 256 or 512
     const int hd = pro->head_dim ? pro->head_dim : 256;

@@ -193,12 +193,14 @@ struct AttnRegs {
   float v[U][EPT];
 };
 
+// pos_idx: params[pos_idx] is the token's slot (0 on sliding layers, kv_idx
+// on counted full layers)
 template <int U, int HS, int HD>
-DEV void attn_issue(const ProArgs& p, AttnRegs<U, HS, HD>& r) {
+DEV void attn_issue(const ProArgs& p, AttnRegs<U, HS, HD>& r, int pos_idx) {
   using R = AttnRegs<U, HS, HD>;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int hb = HS * (int)blockIdx.y;  // the slice's first head
-  r.pos = p.params[p.window > 0 ? 0 : p.kv_idx];
+  r.pos = p.params[pos_idx];
   const int c = min(lane, p.gch - 1);
 #pragma unroll
   for (int hh = 0; hh < R::HPW; ++hh) {
@@ -412,6 +414,55 @@ DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, f
   lds_sync();
 }
 
+// Leading scalar kernel arguments.  The library is built with
+// -amdgpu-kernarg-preload-count, so the dispatcher writes the first 14
+// dwords of a kernel's arguments into SGPRs before its waves start; struct
+// arguments are not preloaded.  Everything a wave needs to issue its first
+// requests (the weight planes, their shape, the prologue's input pointers)
+// therefore comes first, ahead of the structs, and overwrites the structs'
+// copies of the same fields: no request waits for a kernel-argument load
+// (0.24 us a wave measured on MI355X).  lp0..lp3 by prologue:
+//   PROK > 0 (residual + norm): hin, a, w1, w2;
+//   attention combine: params, part_ml, part_o, and gch | pos_idx << 32 as
+//   lp3's bits;
+//   none: xh, xl (lp2, lp3 unused);  layer boundary: unused (its prologue
+//   reads the struct).
+// (lp3 is pointer-typed so that w2 keeps the global address space of a
+// kernel pointer argument; an integer cast back would make its load a flat
+// one, which the compiler can only wait for with vmcnt(0).)
+// ldims = nb | nbk << 16; lunits = rows (2 ff for EPI_GEGLU).
+#define Q40_LEAD_PARAMS                                                                                   \
+  const uint4 *__restrict__ lnib, const uint16_t *__restrict__ lsc, const void *lp0, const void *lp1,    \
+      const void *lp2, const void *lp3, uint32_t ldims, uint32_t lunits
+
+template <int PROK, int EPI>
+DEV void take_lead(const uint4* lnib, const uint16_t* lsc, const void* lp0, const void* lp1, const void* lp2,
+                   const void* lp3, uint32_t ldims, uint32_t lunits, Q40Mat& W, const uint32_t* __restrict__& xh,
+                   const uint32_t* __restrict__& xl, GemvOut& o, ProArgs& pa, int& nbk, int& pos_idx) {
+  W.nib = lnib;
+  W.sc = lsc;
+  W.nb = (int)(ldims & 0xffffu);
+  nbk = (int)(ldims >> 16);
+  if constexpr (EPI == EPI_GEGLU) o.ff = lunits >> 1; else W.rows = lunits;
+  if constexpr (PROK > 0) {
+    pa.hin = static_cast<const float*>(lp0);
+    pa.a = static_cast<const float*>(lp1);
+    pa.w1 = static_cast<const float*>(lp2);
+    pa.w2 = static_cast<const float*>(lp3);
+    pa.H = 256 * PROK;
+  } else if constexpr (pro_attn(PROK)) {
+    pa.params = static_cast<const uint32_t*>(lp0);
+    pa.part_ml = static_cast<const float*>(lp1);
+    pa.part_o = static_cast<const float*>(lp2);
+    const uint64_t bits = (uint64_t)(uintptr_t)lp3;
+    pa.gch = (int)(uint32_t)bits;
+    pos_idx = (int)(bits >> 32);
+  } else if constexpr (PROK == 0) {
+    xh = static_cast<const uint32_t*>(lp0);
+    xl = static_cast<const uint32_t*>(lp1);
+  }
+}
+
 // A wave splits into G = 64/LPR lane groups; with KW = 1 a group owns R rows
 // ("slots") of the wave's tile, with KW = 4 the four waves share the tile's
 // rows and each covers a quarter of the columns.  Lane l of a group covers
@@ -423,9 +474,8 @@ DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, f
 // compiler's wait counts stay exact and a fused prologue computes while the
 // weight stream is in flight.
 template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4>
-__global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __restrict__ xh,
-                                                  const uint32_t* __restrict__ xl, GemvOut o, int64_t ntiles,
-                                                  int nbk, ProArgs pa) {
+__global__ __launch_bounds__(64 * NWV) void k_q40(Q40_LEAD_PARAMS, Q40Mat W, const uint32_t* __restrict__ xh,
+                                                  const uint32_t* __restrict__ xl, GemvOut o, ProArgs pa) {
   constexpr int G = 64 / LPR, SPAN = LPR / R, SLOTS = G * R;
   constexpr int TPB = 64 * NWV;
   [[maybe_unused]] constexpr uint32_t kLog2R = R >= 16 ? 4 : R >= 8 ? 3 : R >= 4 ? 2 : R >= 2 ? 1 : 0;
@@ -446,6 +496,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
+  int nbk = 0, pos_idx = 0;
+  take_lead<PROK, EPI>(lnib, lsc, lp0, lp1, lp2, lp3, ldims, lunits, W, xh, xl, o, pa, nbk, pos_idx);
+  const int64_t ntiles = ((int64_t)lunits + SLOTS - 1) / SLOTS;
   const int kslice = blockIdx.y;
   const int nbw = nbk / KW;  // blocks per wave
   const int jb0 = kslice * nbk + (KW == 4 ? wave * nbw : 0);
@@ -462,7 +515,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
   // UA for this prologue: 8 or 16)
   constexpr int UA = (pro_attn(PROK) && NA > 1) ? NA : kProAttnFirst;
   AttnRegs<UA, attn_hs(PROK), attn_hd(PROK)> ar;
-  if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
+  if constexpr (pro_attn(PROK)) attn_issue(pa, ar, pos_idx);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
   // the prologue's requests stay ahead of the weight requests (vmcnt drains in order)
@@ -584,9 +637,8 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40Mat W, const uint32_t* __re
 // microseconds) and a prologue's block barriers wait only for batch 0.
 template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4, int NB = 2,
           int PRE = 1, int LB = 1>
-__global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __restrict__ xh,
-                                                  const uint32_t* __restrict__ xl, GemvOut o, int64_t ntiles,
-                                                  int nbk, ProArgs pa) {
+__global__ __launch_bounds__(64 * NWV) void k_q40b(Q40_LEAD_PARAMS, Q40Mat W, const uint32_t* __restrict__ xh,
+                                                  const uint32_t* __restrict__ xl, GemvOut o, ProArgs pa) {
   constexpr int G = 64 / LPR, SPAN = LPR / R, SLOTS = G * R;
   constexpr int TPB = 64 * NWV;
   constexpr int RB = R / NB;  // rows per batch
@@ -609,6 +661,9 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / LPR, l = lane - g * LPR;
+  int nbk = 0, pos_idx = 0;
+  take_lead<PROK, EPI>(lnib, lsc, lp0, lp1, lp2, lp3, ldims, lunits, W, xh, xl, o, pa, nbk, pos_idx);
+  const int64_t ntiles = ((int64_t)lunits + SLOTS - 1) / SLOTS;
   const int kslice = blockIdx.y;
   const int nbw = nbk / KW;  // blocks per wave
   const int jb0 = kslice * nbk + (KW == 4 ? wave * nbw : 0);
@@ -625,7 +680,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40Mat W, const uint32_t* __r
   // UA for this prologue: 8 or 16)
   constexpr int UA = (pro_attn(PROK) && NA > 1) ? NA : kProAttnFirst;
   AttnRegs<UA, attn_hs(PROK), attn_hd(PROK)> ar;
-  if constexpr (pro_attn(PROK)) attn_issue(pa, ar);
+  if constexpr (pro_attn(PROK)) attn_issue(pa, ar, pos_idx);
   TailRegs tr;
   if constexpr (PROK == kProTail) tail_issue(pa, tr);
 
@@ -871,12 +926,27 @@ void launch(const Launch& L) {
   constexpr int G = 64 / LPR;
   const int64_t ntiles = (L.units + G * R - 1) / (G * R);
   const int64_t wgs = KW == 1 ? (ntiles + NWV - 1) / NWV : ntiles;  // one tile per wave
+  // the leading scalar arguments (Q40_LEAD_PARAMS); k_q40.hip checks the
+  // packed shape fields
+  const void *p0 = nullptr, *p1 = nullptr, *p2 = nullptr, *p3 = nullptr;
+  if constexpr (PROK > 0) {
+    p0 = L.pa.hin; p1 = L.pa.a; p2 = L.pa.w1; p3 = L.pa.w2;
+  } else if constexpr (pro_attn(PROK)) {
+    p0 = L.pa.params; p1 = L.pa.part_ml; p2 = L.pa.part_o;
+    p3 = (const void*)(uintptr_t)((uint64_t)(uint32_t)L.pa.gch |
+                                  (uint64_t)(uint32_t)(L.pa.window > 0 ? 0 : L.pa.kv_idx) << 32);
+  } else if constexpr (PROK == 0) {
+    p0 = L.xh; p1 = L.xl;
+  }
+  const uint32_t dims = (uint32_t)L.W.nb | (uint32_t)L.nbk << 16;
   if constexpr (NB == 1)
     hipLaunchKernelGGL((k_q40<LPR, BPL, R, KW, XLO, EPI, PROK, NA, NWV>), dim3((unsigned)wgs, (unsigned)L.ks),
-                       dim3(64 * NWV), 0, L.st, L.W, L.xh, L.xl, L.o, ntiles, L.nbk, L.pa);
+                       dim3(64 * NWV), 0, L.st, L.W.nib, L.W.sc, p0, p1, p2, p3, dims, (uint32_t)L.units, L.W,
+                       L.xh, L.xl, L.o, L.pa);
   else
     hipLaunchKernelGGL((k_q40b<LPR, BPL, R, KW, XLO, EPI, PROK, NA, NWV, NB, PRE, LB>), dim3((unsigned)wgs, (unsigned)L.ks),
-                       dim3(64 * NWV), 0, L.st, L.W, L.xh, L.xl, L.o, ntiles, L.nbk, L.pa);
+                       dim3(64 * NWV), 0, L.st, L.W.nib, L.W.sc, p0, p1, p2, p3, dims, (uint32_t)L.units, L.W,
+                       L.xh, L.xl, L.o, L.pa);
 }
 
 template <int LPR, int BPL, int KW, bool XLO, int EPI, int PROK, int NA = 1>
