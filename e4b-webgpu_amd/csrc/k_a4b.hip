@@ -112,14 +112,15 @@ __global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ h_in,
 struct Live {
   int cur, lo, n;
 };
-DEV Live live_of(const AttnGen& A) {
-  const int pos = (int)A.params[0];
+// (from the loaded position and slot word params[kv_idx])
+DEV Live live_at(const AttnGen& A, int pos, int slot) {
   Live L;
-  L.cur = A.window > 0 ? pos : (int)A.params[A.kv_idx];
+  L.cur = A.window > 0 ? pos : slot;
   L.lo = (A.window > 0 && L.cur + 1 > A.window) ? L.cur + 1 - A.window : 0;
   L.n = L.cur + 1 - L.lo;
   return L;
 }
+DEV Live live_of(const AttnGen& A) { return live_at(A, (int)A.params[0], (int)A.params[A.kv_idx]); }
 
 // Block (KV group g, chunk c, V slice z), 8 waves.  Every load is issued
 // before any math: the head-prep rows of the wave (q heads g GQA + r, the k
@@ -133,8 +134,28 @@ DEV Live live_of(const AttnGen& A) {
 // the chunk's 64 positions; P.V with the weights broadcast from LDS, folded
 // over the 8 waves.  A chunk's K is read by all HD / 128 slices (from L2
 // after the first); V is split across them.
+//
+// The leading scalar arguments repeat the fields the first requests need
+// (params, qkv, qw, kw, rope; qh | kvh << 16 | keqv << 31; angles; the
+// index of the token's slot word in params: 0 on sliding layers, kv_idx on
+// full ones): the library is built with -amdgpu-kernarg-preload-count, so
+// they arrive in SGPRs with the wave and no request waits for a
+// kernel-argument load (struct arguments are not preloaded).  The head-prep
+// rows and the RoPE table do not depend on the position: they are requested
+// while the position is in flight.
 template <int HD, int GQA, bool RAW>
-__global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
+__global__ __launch_bounds__(512) void k_attn_gen(const uint32_t* lparams, const float* lqkv, const float* lqw,
+                                                  const float* lkw, const float2* lrope, uint32_t lheads,
+                                                  uint32_t langles, uint32_t lslot_idx, AttnGen A) {
+  A.params = lparams;
+  A.qkv = lqkv;
+  A.qw = lqw;
+  A.kw = lkw;
+  A.rope = lrope;
+  A.qh = (int)(lheads & 0x7fffu);
+  A.kvh = (int)((lheads >> 16) & 0x7fffu);
+  A.keqv = (lheads >> 31) != 0;
+  A.angles = (int)langles;
   E4B_TRACE_SCOPE(trace_tag(TR_ATTN_GEN, HD));
   constexpr int NW = 8, CS = kAttnGenChunk, PER = HD / 64, PW = CS / NW, VD = 128;
   constexpr int NR = GQA + 2, RPW = (NR + NW - 1) / NW, LPH = 64 / GQA;
@@ -147,21 +168,16 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
   __shared__ __align__(16) float po[NW][GQA][VD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = blockIdx.x, c = blockIdx.y, zs = blockIdx.z;
-  const Live L = live_of(A);
-  const int nch = (L.n + CS - 1) / CS;
-  if (c >= nch) return;
-  const int c_lo = L.lo + c * CS;
-  const int m = min(CS, L.n - c * CS);
-  uint16_t* kc = A.kc + (int64_t)g * A.slots * HD;
-  uint16_t* vc = A.vc + (int64_t)g * A.slots * HD;
-  // one modulo per block: j < m <= window <= slots, the ring wraps at most once
-  const int s_lo = A.window > 0 ? c_lo % A.slots : c_lo;
-  auto slot_at = [&](int j) -> int64_t {
-    const int s = s_lo + j;
-    return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
-  };
+  const uint32_t pos_w = A.params[0], slot_w = A.params[lslot_idx];
+  // the cache pointers (kernel-argument loads) are requested here too and
+  // consumed after the position wait below, so the K/V requests do not wait
+  // for a second kernel-argument round trip
+  uint16_t* kc0 = A.kc;
+  uint16_t* vc0 = A.vc;
+  __builtin_amdgcn_sched_barrier(0);
 
-  // 0. loads: head-prep rows and weights, the wave's K rows and V dims
+  // 0. loads: head-prep rows and weights and the RoPE table (while the
+  //    position is in flight), then the wave's K rows and V dims
   float xin[RPW][PER], win[RPW][PER];
 #pragma unroll
   for (int u = 0; u < RPW; ++u) {
@@ -184,6 +200,21 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
   float2 rc[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) rc[e] = rsrc[min(PER * (lane & 31) + e, max(A.angles - 1, 0))];
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::"s"(kc0), "s"(vc0));
+  const Live L = live_at(A, (int)pos_w, (int)slot_w);
+  const int nch = (L.n + CS - 1) / CS;
+  if (c >= nch) return;
+  const int c_lo = L.lo + c * CS;
+  const int m = min(CS, L.n - c * CS);
+  uint16_t* kc = kc0 + (int64_t)g * A.slots * HD;
+  uint16_t* vc = vc0 + (int64_t)g * A.slots * HD;
+  // one modulo per block: j < m <= window <= slots, the ring wraps at most once
+  const int s_lo = A.window > 0 ? c_lo % A.slots : c_lo;
+  auto slot_at = [&](int j) -> int64_t {
+    const int s = s_lo + j;
+    return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
+  };
   uint32_t kr[PW][PER / 2];
   uint32_t vr[PW];
 #pragma unroll
@@ -205,7 +236,7 @@ __global__ __launch_bounds__(512) void k_attn_gen(AttnGen A) {
   //    first `angles` pairs (p, p + HD/2) -- dim p of lane l < 32 pairs with
   //    the same register of lane l + 32
   const bool owner = c == nch - 1;  // the last live chunk holds the token, at j = m - 1
-  const float fpos = (float)A.params[0];
+  const float fpos = (float)pos_w;
 #pragma unroll
   for (int u = 0; u < RPW; ++u) {
     const int r = wave + NW * u;
@@ -624,14 +655,18 @@ int launch_rownorm(const float* h_in, float* h_out, const float* a, const float*
   return E4B_OK;
 }
 
+// k_attn_gen's leading scalar arguments (launch_attn_gen checks qh, kvh < 2^15)
+#define ATTN_GEN_LEAD(a)                                                                                    \
+  a.params, a.qkv, a.qw, a.kw, a.rope, (uint32_t)a.qh | (uint32_t)a.kvh << 16 | (uint32_t)a.keqv << 31,     \
+      (uint32_t)a.angles, (uint32_t)(a.window > 0 ? 0 : a.kv_idx), a
 template <int HD, bool RAW>
 static void launch_attn_hd_raw(const AttnGen& a, hipStream_t st) {
   const dim3 grid(a.kvh, a.gch, HD / 128);
   switch (a.qh / a.kvh) {
-    case 1: hipLaunchKernelGGL((k_attn_gen<HD, 1, RAW>), grid, dim3(512), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((k_attn_gen<HD, 2, RAW>), grid, dim3(512), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((k_attn_gen<HD, 4, RAW>), grid, dim3(512), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((k_attn_gen<HD, 8, RAW>), grid, dim3(512), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((k_attn_gen<HD, 1, RAW>), grid, dim3(512), 0, st, ATTN_GEN_LEAD(a)); break;
+    case 2: hipLaunchKernelGGL((k_attn_gen<HD, 2, RAW>), grid, dim3(512), 0, st, ATTN_GEN_LEAD(a)); break;
+    case 4: hipLaunchKernelGGL((k_attn_gen<HD, 4, RAW>), grid, dim3(512), 0, st, ATTN_GEN_LEAD(a)); break;
+    case 8: hipLaunchKernelGGL((k_attn_gen<HD, 8, RAW>), grid, dim3(512), 0, st, ATTN_GEN_LEAD(a)); break;
   }
 }
 template <int HD>
@@ -645,7 +680,7 @@ static void launch_attn_hd(const AttnGen& a, hipStream_t st) {
 
 int launch_attn_gen(const AttnGen& a, hipStream_t st) {
   const int gqa = a.kvh > 0 ? a.qh / a.kvh : 0;
-  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
+  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh > 0x7fff || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
       a.angles < 0 || a.angles > a.hd / 2 || a.slots <= 0 || a.gch <= 0 || (a.window > 0 && a.slots < a.window) ||
       (int64_t)a.gch * kAttnGenChunk < (a.window > 0 ? a.window : a.slots) || a.gch > kMergeMaxChunks ||
       (a.raw && a.window > 0))
@@ -660,7 +695,7 @@ int launch_attn_gen(const AttnGen& a, hipStream_t st) {
 }
 
 int launch_headprep_rows_gen(const HeadRowsGen& a, int M, hipStream_t st) {
-  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || a.angles < 0 || a.angles > a.hd / 2 ||
+  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh > 0x7fff || a.qh % a.kvh || a.angles < 0 || a.angles > a.hd / 2 ||
       a.slots <= 0 || (a.window > 0 && a.slots < a.window) || M < 1 || a.ld < (int64_t)(a.qh + a.kvh) * a.hd ||
       (a.window == 0 && (int64_t)a.p0 + M > a.slots))
     return e4b_fail(E4B_EINVAL, "head prep rows: head_dim %d, %d/%d heads, %d pairs, %d slots, %d tokens", a.hd, a.qh,
@@ -687,7 +722,7 @@ static void launch_attn_rows_hd(const AttnRowsGen& a, int M, hipStream_t st) {
 
 int launch_attn_rows_gen(const AttnRowsGen& a, int M, hipStream_t st) {
   const int gqa = a.kvh > 0 ? a.qh / a.kvh : 0;
-  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
+  if ((a.hd != 256 && a.hd != 512) || a.kvh <= 0 || a.qh > 0x7fff || a.qh % a.kvh || (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8) ||
       a.slots <= 0 || (a.window > 0 && a.slots < a.window) || M < 1 ||
       (a.window == 0 && (int64_t)a.p0 + M > a.slots))
     return e4b_fail(E4B_EINVAL, "attention rows: head_dim %d, %d/%d heads, %d slots, %d tokens from %u", a.hd, a.qh,

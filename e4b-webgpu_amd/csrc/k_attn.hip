@@ -130,6 +130,11 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams,
   // layers (equal to the position until a compaction moves entries)
   const int pos = (int)(A.params ? A.params[0] : A.pos);
   const int cur_raw = (int)(A.params ? A.params[lcur_idx] : A.pos);
+  // the cache pointers (kernel-argument loads) are requested here too and
+  // consumed after the position wait below, so the K/V requests do not wait
+  // for a second kernel-argument round trip
+  uint16_t* const kc0 = A.kc;
+  uint16_t* const vc0 = A.vc;
   __builtin_amdgcn_sched_barrier(0);
   // 0a. the head-prep inputs do not depend on the position: they are
   //     requested while the position is in flight (this wave's q/k/v row,
@@ -150,6 +155,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams,
   const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
   const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
   __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::"s"(kc0), "s"(vc0));
   const int cur = A.window > 0 ? pos : cur_raw;
   const int lo = (A.window > 0 && cur + 1 > A.window) ? cur + 1 - A.window : 0;
   const int n = cur + 1 - lo;
@@ -158,8 +164,8 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams,
   const int c_lo = lo + c * CS;
   const int m = min(CS, n - c * CS);
   const float fpos = (float)pos;
-  uint16_t* kc = A.kc + (int64_t)g * A.slots * HD;
-  uint16_t* vc = A.vc + (int64_t)g * A.slots * HD;
+  uint16_t* kc = kc0 + (int64_t)g * A.slots * HD;
+  uint16_t* vc = vc0 + (int64_t)g * A.slots * HD;
   // slot of position c_lo + j: one modulo per block; j < m <= window <= slots
   // so the ring index wraps at most once inside a chunk
   const int s_lo = A.window > 0 ? c_lo % A.slots : c_lo;
