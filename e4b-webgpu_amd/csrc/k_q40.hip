@@ -65,7 +65,15 @@ int launch_q40(const Q40Mat& W, const uint32_t* xh, const uint32_t* xl, int epi,
     c.bpl = nbk <= 64 ? 1 : (nbk + 31) / 32;
     c.r = 1;
     const int64_t per_wg = 4 * (64 / c.lpr);
-    while (c.r < 4 && (L.units + per_wg * 2 * c.r - 1) / (per_wg * 2 * c.r) >= 256) c.r *= 2;
+#ifndef E4B_TUNE_TAIL_MINWGS
+#define E4B_TUNE_TAIL_MINWGS 256
+#endif
+#ifdef E4B_TUNE_TAIL_R8
+    constexpr int rmax = 8;
+#else
+    constexpr int rmax = 4;
+#endif
+    while (c.r < rmax && (L.units + per_wg * 2 * c.r - 1) / (per_wg * 2 * c.r) >= E4B_TUNE_TAIL_MINWGS) c.r *= 2;
   }
   if (c.bpl > 8 || c.lpr * c.bpl * c.kw < nbk)
     return e4b_fail(E4B_EINVAL, "q4_0 GEMV: %d blocks per slice exceeds the 2048-block (65536-column) maximum", nbk);

@@ -1054,6 +1054,9 @@ bool launch_pro_tail_r(const Cfg& c, const Launch& L) {
     case 1: launch<LPR, BPL, 1, 1, false, EPI_F32, kProTail>(L); return true;
     case 2: launch<LPR, BPL, 2, 1, false, EPI_F32, kProTail>(L); return true;
     case 4: launch<LPR, BPL, 4, 1, false, EPI_F32, kProTail>(L); return true;
+#ifdef E4B_TUNE_TAIL_R8
+    case 8: launch<LPR, BPL, 8, 1, false, EPI_F32, kProTail>(L); return true;
+#endif
   }
   return false;
 }
