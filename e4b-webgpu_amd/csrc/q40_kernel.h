@@ -301,19 +301,26 @@ DEV void tail_issue(const ProArgs& p, TailRegs& r) {
   const bool has_a = p.a != nullptr;
   const float* a = has_a ? p.a : p.hin;
   const float* a2 = has_a ? p.a2 : p.hin;
-  const float* w1 = has_a ? p.w1 : p.hin;
-  const float* w1b = has_a ? p.w1b : p.hin;
-  const float* wp = has_a ? p.wp : p.hin;
+  // the vectors whose pointers arrive as preloaded arguments first, then
+  // the three norm weights read from the argument struct
 #pragma unroll
   for (int k = 0; k < kProTailK; ++k) {
     const int q = min((int)threadIdx.x + 256 * k, H4 - 1);
     ld4(p.hin, q, r.h + 4 * k);
     ld4(a, q, r.a + 4 * k);
     ld4(a2, q, r.a2 + 4 * k);
+    ld4(p.w2, q, r.w2 + 4 * k);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const float* w1 = has_a ? p.w1 : p.hin;
+  const float* w1b = has_a ? p.w1b : p.hin;
+  const float* wp = has_a ? p.wp : p.hin;
+#pragma unroll
+  for (int k = 0; k < kProTailK; ++k) {
+    const int q = min((int)threadIdx.x + 256 * k, H4 - 1);
     ld4(w1, q, r.w1 + 4 * k);
     ld4(w1b, q, r.w1b + 4 * k);
     ld4(wp, q, r.wp + 4 * k);
-    ld4(p.w2, q, r.w2 + 4 * k);
   }
 }
 
@@ -425,8 +432,9 @@ DEV void pro_finish(const ProArgs& p, ProRegs<PROK, TPB, NA>& r, uint16_t* xs, f
 //   PROK > 0 (residual + norm): hin, a, w1, w2;
 //   attention combine: params, part_ml, part_o, and gch | pos_idx << 32 as
 //   lp3's bits;
-//   none: xh, xl (lp2, lp3 unused);  layer boundary: unused (its prologue
-//   reads the struct).
+//   layer boundary: hin, a, a2, w2 (H = 32 nb; w1, w1b and wp come from
+//   the struct and are requested after these);
+//   none: xh, xl (lp2, lp3 unused).
 // (lp3 is pointer-typed so that w2 keeps the global address space of a
 // kernel pointer argument; an integer cast back would make its load a flat
 // one, which the compiler can only wait for with vmcnt(0).)
@@ -457,6 +465,12 @@ DEV void take_lead(const uint4* lnib, const uint16_t* lsc, const void* lp0, cons
     const uint64_t bits = (uint64_t)(uintptr_t)lp3;
     pa.gch = (int)(uint32_t)bits;
     pos_idx = (int)(bits >> 32);
+  } else if constexpr (PROK == kProTail) {
+    pa.hin = static_cast<const float*>(lp0);
+    pa.a = static_cast<const float*>(lp1);
+    pa.a2 = static_cast<const float*>(lp2);
+    pa.w2 = static_cast<const float*>(lp3);
+    pa.H = 32 * (int)(ldims & 0xffffu);
   } else if constexpr (PROK == 0) {
     xh = static_cast<const uint32_t*>(lp0);
     xl = static_cast<const uint32_t*>(lp1);
@@ -935,6 +949,8 @@ void launch(const Launch& L) {
     p0 = L.pa.params; p1 = L.pa.part_ml; p2 = L.pa.part_o;
     p3 = (const void*)(uintptr_t)((uint64_t)(uint32_t)L.pa.gch |
                                   (uint64_t)(uint32_t)(L.pa.window > 0 ? 0 : L.pa.kv_idx) << 32);
+  } else if constexpr (PROK == kProTail) {
+    p0 = L.pa.hin; p1 = L.pa.a; p2 = L.pa.a2; p3 = L.pa.w2;
   } else if constexpr (PROK == 0) {
     p0 = L.xh; p1 = L.xl;
   }
