@@ -41,6 +41,24 @@
 #define E4B_TUNE_KW4_LB 2
 #endif
 
+// waves, batches and batches requested ahead of the plain f32 GEMV tile of
+// 8 rows x 64 blocks (measured on MI355X for c0, 16384 x 2048 with f32 x:
+// the whole tile requested up front and multiplied in 2 batches 5.23 us,
+// against 6.21 unbatched, 5.34 with one batch ahead, 5.39 in 4 batches,
+// 6.35 / 5.33 with 8-wave workgroups)
+#ifndef E4B_TUNE_PLAIN_NWV
+#define E4B_TUNE_PLAIN_NWV 4
+#endif
+#ifndef E4B_TUNE_PLAIN_NB
+#define E4B_TUNE_PLAIN_NB 2
+#endif
+#ifndef E4B_TUNE_PLAIN_PRE
+#define E4B_TUNE_PLAIN_PRE 2
+#endif
+#ifndef E4B_TUNE_PLAIN_LB
+#define E4B_TUNE_PLAIN_LB 2
+#endif
+
 // rows per wave and waves per workgroup of the fused-prologue GeGLU tile
 #ifndef E4B_TUNE_GEGLU_R
 #define E4B_TUNE_GEGLU_R 8
@@ -991,6 +1009,10 @@ bool launch_r(const Cfg& c, const Launch& L) {
         // unbatched, 791-793 with 4 batches; batching the qkv and o tiles
         // measured slower)
         launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_KW4_NB, E4B_TUNE_KW4_PRE, E4B_TUNE_KW4_LB>(L);
+      } else if constexpr (KW == 1 && EPI == EPI_F32 && PROK == 0 && LPR == 64 && BPL == 1) {
+        // the plain f32 GEMV of 64-block rows (c0, the PLE model projection)
+        launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA, E4B_TUNE_PLAIN_NWV, E4B_TUNE_PLAIN_NB, E4B_TUNE_PLAIN_PRE,
+               E4B_TUNE_PLAIN_LB>(L);
       } else {
         launch<LPR, BPL, 8, KW, XLO, EPI, PROK, NA>(L);
       }
