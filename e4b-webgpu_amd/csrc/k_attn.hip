@@ -394,8 +394,10 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams,
   }
 }
 
-// log-sum-exp merge of the live chunks (kernels/attcomb.wgsl:10-36): one block
-// per q head, thread d = output dim d.
+// log-sum-exp merge of the live chunks (kernels/attcomb.wgsl:10-36): block
+// (h, y) merges q head h's output dims [64 y, 64 y + 64); wave g of the block
+// accumulates chunks g, g + 4, ... of its lane's dim (every chunk's partial
+// requested before the first use), and the four wave sums are added in LDS.
 template <int CS>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
                                                       const float* __restrict__ part_ml, const uint32_t* params,
@@ -403,7 +405,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
                                                       uint16_t* __restrict__ out) {
   __shared__ float wt[kAttnMaxChunks];
   __shared__ float red[4];
-  const int h = blockIdx.x, d = threadIdx.x;
+  __shared__ float sums[4][64];
+  const int h = blockIdx.x, d = 64 * (int)blockIdx.y + (threadIdx.x & 63), grp = threadIdx.x >> 6;
   const int pos = (int)(params ? params[window > 0 ? 0 : kv_idx] : pos_imm);
   const int lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
   const int nch = (pos + 1 - lo + CS - 1) / CS;
@@ -422,9 +425,14 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
   lds_sync();
   const float* po = part_o + (int64_t)h * gch * HD + d;
   float acc = 0.f;
-#pragma unroll 8
-  for (int cc = 0; cc < nch; ++cc) acc = fmaf(po[(int64_t)cc * HD], wt[cc], acc);
-  out[h * HD + d] = f2h(acc / den);
+#pragma unroll 16
+  for (int cc = grp; cc < nch; cc += 4) acc = fmaf(po[(int64_t)cc * HD], wt[cc], acc);
+  sums[grp][threadIdx.x & 63] = acc;
+  lds_sync();
+  if (grp == 0) {
+    const int t = threadIdx.x;
+    out[h * HD + d] = f2h((sums[0][t] + sums[1][t] + sums[2][t] + sums[3][t]) / den);
+  }
 }
 
 // attention mass of a scored full layer (kernels/attnos.wgsl:78-92, SCORE =
@@ -558,10 +566,10 @@ int launch_attn(const AttnLaunch& a, hipStream_t st) {
   }
   if (a.combine) {
     if (a.chunk == 64)
-      hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+      hipLaunchKernelGGL(k_attn_combine<64>, dim3(a.qh, HD / 64), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
                          a.kv_idx, a.window, nch, a.out);
     else
-      hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
+      hipLaunchKernelGGL(k_attn_combine<32>, dim3(a.qh, HD / 64), dim3(256), 0, st, a.part_o, a.part_ml, a.params, a.pos,
                          a.kv_idx, a.window, nch, a.out);
   }
   E4B_HIP(hipGetLastError());
