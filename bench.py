@@ -52,10 +52,10 @@ GEGLU_TRAFFIC_BYTES = int(18609.6 * 1024 * 2.0 + 40.0 * 1024 * 1.0)
 # The same two counter runs for the other configs' timed kernels (per launch
 # or per layer; commands and raw values in profiles/gemv_c0.md,
 # profiles/lmhead_c1.md, profiles/attn_c2.md and profiles/moe_c3.md).
-C0_TRAFFIC_BYTES = int(9283.5 * 1024 * 2.0 + 64.0 * 1024)
+C0_TRAFFIC_BYTES = int(9289.4 * 1024 * 2.0 + 64.0 * 1024)
 C1_TRAFFIC_BYTES = int(215623.7 * 1024 * 2.0 + 1088.6 * 1024)
-C2_GLOBAL_TRAFFIC_BYTES = int((4214.8 + 277.0) * 1024 * 2.0 + (530.0 + 4.0) * 1024)
-C3_TRAFFIC_BYTES = int(19466.5 * 1024 * 2.0 + 75.2 * 1024)
+C2_GLOBAL_TRAFFIC_BYTES = int((4242.3 + 277.0) * 1024 * 2.0 + (530.0 + 4.0) * 1024)
+C3_TRAFFIC_BYTES = int(19468.1 * 1024 * 2.0 + 75.2 * 1024)
 # A4B whole decode step at positions 513-530 (profiles/decode_a4b_traffic.md):
 # FETCH_SIZE 1,270,208.5 KiB x 2.0 + WRITE_SIZE 11,299.5 KiB per token
 A4B_STEP_TRAFFIC_BYTES = int(1270208.5 * 1024 * 2.0 + 11299.5 * 1024)
