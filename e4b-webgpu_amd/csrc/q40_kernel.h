@@ -59,6 +59,30 @@
 #define E4B_TUNE_PLAIN_LB 2
 #endif
 
+// batches of the qkv tile (norm prologue, 4 rows) and of the o tile
+// (attention-combine prologue, 2 rows); 1 = unbatched.  Measured on MI355X
+// at the E4B shape: the o tile requested whole and multiplied in 2 batches
+// 853.1 tok/s against 851.3 unbatched and 840.3 with one batch ahead; the
+// qkv tile 851.5 (whole, 2 batches) and 841.8 (one ahead): left unbatched
+#ifndef E4B_TUNE_QKV_NB
+#define E4B_TUNE_QKV_NB 1
+#endif
+#ifndef E4B_TUNE_QKV_PRE
+#define E4B_TUNE_QKV_PRE 1
+#endif
+#ifndef E4B_TUNE_QKV_LB
+#define E4B_TUNE_QKV_LB 1
+#endif
+#ifndef E4B_TUNE_O_NB
+#define E4B_TUNE_O_NB 2
+#endif
+#ifndef E4B_TUNE_O_PRE
+#define E4B_TUNE_O_PRE 2
+#endif
+#ifndef E4B_TUNE_O_LB
+#define E4B_TUNE_O_LB 2
+#endif
+
 // rows per wave and waves per workgroup of the fused-prologue GeGLU tile
 #ifndef E4B_TUNE_GEGLU_R
 #define E4B_TUNE_GEGLU_R 8
@@ -992,8 +1016,20 @@ bool launch_r(const Cfg& c, const Launch& L) {
         return true;
       }
       return false;
-    case 2: launch<LPR, BPL, 2, KW, XLO, EPI, PROK, NA>(L); return true;
-    case 4: launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA>(L); return true;
+    case 2:
+      if constexpr (pro_attn(PROK)) {
+        launch<LPR, BPL, 2, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_O_NB, E4B_TUNE_O_PRE, E4B_TUNE_O_LB>(L);
+      } else {
+        launch<LPR, BPL, 2, KW, XLO, EPI, PROK, NA>(L);
+      }
+      return true;
+    case 4:
+      if constexpr (PROK > 0 && EPI == EPI_F32) {
+        launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA, 4, E4B_TUNE_QKV_NB, E4B_TUNE_QKV_PRE, E4B_TUNE_QKV_LB>(L);
+      } else {
+        launch<LPR, BPL, 4, KW, XLO, EPI, PROK, NA>(L);
+      }
+      return true;
     case 8:
       if constexpr (BPL == 1 && KW == 1 && LPR == 64 && EPI == EPI_GEGLU && PROK > 0 && E4B_TUNE_GEGLU_R == 8) {
         // the fused-prologue GeGLU: 8-wave workgroups, 4 batches of 2 rows,
