@@ -483,6 +483,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
       }
   };
   if (dense) load_rows(A.dense_gu, u, A.FF2);
+  E4B_TRACE_MARK(0);
   // the block holds expert waves iff its last (clamped) tile is an expert tile
   const bool blk_expert = 2 * GU_U * min((int64_t)blockIdx.x * 4 + 3, ntiles - 1) >= A.FF2;
   if (blockIdx.x == 0) {
@@ -548,6 +549,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     reinterpret_cast<uint4*>(xs[1])[threadIdx.x + 256] = xm1;
   }
   lds_sync();
+  E4B_TRACE_MARK(1);
   int slot = 0, j = u;
   if (!dense) {
     slot = (u - A.FF2) / A.FF;
@@ -559,6 +561,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   uint32_t xp[GU_BPL][16];
 #pragma unroll
   for (int b = 0; b < GU_BPL; ++b) load_x16(x, min(l + GU_LPR * b, nb - 1), xp[b]);
+  E4B_TRACE_MARK(2);
 
   // 4. dot products, GeGLU
   float acc[2 * GU_U];
@@ -578,6 +581,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
       acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8)), acc[r]);
     }
   }
+  E4B_TRACE_MARK(3);
   // lanes [SPAN r, SPAN r + SPAN) of the group hold row r: gate of unit r / 2
   // for even r, its up row for odd r
   constexpr int SPAN = GU_LPR / (2 * GU_U);

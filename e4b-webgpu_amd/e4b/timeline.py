@@ -203,6 +203,7 @@ def main(argv=None) -> int:
     ap.add_argument("--workload", default="c4", choices=["c4", "a4b"])
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--save", default=None, help="also write the raw workgroup records (numpy .npy) here")
     a = ap.parse_args(argv)
     eng, p0 = _engine(a.workload, a.warmup + a.steps)
     eng.time_decode(p0, a.warmup)
@@ -212,6 +213,8 @@ def main(argv=None) -> int:
         ms[0] = eng.time_decode(p0 + a.warmup, a.steps)
 
     recs = capture(run)
+    if a.save:
+        np.save(a.save, recs)
     khz = C.c_int(0)
     check(lib.e4b_trace_clock_khz(C.byref(khz)), "e4b_trace_clock_khz")
     ls = launches(recs)
@@ -221,7 +224,8 @@ def main(argv=None) -> int:
     print(summarize(ls, khz.value, a.steps))
     print("\nPhase marks (mean microseconds after the workgroup's entry; GEMV: 0 loads issued, 1 input vector "
           "ready, 2 dot products done, 3 rows reduced; attention: 0 loads issued, 1 head prep done, 2 scores "
-          "done, 3 P.V merged; PLE: 0 loads issued, 1 prologue done, 2 gate done):\n")
+          "done, 3 P.V merged; PLE: 0 loads issued, 1 prologue done, 2 gate done; MoE gate/up: 0 dense rows and "
+          "inputs requested, 1 top-8 picks in LDS, 2 expert rows requested, 3 dot products done):\n")
     print(phases(recs, khz.value))
     print("\nWorkgroup placement (microseconds after each launch's first entry):\n")
     print(placement(recs, ls, khz.value))
