@@ -52,6 +52,13 @@ DEV void load_x16(const uint32_t* __restrict__ x, int jb, uint32_t* xp) {
 // forms the attention residual h1 = h + rms(attn_o) post_attn
 // (kernels/rmsacc3.wgsl:36-53) from its own loads, stages it in LDS for the
 // branch inputs, and block 0 writes it to h1.
+//
+// Every request goes out before the first wait: the vector loads from the
+// leading (preloaded) pointers, then the struct fields the later steps use
+// (eps, the multiplier, the output and norm pointers) are read in one wait
+// that overlaps those loads, then this block's slice of the two branch
+// norms.  Left to the compiler, the struct reads were issued at the second
+// rms and waited on there, a kernel-argument round trip on the critical path.
 constexpr int kRouterMaxH4 = 768;  // H <= 3072
 
 DEV float4 f4_fma(float4 a, float s, float4 w, float4 b) {
@@ -67,10 +74,11 @@ DEV float f4_ss(float4 v, float acc) {
 // the library is built with -amdgpu-kernarg-preload-count, so they arrive in
 // SGPRs with the wave and no request waits for a kernel-argument load
 // (struct arguments are not preloaded).  Measured on MI355X at the A4B
-// shape: 734 tok/s against 724 without; the same leads for the gate/up and
-// down kernels measured slower (738.6 tok/s without the gate/up leads,
-// 735.6 without the down leads) and are not used.
-template <int NO>
+// shape: 734 tok/s against 724 without.  With the struct fields read in
+// one early wait and the branch norms prefetched, and leads for the down
+// kernel's expert blocks: 776.2 tok/s against 765.2 (c3: 21.0 against
+// 21.4 us per half-layer).
+template <int NO>  // the o projection's column slices; 0: no attention residual
 __global__ __launch_bounds__(128) void k_moe_router(const float* lh, const float* lrs, const float* lo,
                                                     const float* lpa, const float* lrw, uint32_t lhe, MoeArgs A) {
   A.h = lh;
@@ -81,23 +89,22 @@ __global__ __launch_bounds__(128) void k_moe_router(const float* lh, const float
   A.H = (int)(lhe & 0xffffu);
   A.E = (int)(lhe >> 16);
   E4B_TRACE_SCOPE(trace_tag(TR_MOE_ROUTER, 0));
-  // token row y of a batch (the batched prefill); y = 0 in the decode step
+  // token row y of a batch (the batched prefill); y = 0 in the decode step.
+  // The outputs are offset where they are written, so that their struct
+  // fields are not read before the loads below are issued.
   A.h += (int64_t)blockIdx.y * A.H;
-  A.xd += (int64_t)blockIdx.y * A.H;
-  A.xm += (int64_t)blockIdx.y * A.H;
-  A.scores += (int64_t)blockIdx.y * A.E;
+  const int64_t ry = blockIdx.y;
   __shared__ __align__(16) float4 xr[kRouterMaxH4];
   __shared__ __align__(16) float4 h1s[kRouterMaxH4];
   __shared__ float red[2];
   constexpr int PT = kRouterMaxH4 / 128;  // float4 per thread
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int H = A.H, H4 = H / 4;
-  const bool res = A.attn_o != nullptr;
+  constexpr bool res = NO > 0;
   const float4* h4 = reinterpret_cast<const float4*>(A.h);
   const float4* rs4 = reinterpret_cast<const float4*>(A.router_scale);
-  // absent residual inputs read h instead (always valid) and go unused
-  const float4* o4 = reinterpret_cast<const float4*>(res ? A.attn_o : A.h);
-  const float4* pa4 = reinterpret_cast<const float4*>(res ? A.post_attn : A.h);
+  const float4* o4 = reinterpret_cast<const float4*>(A.attn_o);
+  const float4* pa4 = reinterpret_cast<const float4*>(A.post_attn);
   const int e = min((int)blockIdx.x * 2 + wave, A.E - 1);
   const float4* w4 = reinterpret_cast<const float4*>(A.router_w + (int64_t)e * H);
   // every load up front: h, the scale and the residual inputs
@@ -109,13 +116,32 @@ __global__ __launch_bounds__(128) void k_moe_router(const float* lh, const float
     const int i = min((int)threadIdx.x + 128 * k, H4 - 1);
     hv[k] = h4[i];
     sv[k] = rs4[i];
-    ov[k] = o4[i];
+    if (res) {
+      ov[k] = o4[i];
 #pragma unroll
-    for (int q = 1; q < NO; ++q) os[q - 1][k] = o4[(int64_t)q * H4 + i];
-    pv[k] = pa4[i];
+      for (int q = 1; q < NO; ++q) os[q - 1][k] = o4[(int64_t)q * H4 + i];
+      pv[k] = pa4[i];
+    }
   }
 #pragma unroll
   for (int k = 0; k < kRouterMaxH4 / 64; ++k) wv[k] = w4[min(lane + 64 * k, H4 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  // the struct fields, in one wait while the loads above are in flight
+  asm volatile("" ::"s"(A.eps), "s"(A.router_mult), "s"(A.scores), "s"(A.xd), "s"(A.xm), "s"(A.ffn_norm),
+               "s"(A.pre_ffw2));
+  if (res) asm volatile("" ::"s"(A.h1));
+  // this block's slice of the branch inputs: the first element of each
+  // thread's share of the two norms requested now
+  const int nblk = (A.E + 1) / 2;  // gridDim.x, known without the hidden arguments
+  const int per = (H + nblk - 1) / nblk;
+  const int b_lo = (int)blockIdx.x * per, b_hi = min(H, b_lo + per);
+  const int i0 = b_lo + (int)threadIdx.x;
+  float fn0 = 0.f, p20 = 0.f;
+  if (i0 < b_hi) {
+    fn0 = A.ffn_norm[i0];
+    p20 = A.pre_ffw2[i0];
+  }
+  E4B_TRACE_MARK(0);
   if (res) {
     // o = the slices' sum in slice order
 #pragma unroll
@@ -132,6 +158,7 @@ __global__ __launch_bounds__(128) void k_moe_router(const float* lh, const float
     if (lane == 0) red[wave] = so;
     lds_sync();
     const float io = rms_inv(red[0] + red[1], H, A.eps);
+    E4B_TRACE_MARK(1);
     lds_sync();  // red is reused below
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
 #pragma unroll
@@ -161,6 +188,7 @@ __global__ __launch_bounds__(128) void k_moe_router(const float* lh, const float
                           hv[k].z * inv * (sv[k].z * A.router_mult), hv[k].w * inv * (sv[k].w * A.router_mult));
   }
   lds_sync();
+  E4B_TRACE_MARK(2);
   float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < kRouterMaxH4 / 64; ++k) {
@@ -171,14 +199,19 @@ __global__ __launch_bounds__(128) void k_moe_router(const float* lh, const float
     }
   }
   acc = wave_sum(acc);
-  if (lane == 0 && (int)blockIdx.x * 2 + wave < A.E) A.scores[e] = acc;
+  if (lane == 0 && (int)blockIdx.x * 2 + wave < A.E) A.scores[ry * A.E + e] = acc;
+  E4B_TRACE_MARK(3);
   // this block's slice of the f16 branch inputs
-  const int per = (H + gridDim.x - 1) / gridDim.x;
   const float* h1f = reinterpret_cast<const float*>(h1s);
-  for (int i = blockIdx.x * per + threadIdx.x; i < min(H, (int)(blockIdx.x + 1) * per); i += 128) {
+  if (i0 < b_hi) {
+    const float v = (res ? h1f[i0] : A.h[i0]) * inv;
+    A.xd[ry * H + i0] = f2h(v * fn0);
+    A.xm[ry * H + i0] = f2h(v * p20);
+  }
+  for (int i = i0 + 128; i < b_hi; i += 128) {
     const float v = (res ? h1f[i] : A.h[i]) * inv;
-    A.xd[i] = f2h(v * A.ffn_norm[i]);
-    A.xm[i] = f2h(v * A.pre_ffw2[i]);
+    A.xd[ry * H + i] = f2h(v * A.ffn_norm[i]);
+    A.xm[ry * H + i] = f2h(v * A.pre_ffw2[i]);
   }
 }
 
@@ -611,7 +644,25 @@ constexpr int DD_LPR = 32, DD_BPL = 3, DD_R = 1;
 constexpr int DE_LPR = 8, DE_BPL = 3, DE_R = 1;
 constexpr int kMoeMaxX = K * DE_LPR * DE_BPL * 32;  // 6144 >= FF2 and 8 FF
 
-__global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
+//
+// The leading scalar arguments repeat what the expert blocks' first requests
+// need (the picks, the expert down matrix, both inputs, H | FF << 16 and
+// FF2 | nbd << 16): they arrive preloaded in SGPRs, so an expert block
+// requests its picks at entry and its weight rows one global round trip
+// later.  From the struct alone that took a kernel-argument read, a second
+// one for the picks' pointer and then the picks' own read.
+__global__ __launch_bounds__(256) void k_moe_down(uint32_t* ltk, const uint4* lnib, const uint16_t* lsc,
+                                                  uint16_t* lgs, uint16_t* lgd, uint32_t lhf, uint32_t lfn,
+                                                  MoeArgs A) {
+  A.topk_idx = ltk;
+  A.exp_down.nib = lnib;
+  A.exp_down.sc = lsc;
+  A.g_slots = lgs;
+  A.g_dense = lgd;
+  A.H = (int)(lhf & 0xffffu);
+  A.FF = (int)(lhf >> 16);
+  A.FF2 = (int)(lfn & 0xffffu);
+  const int nbd = (int)(lfn >> 16);
   E4B_TRACE_SCOPE(trace_tag(TR_MOE_DOWN, 0));
   __shared__ __align__(16) uint16_t xs[kMoeMaxX];
   const int lane = threadIdx.x & 63;
@@ -689,7 +740,6 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
   const int nb = A.FF / 32;
   const Q40Mat& W = A.exp_down;
   const int e = (int)A.topk_idx[g];
-  const float wk = A.topk_w[g];
   const int64_t ntiles = (A.H + DE_R - 1) / DE_R;
   const int64_t tile_id = (int64_t)(blockIdx.x - nbd) * 4 + wave;
   const int64_t o0 = min(tile_id, ntiles - 1) * DE_R;
@@ -708,7 +758,10 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+  const float wk = A.topk_w[g];  // needed last: its struct read waits behind the rows
+  E4B_TRACE_MARK(0);
   stage_x();
+  E4B_TRACE_MARK(1);
   const uint32_t* x = reinterpret_cast<const uint32_t*>(xs + (int64_t)g * A.FF);
   uint32_t xp[DE_BPL][16];
   float xs8[DE_BPL];
@@ -732,6 +785,7 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs A, int nbd) {
       acc[r] = fmaf(d, fmaf(a1, kTwo24 / 16.f, fmaf(a0, kTwo24, xs8[b])), acc[r]);
     }
   }
+  E4B_TRACE_MARK(2);
   // lane l of slot g holds y_g of row o0 + l / 2; weight it and sum the slots
   float v = reduce_rows<DE_LPR, DE_R>(acc) * wk;
   v = xsum_step<8>(v);
@@ -797,8 +851,8 @@ __global__ __launch_bounds__(256) void k_moe_tail(MoeArgs A) {
 int launch_moe_router(const MoeArgs& A, hipStream_t st) {
   if (A.H % 4 || A.H / 4 > kRouterMaxH4) return e4b_fail(E4B_EINVAL, "router: H=%d (multiple of 4, <= 3072)", A.H);
   if (A.E < 1 || A.E > 0xffff) return e4b_fail(E4B_EINVAL, "router: %d experts", A.E);
-  switch (A.attn_o ? A.attn_o_slices : 1) {
-    case 0:
+  switch (A.attn_o ? (A.attn_o_slices ? A.attn_o_slices : 1) : 0) {
+    case 0: hipLaunchKernelGGL(k_moe_router<0>, dim3((A.E + 1) / 2), dim3(128), 0, st, ROUTER_LEAD(A)); break;
     case 1: hipLaunchKernelGGL(k_moe_router<1>, dim3((A.E + 1) / 2), dim3(128), 0, st, ROUTER_LEAD(A)); break;
     case 2: hipLaunchKernelGGL(k_moe_router<2>, dim3((A.E + 1) / 2), dim3(128), 0, st, ROUTER_LEAD(A)); break;
     case 4: hipLaunchKernelGGL(k_moe_router<4>, dim3((A.E + 1) / 2), dim3(128), 0, st, ROUTER_LEAD(A)); break;
@@ -825,7 +879,9 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
   hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)gu_wgs), dim3(256), 0, st, A, gu_tiles);
   const int dd_tiles = (A.H + 2 * DD_R - 1) / (2 * DD_R), de_tiles = (A.H + DE_R - 1) / DE_R;
   const int nbd = (dd_tiles + 3) / 4, nbe = (de_tiles + 3) / 4;
-  hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A, nbd);
+  hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A.topk_idx, A.exp_down.nib, A.exp_down.sc,
+                     A.g_slots, A.g_dense, (uint32_t)A.H | (uint32_t)A.FF << 16, (uint32_t)A.FF2 | (uint32_t)nbd << 16,
+                     A);
   if (A.h_out) hipLaunchKernelGGL(k_moe_tail, dim3(1), dim3(256), 0, st, A);
   E4B_HIP(hipGetLastError());
   return E4B_OK;

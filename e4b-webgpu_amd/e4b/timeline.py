@@ -225,7 +225,9 @@ def main(argv=None) -> int:
     print("\nPhase marks (mean microseconds after the workgroup's entry; GEMV: 0 loads issued, 1 input vector "
           "ready, 2 dot products done, 3 rows reduced; attention: 0 loads issued, 1 head prep done, 2 scores "
           "done, 3 P.V merged; PLE: 0 loads issued, 1 prologue done, 2 gate done; MoE gate/up: 0 dense rows and "
-          "inputs requested, 1 top-8 picks in LDS, 2 expert rows requested, 3 dot products done):\n")
+          "inputs requested, 1 top-8 picks in LDS, 2 expert rows requested, 3 dot products done; MoE router: 0 "
+          "loads issued, 1 residual rms formed, 2 router input staged, 3 score written; MoE down (expert "
+          "blocks): 0 rows requested, 1 slot outputs staged, 2 dot products done):\n")
     print(phases(recs, khz.value))
     print("\nWorkgroup placement (microseconds after each launch's first entry):\n")
     print(placement(recs, ls, khz.value))
