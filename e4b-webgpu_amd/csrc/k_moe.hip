@@ -467,7 +467,24 @@ constexpr int GU_LPR = 32, GU_BPL = 3;
 constexpr int GU_U = 2;  // units per lane group (a wave tile holds 2 GU_U units)
 constexpr int kMoeMaxH = GU_LPR * GU_BPL * 32;  // 3072
 
-__global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
+//
+// The leading scalar arguments repeat what the first requests need (the
+// scores, both weight matrices, H | E << 16, FF | FF2 << 16): they arrive
+// preloaded in SGPRs, so every block requests the scores and the dense
+// blocks their rows at entry; the two inputs follow from the struct, whose
+// read then waits behind those requests.
+__global__ __launch_bounds__(256) void k_moe_gu(float* lsco, const uint4* ldn, const uint16_t* lds, const uint4* len,
+                                                const uint16_t* les, uint32_t lhe, uint32_t lff, MoeArgs A) {
+  A.scores = lsco;
+  A.dense_gu.nib = ldn;
+  A.dense_gu.sc = lds;
+  A.exp_gu.nib = len;
+  A.exp_gu.sc = les;
+  A.H = (int)(lhe & 0xffffu);
+  A.E = (int)(lhe >> 16);
+  A.FF = (int)(lff & 0xffffu);
+  A.FF2 = (int)(lff >> 16);
+  const int64_t ntiles = (A.FF2 + (int64_t)K * A.FF) / (2 * GU_U);
   E4B_TRACE_SCOPE(trace_tag(TR_MOE_GU, 0));
   __shared__ __align__(16) uint16_t xs[2][kMoeMaxH];
   __shared__ int sel[K];
@@ -485,13 +502,9 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   const int u = (int)(2 * GU_U * tile) + GU_U * g;  // this group's first unit
   const bool dense = 2 * GU_U * tile < A.FF2;        // wave-uniform: FF2 and FF are multiples of 2 GU_U
 
-  // 1. both inputs (independent of the routing), two 16-byte pieces per
-  //    thread and input at most (H <= 3072)
-  // (named registers: an array here is kept in scratch memory by the compiler)
-  const int nv = A.H / 8;
-  const int i0 = min((int)threadIdx.x, nv - 1), i1 = min((int)threadIdx.x + 256, nv - 1);
-  const uint4 xd0 = reinterpret_cast<const uint4*>(A.xd)[i0], xd1 = reinterpret_cast<const uint4*>(A.xd)[i1];
-  const uint4 xm0 = reinterpret_cast<const uint4*>(A.xm)[i0], xm1 = reinterpret_cast<const uint4*>(A.xm)[i1];
+  // 1. the scores (the expert blocks rank them below), one per thread
+  const int E = A.E;
+  const float sv = (int)threadIdx.x < E ? A.scores[threadIdx.x] : -3.0e38f;
 
   // 2. weight rows: dense units are known now; expert units after the top-8
   //    selection, made once per workgroup by wave 0 from the 128 scores and
@@ -516,6 +529,14 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
       }
   };
   if (dense) load_rows(A.dense_gu, u, A.FF2);
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. both inputs (independent of the routing), two 16-byte pieces per
+  //    thread and input at most (H <= 3072)
+  // (named registers: an array here is kept in scratch memory by the compiler)
+  const int nv = A.H / 8;
+  const int i0 = min((int)threadIdx.x, nv - 1), i1 = min((int)threadIdx.x + 256, nv - 1);
+  const uint4 xd0 = reinterpret_cast<const uint4*>(A.xd)[i0], xd1 = reinterpret_cast<const uint4*>(A.xd)[i1];
+  const uint4 xm0 = reinterpret_cast<const uint4*>(A.xm)[i0], xm1 = reinterpret_cast<const uint4*>(A.xm)[i1];
   E4B_TRACE_MARK(0);
   // the block holds expert waves iff its last (clamped) tile is an expert tile
   const bool blk_expert = 2 * GU_U * min((int64_t)blockIdx.x * 4 + 3, ntiles - 1) >= A.FF2;
@@ -539,8 +560,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     // or one (E <= 256); no dependent cross-lane chain, so the picks are in
     // LDS ~1 us after the scores arrive instead of ~3 us for one wave's
     // eight wave-maximum rounds
-    const int t = threadIdx.x, E = A.E;
-    const float sv = t < E ? A.scores[t] : -3.0e38f;
+    const int t = threadIdx.x;
     const float wm = wave_max(sv);
     if (lane == 0) smax[wave] = wm;
     lds_sync();
@@ -571,7 +591,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
     }
   }
 
-  // 3. stage the inputs and the picks, then the expert rows and this lane's
+  // 4. stage the inputs and the picks, then the expert rows and this lane's
   //    blocks from LDS
   if ((int)threadIdx.x < nv) {
     reinterpret_cast<uint4*>(xs[0])[threadIdx.x] = xd0;
@@ -596,7 +616,7 @@ __global__ __launch_bounds__(256) void k_moe_gu(MoeArgs A, int64_t ntiles) {
   for (int b = 0; b < GU_BPL; ++b) load_x16(x, min(l + GU_LPR * b, nb - 1), xp[b]);
   E4B_TRACE_MARK(2);
 
-  // 4. dot products, GeGLU
+  // 5. dot products, GeGLU
   float acc[2 * GU_U];
 #pragma unroll
   for (int r = 0; r < 2 * GU_U; ++r) acc[r] = 0.f;
@@ -876,7 +896,9 @@ int launch_moe_ffn(const MoeArgs& A, hipStream_t st) {
   if (rc) return rc;
   const int64_t gu_tiles = (A.FF2 + (int64_t)K * A.FF) / (2 * GU_U);
   const int64_t gu_wgs = (gu_tiles + 3) / 4;  // one tile per wave
-  hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)gu_wgs), dim3(256), 0, st, A, gu_tiles);
+  hipLaunchKernelGGL(k_moe_gu, dim3((unsigned)gu_wgs), dim3(256), 0, st, A.scores, A.dense_gu.nib, A.dense_gu.sc,
+                     A.exp_gu.nib, A.exp_gu.sc, (uint32_t)A.H | (uint32_t)A.E << 16,
+                     (uint32_t)A.FF | (uint32_t)A.FF2 << 16, A);
   const int dd_tiles = (A.H + 2 * DD_R - 1) / (2 * DD_R), de_tiles = (A.H + DE_R - 1) / DE_R;
   const int nbd = (dd_tiles + 3) / 4, nbe = (de_tiles + 3) / 4;
   hipLaunchKernelGGL(k_moe_down, dim3(nbd + nbe), dim3(256), 0, st, A.topk_idx, A.exp_down.nib, A.exp_down.sc,
