@@ -154,8 +154,12 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams,
   const float2* rsrc = have_cs ? A.rope : reinterpret_cast<const float2*>(A.qkv);  // any readable 1 KB
   const float4 rc0 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[0];
   const float4 rc1 = reinterpret_cast<const float4*>(rsrc + 4 * (lane & 31))[1];
+  // the outputs' fields and the grid's chunk count in the same wait as the
+  // caches' (read where they are used, at the final stores, they cost a
+  // kernel-argument round trip at the end of every workgroup)
+  const int gch = gridDim.y;  // partial stride: chunks allocated per head
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("" ::"s"(kc0), "s"(vc0));
+  asm volatile("" ::"s"(kc0), "s"(vc0), "s"(A.part_o), "s"(A.part_ml), "s"(gch));
   const int cur = A.window > 0 ? pos : cur_raw;
   const int lo = (A.window > 0 && cur + 1 > A.window) ? cur + 1 - A.window : 0;
   const int n = cur + 1 - lo;
@@ -368,7 +372,6 @@ __global__ __launch_bounds__(64 * NW) void k_attn_split(const uint32_t* lparams,
   {
     constexpr int OPT = GQA * VD / (NW * 64);  // outputs per thread
     static_assert(OPT == 1 || OPT == 2, "outputs per thread");
-    const int gch = gridDim.y;  // partial stride: chunks allocated per head
     const int h = threadIdx.x / (VD / OPT), d = OPT * (threadIdx.x % (VD / OPT));
     float M = wml[0][h][0];
 #pragma unroll

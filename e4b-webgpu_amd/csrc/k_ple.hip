@@ -87,6 +87,10 @@ __global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la,
   // no row load a valid neighbour and drop it); requested last, as its
   // pointer is not among the preloaded arguments
   __builtin_amdgcn_sched_barrier(0);
+  // the struct fields read after this point, in the one wait the per-layer
+  // input's pointer takes anyway (else the prologue's LDS waits wait on
+  // them one kernel-argument round trip at a time)
+  asm volatile("" ::"s"(A.ple), "s"(A.part), "s"(pa.hout), "s"(pa.hsnap), "s"(pa.scale), "s"(pa.eps));
   const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
   E4B_TRACE_MARK(0);

@@ -529,6 +529,21 @@ DEV void take_lead(const uint4* lnib, const uint16_t* lsc, const void* lp0, cons
 // issued up front, with no branch between them and their first use, so the
 // compiler's wait counts stay exact and a fused prologue computes while the
 // weight stream is in flight.
+// The struct fields that the residual/tail prologue and the epilogue read
+// after the loads are issued, read in one wait that overlaps those loads.
+// Left to the compiler, each field was read where first used, and the
+// prologue's LDS waits (lgkmcnt also counts scalar loads) then waited on a
+// kernel-argument round trip each.
+template <int PROK, int EPI>
+DEV void read_late_fields(const ProArgs& pa, const GemvOut& o) {
+  if constexpr (PROK > 0 || PROK == kProTail)
+    asm volatile("" ::"s"(pa.eps), "s"(pa.scale), "s"(pa.hout), "s"(pa.hsnap));
+  if constexpr (EPI == EPI_F32)
+    asm volatile("" ::"s"(o.y));
+  else
+    asm volatile("" ::"s"(o.yh));
+}
+
 template <int LPR, int BPL, int R, int KW, bool XLO, int EPI, int PROK, int NA = 1, int NWV = 4>
 __global__ __launch_bounds__(64 * NWV) void k_q40(Q40_LEAD_PARAMS, Q40Mat W, const uint32_t* __restrict__ xh,
                                                   const uint32_t* __restrict__ xl, GemvOut o, ProArgs pa) {
@@ -608,6 +623,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40(Q40_LEAD_PARAMS, Q40Mat W, con
   // keep the scheduler from hoisting prologue math (and its waits) above
   // the weight loads: every load of the tile is in flight before any wait
   __builtin_amdgcn_sched_barrier(0);
+  read_late_fields<PROK, EPI>(pa, o);
   E4B_TRACE_MARK(0);
 
   uint32_t xp[BPL][16];
@@ -824,6 +840,7 @@ __global__ __launch_bounds__(64 * NWV) void k_q40b(Q40_LEAD_PARAMS, Q40Mat W, co
   // keep the scheduler from hoisting prologue math (and its waits) above
   // the weight loads: every load requested so far is in flight before any wait
   __builtin_amdgcn_sched_barrier(0);
+  read_late_fields<PROK, EPI>(pa, o);
   E4B_TRACE_MARK(0);
 
   if constexpr (PROK > 0) pro_finish<PROK, TPB, NA>(pa, pr, xs_lds, red);
