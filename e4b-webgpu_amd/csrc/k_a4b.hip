@@ -132,7 +132,7 @@ DEV Live live_of(const AttnGen& A) { return live_at(A, (int)A.params[0], (int)A.
 // Scores: per position GQA dot products reduced across the wave
 // (reduce_rows), stored to LDS; softmax statistics of head h by wave h over
 // the chunk's 64 positions; P.V with the weights broadcast from LDS, folded
-// over the 8 waves.  A chunk's K is read by all HD / 128 slices (from L2
+// over the 8 waves.  A chunk's K is read by all HD / VD slices (from L2
 // after the first); V is split across them.
 //
 // The leading scalar arguments repeat the fields the first requests need
@@ -143,6 +143,17 @@ DEV Live live_of(const AttnGen& A) { return live_at(A, (int)A.params[0], (int)A.
 // kernel-argument load (struct arguments are not preloaded).  The head-prep
 // rows and the RoPE table do not depend on the position: they are requested
 // while the position is in flight.
+// V dims per slice (blockIdx.z): 128 at head dim 256; at head dim 512 the
+// V slice width is a build knob (128: 4 slices that each read the chunk's
+// K rows; 256: 2 slices, half the K reads, twice the P.V work a block).
+// Measured at the A4B shape: 256 gave 775.5 tok/s against 777.9 for 128,
+// so 128 is the default.
+#ifndef E4B_TUNE_GEN512_VD
+#define E4B_TUNE_GEN512_VD 128
+#endif
+constexpr int gen_vd(int hd) { return hd == 512 ? E4B_TUNE_GEN512_VD : 128; }
+static_assert(gen_vd(512) == 128 || gen_vd(512) == 256, "V slice width");
+
 template <int HD, int GQA, bool RAW>
 __global__ __launch_bounds__(512) void k_attn_gen(const uint32_t* lparams, const float* lqkv, const float* lqw,
                                                   const float* lkw, const float2* lrope, uint32_t lheads,
@@ -157,7 +168,8 @@ __global__ __launch_bounds__(512) void k_attn_gen(const uint32_t* lparams, const
   A.keqv = (lheads >> 31) != 0;
   A.angles = (int)langles;
   E4B_TRACE_SCOPE(trace_tag(TR_ATTN_GEN, HD));
-  constexpr int NW = 8, CS = kAttnGenChunk, PER = HD / 64, PW = CS / NW, VD = 128;
+  constexpr int NW = 8, CS = kAttnGenChunk, PER = HD / 64, PW = CS / NW, VD = gen_vd(HD);
+  constexpr int VW = VD / 128;  // 32-bit words (f16 pairs) of V a lane holds per position
   constexpr int NR = GQA + 2, RPW = (NR + NW - 1) / NW, LPH = 64 / GQA;
   static_assert(CS == 64 && GQA <= NW && (GQA & (GQA - 1)) == 0, "64-position chunks, GQA 1/2/4/8");
   __shared__ __align__(16) float qs[GQA][HD];
@@ -216,7 +228,7 @@ __global__ __launch_bounds__(512) void k_attn_gen(const uint32_t* lparams, const
     return (A.window > 0 && s >= A.slots) ? s - A.slots : s;
   };
   uint32_t kr[PW][PER / 2];
-  uint32_t vr[PW];
+  uint32_t vr[PW][VW];
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
     const int64_t sl = slot_at(min(wave + NW * i, m - 1));
@@ -228,7 +240,13 @@ __global__ __launch_bounds__(512) void k_attn_gen(const uint32_t* lparams, const
       const uint4 t = *reinterpret_cast<const uint4*>(krow);
       kr[i][0] = t.x, kr[i][1] = t.y, kr[i][2] = t.z, kr[i][3] = t.w;
     }
-    vr[i] = *reinterpret_cast<const uint32_t*>(vc + sl * HD + VD * zs + 2 * lane);
+    const uint16_t* vp = vc + sl * HD + VD * zs + 2 * VW * lane;
+    if constexpr (VW == 1) {
+      vr[i][0] = *reinterpret_cast<const uint32_t*>(vp);
+    } else {
+      const uint2 t = *reinterpret_cast<const uint2*>(vp);
+      vr[i][0] = t.x, vr[i][1] = t.y;
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
 
@@ -329,27 +347,37 @@ __global__ __launch_bounds__(512) void k_attn_gen(const uint32_t* lparams, const
   }
   lds_sync();
 
-  // 4. P.V over the wave's positions, V dims 128 z + 2 l, 2 l + 1
+  // 4. P.V over the wave's positions, V dims VD z + 2 VW l .. 2 VW l + 2 VW - 1
   {
-    float acc[GQA][2];
+    float acc[GQA][2 * VW];
 #pragma unroll
-    for (int h = 0; h < GQA; ++h) acc[h][0] = acc[h][1] = 0.f;
-    const uint32_t vn = reinterpret_cast<const uint32_t*>(vnew)[VD / 2 * zs + lane];
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int u = 0; u < 2 * VW; ++u) acc[h][u] = 0.f;
+    uint32_t vn[VW];
+#pragma unroll
+    for (int w = 0; w < VW; ++w) vn[w] = reinterpret_cast<const uint32_t*>(vnew)[VD / 2 * zs + VW * lane + w];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int j = wave + NW * i;
-      // positions past m read a clamped row; their weight is 0 and the row is zeroed
-      const uint32_t vv = (c_lo + j == L.cur) ? vn : (j < m ? vr[i] : 0u);
-      const float v0 = h2f((uint16_t)(vv & 0xffffu)), v1 = h2f((uint16_t)(vv >> 16));
 #pragma unroll
-      for (int h = 0; h < GQA; ++h) {
-        const float p = es[h][j];
-        acc[h][0] = fmaf(p, v0, acc[h][0]);
-        acc[h][1] = fmaf(p, v1, acc[h][1]);
+      for (int w = 0; w < VW; ++w) {
+        // positions past m read a clamped row; their weight is 0 and the row is zeroed
+        const uint32_t vv = (c_lo + j == L.cur) ? vn[w] : (j < m ? vr[i][w] : 0u);
+        const float v0 = h2f((uint16_t)(vv & 0xffffu)), v1 = h2f((uint16_t)(vv >> 16));
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+          const float p = es[h][j];
+          acc[h][2 * w] = fmaf(p, v0, acc[h][2 * w]);
+          acc[h][2 * w + 1] = fmaf(p, v1, acc[h][2 * w + 1]);
+        }
       }
     }
 #pragma unroll
-    for (int h = 0; h < GQA; ++h) *reinterpret_cast<float2*>(&po[wave][h][2 * lane]) = make_float2(acc[h][0], acc[h][1]);
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+      for (int w = 0; w < VW; ++w)
+        *reinterpret_cast<float2*>(&po[wave][h][2 * VW * lane + 2 * w]) = make_float2(acc[h][2 * w], acc[h][2 * w + 1]);
   }
   lds_sync();
 
@@ -661,7 +689,7 @@ int launch_rownorm(const float* h_in, float* h_out, const float* a, const float*
       (uint32_t)a.angles, (uint32_t)(a.window > 0 ? 0 : a.kv_idx), a
 template <int HD, bool RAW>
 static void launch_attn_hd_raw(const AttnGen& a, hipStream_t st) {
-  const dim3 grid(a.kvh, a.gch, HD / 128);
+  const dim3 grid(a.kvh, a.gch, HD / gen_vd(HD));
   switch (a.qh / a.kvh) {
     case 1: hipLaunchKernelGGL((k_attn_gen<HD, 1, RAW>), grid, dim3(512), 0, st, ATTN_GEN_LEAD(a)); break;
     case 2: hipLaunchKernelGGL((k_attn_gen<HD, 2, RAW>), grid, dim3(512), 0, st, ATTN_GEN_LEAD(a)); break;
