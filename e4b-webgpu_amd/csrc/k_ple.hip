@@ -29,7 +29,9 @@ constexpr float kTwo24 = 16777216.0f;
 // quarters (blockIdx.y), PR = PROK / Q projection rows per thread.
 //
 // The leading scalar arguments repeat the pointers the first requests need
-// (the prologue's hin, a, w1; the gate and projection planes): the library
+// (the prologue's hin, a, w1; the gate planes, the projection's nibbles and
+// the per-layer input; the projection's scales, needed last, come from the
+// struct after its one wait): the library
 // is built with -amdgpu-kernarg-preload-count, so they arrive in SGPRs with
 // the wave and no request waits for a kernel-argument load (struct
 // arguments are not preloaded); H and the gate's blocks per row follow from
@@ -37,7 +39,7 @@ constexpr float kTwo24 = 16777216.0f;
 template <int PROK, int Q, int NA>
 __global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la, const float* lw1,
                                              const uint4* lgnib, const uint16_t* lgsc, const uint4* lpnib,
-                                             const uint16_t* lpsc, PleLaunch A, ProArgs pa) {
+                                             const float* lple, PleLaunch A, ProArgs pa) {
   E4B_TRACE_SCOPE(trace_tag(TR_PLE, 0));
   constexpr int H = 256 * PROK, LPR = H / 32, G = 64 / LPR, R = PROK, PR = PROK / Q;
   pa.hin = lhin;
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la,
   A.gate.sc = lgsc;
   A.gate.nb = H / 32;
   A.proj_nib = lpnib;
-  A.proj_sc = lpsc;
+  A.ple = lple;
   static_assert(G * R == 8, "8 gate rows per wave");
   static_assert(PR * Q == PROK, "whole projection rows per thread");
   __shared__ __align__(16) uint16_t xs[H];
@@ -63,6 +65,9 @@ __global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la,
   q40k::pro_issue<PROK, NA, 256, false>(pa, pr);
   // gate rows of this lane group, block l
   const int row0 = 32 * w + 8 * wave + g * R;
+  // the per-layer input of the gate row this lane finishes (lanes that
+  // finish no row load a valid neighbour and drop it)
+  const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
   uint4 wq[R];
   uint32_t wsc[R], wodd = 0;  // aligned scale pairs (ld_scale_pair) and their half
 #pragma unroll
@@ -80,18 +85,15 @@ __global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la,
   for (int i = 0; i < PR; ++i) {
     const uint32_t e = (uint32_t)(w * H + o0) + threadIdx.x + 256 * i;
     pq[i] = ld_nt_u4_off(A.proj_nib, e);
-    psc[i] = ld_scale_pair_off(A.proj_sc, e);
     podd |= (uint32_t)(e & 1) << i;
   }
-  // the per-layer input of the gate row this lane finishes (lanes that finish
-  // no row load a valid neighbour and drop it); requested last, as its
-  // pointer is not among the preloaded arguments
+  // the struct fields read after this point, in one wait (else the
+  // prologue's LDS waits wait on them one kernel-argument round trip at a
+  // time), then the projection's scales, requested last
   __builtin_amdgcn_sched_barrier(0);
-  // the struct fields read after this point, in the one wait the per-layer
-  // input's pointer takes anyway (else the prologue's LDS waits wait on
-  // them one kernel-argument round trip at a time)
-  asm volatile("" ::"s"(A.ple), "s"(A.part), "s"(pa.hout), "s"(pa.hsnap), "s"(pa.scale), "s"(pa.eps));
-  const float ple_v = A.ple[row0 + min(l / (LPR / R), R - 1)];
+  asm volatile("" ::"s"(A.proj_sc), "s"(A.part), "s"(pa.hout), "s"(pa.hsnap), "s"(pa.scale), "s"(pa.eps));
+#pragma unroll
+  for (int i = 0; i < PR; ++i) psc[i] = ld_scale_pair_off(A.proj_sc, (uint32_t)(w * H + o0) + threadIdx.x + 256 * i);
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the prologue waits
   E4B_TRACE_MARK(0);
   q40k::pro_finish<PROK, 256, NA, false>(pa, pr, xs, red);
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(256) void k_ple(const float* lhin, const float* la,
 
 }  // namespace
 
-#define PLE_LEAD(A, pa) pa.hin, pa.a, pa.w1, A.gate.nib, A.gate.sc, A.proj_nib, A.proj_sc, A, pa
+#define PLE_LEAD(A, pa) pa.hin, pa.a, pa.w1, A.gate.nib, A.gate.sc, A.proj_nib, A.ple, A, pa
 template <int NA>
 static void launch_ple_na(const PleLaunch& A, const ProArgs& pa, hipStream_t st) {
   switch (A.H) {
